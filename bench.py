@@ -1,0 +1,266 @@
+"""Benchmark of the W3 packed-LUT decode path on one MI355X.
+
+Metric: W3 GEMV HBM GB/s (% of peak) per Qwen3-8B shape; batch-1
+decode tokens/sec.  Workload (config 1): the seven Qwen3-8B Linear shapes of a
+decoder layer at M = 1, W3 g128, fp16 scales U[0.005,0.02], zero-points U{3,4},
+random codes, synthetic bf16 activations.
+
+A "step" is one replay of a HIP graph that runs the seven W3 GEMVs of a decoder
+layer for ``LAYERS`` distinct layers' payloads (so a replay streams ~600 MB of
+distinct weights; MI355X's 256 MB Infinity Cache cannot hold them).  ``value``
+is algorithmic bytes of all GEMVs in the timed replays / their wall time on the
+GPU (HIP events on the launch stream).
+
+Per shape, a graph of >= 50 launches over rotating payload copies (>= 300 MB)
+gives the average launch duration; the same-run bf16 arm runs torch.nn.functional.linear
+(hipBLASLt) on dequantized bf16 weights with the same rotation.  The CPU baseline
+times the oracle's dequantize-then-matmul restatement of the reference's dense
+CPU route on a bounded sample.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBPS = 8000.0
+SHAPES = {  # name: (O, K)
+    "q_proj": (4096, 4096), "k_proj": (1024, 4096), "v_proj": (1024, 4096), "o_proj": (4096, 4096),
+    "gate_proj": (12288, 4096), "up_proj": (12288, 4096), "down_proj": (4096, 12288),
+}
+UNIQUE = {"q/o": (4096, 4096), "k/v": (1024, 4096), "gate/up": (12288, 4096), "down": (4096, 12288)}
+
+
+def algorithmic_bytes(o: int, k: int, m: int = 1, zeros: bool = True, perm: bool = False) -> int:
+    """Planes 3OK/8 + fp16 scales 2GO (+ uint8 zeros GO) (+ perm 2K) + x 2MK + y 2MO."""
+    g = k // 128
+    total = 3 * o * k // 8 + 2 * g * o + 2 * m * k + 2 * m * o
+    if zeros:
+        total += g * o
+    if perm:
+        total += 2 * k
+    return total
+
+
+def make_payload(o, k, device, generator):
+    import torch
+
+    g = k // 128
+    planes = torch.randint(0, 256, (g, 3, o, 16), dtype=torch.uint8, device=device, generator=generator)
+    scales = (torch.rand((g, o), device=device, generator=generator) * 0.015 + 0.005).half()
+    zeros = torch.randint(3, 5, (g, o), dtype=torch.uint8, device=device, generator=generator)
+    perm = torch.arange(k, dtype=torch.int16, device=device)
+    return {"planes": planes, "scales": scales, "perm": perm, "zeros": zeros}
+
+
+def time_graph(graph, steps, warmup, stream):
+    import torch
+
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(steps):
+        graph.replay()
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps  # ms per replay
+
+
+def capture(fn, stream):
+    import torch
+
+    with torch.cuda.stream(stream):
+        for _ in range(2):
+            fn()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        fn()
+    torch.cuda.synchronize()
+    return graph
+
+
+def bench_shape(o, k, device, steps, warmup, stream, min_bytes=320e6, min_copies=50):
+    """Average launch time of the W3 GEMV and of the bf16 arm over rotating copies."""
+    import torch
+
+    from marlin_style_fluxbin_amd import W3Gemv
+
+    gen = torch.Generator(device=device).manual_seed(o * 7 + k)
+    nbytes = algorithmic_bytes(o, k)
+    copies = max(min_copies, int(min_bytes // nbytes) + 1)
+    payloads = [make_payload(o, k, device, gen) for _ in range(copies)]
+    gemvs = [W3Gemv(p, perm_identity=True) for p in payloads]
+    x = torch.randn(1, k, device=device, generator=gen).to(torch.bfloat16)
+    out = torch.empty(1, o, device=device, dtype=torch.bfloat16)
+
+    def w3_all():
+        for gemv in gemvs:
+            gemv(x, out)
+
+    graph = capture(w3_all, stream)
+    ms = time_graph(graph, steps, warmup, stream)
+    w3_us = ms * 1000 / copies
+    del graph
+
+    # same-run bf16 arm: dense bf16 weights (5.3x the bytes), same rotation rule
+    bf16_bytes = 2 * o * k + 2 * k + 2 * o
+    bcopies = max(min_copies // 5, int(min_bytes // bf16_bytes) + 1)
+    from marlin_style_fluxbin_amd.gptq_deployment import restore_planar_w3
+
+    weights = [restore_planar_w3(payloads[i % copies], dtype=torch.bfloat16) for i in range(bcopies)]
+    bout = torch.empty(1, o, device=device, dtype=torch.bfloat16)
+
+    def bf16_all():
+        for w in weights:
+            torch.matmul(x, w.t(), out=bout)
+
+    bgraph = capture(bf16_all, stream)
+    bms = time_graph(bgraph, steps, warmup, stream)
+    bf16_us = bms * 1000 / bcopies
+    del bgraph, weights, payloads, gemvs
+    torch.cuda.empty_cache()
+    return {
+        "O": o, "K": k, "copies": copies, "algorithmic_bytes": nbytes,
+        "w3_us": round(w3_us, 3), "w3_GBps": round(nbytes / w3_us / 1e3, 1),
+        "w3_frac_hbm": round(nbytes / w3_us / 1e3 / HBM_PEAK_GBPS, 4),
+        "bf16_us": round(bf16_us, 3), "bf16_GBps": round(bf16_bytes / bf16_us / 1e3, 1),
+        "w3_speedup_vs_bf16": round(bf16_us / w3_us, 3),
+    }
+
+
+def cpu_baseline(seconds_budget=15.0):
+    """Oracle restatement of the reference's dense CPU route (dequantize per call,
+    then matmul) on config 0's q_proj shape; one thread."""
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+
+    from oracle import w3
+    from oracle.bf16 import round_bf16
+
+    rng = np.random.default_rng(0)
+    o, k = 4096, 4096
+    g = k // 128
+    layout = {
+        "planes": rng.integers(0, 256, (g, 3, o, 16), dtype=np.uint8),
+        "scales": np.float16(rng.uniform(0.005, 0.02, (g, o))).astype(np.float32),
+        "scale_dtype": "f16", "perm": np.arange(k, dtype=np.int16),
+        "zeros": rng.integers(3, 5, (g, o), dtype=np.uint8),
+    }
+    x = round_bf16(rng.standard_normal((1, k)).astype(np.float32))
+    calls = 0
+    with threadpool_limits(limits=1):
+        start = time.perf_counter()
+        while True:
+            weight = w3.restore_weight(layout, "bf16")
+            _ = x @ weight.T
+            calls += 1
+            elapsed = time.perf_counter() - start
+            if elapsed >= seconds_budget or calls >= 50:
+                break
+    per_call = elapsed / calls
+    nbytes = algorithmic_bytes(o, k)
+    return {"value": round(nbytes / per_call / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"config 0 q_proj 4096x4096 M=1: {calls} calls of oracle restore_weight(bf16) + "
+                      f"x@W.T, {per_call*1e3:.1f} ms/call, numpy single thread"}
+
+
+def main():
+    parser = argparse.ArgumentParser()
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=20)
+    parser.add_argument("--warmup", type=int, default=5)
+    parser.add_argument("--layers", type=int, default=8)
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--shapes", default="all", help="comma list of q/o,k/v,gate/up,down or all")
+    args = parser.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(each box has one MI355X); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from marlin_style_fluxbin_amd import W3Gemv
+    from marlin_style_fluxbin_amd._lib import library
+
+    library()
+    device = torch.device("cuda:0")
+    torch.cuda.set_device(device)
+    stream = torch.cuda.Stream(device)
+
+    # --- per-shape GEMV vs bf16 arm ---------------------------------------------------
+    wanted = list(UNIQUE) if args.shapes == "all" else args.shapes.split(",")
+    shapes = {}
+    for name in wanted:
+        o, k = UNIQUE[name]
+        shapes[name] = bench_shape(o, k, device, max(args.steps, 10), args.warmup, stream)
+        print(f"# {name}: {shapes[name]}", file=sys.stderr, flush=True)
+
+    # --- the step: 7 GEMVs x LAYERS distinct layers, one graph ------------------------
+    gen = torch.Generator(device=device).manual_seed(0)
+    layers = []
+    for _ in range(args.layers):
+        layer = {}
+        for name, (o, k) in SHAPES.items():
+            layer[name] = W3Gemv(make_payload(o, k, device, gen), perm_identity=True)
+        layers.append(layer)
+    xs = {4096: torch.randn(1, 4096, device=device, generator=gen).to(torch.bfloat16),
+          12288: torch.randn(1, 12288, device=device, generator=gen).to(torch.bfloat16)}
+    outs = {name: torch.empty(1, o, device=device, dtype=torch.bfloat16) for name, (o, k) in SHAPES.items()}
+
+    def step():
+        for layer in layers:
+            for name, (o, k) in SHAPES.items():
+                layer[name](xs[k], outs[name])
+
+    graph = capture(step, stream)
+    torch.cuda.synchronize()
+    ms = time_graph(graph, args.steps, args.warmup, stream)
+    step_bytes = args.layers * sum(algorithmic_bytes(o, k) for o, k in SHAPES.values())
+    value = step_bytes / (ms / 1e3) / 1e9
+
+    dominant = shapes.get("gate/up") or next(iter(shapes.values()))
+    result = {
+        "metric": "W3 GEMV HBM GB/s (% of peak) per Qwen3-8B shape; batch-1 decode tokens/sec",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u8 codes, fp32 accumulate, bf16 io",
+        "data": "synthetic (random W3 codes, fp16 scales U[0.005,0.02], zeros U{3,4}, bf16 x ~ N(0,1))",
+        "config": {
+            "workload": f"config 1: 7 Qwen3-8B Linear shapes at M=1 x {args.layers} distinct layers per step",
+            "frac_hbm_peak": round(value / HBM_PEAK_GBPS, 4),
+            "shapes": shapes,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": dominant["w3_GBps"],
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": dominant["w3_frac_hbm"],
+            "traffic": None,
+            "kernel": f"w3_lut_kernel at gate/up {dominant['O']}x{dominant['K']}, M=1",
+        },
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,41 @@
+"""MI355X-native (gfx950) W3 packed-LUT batch-1 decode path.
+
+Drop-in for the deployment API of maxiu188-afk/Marlin_Style_Fluxbin's
+``fluxbin_style`` package: the planar W3 payload (``gptq_deployment``), the W3
+LUT Linear (``w3_lut_deployment``), fused RMSNorm / RoPE (``fused_modules``) and
+the static-KV decode session (``static_decode``).  GPU work runs in hand-written
+HIP kernels behind the C ABI of ``libfluxbin_amd.so`` (``include/fluxbin_amd.h``).
+"""
+from .gptq_deployment import (  # noqa: F401
+    FIELDS,
+    FORMAT,
+    GROUP_SIZE,
+    OPTIONAL_FIELDS,
+    ZERO,
+    bf16_weight_semantics_w3_matvec,
+    convert_gptq_w3_to_planar,
+    decode_planar_w3_codes,
+    inspect_gptq_checkpoint,
+    layout_storage,
+    pack_gptq_w3_codes,
+    planar_from_codes,
+    restore_planar_w3,
+    structural_w3_matvec,
+    unpack_gptq_w3_qweight,
+    unpack_gptq_w3_qzeros,
+    validate_planar_w3,
+)
+from .w3_lut_deployment import (  # noqa: F401
+    PackedW3Linear,
+    W3Gemv,
+    finish,
+    inline_main,
+    load_w3_lut_extension,
+    qwen3_row_tile,
+    qwen3_w3_route,
+    replace_w3_block_linears,
+    w3_lut_m1_out,
+    workspace_shape,
+)
+
+__version__ = "0.1.0"

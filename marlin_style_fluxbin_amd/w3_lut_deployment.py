@@ -1,0 +1,450 @@
+"""W3 LUT Linear on MI355X: functional ops, route policy and ``PackedW3Linear``.
+
+Mirrors the public surface of the reference's ``w3_lut_deployment.py``
+(maxiu188-afk/Marlin_Style_Fluxbin ``src/fluxbin_style/w3_lut_deployment.py:15-417``);
+every GPU call goes to the hand-written gfx950 kernels in ``libfluxbin_amd.so``
+through its C ABI (``include/fluxbin_amd.h``).  There is no CPU substitute on the
+packed route: a missing library raises.
+
+Differences from the reference, all deliberate:
+* ``x`` may carry up to 8 rows on the packed route (config 1's small-M GEMV);
+  the reference sends M > 1 to the dense fallback.
+* The layout may carry ``zeros`` and fp16 scales (see ``gptq_deployment``).
+* ``row_tile`` / ``groups_per_split`` select rows per workgroup and the K split
+  of the reference-shaped functional ops (``inline_main``, ``finish``,
+  ``w3_lut_m1_out``) exactly; the module's own packed route and its prepared
+  decode binding use the single-launch kernel whose K split is reduced inside
+  the launch and whose tiling is chosen from the shape and CU count.
+"""
+from __future__ import annotations
+
+from functools import lru_cache
+
+import torch
+from torch import nn
+from torch.nn import functional as F
+
+from . import _lib
+from .gptq_deployment import FIELDS, OPTIONAL_FIELDS, restore_planar_w3, validate_planar_w3
+
+ROW_TILES = (256, 512, 1024)
+EXPERIMENTAL_ROW_TILES = ROW_TILES
+ARITHMETIC_MODES = ("structural", "decoded_bf16")
+MAX_PACKED_ROWS = 8
+QWEN3_ROW_TILE_BY_SHAPE = {
+    (4096, 4096): 256,
+    (1024, 4096): 512,
+    (12288, 4096): 1024,
+    (4096, 12288): 1024,
+}
+QWEN3_W3_ROUTE_POLICIES = {
+    "structural": {
+        shape: {"row_tile": row_tile, "groups_per_split": 1, "arithmetic": "structural"}
+        for shape, row_tile in QWEN3_ROW_TILE_BY_SHAPE.items()
+    },
+    "fast_corrected": {
+        shape: {"row_tile": row_tile, "groups_per_split": 1, "arithmetic": "decoded_bf16"}
+        for shape, row_tile in QWEN3_ROW_TILE_BY_SHAPE.items()
+    },
+    "observed_exact": {
+        shape: {
+            "row_tile": row_tile,
+            "groups_per_split": {(4096, 4096): 1, (1024, 4096): 1, (12288, 4096): 4, (4096, 12288): 2}[shape],
+            "arithmetic": "decoded_bf16",
+        }
+        for shape, row_tile in QWEN3_ROW_TILE_BY_SHAPE.items()
+    },
+}
+
+
+def _arith_code(arithmetic: str) -> int:
+    if arithmetic not in ARITHMETIC_MODES:
+        raise ValueError(f"arithmetic must be one of {ARITHMETIC_MODES}")
+    return _lib.ARITH_STRUCTURAL if arithmetic == "structural" else _lib.ARITH_DECODED_BF16
+
+
+class _Extension:
+    """Tensor-level view of the C ABI with the reference extension's method names
+    (``csrc/w3_lut.cu:334-339``: inline_main, inline_main_bf16_weight, finish, m1_out)."""
+
+    def __init__(self, row_tile: int):
+        self.row_tile = row_tile
+        self.lib = _lib.library()
+
+    def _main(self, x, planes, scales, perm, partial, arithmetic, zeros=None, groups_per_split=1):
+        g, _, o, _ = planes.shape
+        m, k = x.shape
+        _lib.check(self.lib.fx_w3_inline_main(
+            x.data_ptr(), _lib.dtype_code(x.dtype), planes.data_ptr(), scales.data_ptr(),
+            _lib.dtype_code(scales.dtype), _lib.ptr(zeros), _lib.ptr(perm), partial.data_ptr(),
+            m, o, k, groups_per_split, self.row_tile, arithmetic, _lib.stream_handle(x.device)),
+            "fx_w3_inline_main")
+
+    def inline_main(self, x, planes, scales, perm, partial, zeros=None):
+        self._main(x, planes, scales, perm, partial, _lib.ARITH_STRUCTURAL, zeros)
+
+    def inline_main_bf16_weight(self, x, planes, scales, perm, partial, zeros=None):
+        self._main(x, planes, scales, perm, partial, _lib.ARITH_DECODED_BF16, zeros)
+
+    def finish(self, partial, out):
+        splits = partial.shape[0]
+        m, o = out.shape
+        _lib.check(self.lib.fx_w3_finish(partial.data_ptr(), out.data_ptr(), _lib.dtype_code(out.dtype),
+                                         splits, m, o, _lib.stream_handle(out.device)), "fx_w3_finish")
+
+    def m1_out(self, x, planes, scales, perm, partial, out, groups_per_split, dense_bf16_weight_semantics,
+               zeros=None):
+        g, _, o, _ = planes.shape
+        m, k = x.shape
+        arith = _lib.ARITH_DECODED_BF16 if dense_bf16_weight_semantics else _lib.ARITH_STRUCTURAL
+        _lib.check(self.lib.fx_w3_m1_out(
+            x.data_ptr(), _lib.dtype_code(x.dtype), planes.data_ptr(), scales.data_ptr(),
+            _lib.dtype_code(scales.dtype), _lib.ptr(zeros), _lib.ptr(perm), partial.data_ptr(),
+            out.data_ptr(), m, o, k, groups_per_split, self.row_tile, arith,
+            _lib.stream_handle(x.device)), "fx_w3_m1_out")
+
+
+@lru_cache(maxsize=2 * len(EXPERIMENTAL_ROW_TILES))
+def load_w3_lut_extension(row_tile: int, uniform_index_probe: bool = False):
+    """Return the loaded kernel library for one row tile.
+
+    ``uniform_index_probe`` (the reference's timing-only wrong-result build,
+    ``csrc/w3_lut.cu:17-27``) is not offered: LDS bank conflicts are read from
+    rocprof counters instead, so no build ever returns wrong values on purpose.
+    """
+    if row_tile not in EXPERIMENTAL_ROW_TILES:
+        raise ValueError(f"row_tile must be one of {EXPERIMENTAL_ROW_TILES}")
+    if uniform_index_probe:
+        raise ValueError("the uniform-index probe build is not provided; use rocprof LDS counters")
+    if not torch.cuda.is_available():
+        raise RuntimeError("W3 LUT requires a ROCm GPU; there is no CPU substitute")
+    return _Extension(row_tile)
+
+
+def workspace_shape(out_features: int, in_features: int, groups_per_split: int = 1) -> tuple[int, int]:
+    if not 1 <= out_features <= 65536 or not 128 <= in_features <= 32767 or in_features % 128:
+        raise ValueError("invalid W3 LUT dimensions")
+    groups = in_features // 128
+    if not isinstance(groups_per_split, int) or not 1 <= groups_per_split <= groups:
+        raise ValueError("groups_per_split must be an integer in [1,K/128]")
+    return (groups + groups_per_split - 1) // groups_per_split, out_features
+
+
+def _check_layout_device(layout, *tensors):
+    device = layout["planes"].device
+    if device.type != "cuda":
+        raise ValueError("the W3 LUT kernels require the layout on a ROCm GPU")
+    if any(t.device != device for t in tensors) or any(v.device != device for v in layout.values()):
+        raise ValueError("x, layout and workspace must share a device")
+
+
+def inline_main(x: torch.Tensor, layout: dict, workspace: torch.Tensor, *, row_tile: int,
+                arithmetic: str = "structural") -> None:
+    """fp32 per-group partials ``workspace [K/128, O]`` for ``x [1, K]`` (one split per group)."""
+    out_features, in_features = validate_planar_w3(layout, check_values=False)
+    if x.shape != (1, in_features):
+        raise ValueError("x must have shape [1,K]")
+    if arithmetic not in ARITHMETIC_MODES:
+        raise ValueError(f"arithmetic must be one of {ARITHMETIC_MODES}")
+    if tuple(workspace.shape) != workspace_shape(out_features, in_features) or workspace.dtype != torch.float32:
+        raise ValueError("workspace must be FP32 [K/128,O]")
+    _check_layout_device(layout, x, workspace)
+    ext = load_w3_lut_extension(row_tile)
+    fn = ext.inline_main if arithmetic == "structural" else ext.inline_main_bf16_weight
+    fn(x, layout["planes"], layout["scales"], layout["perm"], workspace, zeros=layout.get("zeros"))
+
+
+def finish(workspace: torch.Tensor, out: torch.Tensor, *, row_tile: int) -> torch.Tensor:
+    if workspace.ndim != 2 or workspace.dtype != torch.float32:
+        raise ValueError("workspace must be FP32 [G,O]")
+    if out.shape != (1, workspace.shape[1]) or out.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError("out must be FP16/BF16 [1,O]")
+    load_w3_lut_extension(row_tile).finish(workspace, out)
+    return out
+
+
+def w3_lut_m1_out(x: torch.Tensor, layout: dict, out: torch.Tensor, workspace: torch.Tensor, *,
+                  row_tile: int, groups_per_split: int = 1, arithmetic: str = "structural") -> torch.Tensor:
+    """Allocation-free GEMV on the current stream with the reference's split semantics.
+
+    ``x [M, K]`` (M in {1, 2, 4, 8}), ``out [M, O]``, ``workspace`` fp32
+    ``[ceil(G/groups_per_split), O]`` for M = 1 (``[splits, M, O]`` otherwise).
+    With one split the workspace is left untouched.
+    """
+    if out.dtype != x.dtype:
+        raise ValueError("out dtype must match x dtype")
+    code = _arith_code(arithmetic)
+    out_features, in_features = validate_planar_w3(layout, check_values=False)
+    if x.ndim != 2 or x.shape[1] != in_features or x.shape[0] not in (1, 2, 4, 8):
+        raise ValueError("x/out shape mismatch")
+    m = x.shape[0]
+    if tuple(out.shape) != (m, out_features):
+        raise ValueError("x/out shape mismatch")
+    splits, _ = workspace_shape(out_features, in_features, groups_per_split)
+    expected = (splits, out_features) if m == 1 else (splits, m, out_features)
+    if tuple(workspace.shape) != expected or workspace.dtype != torch.float32:
+        raise ValueError("workspace must be FP32 [ceil(G/groups_per_split),O]")
+    _check_layout_device(layout, x, out, workspace)
+    load_w3_lut_extension(row_tile).m1_out(
+        x, layout["planes"], layout["scales"], layout["perm"], workspace, out, groups_per_split,
+        code == _lib.ARITH_DECODED_BF16, zeros=layout.get("zeros"))
+    return out
+
+
+def qwen3_row_tile(out_features: int, in_features: int) -> int:
+    try:
+        return QWEN3_ROW_TILE_BY_SHAPE[(out_features, in_features)]
+    except KeyError as exc:
+        raise ValueError(f"unsupported Qwen3-8B W3 shape: {(out_features, in_features)}") from exc
+
+
+def qwen3_w3_route(route: str, out_features: int, in_features: int) -> dict:
+    if route not in QWEN3_W3_ROUTE_POLICIES:
+        raise ValueError(f"unknown Qwen3-8B W3 route: {route}")
+    try:
+        return dict(QWEN3_W3_ROUTE_POLICIES[route][(out_features, in_features)])
+    except KeyError as exc:
+        raise ValueError(f"unsupported Qwen3-8B W3 shape: {(out_features, in_features)}") from exc
+
+
+# --------------------------------------------------------------------------- device helpers
+def restore_planar_w3_device(layout: dict, *, dtype: torch.dtype) -> torch.Tensor:
+    """HIP dequantize of a GPU layout into a new dense ``[O, K]`` weight."""
+    out_features, in_features = validate_planar_w3(layout, check_values=False)
+    weight = torch.empty(out_features, in_features, dtype=dtype, device=layout["planes"].device)
+    restore_planar_w3_into(layout, weight)
+    return weight
+
+
+def restore_planar_w3_into(layout: dict, weight: torch.Tensor) -> torch.Tensor:
+    out_features, in_features = validate_planar_w3(layout, check_values=False)
+    if tuple(weight.shape) != (out_features, in_features) or not weight.is_contiguous():
+        raise ValueError("weight must be a contiguous [O,K] tensor")
+    _check_layout_device(layout, weight)
+    lib = _lib.library()
+    _lib.check(lib.fx_w3_restore(
+        layout["planes"].data_ptr(), layout["scales"].data_ptr(), _lib.dtype_code(layout["scales"].dtype),
+        _lib.ptr(layout.get("zeros")), layout["perm"].data_ptr(), weight.data_ptr(),
+        _lib.dtype_code(weight.dtype), out_features, in_features, _lib.stream_handle(weight.device)),
+        "fx_w3_restore")
+    return weight
+
+
+def gemv_fp32_device(x: torch.Tensor, layout: dict, *, arithmetic: str) -> torch.Tensor:
+    """fp32 ``[M, O]`` from the HIP kernel with one K split (no output cast)."""
+    out_features, in_features = validate_planar_w3(layout, check_values=False)
+    m = x.shape[0]
+    if m not in (1, 2, 4, 8):
+        raise ValueError("fp32 device GEMV supports M in {1,2,4,8}")
+    groups = in_features // 128
+    xin = x if x.dtype in (torch.float16, torch.bfloat16) else x.to(torch.bfloat16)
+    partial = torch.empty(1, m, out_features, dtype=torch.float32, device=x.device)
+    _check_layout_device(layout, x)
+    lib = _lib.library()
+    _lib.check(lib.fx_w3_inline_main(
+        xin.contiguous().data_ptr(), _lib.dtype_code(xin.dtype), layout["planes"].data_ptr(),
+        layout["scales"].data_ptr(), _lib.dtype_code(layout["scales"].dtype), _lib.ptr(layout.get("zeros")),
+        layout["perm"].data_ptr(), partial.data_ptr(), m, out_features, in_features, groups, 256,
+        _arith_code(arithmetic), _lib.stream_handle(x.device)), "fx_w3_inline_main")
+    return partial[0]
+
+
+class W3Gemv:
+    """Allocation-free fast path bound to one payload: ``out = x @ W.T`` in one launch.
+
+    Owns the zero-initialised workspace the single-launch K split needs; calls
+    sharing it must stay ordered on one stream (the decode graph does).
+    """
+
+    def __init__(self, layout: dict, *, arithmetic: str = "structural", max_rows: int = MAX_PACKED_ROWS,
+                 perm_identity: bool | None = None):
+        self.out_features, self.in_features = validate_planar_w3(layout, check_values=False)
+        self.layout = layout
+        self.arith = _arith_code(arithmetic)
+        device = layout["planes"].device
+        if device.type != "cuda":
+            raise ValueError("W3Gemv requires a GPU layout")
+        self.lib = _lib.library()
+        if perm_identity is None:
+            perm = layout["perm"]
+            perm_identity = bool(torch.equal(perm.long(), torch.arange(self.in_features, device=device)))
+        self.perm_ptr = None if perm_identity else layout["perm"].data_ptr()
+        self.zeros_ptr = _lib.ptr(layout.get("zeros"))
+        self.scale_code = _lib.dtype_code(layout["scales"].dtype)
+        self.max_rows = max_rows
+        nbytes = max(self.lib.fx_w3_gemv_workspace_bytes(m, self.out_features, self.in_features)
+                     for m in range(1, max_rows + 1))
+        self.workspace = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=device)
+
+    def __call__(self, x: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
+        m = x.shape[0]
+        _lib.check(self.lib.fx_w3_gemv(
+            x.data_ptr(), _lib.dtype_code(x.dtype), self.layout["planes"].data_ptr(),
+            self.layout["scales"].data_ptr(), self.scale_code, self.zeros_ptr, self.perm_ptr,
+            self.workspace.data_ptr(), self.workspace.numel(), out.data_ptr(), m, self.out_features,
+            self.in_features, self.arith, _lib.stream_handle(x.device)), "fx_w3_gemv")
+        return out
+
+
+class PackedW3Linear(nn.Module):
+    """Decode-oriented W3 Linear with an explicit dense fallback.
+
+    Reference: ``w3_lut_deployment.py:190-359``.  The packed route serves GPU
+    fp16/bf16 inputs with 1..8 rows; anything else raises unless
+    ``fallback='dense'``, which dequantizes (HIP kernel on GPU) and calls
+    ``F.linear``.  ``route_counts`` counts packed calls under ``packed_m1`` for
+    one row and ``packed_small_m`` for 2..8 rows.
+    """
+
+    def __init__(self, layout: dict, *, bias: torch.Tensor | None = None, fallback: str = "error",
+                 row_tile: int | None = None, groups_per_split: int = 1, arithmetic: str = "structural",
+                 route: str = "structural"):
+        super().__init__()
+        if fallback not in {"error", "dense"}:
+            raise ValueError("fallback must be error or dense")
+        self.out_features, self.in_features = validate_planar_w3(layout)
+        self.row_tile = qwen3_row_tile(self.out_features, self.in_features) if row_tile is None else row_tile
+        if self.row_tile not in ROW_TILES:
+            raise ValueError(f"row_tile must be one of {ROW_TILES}")
+        if arithmetic not in ARITHMETIC_MODES:
+            raise ValueError(f"arithmetic must be one of {ARITHMETIC_MODES}")
+        if arithmetic == "decoded_bf16":
+            if layout["scales"].dtype != torch.bfloat16:
+                raise ValueError("decoded_bf16 arithmetic requires bf16 scales")
+            zeros = layout.get("zeros")
+            if zeros is not None and not bool(((zeros == 3) | (zeros == 4)).all()):
+                raise ValueError("decoded_bf16 arithmetic supports zero-points 3 and 4")
+        workspace_shape(self.out_features, self.in_features, groups_per_split)
+        self.groups_per_split = groups_per_split
+        self.arithmetic = arithmetic
+        self.route = route
+        self.fallback = fallback
+        self.route_counts = {"packed_m1": 0, "dense_fallback": 0}
+        self.last_route = "not_called"
+        self._decode_binding = None
+        self._decode_audit = False
+        self._gemv = None
+        perm = layout["perm"]
+        self._perm_identity = bool(torch.equal(perm.long().cpu(), torch.arange(self.in_features)))
+        self._fields = FIELDS + tuple(f for f in OPTIONAL_FIELDS if f in layout)
+        for name in self._fields:
+            self.register_buffer(name, layout[name].detach().clone())
+        self.register_buffer("bias", None if bias is None else bias.detach().clone())
+        self.register_buffer("_decode_output", None, persistent=False)
+
+    def layout(self) -> dict:
+        return {name: getattr(self, name) for name in self._fields}
+
+    def clear_prepared_decode(self) -> None:
+        self._decode_binding = None
+        self._decode_output = None
+        self._decode_audit = False
+
+    def _apply(self, fn, recurse=True):
+        self.clear_prepared_decode()
+        self._gemv = None
+        return super()._apply(fn, recurse=recurse)
+
+    def _kernel(self) -> W3Gemv:
+        if self._gemv is None or self._gemv.layout["planes"].data_ptr() != self.planes.data_ptr():
+            self._gemv = W3Gemv(self.layout(), arithmetic=self.arithmetic, perm_identity=self._perm_identity)
+        return self._gemv
+
+    def bind_prepared_decode(self, dtype: torch.dtype) -> None:
+        if self._decode_binding is not None:
+            raise ValueError("decode already bound")
+        if dtype not in (torch.float16, torch.bfloat16):
+            raise ValueError("FP16/BF16 required")
+        layout = self.layout()
+        device = layout["planes"].device
+        if device.type != "cuda":
+            raise ValueError("prepared decode requires CUDA (a ROCm GPU)")
+        validate_planar_w3(layout, check_values=False)
+        kernel = self._kernel()
+        self._decode_output = torch.empty((1, self.out_features), device=device, dtype=dtype)
+        output = self._decode_output
+        shaped = output.view(1, 1, self.out_features)
+        expected = (1, 1, self.in_features)
+        bias = self.bias
+
+        def apply(x: torch.Tensor) -> torch.Tensor:
+            if torch.is_grad_enabled():
+                raise RuntimeError("prepared decode is inference only")
+            if tuple(x.shape) != expected or x.dtype != dtype or x.device != device or not x.is_contiguous():
+                raise ValueError("prepared decode input shape/dtype/device/stride mismatch")
+            if self._decode_audit:
+                self.route_counts["packed_m1"] += 1
+                self.last_route = "packed_m1"
+            kernel(x.view(1, self.in_features), output)
+            if bias is not None:
+                output.add_(bias)
+            return shaped
+
+        self._decode_binding = apply
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if self._decode_binding is not None:
+            return self._decode_binding(x)
+        if torch.is_grad_enabled():
+            raise RuntimeError("packed inference requires no_grad/inference_mode")
+        if x.ndim < 2 or x.shape[-1] != self.in_features:
+            raise ValueError("expected [...,K] input")
+        m = x.numel() // self.in_features
+        if not (1 <= m <= MAX_PACKED_ROWS) or not x.is_cuda or x.dtype not in (torch.float16, torch.bfloat16):
+            if self.fallback != "dense":
+                raise ValueError("unsupported input; enable explicit dense fallback if needed")
+            self.last_route = "dense_fallback"
+            self.route_counts["dense_fallback"] += 1
+            return F.linear(x, restore_planar_w3(self.layout(), dtype=x.dtype), self.bias)
+        route = "packed_m1" if m == 1 else "packed_small_m"
+        self.last_route = route
+        self.route_counts[route] = self.route_counts.get(route, 0) + 1
+        flat = x.reshape(m, self.in_features).contiguous()
+        output = torch.empty((m, self.out_features), device=x.device, dtype=x.dtype)
+        self._kernel()(flat, output)
+        if self.bias is not None:
+            output.add_(self.bias)
+        return output.reshape(*x.shape[:-1], self.out_features)
+
+
+def replace_w3_block_linears(block, layer_payload, *, fallback: str = "error",
+                             row_tile_by_shape: dict | None = None, route: str = "structural") -> list[str]:
+    """Replace exactly the seven Qwen3 Linears of a block after validating all of them."""
+    from .qwen3 import QWEN3_LINEAR_MODULES
+
+    names_with_zeros = {name for name in QWEN3_LINEAR_MODULES if f"{name}.zeros" in layer_payload}
+    expected = {f"{module}.{field}" for module in QWEN3_LINEAR_MODULES for field in FIELDS}
+    expected |= {f"{module}.zeros" for module in names_with_zeros}
+    if set(layer_payload) != expected:
+        raise ValueError("layer must contain exactly seven complete W3 payloads")
+    if route not in QWEN3_W3_ROUTE_POLICIES:
+        raise ValueError(f"unknown Qwen3-8B W3 route: {route}")
+    row_policy = QWEN3_ROW_TILE_BY_SHAPE if row_tile_by_shape is None else row_tile_by_shape
+    replacements = []
+    for name in QWEN3_LINEAR_MODULES:
+        old = block.get_submodule(name)
+        fields = FIELDS + (("zeros",) if name in names_with_zeros else ())
+        layout = {field: layer_payload[f"{name}.{field}"] for field in fields}
+        out_features, in_features = validate_planar_w3(layout)
+        if not isinstance(old, nn.Linear) or (old.out_features, old.in_features) != (out_features, in_features):
+            raise ValueError(f"Linear shape/type mismatch: {name}")
+        try:
+            row_tile = row_policy[(out_features, in_features)]
+        except KeyError as exc:
+            raise ValueError(f"row-tile policy missing shape: {(out_features, in_features)}") from exc
+        if row_tile_by_shape is None:
+            route_policy = qwen3_w3_route(route, out_features, in_features)
+            if route_policy["row_tile"] != row_tile:
+                raise ValueError("route and row-tile policies disagree")
+        else:
+            route_policy = {"groups_per_split": 1, "arithmetic": "structural"}
+        replacement = PackedW3Linear(
+            layout, bias=old.bias, fallback=fallback, row_tile=row_tile,
+            groups_per_split=route_policy["groups_per_split"], arithmetic=route_policy["arithmetic"],
+            route=route,
+        ).to(old.weight.device)
+        replacements.append((name, replacement))
+    for name, replacement in replacements:
+        parent_name, attribute = name.rsplit(".", 1)
+        setattr(block.get_submodule(parent_name), attribute, replacement)
+    return [name for name, _ in replacements]

@@ -1,0 +1,244 @@
+"""numpy restatement of the W3 g128 planar payload and its GEMV semantics.
+
+TEST INFRASTRUCTURE ONLY (see ``oracle/__init__.py``).
+
+Reference: ``src/fluxbin_style/gptq_deployment.py`` in maxiu188-afk/Marlin_Style_Fluxbin.
+Everything here is written from the format's definition, not from that code's
+shift tables, so the two can disagree if either has a mistake:
+
+* GPTQ int3 packing (``gptq_deployment.py:25-71,331-348``) is a little-endian
+  96-bit bitstream per 32 codes: code ``i`` occupies bits ``3i..3i+2`` of
+  ``word0 | word1 << 32 | word2 << 64``.  Pinned by the reference's boundary KAT
+  (``tests/test_gptq_w3_planar.py:43-60``, re-run in ``tests/test_oracle_w3.py``).
+* Planar layout (``gptq_deployment.py:199-244``): input columns sorted by
+  ``g_idx`` (stable), ``planes[g, p, o, c]`` holds bit ``p`` of the 8 codes
+  ``k = 128 g + 8 c + j`` (``j`` = bit position, LSB first) of output row ``o``;
+  plane 2 is stored inverted.  Pinned by brute force over every byte value and
+  every (code, position) pair.
+* Dequantize (``restore_planar_w3``, ``gptq_deployment.py:247-260``):
+  ``W[o, perm[s]] = round_scale_dtype(scale[g, o] * (q - zero))`` then cast to the
+  output dtype.  The reference fixes ``zero = 4`` and bf16 scales; the benchmark
+  configs add per-group integer zero-points (``zeros`` uint8 ``[G, O]``) and fp16
+  scales, which follow the same formula.  Pinned bitwise against the direct
+  formula of ``tests/test_gptq_w3_planar.py:83-90``.
+* ``matvec_exact`` / ``matvec_decoded`` are float64 dequantize-then-matmul
+  (exact scales, or per-weight rounded weights); pinned by basis-vector inputs,
+  linearity and brute-force loops on tiny shapes.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from .bf16 import round_to
+
+GROUP = 128
+BITS = 3
+ZERO = 4
+
+
+# --------------------------------------------------------------------------- GPTQ int3
+def pack_gptq_w3_codes(codes: np.ndarray, packed_axis: int = 0) -> np.ndarray:
+    """Pack uint8 codes in [0,7] (packed dimension multiple of 32) into int32 words.
+
+    Restates ``pack_gptq_w3_codes`` (``gptq_deployment.py:331-348``) as a bitstream.
+    """
+    codes = np.asarray(codes, dtype=np.uint8)
+    logical = codes if packed_axis == 0 else codes.T
+    if logical.shape[0] % 32 or (logical > 7).any():
+        raise ValueError("packed dimension must be a multiple of 32 and codes must be W3")
+    blocks = logical.astype(np.uint64).reshape(-1, 32, logical.shape[1])
+    words = np.zeros((blocks.shape[0], 3, logical.shape[1]), dtype=np.uint64)
+    for i in range(32):
+        bit = 3 * i
+        for b in range(3):
+            position = bit + b
+            value = (blocks[:, i] >> np.uint64(b)) & np.uint64(1)
+            words[:, position // 32] |= value << np.uint64(position % 32)
+    packed = words.reshape(-1, logical.shape[1]).astype(np.uint32).view(np.int32)
+    return packed if packed_axis == 0 else np.ascontiguousarray(packed.T)
+
+
+def unpack_gptq_w3(words: np.ndarray, packed_axis: int = 0) -> np.ndarray:
+    """Inverse of :func:`pack_gptq_w3_codes` (``gptq_deployment.py:42-77``)."""
+    words = np.asarray(words, dtype=np.int32)
+    logical = words if packed_axis == 0 else words.T
+    if logical.shape[0] % 3:
+        raise ValueError("packed count must be divisible by three")
+    u = logical.view(np.uint32).astype(np.uint64).reshape(-1, 3, logical.shape[1])
+    out = np.zeros((u.shape[0], 32, logical.shape[1]), dtype=np.uint8)
+    for i in range(32):
+        value = np.zeros((u.shape[0], logical.shape[1]), dtype=np.uint64)
+        for b in range(3):
+            position = 3 * i + b
+            value |= ((u[:, position // 32] >> np.uint64(position % 32)) & np.uint64(1)) << np.uint64(b)
+        out[:, i] = value.astype(np.uint8)
+    codes = out.reshape(-1, logical.shape[1])
+    return codes if packed_axis == 0 else np.ascontiguousarray(codes.T)
+
+
+def unpack_gptq_w3_qzeros(qzeros: np.ndarray, qzero_format: int) -> np.ndarray:
+    """Logical zero points ``[G, O]``; format 1 stores ``zero - 1`` (``gptq_deployment.py:80-93``)."""
+    if qzero_format not in (1, 2):
+        raise ValueError("qzero_format must be 1 or 2")
+    zeros = unpack_gptq_w3(qzeros, packed_axis=1)
+    if qzero_format == 1:
+        zeros = ((zeros.astype(np.int16) + 1) & 7).astype(np.uint8)
+    return zeros
+
+
+# --------------------------------------------------------------------------- planar layout
+def pack_bytes_lsb(bits: np.ndarray) -> np.ndarray:
+    """``[..., 128]`` 0/1 -> ``[..., 16]`` uint8, bit ``j`` of byte ``c`` = element ``8c+j``."""
+    bits = np.asarray(bits, dtype=np.uint8)
+    chunks = bits.reshape(*bits.shape[:-1], bits.shape[-1] // 8, 8).astype(np.uint16)
+    weights = (1 << np.arange(8, dtype=np.uint16))
+    return (chunks * weights).sum(-1).astype(np.uint8)
+
+
+def unpack_bytes_lsb(values: np.ndarray) -> np.ndarray:
+    values = np.asarray(values, dtype=np.uint8)
+    bits = (values[..., None] >> np.arange(8, dtype=np.uint8)) & 1
+    return bits.reshape(*values.shape[:-1], values.shape[-1] * 8).astype(np.uint8)
+
+
+def planar_from_codes(codes: np.ndarray, perm: np.ndarray | None = None) -> np.ndarray:
+    """Original-order codes ``[K, O]`` -> planes ``[G, 3, O, 16]``.
+
+    ``perm[s]`` is the original input column at sorted position ``s``
+    (``gptq_deployment.py:209-224``); ``None`` means identity.
+    """
+    codes = np.asarray(codes, dtype=np.uint8)
+    k, o = codes.shape
+    if k % GROUP:
+        raise ValueError("K must be a multiple of 128")
+    sorted_codes = codes if perm is None else codes[np.asarray(perm, dtype=np.int64)]
+    grouped = sorted_codes.reshape(k // GROUP, GROUP, o).transpose(0, 2, 1)  # [G, O, 128]
+    b0 = grouped & 1
+    b1 = (grouped >> 1) & 1
+    b2_inverted = 1 - ((grouped >> 2) & 1)
+    return np.ascontiguousarray(
+        np.stack([pack_bytes_lsb(b0), pack_bytes_lsb(b1), pack_bytes_lsb(b2_inverted)], axis=1)
+    )
+
+
+def codes_from_planar(planes: np.ndarray, perm: np.ndarray | None = None) -> np.ndarray:
+    """planes ``[G,3,O,16]`` -> codes ``[K, O]`` (original order when ``perm`` is given)."""
+    planes = np.asarray(planes, dtype=np.uint8)
+    g, three, o, sixteen = planes.shape
+    if three != 3 or sixteen != 16:
+        raise ValueError("planes must be [G,3,O,16]")
+    b0 = unpack_bytes_lsb(planes[:, 0])
+    b1 = unpack_bytes_lsb(planes[:, 1])
+    b2 = 1 - unpack_bytes_lsb(planes[:, 2])
+    sorted_codes = (b0 | (b1 << 1) | (b2 << 2)).transpose(0, 2, 1).reshape(g * GROUP, o)
+    if perm is None:
+        return np.ascontiguousarray(sorted_codes)
+    out = np.empty_like(sorted_codes)
+    out[np.asarray(perm, dtype=np.int64)] = sorted_codes
+    return out
+
+
+def convert_gptq_w3_to_planar(qweight, qzeros, scales_f16, g_idx, *, qzero_format=1,
+                              scale_dtype="bf16", allow_zeros=False):
+    """Raw GPTQ tensors -> planar layout dict (numpy).
+
+    Follows ``convert_gptq_w3_to_planar`` (``gptq_deployment.py:199-227``): stable
+    argsort of ``g_idx`` gives ``perm``; scales are cast from fp16 to
+    ``scale_dtype``.  With ``allow_zeros`` a non-constant zero-point becomes the
+    ``zeros`` field; without it only zero == 4 is accepted, as in the reference.
+    """
+    codes = unpack_gptq_w3(qweight, 0)
+    zeros = unpack_gptq_w3_qzeros(qzeros, qzero_format)
+    g_idx = np.asarray(g_idx, dtype=np.int64)
+    perm = np.argsort(g_idx, kind="stable")
+    groups = codes.shape[0] // GROUP
+    if not np.array_equal(g_idx[perm], np.repeat(np.arange(groups), GROUP)):
+        raise ValueError("sorted g_idx is not canonical group128")
+    uniform = np.unique(zeros).tolist() == [ZERO]
+    if not uniform and not allow_zeros:
+        raise ValueError("constant-zero layout requires decoded zero=4")
+    scales = round_to(np.asarray(scales_f16, dtype=np.float16).astype(np.float32), scale_dtype)
+    layout = {
+        "planes": planar_from_codes(codes, perm),
+        "scales": scales,
+        "scale_dtype": scale_dtype,
+        "perm": perm.astype(np.int16),
+        "zeros": None if uniform else zeros,
+    }
+    return layout
+
+
+# --------------------------------------------------------------------------- dequantize
+def _zeros_or_default(layout):
+    planes = layout["planes"]
+    zeros = layout.get("zeros")
+    if zeros is None:
+        return np.full((planes.shape[0], planes.shape[2]), ZERO, dtype=np.int16)
+    return np.asarray(zeros, dtype=np.int16)
+
+
+def _expand_groups(per_group: np.ndarray) -> np.ndarray:
+    """``[G, O]`` -> ``[O, K_sorted]`` by repeating each group 128 times along K."""
+    return np.repeat(np.asarray(per_group).T, GROUP, axis=1)
+
+
+def signed_codes_sorted(layout) -> np.ndarray:
+    """``q - zero`` as int16 ``[O, K]`` in sorted-column order."""
+    codes = codes_from_planar(layout["planes"]).T.astype(np.int16)  # [O, K_sorted]
+    return codes - _expand_groups(_zeros_or_default(layout))
+
+
+def _unsort_columns(sorted_weight: np.ndarray, perm) -> np.ndarray:
+    if perm is None:
+        return sorted_weight
+    out = np.empty_like(sorted_weight)
+    out[:, np.asarray(perm, dtype=np.int64)] = sorted_weight
+    return out
+
+
+def restore_weight(layout, out_dtype: str = "bf16") -> np.ndarray:
+    """Dequantize ``[O, K]`` with the reference's per-weight rounding.
+
+    ``round_scale_dtype(scale * (q - zero))`` then ``round_out_dtype`` -- the
+    arithmetic of ``restore_planar_w3`` (``gptq_deployment.py:254-260``), where a
+    bf16 (or fp16) scale tensor times an int16 tensor rounds once to the scale
+    dtype.  Returned as float32 holding ``out_dtype`` values.
+    """
+    signed = signed_codes_sorted(layout).astype(np.float32)
+    scales = _expand_groups(np.asarray(layout["scales"], dtype=np.float32))
+    product = round_to(scales * signed, layout["scale_dtype"])
+    return round_to(_unsort_columns(product, layout.get("perm")), out_dtype)
+
+
+def dequant_exact(layout) -> np.ndarray:
+    """``[O, K]`` float64 ``scale * (q - zero)`` with no rounding."""
+    signed = signed_codes_sorted(layout).astype(np.float64)
+    scales = _expand_groups(np.asarray(layout["scales"], dtype=np.float64))
+    return _unsort_columns(scales * signed, layout.get("perm"))
+
+
+def matvec_exact(x: np.ndarray, layout) -> np.ndarray:
+    """``[M, K] -> [M, O]`` float64 ``x @ (scale*(q-zero)).T`` (the structural truth)."""
+    return np.asarray(x, dtype=np.float64) @ dequant_exact(layout).T
+
+
+def matvec_decoded(x: np.ndarray, layout, weight_dtype: str = "bf16") -> np.ndarray:
+    """float64 dot of ``x`` with the restored (per-weight rounded) weight.
+
+    This is dequantize-then-matmul with exact accumulation: the value
+    ``bf16_weight_semantics_w3_matvec`` approximates in fp32
+    (``gptq_deployment.py:280-315``) and ``F.linear(x, restore_planar_w3(...))``
+    approximates in the matmul's own order.
+    """
+    weight = restore_weight(layout, weight_dtype).astype(np.float64)
+    return np.asarray(x, dtype=np.float64) @ weight.T
+
+
+def layout_storage_bytes(layout) -> int:
+    """Stored bytes: planes + 2-byte scales + 2-byte perm (+ 1-byte zeros)."""
+    planes = layout["planes"]
+    g, _, o, _ = planes.shape
+    total = planes.size + 2 * g * o + 2 * g * GROUP
+    if layout.get("zeros") is not None:
+        total += g * o
+    return total

@@ -1,0 +1,82 @@
+"""Seeded synthetic payloads shared by the tests (not a test module).
+
+``synthetic_raw`` follows the generator of the reference's
+``tests/test_gptq_w3_planar.py:21-39`` (same seed, same draw order), so the raw
+GPTQ tensors equal the ones the reference's own tests use.  ``config_codes``
+draws the benchmark configs' distributions (codes U{0..7}, fp16 scales
+U[0.005,0.02], zero-points U{3,4}).
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from marlin_style_fluxbin_amd.gptq_deployment import pack_gptq_w3_codes
+
+
+def synthetic_raw(*, k=256, o=64, seed=20260916, zero=4):
+    generator = torch.Generator().manual_seed(seed)
+    codes = torch.randint(0, 8, (k, o), generator=generator, dtype=torch.uint8)
+    groups = k // 128
+    zeros = torch.full((groups, o), zero, dtype=torch.uint8)
+    scales = (torch.rand((groups, o), generator=generator) * 0.125 + 0.001).half()
+    activation_order = torch.randperm(k, generator=generator)
+    g_idx = torch.empty(k, dtype=torch.int32)
+    g_idx[activation_order] = torch.arange(groups, dtype=torch.int32).repeat_interleave(128)
+    raw = {
+        "qweight": pack_gptq_w3_codes(codes),
+        "qzeros": pack_gptq_w3_codes(((zeros.to(torch.int16) - 1) & 7).to(torch.uint8), packed_axis=1),
+        "scales": scales,
+        "g_idx": g_idx,
+    }
+    return raw, codes, zeros
+
+
+def config_codes(o: int, k: int, *, seed: int = 0, zeros: bool = True, scale_dtype=torch.float16,
+                 permute: bool = False):
+    """Original-order codes [K,O] uint8, scales [G,O], zeros [G,O] or None, perm or None."""
+    generator = torch.Generator().manual_seed(seed)
+    groups = k // 128
+    codes = torch.randint(0, 8, (k, o), generator=generator, dtype=torch.uint8)
+    scales = (torch.rand((groups, o), generator=generator) * 0.015 + 0.005).to(scale_dtype)
+    zero = torch.randint(3, 5, (groups, o), generator=generator, dtype=torch.uint8) if zeros else None
+    perm = None
+    if permute:
+        # a desc_act-style permutation: each sorted position reads a scattered column
+        perm = torch.randperm(k, generator=generator).to(torch.int16)
+    return codes, scales, zero, perm
+
+
+def layout_from_codes(codes, scales, zeros, perm):
+    """Product-side planar layout (torch, CPU) for original-order codes."""
+    from marlin_style_fluxbin_amd.gptq_deployment import planar_from_codes
+
+    k = codes.shape[0]
+    perm_t = torch.arange(k, dtype=torch.int16) if perm is None else perm
+    layout = {
+        "planes": planar_from_codes(codes, perm_t.to(torch.int64)),
+        "scales": scales.contiguous(),
+        "perm": perm_t.contiguous(),
+    }
+    if zeros is not None:
+        layout["zeros"] = zeros.contiguous()
+    return layout
+
+
+def oracle_layout(layout):
+    """numpy view of a torch layout for the oracle."""
+    scales = layout["scales"]
+    return {
+        "planes": layout["planes"].cpu().numpy(),
+        "scales": scales.float().cpu().numpy(),
+        "scale_dtype": "bf16" if scales.dtype == torch.bfloat16 else "f16",
+        "perm": layout["perm"].cpu().numpy(),
+        "zeros": None if layout.get("zeros") is None else layout["zeros"].cpu().numpy(),
+    }
+
+
+def max_rel(actual, expected) -> float:
+    """Normwise max relative error max|a-b| / max|b| in float64."""
+    a = np.asarray(actual, dtype=np.float64)
+    b = np.asarray(expected, dtype=np.float64)
+    return float(np.abs(a - b).max() / max(np.abs(b).max(), 1e-30))

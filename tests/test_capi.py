@@ -1,0 +1,54 @@
+"""The C-ABI library loads and exports exactly what include/fluxbin_amd.h declares.
+
+CPU-only: argument validation returns FX_EINVAL before any device call, so no
+kernel is launched here.
+"""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from marlin_style_fluxbin_amd import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "fluxbin_amd.h"
+
+
+def declared_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(fx_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.library()
+    names = declared_functions()
+    assert "fx_w3_gemv" in names and "fx_w3_restore" in names
+    for name in names:
+        assert hasattr(lib, name), name
+    assert set(names) == set(_lib.SIGNATURES), "ctypes signature table out of sync with the header"
+    assert lib.fx_abi_version() == _lib.ABI_VERSION
+
+
+def test_invalid_arguments_fail_closed_without_launching():
+    lib = _lib.library()
+    rc = lib.fx_w3_gemv(None, 2, None, None, 2, None, None, None, 0, None, 1, 64, 256, 0, None)
+    assert rc == 1
+    assert "non-null" in lib.fx_last_error().decode()
+    dummy = ctypes.c_void_p(4096)
+    rc = lib.fx_w3_gemv(dummy, 2, dummy, dummy, 2, None, None, None, 0, dummy, 1, 64, 100, 0, None)
+    assert rc == 1 and "multiple of 128" in lib.fx_last_error().decode()
+    rc = lib.fx_w3_gemv(dummy, 2, ctypes.c_void_p(4097), dummy, 2, None, None, None, 0, dummy, 1, 64, 256, 0, None)
+    assert rc == 1 and "aligned" in lib.fx_last_error().decode()
+    rc = lib.fx_w3_gemv(dummy, 2, dummy, dummy, 1, None, None, None, 0, dummy, 1, 64, 256, 1, None)
+    assert rc == 1 and "bf16 scales" in lib.fx_last_error().decode()
+    rc = lib.fx_w3_m1_out(dummy, 2, dummy, dummy, 2, None, None, None, dummy, 1, 64, 256, 1, 300, 0, None)
+    assert rc == 1 and "row_tile" in lib.fx_last_error().decode()
+    assert lib.fx_w3_gemv_tile_workspace_bytes(1, 4096, 4096, 1, 32) == 0
+    assert lib.fx_w3_gemv_tile_workspace_bytes(1, 4096, 4096, 1, 1) == 256 + 32 * 4096 * 4
+
+
+def test_check_raises_runtime_error_with_message():
+    lib = _lib.library()
+    rc = lib.fx_w3_finish(None, None, 2, 1, 1, 1, None)
+    with pytest.raises(RuntimeError, match="non-null"):
+        _lib.check(rc, "fx_w3_finish")

@@ -1,0 +1,209 @@
+"""GPU parity of the HIP W3 GEMV against the oracle (runs on the MI355X box).
+
+Truths (oracle/w3.py, pinned in tests/test_oracle_w3.py):
+* ``matvec_exact``   float64 x @ (s*(q-z)).T -- the structural route's target;
+* ``matvec_decoded`` float64 x @ restore(W).T -- dequantize-then-matmul, the
+  decoded_bf16 route's target and the reference's dense fallback value.
+Tolerances (normwise max relative error, max|a-b|/max|b|):
+* fp32 kernel results (single K split, no output cast) vs their own truth: 1e-5;
+* fp16/bf16 outputs vs their own truth: 2^-8 (one output rounding) + 1e-5;
+* any route vs dequantize-then-matmul: 1e-3 (fp32) / 1e-2 (bf16), the stated bar.
+"""
+import numpy as np
+import pytest
+import torch
+
+from marlin_style_fluxbin_amd import (
+    PackedW3Linear, W3Gemv, bf16_weight_semantics_w3_matvec, restore_planar_w3, structural_w3_matvec,
+    w3_lut_m1_out, workspace_shape,
+)
+from oracle import w3
+from tests.payloads import config_codes, layout_from_codes, max_rel, oracle_layout
+
+pytestmark = pytest.mark.gpu
+
+FP32_TOL = 1e-5
+HALF_TOL = 2.0 ** -8 + 1e-5
+
+
+def _setup(o, k, *, seed=0, zeros=True, scale_dtype=torch.bfloat16, permute=False, device="cuda"):
+    codes, scales, z, perm = config_codes(o, k, seed=seed, zeros=zeros, scale_dtype=scale_dtype, permute=permute)
+    layout = layout_from_codes(codes, scales, z, perm)
+    return layout, {name: t.to(device) for name, t in layout.items()}, oracle_layout(layout)
+
+
+def _x(m, k, dtype, seed=1):
+    return torch.randn(m, k, generator=torch.Generator().manual_seed(seed)).to(dtype)
+
+
+SMALL = [(64, 256), (288, 384), (1, 128), (17, 256), (65, 384), (1025, 512), (300, 1280)]
+
+
+@pytest.mark.parametrize("o,k", SMALL)
+@pytest.mark.parametrize("m", [1, 2, 4, 8])
+@pytest.mark.parametrize("zeros,permute", [(False, False), (True, True)])
+def test_structural_fp32_matches_exact(gpu, o, k, m, zeros, permute):
+    layout, dl, ol = _setup(o, k, seed=o + k, zeros=zeros, permute=permute)
+    x = _x(m, k, torch.bfloat16, seed=m)
+    got = structural_w3_matvec(x.to(gpu), dl).cpu().numpy()
+    assert max_rel(got, w3.matvec_exact(x.float().numpy(), ol)) <= FP32_TOL
+
+
+@pytest.mark.parametrize("o,k", SMALL)
+@pytest.mark.parametrize("zeros", [False, True])
+def test_decoded_fp32_matches_dequantize_then_matmul(gpu, o, k, zeros):
+    layout, dl, ol = _setup(o, k, seed=3 * o + k, zeros=zeros)
+    x = _x(1, k, torch.bfloat16, seed=o)
+    got = bf16_weight_semantics_w3_matvec(x.to(gpu), dl).cpu().numpy()
+    assert max_rel(got, w3.matvec_decoded(x.float().numpy(), ol, "bf16")) <= FP32_TOL
+
+
+@pytest.mark.parametrize("o,k", SMALL)
+@pytest.mark.parametrize("m", [1, 3, 8])
+@pytest.mark.parametrize("xdtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("scale_dtype", [torch.bfloat16, torch.float16])
+def test_fused_fast_path(gpu, o, k, m, xdtype, scale_dtype):
+    layout, dl, ol = _setup(o, k, seed=o * 7 + m, zeros=True, scale_dtype=scale_dtype, permute=True)
+    x = _x(m, k, xdtype, seed=k + m)
+    gemv = W3Gemv(dl)
+    out = torch.full((m, o), float("nan"), dtype=xdtype, device=gpu)
+    gemv(x.to(gpu), out)
+    exact = w3.matvec_exact(x.float().numpy(), ol)
+    got = out.float().cpu().numpy()
+    assert max_rel(got, exact) <= HALF_TOL
+    # a second call through the same workspace is bit-identical (counters reset)
+    again = torch.empty_like(out)
+    gemv(x.to(gpu), again)
+    assert torch.equal(out, again)
+
+
+@pytest.mark.parametrize("row_tile", [256, 512, 1024])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_reference_split_contract(gpu, row_tile, dtype):
+    """Reference tests/test_w3_lut_correctness.py:51-135: NaN-poisoned workspace,
+    repeat-exact after re-poisoning, graph replay bit-equality, both arithmetics."""
+    for out_features, in_features in ((32, 128), (64, 256), (288, 384)):
+        layout, dl, ol = _setup(out_features, in_features, seed=out_features, zeros=False)
+        x = _x(1, in_features, dtype, seed=in_features).to(gpu)
+        exact = w3.matvec_exact(x.float().cpu().numpy(), ol)
+        for gps in sorted({1, in_features // 128}):
+            out = torch.empty(1, out_features, device=gpu, dtype=dtype)
+            workspace = torch.full(workspace_shape(out_features, in_features, gps), float("nan"), device=gpu)
+
+            def run():
+                return w3_lut_m1_out(x, dl, out, workspace, row_tile=row_tile, groups_per_split=gps)
+
+            run()
+            torch.cuda.synchronize()
+            if workspace.shape[0] == 1:
+                assert torch.isnan(workspace).all()
+            else:
+                assert torch.isfinite(workspace).all()
+            assert max_rel(out.float().cpu().numpy(), exact) <= HALF_TOL
+            saved = out.clone()
+            workspace.fill_(float("nan"))
+            run()
+            assert torch.equal(out, saved)
+            graph = torch.cuda.CUDAGraph()
+            for _ in range(3):
+                run()
+            torch.cuda.synchronize()
+            with torch.cuda.graph(graph):
+                run()
+            for _ in range(3):
+                out.zero_()
+                graph.replay()
+                torch.cuda.synchronize()
+                assert torch.equal(out, saved)
+        if dtype == torch.bfloat16:
+            decoded = w3.matvec_decoded(x.float().cpu().numpy(), ol, "bf16")
+            for gps in (1, in_features // 128):
+                corrected = torch.empty(1, out_features, device=gpu, dtype=dtype)
+                ws = torch.full(workspace_shape(out_features, in_features, gps), float("nan"), device=gpu)
+                w3_lut_m1_out(x, dl, corrected, ws, row_tile=256, groups_per_split=gps, arithmetic="decoded_bf16")
+                assert max_rel(corrected.float().cpu().numpy(), decoded) <= HALF_TOL
+
+
+def test_fused_path_graph_replays_track_input(gpu):
+    """Graph-captured single-launch GEMV: every replay equals the eager result for
+    the current input (the in-launch split counters must reset every time)."""
+    layout, dl, ol = _setup(4096, 4096, seed=11, zeros=True, scale_dtype=torch.float16)
+    gemv = W3Gemv(dl)
+    x = _x(1, 4096, torch.bfloat16, seed=12).to(gpu)
+    out = torch.empty(1, 4096, dtype=torch.bfloat16, device=gpu)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        for _ in range(3):
+            gemv(x, out)
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        gemv(x, out)
+    for step in range(4):
+        x.mul_(0.5 if step % 2 else -1.25)
+        eager = torch.empty_like(out)
+        gemv(x, eager)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), step
+
+
+QWEN3_SHAPES = [(4096, 4096), (1024, 4096), (12288, 4096), (4096, 12288)]
+
+
+@pytest.mark.parametrize("o,k", QWEN3_SHAPES)
+@pytest.mark.parametrize("m", [1, 2, 4, 8])
+def test_qwen3_shapes_config1(gpu, o, k, m):
+    """Config 1: every Qwen3-8B Linear shape, W3 g128, fp16 scales, zeros U{3,4}."""
+    layout, dl, ol = _setup(o, k, seed=0, zeros=True, scale_dtype=torch.float16)
+    x = _x(m, k, torch.bfloat16, seed=0)
+    exact = w3.matvec_exact(x.float().numpy(), ol)
+    if m in (1, 2, 4, 8):
+        got32 = structural_w3_matvec(x.to(gpu), dl).cpu().numpy()
+        assert max_rel(got32, exact) <= FP32_TOL
+    gemv = W3Gemv(dl)
+    out = torch.empty(m, o, dtype=torch.bfloat16, device=gpu)
+    gemv(x.to(gpu), out)
+    got = out.float().cpu().numpy()
+    assert max_rel(got, exact) <= HALF_TOL
+    # the stated bar against dequantize-then-matmul (bf16 weights from fp16 scales)
+    decoded = w3.matvec_decoded(x.float().numpy(), ol, "bf16")
+    assert max_rel(got, decoded) <= 1e-2
+
+
+def test_config0_q_proj_seed0(gpu):
+    """Config 0: q_proj 4096x4096, x N(0,1) bf16, fp16 scales U[0.005,0.02], zeros U{3,4}, seed 0."""
+    layout, dl, ol = _setup(4096, 4096, seed=0, zeros=True, scale_dtype=torch.float16)
+    x = _x(1, 4096, torch.bfloat16, seed=0)
+    module = PackedW3Linear(dl, row_tile=256)
+    with torch.inference_mode():
+        y = module(x.to(gpu))
+    assert module.route_counts == {"packed_m1": 1, "dense_fallback": 0}
+    exact = w3.matvec_exact(x.float().numpy(), ol)
+    assert max_rel(y.float().cpu().numpy(), exact) <= HALF_TOL
+    got32 = structural_w3_matvec(x.to(gpu), dl).cpu().numpy()
+    assert max_rel(got32, exact) <= FP32_TOL
+
+
+@pytest.mark.parametrize("scale_dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("weight_dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("zeros", [False, True])
+def test_restore_kernel_bitwise(gpu, scale_dtype, weight_dtype, zeros):
+    layout, dl, ol = _setup(96, 384, seed=9, zeros=zeros, scale_dtype=scale_dtype, permute=True)
+    got = restore_planar_w3(dl, dtype=weight_dtype).float().cpu().numpy()
+    expected = w3.restore_weight(ol, "bf16" if weight_dtype == torch.bfloat16 else "f16")
+    assert np.array_equal(got, expected)
+
+
+def test_dense_fallback_on_gpu_uses_device_restore(gpu):
+    layout, dl, ol = _setup(64, 256, seed=4, zeros=False)
+    module = PackedW3Linear(dl, fallback="dense", row_tile=256)
+    x = _x(16, 256, torch.bfloat16, seed=4).to(gpu)
+    with torch.inference_mode():
+        y = module(x)
+    assert module.route_counts["dense_fallback"] == 1
+    decoded = w3.matvec_decoded(x.float().cpu().numpy(), ol, "bf16")
+    assert max_rel(y.float().cpu().numpy(), decoded) <= 1e-2
