@@ -60,18 +60,20 @@ def make_payload(o, k, device, generator):
 
 
 def time_graph(graph, steps, warmup, stream):
+    """ms per replay; replays and both events are issued on ``stream``."""
     import torch
 
-    for _ in range(warmup):
-        graph.replay()
+    with torch.cuda.stream(stream):
+        for _ in range(warmup):
+            graph.replay()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(steps):
+            graph.replay()
+        end.record(stream)
     torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record(stream)
-    for _ in range(steps):
-        graph.replay()
-    end.record(stream)
-    torch.cuda.synchronize()
-    return start.elapsed_time(end) / steps  # ms per replay
+    return start.elapsed_time(end) / steps
 
 
 def capture(fn, stream):

@@ -74,26 +74,32 @@ int fx_w3_m1_out(const void *x, int x_dtype, const uint8_t *planes, const void *
                  int arithmetic, void *stream);
 
 /*
- * Fast path used by the prepared decode binding (PackedW3Linear.bind_prepared_decode,
- * w3_lut_deployment.py:250-317): one launch, K split and reduced inside the
- * launch.  The tiling is chosen from (M, O, K) and the device's CU count.
- * workspace: fx_w3_gemv_workspace_bytes(M, O, K) bytes, zero-filled once by the
- * caller before first use (the library leaves its counters zeroed).  Calls that
- * share a workspace must be ordered on one stream.
+ * Fast path used by PackedW3Linear and its prepared decode binding
+ * (w3_lut_deployment.py:250-359 in the reference).  structural arithmetic: the
+ * gfx950 MFMA kernel -- codes dequantized in registers to bf16/fp16 subnormal
+ * MFMA operands against exact activations, fp32 accumulation, K split over the
+ * waves of a workgroup (and over workgroups with a stream-ordered finish when
+ * the output has fewer 16-row tiles than CUs); one small x-packing launch per
+ * call.  decoded_bf16 arithmetic: the LUT kernel plus finish.  Tiling comes
+ * from (M, O, K) and the CU count.  workspace: fx_w3_gemv_workspace_bytes(M, O,
+ * K) bytes, 256-byte aligned, no initial contents required.  Calls that share a
+ * workspace must be ordered on one stream.
  */
 size_t fx_w3_gemv_workspace_bytes(int M, int O, int K);
 int fx_w3_gemv(const void *x, int x_dtype, const uint8_t *planes, const void *scales,
                int scale_dtype, const uint8_t *zeros, const int16_t *perm, void *workspace,
                size_t workspace_bytes, void *out, int M, int O, int K, int arithmetic,
                void *stream);
-/* Same with an explicit tile (rows_per_thread in {1,2,4}, groups_per_split >= 1);
- * used by the benchmark sweep.  Workspace from fx_w3_gemv_tile_workspace_bytes. */
-size_t fx_w3_gemv_tile_workspace_bytes(int M, int O, int K, int rows_per_thread,
-                                       int groups_per_split);
-int fx_w3_gemv_tile(const void *x, int x_dtype, const uint8_t *planes, const void *scales,
-                    int scale_dtype, const uint8_t *zeros, const int16_t *perm, void *workspace,
-                    size_t workspace_bytes, void *out, int M, int O, int K, int arithmetic,
-                    int rows_per_thread, int groups_per_split, void *stream);
+/* Structural MFMA path with an explicit tiling (benchmark sweeps): waves per
+ * workgroup in {2,4,8}, 16-row tiles per wave in {1,2} (2 needs 4 or 8 waves),
+ * groups per K split (rounded up to a multiple of 4, clamped to the padded group
+ * count). */
+size_t fx_w3_gemv_config_workspace_bytes(int M, int O, int K, int waves, int tiles_per_wave,
+                                         int groups_per_split);
+int fx_w3_gemv_config(const void *x, int x_dtype, const uint8_t *planes, const void *scales,
+                      int scale_dtype, const uint8_t *zeros, const int16_t *perm,
+                      void *workspace, size_t workspace_bytes, void *out, int M, int O, int K,
+                      int waves, int tiles_per_wave, int groups_per_split, void *stream);
 
 /*
  * Reference: restore_planar_w3 (gptq_deployment.py:247-260), the dequantize

@@ -1,8 +1,8 @@
 // extern "C" boundary of libfluxbin_amd.so (declarations: include/fluxbin_amd.h).
 // Validates arguments, picks kernel instantiations and tilings, launches on the
 // caller's stream.  Nothing here allocates or synchronises.
-#include <cstdio>
 #include <cstdarg>
+#include <cstdio>
 #include <cstring>
 #include <mutex>
 
@@ -10,8 +10,10 @@
 #include "common.h"
 #include "w3_lut_launch.h"
 #include "w3_lut.hip"
+#include "w3_mfma_launch.h"
 
 using fx::LutArgs;
+using fx::MfmaArgs;
 
 namespace {
 
@@ -67,6 +69,9 @@ int validate_payload(const void* x, int x_dtype, const uint8_t* planes, const vo
   return FX_OK;
 }
 
+size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// ------------------------------------------------------------------ LUT kernel
 int rows_per_thread_from_tile(int row_tile) {
   switch (row_tile) {
     case 256: return 1;
@@ -76,17 +81,15 @@ int rows_per_thread_from_tile(int row_tile) {
   }
 }
 
-// Largest supported activation-row block not above m.
-int m_block_for(int m) { return m >= 8 ? 8 : m >= 4 ? 4 : m >= 2 ? 2 : 1; }
+// Largest supported LUT activation-row block not above m.
+int lut_block_for(int m) { return m >= 8 ? 8 : m >= 4 ? 4 : m >= 2 ? 2 : 1; }
 
-size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
-
-struct Tile {
+struct LutTile {
   int rpt, gps, splits, row_tiles;
 };
 
-Tile make_tile(int O, int G, int rpt, int gps) {
-  Tile t;
+LutTile make_lut_tile(int O, int G, int rpt, int gps) {
+  LutTile t;
   t.rpt = rpt;
   t.gps = gps < 1 ? 1 : (gps > G ? G : gps);
   t.splits = (G + t.gps - 1) / t.gps;
@@ -94,63 +97,192 @@ Tile make_tile(int O, int G, int rpt, int gps) {
   return t;
 }
 
-// Default tiling: one row per thread, enough K splits to give every CU about
-// two workgroups.
-Tile default_tile(int M, int O, int K) {
-  const int G = K / 128;
-  const int rpt = 1;
-  const int row_tiles = (O + fx::kLutThreads * rpt - 1) / (fx::kLutThreads * rpt);
-  const int target = 2 * device_cu_count();
-  int splits = (target + row_tiles - 1) / row_tiles;
-  if (splits < 1) splits = 1;
-  if (splits > G) splits = G;
-  const int gps = (G + splits - 1) / splits;
-  (void)M;
-  return make_tile(O, G, rpt, gps);
+// LUT tiling for the decoded route: one row per thread, enough K splits for
+// about two workgroups per CU.
+LutTile default_lut_tile(int O, int G) {
+  const int row_tiles = (O + fx::kLutThreads - 1) / fx::kLutThreads;
+  int splits = (2 * device_cu_count() + row_tiles - 1) / row_tiles;
+  splits = splits < 1 ? 1 : (splits > G ? G : splits);
+  return make_lut_tile(O, G, 1, (G + splits - 1) / splits);
 }
 
-size_t fused_workspace_bytes(int M, int O, const Tile& t) {
-  if (t.splits == 1) return 0;
-  const int mb = m_block_for(M);
-  return align_up(size_t(t.row_tiles) * sizeof(unsigned), 256) +
-         size_t(t.splits) * size_t(mb) * size_t(O) * sizeof(float);
-}
-
-// Launch the GEMV over all M rows in blocks of 8/4/2/1 activation rows.
+// Direct (one split) or partial mode over M rows in LUT blocks of 8/4/2/1.
+// In partial mode block b writes partial[s][m][o] of its own [splits, mb, O] slice.
 int run_lut(const void* x, int x_dtype, const uint8_t* planes, const void* scales, int scale_dtype,
-            const uint8_t* zeros, const int16_t* perm, float* partial, unsigned* counters,
-            void* out, int M, int O, int K, int arithmetic, const Tile& tile, int mode,
-            hipStream_t stream) {
+            const uint8_t* zeros, const int16_t* perm, float* partial, void* out, int M, int O,
+            int K, int arithmetic, const LutTile& tile, bool partial_mode, hipStream_t stream) {
   const int G = K / 128;
   const bool dec = arithmetic == FX_ARITH_DECODED_BF16;
   int done = 0;
   while (done < M) {
-    const int mb = m_block_for(M - done);
+    const int mb = lut_block_for(M - done);
     LutArgs a;
     a.x = static_cast<const uint16_t*>(x) + size_t(done) * K;
     a.planes = planes;
     a.scales = static_cast<const uint16_t*>(scales);
     a.zeros = zeros;
     a.perm = perm;
-    a.partial = partial;
-    a.counters = counters;
-    a.out = static_cast<uint16_t*>(out) + size_t(done) * O;
+    a.partial = partial ? partial + size_t(tile.splits) * size_t(done) * O : nullptr;
+    a.out = out ? static_cast<uint16_t*>(out) + size_t(done) * O : nullptr;
     a.O = O;
     a.G = G;
     a.gps = tile.gps;
-    a.splits = tile.splits;
-    a.mode = tile.splits == 1 && mode != fx::kModePartial ? fx::kModeDirect : mode;
-    // In partial mode each M block writes its own slice of the [splits, M, O]
-    // buffer; the kernel indexes partial[(s*mb + m)*O + o], so blocks after the
-    // first use a separate region.
-    if (mode == fx::kModePartial && partial)
-      a.partial = partial + size_t(tile.splits) * size_t(done) * O;
+    a.mode = partial_mode ? fx::kModePartial : fx::kModeDirect;
     const dim3 grid(tile.row_tiles, tile.splits);
     if (!fx::dispatch_lut(mb, tile.rpt, x_dtype, scale_dtype, dec, a, grid, stream))
-      return fail(FX_EINVAL, "no kernel for M-block %d rpt %d dtypes %d/%d", mb, tile.rpt,
+      return fail(FX_EINVAL, "no LUT kernel for M-block %d rpt %d dtypes %d/%d", mb, tile.rpt,
                   x_dtype, scale_dtype);
     int rc = check_launch("w3_lut_kernel");
     if (rc) return rc;
+    done += mb;
+  }
+  return FX_OK;
+}
+
+int launch_finish(const float* partial, void* out, int out_dtype, int splits, int MO,
+                  hipStream_t s) {
+  const dim3 grid((MO + 255) / 256);
+  if (out_dtype == FX_BF16)
+    hipLaunchKernelGGL(fx::w3_finish_kernel<fx::kBF16>, grid, dim3(256), 0, s, partial,
+                       static_cast<uint16_t*>(out), MO, splits);
+  else
+    hipLaunchKernelGGL(fx::w3_finish_kernel<fx::kF16>, grid, dim3(256), 0, s, partial,
+                       static_cast<uint16_t*>(out), MO, splits);
+  return check_launch("w3_finish_kernel");
+}
+
+// Decoded route for the fast entry point: LUT partials + finish (or direct).
+size_t lut_route_workspace(int M, int O, int K) {
+  const LutTile t = default_lut_tile(O, K / 128);
+  if (t.splits == 1) return 0;
+  return size_t(t.splits) * size_t(lut_block_for(M)) * size_t(O) * sizeof(float);
+}
+
+int run_lut_route(const void* x, int x_dtype, const uint8_t* planes, const void* scales,
+                  int scale_dtype, const uint8_t* zeros, const int16_t* perm, void* workspace,
+                  size_t workspace_bytes, void* out, int M, int O, int K, int arithmetic,
+                  hipStream_t s) {
+  const LutTile tile = default_lut_tile(O, K / 128);
+  if (tile.splits == 1)
+    return run_lut(x, x_dtype, planes, scales, scale_dtype, zeros, perm, nullptr, out, M, O, K,
+                   arithmetic, tile, false, s);
+  const size_t need = lut_route_workspace(M, O, K);
+  if (!workspace || workspace_bytes < need)
+    return fail(FX_EINVAL, "workspace needs %zu bytes, got %zu", need, workspace_bytes);
+  float* partial = static_cast<float*>(workspace);
+  int done = 0;
+  while (done < M) {  // finish per LUT block: each block's partials are [splits, mb, O]
+    const int mb = lut_block_for(M - done);
+    const void* xb = static_cast<const uint16_t*>(x) + size_t(done) * K;
+    void* ob = static_cast<uint16_t*>(out) + size_t(done) * O;
+    int rc = run_lut(xb, x_dtype, planes, scales, scale_dtype, zeros, perm, partial, nullptr, mb,
+                     O, K, arithmetic, tile, true, s);
+    if (rc) return rc;
+    rc = launch_finish(partial, ob, x_dtype, tile.splits, mb * O, s);
+    if (rc) return rc;
+    done += mb;
+  }
+  return FX_OK;
+}
+
+// ------------------------------------------------------------------ MFMA kernel
+struct MfmaPlan {
+  int nw, tr, gps, splits, row_tiles;
+};
+
+int mfma_chunk_for(int m) { return m >= 4 ? 4 : m >= 2 ? 2 : 1; }
+
+MfmaPlan make_mfma_plan(int O, int G, int nw, int tr, int gps) {
+  MfmaPlan p;
+  p.nw = nw;
+  p.tr = tr;
+  const int gmax = (G + 3) / 4 * 4;
+  p.gps = gps < 4 ? 4 : (gps + 3) / 4 * 4;
+  if (p.gps > gmax) p.gps = gmax;
+  p.splits = (G + p.gps - 1) / p.gps;
+  p.row_tiles = (O + 16 * tr - 1) / (16 * tr);
+  return p;
+}
+
+// Default: 16-row tiles, K split over the waves of a workgroup, and over
+// workgroups only when there are fewer row tiles than CUs.
+MfmaPlan default_mfma_plan(int O, int G) {
+  const int cus = device_cu_count();
+  const int row_tiles = (O + 15) / 16;
+  const int batches = (G + 3) / 4;
+  int splits = 1;
+  if (row_tiles < cus) splits = (cus + row_tiles - 1) / row_tiles;
+  if (splits > batches) splits = batches;
+  const int per_split = (batches + splits - 1) / splits;  // batches per workgroup
+  const int nw = per_split >= 8 ? 8 : per_split >= 4 ? 4 : 2;
+  return make_mfma_plan(O, G, nw, 1, per_split * 4);
+}
+
+struct MfmaWorkspace {
+  size_t xs, sx, fe, partial, total;
+};
+
+MfmaWorkspace mfma_workspace(int M, int O, int G, const MfmaPlan& p) {
+  const int mb = mfma_chunk_for(M);
+  MfmaWorkspace w;
+  w.xs = 0;
+  w.sx = align_up(size_t(G) * 256 * mb, 256);
+  w.fe = w.sx + align_up(size_t(G) * mb * sizeof(float), 256);
+  w.partial = w.fe + 256;
+  w.total = w.partial + (p.splits > 1 ? size_t(p.splits) * mb * O * sizeof(float) : 0);
+  return w;
+}
+
+int run_mfma(const void* x, int x_dtype, const uint8_t* planes, const void* scales,
+             int scale_dtype, const uint8_t* zeros, const int16_t* perm, void* workspace,
+             size_t workspace_bytes, void* out, int M, int O, int K, const MfmaPlan& p,
+             hipStream_t s) {
+  const int G = K / 128;
+  const MfmaWorkspace w = mfma_workspace(M, O, G, p);
+  if (!workspace || workspace_bytes < w.total)
+    return fail(FX_EINVAL, "workspace needs %zu bytes, got %zu", w.total, workspace_bytes);
+  if (reinterpret_cast<uintptr_t>(workspace) % 256 != 0)
+    return fail(FX_EINVAL, "workspace must be 256-byte aligned");
+  const size_t lds = fx::mfma_lds_bytes(p.nw, p.tr, mfma_chunk_for(M), p.gps < G ? p.gps : G);
+  if (lds > 160 * 1024) return fail(FX_EINVAL, "K slice too large for LDS (%zu bytes)", lds);
+  char* base = static_cast<char*>(workspace);
+  uint16_t* xs = reinterpret_cast<uint16_t*>(base + w.xs);
+  float* sx = reinterpret_cast<float*>(base + w.sx);
+  int* fe = reinterpret_cast<int*>(base + w.fe);
+  float* partial = p.splits > 1 ? reinterpret_cast<float*>(base + w.partial) : nullptr;
+  int done = 0;
+  while (done < M) {
+    const int mb = mfma_chunk_for(M - done);
+    const uint16_t* xb = static_cast<const uint16_t*>(x) + size_t(done) * K;
+    uint16_t* ob = static_cast<uint16_t*>(out) + size_t(done) * O;
+    if (!fx::launch_xprep(x_dtype, xb, perm, xs, sx, fe, K, mb, s))
+      return fail(FX_EINVAL, "no x packer for dtype %d", x_dtype);
+    int rc = check_launch("w3_xprep_kernel");
+    if (rc) return rc;
+    MfmaArgs a;
+    a.planes = planes;
+    a.scales = static_cast<const uint16_t*>(scales);
+    a.zeros = zeros;
+    a.xs = xs;
+    a.sx = sx;
+    a.fe = fe;
+    a.partial = partial;
+    a.out = ob;
+    a.O = O;
+    a.G = G;
+    a.gps = p.gps;
+    const dim3 grid(p.row_tiles, p.splits);
+    const size_t lds_mb = fx::mfma_lds_bytes(p.nw, p.tr, mb, p.gps < G ? p.gps : G);
+    const bool ok = x_dtype == FX_BF16
+                        ? fx::dispatch_mfma_bf16(p.nw, p.tr, mb, scale_dtype, a, grid, lds_mb, s)
+                        : fx::dispatch_mfma_f16(p.nw, p.tr, mb, scale_dtype, a, grid, lds_mb, s);
+    if (!ok) return fail(FX_EINVAL, "no MFMA kernel for waves %d tiles %d rows %d", p.nw, p.tr, mb);
+    rc = check_launch("w3_mfma_kernel");
+    if (rc) return rc;
+    if (partial) {
+      rc = launch_finish(partial, ob, x_dtype, p.splits, mb * O, s);
+      if (rc) return rc;
+    }
     done += mb;
   }
   return FX_OK;
@@ -160,7 +292,7 @@ int run_lut(const void* x, int x_dtype, const uint8_t* planes, const void* scale
 
 extern "C" {
 
-int fx_abi_version(void) { return 1; }
+int fx_abi_version(void) { return 2; }
 
 const char* fx_last_error(void) { return g_error; }
 
@@ -176,12 +308,10 @@ int fx_w3_inline_main(const void* x, int x_dtype, const uint8_t* planes, const v
   const int G = K / 128;
   if (groups_per_split < 1 || groups_per_split > G)
     return fail(FX_EINVAL, "groups_per_split must be in [1, K/128]");
-  Tile tile = make_tile(O, G, rpt, groups_per_split);
-  // Partial mode writes [splits, M, O]; M blocks are laid out per block (see run_lut),
-  // which equals [splits, M, O] only when M is a single block.
-  if (m_block_for(M) != M) return fail(FX_EINVAL, "inline_main supports M in {1,2,4,8}");
-  return run_lut(x, x_dtype, planes, scales, scale_dtype, zeros, perm, partial, nullptr, nullptr,
-                 M, O, K, arithmetic, tile, fx::kModePartial, static_cast<hipStream_t>(stream));
+  if (lut_block_for(M) != M) return fail(FX_EINVAL, "inline_main supports M in {1,2,4,8}");
+  return run_lut(x, x_dtype, planes, scales, scale_dtype, zeros, perm, partial, nullptr, M, O, K,
+                 arithmetic, make_lut_tile(O, G, rpt, groups_per_split), true,
+                 static_cast<hipStream_t>(stream));
 }
 
 int fx_w3_finish(const float* partial, void* out, int out_dtype, int splits, int M, int O,
@@ -189,16 +319,7 @@ int fx_w3_finish(const float* partial, void* out, int out_dtype, int splits, int
   if (!partial || !out) return fail(FX_EINVAL, "partial and out must be non-null");
   if (!is_half_dtype(out_dtype)) return fail(FX_EINVAL, "out dtype must be fp16 or bf16");
   if (splits < 1 || M < 1 || O < 1) return fail(FX_EINVAL, "splits, M and O must be positive");
-  const int MO = M * O;
-  const dim3 grid((MO + 255) / 256);
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  if (out_dtype == FX_BF16)
-    hipLaunchKernelGGL(fx::w3_finish_kernel<fx::kBF16>, grid, dim3(256), 0, s, partial,
-                       static_cast<uint16_t*>(out), MO, splits);
-  else
-    hipLaunchKernelGGL(fx::w3_finish_kernel<fx::kF16>, grid, dim3(256), 0, s, partial,
-                       static_cast<uint16_t*>(out), MO, splits);
-  return check_launch("w3_finish_kernel");
+  return launch_finish(partial, out, out_dtype, splits, M * O, static_cast<hipStream_t>(stream));
 }
 
 int fx_w3_m1_out(const void* x, int x_dtype, const uint8_t* planes, const void* scales,
@@ -213,48 +334,25 @@ int fx_w3_m1_out(const void* x, int x_dtype, const uint8_t* planes, const void* 
   const int G = K / 128;
   if (groups_per_split < 1 || groups_per_split > G)
     return fail(FX_EINVAL, "groups_per_split must be in [1, K/128]");
-  if (m_block_for(M) != M) return fail(FX_EINVAL, "m1_out supports M in {1,2,4,8}");
-  Tile tile = make_tile(O, G, rpt, groups_per_split);
+  if (lut_block_for(M) != M) return fail(FX_EINVAL, "m1_out supports M in {1,2,4,8}");
+  const LutTile tile = make_lut_tile(O, G, rpt, groups_per_split);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (tile.splits == 1)
-    return run_lut(x, x_dtype, planes, scales, scale_dtype, zeros, perm, nullptr, nullptr, out,
-                   M, O, K, arithmetic, tile, fx::kModeDirect, s);
+    return run_lut(x, x_dtype, planes, scales, scale_dtype, zeros, perm, nullptr, out, M, O, K,
+                   arithmetic, tile, false, s);
   if (!workspace) return fail(FX_EINVAL, "workspace must be non-null when K is split");
-  rc = run_lut(x, x_dtype, planes, scales, scale_dtype, zeros, perm, workspace, nullptr, nullptr,
-               M, O, K, arithmetic, tile, fx::kModePartial, s);
+  rc = run_lut(x, x_dtype, planes, scales, scale_dtype, zeros, perm, workspace, nullptr, M, O, K,
+               arithmetic, tile, true, s);
   if (rc) return rc;
-  return fx_w3_finish(workspace, out, x_dtype, tile.splits, M, O, stream);
+  return launch_finish(workspace, out, x_dtype, tile.splits, M * O, s);
 }
 
 size_t fx_w3_gemv_workspace_bytes(int M, int O, int K) {
   if (M < 1 || O < 1 || K < 128 || K % 128) return 0;
-  return fused_workspace_bytes(M, O, default_tile(M, O, K));
-}
-
-size_t fx_w3_gemv_tile_workspace_bytes(int M, int O, int K, int rows_per_thread,
-                                       int groups_per_split) {
-  if (M < 1 || O < 1 || K < 128 || K % 128) return 0;
-  return fused_workspace_bytes(M, O, make_tile(O, K / 128, rows_per_thread, groups_per_split));
-}
-
-static int gemv_with_tile(const void* x, int x_dtype, const uint8_t* planes, const void* scales,
-                          int scale_dtype, const uint8_t* zeros, const int16_t* perm,
-                          void* workspace, size_t workspace_bytes, void* out, int M, int O, int K,
-                          int arithmetic, const Tile& tile, hipStream_t s) {
-  if (!out) return fail(FX_EINVAL, "out must be non-null");
-  if (tile.splits == 1)
-    return run_lut(x, x_dtype, planes, scales, scale_dtype, zeros, perm, nullptr, nullptr, out, M,
-                   O, K, arithmetic, tile, fx::kModeDirect, s);
-  const size_t need = fused_workspace_bytes(M, O, tile);
-  if (!workspace || workspace_bytes < need)
-    return fail(FX_EINVAL, "workspace needs %zu bytes, got %zu", need, workspace_bytes);
-  if (reinterpret_cast<uintptr_t>(workspace) % 256 != 0)
-    return fail(FX_EINVAL, "workspace must be 256-byte aligned");
-  unsigned* counters = static_cast<unsigned*>(workspace);
-  float* partial = reinterpret_cast<float*>(static_cast<char*>(workspace) +
-                                            align_up(size_t(tile.row_tiles) * sizeof(unsigned), 256));
-  return run_lut(x, x_dtype, planes, scales, scale_dtype, zeros, perm, partial, counters, out, M,
-                 O, K, arithmetic, tile, fx::kModeFused, s);
+  const int G = K / 128;
+  const size_t mfma = mfma_workspace(M, O, G, default_mfma_plan(O, G)).total;
+  const size_t lut = lut_route_workspace(M, O, K);
+  return mfma > lut ? mfma : lut;
 }
 
 int fx_w3_gemv(const void* x, int x_dtype, const uint8_t* planes, const void* scales,
@@ -263,26 +361,40 @@ int fx_w3_gemv(const void* x, int x_dtype, const uint8_t* planes, const void* sc
                void* stream) {
   int rc = validate_payload(x, x_dtype, planes, scales, scale_dtype, M, O, K, arithmetic);
   if (rc) return rc;
-  return gemv_with_tile(x, x_dtype, planes, scales, scale_dtype, zeros, perm, workspace,
-                        workspace_bytes, out, M, O, K, arithmetic, default_tile(M, O, K),
-                        static_cast<hipStream_t>(stream));
+  if (!out) return fail(FX_EINVAL, "out must be non-null");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (arithmetic == FX_ARITH_DECODED_BF16)
+    return run_lut_route(x, x_dtype, planes, scales, scale_dtype, zeros, perm, workspace,
+                         workspace_bytes, out, M, O, K, arithmetic, s);
+  return run_mfma(x, x_dtype, planes, scales, scale_dtype, zeros, perm, workspace,
+                  workspace_bytes, out, M, O, K, default_mfma_plan(O, K / 128), s);
 }
 
-int fx_w3_gemv_tile(const void* x, int x_dtype, const uint8_t* planes, const void* scales,
-                    int scale_dtype, const uint8_t* zeros, const int16_t* perm, void* workspace,
-                    size_t workspace_bytes, void* out, int M, int O, int K, int arithmetic,
-                    int rows_per_thread, int groups_per_split, void* stream) {
-  int rc = validate_payload(x, x_dtype, planes, scales, scale_dtype, M, O, K, arithmetic);
-  if (rc) return rc;
-  if (rows_per_thread != 1 && rows_per_thread != 2 && rows_per_thread != 4)
-    return fail(FX_EINVAL, "rows_per_thread must be 1, 2 or 4");
+size_t fx_w3_gemv_config_workspace_bytes(int M, int O, int K, int waves, int tiles_per_wave,
+                                         int groups_per_split) {
+  if (M < 1 || O < 1 || K < 128 || K % 128) return 0;
   const int G = K / 128;
-  if (groups_per_split < 1 || groups_per_split > G)
-    return fail(FX_EINVAL, "groups_per_split must be in [1, K/128]");
-  return gemv_with_tile(x, x_dtype, planes, scales, scale_dtype, zeros, perm, workspace,
-                        workspace_bytes, out, M, O, K, arithmetic,
-                        make_tile(O, G, rows_per_thread, groups_per_split),
-                        static_cast<hipStream_t>(stream));
+  return mfma_workspace(M, O, G, make_mfma_plan(O, G, waves, tiles_per_wave, groups_per_split))
+      .total;
+}
+
+int fx_w3_gemv_config(const void* x, int x_dtype, const uint8_t* planes, const void* scales,
+                      int scale_dtype, const uint8_t* zeros, const int16_t* perm, void* workspace,
+                      size_t workspace_bytes, void* out, int M, int O, int K, int waves,
+                      int tiles_per_wave, int groups_per_split, void* stream) {
+  int rc = validate_payload(x, x_dtype, planes, scales, scale_dtype, M, O, K, FX_ARITH_STRUCTURAL);
+  if (rc) return rc;
+  if (!out) return fail(FX_EINVAL, "out must be non-null");
+  const bool supported = (waves == 2 && tiles_per_wave == 1) ||
+                         ((waves == 4 || waves == 8) && (tiles_per_wave == 1 || tiles_per_wave == 2));
+  if (!supported)
+    return fail(FX_EINVAL, "unsupported waves/tiles_per_wave %d/%d", waves, tiles_per_wave);
+  const int G = K / 128;
+  if (groups_per_split < 1) return fail(FX_EINVAL, "groups_per_split must be positive");
+  return run_mfma(x, x_dtype, planes, scales, scale_dtype, zeros, perm, workspace,
+                  workspace_bytes, out, M, O, K,
+                  make_mfma_plan(O, G, waves, tiles_per_wave, groups_per_split),
+                  static_cast<hipStream_t>(stream));
 }
 
 int fx_w3_restore(const uint8_t* planes, const void* scales, int scale_dtype,

@@ -14,17 +14,16 @@
 // 8-column chunk; reference csrc/lut8_unsigned.cuh:13-27 computes the same
 // table values) and each thread evaluates its rows with 48 table reads per
 // group: a0 + 2 a1 - 4 a2 + (4 - z) * sum(x), times the scale.
-// K splits are reduced inside the same launch: every workgroup writes its fp32
-// partial rows, and the last workgroup of a row tile to arrive (device-scope
-// counter) sums the partials in split order and writes the output, so the
-// result does not depend on arrival order.
+// With one K split the workgroup writes the output; otherwise it writes fp32
+// partial rows partial[split, m, o] that w3_finish_kernel sums in split order
+// (the reference's inline_main + finish contract, csrc/w3_lut.cu:141-189).
 #include "common.h"
 
 namespace fx {
 
 constexpr int kLutThreads = 256;
 
-enum : int { kModeDirect = 0, kModePartial = 1, kModeFused = 2 };
+enum : int { kModeDirect = 0, kModePartial = 1 };
 
 template <int SDT>
 __device__ __forceinline__ float load_scale(const uint16_t* scales, size_t index) {
@@ -42,11 +41,9 @@ __global__ __launch_bounds__(kLutThreads) void w3_lut_kernel(
     const uint16_t* __restrict__ x, const uint8_t* __restrict__ planes,
     const uint16_t* __restrict__ scales, const uint8_t* __restrict__ zeros,
     const int16_t* __restrict__ perm, float* __restrict__ partial,
-    unsigned* __restrict__ counters, uint16_t* __restrict__ out, int O, int G,
-    int gps, int splits, int mode) {
+    uint16_t* __restrict__ out, int O, int G, int gps, int mode) {
   __shared__ float lut[M][16][256];
   __shared__ float chunk_sum[M][16];
-  __shared__ int last_flag;
 
   const int t = threadIdx.x;
   const int K = G * 128;
@@ -132,6 +129,27 @@ __global__ __launch_bounds__(kLutThreads) void w3_lut_kernel(
 
 #pragma unroll
     for (int r = 0; r < RPT; ++r) {
+      // decoded_bf16: byte masks of the columns whose signed code is +3 / -3,
+      // i.e. q = z + 3 / q = z - 3.  Stored bits of code q are (q0, q1, 1 - q2);
+      // a column matches when every stored bit equals the code's bit, so the
+      // mask is AND_p (byte_p XOR flip_p) with flip_p = 0xff where the code's
+      // stored bit is 0.
+      unsigned plus_flip[3] = {0u, 0u, 0u}, minus_flip[3] = {0u, 0u, 0u};
+      unsigned plus_keep = 0u, minus_keep = 0u;
+      if constexpr (DECODED) {
+        const int z = 4 - int(zshift[r]);
+        const int plus_code = z + 3, minus_code = z - 3;
+        plus_keep = (plus_code <= 7) ? 0xffu : 0u;
+        minus_keep = (minus_code >= 0) ? 0xffu : 0u;
+#pragma unroll
+        for (int p = 0; p < 3; ++p) {
+          const int pb = (plus_code >> p) & 1, mb = (minus_code >> p) & 1;
+          const int pstored = (p == 2) ? 1 - pb : pb;
+          const int mstored = (p == 2) ? 1 - mb : mb;
+          plus_flip[p] = pstored ? 0u : 0xffu;
+          minus_flip[p] = mstored ? 0u : 0xffu;
+        }
+      }
 #pragma unroll
       for (int m = 0; m < M; ++m) {
         float a0 = 0.f, a1 = 0.f, a2 = 0.f, corr = 0.f;
@@ -144,9 +162,10 @@ __global__ __launch_bounds__(kLutThreads) void w3_lut_kernel(
           a1 += lut[m][c][b1];
           a2 += lut[m][c][b2];
           if constexpr (DECODED) {
-            // signed code +3 is q=7 (stored bits 1,1,0); -3 is q=1 (1,0,1)
-            const unsigned plus = b0 & b1 & (~b2 & 0xffu);
-            const unsigned minus = b0 & (~b1 & 0xffu) & b2;
+            const unsigned plus =
+                (b0 ^ plus_flip[0]) & (b1 ^ plus_flip[1]) & (b2 ^ plus_flip[2]) & plus_keep;
+            const unsigned minus =
+                (b0 ^ minus_flip[0]) & (b1 ^ minus_flip[1]) & (b2 ^ minus_flip[2]) & minus_keep;
             corr += lut[m][c][plus] - lut[m][c][minus];
           }
         }
@@ -181,32 +200,6 @@ __global__ __launch_bounds__(kLutThreads) void w3_lut_kernel(
 #pragma unroll
       for (int m = 0; m < M; ++m) partial[(size_t(split) * M + m) * O + o] = acc[m][r];
   }
-  if (mode == kModePartial) return;
-
-  // Fused reduction: publish this split, count arrivals per row tile.
-  __threadfence();
-  __syncthreads();
-  if (t == 0) {
-    const unsigned previous = atomicAdd(&counters[blockIdx.x], 1u);
-    last_flag = (previous == unsigned(splits - 1)) ? 1 : 0;
-  }
-  __syncthreads();
-  if (!last_flag) return;
-  __threadfence();
-#pragma unroll
-  for (int r = 0; r < RPT; ++r) {
-    const int o = row0 + r * kLutThreads + t;
-    if (o < O) {
-#pragma unroll
-      for (int m = 0; m < M; ++m) {
-        float total = 0.f;
-        for (int s = 0; s < splits; ++s)
-          total += __builtin_nontemporal_load(&partial[(size_t(s) * M + m) * O + o]);
-        out[size_t(m) * O + o] = from_f32<XDT>(total);
-      }
-    }
-  }
-  if (t == 0) counters[blockIdx.x] = 0u;  // ready for the next launch
 }
 
 // out[m,o] = sum over splits of partial[s,m,o], sequential in s
@@ -218,6 +211,7 @@ __global__ __launch_bounds__(256) void w3_finish_kernel(const float* __restrict_
   const int i = int(blockIdx.x) * 256 + threadIdx.x;
   if (i >= MO) return;
   float total = 0.f;
+#pragma unroll 8
   for (int s = 0; s < splits; ++s) total += partial[size_t(s) * MO + i];
   out[i] = from_f32<XDT>(total);
 }

@@ -8,8 +8,8 @@ namespace fx {
 template <int M, int RPT, int XDT, int SDT, bool DEC>
 void launch_lut(const LutArgs& a, dim3 grid, hipStream_t stream) {
   hipLaunchKernelGGL((w3_lut_kernel<M, RPT, XDT, SDT, DEC>), grid, dim3(kLutThreads), 0,
-                     stream, a.x, a.planes, a.scales, a.zeros, a.perm, a.partial, a.counters,
-                     a.out, a.O, a.G, a.gps, a.splits, a.mode);
+                     stream, a.x, a.planes, a.scales, a.zeros, a.perm, a.partial, a.out, a.O,
+                     a.G, a.gps, a.mode);
 }
 
 template <int M, int RPT, int XDT>

@@ -12,9 +12,8 @@ struct LutArgs {
   const uint8_t* zeros;
   const int16_t* perm;
   float* partial;
-  unsigned* counters;
   uint16_t* out;
-  int O, G, gps, splits, mode;
+  int O, G, gps, mode;
 };
 
 // One instantiation unit per activation-row block (w3_lut_m{1,2,4,8}.hip).

@@ -80,3 +80,24 @@ def max_rel(actual, expected) -> float:
     a = np.asarray(actual, dtype=np.float64)
     b = np.asarray(expected, dtype=np.float64)
     return float(np.abs(a - b).max() / max(np.abs(b).max(), 1e-30))
+
+
+def assert_rel(actual, expected, tol: float, what: str = "") -> float:
+    """Assert the normwise max relative error, with a short failure message."""
+    err = max_rel(actual, expected)
+    assert err <= tol, f"{what} max_rel {err:.4g} > {tol:.4g}"
+    return err
+
+
+def assert_half_ulp(actual, exact, dtype: str, rel_slack: float = 2e-6, what: str = "") -> None:
+    """Element-wise: |actual - exact| <= half an ulp of the output dtype at exact,
+    plus rel_slack * max|exact| for the fp32 accumulation before the final cast."""
+    a = np.asarray(actual, dtype=np.float64)
+    e = np.asarray(exact, dtype=np.float64)
+    mantissa = 7 if dtype == "bf16" else 10
+    exponent = np.floor(np.log2(np.maximum(np.abs(e), 1e-30)))
+    bound = 2.0 ** (exponent - mantissa - 1) + rel_slack * np.abs(e).max()
+    excess = np.abs(a - e) - bound
+    worst = int(np.argmax(excess))
+    assert excess.max() <= 0, (f"{what} element {worst}: |{a.flat[worst]} - {e.flat[worst]}| exceeds "
+                               f"half-ulp bound {bound.flat[worst]:.3g}")

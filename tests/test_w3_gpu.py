@@ -18,7 +18,7 @@ from marlin_style_fluxbin_amd import (
     w3_lut_m1_out, workspace_shape,
 )
 from oracle import w3
-from tests.payloads import config_codes, layout_from_codes, max_rel, oracle_layout
+from tests.payloads import assert_half_ulp, assert_rel, config_codes, layout_from_codes, oracle_layout
 
 pytestmark = pytest.mark.gpu
 
@@ -46,7 +46,7 @@ def test_structural_fp32_matches_exact(gpu, o, k, m, zeros, permute):
     layout, dl, ol = _setup(o, k, seed=o + k, zeros=zeros, permute=permute)
     x = _x(m, k, torch.bfloat16, seed=m)
     got = structural_w3_matvec(x.to(gpu), dl).cpu().numpy()
-    assert max_rel(got, w3.matvec_exact(x.float().numpy(), ol)) <= FP32_TOL
+    assert_rel(got, w3.matvec_exact(x.float().numpy(), ol), FP32_TOL)
 
 
 @pytest.mark.parametrize("o,k", SMALL)
@@ -55,7 +55,7 @@ def test_decoded_fp32_matches_dequantize_then_matmul(gpu, o, k, zeros):
     layout, dl, ol = _setup(o, k, seed=3 * o + k, zeros=zeros)
     x = _x(1, k, torch.bfloat16, seed=o)
     got = bf16_weight_semantics_w3_matvec(x.to(gpu), dl).cpu().numpy()
-    assert max_rel(got, w3.matvec_decoded(x.float().numpy(), ol, "bf16")) <= FP32_TOL
+    assert_rel(got, w3.matvec_decoded(x.float().numpy(), ol, "bf16"), FP32_TOL)
 
 
 @pytest.mark.parametrize("o,k", SMALL)
@@ -70,8 +70,12 @@ def test_fused_fast_path(gpu, o, k, m, xdtype, scale_dtype):
     gemv(x.to(gpu), out)
     exact = w3.matvec_exact(x.float().numpy(), ol)
     got = out.float().cpu().numpy()
-    assert max_rel(got, exact) <= HALF_TOL
-    # a second call through the same workspace is bit-identical (counters reset)
+    assert_rel(got, exact, HALF_TOL)
+    # fp16 activations run on the fp16 MFMA, whose products with subnormal fp16
+    # code operands round at ~2e-7 relative (measured per instruction); bf16 is exact
+    slack = 2e-6 if xdtype == torch.bfloat16 else 3e-5
+    assert_half_ulp(got, exact, "bf16" if xdtype == torch.bfloat16 else "f16", rel_slack=slack)
+    # a second call through the same workspace is bit-identical
     again = torch.empty_like(out)
     gemv(x.to(gpu), again)
     assert torch.equal(out, again)
@@ -99,7 +103,7 @@ def test_reference_split_contract(gpu, row_tile, dtype):
                 assert torch.isnan(workspace).all()
             else:
                 assert torch.isfinite(workspace).all()
-            assert max_rel(out.float().cpu().numpy(), exact) <= HALF_TOL
+            assert_rel(out.float().cpu().numpy(), exact, HALF_TOL)
             saved = out.clone()
             workspace.fill_(float("nan"))
             run()
@@ -121,7 +125,7 @@ def test_reference_split_contract(gpu, row_tile, dtype):
                 corrected = torch.empty(1, out_features, device=gpu, dtype=dtype)
                 ws = torch.full(workspace_shape(out_features, in_features, gps), float("nan"), device=gpu)
                 w3_lut_m1_out(x, dl, corrected, ws, row_tile=256, groups_per_split=gps, arithmetic="decoded_bf16")
-                assert max_rel(corrected.float().cpu().numpy(), decoded) <= HALF_TOL
+                assert_rel(corrected.float().cpu().numpy(), decoded, HALF_TOL)
 
 
 def test_fused_path_graph_replays_track_input(gpu):
@@ -163,15 +167,16 @@ def test_qwen3_shapes_config1(gpu, o, k, m):
     exact = w3.matvec_exact(x.float().numpy(), ol)
     if m in (1, 2, 4, 8):
         got32 = structural_w3_matvec(x.to(gpu), dl).cpu().numpy()
-        assert max_rel(got32, exact) <= FP32_TOL
+        assert_rel(got32, exact, FP32_TOL)
     gemv = W3Gemv(dl)
     out = torch.empty(m, o, dtype=torch.bfloat16, device=gpu)
     gemv(x.to(gpu), out)
     got = out.float().cpu().numpy()
-    assert max_rel(got, exact) <= HALF_TOL
+    assert_rel(got, exact, HALF_TOL)
+    assert_half_ulp(got, exact, "bf16")
     # the stated bar against dequantize-then-matmul (bf16 weights from fp16 scales)
     decoded = w3.matvec_decoded(x.float().numpy(), ol, "bf16")
-    assert max_rel(got, decoded) <= 1e-2
+    assert_rel(got, decoded, 1e-2)
 
 
 def test_config0_q_proj_seed0(gpu):
@@ -183,9 +188,9 @@ def test_config0_q_proj_seed0(gpu):
         y = module(x.to(gpu))
     assert module.route_counts == {"packed_m1": 1, "dense_fallback": 0}
     exact = w3.matvec_exact(x.float().numpy(), ol)
-    assert max_rel(y.float().cpu().numpy(), exact) <= HALF_TOL
+    assert_rel(y.float().cpu().numpy(), exact, HALF_TOL)
     got32 = structural_w3_matvec(x.to(gpu), dl).cpu().numpy()
-    assert max_rel(got32, exact) <= FP32_TOL
+    assert_rel(got32, exact, FP32_TOL)
 
 
 @pytest.mark.parametrize("scale_dtype", [torch.bfloat16, torch.float16])
@@ -206,4 +211,4 @@ def test_dense_fallback_on_gpu_uses_device_restore(gpu):
         y = module(x)
     assert module.route_counts["dense_fallback"] == 1
     decoded = w3.matvec_decoded(x.float().cpu().numpy(), ol, "bf16")
-    assert max_rel(y.float().cpu().numpy(), decoded) <= 1e-2
+    assert_rel(y.float().cpu().numpy(), decoded, 1e-2)

@@ -1,0 +1,85 @@
+"""GPU parity of the MFMA W3 GEMV (the fast structural path) against the float64 oracle.
+
+Every output element must lie within half an output ulp of the exact value
+x @ (s*(q-z)).T plus 2e-6 * max|y| (fp32 accumulation before the final cast),
+for every tiling variant, K split, activation-row count and dtype combination.
+fp16 activations use 3e-5: the fp16 MFMA rounds products with subnormal fp16
+operands at ~2e-7 relative per instruction (bf16 MFMA is exact).
+"""
+import numpy as np
+import pytest
+import torch
+
+from marlin_style_fluxbin_amd import _lib
+from oracle import w3
+from tests.payloads import assert_half_ulp, config_codes, layout_from_codes, oracle_layout
+
+pytestmark = pytest.mark.gpu
+
+PLANS = [(2, 1, 4), (4, 1, 4), (4, 1, 8), (4, 2, 8), (8, 1, 32), (8, 2, 16), (8, 1, 12)]
+
+
+def _run_config(dl, x, out, waves, tiles, gps):
+    lib = _lib.library()
+    m, k = x.shape
+    o = out.shape[1]
+    nbytes = lib.fx_w3_gemv_config_workspace_bytes(m, o, k, waves, tiles, gps)
+    ws = torch.empty(nbytes + 256, dtype=torch.uint8, device=x.device)
+    _lib.check(lib.fx_w3_gemv_config(
+        x.data_ptr(), _lib.dtype_code(x.dtype), dl["planes"].data_ptr(), dl["scales"].data_ptr(),
+        _lib.dtype_code(dl["scales"].dtype), _lib.ptr(dl.get("zeros")), dl["perm"].data_ptr(),
+        ws.data_ptr(), nbytes, out.data_ptr(), m, o, k, waves, tiles, gps, _lib.stream_handle(x.device)),
+        "fx_w3_gemv_config")
+
+
+@pytest.mark.parametrize("o,k", [(64, 512), (37, 1536), (300, 2048), (1, 128), (17, 384)])
+@pytest.mark.parametrize("plan", PLANS)
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 8])
+def test_mfma_plans(gpu, o, k, plan, m):
+    codes, scales, zeros, perm = config_codes(o, k, seed=o + k + m, zeros=True, scale_dtype=torch.float16,
+                                              permute=True)
+    layout = layout_from_codes(codes, scales, zeros, perm)
+    dl = {n: t.to(gpu) for n, t in layout.items()}
+    x = torch.randn(m, k, generator=torch.Generator().manual_seed(m)).to(torch.bfloat16)
+    out = torch.full((m, o), float("nan"), dtype=torch.bfloat16, device=gpu)
+    _run_config(dl, x.to(gpu), out, *plan)
+    exact = w3.matvec_exact(x.float().numpy(), oracle_layout(layout))
+    assert_half_ulp(out.float().cpu().numpy(), exact, "bf16", what=f"plan {plan} m {m}")
+
+
+@pytest.mark.parametrize("xdtype,tag", [(torch.bfloat16, "bf16"), (torch.float16, "f16")])
+@pytest.mark.parametrize("scale_dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("zeros", [False, True])
+def test_mfma_dtypes_and_zero_modes(gpu, xdtype, tag, scale_dtype, zeros):
+    codes, scales, z, perm = config_codes(256, 1024, seed=5, zeros=zeros, scale_dtype=scale_dtype)
+    layout = layout_from_codes(codes, scales, z, perm)
+    dl = {n: t.to(gpu) for n, t in layout.items()}
+    x = torch.randn(1, 1024, generator=torch.Generator().manual_seed(3)).to(xdtype)
+    out = torch.empty(1, 256, dtype=xdtype, device=gpu)
+    _run_config(dl, x.to(gpu), out, 8, 1, 8)
+    exact = w3.matvec_exact(x.float().numpy(), oracle_layout(layout))
+    # fp16 MFMA products with subnormal fp16 code operands round at ~2e-7 relative
+    assert_half_ulp(out.float().cpu().numpy(), exact, tag, rel_slack=2e-6 if tag == "bf16" else 3e-5)
+
+
+@pytest.mark.parametrize("scale", [1e-30, 1e-6, 1.0, 1e6, 1e30])
+def test_mfma_activation_range(gpu, scale):
+    """The per-row exponent offset keeps tiny and huge activations exact."""
+    codes, scales, z, perm = config_codes(128, 512, seed=2, zeros=True, scale_dtype=torch.bfloat16)
+    layout = layout_from_codes(codes, scales, z, perm)
+    dl = {n: t.to(gpu) for n, t in layout.items()}
+    x = (torch.randn(1, 512, generator=torch.Generator().manual_seed(4)) * scale).to(torch.bfloat16)
+    out = torch.empty(1, 128, dtype=torch.bfloat16, device=gpu)
+    _run_config(dl, x.to(gpu), out, 4, 1, 4)
+    exact = w3.matvec_exact(x.float().numpy(), oracle_layout(layout))
+    assert np.all(np.isfinite(out.float().cpu().numpy()))
+    assert_half_ulp(out.float().cpu().numpy(), exact, "bf16", what=f"scale {scale}")
+
+
+def test_mfma_zero_activation(gpu):
+    codes, scales, z, perm = config_codes(64, 256, seed=1)
+    layout = layout_from_codes(codes, scales, z, perm)
+    dl = {n: t.to(gpu) for n, t in layout.items()}
+    out = torch.full((1, 64), float("nan"), dtype=torch.bfloat16, device=gpu)
+    _run_config(dl, torch.zeros(1, 256, dtype=torch.bfloat16, device=gpu), out, 4, 1, 4)
+    assert torch.equal(out, torch.zeros_like(out))
