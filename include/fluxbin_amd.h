@@ -91,15 +91,15 @@ int fx_w3_gemv(const void *x, int x_dtype, const uint8_t *planes, const void *sc
                size_t workspace_bytes, void *out, int M, int O, int K, int arithmetic,
                void *stream);
 /* Structural MFMA path with an explicit tiling (benchmark sweeps): waves per
- * workgroup in {2,4,8}, 16-row tiles per wave in {1,2} (2 needs 4 or 8 waves),
+ * workgroup in {2,4,8}, 4-group batches kept in flight per wave in {1,2,4},
  * groups per K split (rounded up to a multiple of 4, clamped to the padded group
  * count). */
-size_t fx_w3_gemv_config_workspace_bytes(int M, int O, int K, int waves, int tiles_per_wave,
+size_t fx_w3_gemv_config_workspace_bytes(int M, int O, int K, int waves, int prefetch,
                                          int groups_per_split);
 int fx_w3_gemv_config(const void *x, int x_dtype, const uint8_t *planes, const void *scales,
                       int scale_dtype, const uint8_t *zeros, const int16_t *perm,
                       void *workspace, size_t workspace_bytes, void *out, int M, int O, int K,
-                      int waves, int tiles_per_wave, int groups_per_split, void *stream);
+                      int waves, int prefetch, int groups_per_split, void *stream);
 
 /*
  * Reference: restore_planar_w3 (gptq_deployment.py:247-260), the dequantize

@@ -187,24 +187,25 @@ int run_lut_route(const void* x, int x_dtype, const uint8_t* planes, const void*
 
 // ------------------------------------------------------------------ MFMA kernel
 struct MfmaPlan {
-  int nw, tr, gps, splits, row_tiles;
+  int nw, pd, gps, splits, row_tiles;  // waves, batches in flight per wave, groups per split
 };
 
 int mfma_chunk_for(int m) { return m >= 4 ? 4 : m >= 2 ? 2 : 1; }
 
-MfmaPlan make_mfma_plan(int O, int G, int nw, int tr, int gps) {
+MfmaPlan make_mfma_plan(int O, int G, int nw, int pd, int gps) {
   MfmaPlan p;
   p.nw = nw;
-  p.tr = tr;
+  p.pd = pd;
   const int gmax = (G + 3) / 4 * 4;
   p.gps = gps < 4 ? 4 : (gps + 3) / 4 * 4;
   if (p.gps > gmax) p.gps = gmax;
   p.splits = (G + p.gps - 1) / p.gps;
-  p.row_tiles = (O + 16 * tr - 1) / (16 * tr);
+  p.row_tiles = (O + 15) / 16;
   return p;
 }
 
-// Default: 16-row tiles, K split over the waves of a workgroup, and over
+// Default: 16-row tiles, K split over the waves of a workgroup (each wave
+// keeping all of its batches in flight when it has at most four), and over
 // workgroups only when there are fewer row tiles than CUs.
 MfmaPlan default_mfma_plan(int O, int G) {
   const int cus = device_cu_count();
@@ -215,7 +216,9 @@ MfmaPlan default_mfma_plan(int O, int G) {
   if (splits > batches) splits = batches;
   const int per_split = (batches + splits - 1) / splits;  // batches per workgroup
   const int nw = per_split >= 8 ? 8 : per_split >= 4 ? 4 : 2;
-  return make_mfma_plan(O, G, nw, 1, per_split * 4);
+  const int per_wave = (per_split + nw - 1) / nw;
+  const int pd = per_wave >= 3 ? 4 : per_wave;
+  return make_mfma_plan(O, G, nw, pd, per_split * 4);
 }
 
 struct MfmaWorkspace {
@@ -224,11 +227,12 @@ struct MfmaWorkspace {
 
 MfmaWorkspace mfma_workspace(int M, int O, int G, const MfmaPlan& p) {
   const int mb = mfma_chunk_for(M);
+  const size_t gp = size_t(G + 3) / 4 * 4;  // packed x is zero-padded to whole batches
   MfmaWorkspace w;
   w.xs = 0;
-  w.sx = align_up(size_t(G) * 256 * mb, 256);
-  w.fe = w.sx + align_up(size_t(G) * mb * sizeof(float), 256);
-  w.partial = w.fe + 256;
+  w.sx = align_up(gp * 256 * mb, 256);
+  w.fe = w.sx + align_up(gp * mb * sizeof(float), 256);
+  w.partial = w.fe + align_up(gp * mb * sizeof(int), 256);
   w.total = w.partial + (p.splits > 1 ? size_t(p.splits) * mb * O * sizeof(float) : 0);
   return w;
 }
@@ -243,8 +247,6 @@ int run_mfma(const void* x, int x_dtype, const uint8_t* planes, const void* scal
     return fail(FX_EINVAL, "workspace needs %zu bytes, got %zu", w.total, workspace_bytes);
   if (reinterpret_cast<uintptr_t>(workspace) % 256 != 0)
     return fail(FX_EINVAL, "workspace must be 256-byte aligned");
-  const size_t lds = fx::mfma_lds_bytes(p.nw, p.tr, mfma_chunk_for(M), p.gps < G ? p.gps : G);
-  if (lds > 160 * 1024) return fail(FX_EINVAL, "K slice too large for LDS (%zu bytes)", lds);
   char* base = static_cast<char*>(workspace);
   uint16_t* xs = reinterpret_cast<uint16_t*>(base + w.xs);
   float* sx = reinterpret_cast<float*>(base + w.sx);
@@ -272,11 +274,10 @@ int run_mfma(const void* x, int x_dtype, const uint8_t* planes, const void* scal
     a.G = G;
     a.gps = p.gps;
     const dim3 grid(p.row_tiles, p.splits);
-    const size_t lds_mb = fx::mfma_lds_bytes(p.nw, p.tr, mb, p.gps < G ? p.gps : G);
     const bool ok = x_dtype == FX_BF16
-                        ? fx::dispatch_mfma_bf16(p.nw, p.tr, mb, scale_dtype, a, grid, lds_mb, s)
-                        : fx::dispatch_mfma_f16(p.nw, p.tr, mb, scale_dtype, a, grid, lds_mb, s);
-    if (!ok) return fail(FX_EINVAL, "no MFMA kernel for waves %d tiles %d rows %d", p.nw, p.tr, mb);
+                        ? fx::dispatch_mfma_bf16(p.nw, p.pd, mb, scale_dtype, a, grid, s)
+                        : fx::dispatch_mfma_f16(p.nw, p.pd, mb, scale_dtype, a, grid, s);
+    if (!ok) return fail(FX_EINVAL, "no MFMA kernel for waves %d prefetch %d rows %d", p.nw, p.pd, mb);
     rc = check_launch("w3_mfma_kernel");
     if (rc) return rc;
     if (partial) {
@@ -370,30 +371,28 @@ int fx_w3_gemv(const void* x, int x_dtype, const uint8_t* planes, const void* sc
                   workspace_bytes, out, M, O, K, default_mfma_plan(O, K / 128), s);
 }
 
-size_t fx_w3_gemv_config_workspace_bytes(int M, int O, int K, int waves, int tiles_per_wave,
+size_t fx_w3_gemv_config_workspace_bytes(int M, int O, int K, int waves, int prefetch,
                                          int groups_per_split) {
   if (M < 1 || O < 1 || K < 128 || K % 128) return 0;
   const int G = K / 128;
-  return mfma_workspace(M, O, G, make_mfma_plan(O, G, waves, tiles_per_wave, groups_per_split))
-      .total;
+  return mfma_workspace(M, O, G, make_mfma_plan(O, G, waves, prefetch, groups_per_split)).total;
 }
 
 int fx_w3_gemv_config(const void* x, int x_dtype, const uint8_t* planes, const void* scales,
                       int scale_dtype, const uint8_t* zeros, const int16_t* perm, void* workspace,
                       size_t workspace_bytes, void* out, int M, int O, int K, int waves,
-                      int tiles_per_wave, int groups_per_split, void* stream) {
+                      int prefetch, int groups_per_split, void* stream) {
   int rc = validate_payload(x, x_dtype, planes, scales, scale_dtype, M, O, K, FX_ARITH_STRUCTURAL);
   if (rc) return rc;
   if (!out) return fail(FX_EINVAL, "out must be non-null");
-  const bool supported = (waves == 2 && tiles_per_wave == 1) ||
-                         ((waves == 4 || waves == 8) && (tiles_per_wave == 1 || tiles_per_wave == 2));
-  if (!supported)
-    return fail(FX_EINVAL, "unsupported waves/tiles_per_wave %d/%d", waves, tiles_per_wave);
+  const bool supported = (waves == 2 || waves == 4 || waves == 8) &&
+                         (prefetch == 1 || prefetch == 2 || prefetch == 4);
+  if (!supported) return fail(FX_EINVAL, "unsupported waves/prefetch %d/%d", waves, prefetch);
   const int G = K / 128;
   if (groups_per_split < 1) return fail(FX_EINVAL, "groups_per_split must be positive");
   return run_mfma(x, x_dtype, planes, scales, scale_dtype, zeros, perm, workspace,
                   workspace_bytes, out, M, O, K,
-                  make_mfma_plan(O, G, waves, tiles_per_wave, groups_per_split),
+                  make_mfma_plan(O, G, waves, prefetch, groups_per_split),
                   static_cast<hipStream_t>(stream));
 }
 

@@ -3,7 +3,7 @@
 
 namespace fx {
 bool dispatch_mfma_f16(int nw, int tr, int mb, int sdt, const MfmaArgs& a, dim3 grid,
-                       size_t lds, hipStream_t s) {
-  return mfma_dispatch<kF16>(nw, tr, mb, sdt, a, grid, lds, s);
+                       hipStream_t s) {
+  return mfma_dispatch<kF16>(nw, tr, mb, sdt, a, grid, s);
 }
 }  // namespace fx

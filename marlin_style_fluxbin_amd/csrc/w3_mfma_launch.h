@@ -17,17 +17,10 @@ struct MfmaArgs {
   int O, G, gps;
 };
 
-// Dynamic LDS of one workgroup: B chunks of ng groups + zero chunk + sums + reduction.
-inline size_t mfma_lds_bytes(int nw, int tr, int mb, int ng) {
-  const size_t chunks = size_t(ng) * 16 * mb + 1;
-  const size_t sums = (size_t(ng) * mb + 3) & ~size_t(3);
-  return chunks * 16 + sums * 4 + size_t(nw) * tr * 16 * mb * 4;
-}
-
 bool dispatch_mfma_bf16(int nw, int tr, int mb, int sdt, const MfmaArgs& a, dim3 grid,
-                        size_t lds, hipStream_t s);
+                        hipStream_t s);
 bool dispatch_mfma_f16(int nw, int tr, int mb, int sdt, const MfmaArgs& a, dim3 grid,
-                       size_t lds, hipStream_t s);
+                       hipStream_t s);
 // x [mb, K] -> packed B operands, per-group sums, exponents (one launch)
 bool launch_xprep(int xdt, const uint16_t* x, const int16_t* perm, uint16_t* xs, float* sx,
                   int* fe, int K, int mb, hipStream_t s);

@@ -16,19 +16,20 @@ from tests.payloads import assert_half_ulp, config_codes, layout_from_codes, ora
 
 pytestmark = pytest.mark.gpu
 
-PLANS = [(2, 1, 4), (4, 1, 4), (4, 1, 8), (4, 2, 8), (8, 1, 32), (8, 2, 16), (8, 1, 12)]
+# (waves, batches in flight per wave, groups per K split)
+PLANS = [(2, 1, 4), (2, 4, 32), (4, 1, 4), (4, 2, 8), (4, 4, 16), (8, 1, 32), (8, 2, 16), (8, 4, 12)]
 
 
-def _run_config(dl, x, out, waves, tiles, gps):
+def _run_config(dl, x, out, waves, prefetch, gps):
     lib = _lib.library()
     m, k = x.shape
     o = out.shape[1]
-    nbytes = lib.fx_w3_gemv_config_workspace_bytes(m, o, k, waves, tiles, gps)
+    nbytes = lib.fx_w3_gemv_config_workspace_bytes(m, o, k, waves, prefetch, gps)
     ws = torch.empty(nbytes + 256, dtype=torch.uint8, device=x.device)
     _lib.check(lib.fx_w3_gemv_config(
         x.data_ptr(), _lib.dtype_code(x.dtype), dl["planes"].data_ptr(), dl["scales"].data_ptr(),
         _lib.dtype_code(dl["scales"].dtype), _lib.ptr(dl.get("zeros")), dl["perm"].data_ptr(),
-        ws.data_ptr(), nbytes, out.data_ptr(), m, o, k, waves, tiles, gps, _lib.stream_handle(x.device)),
+        ws.data_ptr(), nbytes, out.data_ptr(), m, o, k, waves, prefetch, gps, _lib.stream_handle(x.device)),
         "fx_w3_gemv_config")
 
 
@@ -56,7 +57,7 @@ def test_mfma_dtypes_and_zero_modes(gpu, xdtype, tag, scale_dtype, zeros):
     dl = {n: t.to(gpu) for n, t in layout.items()}
     x = torch.randn(1, 1024, generator=torch.Generator().manual_seed(3)).to(xdtype)
     out = torch.empty(1, 256, dtype=xdtype, device=gpu)
-    _run_config(dl, x.to(gpu), out, 8, 1, 8)
+    _run_config(dl, x.to(gpu), out, 8, 2, 8)
     exact = w3.matvec_exact(x.float().numpy(), oracle_layout(layout))
     # fp16 MFMA products with subnormal fp16 code operands round at ~2e-7 relative
     assert_half_ulp(out.float().cpu().numpy(), exact, tag, rel_slack=2e-6 if tag == "bf16" else 3e-5)
