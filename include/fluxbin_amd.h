@@ -77,13 +77,14 @@ int fx_w3_m1_out(const void *x, int x_dtype, const uint8_t *planes, const void *
  * Fast path used by PackedW3Linear and its prepared decode binding
  * (w3_lut_deployment.py:250-359 in the reference).  structural arithmetic: the
  * gfx950 MFMA kernel -- codes dequantized in registers to bf16/fp16 subnormal
- * MFMA operands against exact activations, fp32 accumulation, K split over the
- * waves of a workgroup (and over workgroups with a stream-ordered finish when
- * the output has fewer 16-row tiles than CUs); one small x-packing launch per
- * call.  decoded_bf16 arithmetic: the LUT kernel plus finish.  Tiling comes
- * from (M, O, K) and the CU count.  workspace: fx_w3_gemv_workspace_bytes(M, O,
- * K) bytes, 256-byte aligned, no initial contents required.  Calls that share a
- * workspace must be ordered on one stream.
+ * MFMA operands against exact power-of-two-scaled activations, fp32
+ * accumulation, K split over the waves of a workgroup; one launch per call,
+ * plus a stream-ordered finish launch when the output has fewer 16-row tiles
+ * than CUs and K is also split over workgroups.  decoded_bf16 arithmetic: the
+ * LUT kernel plus finish.  Tiling comes from (M, O, K) and the CU count.
+ * workspace: fx_w3_gemv_workspace_bytes(M, O, K) bytes, 256-byte aligned, no
+ * initial contents required; NULL is accepted when that size is 0.  Calls that
+ * share a workspace must be ordered on one stream.
  */
 size_t fx_w3_gemv_workspace_bytes(int M, int O, int K);
 int fx_w3_gemv(const void *x, int x_dtype, const uint8_t *planes, const void *scales,
@@ -91,15 +92,15 @@ int fx_w3_gemv(const void *x, int x_dtype, const uint8_t *planes, const void *sc
                size_t workspace_bytes, void *out, int M, int O, int K, int arithmetic,
                void *stream);
 /* Structural MFMA path with an explicit tiling (benchmark sweeps): waves per
- * workgroup in {2,4,8}, 4-group batches kept in flight per wave in {1,2,4},
+ * workgroup in {4,8}, 4-group batches kept in flight per wave in {1,2},
  * groups per K split (rounded up to a multiple of 4, clamped to the padded group
- * count). */
+ * count), 16-row tiles per wave in {1,2}. */
 size_t fx_w3_gemv_config_workspace_bytes(int M, int O, int K, int waves, int prefetch,
-                                         int groups_per_split);
+                                         int groups_per_split, int tiles);
 int fx_w3_gemv_config(const void *x, int x_dtype, const uint8_t *planes, const void *scales,
                       int scale_dtype, const uint8_t *zeros, const int16_t *perm,
                       void *workspace, size_t workspace_bytes, void *out, int M, int O, int K,
-                      int waves, int prefetch, int groups_per_split, void *stream);
+                      int waves, int prefetch, int groups_per_split, int tiles, void *stream);
 
 /*
  * Reference: restore_planar_w3 (gptq_deployment.py:247-260), the dequantize

@@ -62,6 +62,9 @@ int validate_payload(const void* x, int x_dtype, const uint8_t* planes, const vo
     return fail(FX_EINVAL, "K must be a positive multiple of 128, got %d", K);
   if (reinterpret_cast<uintptr_t>(planes) % 16 != 0)
     return fail(FX_EINVAL, "planes must be 16-byte aligned");
+  // kernels address the payload with 32-bit byte offsets
+  if (size_t(K / 128) * 3 * size_t(O) * 16 > 0x7fffffffu || size_t(M) * K * 2 > 0x7fffffffu)
+    return fail(FX_EINVAL, "payload of %d x %d exceeds 2 GiB", O, K);
   if (arithmetic != FX_ARITH_STRUCTURAL && arithmetic != FX_ARITH_DECODED_BF16)
     return fail(FX_EINVAL, "unknown arithmetic %d", arithmetic);
   if (arithmetic == FX_ARITH_DECODED_BF16 && scale_dtype != FX_BF16)
@@ -187,54 +190,49 @@ int run_lut_route(const void* x, int x_dtype, const uint8_t* planes, const void*
 
 // ------------------------------------------------------------------ MFMA kernel
 struct MfmaPlan {
-  int nw, pd, gps, splits, row_tiles;  // waves, batches in flight per wave, groups per split
+  int nw, pd, tiles;  // waves per workgroup, batches in flight per wave, 16-row tiles per wave
+  int gps, splits, row_blocks;
 };
 
 int mfma_chunk_for(int m) { return m >= 4 ? 4 : m >= 2 ? 2 : 1; }
 
-MfmaPlan make_mfma_plan(int O, int G, int nw, int pd, int gps) {
+constexpr int kXcds = 8;  // MI355X deals workgroups round-robin over 8 XCDs
+
+MfmaPlan make_mfma_plan(int O, int G, int nw, int pd, int gps, int tiles) {
   MfmaPlan p;
   p.nw = nw;
   p.pd = pd;
+  p.tiles = tiles;
   const int gmax = (G + 3) / 4 * 4;
   p.gps = gps < 4 ? 4 : (gps + 3) / 4 * 4;
   if (p.gps > gmax) p.gps = gmax;
   p.splits = (G + p.gps - 1) / p.gps;
-  p.row_tiles = (O + 15) / 16;
+  p.row_blocks = (O + 16 * tiles - 1) / (16 * tiles);
   return p;
 }
 
-// Default: 16-row tiles, K split over the waves of a workgroup (each wave
-// keeping all of its batches in flight when it has at most four), and over
-// workgroups only when there are fewer row tiles than CUs.
+// Default (from graph-timed sweeps over the Qwen3-8B shapes on MI355X): one
+// 16-row tile and one batch in flight per wave (more tiles or a deeper ring
+// cost occupancy and measured slower), eight waves splitting K inside the
+// workgroup, and a K split over workgroups only for very narrow outputs (a
+// split costs a finish launch, which is more than idle CUs cost at these sizes).
 MfmaPlan default_mfma_plan(int O, int G) {
-  const int cus = device_cu_count();
-  const int row_tiles = (O + 15) / 16;
+  const int tiles = 1;
+  const int row_blocks = (O + 15) / 16;
   const int batches = (G + 3) / 4;
   int splits = 1;
-  if (row_tiles < cus) splits = (cus + row_tiles - 1) / row_tiles;
+  if (row_blocks < 32) splits = (64 + row_blocks - 1) / row_blocks;
   if (splits > batches) splits = batches;
   const int per_split = (batches + splits - 1) / splits;  // batches per workgroup
-  const int nw = per_split >= 8 ? 8 : per_split >= 4 ? 4 : 2;
-  const int per_wave = (per_split + nw - 1) / nw;
-  const int pd = per_wave >= 3 ? 4 : per_wave;
-  return make_mfma_plan(O, G, nw, pd, per_split * 4);
+  const int nw = per_split >= 8 ? 8 : 4;
+  return make_mfma_plan(O, G, nw, 1, per_split * 4, tiles);
 }
 
-struct MfmaWorkspace {
-  size_t xs, sx, fe, partial, total;
-};
-
-MfmaWorkspace mfma_workspace(int M, int O, int G, const MfmaPlan& p) {
+// The MFMA path needs workspace only for fp32 partials when K is split over
+// workgroups: [splits, mb, O] for the largest activation chunk mb.
+size_t mfma_workspace(int M, int O, const MfmaPlan& p) {
   const int mb = mfma_chunk_for(M);
-  const size_t gp = size_t(G + 3) / 4 * 4;  // packed x is zero-padded to whole batches
-  MfmaWorkspace w;
-  w.xs = 0;
-  w.sx = align_up(gp * 256 * mb, 256);
-  w.fe = w.sx + align_up(gp * mb * sizeof(float), 256);
-  w.partial = w.fe + align_up(gp * mb * sizeof(int), 256);
-  w.total = w.partial + (p.splits > 1 ? size_t(p.splits) * mb * O * sizeof(float) : 0);
-  return w;
+  return p.splits > 1 ? size_t(p.splits) * mb * O * sizeof(float) : 0;
 }
 
 int run_mfma(const void* x, int x_dtype, const uint8_t* planes, const void* scales,
@@ -242,43 +240,36 @@ int run_mfma(const void* x, int x_dtype, const uint8_t* planes, const void* scal
              size_t workspace_bytes, void* out, int M, int O, int K, const MfmaPlan& p,
              hipStream_t s) {
   const int G = K / 128;
-  const MfmaWorkspace w = mfma_workspace(M, O, G, p);
-  if (!workspace || workspace_bytes < w.total)
-    return fail(FX_EINVAL, "workspace needs %zu bytes, got %zu", w.total, workspace_bytes);
-  if (reinterpret_cast<uintptr_t>(workspace) % 256 != 0)
-    return fail(FX_EINVAL, "workspace must be 256-byte aligned");
-  char* base = static_cast<char*>(workspace);
-  uint16_t* xs = reinterpret_cast<uint16_t*>(base + w.xs);
-  float* sx = reinterpret_cast<float*>(base + w.sx);
-  int* fe = reinterpret_cast<int*>(base + w.fe);
-  float* partial = p.splits > 1 ? reinterpret_cast<float*>(base + w.partial) : nullptr;
+  const size_t need = mfma_workspace(M, O, p);
+  if (need > 0) {
+    if (!workspace || workspace_bytes < need)
+      return fail(FX_EINVAL, "workspace needs %zu bytes, got %zu", need, workspace_bytes);
+    if (reinterpret_cast<uintptr_t>(workspace) % 256 != 0)
+      return fail(FX_EINVAL, "workspace must be 256-byte aligned");
+  }
+  float* partial = p.splits > 1 ? static_cast<float*>(workspace) : nullptr;
   int done = 0;
   while (done < M) {
     const int mb = mfma_chunk_for(M - done);
-    const uint16_t* xb = static_cast<const uint16_t*>(x) + size_t(done) * K;
     uint16_t* ob = static_cast<uint16_t*>(out) + size_t(done) * O;
-    if (!fx::launch_xprep(x_dtype, xb, perm, xs, sx, fe, K, mb, s))
-      return fail(FX_EINVAL, "no x packer for dtype %d", x_dtype);
-    int rc = check_launch("w3_xprep_kernel");
-    if (rc) return rc;
     MfmaArgs a;
+    a.x = static_cast<const uint16_t*>(x) + size_t(done) * K;
+    a.perm = perm;
     a.planes = planes;
     a.scales = static_cast<const uint16_t*>(scales);
     a.zeros = zeros;
-    a.xs = xs;
-    a.sx = sx;
-    a.fe = fe;
     a.partial = partial;
     a.out = ob;
     a.O = O;
     a.G = G;
     a.gps = p.gps;
-    const dim3 grid(p.row_tiles, p.splits);
-    const bool ok = x_dtype == FX_BF16
-                        ? fx::dispatch_mfma_bf16(p.nw, p.pd, mb, scale_dtype, a, grid, s)
-                        : fx::dispatch_mfma_f16(p.nw, p.pd, mb, scale_dtype, a, grid, s);
-    if (!ok) return fail(FX_EINVAL, "no MFMA kernel for waves %d prefetch %d rows %d", p.nw, p.pd, mb);
-    rc = check_launch("w3_mfma_kernel");
+    a.row_blocks = p.row_blocks;
+    a.xcds = kXcds;
+    const dim3 grid(p.row_blocks * p.splits);
+    if (!fx::dispatch_mfma(x_dtype, p.tiles, p.nw, p.pd, mb, scale_dtype, a, grid, s))
+      return fail(FX_EINVAL, "no MFMA kernel for waves %d prefetch %d tiles %d rows %d", p.nw,
+                  p.pd, p.tiles, mb);
+    int rc = check_launch("w3_mfma_kernel");
     if (rc) return rc;
     if (partial) {
       rc = launch_finish(partial, ob, x_dtype, p.splits, mb * O, s);
@@ -293,7 +284,7 @@ int run_mfma(const void* x, int x_dtype, const uint8_t* planes, const void* scal
 
 extern "C" {
 
-int fx_abi_version(void) { return 2; }
+int fx_abi_version(void) { return 3; }
 
 const char* fx_last_error(void) { return g_error; }
 
@@ -351,7 +342,7 @@ int fx_w3_m1_out(const void* x, int x_dtype, const uint8_t* planes, const void* 
 size_t fx_w3_gemv_workspace_bytes(int M, int O, int K) {
   if (M < 1 || O < 1 || K < 128 || K % 128) return 0;
   const int G = K / 128;
-  const size_t mfma = mfma_workspace(M, O, G, default_mfma_plan(O, G)).total;
+  const size_t mfma = mfma_workspace(M, O, default_mfma_plan(O, G));
   const size_t lut = lut_route_workspace(M, O, K);
   return mfma > lut ? mfma : lut;
 }
@@ -372,27 +363,29 @@ int fx_w3_gemv(const void* x, int x_dtype, const uint8_t* planes, const void* sc
 }
 
 size_t fx_w3_gemv_config_workspace_bytes(int M, int O, int K, int waves, int prefetch,
-                                         int groups_per_split) {
-  if (M < 1 || O < 1 || K < 128 || K % 128) return 0;
+                                         int groups_per_split, int tiles) {
+  if (M < 1 || O < 1 || K < 128 || K % 128 || tiles < 1) return 0;
   const int G = K / 128;
-  return mfma_workspace(M, O, G, make_mfma_plan(O, G, waves, prefetch, groups_per_split)).total;
+  return mfma_workspace(M, O, make_mfma_plan(O, G, waves, prefetch, groups_per_split, tiles));
 }
 
 int fx_w3_gemv_config(const void* x, int x_dtype, const uint8_t* planes, const void* scales,
                       int scale_dtype, const uint8_t* zeros, const int16_t* perm, void* workspace,
                       size_t workspace_bytes, void* out, int M, int O, int K, int waves,
-                      int prefetch, int groups_per_split, void* stream) {
+                      int prefetch, int groups_per_split, int tiles, void* stream) {
   int rc = validate_payload(x, x_dtype, planes, scales, scale_dtype, M, O, K, FX_ARITH_STRUCTURAL);
   if (rc) return rc;
   if (!out) return fail(FX_EINVAL, "out must be non-null");
-  const bool supported = (waves == 2 || waves == 4 || waves == 8) &&
-                         (prefetch == 1 || prefetch == 2 || prefetch == 4);
-  if (!supported) return fail(FX_EINVAL, "unsupported waves/prefetch %d/%d", waves, prefetch);
+  const bool supported = (waves == 4 || waves == 8) &&
+                         (prefetch == 1 || prefetch == 2) &&
+                         (tiles == 1 || tiles == 2);
+  if (!supported)
+    return fail(FX_EINVAL, "unsupported waves/prefetch/tiles %d/%d/%d", waves, prefetch, tiles);
   const int G = K / 128;
   if (groups_per_split < 1) return fail(FX_EINVAL, "groups_per_split must be positive");
   return run_mfma(x, x_dtype, planes, scales, scale_dtype, zeros, perm, workspace,
                   workspace_bytes, out, M, O, K,
-                  make_mfma_plan(O, G, waves, prefetch, groups_per_split),
+                  make_mfma_plan(O, G, waves, prefetch, groups_per_split, tiles),
                   static_cast<hipStream_t>(stream));
 }
 

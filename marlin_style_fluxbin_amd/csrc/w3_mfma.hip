@@ -1,6 +1,7 @@
 // W3 g128 planar GEMV for gfx950 on the matrix cores: codes are dequantized in
 // registers into bf16 MFMA operands and multiplied against exact bf16
-// activations with fp32 accumulation.
+// activations with fp32 accumulation.  One launch per GEMV (plus a finish
+// launch when K is split over workgroups).
 //
 // Why not table lookups: a 256-entry activation table indexed by weight bytes
 // makes every lookup a data-dependent LDS read, and on gfx950 those serialise
@@ -19,19 +20,22 @@
 //   {0,4,2,6,1,5,3,7}[j], weighted 1 (j < 4) or 16 (j >= 4).
 // * B (activations): x * 2^E / weight_j, exact in the activation's own type
 //   (power-of-two scale), E chosen per (group, activation row) from max|x| so
-//   products are normal fp32.  fp16 activations use the fp16 MFMA with fp16 subnormal
-//   codes (q * 2^-24) the same way.
+//   products are normal fp32.  fp16 activations use the fp16 MFMA with fp16
+//   subnormal codes (q * 2^-24) the same way.
 // * Columns: one MFMA chain covers 4 groups at once; k-block b of the
 //   instruction carries group 4i+b and column c = b + 4m only sees k-block b,
 //   so D[row][b + 4m] is the group's dot product for activation row m.
 // y[m,o] = sum_g s[g,o] * (D * 2^(133-E) - z[g,o] * sum_{k in g} x[m,k]).
 //
-// x is first packed by w3_xprep_kernel (one wave per group, one pass) into the
-// B layout ([G][16 steps][MB][8]), per-group sums and exponents.  Each wave
-// stages one batch's B slice in its own LDS region (no workgroup barrier) and
-// prefetches the next batch.  K is split across the waves of a workgroup
-// (reduced through LDS) and optionally across workgroups (fp32 partials reduced
-// by w3_finish_kernel, stream-ordered, no device-scope fences).
+// Each wave builds the B operands of its own batch from x: the 16 lanes of
+// k-block b each load 8 consecutive activations of group 4i+b, reduce max|x|
+// and sum(x) over their DPP row, scale, and scatter the values into the wave's
+// LDS stage in operand order (no workgroup barrier; x is L2-resident).  A wave
+// applies one batch's operands to RT 16-row tiles.  Wave w of a workgroup
+// takes batches w, w + NW, ... of its K split and keeps PD of them in flight.
+// K splits across waves are reduced through LDS; across workgroups through
+// fp32 partials summed by w3_finish_kernel (stream-ordered, no device-scope
+// fences).
 #pragma once
 #include "common.h"
 
@@ -60,46 +64,12 @@ __device__ __forceinline__ int choose_exponent(float max_abs) {
   return (XDT == kBF16 ? 100 : 14) - e;
 }
 
-// x [MB, K] -> xs [Gp][16][MB][8] (B operands in the activation's type),
-// sx f32 [Gp][MB] (sum of the group's x), fe int [Gp][MB] (subnormal exponent - E),
-// with Gp = G rounded up to a multiple of 4 (the padding groups are zero).
-// One wave per (group, activation row); E is chosen per group from its max|x|.
+// Bits of a value that is exactly representable in the activation type (a
+// power-of-two multiple of one): bf16 keeps the high half of the fp32 bits.
 template <int XDT>
-__global__ __launch_bounds__(256) void w3_xprep_kernel(const uint16_t* __restrict__ x,
-                                                       const int16_t* __restrict__ perm,
-                                                       uint16_t* __restrict__ xs,
-                                                       float* __restrict__ sx,
-                                                       int* __restrict__ fe, int K, int MB) {
-  const int lane = threadIdx.x & 63;
-  const int g = blockIdx.x * 4 + (threadIdx.x >> 6);  // groups padded to a multiple of 4
-  const int m = blockIdx.y;
-  const bool real = g * 128 < K;                       // padding groups get zeros
-  const uint16_t* xr = x + size_t(m) * K;
-  float v[2];
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int k = g * 128 + h * 64 + lane;
-    v[h] = real ? to_f32<XDT>(xr[perm ? int(perm[k]) : k]) : 0.f;
-  }
-  const float mx = wave_max(fmaxf(fabsf(v[0]), fabsf(v[1])));
-  const float total = wave_sum(v[0] + v[1]);
-  const int E = choose_exponent<XDT>(mx);
-  if (lane == 0) {
-    sx[size_t(g) * MB + m] = total;
-    fe[size_t(g) * MB + m] = subnormal_exponent<XDT>() - E;
-  }
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int kl = h * 64 + lane;
-    const int w = kl >> 5, n = (kl & 31) >> 2, s = kl & 3;
-    const int step = 4 * w + s;
-    // nibble n -> operand slot: {0,4,2,6} -> 0..3 (weight 1), {1,5,3,7} -> 4..7 (weight 16)
-    const int j = (n & 1) ? (4 + ((n >> 2) & 1) + ((n >> 1) & 1) * 2)
-                          : (((n >> 2) & 1) + ((n >> 1) & 1) * 2);
-    // exact: power-of-two scaling of a bf16/fp16 value (ldexp handles the range)
-    const float scaled = ldexpf(v[h], (n & 1) ? E - 4 : E);
-    xs[((size_t(g) * 16 + step) * MB + m) * 8 + j] = from_f32<XDT>(scaled);
-  }
+__device__ __forceinline__ uint16_t exact_bits(float v) {
+  if constexpr (XDT == kBF16) return uint16_t(__float_as_uint(v) >> 16);
+  else return f32_to_f16_bits(v);
 }
 
 // Build the four 8-element A operands of one plane word (32 columns, steps s = 0..3).
@@ -128,11 +98,6 @@ __device__ __forceinline__ void dequant_word(unsigned p0, unsigned p1, unsigned 
   }
 }
 
-template <int SDT>
-__device__ __forceinline__ float scale_at(const uint16_t* scales, size_t idx) {
-  return to_f32<SDT>(scales[idx]);
-}
-
 // Buffer resource over [base, base + bytes): loads at offsets past the end
 // return zero instead of touching memory.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_resource(const void* base, size_t bytes) {
@@ -144,132 +109,227 @@ __device__ __forceinline__ u32x4_t load_b128(__amdgpu_buffer_rsrc_t r, int offse
   return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, offset, soffset, 0));
 }
 
+constexpr int kOutOfRange = int(0x80000000u);  // > every record count: loads return 0
+
 // Everything one wave loads for one batch, kept as raw bits: this lane's plane
-// row, its share of the batch's B slice, and the epilogue's scales, zero-points,
-// sums and exponents.  Nothing loaded is used before consume(), so the
-// prefetched batches stay in flight.
-template <int MB>
+// rows (one per row tile), its 8 activations per row (or, with a permutation,
+// its 8 column indices), and the epilogue's scales and zero-points.  Nothing
+// loaded is used before consume(), so the prefetched batches stay in flight.
+template <int MB, int RT>
 struct BatchLoads {
-  u32x4_t w[3];
-  u32x4_t b[MB];
-  unsigned s[4];   // scales of rows erow..erow+3 (vector path: s[0], s[1] hold pairs)
-  unsigned z[4];   // zero-points (vector path: z[0] holds four)
-  float sxv;
-  int fev;
+  u32x4_t w[RT][3];
+  u32x4_t xv[MB];    // activation bits of rows 0..MB-1 (PERM: xv[0] = 8 int16 columns)
+  unsigned s[RT][2]; // scales of rows erow..erow+3 of each tile, two per word
+  unsigned z[RT];    // zero-points of rows erow..erow+3, one per byte
 };
 
-// grid (ceil(O / 16), splits); block NW*64.  Workgroup: rows [16 bx, +16),
-// groups [gps*split, +gps) with gps a multiple of 4.  Wave w takes batches
-// w, w + NW, ... of its split and keeps PD of them in flight: their loads are
-// issued before the oldest one is dequantized and multiplied.  Rows past O and
-// groups past G need no masking of the A operand: padded groups have B = 0 and
-// rows past O get scale 0 and are never stored.
-template <int NW, int PD, int MB, int XDT, int SDT>
+// Workgroup index -> (row block, K split) so that the workgroups one XCD runs
+// (hardware dispatch deals consecutive workgroup ids round-robin over the XCDs)
+// take consecutive row blocks and share the scale / zero-point cache lines in
+// that XCD's L2.  A bijection for any grid size.
+__device__ __forceinline__ int xcd_local_index(int linear, int total, int xcds) {
+  const int xcd = linear % xcds, local = linear / xcds;
+  const int q = total / xcds, rem = total % xcds;
+  return xcd < rem ? xcd * (q + 1) + local : rem * (q + 1) + (xcd - rem) * q + local;
+}
+
+// grid (ceil(O / (16 RT)) * splits) workgroups of NW*64 threads.  Workgroup:
+// rows [16 RT b, +16 RT), groups [gps*split, +gps) with gps a multiple of 4.
+// Rows past O and groups past G need no masking: padded groups have zero
+// activations (so D = 0 and sum(x) = 0), and rows past O are never stored.
+// x is [MB, 128 G] row-major; with PERM, sorted column k reads x column perm[k].
+template <int NW, int PD, int MB, int RT, bool PERM, int XDT, int SDT>
 __global__ __launch_bounds__(NW * 64) void w3_mfma_kernel(
+    const uint16_t* __restrict__ x, const int16_t* __restrict__ perm,
     const uint8_t* __restrict__ planes, const uint16_t* __restrict__ scales,
-    const uint8_t* __restrict__ zeros, const uint16_t* __restrict__ xs,
-    const float* __restrict__ sx, const int* __restrict__ fe, float* __restrict__ partial,
-    uint16_t* __restrict__ out, int O, int G, int gps) {
-  __shared__ u32x4_t bstage[NW][64 * MB + 1];  // per-wave B slice of one batch + zero chunk
-  __shared__ float red[NW][16 * MB];
+    const uint8_t* __restrict__ zeros, float* __restrict__ partial,
+    uint16_t* __restrict__ out, int O, int G, int gps, int row_blocks, int xcds) {
+  // per wave: B operands [k-block][step][row] (16 B each), and zero operands
+  // [step][row] read by the lanes whose column belongs to another k-block
+  __shared__ u32x4_t bstage[NW][64 * MB];
+  __shared__ u32x4_t bzero[NW][16 * MB];
+  __shared__ float gsum[NW][4 * MB];   // sum of x per (k-block group, row)
+  __shared__ int gexp[NW][4 * MB];     // subnormal exponent - E per (k-block group, row)
+  __shared__ float red[NW][16 * RT * MB];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int split = blockIdx.y;
+  const int K = G * 128;
+  const int block = xcd_local_index(blockIdx.x, gridDim.x, xcds);
+  const int split = block / row_blocks;
+  const int row0 = (block - split * row_blocks) * (16 * RT);
   const int g0 = split * gps;
   const int g1 = min(G, g0 + gps);
   const int nbatch = (g1 - g0 + 3) >> 2;
-  const int row0 = blockIdx.x * 16;
-  const int Gp = (G + 3) & ~3;
   // four consecutive scales / zero-points of a row block are one aligned load
   const bool vec = (O & 3) == 0;
-  const bool has_zeros = zeros != nullptr;
+  // absent zero-points read as 0 (empty buffer) and become 4 through this OR
+  const unsigned zero_default = zeros ? 0u : 0x04040404u;
 
   const auto rp = buffer_resource(planes, size_t(G) * 3 * O * 16);
   const auto rs = buffer_resource(scales, size_t(G) * O * 2);
-  const auto rz = buffer_resource(has_zeros ? (const void*)zeros : (const void*)scales,
-                                  has_zeros ? size_t(G) * O : 0);
-  const auto rx = buffer_resource(xs, size_t(Gp) * 256 * MB);
-  const auto rsx = buffer_resource(sx, size_t(Gp) * MB * 4);
-  const auto rfe = buffer_resource(fe, size_t(Gp) * MB * 4);
+  const auto rz = buffer_resource(zeros ? (const void*)zeros : (const void*)scales,
+                                  zeros ? size_t(G) * O : 0);
+  const auto rx = buffer_resource(x, size_t(MB) * K * 2);
+  const auto rperm = buffer_resource(PERM ? (const void*)perm : (const void*)x, PERM ? size_t(K) * 2 : 0);
 
-  const int r = lane & 15;    // A role: row within tile
+  const int r = lane & 15;    // A role: row within tile; x role: 8-column chunk
   const int kb = lane >> 4;   // A role: k-block = group slot; D role: row block
   const int c = lane & 15;    // B / D role: column
   const int cslot = c & 3, cm = c >> 2;
+  const int cmc = cm < MB ? cm : 0;
   const bool b_active = (cslot == kb) && (cm < MB);
   u32x4_t* my_stage = bstage[wave];
-  if (lane == 0) my_stage[64 * MB] = u32x4_t{0u, 0u, 0u, 0u};
-  const u32x4_t* bsrc = b_active ? my_stage + kb * 16 * MB + cm : my_stage + 64 * MB;
-  const int bstride = b_active ? MB : 0;
-  const int row = row0 + r;
-  const int erow = row0 + 4 * kb;
+  uint16_t* stage16 = reinterpret_cast<uint16_t*>(my_stage);
+  if (lane < 16 * MB) bzero[wave][lane] = u32x4_t{0u, 0u, 0u, 0u};
+  // operand of step st: bsrc[st * MB]
+  const u32x4_t* bsrc = (b_active ? my_stage + kb * 16 * MB : bzero[wave]) + cmc;
   const int plane_stride = O * 16;
-  const int cmc = cm < MB ? cm : 0;
+  // x role: lane (kb, r) owns columns 8r .. 8r+7 of its group; they land in
+  // steps 4(r>>2) + s, operand slots je (weight 1) and je + 4 (weight 16).
+  const int xstep = 4 * (r >> 2);
+  const int je = ((r >> 1) & 1) + 2 * (r & 1);
 
-  auto issue = [&](int batch, BatchLoads<MB>& L) {
+  auto issue = [&](int batch, BatchLoads<MB, RT>& L) __attribute__((always_inline)) {
     const int gb = g0 + 4 * batch;
-    const int poff = ((gb + kb) * 3 * O + row) * 16;  // past the end -> zeros
-    L.w[0] = load_b128(rp, poff, 0);
-    L.w[1] = load_b128(rp, poff, plane_stride);
-    L.w[2] = load_b128(rp, poff, 2 * plane_stride);
+    const int poff = ((gb + kb) * 3 * O + row0 + r) * 16;  // past the end -> zeros
 #pragma unroll
-    for (int i = 0; i < MB; ++i) L.b[i] = load_b128(rx, ((gb * 16 * MB) + i * 64 + lane) * 16, 0);
-    const int ge = gb + cslot;
-    const int eoff = ge * O + erow;
-    if (vec) {
-      const uint2 s4 = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rs, eoff * 2, 0, 0));
-      L.s[0] = s4.x;
-      L.s[1] = s4.y;
-      L.z[0] = __builtin_amdgcn_raw_buffer_load_b32(rz, eoff, 0, 0);
-    } else {  // odd O (tests, tiny layers): element loads
+    for (int tt = 0; tt < RT; ++tt) {
+      L.w[tt][0] = load_b128(rp, poff + tt * 256, 0);
+      L.w[tt][1] = load_b128(rp, poff + tt * 256, plane_stride);
+      L.w[tt][2] = load_b128(rp, poff + tt * 256, 2 * plane_stride);
+    }
+    const int col = (gb + kb) * 128 + 8 * r;
+    const bool real = gb + kb < G;
+    if constexpr (PERM) {
+      L.xv[0] = load_b128(rperm, real ? col * 2 : kOutOfRange, 0);
+    } else {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        L.s[j] = __builtin_amdgcn_raw_buffer_load_b16(rs, (eoff + j) * 2, 0, 0);
-        L.z[j] = __builtin_amdgcn_raw_buffer_load_b8(rz, eoff + j, 0, 0);
+      for (int m = 0; m < MB; ++m) L.xv[m] = load_b128(rx, real ? (m * K + col) * 2 : kOutOfRange, 0);
+    }
+    const int eoff = (gb + cslot) * O + row0 + 4 * kb;
+#pragma unroll
+    for (int tt = 0; tt < RT; ++tt) {
+      const int e = eoff + 16 * tt;
+      if (vec) {
+        const uint2 s4 = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rs, e * 2, 0, 0));
+        L.s[tt][0] = s4.x;
+        L.s[tt][1] = s4.y;
+        L.z[tt] = __builtin_amdgcn_raw_buffer_load_b32(rz, e, 0, 0);
+      } else {  // O not a multiple of 4 (tests, tiny layers): element loads, same packing
+        unsigned sv[4], zv[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          sv[j] = __builtin_amdgcn_raw_buffer_load_b16(rs, (e + j) * 2, 0, 0);
+          zv[j] = __builtin_amdgcn_raw_buffer_load_b8(rz, e + j, 0, 0);
+        }
+        L.s[tt][0] = sv[0] | (sv[1] << 16);
+        L.s[tt][1] = sv[2] | (sv[3] << 16);
+        L.z[tt] = zv[0] | (zv[1] << 8) | (zv[2] << 16) | (zv[3] << 24);
       }
     }
-    L.sxv = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsx, (ge * MB + cmc) * 4, 0, 0));
-    L.fev = int(__builtin_amdgcn_raw_buffer_load_b32(rfe, (ge * MB + cmc) * 4, 0, 0));
   };
 
-  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  // B operands of one batch for activation row m from this lane's 8 values.
+  auto stage_row = [&](int m, const float v[8]) __attribute__((always_inline)) {
+    float mx = 0.f, sm = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      mx = fmaxf(mx, fabsf(v[i]));
+      sm += v[i];
+    }
+    mx = row16_max(mx);
+    sm = row16_sum(sm);
+    const int E = choose_exponent<XDT>(mx);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      uint16_t* dst = stage16 + ((kb * 16 + xstep + s) * MB + m) * 8;
+      dst[je] = exact_bits<XDT>(ldexpf(v[s], E));
+      dst[je + 4] = exact_bits<XDT>(ldexpf(v[4 + s], E - 4));
+    }
+    if (r == 0) {
+      gsum[wave][kb * MB + m] = sm;
+      gexp[wave][kb * MB + m] = subnormal_exponent<XDT>() - E;
+    }
+  };
+
+  float acc[RT][4];
+#pragma unroll
+  for (int tt = 0; tt < RT; ++tt)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[tt][j] = 0.f;
   int cur_batch = 0;
-  auto consume = [&](const BatchLoads<MB>& L) {
+  auto consume = [&](const BatchLoads<MB, RT>& L) __attribute__((always_inline)) {
+    const int gb = g0 + 4 * cur_batch;
+    if constexpr (PERM) {
+      const bool real = gb + kb < G;
+      const unsigned pw[4] = {L.xv[0].x, L.xv[0].y, L.xv[0].z, L.xv[0].w};
 #pragma unroll
-    for (int i = 0; i < MB; ++i) my_stage[i * 64 + lane] = L.b[i];
-    f32x4_t d = {0.f, 0.f, 0.f, 0.f};
-    const unsigned w0[4] = {L.w[0].x, L.w[0].y, L.w[0].z, L.w[0].w};
-    const unsigned w1[4] = {L.w[1].x, L.w[1].y, L.w[1].z, L.w[1].w};
-    const unsigned w2[4] = {L.w[2].x, L.w[2].y, L.w[2].z, L.w[2].w};
+      for (int m = 0; m < MB; ++m) {
+        float v[8];
 #pragma unroll
-    for (int word = 0; word < 4; ++word) {
-      u32x4_t a[4];
-      dequant_word(w0[word], w1[word], w2[word], a);
+        for (int i = 0; i < 8; ++i) {
+          const int src = int(int16_t(pw[i >> 1] >> (16 * (i & 1))));
+          const unsigned bits = __builtin_amdgcn_raw_buffer_load_b16(
+              rx, real ? (m * K + src) * 2 : kOutOfRange, 0, 0);
+          v[i] = to_f32<XDT>(uint16_t(bits));
+        }
+        stage_row(m, v);
+      }
+    } else {
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const u32x4_t b = bsrc[(4 * word + s) * bstride];
-        if constexpr (XDT == kBF16)
-          d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a[s]),
-                                                      __builtin_bit_cast(bf16x8_t, b), d, 0, 0, 0);
-        else
-          d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a[s]),
-                                                     __builtin_bit_cast(f16x8_t, b), d, 0, 0, 0);
+      for (int m = 0; m < MB; ++m) {
+        const unsigned xw[4] = {L.xv[m].x, L.xv[m].y, L.xv[m].z, L.xv[m].w};
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = to_f32<XDT>(uint16_t(xw[i >> 1] >> (16 * (i & 1))));
+        stage_row(m, v);
       }
     }
-    const int ge = g0 + 4 * cur_batch + cslot;
-    const bool e_ok = (cm < MB) && (ge < g1);
+    __builtin_amdgcn_wave_barrier();
+
+    f32x4_t d[RT];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const unsigned sb = vec ? ((j & 1) ? (L.s[j >> 1] >> 16) : (L.s[j >> 1] & 0xffffu)) : L.s[j];
-      const unsigned zb = !has_zeros ? 4u : (vec ? (L.z[0] >> (8 * j)) & 0xffu : L.z[j]);
-      const bool ok = e_ok && (erow + j < O);
-      const float se = ok ? to_f32<SDT>(uint16_t(sb)) : 0.f;
-      acc[j] += se * (ldexpf(d[j], L.fev) - float(zb) * L.sxv);
+    for (int tt = 0; tt < RT; ++tt) d[tt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int word = 0; word < 4; ++word) {
+      u32x4_t a[RT][4];
+#pragma unroll
+      for (int tt = 0; tt < RT; ++tt) {
+        const u32x4_t* w = L.w[tt];
+        dequant_word(w[0][word], w[1][word], w[2][word], a[tt]);
+      }
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const u32x4_t b = bsrc[(4 * word + s) * MB];
+#pragma unroll
+        for (int tt = 0; tt < RT; ++tt) {
+          if constexpr (XDT == kBF16)
+            d[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                __builtin_bit_cast(bf16x8_t, a[tt][s]), __builtin_bit_cast(bf16x8_t, b), d[tt], 0, 0, 0);
+          else
+            d[tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                __builtin_bit_cast(f16x8_t, a[tt][s]), __builtin_bit_cast(f16x8_t, b), d[tt], 0, 0, 0);
+        }
+      }
     }
+    const float sxv = gsum[wave][cslot * MB + cmc];
+    const int fev = gexp[wave][cslot * MB + cmc];
+#pragma unroll
+    for (int tt = 0; tt < RT; ++tt) {
+      const unsigned zw = L.z[tt] | zero_default;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const unsigned sb = (j & 1) ? (L.s[tt][j >> 1] >> 16) : (L.s[tt][j >> 1] & 0xffffu);
+        const float se = to_f32<SDT>(uint16_t(sb));
+        const float zf = float((zw >> (8 * j)) & 0xffu);
+        acc[tt][j] += se * (ldexpf(d[tt][j], fev) - zf * sxv);
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
   };
 
   // my batches: wave, wave + NW, ...; the i-th is batch wave + i*NW
   const int mine = wave < nbatch ? (nbatch - wave + NW - 1) / NW : 0;
-  BatchLoads<MB> ring[PD];
+  BatchLoads<MB, RT> ring[PD];
 #pragma unroll
   for (int i = 0; i < PD; ++i)
     if (i < mine) issue(wave + i * NW, ring[i]);
@@ -286,18 +346,22 @@ __global__ __launch_bounds__(NW * 64) void w3_mfma_kernel(
 
   // sum the four group slots of each activation row (lanes c = 4m .. 4m+3)
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    float v = acc[j];
-    v += __shfl_xor(v, 1, 64);
-    v += __shfl_xor(v, 2, 64);
-    acc[j] = v;
-  }
+  for (int tt = 0; tt < RT; ++tt)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float v = acc[tt][j];
+      v += dpp_move<kDppXor1>(v);
+      v += dpp_move<kDppXor2>(v);
+      acc[tt][j] = v;
+    }
   if (cslot == 0 && cm < MB) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) red[wave][(4 * kb + j) * MB + cm] = acc[j];
+    for (int tt = 0; tt < RT; ++tt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) red[wave][(16 * tt + 4 * kb + j) * MB + cm] = acc[tt][j];
   }
   __syncthreads();
-  for (int i = t; i < 16 * MB; i += NW * 64) {
+  for (int i = t; i < 16 * RT * MB; i += NW * 64) {
     float total = 0.f;
 #pragma unroll
     for (int wv = 0; wv < NW; ++wv) total += red[wv][i];

@@ -1,28 +1,55 @@
 // Launch plumbing for the MFMA W3 GEMV (w3_mfma.hip), shared by its
-// instantiation units (w3_mfma_bf16.hip, w3_mfma_f16.hip) and the C ABI.
+// instantiation units (w3_mfma_{bf16,f16}_t{1,2}[_perm].hip) and the C ABI.
 #pragma once
 #include "common.h"
 
 namespace fx {
 
 struct MfmaArgs {
+  const uint16_t* x;     // [mb, K] activations of this launch
+  const int16_t* perm;   // null: identity
   const uint8_t* planes;
   const uint16_t* scales;
   const uint8_t* zeros;
-  const uint16_t* xs;
-  const float* sx;
-  const int* fe;
   float* partial;  // null: write out directly (single K split)
   uint16_t* out;
   int O, G, gps;
+  int row_blocks;  // ceil(O / (16 * tiles))
+  int xcds;        // XCDs the hardware deals workgroups over
 };
 
-bool dispatch_mfma_bf16(int nw, int tr, int mb, int sdt, const MfmaArgs& a, dim3 grid,
-                        hipStream_t s);
-bool dispatch_mfma_f16(int nw, int tr, int mb, int sdt, const MfmaArgs& a, dim3 grid,
-                       hipStream_t s);
-// x [mb, K] -> packed B operands, per-group sums, exponents (one launch)
-bool launch_xprep(int xdt, const uint16_t* x, const int16_t* perm, uint16_t* xs, float* sx,
-                  int* fe, int K, int mb, hipStream_t s);
+// nw waves per workgroup in {4, 8}; pd batches in flight per wave in {1, 2};
+// mb activation rows in {1, 2, 4}; tiles 16-row tiles per wave in {1, 2};
+// sdt the scale dtype; the permutation instantiations are used when a.perm is
+// set.  False if no instantiation matches.
+#define FX_MFMA_DECL(NAME) \
+  bool NAME(int nw, int pd, int mb, int sdt, const MfmaArgs& a, dim3 grid, hipStream_t s);
+FX_MFMA_DECL(dispatch_mfma_bf16_t1)
+FX_MFMA_DECL(dispatch_mfma_bf16_t2)
+FX_MFMA_DECL(dispatch_mfma_f16_t1)
+FX_MFMA_DECL(dispatch_mfma_f16_t2)
+FX_MFMA_DECL(dispatch_mfma_bf16_t1_perm)
+FX_MFMA_DECL(dispatch_mfma_bf16_t2_perm)
+FX_MFMA_DECL(dispatch_mfma_f16_t1_perm)
+FX_MFMA_DECL(dispatch_mfma_f16_t2_perm)
+#undef FX_MFMA_DECL
+
+inline bool dispatch_mfma(int xdt, int tiles, int nw, int pd, int mb, int sdt, const MfmaArgs& a,
+                          dim3 grid, hipStream_t s) {
+  const bool p = a.perm != nullptr;
+  if (xdt == kBF16 && tiles == 1)
+    return p ? dispatch_mfma_bf16_t1_perm(nw, pd, mb, sdt, a, grid, s)
+             : dispatch_mfma_bf16_t1(nw, pd, mb, sdt, a, grid, s);
+  if (xdt == kBF16 && tiles == 2)
+    return p ? dispatch_mfma_bf16_t2_perm(nw, pd, mb, sdt, a, grid, s)
+             : dispatch_mfma_bf16_t2(nw, pd, mb, sdt, a, grid, s);
+  if (xdt == kF16 && tiles == 1)
+    return p ? dispatch_mfma_f16_t1_perm(nw, pd, mb, sdt, a, grid, s)
+             : dispatch_mfma_f16_t1(nw, pd, mb, sdt, a, grid, s);
+  if (xdt == kF16 && tiles == 2)
+    return p ? dispatch_mfma_f16_t2_perm(nw, pd, mb, sdt, a, grid, s)
+             : dispatch_mfma_f16_t2(nw, pd, mb, sdt, a, grid, s);
+  return false;
+}
 
 }  // namespace fx

@@ -43,11 +43,14 @@ def test_invalid_arguments_fail_closed_without_launching():
     assert rc == 1 and "bf16 scales" in lib.fx_last_error().decode()
     rc = lib.fx_w3_m1_out(dummy, 2, dummy, dummy, 2, None, None, None, dummy, 1, 64, 256, 1, 300, 0, None)
     assert rc == 1 and "row_tile" in lib.fx_last_error().decode()
-    # MFMA workspace: packed x (G*256*mb) + sums + exponents (+ partials when K is split)
-    assert lib.fx_w3_gemv_config_workspace_bytes(1, 4096, 4096, 8, 1, 32) == 32 * 256 + 256 + 256
-    assert lib.fx_w3_gemv_config_workspace_bytes(1, 64, 384, 2, 1, 4) == 4 * 256 + 256 + 256
-    assert lib.fx_w3_gemv_config_workspace_bytes(1, 4096, 4096, 8, 1, 16) == 32 * 256 + 512 + 2 * 4096 * 4
-    rc = lib.fx_w3_gemv_config(dummy, 2, dummy, dummy, 2, None, None, dummy, 1 << 20, dummy, 1, 64, 256, 3, 1, 4, None)
+    # MFMA workspace: fp32 partials [splits, mb, O] only when K is split over workgroups
+    assert lib.fx_w3_gemv_config_workspace_bytes(1, 4096, 4096, 8, 1, 32, 1) == 0
+    assert lib.fx_w3_gemv_config_workspace_bytes(1, 64, 384, 4, 1, 4, 2) == 0
+    assert lib.fx_w3_gemv_config_workspace_bytes(1, 4096, 4096, 8, 1, 16, 2) == 2 * 4096 * 4
+    assert lib.fx_w3_gemv_config_workspace_bytes(3, 4096, 4096, 8, 1, 8, 1) == 4 * 2 * 4096 * 4
+    rc = lib.fx_w3_gemv(dummy, 2, dummy, dummy, 2, None, None, None, 0, dummy, 1, 65536, 32768 * 4, 0, None)
+    assert rc == 1 and "2 GiB" in lib.fx_last_error().decode()
+    rc = lib.fx_w3_gemv_config(dummy, 2, dummy, dummy, 2, None, None, dummy, 1 << 20, dummy, 1, 64, 256, 3, 1, 4, 1, None)
     assert rc == 1 and "waves" in lib.fx_last_error().decode()
 
 

@@ -16,36 +16,43 @@ from tests.payloads import assert_half_ulp, config_codes, layout_from_codes, ora
 
 pytestmark = pytest.mark.gpu
 
-# (waves, batches in flight per wave, groups per K split)
-PLANS = [(2, 1, 4), (2, 4, 32), (4, 1, 4), (4, 2, 8), (4, 4, 16), (8, 1, 32), (8, 2, 16), (8, 4, 12)]
+# (waves, batches in flight per wave, groups per K split, 16-row tiles per wave)
+PLANS = [(4, 1, 4, 1), (4, 2, 8, 2), (4, 1, 16, 2), (8, 1, 32, 1), (8, 2, 16, 1), (8, 2, 12, 2),
+         (8, 1, 64, 2), (4, 2, 32, 1)]
 
 
-def _run_config(dl, x, out, waves, prefetch, gps):
+def _run_config(dl, x, out, waves, prefetch, gps, tiles, use_perm=True):
     lib = _lib.library()
     m, k = x.shape
     o = out.shape[1]
-    nbytes = lib.fx_w3_gemv_config_workspace_bytes(m, o, k, waves, prefetch, gps)
+    nbytes = lib.fx_w3_gemv_config_workspace_bytes(m, o, k, waves, prefetch, gps, tiles)
     ws = torch.empty(nbytes + 256, dtype=torch.uint8, device=x.device)
+    perm = dl["perm"].data_ptr() if use_perm else None
     _lib.check(lib.fx_w3_gemv_config(
         x.data_ptr(), _lib.dtype_code(x.dtype), dl["planes"].data_ptr(), dl["scales"].data_ptr(),
-        _lib.dtype_code(dl["scales"].dtype), _lib.ptr(dl.get("zeros")), dl["perm"].data_ptr(),
-        ws.data_ptr(), nbytes, out.data_ptr(), m, o, k, waves, prefetch, gps, _lib.stream_handle(x.device)),
+        _lib.dtype_code(dl["scales"].dtype), _lib.ptr(dl.get("zeros")), perm,
+        ws.data_ptr(), nbytes, out.data_ptr(), m, o, k, waves, prefetch, gps, tiles,
+        _lib.stream_handle(x.device)),
         "fx_w3_gemv_config")
 
 
 @pytest.mark.parametrize("o,k", [(64, 512), (37, 1536), (300, 2048), (1, 128), (17, 384)])
 @pytest.mark.parametrize("plan", PLANS)
 @pytest.mark.parametrize("m", [1, 2, 3, 4, 8])
-def test_mfma_plans(gpu, o, k, plan, m):
+@pytest.mark.parametrize("permute", [True, False])
+def test_mfma_plans(gpu, o, k, plan, m, permute):
+    """Every tiling (waves, prefetch depth, K split, row tiles) at ragged O, K and
+    M, with a random group-preserving permutation (gathered in the kernel) and
+    with the identity passed as a null permutation."""
     codes, scales, zeros, perm = config_codes(o, k, seed=o + k + m, zeros=True, scale_dtype=torch.float16,
-                                              permute=True)
+                                              permute=permute)
     layout = layout_from_codes(codes, scales, zeros, perm)
     dl = {n: t.to(gpu) for n, t in layout.items()}
     x = torch.randn(m, k, generator=torch.Generator().manual_seed(m)).to(torch.bfloat16)
     out = torch.full((m, o), float("nan"), dtype=torch.bfloat16, device=gpu)
-    _run_config(dl, x.to(gpu), out, *plan)
+    _run_config(dl, x.to(gpu), out, *plan, use_perm=permute)
     exact = w3.matvec_exact(x.float().numpy(), oracle_layout(layout))
-    assert_half_ulp(out.float().cpu().numpy(), exact, "bf16", what=f"plan {plan} m {m}")
+    assert_half_ulp(out.float().cpu().numpy(), exact, "bf16", what=f"plan {plan} m {m} perm {permute}")
 
 
 @pytest.mark.parametrize("xdtype,tag", [(torch.bfloat16, "bf16"), (torch.float16, "f16")])
@@ -57,7 +64,7 @@ def test_mfma_dtypes_and_zero_modes(gpu, xdtype, tag, scale_dtype, zeros):
     dl = {n: t.to(gpu) for n, t in layout.items()}
     x = torch.randn(1, 1024, generator=torch.Generator().manual_seed(3)).to(xdtype)
     out = torch.empty(1, 256, dtype=xdtype, device=gpu)
-    _run_config(dl, x.to(gpu), out, 8, 2, 8)
+    _run_config(dl, x.to(gpu), out, 8, 2, 8, 2)
     exact = w3.matvec_exact(x.float().numpy(), oracle_layout(layout))
     # fp16 MFMA products with subnormal fp16 code operands round at ~2e-7 relative
     assert_half_ulp(out.float().cpu().numpy(), exact, tag, rel_slack=2e-6 if tag == "bf16" else 3e-5)
@@ -71,7 +78,7 @@ def test_mfma_activation_range(gpu, scale):
     dl = {n: t.to(gpu) for n, t in layout.items()}
     x = (torch.randn(1, 512, generator=torch.Generator().manual_seed(4)) * scale).to(torch.bfloat16)
     out = torch.empty(1, 128, dtype=torch.bfloat16, device=gpu)
-    _run_config(dl, x.to(gpu), out, 4, 1, 4)
+    _run_config(dl, x.to(gpu), out, 4, 1, 4, 1)
     exact = w3.matvec_exact(x.float().numpy(), oracle_layout(layout))
     assert np.all(np.isfinite(out.float().cpu().numpy()))
     assert_half_ulp(out.float().cpu().numpy(), exact, "bf16", what=f"scale {scale}")
@@ -82,5 +89,5 @@ def test_mfma_zero_activation(gpu):
     layout = layout_from_codes(codes, scales, z, perm)
     dl = {n: t.to(gpu) for n, t in layout.items()}
     out = torch.full((1, 64), float("nan"), dtype=torch.bfloat16, device=gpu)
-    _run_config(dl, torch.zeros(1, 256, dtype=torch.bfloat16, device=gpu), out, 4, 1, 4)
+    _run_config(dl, torch.zeros(1, 256, dtype=torch.bfloat16, device=gpu), out, 4, 1, 4, 2)
     assert torch.equal(out, torch.zeros_like(out))
