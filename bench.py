@@ -12,8 +12,13 @@ is algorithmic bytes of all GEMVs in the timed replays / their wall time on the
 GPU (HIP events on the launch stream).
 
 Per shape, a graph of >= 50 launches over rotating payload copies (>= 300 MB)
-gives the average launch duration; the same-run bf16 arm runs torch.nn.functional.linear
-(hipBLASLt) on dequantized bf16 weights with the same rotation.  The CPU baseline
+gives the average launch duration (one w3_mfma_kernel launch per call, plus a
+finish launch only for split-K plans); the same-run bf16 arm runs torch.matmul
+(hipBLASLt) on dequantized bf16 weights with the same rotation.  ``roofline``
+is the gate/up shape's measurement: the dominant kernel of a decode step.
+``roofline.traffic`` is the HBM bytes per launch measured with rocprofv3 PMC
+counters (FETCH_SIZE + WRITE_SIZE, scaled by a plain read kernel of known size),
+read from ``profiles/w3_mfma_traffic.json`` when present.  The CPU baseline
 times the oracle's dequantize-then-matmul restatement of the reference's dense
 CPU route on a bounded sample.
 """
@@ -175,6 +180,81 @@ def cpu_baseline(seconds_budget=15.0):
                       f"x@W.T, {per_call*1e3:.1f} ms/call, numpy single thread"}
 
 
+def pmc_target():
+    """Workload for ``rocprofv3 --pmc`` passes: the gate/up W3 GEMV (default plan)
+    over 24 rotating payloads, twice; the LUT kernel (reference-style tables in
+    LDS) at the same shape, 8 launches; and torch's copy kernel over 16 distinct
+    20 MiB float32 buffers, whose FETCH_SIZE / WRITE_SIZE readings calibrate the
+    counters to bytes."""
+    import torch
+
+    from marlin_style_fluxbin_amd import W3Gemv
+    from marlin_style_fluxbin_amd.w3_lut_deployment import inline_main, workspace_shape
+
+    device = torch.device("cuda:0")
+    gen = torch.Generator(device=device).manual_seed(0)
+    o, k = UNIQUE["gate/up"]
+    payloads = [make_payload(o, k, device, gen) for _ in range(24)]
+    gemvs = [W3Gemv(p, perm_identity=True) for p in payloads]
+    x = torch.randn(1, k, device=device, generator=gen).to(torch.bfloat16)
+    out = torch.empty(1, o, device=device, dtype=torch.bfloat16)
+    for _ in range(2):
+        for gemv in gemvs:
+            gemv(x, out)
+    partial = torch.empty(workspace_shape(o, k), dtype=torch.float32, device=device)
+    for p in payloads[:8]:
+        inline_main(x, p, partial, row_tile=256)
+    src = [torch.empty(CALIBRATION_BYTES // 4, device=device) for _ in range(16)]
+    dst = [torch.empty_like(t) for t in src]
+    for a, b in zip(src, dst):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print("pmc target done", flush=True)
+
+
+CALIBRATION_BYTES = 20 * 1024 * 1024
+
+
+def summarize_pmc(csv_paths, out_json):
+    """Average rocprofv3 counter CSVs per kernel; scale FETCH_SIZE / WRITE_SIZE
+    (KiB per dispatch) by what they read for the copy kernel of known size."""
+    import csv
+    from collections import defaultdict
+
+    values = defaultdict(lambda: defaultdict(list))
+    for path in csv_paths:
+        with open(path, newline="") as f:
+            for row in csv.DictReader(f):
+                values[row["Kernel_Name"]][row["Counter_Name"]].append(float(row["Counter_Value"]))
+    mean = {k: {c: sum(v) / len(v) for c, v in d.items()} for k, d in values.items()}
+    # the 20 MiB same-dtype copies run as the runtime's buffer-copy kernel
+    copy = [k for k in mean if "copyBuffer" in k and "FETCH_SIZE" in mean[k]]
+    w3 = [k for k in mean if "w3_mfma_kernel" in k]
+    if not copy or not w3:
+        raise SystemExit("counter CSVs lack the copy kernel or the W3 kernel")
+    kib = CALIBRATION_BYTES / 1024
+    fetch_scale = kib / mean[copy[0]]["FETCH_SIZE"]
+    write_scale = kib / mean[copy[0]]["WRITE_SIZE"] if mean[copy[0]].get("WRITE_SIZE") else None
+    kernel = w3[0]
+    fetch = mean[kernel]["FETCH_SIZE"] * fetch_scale * 1024
+    write = mean[kernel].get("WRITE_SIZE", 0.0) * (write_scale or 1.0) * 1024
+    o, k = UNIQUE["gate/up"]
+    summary = {
+        "kernel": kernel.split("(")[0],
+        "workload": "gate/up 12288x4096 M=1, fp16 scales, uint8 zeros, identity perm",
+        "fetch_kib_raw": round(mean[kernel]["FETCH_SIZE"], 1),
+        "write_kib_raw": round(mean[kernel].get("WRITE_SIZE", 0.0), 1),
+        "fetch_scale": round(fetch_scale, 4),
+        "write_scale": None if write_scale is None else round(write_scale, 4),
+        "traffic_bytes": int(round(fetch + write)),
+        "algorithmic_bytes": algorithmic_bytes(o, k),
+        "counters": {k.split("(")[0]: {c: round(v, 1) for c, v in d.items()} for k, d in mean.items()
+                     if "w3_" in k or "copyBuffer" in k},
+    }
+    Path(out_json).write_text(json.dumps(summary, indent=1) + "\n")
+    print(json.dumps(summary, indent=1))
+
+
 def main():
     parser = argparse.ArgumentParser()
     parser.add_argument("--gpus", type=int, default=1)
@@ -183,7 +263,16 @@ def main():
     parser.add_argument("--layers", type=int, default=8)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--shapes", default="all", help="comma list of q/o,k/v,gate/up,down or all")
+    parser.add_argument("--pmc-target", action="store_true", help="run the counter-collection workload")
+    parser.add_argument("--summarize-pmc", nargs="+", metavar="CSV",
+                        help="rocprofv3 counter CSVs -> profiles/w3_mfma_traffic.json")
     args = parser.parse_args()
+    if args.summarize_pmc:
+        summarize_pmc(args.summarize_pmc, ROOT / "profiles" / "w3_mfma_traffic.json")
+        return
+    if args.pmc_target:
+        pmc_target()
+        return
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
               "(each box has one MI355X); run with --gpus 1", file=sys.stderr)
@@ -231,6 +320,10 @@ def main():
     value = step_bytes / (ms / 1e3) / 1e9
 
     dominant = shapes.get("gate/up") or next(iter(shapes.values()))
+    traffic = None
+    traffic_file = ROOT / "profiles" / "w3_mfma_traffic.json"
+    if traffic_file.exists() and "gate/up" in shapes:
+        traffic = json.loads(traffic_file.read_text()).get("traffic_bytes")
     result = {
         "metric": "W3 GEMV HBM GB/s (% of peak) per Qwen3-8B shape; batch-1 decode tokens/sec",
         "value": round(value, 1),
@@ -242,7 +335,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "u8 codes, fp32 accumulate, bf16 io",
+        "dtype": "bf16",
         "data": "synthetic (random W3 codes, fp16 scales U[0.005,0.02], zeros U{3,4}, bf16 x ~ N(0,1))",
         "config": {
             "workload": f"config 1: 7 Qwen3-8B Linear shapes at M=1 x {args.layers} distinct layers per step",
@@ -255,8 +348,10 @@ def main():
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": dominant["w3_frac_hbm"],
-            "traffic": None,
-            "kernel": f"w3_lut_kernel at gate/up {dominant['O']}x{dominant['K']}, M=1",
+            "traffic": traffic,
+            "algorithmic_bytes": dominant["algorithmic_bytes"],
+            "kernel": f"w3_mfma_kernel at gate/up {dominant['O']}x{dominant['K']}, M=1 "
+                      f"(average launch over {dominant['copies']} rotating payloads)",
         },
     }
     if not args.no_cpu_baseline:
