@@ -111,6 +111,41 @@ int fx_w3_restore(const uint8_t *planes, const void *scales, int scale_dtype,
                   const uint8_t *zeros, const int16_t *perm, void *weight, int weight_dtype,
                   int O, int K, void *stream);
 
+/*
+ * Reference: rms_norm_reference / fused_rms_norm_forward (fused_modules.py:30-63),
+ * i.e. stock Qwen3RMSNorm.forward (transformers modeling_qwen3.py), optionally
+ * fused with the decoder layer's residual add.  x, residual, out, residual_out are
+ * [rows, hidden] row-major, weight [hidden], all in dtype, 16-byte aligned,
+ * hidden % 8 == 0.  With residual (non-NULL): s = round(x + residual) is written
+ * to residual_out, then out = round(weight * round(s * rsqrt(mean(s^2) + eps)));
+ * without: the same on x.  out may alias x; residual_out may alias x or
+ * residual.
+ */
+int fx_rmsnorm(const void *x, const void *residual, const void *weight, void *out,
+               void *residual_out, int rows, int hidden, float eps, int dtype, void *stream);
+
+#define FX_ROPE_NONE 0
+#define FX_ROPE_STOCK 1 /* HF apply_rotary_pos_emb: round(round(y*cos) + round(rot(y)*sin)) */
+#define FX_ROPE_FUSED 2 /* fused_apply_rotary_pos_emb (addcmul): round(round(y*cos) + rot(y)*sin) */
+
+/*
+ * Reference: per-head q_norm / k_norm (Qwen3RMSNorm over head_dim) followed by
+ * apply_rotary_pos_emb (modeling_qwen3.py) or fused_apply_rotary_pos_emb
+ * (fused_modules.py:66-85), for up to 4 tensors in one launch.  Tensor i has
+ * batch x heads[i] x seq rows of head_dim contiguous elements; strides[6i..6i+2]
+ * are its input element strides (batch, head, position), strides[6i+3..6i+5] its
+ * output strides (e.g. a KV cache slot).  weights[i] NULL: no norm; rope[i] 0: no
+ * rotation (a strided copy).  cos/sin rows are at batch*cos_strides[0] +
+ * position*cos_strides[1] (+ position[0]*head_dim when the device scalar
+ * `position` is given, for graph-replayed decode).  Outputs must not overlap
+ * inputs of another tensor.
+ */
+int fx_head_norm_rope(int ntensors, const void *const *inputs, void *const *outputs,
+                      const void *const *weights, const int *heads, const int *rope,
+                      const long long *strides, int batch, int seq, int head_dim,
+                      const void *cos, const void *sin, const long long *cos_strides,
+                      const int *position, float eps, int rope_mode, int dtype, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

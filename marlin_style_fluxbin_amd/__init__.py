@@ -38,4 +38,14 @@ from .w3_lut_deployment import (  # noqa: F401
     workspace_shape,
 )
 
+from .fused_modules import (  # noqa: F401
+    add_rms_norm,
+    fused_apply_rotary_pos_emb,
+    fused_qwen3_modules,
+    fused_rms_norm_forward,
+    head_norm_rope,
+    rms_norm,
+    rms_norm_reference,
+)
+
 __version__ = "0.1.0"

@@ -19,12 +19,14 @@ ABI_VERSION = 3
 
 FX_F32, FX_F16, FX_BF16 = 0, 1, 2
 ARITH_STRUCTURAL, ARITH_DECODED_BF16 = 0, 1
+ROPE_NONE, ROPE_STOCK, ROPE_FUSED = 0, 1, 2
 
 _DTYPE_CODES = {torch.float32: FX_F32, torch.float16: FX_F16, torch.bfloat16: FX_BF16}
 
 _p = ctypes.c_void_p
 _i = ctypes.c_int
 _sz = ctypes.c_size_t
+_f = ctypes.c_float
 
 # name -> (restype, argtypes); mirrors include/fluxbin_amd.h
 SIGNATURES: dict[str, tuple] = {
@@ -38,6 +40,8 @@ SIGNATURES: dict[str, tuple] = {
     "fx_w3_gemv_config_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _i, _i]),
     "fx_w3_gemv_config": (_i, [_p, _i, _p, _p, _i, _p, _p, _p, _sz, _p, _i, _i, _i, _i, _i, _i, _i, _p]),
     "fx_w3_restore": (_i, [_p, _p, _i, _p, _p, _p, _i, _i, _i, _p]),
+    "fx_rmsnorm": (_i, [_p, _p, _p, _p, _p, _i, _i, _f, _i, _p]),
+    "fx_head_norm_rope": (_i, [_i, _p, _p, _p, _p, _p, _p, _i, _i, _i, _p, _p, _p, _p, _f, _i, _i, _p]),
 }
 
 _lock = threading.Lock()

@@ -11,6 +11,7 @@
 #include "w3_lut_launch.h"
 #include "w3_lut.hip"
 #include "w3_mfma_launch.h"
+#include "norms_launch.h"
 
 using fx::LutArgs;
 using fx::MfmaArgs;
@@ -416,6 +417,79 @@ int fx_w3_restore(const uint8_t* planes, const void* scales, int scale_dtype,
     hipLaunchKernelGGL((fx::w3_restore_kernel<fx::kF16, fx::kF16>), grid, dim3(256), 0, s, planes,
                        sc, zeros, perm, w, O, G);
   return check_launch("w3_restore_kernel");
+}
+
+int fx_rmsnorm(const void* x, const void* residual, const void* weight, void* out,
+               void* residual_out, int rows, int hidden, float eps, int dtype, void* stream) {
+  if (!x || !weight || !out) return fail(FX_EINVAL, "x, weight and out must be non-null");
+  if (residual && !residual_out) return fail(FX_EINVAL, "a residual needs residual_out");
+  if (!is_half_dtype(dtype)) return fail(FX_EINVAL, "dtype must be fp16 or bf16");
+  if (rows < 1 || hidden < 8 || hidden % 8 != 0 || hidden > (1 << 20))
+    return fail(FX_EINVAL, "rows must be positive and hidden a multiple of 8, got %d x %d", rows, hidden);
+  const void* ptrs[5] = {x, residual, weight, out, residual_out};
+  for (const void* p : ptrs)
+    if (reinterpret_cast<uintptr_t>(p) % 16 != 0) return fail(FX_EINVAL, "tensors must be 16-byte aligned");
+  if (!(eps >= 0.f)) return fail(FX_EINVAL, "eps must be non-negative");
+  fx::launch_rmsnorm(dtype, static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(residual),
+                     static_cast<const uint16_t*>(weight), static_cast<uint16_t*>(out),
+                     static_cast<uint16_t*>(residual_out), rows, hidden, eps,
+                     static_cast<hipStream_t>(stream));
+  return check_launch("rmsnorm_kernel");
+}
+
+int fx_head_norm_rope(int ntensors, const void* const* inputs, void* const* outputs,
+                      const void* const* weights, const int* heads, const int* rope,
+                      const long long* strides, int batch, int seq, int head_dim,
+                      const void* cos, const void* sin, const long long* cos_strides,
+                      const int* position, float eps, int rope_mode, int dtype, void* stream) {
+  if (ntensors < 1 || ntensors > fx::kMaxHeadTensors)
+    return fail(FX_EINVAL, "ntensors must be in [1,%d]", fx::kMaxHeadTensors);
+  if (!inputs || !outputs || !heads || !rope || !strides)
+    return fail(FX_EINVAL, "tensor arrays must be non-null");
+  if (!is_half_dtype(dtype)) return fail(FX_EINVAL, "dtype must be fp16 or bf16");
+  if (batch < 1 || seq < 1 || head_dim < 2 || head_dim % 2 || head_dim > 4096)
+    return fail(FX_EINVAL, "bad batch/seq/head_dim %d/%d/%d", batch, seq, head_dim);
+  if (rope_mode < fx::kRopeNone || rope_mode > fx::kRopeFused)
+    return fail(FX_EINVAL, "unknown rope_mode %d", rope_mode);
+  if (!(eps >= 0.f)) return fail(FX_EINVAL, "eps must be non-negative");
+  fx::HeadNormRopeArgs a = {};
+  a.ntensors = ntensors;
+  a.seq = seq;
+  a.head_dim = head_dim;
+  a.eps = eps;
+  a.rope_mode = rope_mode;
+  a.position = position;
+  bool any_rope = false;
+  long long total_rows = 0;
+  for (int i = 0; i < ntensors; ++i) {
+    if (!inputs[i] || !outputs[i]) return fail(FX_EINVAL, "tensor %d: null input or output", i);
+    if (heads[i] < 1) return fail(FX_EINVAL, "tensor %d: heads must be positive", i);
+    fx::HeadTensor& t = a.t[i];
+    t.in = inputs[i];
+    t.out = outputs[i];
+    t.weight = weights ? weights[i] : nullptr;
+    for (int j = 0; j < 3; ++j) {
+      t.in_stride[j] = strides[6 * i + j];
+      t.out_stride[j] = strides[6 * i + 3 + j];
+    }
+    t.heads = heads[i];
+    t.rope = rope[i] ? 1 : 0;
+    any_rope = any_rope || (t.rope && rope_mode != fx::kRopeNone);
+    const long long r = (long long)batch * heads[i] * seq;
+    if (r > (1 << 24)) return fail(FX_EINVAL, "tensor %d: too many rows", i);
+    a.rows[i] = int(r);
+    total_rows += r;
+  }
+  if (total_rows > (1 << 26)) return fail(FX_EINVAL, "too many rows");
+  if (any_rope) {
+    if (!cos || !sin || !cos_strides) return fail(FX_EINVAL, "RoPE needs cos, sin and their strides");
+    a.cos = cos;
+    a.sin = sin;
+    a.cs_stride[0] = cos_strides[0];
+    a.cs_stride[1] = cos_strides[1];
+  }
+  fx::launch_head_norm_rope(dtype, a, static_cast<hipStream_t>(stream));
+  return check_launch("head_norm_rope_kernel");
 }
 
 }  // extern "C"

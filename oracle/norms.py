@@ -29,8 +29,8 @@ from .bf16 import round_to
 def rms_norm(x: np.ndarray, weight: np.ndarray, eps: float, dtype: str = "bf16") -> np.ndarray:
     """Qwen3RMSNorm over the last axis; ``x``/``weight`` hold ``dtype`` values."""
     h = np.asarray(x, dtype=np.float32)
-    variance = np.float32(np.mean(h.astype(np.float64) ** 2, axis=-1, keepdims=True))
-    inv = np.float32(1.0 / np.sqrt(np.float64(variance) + np.float64(np.float32(eps))))
+    variance = np.mean(h.astype(np.float64) ** 2, axis=-1, keepdims=True).astype(np.float32)
+    inv = (1.0 / np.sqrt(variance.astype(np.float64) + np.float64(np.float32(eps)))).astype(np.float32)
     normed = round_to((h * inv).astype(np.float32), dtype)
     return round_to(np.asarray(weight, dtype=np.float32) * normed, dtype)
 
@@ -41,9 +41,14 @@ def rope_inv_freq(head_dim: int, theta: float) -> np.ndarray:
     return (np.float32(1.0) / powered).astype(np.float32)
 
 
-def rope_cos_sin(positions, head_dim: int, theta: float, dtype: str = "bf16"):
-    """``[L] -> ([L, head_dim], [L, head_dim])`` cos/sin as HF builds them."""
-    inv = rope_inv_freq(head_dim, theta)
+def rope_cos_sin(positions, head_dim: int, theta: float, dtype: str = "bf16", inv_freq=None):
+    """``[L] -> ([L, head_dim], [L, head_dim])`` cos/sin as HF builds them.
+
+    ``inv_freq`` (fp32 ``[head_dim/2]``) defaults to :func:`rope_inv_freq`; a
+    caller may pass another fp32 rounding of the same frequencies (torch's ``pow``
+    can differ from numpy's in the last bit, and positions up to 4096 amplify it).
+    """
+    inv = rope_inv_freq(head_dim, theta) if inv_freq is None else np.asarray(inv_freq, np.float32)
     pos = np.asarray(positions, dtype=np.float32).reshape(-1, 1)
     freqs = (pos * inv[None, :]).astype(np.float32)
     emb = np.concatenate([freqs, freqs], axis=-1)
