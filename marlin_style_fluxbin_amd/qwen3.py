@@ -51,3 +51,103 @@ def expected_qwen3_linear_shape(config: dict[str, Any], module: str) -> list[int
 
 def qwen3_8b_linear_shapes() -> dict[str, tuple[int, int]]:
     return {m: tuple(expected_qwen3_linear_shape(ARCHITECTURE, m)) for m in QWEN3_LINEAR_MODULES}
+
+
+def qwen3_config(**overrides):
+    """``transformers.Qwen3Config`` of the Qwen3-8B architecture (random-init decode
+    benchmarks), full attention, untied bf16 LM head; keyword overrides shrink it."""
+    from transformers import Qwen3Config
+
+    values = dict(
+        hidden_size=ARCHITECTURE["hidden_size"], intermediate_size=ARCHITECTURE["intermediate_size"],
+        num_hidden_layers=ARCHITECTURE["num_hidden_layers"],
+        num_attention_heads=ARCHITECTURE["num_attention_heads"],
+        num_key_value_heads=ARCHITECTURE["num_key_value_heads"], head_dim=ARCHITECTURE["head_dim"],
+        vocab_size=VOCAB_SIZE, rms_norm_eps=RMS_NORM_EPS, max_position_embeddings=40960,
+        rope_parameters={"rope_type": "default", "rope_theta": ROPE_THETA}, tie_word_embeddings=False,
+        attn_implementation="sdpa",
+    )
+    values.update(overrides)
+    return Qwen3Config(**values)
+
+
+def random_qwen3_model(config, *, device, dtype, seed: int = 0):
+    """Random-init ``Qwen3ForCausalLM`` (HF init: weights ~ N(0, initializer_range=0.02))
+    built directly on ``device`` in ``dtype``, in eval mode."""
+    import torch
+    from transformers.models.qwen3.modeling_qwen3 import Qwen3ForCausalLM
+
+    torch.manual_seed(seed)
+    previous = torch.get_default_dtype()
+    torch.set_default_dtype(dtype)
+    try:
+        with torch.device(device):
+            model = Qwen3ForCausalLM(config)
+    finally:
+        torch.set_default_dtype(previous)
+    return model.eval()
+
+
+def quantize_w3_rtn(weight, *, scale_dtype=None, zeros: bool = True) -> dict:
+    """Round-to-nearest W3 g128 planar payload of a dense ``[O, K]`` weight.
+
+    Asymmetric per (row, 128-column group): ``s = (max - min) / 7`` rounded to
+    ``scale_dtype`` (fp16 by default), ``z = clamp(round(-min / s), 0, 7)``,
+    ``q = clamp(round(w / s) + z, 0, 7)``; identity permutation.  With
+    ``zeros=False`` the GPTQ-symmetric convention ``s = 2 max|w| / 7``, ``z = 4``
+    is used and no ``zeros`` field is stored.  Runs on the weight's device.
+    """
+    import torch
+
+    from .gptq_deployment import planar_from_codes
+
+    scale_dtype = torch.float16 if scale_dtype is None else scale_dtype
+    o, k = weight.shape
+    if k % 128:
+        raise ValueError("K must be a multiple of 128")
+    w = weight.detach().float().reshape(o, k // 128, 128)
+    if zeros:
+        lo = w.amin(-1)
+        hi = w.amax(-1)
+        scale = ((hi - lo) / 7).to(scale_dtype).float()
+        scale = torch.where(scale > 0, scale, torch.ones_like(scale))
+        zero = torch.clamp(torch.round(-lo / scale), 0, 7)
+    else:
+        scale = (2 * w.abs().amax(-1) / 7).to(scale_dtype).float()
+        scale = torch.where(scale > 0, scale, torch.ones_like(scale))
+        zero = torch.full_like(scale, 4.0)
+    q = torch.clamp(torch.round(w / scale[..., None]) + zero[..., None], 0, 7).to(torch.uint8)
+    codes = q.reshape(o, k).t().contiguous()  # [K, O]
+    layout = {
+        "planes": planar_from_codes(codes),
+        "scales": scale.t().contiguous().to(scale_dtype),          # [G, O]
+        "perm": torch.arange(k, dtype=torch.int16, device=weight.device),
+    }
+    if zeros:
+        layout["zeros"] = zero.t().contiguous().to(torch.uint8)
+    return layout
+
+
+def quantize_qwen3_block(block, **kwargs) -> dict:
+    """W3 payload ``{"<module>.<field>": tensor}`` for the seven Linears of a block."""
+    payload = {}
+    for name in QWEN3_LINEAR_MODULES:
+        layout = quantize_w3_rtn(block.get_submodule(name).weight, **kwargs)
+        payload.update({f"{name}.{field}": value for field, value in layout.items()})
+    return payload
+
+
+def w3_quantize_qwen3_model(model, *, fallback: str = "dense", row_tile_by_shape=None, **kwargs) -> int:
+    """Replace every decoder block's seven Linears by ``PackedW3Linear`` (in place).
+    Returns the number of replaced Linears."""
+    from .w3_lut_deployment import QWEN3_ROW_TILE_BY_SHAPE, replace_w3_block_linears
+
+    count = 0
+    for block in model.model.layers:
+        payload = quantize_qwen3_block(block, **kwargs)
+        policy = row_tile_by_shape
+        if policy is None:
+            shapes = {tuple(block.get_submodule(n).weight.shape) for n in QWEN3_LINEAR_MODULES}
+            policy = None if shapes <= set(QWEN3_ROW_TILE_BY_SHAPE) else {s: 256 for s in shapes}
+        count += len(replace_w3_block_linears(block, payload, fallback=fallback, row_tile_by_shape=policy))
+    return count
