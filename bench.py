@@ -180,6 +180,72 @@ def cpu_baseline(seconds_budget=15.0):
                       f"x@W.T, {per_call*1e3:.1f} ms/call, numpy single thread"}
 
 
+def decode_bench(layers=36, prefix=512, steps=32, replays=5, seed=0):
+    """Config 3: random-init Qwen3-8B architecture, batch-1 greedy decode of
+    ``steps`` tokens after a ``prefix``-token prefill, every step in one hipGraph
+    (StaticDecodeSession).  bf16 arm first (HF Linears, hipBLASLt), then the same
+    model W3-quantized in place (RTN, fp16 scales, zeros).  Both arms use the
+    fused RMSNorm / RoPE modules.  The W3 arm's greedy trace is gated against its
+    own dynamic-KV trace (prefill via the dense fallback, packed M=1 steps)."""
+    import statistics
+
+    import torch
+
+    from marlin_style_fluxbin_amd.full_model_trial import compare_trace, decode_trace, validate_routes
+    from marlin_style_fluxbin_amd.fused_modules import fused_qwen3_modules
+    from marlin_style_fluxbin_amd.qwen3 import qwen3_config, random_qwen3_model, w3_quantize_qwen3_model
+    from marlin_style_fluxbin_amd.static_decode import StaticDecodeSession, prepared_linears
+
+    device = torch.device("cuda:0")
+    config = qwen3_config(num_hidden_layers=layers)
+    t0 = time.perf_counter()
+    model = random_qwen3_model(config, device=device, dtype=torch.bfloat16, seed=seed)
+    g = torch.Generator().manual_seed(seed)
+    ids = torch.randint(0, config.vocab_size, (1, prefix), generator=g).to(device)
+    print(f"# decode: model built in {time.perf_counter() - t0:.1f}s", file=sys.stderr, flush=True)
+
+    def arm(name, packed):
+        t = time.perf_counter()
+        dynamic = decode_trace(model, ids, steps=steps)
+        session = StaticDecodeSession(model, ids, dynamic["fed_tokens"].to(device))
+        if packed:
+            with prepared_linears(model, torch.bfloat16):
+                traced = session.capture()
+                samples = [session.measure("sequence_graph")[0]["device_ms"] for _ in range(replays)]
+        else:
+            traced = session.capture()
+            samples = [session.measure("sequence_graph")[0]["device_ms"] for _ in range(replays)]
+        ms = statistics.median(samples)
+        result = {
+            "tokens_per_s": round(steps / (ms / 1e3), 2), "ms_per_token": round(ms / steps, 4),
+            "graph_ms": [round(v, 3) for v in samples],
+            "kernels_per_token": None if session.kernel_nodes is None else round(session.kernel_nodes / steps, 1),
+        }
+        if packed:
+            report = compare_trace(traced, dynamic, logprob_tolerance=0.1)
+            result["parity_vs_dynamic_trace"] = {
+                "passed": report["passed"], "greedy_tokens_equal": report["greedy_tokens_equal"],
+                "max_abs_logprob_error": round(report["max_abs_logprob_error"], 5),
+                "logits_normalized_rmse": report["logits"].get("normalized_rmse"),
+                "routes_ok": validate_routes(dynamic, expected_linears=7 * layers, steps=steps)}
+        session.graph = None
+        del session
+        torch.cuda.empty_cache()
+        print(f"# decode {name}: {result} ({time.perf_counter() - t:.1f}s)", file=sys.stderr, flush=True)
+        return result
+
+    with fused_qwen3_modules():
+        bf16 = arm("bf16", packed=False)
+        t = time.perf_counter()
+        w3_quantize_qwen3_model(model)
+        torch.cuda.empty_cache()
+        print(f"# decode: W3 quantization {time.perf_counter() - t:.1f}s", file=sys.stderr, flush=True)
+        w3 = arm("w3", packed=True)
+    return {"workload": f"config 3: Qwen3-8B arch random init, {layers} layers, prefill {prefix}, "
+                        f"{steps} greedy steps in one hipGraph, batch 1",
+            "w3": w3, "bf16": bf16, "w3_speedup_vs_bf16": round(w3["tokens_per_s"] / bf16["tokens_per_s"], 3)}
+
+
 def pmc_target():
     """Workload for ``rocprofv3 --pmc`` passes: the gate/up W3 GEMV (default plan)
     over 24 rotating payloads, twice; the LUT kernel (reference-style tables in
@@ -264,6 +330,9 @@ def main():
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--shapes", default="all", help="comma list of q/o,k/v,gate/up,down or all")
     parser.add_argument("--pmc-target", action="store_true", help="run the counter-collection workload")
+    parser.add_argument("--decode", action="store_true", help="run only the config-3 decode benchmark")
+    parser.add_argument("--decode-layers", type=int, default=36)
+    parser.add_argument("--no-decode", action="store_true", help="skip the config-3 decode benchmark")
     parser.add_argument("--summarize-pmc", nargs="+", metavar="CSV",
                         help="rocprofv3 counter CSVs -> profiles/w3_mfma_traffic.json")
     args = parser.parse_args()
@@ -272,6 +341,9 @@ def main():
         return
     if args.pmc_target:
         pmc_target()
+        return
+    if args.decode:
+        print(json.dumps(decode_bench(layers=args.decode_layers)), flush=True)
         return
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -354,6 +426,10 @@ def main():
                       f"(average launch over {dominant['copies']} rotating payloads)",
         },
     }
+    if not args.no_decode:
+        del graph, layers
+        torch.cuda.empty_cache()
+        result["config"]["decode"] = decode_bench(layers=args.decode_layers)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline()
     print(json.dumps(result), flush=True)

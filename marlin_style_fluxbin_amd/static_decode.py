@@ -19,6 +19,46 @@ import torch
 from .full_model_trial import packed_modules
 
 
+def _loaded_hip_runtime():
+    """The HIP runtime already mapped into this process (torch's), opened by its
+    exact path so no second runtime gets loaded; None if none is mapped."""
+    import ctypes
+
+    try:
+        with open("/proc/self/maps") as maps:
+            paths = {line.split()[-1] for line in maps if "libamdhip64" in line}
+    except OSError:
+        return None
+    paths = sorted(p for p in paths if p.startswith("/"))
+    return ctypes.CDLL(paths[0]) if paths else None
+
+
+def graph_kernel_count(graph) -> int | None:
+    """Kernel nodes of a captured ``torch.cuda.CUDAGraph(keep_graph=True)`` (a
+    hipGraph), from the HIP runtime; None if the runtime query is unavailable."""
+    import ctypes
+
+    try:
+        raw = graph.raw_cuda_graph()
+        hip = _loaded_hip_runtime()
+    except (AttributeError, OSError, RuntimeError):
+        return None
+    if hip is None:
+        return None
+    count = ctypes.c_size_t(0)
+    if hip.hipGraphGetNodes(ctypes.c_void_p(raw), None, ctypes.byref(count)) != 0:
+        return None
+    nodes = (ctypes.c_void_p * count.value)()
+    if hip.hipGraphGetNodes(ctypes.c_void_p(raw), nodes, ctypes.byref(count)) != 0:
+        return None
+    kind = ctypes.c_int(0)
+    kernels = 0
+    for node in nodes:
+        if hip.hipGraphNodeGetType(ctypes.c_void_p(node), ctypes.byref(kind)) == 0 and kind.value == 0:
+            kernels += 1  # hipGraphNodeTypeKernel
+    return kernels
+
+
 @contextmanager
 def prepared_linears(model, dtype):
     """Bind every packed Linear's allocation-free decode route for the duration."""
@@ -69,6 +109,7 @@ class StaticDecodeSession:
         self.graph = None
         self.graph_outputs = None
         self.capture_routes = None
+        self.kernel_nodes = None
 
     @torch.inference_mode()
     def reset(self):
@@ -135,13 +176,15 @@ class StaticDecodeSession:
         self.reset()
         torch.cuda.synchronize()
         self.set_audit(True)
-        graph = torch.cuda.CUDAGraph()
+        graph = torch.cuda.CUDAGraph(keep_graph=True)
         try:
             with torch.cuda.graph(graph, stream=stream):
                 outputs = self.run()
             self.capture_routes = self.routes()
         finally:
             self.set_audit(False)
+        self.kernel_nodes = graph_kernel_count(graph)
+        graph.instantiate()
         self.graph, self.graph_outputs = graph, outputs
         self.reset()
         graph.replay()
