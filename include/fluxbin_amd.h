@@ -146,6 +146,29 @@ int fx_head_norm_rope(int ntensors, const void *const *inputs, void *const *outp
                       const void *cos, const void *sin, const long long *cos_strides,
                       const int *position, float eps, int rope_mode, int dtype, void *stream);
 
+/*
+ * Decode attention of one token over a static KV cache: the attention the
+ * reference's decode runs inside stock HF Qwen3Attention (static_decode.py:73-81:
+ * StaticCache + boolean mask, SDPA).  q [n_q_heads, head_dim]; caches
+ * [n_kv_heads, max_len, head_dim]; query head h reads KV head h / (n_q_heads /
+ * n_kv_heads) at slots 0..position (later slots are never read); fp32 scores
+ * scaled by `scale`, fp32 softmax and accumulation, out [n_q_heads, head_dim]
+ * rounded to dtype.  Two launches (key-chunk split + combine) through
+ * `workspace` (fx_decode_attention_workspace_bytes, no initial contents).
+ * head_dim in {64, 128, 256}.
+ */
+size_t fx_decode_attention_workspace_bytes(int n_q_heads, int max_len, int head_dim);
+int fx_decode_attention(const void *q, const void *k_cache, const void *v_cache, void *workspace,
+                        size_t workspace_bytes, void *out, int n_q_heads, int n_kv_heads,
+                        int max_len, int head_dim, int position, float scale, int dtype,
+                        void *stream);
+
+/*
+ * Qwen3MLP activation (transformers modeling_qwen3.py, run by the reference's
+ * decode): out = round(round(silu(gate)) * up) elementwise over n values.
+ */
+int fx_silu_mul(const void *gate, const void *up, void *out, int n, int dtype, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

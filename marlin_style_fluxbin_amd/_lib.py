@@ -42,6 +42,9 @@ SIGNATURES: dict[str, tuple] = {
     "fx_w3_restore": (_i, [_p, _p, _i, _p, _p, _p, _i, _i, _i, _p]),
     "fx_rmsnorm": (_i, [_p, _p, _p, _p, _p, _i, _i, _f, _i, _p]),
     "fx_head_norm_rope": (_i, [_i, _p, _p, _p, _p, _p, _p, _i, _i, _i, _p, _p, _p, _p, _f, _i, _i, _p]),
+    "fx_decode_attention_workspace_bytes": (_sz, [_i, _i, _i]),
+    "fx_decode_attention": (_i, [_p, _p, _p, _p, _sz, _p, _i, _i, _i, _i, _i, _f, _i, _p]),
+    "fx_silu_mul": (_i, [_p, _p, _p, _i, _i, _p]),
 }
 
 _lock = threading.Lock()

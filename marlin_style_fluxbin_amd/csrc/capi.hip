@@ -12,6 +12,7 @@
 #include "w3_lut.hip"
 #include "w3_mfma_launch.h"
 #include "norms_launch.h"
+#include "decode_launch.h"
 
 using fx::LutArgs;
 using fx::MfmaArgs;
@@ -490,6 +491,55 @@ int fx_head_norm_rope(int ntensors, const void* const* inputs, void* const* outp
   }
   fx::launch_head_norm_rope(dtype, a, static_cast<hipStream_t>(stream));
   return check_launch("head_norm_rope_kernel");
+}
+
+size_t fx_decode_attention_workspace_bytes(int n_q_heads, int max_len, int head_dim) {
+  if (n_q_heads < 1 || max_len < 1 || head_dim < 1) return 0;
+  const size_t splits = (size_t(max_len) + 63) / 64;
+  return size_t(n_q_heads) * splits * (size_t(head_dim) + 2) * sizeof(float);
+}
+
+int fx_decode_attention(const void* q, const void* k_cache, const void* v_cache, void* workspace,
+                        size_t workspace_bytes, void* out, int n_q_heads, int n_kv_heads,
+                        int max_len, int head_dim, int position, float scale, int dtype,
+                        void* stream) {
+  if (!q || !k_cache || !v_cache || !out) return fail(FX_EINVAL, "q, caches and out must be non-null");
+  if (!is_half_dtype(dtype)) return fail(FX_EINVAL, "dtype must be fp16 or bf16");
+  if (head_dim != 64 && head_dim != 128 && head_dim != 256)
+    return fail(FX_EINVAL, "head_dim must be 64, 128 or 256, got %d", head_dim);
+  if (n_kv_heads < 1 || n_q_heads < n_kv_heads || n_q_heads % n_kv_heads)
+    return fail(FX_EINVAL, "query heads %d must be a positive multiple of KV heads %d", n_q_heads, n_kv_heads);
+  if (max_len < 1 || max_len > (1 << 22) || position < 0 || position >= max_len)
+    return fail(FX_EINVAL, "position %d outside the cache [0, %d)", position, max_len);
+  const void* vec[5] = {q, k_cache, v_cache, out, nullptr};
+  for (int i = 0; i < 3; ++i)
+    if (reinterpret_cast<uintptr_t>(vec[i]) % 16 != 0) return fail(FX_EINVAL, "q and caches must be 16-byte aligned");
+  const size_t need = fx_decode_attention_workspace_bytes(n_q_heads, max_len, head_dim);
+  if (!workspace || workspace_bytes < need)
+    return fail(FX_EINVAL, "attention workspace needs %zu bytes, got %zu", need, workspace_bytes);
+  fx::AttnArgs a;
+  a.q = static_cast<const uint16_t*>(q);
+  a.k = static_cast<const uint16_t*>(k_cache);
+  a.v = static_cast<const uint16_t*>(v_cache);
+  a.partial = static_cast<float*>(workspace);
+  a.out = static_cast<uint16_t*>(out);
+  a.Hq = n_q_heads;
+  a.Hk = n_kv_heads;
+  a.Lmax = max_len;
+  a.pos = position;
+  a.splits = (max_len + 63) / 64;
+  a.scale = scale;
+  fx::launch_decode_attention(dtype, head_dim, a, static_cast<hipStream_t>(stream));
+  return check_launch("attn_split_kernel");
+}
+
+int fx_silu_mul(const void* gate, const void* up, void* out, int n, int dtype, void* stream) {
+  if (!gate || !up || !out) return fail(FX_EINVAL, "gate, up and out must be non-null");
+  if (!is_half_dtype(dtype)) return fail(FX_EINVAL, "dtype must be fp16 or bf16");
+  if (n < 1) return fail(FX_EINVAL, "n must be positive");
+  fx::launch_silu_mul(dtype, static_cast<const uint16_t*>(gate), static_cast<const uint16_t*>(up),
+                      static_cast<uint16_t*>(out), n, static_cast<hipStream_t>(stream));
+  return check_launch("silu_mul_kernel");
 }
 
 }  // extern "C"

@@ -104,10 +104,17 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* __restrict
 template <int DT>
 __global__ __launch_bounds__(256) void head_norm_rope_kernel(HeadNormRopeArgs a) {
   const int lane = threadIdx.x & 63;
-  int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  // a row belongs to one wave: select its tensor with scalar (wave-uniform)
+  // values so the descriptors are read with scalar loads
+  int row = __builtin_amdgcn_readfirstlane(int(blockIdx.x) * 4 + int(threadIdx.x >> 6));
   int ti = 0;
-  while (ti < a.ntensors && row >= a.rows[ti]) row -= a.rows[ti++];
+  while (ti < a.ntensors && row >= a.rows[ti]) {
+    row -= a.rows[ti];
+    ++ti;
+  }
   if (ti >= a.ntensors) return;
+  ti = __builtin_amdgcn_readfirstlane(ti);
+  row = __builtin_amdgcn_readfirstlane(row);
   const HeadTensor& T = a.t[ti];
   const int S = a.seq, H = T.heads;
   const int b = row / (H * S), h = (row / S) % H, s = row % S;

@@ -168,17 +168,25 @@ def head_norm_rope(tensors, *, cos, sin, eps, seq=1, batch=1, position=None, rop
                    cos_strides=(0, 0)):
     """One launch over up to four head tensors (decode: q, k, v).
 
-    ``tensors``: list of dicts with ``x`` (input, head_dim contiguous), ``out``,
-    ``weight`` (per-head RMSNorm weight or None), ``heads``, ``rope`` (bool) and
-    element strides ``in_strides`` / ``out_strides`` as (batch, head, position).
-    ``position`` (device int32 scalar) offsets the cos/sin rows by
-    ``position * head_dim`` for graph-replayed decode.
+    ``tensors``: list of dicts with ``x`` (input) and ``out`` whose last
+    dimension is head_dim (contiguous), ``weight`` (per-head RMSNorm weight or
+    None), ``heads``, ``rope`` (bool) and element strides ``in_strides`` /
+    ``out_strides`` as (batch, head, position).  ``position`` (device int32
+    scalar) offsets the cos/sin rows by ``position * head_dim`` for
+    graph-replayed decode.
     """
-    call = _HeadCall()
+    head_dim = tensors[0]["x"].shape[-1]
     dtype = tensors[0]["x"].dtype
     for t in tensors:
+        for key in ("x", "out"):
+            if t[key].shape[-1] != head_dim or t[key].stride(-1) != 1 or t[key].dtype != dtype:
+                raise ValueError(f"head_norm_rope: every {key} must end in a contiguous head_dim={head_dim} axis")
+        if t.get("weight") is not None and t["weight"].shape != (head_dim,):
+            raise ValueError("head_norm_rope: norm weights must have shape [head_dim]")
+    call = _HeadCall()
+    for t in tensors:
         call.add(t["x"], t["out"], t.get("weight"), t["heads"], t["in_strides"], t["out_strides"], t["rope"])
-    call.run(batch=batch, seq=seq, head_dim=tensors[0]["x"].shape[-1], cos=cos, sin=sin,
+    call.run(batch=batch, seq=seq, head_dim=head_dim, cos=cos, sin=sin,
              cos_strides=cos_strides, position=position, eps=eps, rope_mode=rope_mode, dtype=dtype,
              device=tensors[0]["x"].device)
 

@@ -1,0 +1,251 @@
+"""Native batch-1 Qwen3 decode: every step is a short, fixed chain of HIP kernels.
+
+Same protocol and interface as :class:`static_decode.StaticDecodeSession`
+(reference ``static_decode.py:26-138``): prefill the real prefix (through the HF
+model and its dense fallback), keep the prefix KV, decode a fixed continuation,
+capture all steps in one hipGraph, time a replay.  What differs is the step:
+instead of the HF module tree (~27 kernels per layer) each decoder layer is
+
+    add+RMSNorm -> q, k, v GEMV -> q/k norm + RoPE + KV-cache write -> attention
+    (split + combine) -> o GEMV -> add+RMSNorm -> gate, up GEMV -> SwiGLU -> down GEMV
+
+(12 launches with W3 Linears), followed once per token by the final add+RMSNorm,
+the bf16 LM head (hipBLASLt) and argmax.  The arithmetic and rounding points are
+the stock HF Qwen3 modules' (RMSNorm, RoPE, SDPA with fp32 softmax, SwiGLU); W3
+Linears run the MFMA GEMV, dense Linears ``torch.matmul`` (the bf16 arm).
+"""
+from __future__ import annotations
+
+import math
+import time
+
+import torch
+
+from . import _lib
+from .fused_modules import add_rms_norm, head_norm_rope
+from .static_decode import graph_kernel_count
+from .w3_lut_deployment import PackedW3Linear, W3Gemv
+
+_ATTN = ("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj", "self_attn.o_proj")
+_MLP = ("mlp.gate_proj", "mlp.up_proj", "mlp.down_proj")
+
+
+class _Linear:
+    """One decode Linear: W3 MFMA GEMV or a dense bf16 matmul, writing ``out``."""
+
+    def __init__(self, module):
+        if isinstance(module, PackedW3Linear):
+            self.gemv = W3Gemv(module.layout(), arithmetic=module.arithmetic)
+            self.weight = None
+            self.packed = True
+        elif isinstance(module, torch.nn.Linear):
+            self.gemv = None
+            self.weight = module.weight
+            self.packed = False
+        else:
+            raise TypeError(f"unsupported Linear type {type(module).__name__}")
+        self.bias = module.bias
+
+    def __call__(self, x, out):
+        if self.packed:
+            self.gemv(x, out)
+        else:
+            torch.matmul(x, self.weight.t(), out=out)
+        if self.bias is not None:
+            out.add_(self.bias)
+
+
+class NativeDecodeSession:
+    def __init__(self, model, input_ids: torch.Tensor, forced_tokens: torch.Tensor):
+        from transformers import StaticCache
+
+        if input_ids.ndim != 2 or input_ids.shape[0] != 1 or input_ids.shape[1] < 2:
+            raise ValueError("batch1 nonempty real prefix required")
+        if forced_tokens.ndim != 2 or forced_tokens.shape[0] != 1 or forced_tokens.shape[1] < 1:
+            raise ValueError("batch1 continuation required")
+        if model.training:
+            raise ValueError("eval model required")
+        if not input_ids.is_cuda:
+            raise ValueError("native decode runs on a GPU")
+        cfg = model.config
+        if set(cfg.layer_types) != {"full_attention"}:
+            raise ValueError("this protocol supports full-attention Qwen3 only")
+        dtype = model.model.embed_tokens.weight.dtype
+        if dtype not in (torch.bfloat16, torch.float16):
+            raise ValueError("native decode needs a bf16 or fp16 model")
+        self.model, self.dtype, self.device = model, dtype, input_ids.device
+        self.ids = input_ids
+        self.tokens = forced_tokens.to(self.device).contiguous()
+        self.steps = self.tokens.shape[1]
+        self.prefix_length = input_ids.shape[1]
+        self.maximum_length = self.prefix_length + self.steps
+        self.hidden = cfg.hidden_size
+        self.heads, self.kv_heads, self.head_dim = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+        self.eps = cfg.rms_norm_eps
+        self.scale = 1.0 / math.sqrt(self.head_dim)
+        self.layers = model.model.layers
+        n = len(self.layers)
+
+        # prefill through the HF model (dense fallback for packed Linears)
+        cache = StaticCache(config=cfg, max_cache_len=self.maximum_length)
+        with torch.inference_mode():
+            out = model(input_ids=input_ids, past_key_values=cache, use_cache=True, logits_to_keep=1)
+            self.prefill_logits = out.logits[:, -1, :].detach().clone()
+            shape = (n, self.kv_heads, self.maximum_length, self.head_dim)
+            self.k_cache = torch.zeros(shape, dtype=dtype, device=self.device)
+            self.v_cache = torch.zeros(shape, dtype=dtype, device=self.device)
+            self.prefix_k = torch.stack([l.keys[0, :, :self.prefix_length] for l in cache.layers]).clone()
+            self.prefix_v = torch.stack([l.values[0, :, :self.prefix_length] for l in cache.layers]).clone()
+            # cos/sin rows for every position, built by the model's own rotary module
+            positions = torch.arange(self.maximum_length, device=self.device)[None]
+            cos, sin = model.model.rotary_emb(self.prefill_logits.to(dtype), positions)
+            self.cos = cos[0].contiguous()
+            self.sin = sin[0].contiguous()
+        del cache
+
+        # weights
+        self.embed = model.model.embed_tokens.weight
+        self.final_norm = model.model.norm.weight
+        self.lm_head = model.lm_head.weight
+        self.lin = [{name: _Linear(block.get_submodule(name)) for name in _ATTN + _MLP} for block in self.layers]
+        self.in_norm = [b.input_layernorm.weight for b in self.layers]
+        self.post_norm = [b.post_attention_layernorm.weight for b in self.layers]
+        self.q_norm = [b.self_attn.q_norm.weight for b in self.layers]
+        self.k_norm = [b.self_attn.k_norm.weight for b in self.layers]
+
+        # static activations (one token)
+        def buf(width):
+            return torch.empty((1, width), dtype=dtype, device=self.device)
+
+        qd, kd = self.heads * self.head_dim, self.kv_heads * self.head_dim
+        inter = cfg.intermediate_size
+        self.residual, self.normed = buf(self.hidden), buf(self.hidden)
+        self.q, self.k, self.v, self.q_rot, self.attn = buf(qd), buf(kd), buf(kd), buf(qd), buf(qd)
+        self.o, self.gate, self.up, self.act, self.down = buf(self.hidden), buf(inter), buf(inter), buf(inter), buf(self.hidden)
+        self.logits = torch.empty((self.steps, cfg.vocab_size), dtype=dtype, device=self.device)
+        self.predictions = torch.empty((self.steps, 1), dtype=torch.int64, device=self.device)
+        lib = _lib.library()
+        self.lib = lib
+        nbytes = lib.fx_decode_attention_workspace_bytes(self.heads, self.maximum_length, self.head_dim)
+        self.attn_ws = torch.empty(nbytes // 4 + 64, dtype=torch.float32, device=self.device)
+        self.graph = None
+        self.kernel_nodes = None
+        self.launches_per_step = None
+
+    # -- one token -------------------------------------------------------------------
+    def _attention(self, layer, pos):
+        lib = self.lib
+        _lib.check(lib.fx_decode_attention(
+            self.q_rot.data_ptr(), self.k_cache[layer].data_ptr(), self.v_cache[layer].data_ptr(),
+            self.attn_ws.data_ptr(), self.attn_ws.numel() * 4, self.attn.data_ptr(), self.heads, self.kv_heads,
+            self.maximum_length, self.head_dim, pos, self.scale, _lib.dtype_code(self.dtype),
+            _lib.stream_handle(self.device)), "fx_decode_attention")
+
+    def _silu_mul(self):
+        _lib.check(self.lib.fx_silu_mul(self.gate.data_ptr(), self.up.data_ptr(), self.act.data_ptr(),
+                                        self.act.shape[1], _lib.dtype_code(self.dtype),
+                                        _lib.stream_handle(self.device)), "fx_silu_mul")
+
+    def _step(self, i):
+        pos = self.prefix_length + i
+        d, lmax = self.head_dim, self.maximum_length
+        torch.index_select(self.embed, 0, self.tokens[0, i:i + 1], out=self.residual)
+        from .fused_modules import rms_norm
+
+        rms_norm(self.residual, self.in_norm[0], self.eps, out=self.normed)
+        for l, lin in enumerate(self.lin):
+            if l > 0:
+                add_rms_norm(self.down, self.residual, self.in_norm[l], self.eps, out=self.normed,
+                             residual_out=self.residual)
+            lin["self_attn.q_proj"](self.normed, self.q)
+            lin["self_attn.k_proj"](self.normed, self.k)
+            lin["self_attn.v_proj"](self.normed, self.v)
+            head_norm_rope([
+                dict(x=self.q.view(self.heads, d), out=self.q_rot.view(self.heads, d), weight=self.q_norm[l],
+                     heads=self.heads, rope=True, in_strides=(0, d, 0), out_strides=(0, d, 0)),
+                dict(x=self.k.view(self.kv_heads, d), out=self.k_cache[l, :, pos], weight=self.k_norm[l],
+                     heads=self.kv_heads, rope=True, in_strides=(0, d, 0), out_strides=(0, lmax * d, 0)),
+                dict(x=self.v.view(self.kv_heads, d), out=self.v_cache[l, :, pos], weight=None,
+                     heads=self.kv_heads, rope=False, in_strides=(0, d, 0), out_strides=(0, lmax * d, 0)),
+            ], cos=self.cos[pos], sin=self.sin[pos], eps=self.eps, rope_mode=_lib.ROPE_STOCK)
+            self._attention(l, pos)
+            lin["self_attn.o_proj"](self.attn, self.o)
+            add_rms_norm(self.o, self.residual, self.post_norm[l], self.eps, out=self.normed,
+                         residual_out=self.residual)
+            lin["mlp.gate_proj"](self.normed, self.gate)
+            lin["mlp.up_proj"](self.normed, self.up)
+            self._silu_mul()
+            lin["mlp.down_proj"](self.act, self.down)
+        add_rms_norm(self.down, self.residual, self.final_norm, self.eps, out=self.normed,
+                     residual_out=self.residual)
+        torch.matmul(self.normed, self.lm_head.t(), out=self.logits[i:i + 1])
+        torch.argmax(self.logits[i:i + 1], dim=-1, keepdim=True, out=self.predictions[i:i + 1])
+
+    # -- session protocol --------------------------------------------------------------
+    @torch.inference_mode()
+    def reset(self):
+        self.k_cache.zero_()
+        self.v_cache.zero_()
+        self.k_cache[:, :, :self.prefix_length].copy_(self.prefix_k)
+        self.v_cache[:, :, :self.prefix_length].copy_(self.prefix_v)
+
+    @torch.inference_mode()
+    def run(self):
+        for i in range(self.steps):
+            self._step(i)
+        return self.logits, self.predictions
+
+    def trace(self, outputs=None) -> dict:
+        logits = torch.cat([self.prefill_logits, self.logits], 0)[None].detach().cpu()
+        predictions = torch.cat([self.prefill_logits.argmax(-1, keepdim=True), self.predictions], 0).t().cpu()
+        if not bool(torch.isfinite(logits).all()):
+            raise RuntimeError("nonfinite native decode logits")
+        return {"logits": logits, "predictions": predictions, "fed_tokens": self.tokens.cpu(),
+                "cache_length": self.maximum_length, "routes": {}}
+
+    @torch.inference_mode()
+    def audit(self) -> dict:
+        self.reset()
+        return self.trace(self.run())
+
+    @torch.inference_mode()
+    def capture(self) -> dict:
+        stream = torch.cuda.Stream()
+        stream.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(stream):
+            for _ in range(2):
+                self.reset()
+                self.run()
+        torch.cuda.current_stream().wait_stream(stream)
+        self.reset()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph(keep_graph=True)
+        with torch.cuda.graph(graph, stream=stream):
+            self.run()
+        self.kernel_nodes = graph_kernel_count(graph)
+        graph.instantiate()
+        self.graph = graph
+        self.reset()
+        graph.replay()
+        torch.cuda.synchronize()
+        return self.trace()
+
+    @torch.inference_mode()
+    def measure(self, mode: str):
+        if mode not in ("prepared_eager", "sequence_graph"):
+            raise ValueError("unknown mode")
+        if mode == "sequence_graph" and self.graph is None:
+            raise ValueError("capture first")
+        self.reset()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        wall = time.perf_counter()
+        start.record()
+        if mode == "sequence_graph":
+            self.graph.replay()
+        else:
+            self.run()
+        end.record()
+        end.synchronize()
+        wall_ms = (time.perf_counter() - wall) * 1000
+        return {"wall_ms": wall_ms, "device_ms": start.elapsed_time(end)}, self.trace()

@@ -148,3 +148,68 @@ def test_patched_hf_decoder_matches_stock(gpu):
             fused = model(input_ids=ids).logits.float()
     rel = (fused - stock).abs().max() / stock.abs().max()
     assert rel < 2e-2, rel
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_head_norm_rope_rows_land_in_their_slots_across_many_launches(gpu, d):
+    """Many launches with different descriptors (outputs in NaN-padded buffers):
+    every row must land exactly in its own output slot.  Guards the per-wave
+    descriptor selection in the kernel (kernel arguments read as scalars)."""
+    hq, hk, cache_len = 4, 2, 28
+    pad = 4096
+    dt = torch.bfloat16
+    w = torch.ones(d, dtype=dt, device=gpu)
+    cos = torch.ones(d, dtype=dt, device=gpu)
+    sin = torch.zeros(d, dtype=dt, device=gpu)
+    q = torch.zeros(hq, d, dtype=dt, device=gpu)
+    k = torch.zeros(hk, d, dtype=dt, device=gpu)
+    v = torch.zeros(hk, d, dtype=dt, device=gpu)
+    for h in range(hq):
+        q[h] = 10 + h
+    for h in range(hk):
+        k[h] = 20 + h
+        v[h] = 30 + h
+    outs = []
+    for trial in range(40):
+        qo = torch.full((2 * pad + hq * d,), float("nan"), dtype=dt, device=gpu)
+        kc = torch.full((2 * pad + hk * cache_len * d,), float("nan"), dtype=dt, device=gpu)
+        vc = torch.full((2 * pad + hk * cache_len * d,), float("nan"), dtype=dt, device=gpu)
+        slot = trial % cache_len
+        kview = kc[pad:pad + hk * cache_len * d].view(hk, cache_len, d)
+        vview = vc[pad:pad + hk * cache_len * d].view(hk, cache_len, d)
+        head_norm_rope([
+            dict(x=q, out=qo[pad:pad + hq * d].view(hq, d), weight=None, heads=hq, rope=True,
+                 in_strides=(0, d, 0), out_strides=(0, d, 0)),
+            dict(x=k, out=kview[:, slot], weight=None, heads=hk, rope=True, in_strides=(0, d, 0),
+                 out_strides=(0, cache_len * d, 0)),
+            dict(x=v, out=vview[:, slot], weight=None, heads=hk, rope=False, in_strides=(0, d, 0),
+                 out_strides=(0, cache_len * d, 0)),
+        ], cos=cos, sin=sin, eps=1e-6, rope_mode=_lib.ROPE_STOCK)
+        # an unrelated launch in between, with another descriptor set
+        head_norm_rope([dict(x=q, out=torch.empty_like(q), weight=w, heads=hq, rope=False,
+                             in_strides=(0, d, 0), out_strides=(0, d, 0))], cos=None, sin=None, eps=1e-6,
+                       rope_mode=_lib.ROPE_NONE)
+        outs.append((qo, kc, vc, slot))
+    torch.cuda.synchronize()
+    for qo, kc, vc, slot in outs:
+        for big, base, heads, stride, value, row_slot in ((qo, pad, hq, d, 10, None), (kc, pad, hk, cache_len * d, 20, slot),
+                                                          (vc, pad, hk, cache_len * d, 30, slot)):
+            f = big.float().cpu()
+            expect = torch.full_like(f, float("nan"))
+            for h in range(heads):
+                start = base + h * stride + (0 if row_slot is None else row_slot * d)
+                expect[start:start + d] = value + h
+            assert torch.equal(torch.isnan(f), torch.isnan(expect))
+            assert torch.equal(f[~torch.isnan(f)], expect[~torch.isnan(expect)])
+
+
+def test_head_norm_rope_rejects_flat_head_buffers(gpu):
+    """Head tensors must end in the head_dim axis: a flat [1, heads*head_dim]
+    buffer next to a [heads, head_dim] one is rejected before any launch."""
+    q = torch.zeros(1, 4 * 64, dtype=torch.bfloat16, device=gpu)
+    k = torch.zeros(2, 64, dtype=torch.bfloat16, device=gpu)
+    with pytest.raises(ValueError):
+        head_norm_rope([dict(x=k, out=k.clone(), weight=None, heads=2, rope=False, in_strides=(0, 64, 0),
+                             out_strides=(0, 64, 0)),
+                        dict(x=q, out=q.clone(), weight=None, heads=4, rope=False, in_strides=(0, 64, 0),
+                             out_strides=(0, 64, 0))], cos=None, sin=None, eps=1e-6, rope_mode=_lib.ROPE_NONE)
