@@ -182,17 +182,23 @@ def cpu_baseline(seconds_budget=15.0):
 
 def decode_bench(layers=36, prefix=512, steps=32, replays=5, seed=0):
     """Config 3: random-init Qwen3-8B architecture, batch-1 greedy decode of
-    ``steps`` tokens after a ``prefix``-token prefill, every step in one hipGraph
-    (StaticDecodeSession).  bf16 arm first (HF Linears, hipBLASLt), then the same
-    model W3-quantized in place (RTN, fp16 scales, zeros).  Both arms use the
-    fused RMSNorm / RoPE modules.  The W3 arm's greedy trace is gated against its
-    own dynamic-KV trace (prefill via the dense fallback, packed M=1 steps)."""
+    ``steps`` tokens after a ``prefix``-token prefill, every step in one hipGraph.
+
+    Four arms on one model: the bf16 model first (HF Linears = hipBLASLt), then
+    the same model W3-quantized in place (RTN, fp16 scales, zeros).  For each,
+    ``hf``: the reference protocol (StaticDecodeSession over the HF module tree
+    with the fused RMSNorm / RoPE modules); ``native``: NativeDecodeSession (our
+    kernel chain).  The W3 HF arm is gated against its own dynamic-KV trace
+    (prefill via the dense fallback, packed M=1 steps), the W3 native arm against
+    the W3 HF arm (same tokens).  Headline: W3 native vs bf16 native tokens/s.
+    """
     import statistics
 
     import torch
 
     from marlin_style_fluxbin_amd.full_model_trial import compare_trace, decode_trace, validate_routes
     from marlin_style_fluxbin_amd.fused_modules import fused_qwen3_modules
+    from marlin_style_fluxbin_amd.native_decode import NativeDecodeSession
     from marlin_style_fluxbin_amd.qwen3 import qwen3_config, random_qwen3_model, w3_quantize_qwen3_model
     from marlin_style_fluxbin_amd.static_decode import StaticDecodeSession, prepared_linears
 
@@ -204,46 +210,63 @@ def decode_bench(layers=36, prefix=512, steps=32, replays=5, seed=0):
     ids = torch.randint(0, config.vocab_size, (1, prefix), generator=g).to(device)
     print(f"# decode: model built in {time.perf_counter() - t0:.1f}s", file=sys.stderr, flush=True)
 
-    def arm(name, packed):
+    def timed(session):
+        samples = [session.measure("sequence_graph")[0]["device_ms"] for _ in range(replays)]
+        ms = statistics.median(samples)
+        return {"tokens_per_s": round(steps / (ms / 1e3), 2), "ms_per_token": round(ms / steps, 4),
+                "graph_ms": [round(v, 3) for v in samples],
+                "kernels_per_token": None if session.kernel_nodes is None else round(session.kernel_nodes / steps, 1)}
+
+    def arms(name, packed):
         t = time.perf_counter()
         dynamic = decode_trace(model, ids, steps=steps)
-        session = StaticDecodeSession(model, ids, dynamic["fed_tokens"].to(device))
+        tokens = dynamic["fed_tokens"].to(device)
+        hf = StaticDecodeSession(model, ids, tokens)
         if packed:
             with prepared_linears(model, torch.bfloat16):
-                traced = session.capture()
-                samples = [session.measure("sequence_graph")[0]["device_ms"] for _ in range(replays)]
+                hf_trace = hf.capture()
+                hf_result = timed(hf)
         else:
-            traced = session.capture()
-            samples = [session.measure("sequence_graph")[0]["device_ms"] for _ in range(replays)]
-        ms = statistics.median(samples)
-        result = {
-            "tokens_per_s": round(steps / (ms / 1e3), 2), "ms_per_token": round(ms / steps, 4),
-            "graph_ms": [round(v, 3) for v in samples],
-            "kernels_per_token": None if session.kernel_nodes is None else round(session.kernel_nodes / steps, 1),
-        }
+            hf_trace = hf.capture()
+            hf_result = timed(hf)
+        hf.graph = None
+        del hf
+        torch.cuda.empty_cache()
+        native = NativeDecodeSession(model, ids, tokens)
+        native_trace = native.capture()
+        native_result = timed(native)
+        native.graph = None
+        del native
+        torch.cuda.empty_cache()
+        vs_hf = compare_trace(native_trace, hf_trace, logprob_tolerance=0.1)
+        native_result["parity_vs_hf_static"] = {
+            "passed": vs_hf["passed"], "greedy_tokens_equal": vs_hf["greedy_tokens_equal"],
+            "max_abs_logprob_error": round(vs_hf["max_abs_logprob_error"], 5),
+            "logits_normalized_rmse": vs_hf["logits"].get("normalized_rmse")}
         if packed:
-            report = compare_trace(traced, dynamic, logprob_tolerance=0.1)
-            result["parity_vs_dynamic_trace"] = {
+            report = compare_trace(hf_trace, dynamic, logprob_tolerance=0.1)
+            hf_result["parity_vs_dynamic_trace"] = {
                 "passed": report["passed"], "greedy_tokens_equal": report["greedy_tokens_equal"],
                 "max_abs_logprob_error": round(report["max_abs_logprob_error"], 5),
                 "logits_normalized_rmse": report["logits"].get("normalized_rmse"),
                 "routes_ok": validate_routes(dynamic, expected_linears=7 * layers, steps=steps)}
-        session.graph = None
-        del session
-        torch.cuda.empty_cache()
-        print(f"# decode {name}: {result} ({time.perf_counter() - t:.1f}s)", file=sys.stderr, flush=True)
-        return result
+        print(f"# decode {name}: hf {hf_result} native {native_result} ({time.perf_counter() - t:.1f}s)",
+              file=sys.stderr, flush=True)
+        return {"hf": hf_result, "native": native_result}
 
     with fused_qwen3_modules():
-        bf16 = arm("bf16", packed=False)
+        bf16 = arms("bf16", packed=False)
         t = time.perf_counter()
         w3_quantize_qwen3_model(model)
         torch.cuda.empty_cache()
         print(f"# decode: W3 quantization {time.perf_counter() - t:.1f}s", file=sys.stderr, flush=True)
-        w3 = arm("w3", packed=True)
+        w3 = arms("w3", packed=True)
     return {"workload": f"config 3: Qwen3-8B arch random init, {layers} layers, prefill {prefix}, "
                         f"{steps} greedy steps in one hipGraph, batch 1",
-            "w3": w3, "bf16": bf16, "w3_speedup_vs_bf16": round(w3["tokens_per_s"] / bf16["tokens_per_s"], 3)}
+            "w3": w3, "bf16": bf16,
+            "w3_native_tokens_per_s": w3["native"]["tokens_per_s"],
+            "w3_speedup_vs_bf16_native": round(w3["native"]["tokens_per_s"] / bf16["native"]["tokens_per_s"], 3),
+            "w3_speedup_vs_bf16_hf": round(w3["hf"]["tokens_per_s"] / bf16["hf"]["tokens_per_s"], 3)}
 
 
 def pmc_target():

@@ -4,11 +4,9 @@
 // Attention semantics (stock HF Qwen3 attention through SDPA with a boolean
 // mask): for query head h of KV head g = h / (Hq / Hk),
 //   s_j = (q_h . k_{g,j}) * scale            j = 0 .. pos (later slots masked)
-//   o_h = sum_j round(e^(s_j - m)) v_{g,j} / sum_j e^(s_j - m)
-// with fp32 scores, exponentials, sums and accumulation; the probabilities are
-// rounded to the activation dtype before the P.V product, as the fused SDPA
-// kernels do (per 64-key chunk maximum m).  Output rounded once.  KV cache
-// layout [Hk, Lmax, D].
+//   o_h = sum_j softmax(s)_j v_{g,j}
+// with fp32 scores, probabilities and accumulation (SDPA's math form), rounded
+// once to the activation dtype.  KV cache layout [Hk, Lmax, D].
 #include "common.h"
 #include "decode_launch.h"
 
@@ -67,9 +65,7 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const uint16_t* __restr
     const float m = wave_max(s);  // finite: key `first` <= pos is live
     const float p = live ? __expf(s - m) : 0.f;
     const float l = wave_sum(p);
-    // the probabilities enter the P.V product in the activation dtype (the
-    // rounding point of the fused SDPA kernels); their sum stays fp32
-    ps[wave][lane] = round_to<DT>(p);
+    ps[wave][lane] = p;
     __builtin_amdgcn_wave_barrier();
     const int keys = min(kAttnChunk, pos - first + 1);
     float o[D / 64];

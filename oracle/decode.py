@@ -16,15 +16,11 @@ import numpy as np
 from .bf16 import round_to
 
 
-def gqa_attention(q, k_cache, v_cache, position: int, scale: float, prob_dtype: str | None = None,
-                  chunk: int = 64) -> np.ndarray:
+def gqa_attention(q, k_cache, v_cache, position: int, scale: float) -> np.ndarray:
     """float64 attention of one token.
 
     ``q [Hq, D]``, caches ``[Hk, L, D]``; query head ``h`` uses KV head
     ``h // (Hq // Hk)`` and slots ``0..position``.  Returns ``[Hq, D]`` float64.
-    With ``prob_dtype``, the probabilities ``e^(s - m)`` (m = the maximum of each
-    ``chunk`` of keys) are rounded to that dtype before the P.V product while
-    their sum stays exact -- the fused SDPA kernels' rounding point.
     """
     q = np.asarray(q, np.float64)
     k = np.asarray(k_cache, np.float64)[:, :position + 1]
@@ -35,22 +31,8 @@ def gqa_attention(q, k_cache, v_cache, position: int, scale: float, prob_dtype: 
     for h in range(hq):
         g = h // group
         s = k[g] @ q[h] * scale
-        if prob_dtype is None:
-            p = np.exp(s - s.max())
-            out[h] = (p / p.sum()) @ v[g]
-            continue
-        m = s.max()
-        num = np.zeros(q.shape[1])
-        den = 0.0
-        for c in range(0, s.shape[0], chunk):
-            sc = s[c:c + chunk]
-            mc = sc.max()
-            pc = np.exp(sc - mc)
-            pr = round_to(pc.astype(np.float32), prob_dtype).astype(np.float64)
-            w = np.exp(mc - m)
-            num += w * (pr @ v[g][c:c + chunk])
-            den += w * pc.sum()
-        out[h] = num / den
+        p = np.exp(s - s.max())
+        out[h] = (p / p.sum()) @ v[g]
     return out
 
 
