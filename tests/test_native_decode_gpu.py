@@ -102,6 +102,7 @@ def test_native_session_matches_hf_static_session(gpu, quantize):
     from torch.nn.attention import SDPBackend, sdpa_kernel
 
     model, ids, forced = _setup(gpu, quantize)
+    # both prefills (the prefix KV) run the same attention backend
     with sdpa_kernel([SDPBackend.MATH]):
         hf = StaticDecodeSession(model, ids, forced)
         if quantize:
@@ -109,7 +110,7 @@ def test_native_session_matches_hf_static_session(gpu, quantize):
                 want = hf.audit()
         else:
             want = hf.audit()
-    native = NativeDecodeSession(model, ids, forced)
+        native = NativeDecodeSession(model, ids, forced)
     eager = native.audit()
     graph = native.capture()
     assert torch.equal(graph["logits"], eager["logits"])
@@ -122,6 +123,8 @@ def test_native_session_matches_hf_static_session(gpu, quantize):
     assert report["greedy_tokens_equal"] and report["fed_tokens_equal"], report
     assert report["max_abs_logprob_error"] <= 0.05, report
     assert report["logits"]["normalized_rmse"] <= 0.02, report
+    # the first decode step sees identical inputs and a single layer stack pass
+    assert report["stepwise_normalized_rmse"][1] <= 0.01, report
     # 12 launches per W3 layer (13 with dense Linears' matmuls) + embedding, first norm, final norm,
     # LM head, argmax per token
     per_step = native.kernel_nodes / STEPS
