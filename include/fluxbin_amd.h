@@ -169,6 +169,40 @@ int fx_decode_attention(const void *q, const void *k_cache, const void *v_cache,
  */
 int fx_silu_mul(const void *gate, const void *up, void *out, int n, int dtype, void *stream);
 
+/*
+ * Two-base binary-basis GEMV, rank-one format with salient columns, batch 1:
+ * the benchmark's config-4 form of the reference's two-base M=1 GEMV
+ * (deployment.py:168-179 m1_out -> csrc/m1_v5.cu:26-104 lut_m1; same
+ * contract: caller-owned output and workspace, current stream, no allocation,
+ * fp32 accumulation, x [1, K] contiguous):
+ *   y[o] = s_r[o] * (a1[o] * (B1[o,:] . u) + a2[o] * (B2[o,:] . u))
+ *          + sum_j salient[o, j] * x[salient_idx[j]],   u[k] = t_c[k] * x[k]
+ * planes uint8 [K/128, O, 2, 16] (16-byte aligned): sign bit (1 = +1) of column
+ * 128 g + k of base b, row o at bit k >> 4 of byte k & 15 of planes[g][o][b];
+ * coef fp16 [2, O] (a1, a2); srow fp16 [O]; tcol fp16 [K]; salient bf16
+ * [O, n_salient] and salient_idx int32 [n_salient], n_salient <= 32 (both may
+ * be null when n_salient == 0; indices outside [0, K) contribute nothing).  x / out fp16 or
+ * bf16 (x_dtype), x and tcol 16-byte aligned.  Workspace: fp32 partials when K
+ * is split over workgroups (fx_two_base_gemv_workspace_bytes, may be 0).
+ */
+size_t fx_two_base_gemv_workspace_bytes(int O, int K);
+int fx_two_base_gemv(const void *x, int x_dtype, const uint8_t *planes, const void *coef,
+                     const void *srow, const void *tcol, const void *salient,
+                     const int32_t *salient_idx, int n_salient, void *workspace,
+                     size_t workspace_bytes, void *out, int O, int K, void *stream);
+/* Same with an explicit tiling: `tiles` 16-row tiles per workgroup, waves =
+ * tiles * (waves per tile along K), prefetch = batches of sign loads in flight;
+ * (tiles, waves/tiles, prefetch) in (1,4,1|2) (1,8,1|2) (2,4,1|2) (3,4,1|2)
+ * (4,4,2) (2,8,2).  groups_per_split is rounded up to a multiple of 4 and capped
+ * at what one workgroup stages (96 groups, 16 per wave). */
+size_t fx_two_base_gemv_config_workspace_bytes(int O, int K, int waves, int prefetch,
+                                               int groups_per_split, int tiles);
+int fx_two_base_gemv_config(const void *x, int x_dtype, const uint8_t *planes, const void *coef,
+                            const void *srow, const void *tcol, const void *salient,
+                            const int32_t *salient_idx, int n_salient, void *workspace,
+                            size_t workspace_bytes, void *out, int O, int K, int waves,
+                            int prefetch, int groups_per_split, int tiles, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,6 +1,7 @@
 // extern "C" boundary of libfluxbin_amd.so (declarations: include/fluxbin_amd.h).
 // Validates arguments, picks kernel instantiations and tilings, launches on the
 // caller's stream.  Nothing here allocates or synchronises.
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -13,6 +14,7 @@
 #include "w3_mfma_launch.h"
 #include "norms_launch.h"
 #include "decode_launch.h"
+#include "two_base_launch.h"
 
 using fx::LutArgs;
 using fx::MfmaArgs;
@@ -282,11 +284,136 @@ int run_mfma(const void* x, int x_dtype, const uint8_t* planes, const void* scal
   return FX_OK;
 }
 
+// ------------------------------------------------------------------ two-base GEMV
+struct TwoBasePlan {
+  int nt, nk, pd;  // row tiles per workgroup, waves per tile along K, batches in flight
+  int gps, splits, row_blocks;
+};
+
+bool two_base_instantiated(int nt, int nk, int pd) {
+  switch (nt * 100 + nk * 10 + pd) {
+    case 141: case 142: case 181: case 182: case 183: case 242: case 282: case 341: case 342:
+    case 442:
+      return true;
+  }
+  return false;
+}
+
+// K split so that one workgroup stages at most kRankOneMaxBatches batches and
+// each thread at most kRankOneMaxUnits 8-column units.
+TwoBasePlan make_two_base_plan(int O, int G, int nt, int nk, int pd, int gps) {
+  TwoBasePlan p;
+  p.nt = nt;
+  p.nk = nk;
+  p.pd = pd;
+  const int gmax = (G + 3) / 4 * 4;
+  p.gps = gps < 4 ? 4 : (gps + 3) / 4 * 4;
+  if (p.gps > gmax) p.gps = gmax;
+  const int cap = 4 * std::min(fx::kRankOneMaxBatches, fx::kRankOneMaxUnits * nt * nk);
+  if (p.gps > cap) p.gps = cap;
+  p.splits = (G + p.gps - 1) / p.gps;
+  p.row_blocks = (O + 16 * nt - 1) / (16 * nt);
+  return p;
+}
+
+// Default (graph-timed on MI355X): enough row tiles per workgroup to land near
+// one workgroup per CU (the dispatcher starts ~one workgroup per 2.7 ns, and each
+// workgroup stages its K range once), waves along K so every wave owns one to
+// three batches, and a K split over workgroups only for narrow outputs or K
+// beyond one workgroup's staging capacity.
+TwoBasePlan default_two_base_plan(int O, int G) {
+  const int cus = device_cu_count();
+  const int tiles_total = (O + 15) / 16;
+  int nt = tiles_total / cus;
+  nt = nt < 1 ? 1 : (nt > 3 ? 3 : nt);
+  const int row_blocks = (tiles_total + nt - 1) / nt;
+  const int batches = (G + 3) / 4;
+  int splits = 1;
+  if (row_blocks < 32) splits = (64 + row_blocks - 1) / row_blocks;
+  if (splits > batches) splits = batches;
+  int per_split = (batches + splits - 1) / splits;
+  const int nk = (nt == 1 && per_split >= 8) ? 8 : 4;
+  const int cap = std::min(fx::kRankOneMaxBatches, fx::kRankOneMaxUnits * nt * nk);
+  if (per_split > cap) {
+    splits = (batches + cap - 1) / cap;
+    per_split = (batches + splits - 1) / splits;
+  }
+  // one batch of sign loads in flight per wave measured fastest at the gate
+  // shape (a second one issued up front queues behind the first in HBM)
+  return make_two_base_plan(O, G, nt, nk, 1, per_split * 4);
+}
+
+size_t two_base_workspace(int O, const TwoBasePlan& p) {
+  return p.splits > 1 ? size_t(p.splits) * O * sizeof(float) : 0;
+}
+
+int run_rank_one(const void* x, int x_dtype, const uint8_t* planes, const void* coef,
+                 const void* srow, const void* tcol, const void* salient,
+                 const int32_t* salient_idx, int n_salient, void* workspace,
+                 size_t workspace_bytes, void* out, int O, int K, const TwoBasePlan& p,
+                 hipStream_t s) {
+  if (!x || !planes || !coef || !srow || !tcol || !out)
+    return fail(FX_EINVAL, "x, planes, coef, srow, tcol and out must be non-null");
+  if (!is_half_dtype(x_dtype)) return fail(FX_EINVAL, "x dtype must be fp16 or bf16");
+  if (O < 1 || O > (1 << 20)) return fail(FX_EINVAL, "O out of range: %d", O);
+  if (K < 128 || K % 128 != 0 || K > 32768 * 4)
+    return fail(FX_EINVAL, "K must be a positive multiple of 128, got %d", K);
+  if (n_salient < 0 || n_salient > 32)
+    return fail(FX_EINVAL, "n_salient must be in [0, 32], got %d", n_salient);
+  if (n_salient > 0 && (!salient || !salient_idx))
+    return fail(FX_EINVAL, "salient values and indices must be non-null when n_salient > 0");
+  if (reinterpret_cast<uintptr_t>(planes) % 16 || reinterpret_cast<uintptr_t>(x) % 16 ||
+      reinterpret_cast<uintptr_t>(tcol) % 16)
+    return fail(FX_EINVAL, "planes, x and tcol must be 16-byte aligned");
+  if (size_t(K / 128) * size_t(O) * 32 > 0x7fffffffu)
+    return fail(FX_EINVAL, "payload of %d x %d exceeds 2 GiB", O, K);
+  if (!two_base_instantiated(p.nt, p.nk, p.pd))
+    return fail(FX_EINVAL, "no two-base kernel for tiles %d kparts %d prefetch %d", p.nt, p.nk, p.pd);
+  const size_t need = two_base_workspace(O, p);
+  if (need > 0) {
+    if (!workspace || workspace_bytes < need)
+      return fail(FX_EINVAL, "workspace needs %zu bytes, got %zu", need, workspace_bytes);
+    if (reinterpret_cast<uintptr_t>(workspace) % 256 != 0)
+      return fail(FX_EINVAL, "workspace must be 256-byte aligned");
+  }
+  fx::RankOneArgs a;
+  a.x = static_cast<const uint16_t*>(x);
+  a.planes = planes;
+  a.coef = static_cast<const uint16_t*>(coef);
+  a.srow = static_cast<const uint16_t*>(srow);
+  a.tcol = static_cast<const uint16_t*>(tcol);
+  a.sal = static_cast<const uint16_t*>(salient);
+  a.sal_idx = salient_idx;
+  a.partial = p.splits > 1 ? static_cast<float*>(workspace) : nullptr;
+  a.out = static_cast<uint16_t*>(out);
+  a.O = O;
+  a.G = K / 128;
+  a.S = n_salient;
+  a.gps = p.gps;
+  a.row_blocks = p.row_blocks;
+  a.xcds = kXcds;
+  if (!fx::dispatch_rank_one(x_dtype, p.nt, p.nk, p.pd, a, dim3(p.row_blocks * p.splits), s))
+    return fail(FX_EINVAL, "no two-base kernel for tiles %d kparts %d prefetch %d", p.nt, p.nk, p.pd);
+  int rc = check_launch("rank_one_kernel");
+  if (rc || p.splits == 1) return rc;
+  return launch_finish(a.partial, out, x_dtype, p.splits, O, s);
+}
+
+// Explicit tiling of the public config entry: waves = tiles * kparts.
+bool two_base_config(int O, int G, int waves, int prefetch, int groups_per_split, int tiles,
+                     TwoBasePlan* plan) {
+  if (tiles < 1 || waves < tiles || waves % tiles || groups_per_split < 1) return false;
+  const int nk = waves / tiles;
+  if (!two_base_instantiated(tiles, nk, prefetch)) return false;
+  *plan = make_two_base_plan(O, G, tiles, nk, prefetch, groups_per_split);
+  return true;
+}
+
 }  // namespace
 
 extern "C" {
 
-int fx_abi_version(void) { return 3; }
+int fx_abi_version(void) { return 4; }
 
 const char* fx_last_error(void) { return g_error; }
 
@@ -540,6 +667,44 @@ int fx_silu_mul(const void* gate, const void* up, void* out, int n, int dtype, v
   fx::launch_silu_mul(dtype, static_cast<const uint16_t*>(gate), static_cast<const uint16_t*>(up),
                       static_cast<uint16_t*>(out), n, static_cast<hipStream_t>(stream));
   return check_launch("silu_mul_kernel");
+}
+
+size_t fx_two_base_gemv_workspace_bytes(int O, int K) {
+  if (O < 1 || K < 128 || K % 128) return 0;
+  return two_base_workspace(O, default_two_base_plan(O, K / 128));
+}
+
+int fx_two_base_gemv(const void* x, int x_dtype, const uint8_t* planes, const void* coef,
+                     const void* srow, const void* tcol, const void* salient,
+                     const int32_t* salient_idx, int n_salient, void* workspace,
+                     size_t workspace_bytes, void* out, int O, int K, void* stream) {
+  if (O < 1 || K < 128 || K % 128)
+    return fail(FX_EINVAL, "O must be positive and K a positive multiple of 128, got %d/%d", O, K);
+  return run_rank_one(x, x_dtype, planes, coef, srow, tcol, salient, salient_idx, n_salient,
+                      workspace, workspace_bytes, out, O, K, default_two_base_plan(O, K / 128),
+                      static_cast<hipStream_t>(stream));
+}
+
+size_t fx_two_base_gemv_config_workspace_bytes(int O, int K, int waves, int prefetch,
+                                               int groups_per_split, int tiles) {
+  TwoBasePlan p;
+  if (O < 1 || K < 128 || K % 128 || !two_base_config(O, K / 128, waves, prefetch, groups_per_split, tiles, &p))
+    return 0;
+  return two_base_workspace(O, p);
+}
+
+int fx_two_base_gemv_config(const void* x, int x_dtype, const uint8_t* planes, const void* coef,
+                            const void* srow, const void* tcol, const void* salient,
+                            const int32_t* salient_idx, int n_salient, void* workspace,
+                            size_t workspace_bytes, void* out, int O, int K, int waves,
+                            int prefetch, int groups_per_split, int tiles, void* stream) {
+  if (O < 1 || K < 128 || K % 128)
+    return fail(FX_EINVAL, "O must be positive and K a positive multiple of 128, got %d/%d", O, K);
+  TwoBasePlan p;
+  if (!two_base_config(O, K / 128, waves, prefetch, groups_per_split, tiles, &p))
+    return fail(FX_EINVAL, "unsupported waves/prefetch/tiles %d/%d/%d", waves, prefetch, tiles);
+  return run_rank_one(x, x_dtype, planes, coef, srow, tcol, salient, salient_idx, n_salient,
+                      workspace, workspace_bytes, out, O, K, p, static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

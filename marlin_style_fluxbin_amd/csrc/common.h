@@ -90,4 +90,29 @@ __device__ __forceinline__ float row16_max(float v) {
   return v;
 }
 
+typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+
+// Buffer resource over [base, base + bytes): loads at offsets past the end
+// return zero instead of touching memory.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_resource(const void* base, size_t bytes) {
+  const int records = bytes > 0x7fffffffu ? 0x7fffffff : int(bytes);
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), short(0), records, 0x00020000);
+}
+
+__device__ __forceinline__ u32x4_t load_b128(__amdgpu_buffer_rsrc_t r, int offset, int soffset) {
+  return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, offset, soffset, 0));
+}
+
+constexpr int kOutOfRange = int(0x80000000u);  // > every record count: loads return 0
+
+// Workgroup index -> (row block, K split) so that the workgroups one XCD runs
+// (hardware dispatch deals consecutive workgroup ids round-robin over the XCDs)
+// take consecutive row blocks and share the per-row metadata cache lines in
+// that XCD's L2.  A bijection for any grid size.
+__device__ __forceinline__ int xcd_local_index(int linear, int total, int xcds) {
+  const int xcd = linear % xcds, local = linear / xcds;
+  const int q = total / xcds, rem = total % xcds;
+  return xcd < rem ? xcd * (q + 1) + local : rem * (q + 1) + (xcd - rem) * q + local;
+}
+
 }  // namespace fx

@@ -1,0 +1,38 @@
+// Launch plumbing for the two-base binary-basis GEMV (two_base.hip), shared with
+// the C ABI.
+#pragma once
+#include "common.h"
+
+namespace fx {
+
+// Rank-one two-base payload with salient columns, batch 1:
+//   y[o] = s_r[o] (a1[o] (B1[o,:] . u) + a2[o] (B2[o,:] . u)) + sum_j sal[o,j] x[idx[j]],
+//   u[k] = t_c[k] x[k],  B in {-1, +1} stored as bits (1 = +1).
+struct RankOneArgs {
+  const uint16_t* x;       // [K] activations (fp16 / bf16)
+  const uint8_t* planes;   // [G, O, 2, 16] sign bits, bit j of byte c = column 128 g + 8 c + j
+  const uint16_t* coef;    // fp16 [2, O]: a1, a2
+  const uint16_t* srow;    // fp16 [O]
+  const uint16_t* tcol;    // fp16 [K]
+  const uint16_t* sal;     // bf16 [O, S] (null when S == 0)
+  const int32_t* sal_idx;  // [S] column indices
+  float* partial;          // null: write out directly (single K split)
+  uint16_t* out;           // [O]
+  int O, G, S, gps;
+  int row_blocks;  // ceil(O / (16 * tiles))
+  int xcds;
+};
+
+constexpr int kRankOneMaxBatches = 24;  // four-group batches one workgroup stages (48 KB LDS)
+constexpr int kRankOneMaxUnits = 4;     // staging units (8 columns) per thread
+
+// Dynamic LDS of one workgroup: 2 KB per staged four-group batch.
+inline size_t rank_one_lds_bytes(int gps) { return size_t(gps / 4) * 2048; }
+
+// tiles 16-row tiles per workgroup, kparts waves per tile splitting the K range,
+// pd batches of sign loads in flight per wave; instantiated (tiles, kparts, pd):
+// (1,4,1..2) (1,8,1..3) (2,4,2) (2,8,2) (3,4,1..2) (4,4,2).  False otherwise.
+bool dispatch_rank_one(int xdt, int tiles, int kparts, int pd, const RankOneArgs& a, dim3 grid,
+                       hipStream_t s);
+
+}  // namespace fx

@@ -44,7 +44,6 @@ namespace fx {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
-typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kMfmaMaxRows = 4;  // activation rows per launch (columns b + 4m)
 
@@ -98,19 +97,6 @@ __device__ __forceinline__ void dequant_word(unsigned p0, unsigned p1, unsigned 
   }
 }
 
-// Buffer resource over [base, base + bytes): loads at offsets past the end
-// return zero instead of touching memory.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_resource(const void* base, size_t bytes) {
-  const int records = bytes > 0x7fffffffu ? 0x7fffffff : int(bytes);
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), short(0), records, 0x00020000);
-}
-
-__device__ __forceinline__ u32x4_t load_b128(__amdgpu_buffer_rsrc_t r, int offset, int soffset) {
-  return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, offset, soffset, 0));
-}
-
-constexpr int kOutOfRange = int(0x80000000u);  // > every record count: loads return 0
-
 // Everything one wave loads for one batch, kept as raw bits: this lane's plane
 // rows (one per row tile), its 8 activations per row (or, with a permutation,
 // its 8 column indices), and the epilogue's scales and zero-points.  Nothing
@@ -122,16 +108,6 @@ struct BatchLoads {
   unsigned s[RT][2]; // scales of rows erow..erow+3 of each tile, two per word
   unsigned z[RT];    // zero-points of rows erow..erow+3, one per byte
 };
-
-// Workgroup index -> (row block, K split) so that the workgroups one XCD runs
-// (hardware dispatch deals consecutive workgroup ids round-robin over the XCDs)
-// take consecutive row blocks and share the scale / zero-point cache lines in
-// that XCD's L2.  A bijection for any grid size.
-__device__ __forceinline__ int xcd_local_index(int linear, int total, int xcds) {
-  const int xcd = linear % xcds, local = linear / xcds;
-  const int q = total / xcds, rem = total % xcds;
-  return xcd < rem ? xcd * (q + 1) + local : rem * (q + 1) + (xcd - rem) * q + local;
-}
 
 // grid (ceil(O / (16 RT)) * splits) workgroups of NW*64 threads.  Workgroup:
 // rows [16 RT b, +16 RT), groups [gps*split, +gps) with gps a multiple of 4.
