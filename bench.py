@@ -144,6 +144,66 @@ def bench_shape(o, k, device, steps, warmup, stream, min_bytes=320e6, min_copies
     }
 
 
+def two_base_bench(device, steps, warmup, stream, o=12288, k=4096, salient=32, min_bytes=640e6):
+    """Config 4: rank-one two-base GEMV with 32 salient columns at the gate shape,
+    M=1, over rotating payload copies, beside the bf16 arm on the dense weight."""
+    import torch
+
+    from marlin_style_fluxbin_amd.two_base import TwoBaseGemv, pack_rank_one_planes, rank_one_reference_weight
+
+    gen = torch.Generator(device=device).manual_seed(4)
+    nbytes = (2 * o * k // 8 + 4 * o + 2 * o + 2 * k + 2 * salient * o + 4 * salient) + 2 * k + 2 * o
+    copies = max(50, int(min_bytes // nbytes) + 1)
+
+    def payload():
+        bases = torch.randint(0, 2, (2, o, k), device=device, generator=gen, dtype=torch.int8) * 2 - 1
+        return {
+            "planes": pack_rank_one_planes(bases),
+            "coef": (torch.rand(2, o, device=device, generator=gen) + 0.5).half(),
+            "srow": (torch.rand(o, device=device, generator=gen) * 0.015 + 0.005).half(),
+            "tcol": (torch.rand(k, device=device, generator=gen) * 0.4 + 0.8).half(),
+            "salient": (torch.randn(o, salient, device=device, generator=gen) * 0.05).bfloat16(),
+            "salient_idx": torch.randperm(k, device=device, generator=gen)[:salient].sort().values.int(),
+        }
+
+    layouts = [payload() for _ in range(copies)]
+    gemvs = [TwoBaseGemv(layout) for layout in layouts]
+    x = torch.randn(1, k, device=device, generator=gen).to(torch.bfloat16)
+    outs = [torch.empty(1, o, dtype=torch.bfloat16, device=device) for _ in range(copies)]
+    # parity spot check against the dequantize-then-matmul of the same payload (fp32)
+    gemvs[0](x, outs[0])
+    want = x.float() @ rank_one_reference_weight(layouts[0]).t()
+    max_rel = float((outs[0].float() - want).abs().max() / want.abs().max())
+
+    def run():
+        for gemv, out in zip(gemvs, outs):
+            gemv(x, out)
+
+    ms = time_graph(capture(run, stream), steps, warmup, stream) / copies
+    dense_copies = max(4, int(min_bytes // (2 * o * k)) + 1)
+    dense = [rank_one_reference_weight(layouts[i % copies], torch.bfloat16) for i in range(dense_copies)]
+
+    def bf16_arm():
+        for i, w in enumerate(dense):
+            torch.matmul(x, w.t(), out=outs[i % copies])
+
+    ms_bf16 = time_graph(capture(bf16_arm, stream), steps, warmup, stream) / dense_copies
+    gbps = nbytes / (ms / 1e3) / 1e9
+    return {
+        "workload": f"config 4: rank-one two-base GEMV {o}x{k}, M=1, {salient} salient bf16 columns",
+        "algorithmic_bytes": nbytes,
+        "us": round(ms * 1e3, 3),
+        "GBps": round(gbps, 1),
+        "frac_hbm": round(gbps / HBM_PEAK_GBPS, 4),
+        "bf16_arm_us": round(ms_bf16 * 1e3, 3),
+        "speedup_vs_bf16": round(ms_bf16 / ms, 3),
+        "copies": copies,
+        "parity_max_rel_vs_fp32_dequant_matmul": round(max_rel, 6),
+        "data": "synthetic: random +-1 bases, a1,a2 ~U[0.5,1.5], s_r ~U[0.005,0.02], t_c ~U[0.8,1.2] (fp16), "
+                "salient bf16 ~N(0,0.05), x bf16 ~N(0,1)",
+    }
+
+
 def cpu_baseline(seconds_budget=15.0):
     """Oracle restatement of the reference's dense CPU route (dequantize per call,
     then matmul) on config 0's q_proj shape; one thread."""
@@ -389,6 +449,7 @@ def main():
     parser.add_argument("--decode", action="store_true", help="run only the config-3 decode benchmark")
     parser.add_argument("--decode-layers", type=int, default=36)
     parser.add_argument("--no-decode", action="store_true", help="skip the config-3 decode benchmark")
+    parser.add_argument("--no-two-base", action="store_true", help="skip the config-4 two-base benchmark")
     parser.add_argument("--summarize-pmc", nargs="+", metavar="CSV",
                         help="rocprofv3 counter CSVs -> profiles/w3_mfma_traffic.json")
     args = parser.parse_args()
@@ -482,6 +543,10 @@ def main():
                       f"(average launch over {dominant['copies']} rotating payloads)",
         },
     }
+    if not args.no_two_base:
+        result["config"]["two_base"] = two_base_bench(device, max(args.steps, 10), args.warmup, stream)
+        print(f"# two-base: {result['config']['two_base']}", file=sys.stderr, flush=True)
+        torch.cuda.empty_cache()
     if not args.no_decode:
         del graph, layers
         torch.cuda.empty_cache()
