@@ -203,6 +203,26 @@ int fx_two_base_gemv_config(const void *x, int x_dtype, const uint8_t *planes, c
                             size_t workspace_bytes, void *out, int O, int K, int waves,
                             int prefetch, int groups_per_split, int tiles, void *stream);
 
+/*
+ * Two-base hybrid g128/s8 GEMV over the reference's planar deployment layout,
+ * batch 1: deployment.py:168-179 m1_out with a v5_p* kernel (csrc/m1_v5.cu:26-112,
+ * PLANAR_CODES) -- caller-owned output and workspace, current stream, no
+ * allocation, x [1, K] contiguous:
+ *   y[o] = sum_g sum_b rows[g,o,b] * (B_b[o,g,:] . (x_g * columns[g,:,b]))
+ *        + sum_g sum_b sparse_rows[g,o,b] * (R_b[o,g,:] . (x[128g + indices[g,:]] * sparse_columns[g,:,b]))
+ * codes uint8 [G, O, 2, 16] (bit j of byte c of base b = column 8c + j, 1 = +1),
+ * rows / sparse_rows fp32 [G, O, 2], columns fp32 [G, 128, 2], indices int16
+ * [G, 8] (0..127), sparse_codes uint8 [G, O, 2, 1], sparse_columns fp32 [G, 8, 2]
+ * (convert_artifact, deployment.py:84-103).  The workspace bounds the K split:
+ * the kernel uses at most workspace_bytes / (4 O) splits (the reference's fp32
+ * [splits, O] workspace fits), and none when the output is wide enough.
+ */
+size_t fx_hybrid_gemv_workspace_bytes(int O, int K);
+int fx_hybrid_gemv(const void *x, int x_dtype, const uint8_t *codes, const float *rows,
+                   const float *columns, const int16_t *indices, const uint8_t *sparse_codes,
+                   const float *sparse_rows, const float *sparse_columns, void *workspace,
+                   size_t workspace_bytes, void *out, int O, int K, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -3,7 +3,9 @@
 Drop-in for the deployment API of maxiu188-afk/Marlin_Style_Fluxbin's
 ``fluxbin_style`` package: the planar W3 payload (``gptq_deployment``), the W3
 LUT Linear (``w3_lut_deployment``), fused RMSNorm / RoPE (``fused_modules``) and
-the static-KV decode session (``static_decode``).  GPU work runs in hand-written
+the static-KV decode session (``static_decode``), and the two-base binary-basis
+formats (``packing``, ``evaluation``, ``deployment``, ``engine_interface``; the
+benchmark's rank-one variant in ``two_base``).  GPU work runs in hand-written
 HIP kernels behind the C ABI of ``libfluxbin_amd.so`` (``include/fluxbin_amd.h``).
 """
 from .gptq_deployment import (  # noqa: F401
@@ -47,5 +49,10 @@ from .fused_modules import (  # noqa: F401
     rms_norm,
     rms_norm_reference,
 )
+
+from .packing import pack_two_bases, unpack_two_bases  # noqa: F401
+from .evaluation import materialize_global_two_base_weight, materialize_hybrid_s8_weight  # noqa: F401
+from .deployment import PackedHybridLinear  # noqa: F401
+from .two_base import TwoBaseGemv, pack_rank_one_planes, two_base_gemv, unpack_rank_one_planes  # noqa: F401
 
 __version__ = "0.1.0"

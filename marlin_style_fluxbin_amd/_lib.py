@@ -50,6 +50,8 @@ SIGNATURES: dict[str, tuple] = {
     "fx_two_base_gemv_config_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _i]),
     "fx_two_base_gemv_config": (_i, [_p, _i, _p, _p, _p, _p, _p, _p, _i, _p, _sz, _p, _i, _i,
                                      _i, _i, _i, _i, _p]),
+    "fx_hybrid_gemv_workspace_bytes": (_sz, [_i, _i]),
+    "fx_hybrid_gemv": (_i, [_p, _i, _p, _p, _p, _p, _p, _p, _p, _p, _sz, _p, _i, _i, _p]),
 }
 
 _lock = threading.Lock()

@@ -399,6 +399,87 @@ int run_rank_one(const void* x, int x_dtype, const uint8_t* planes, const void* 
   return launch_finish(a.partial, out, x_dtype, p.splits, O, s);
 }
 
+// Hybrid layout: the rank-one tiling rules with a smaller staging cap (3.3 KB of
+// LDS per batch) and at most `max_splits` K splits (the caller's workspace).
+TwoBasePlan default_hybrid_plan(int O, int G, int max_splits) {
+  const int cus = device_cu_count();
+  const int tiles_total = (O + 15) / 16;
+  int nt = tiles_total / cus;
+  nt = nt < 1 ? 1 : (nt > 3 ? 3 : nt);
+  const int row_blocks = (tiles_total + nt - 1) / nt;
+  const int batches = (G + 3) / 4;
+  int splits = 1;
+  if (row_blocks < 32) splits = (64 + row_blocks - 1) / row_blocks;
+  if (splits > batches) splits = batches;
+  int per_split = (batches + splits - 1) / splits;
+  const int nk = (nt == 1 && per_split >= 8) ? 8 : 4;
+  const int cap = std::min(fx::kHybridMaxBatches, 4 * nt * nk);
+  if (per_split > cap) {
+    splits = (batches + cap - 1) / cap;
+    per_split = (batches + splits - 1) / splits;
+  }
+  if (splits > max_splits && max_splits >= 1) {  // fewer, longer splits (never beyond the cap)
+    const int fewer = std::max(max_splits, (batches + cap - 1) / cap);
+    splits = fewer;
+    per_split = (batches + splits - 1) / splits;
+  }
+  TwoBasePlan p;
+  p.nt = nt;
+  p.nk = nk;
+  p.pd = 1;
+  p.gps = per_split * 4;
+  p.splits = (G + p.gps - 1) / p.gps;
+  p.row_blocks = (O + 16 * nt - 1) / (16 * nt);
+  return p;
+}
+
+int run_hybrid(const void* x, int x_dtype, const uint8_t* codes, const float* rows, const float* cols,
+               const int16_t* idx, const uint8_t* scodes, const float* srows, const float* scols,
+               void* workspace, size_t workspace_bytes, void* out, int O, int K, hipStream_t s) {
+  if (!x || !codes || !rows || !cols || !idx || !scodes || !srows || !scols || !out)
+    return fail(FX_EINVAL, "x, every layout field and out must be non-null");
+  if (!is_half_dtype(x_dtype)) return fail(FX_EINVAL, "x dtype must be fp16 or bf16");
+  if (O < 1 || O > 65536) return fail(FX_EINVAL, "O must be in [1, 65536], got %d", O);
+  if (K < 128 || K % 128 != 0 || K > 131072)
+    return fail(FX_EINVAL, "K must be a multiple of 128 in [128, 131072], got %d", K);
+  if (reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(codes) % 16 ||
+      reinterpret_cast<uintptr_t>(cols) % 16 || reinterpret_cast<uintptr_t>(rows) % 16 ||
+      reinterpret_cast<uintptr_t>(srows) % 16)
+    return fail(FX_EINVAL, "x, codes, rows, columns and sparse rows must be 16-byte aligned");
+  const int G = K / 128;
+  if (size_t(G) * size_t(O) * 32 > 0x7fffffffu) return fail(FX_EINVAL, "payload exceeds 2 GiB");
+  const int max_splits = int(std::min<size_t>(workspace ? workspace_bytes / (size_t(O) * 4) : 0, 1 << 20));
+  const TwoBasePlan p = default_hybrid_plan(O, G, max_splits < 1 ? 1 : max_splits);
+  const size_t need = two_base_workspace(O, p);
+  if (need > 0) {
+    if (!workspace || workspace_bytes < need)
+      return fail(FX_EINVAL, "workspace needs %zu bytes, got %zu", need, workspace_bytes);
+    if (reinterpret_cast<uintptr_t>(workspace) % 16 != 0)
+      return fail(FX_EINVAL, "workspace must be 16-byte aligned");
+  }
+  fx::HybridArgs a;
+  a.x = static_cast<const uint16_t*>(x);
+  a.codes = codes;
+  a.rows = rows;
+  a.cols = cols;
+  a.idx = idx;
+  a.scodes = scodes;
+  a.srows = srows;
+  a.scols = scols;
+  a.partial = p.splits > 1 ? static_cast<float*>(workspace) : nullptr;
+  a.out = static_cast<uint16_t*>(out);
+  a.O = O;
+  a.G = G;
+  a.gps = p.gps;
+  a.row_blocks = p.row_blocks;
+  a.xcds = kXcds;
+  if (!fx::dispatch_hybrid(x_dtype, p.nt, p.nk, a, dim3(p.row_blocks * p.splits), s))
+    return fail(FX_EINVAL, "no hybrid kernel for tiles %d kparts %d", p.nt, p.nk);
+  int rc = check_launch("hybrid_kernel");
+  if (rc || p.splits == 1) return rc;
+  return launch_finish(a.partial, out, x_dtype, p.splits, O, s);
+}
+
 // Explicit tiling of the public config entry: waves = tiles * kparts.
 bool two_base_config(int O, int G, int waves, int prefetch, int groups_per_split, int tiles,
                      TwoBasePlan* plan) {
@@ -705,6 +786,19 @@ int fx_two_base_gemv_config(const void* x, int x_dtype, const uint8_t* planes, c
     return fail(FX_EINVAL, "unsupported waves/prefetch/tiles %d/%d/%d", waves, prefetch, tiles);
   return run_rank_one(x, x_dtype, planes, coef, srow, tcol, salient, salient_idx, n_salient,
                       workspace, workspace_bytes, out, O, K, p, static_cast<hipStream_t>(stream));
+}
+
+size_t fx_hybrid_gemv_workspace_bytes(int O, int K) {
+  if (O < 1 || K < 128 || K % 128) return 0;
+  return two_base_workspace(O, default_hybrid_plan(O, K / 128, 1 << 20));
+}
+
+int fx_hybrid_gemv(const void* x, int x_dtype, const uint8_t* codes, const float* rows,
+                   const float* columns, const int16_t* indices, const uint8_t* sparse_codes,
+                   const float* sparse_rows, const float* sparse_columns, void* workspace,
+                   size_t workspace_bytes, void* out, int O, int K, void* stream) {
+  return run_hybrid(x, x_dtype, codes, rows, columns, indices, sparse_codes, sparse_rows, sparse_columns,
+                    workspace, workspace_bytes, out, O, K, static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

@@ -1,0 +1,280 @@
+// Hybrid g128/s8 two-base GEMV for gfx950 on the integer matrix cores (batch 1),
+// over the reference's planar deployment layout (deployment.py:59-103).
+//
+// Per 128-column group g and base b the weight is sign * rows[g,o,b] * cols[g,k,b],
+// plus an 8-column two-base refinement with its own row and column scales.  As
+// in the rank-one kernel (two_base.hip), sign bits become int8 MFMA operands and
+// activations become 16-bit fixed-point integers split into two int8 digits, but
+// every group keeps its own accumulator column because its row scale differs:
+//
+// * A (main): word_v >> i & 0x01010101 holds, as int8 0/1, the bits of columns
+//   8 (4v + q) + i for bytes q = 0..3 of word v (the layout's bit j of byte c is
+//   column 8c + j), so bit position i of a 16-byte plane row is one operand with
+//   element e covering column 8e + i.  A (refinement): the 8 bits of the
+//   refinement byte spread to bytes by a multiply ((n * 0x204081) & 0x01010101).
+// * B: D column c < 8 is (group slot c >> 1, digit c & 1) of the main product,
+//   c >= 8 the same for the refinement; an operand is non-zero only in the lanes
+//   of its own column and k-block (the others read a shared zero block).
+// * Activations u_b = x * cols[.., b] are rounded to v = rint(u_b 2^F) with F per
+//   (batch, base), |v| <= 2^14, and split into digits 256 hi + lo.  Per batch the
+//   int32 products are folded: acc += rows[g,o,b] (2 S - U_g,b) with S the
+//   weighted digit sum and U the exact sum of the same v (per group and base);
+//   the refinement the same with its own scales.
+//
+// Work split as in the rank-one kernel: a workgroup owns NT 16-row tiles and a K
+// range; wave w stages batches w, w + NW, ... (one 8-column unit per lane and
+// base, the refinement columns one per lane); after one barrier wave (tile,
+// kpart) multiplies its batches; the K parts meet in LDS.
+#include "common.h"
+#include "two_base_launch.h"
+
+namespace fx {
+
+typedef int hy_i32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr float kHyMagic = 12583040.0f;  // 1.5 * 2^23 + 128: low 16 bits of the sum are v + 128
+constexpr int kHyMaxUnits = 4;           // staged batches per wave
+
+__device__ __forceinline__ float hy_wave_max(float v) {
+  v = row16_max(v);
+  v = fmaxf(v, __shfl_xor(v, 16, 64));
+  v = fmaxf(v, __shfl_xor(v, 32, 64));
+  return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v)));
+}
+
+__device__ __forceinline__ int hy_exponent(float max_abs) {
+  if (!(max_abs > 0.f)) return 0;
+  int e;
+  frexpf(max_abs, &e);
+  return min(14 - e, 126);  // max_abs * 2^F in [2^13, 2^14) unless max_abs < 2^-112
+}
+
+// Refinement byte -> int8 0/1 elements 0..7 (four per word).
+__device__ __forceinline__ u32x4_t refine_operand(unsigned byte) {
+  return u32x4_t{((byte & 15u) * 0x204081u) & 0x01010101u, (((byte >> 4) & 15u) * 0x204081u) & 0x01010101u,
+                 0u, 0u};
+}
+
+template <int NT, int NK, int XDT>
+__global__ __launch_bounds__(NT * NK * 64) void hybrid_kernel(HybridArgs a) {
+  constexpr int NW = NT * NK;
+  extern __shared__ u32x4_t hy_dyn[];
+  __shared__ u32x4_t zero16;
+  __shared__ float fsc[kHybridMaxBatches][2];      // 2^-F per (batch, base)
+  __shared__ float fref[kHybridMaxBatches];        // 2^-F of the refinement operands
+  __shared__ float ug[kHybridMaxBatches][4][2];    // U per (batch, group slot, base)
+  __shared__ float vg[kHybridMaxBatches][4][2];    // refinement U per (batch, slot, base)
+  __shared__ float red[NK][16 * NT];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int O = a.O, G = a.G, K = G * 128;
+  const int block = xcd_local_index(blockIdx.x, gridDim.x, a.xcds);
+  const int split = block / a.row_blocks;
+  const int row0 = (block - split * a.row_blocks) * (16 * NT);
+  const int g0 = split * a.gps;
+  const int g1 = min(G, g0 + a.gps);
+  const int nbatch = (g1 - g0 + 3) >> 2;
+  const int maxb = a.gps / 4;
+  uint8_t* mslot = reinterpret_cast<uint8_t*>(hy_dyn);          // [batch][base][pos][slot][digit][16]
+  uint8_t* rslot = mslot + size_t(maxb) * 2048;                 // [batch][base][slot][digit][16]
+  u32x4_t* xs = reinterpret_cast<u32x4_t*>(rslot + size_t(maxb) * 256);  // [batch][64 units]
+
+  const auto rx = buffer_resource(a.x, size_t(K) * 2);
+  const auto rcol = buffer_resource(a.cols, size_t(G) * 128 * 2 * 4);
+  const auto ridx = buffer_resource(a.idx, size_t(G) * 8 * 2);
+  const auto rscol = buffer_resource(a.scols, size_t(G) * 8 * 2 * 4);
+  const auto rp = buffer_resource(a.codes, size_t(G) * O * 32);
+  const auto rsp = buffer_resource(a.scodes, size_t(G) * O * 2);
+  const auto rrow = buffer_resource(a.rows, size_t(G) * O * 2 * 4);
+  const auto rsrow = buffer_resource(a.srows, size_t(G) * O * 2 * 4);
+  const int r = lane & 15, kb = lane >> 4, c = lane & 15;
+
+  // ---- loads in consumption order (raw bits; nothing waits until all are issued)
+  const int staged = wave < nbatch ? (nbatch - wave + NW - 1) / NW : 0;
+  u32x4_t sx[kHyMaxUnits], sc[kHyMaxUnits][4];
+  unsigned sidx[kHyMaxUnits], sscol[kHyMaxUnits];
+#pragma unroll
+  for (int q = 0; q < kHyMaxUnits; ++q) {
+    const int g = g0 + 4 * (wave + q * NW) + kb;
+    const bool real = q < staged && g < g1;
+    const int col = g * 128 + 8 * r;
+    sx[q] = load_b128(rx, real ? col * 2 : kOutOfRange, 0);
+#pragma unroll
+    for (int h = 0; h < 4; ++h) sc[q][h] = load_b128(rcol, real ? (col * 2 + 4 * h) * 4 : kOutOfRange, 0);
+    sidx[q] = __builtin_amdgcn_raw_buffer_load_b16(ridx, real ? (g * 8 + (r & 7)) * 2 : kOutOfRange, 0, 0);
+    sscol[q] = __builtin_amdgcn_raw_buffer_load_b32(rscol, real ? ((g * 8 + (r & 7)) * 2 + (r >> 3)) * 4 : kOutOfRange, 0, 0);
+  }
+  const int tile = wave % NT, kpart = wave / NT;
+  const int prow = row0 + 16 * tile + r;          // A role row
+  const int drow = row0 + 16 * tile + 4 * kb;     // D role: rows drow .. drow + 3
+  const bool is_ref = c >= 8;
+  const int dslot = (c & 7) >> 1, digit = c & 1;
+  const int mine = kpart < nbatch ? (nbatch - kpart + NK - 1) / NK : 0;
+  u32x4_t w0, w1, rv0, rv1;
+  unsigned sb;
+  auto issue = [&](int i) __attribute__((always_inline)) {
+    const int bt = kpart + i * NK;
+    const int g = g0 + 4 * bt + kb;
+    const int poff = (g * O + prow) * 32;  // past the end -> zeros
+    w0 = load_b128(rp, poff, 0);
+    w1 = load_b128(rp, poff + 16, 0);
+    sb = __builtin_amdgcn_raw_buffer_load_b16(rsp, (g * O + prow) * 2, 0, 0);
+    // row scales of D rows drow .. +3 for this lane's group slot, both bases
+    const int gd = g0 + 4 * bt + dslot;
+    const auto& rr = is_ref ? rsrow : rrow;
+    const int roff = (gd * O + drow) * 8;
+    rv0 = load_b128(rr, roff, 0);
+    rv1 = load_b128(rr, roff + 16, 0);
+  };
+  if (mine > 0) issue(0);
+
+  // ---- staging: wave w stages batches w, w + NW, ...
+  if (t == 0) zero16 = u32x4_t{0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int q = 0; q < kHyMaxUnits; ++q) {
+    if (q < staged) {
+      const int bt = wave + q * NW;
+      xs[bt * 64 + lane] = sx[q];
+      float xv[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) xv[j] = to_f32<XDT>(uint16_t(sx[q][j >> 1] >> (16 * (j & 1))));
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        float u[8], mx = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          // cols[g][8r + j][b]: float 2 j + b of the lane's 16
+          u[j] = xv[j] * __uint_as_float(sc[q][(2 * j + b) >> 2][(2 * j + b) & 3]);
+          mx = fmaxf(mx, fabsf(u[j]));
+        }
+        const int F = hy_exponent(hy_wave_max(mx));
+        const float scale = ldexpf(1.f, F);
+        int vsum = 0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const unsigned wv = __float_as_uint(fmaf(u[j], scale, kHyMagic));  // low 16 bits: v + 128
+          vsum += int(int16_t(uint16_t(wv))) - 128;
+          // column 8r + j: position j, element r
+          uint8_t* dst = mslot + ((((bt * 2 + b) * 8 + j) * 4 + kb) * 2) * 16 + r;
+          dst[0] = uint8_t(wv >> 8);          // hi digit
+          dst[16] = uint8_t(wv ^ 0x80u);      // lo digit
+        }
+        const float us = row16_sum(float(vsum));  // group slot kb; |sum| < 2^22: exact
+        if (r == 0) ug[bt][kb][b] = ldexpf(us, -F);
+        if (lane == 0) fsc[bt][b] = ldexpf(1.f, -F);
+      }
+      __builtin_amdgcn_wave_barrier();  // xs of this batch written by this wave
+      // refinement: lane (kb, r) takes column idx[g][r & 7] of base r >> 3
+      const int j = r & 7, b = r >> 3;
+      const int cc = int(int16_t(uint16_t(sidx[q]))) & 127;
+      const uint16_t* xs16 = reinterpret_cast<const uint16_t*>(xs + bt * 64 + kb * 16);
+      const float v = to_f32<XDT>(xs16[cc]) * __uint_as_float(sscol[q]);
+      const int F = hy_exponent(hy_wave_max(fabsf(v)));
+      const unsigned wv = __float_as_uint(fmaf(v, ldexpf(1.f, F), kHyMagic));
+      uint8_t* dst = rslot + (((bt * 2 + b) * 4 + kb) * 2) * 16 + j;
+      dst[0] = uint8_t(wv >> 8);
+      dst[16] = uint8_t(wv ^ 0x80u);
+      float vs = float(int(int16_t(uint16_t(wv))) - 128);
+      vs += dpp_move<kDppXor1>(vs);
+      vs += dpp_move<kDppXor2>(vs);
+      vs += dpp_move<kDppHalfMirror>(vs);  // lanes j and 7 - j: completes the 8-lane sum
+      if (j == 0) vg[bt][kb][b] = ldexpf(vs, -F);
+      if (lane == 0) fref[bt] = ldexpf(1.f, -F);
+    }
+  }
+  __syncthreads();
+
+  // ---- main loop: eight bit positions + the refinement per batch and base
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  const u32x4_t* zp = &zero16;
+  const bool main_lane = !is_ref && dslot == kb;
+  const bool ref_lane = is_ref && dslot == kb;
+  const float dw = digit ? 1.f : 256.f;
+  for (int i = 0; i < mine; ++i) {
+    const int bt = kpart + i * NK;
+    const u32x4_t p0 = w0, p1 = w1, r0 = rv0, r1 = rv1;
+    const unsigned sbv = sb;
+    if (i + 1 < mine) issue(i + 1);
+    hy_i32x4_t d0 = {0, 0, 0, 0}, d1 = {0, 0, 0, 0};
+#pragma unroll
+    for (int pos = 0; pos < 8; ++pos) {
+      const u32x4_t* b0p = main_lane ? reinterpret_cast<const u32x4_t*>(mslot + ((((bt * 2 + 0) * 8 + pos) * 4 + kb) * 2 + digit) * 16) : zp;
+      const u32x4_t* b1p = main_lane ? reinterpret_cast<const u32x4_t*>(mslot + ((((bt * 2 + 1) * 8 + pos) * 4 + kb) * 2 + digit) * 16) : zp;
+      const u32x4_t bop0 = *b0p, bop1 = *b1p;
+      const u32x4_t a0{(p0.x >> pos) & 0x01010101u, (p0.y >> pos) & 0x01010101u, (p0.z >> pos) & 0x01010101u,
+                       (p0.w >> pos) & 0x01010101u};
+      const u32x4_t a1{(p1.x >> pos) & 0x01010101u, (p1.y >> pos) & 0x01010101u, (p1.z >> pos) & 0x01010101u,
+                       (p1.w >> pos) & 0x01010101u};
+      d0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(hy_i32x4_t, a0), __builtin_bit_cast(hy_i32x4_t, bop0), d0, 0, 0, 0);
+      d1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(hy_i32x4_t, a1), __builtin_bit_cast(hy_i32x4_t, bop1), d1, 0, 0, 0);
+    }
+    {
+      const u32x4_t* b0p = ref_lane ? reinterpret_cast<const u32x4_t*>(rslot + (((bt * 2 + 0) * 4 + kb) * 2 + digit) * 16) : zp;
+      const u32x4_t* b1p = ref_lane ? reinterpret_cast<const u32x4_t*>(rslot + (((bt * 2 + 1) * 4 + kb) * 2 + digit) * 16) : zp;
+      const u32x4_t bop0 = *b0p, bop1 = *b1p;
+      d0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(hy_i32x4_t, refine_operand(sbv & 0xffu)),
+                                                __builtin_bit_cast(hy_i32x4_t, bop0), d0, 0, 0, 0);
+      d1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(hy_i32x4_t, refine_operand((sbv >> 8) & 0xffu)),
+                                                __builtin_bit_cast(hy_i32x4_t, bop1), d1, 0, 0, 0);
+    }
+    // fold: this lane's column is (group slot, digit) of the main or the refinement product
+    const float s0 = dw * (is_ref ? fref[bt] : fsc[bt][0]);
+    const float s1 = dw * (is_ref ? fref[bt] : fsc[bt][1]);
+    const float u0 = digit ? 0.f : (is_ref ? vg[bt][dslot][0] : ug[bt][dslot][0]);
+    const float u1 = digit ? 0.f : (is_ref ? vg[bt][dslot][1] : ug[bt][dslot][1]);
+    // rv: rows drow + j, base b at float 2 j + b
+    const float rs[8] = {__uint_as_float(r0.x), __uint_as_float(r0.y), __uint_as_float(r0.z), __uint_as_float(r0.w),
+                         __uint_as_float(r1.x), __uint_as_float(r1.y), __uint_as_float(r1.z), __uint_as_float(r1.w)};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      acc[j] = fmaf(rs[2 * j], fmaf(2.f * float(d0[j]), s0, -u0), acc[j]);
+      acc[j] = fmaf(rs[2 * j + 1], fmaf(2.f * float(d1[j]), s1, -u1), acc[j]);
+    }
+  }
+
+  // ---- rows 4 kb + j: sum over the 16 columns of the quad, then over the K parts
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float s = row16_sum(acc[j]);
+    if (c == 0) red[kpart][16 * tile + 4 * kb + j] = s;
+  }
+  __syncthreads();
+  const int orow = row0 + t;
+  if (t < 16 * NT && orow < O) {
+    float y = 0.f;
+#pragma unroll
+    for (int q = 0; q < NK; ++q) y += red[q][t];
+    if (a.partial)
+      a.partial[size_t(split) * O + orow] = y;
+    else
+      a.out[orow] = from_f32<XDT>(y);
+  }
+}
+
+// Dynamic LDS beyond the default 64 KB must be allowed per kernel, once.
+template <int NT, int NK, int XDT>
+bool hybrid_launch(const HybridArgs& a, dim3 grid, hipStream_t s) {
+  static const bool allowed =
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&hybrid_kernel<NT, NK, XDT>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize,
+                          int(hybrid_lds_bytes(4 * kHybridMaxBatches))) == hipSuccess;
+  if (!allowed) return false;
+  hipLaunchKernelGGL((hybrid_kernel<NT, NK, XDT>), grid, dim3(NT * NK * 64), hybrid_lds_bytes(a.gps), s, a);
+  return true;
+}
+
+template <int NT, int NK>
+bool hybrid_for_dtype(int xdt, const HybridArgs& a, dim3 grid, hipStream_t s) {
+  if (xdt == kBF16) return hybrid_launch<NT, NK, kBF16>(a, grid, s);
+  if (xdt == kF16) return hybrid_launch<NT, NK, kF16>(a, grid, s);
+  return false;
+}
+
+bool dispatch_hybrid(int xdt, int tiles, int kparts, const HybridArgs& a, dim3 grid, hipStream_t s) {
+  if (tiles == 1 && kparts == 4) return hybrid_for_dtype<1, 4>(xdt, a, grid, s);
+  if (tiles == 1 && kparts == 8) return hybrid_for_dtype<1, 8>(xdt, a, grid, s);
+  if (tiles == 2 && kparts == 4) return hybrid_for_dtype<2, 4>(xdt, a, grid, s);
+  if (tiles == 3 && kparts == 4) return hybrid_for_dtype<3, 4>(xdt, a, grid, s);
+  return false;
+}
+
+}  // namespace fx

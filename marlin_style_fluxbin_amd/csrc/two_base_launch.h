@@ -36,3 +36,36 @@ bool dispatch_rank_one(int xdt, int tiles, int kparts, int pd, const RankOneArgs
                        hipStream_t s);
 
 }  // namespace fx
+
+namespace fx {
+
+// Hybrid g128/s8 payload in the reference's planar deployment layout, batch 1:
+//   y[o] = sum_g sum_b rows[g,o,b] (B_b[o, g, :] . (x_g * cols[g, :, b]))
+//        + sum_g sum_b srows[g,o,b] (R_b[o, g, :] . (x[128 g + idx[g, :]] * scols[g, :, b]))
+// with B, R in {-1, +1} stored as bits (1 = +1).
+struct HybridArgs {
+  const uint16_t* x;       // [K] activations (fp16 / bf16)
+  const uint8_t* codes;    // [G, O, 2, 16]: bit j of byte c of base b = column 8 c + j
+  const float* rows;       // [G, O, 2]
+  const float* cols;       // [G, 128, 2]
+  const int16_t* idx;      // [G, 8] refinement columns inside each group
+  const uint8_t* scodes;   // [G, O, 2, 1]: bit j = refinement column j
+  const float* srows;      // [G, O, 2]
+  const float* scols;      // [G, 8, 2]
+  float* partial;          // null: write out directly (single K split)
+  uint16_t* out;           // [O]
+  int O, G, gps;
+  int row_blocks;  // ceil(O / (16 * tiles))
+  int xcds;
+};
+
+constexpr int kHybridMaxBatches = 36;  // four-group batches one workgroup stages (117 KB LDS)
+
+// Dynamic LDS of one workgroup: main digit operands (2 KB), refinement operands
+// (256 B) and activations (1 KB) per staged batch.
+inline size_t hybrid_lds_bytes(int gps) { return size_t(gps / 4) * (2048 + 256 + 1024); }
+
+// Instantiated (tiles, kparts): (1,4) (1,8) (2,4) (3,4).  False otherwise.
+bool dispatch_hybrid(int xdt, int tiles, int kparts, const HybridArgs& a, dim3 grid, hipStream_t s);
+
+}  // namespace fx

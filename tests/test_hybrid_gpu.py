@@ -1,0 +1,147 @@
+"""GPU parity of the hybrid g128/s8 two-base GEMV (``fx_hybrid_gemv`` via ``m1_out``
+and ``PackedHybridLinear``) against the float64 ``oracle.two_base.structural_reference``.
+
+Bars: the reference's structural gate for bf16 outputs (``factored_reference.py``:
+every |err| <= 0.02 (rms + |ref|), normalized RMSE <= 0.005), and the tighter
+normwise max relative error 2^-8 for bf16 / fp16 outputs (output rounding plus the
+kernel's 16-bit fixed-point activation operands).  Tails, K splits, both layout
+families, refinement columns (basis vectors), streams, graphs and the prepared
+decode binding are covered, after the reference's CUDA tests
+(``tests/test_deployment.py:179-276``).
+"""
+import numpy as np
+import pytest
+import torch
+
+from marlin_style_fluxbin_amd import deployment as d
+from oracle import two_base as tb
+
+pytestmark = pytest.mark.gpu
+
+DT = {"bf16": torch.bfloat16, "f16": torch.float16}
+
+
+def _payload(o, g, seed=19):
+    return {k: torch.from_numpy(v) for k, v in tb.make_hybrid_payload(o, g, seed=seed).items()}
+
+
+def _layout(p, kernel, device):
+    return {k: v.to(device) for k, v in d.convert_artifact(p, kernel=kernel).items()}
+
+
+def _reference(x, p):
+    layout = tb.convert_artifact({k: v.numpy() for k, v in p.items()})
+    return tb.structural_reference(x.float().cpu().numpy().astype(np.float64), layout)
+
+
+def _check(y, ref):
+    got = y.float().cpu().numpy().astype(np.float64)
+    assert np.all(np.isfinite(got))
+    rms = float(np.sqrt(np.mean(ref ** 2)))
+    assert np.all(np.abs(got - ref) <= 0.02 * (rms + np.abs(ref)) + 1e-6)
+    nrmse = float(np.sqrt(np.mean((got - ref) ** 2)) / max(rms, 1e-30))
+    assert nrmse <= 0.005, nrmse
+    assert float(np.max(np.abs(got - ref)) / max(np.max(np.abs(ref)), 1e-30)) <= 2 ** -8
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+@pytest.mark.parametrize("o,g", [(1, 1), (7, 3), (17, 3), (65, 10), (1025, 2), (300, 32), (12288, 32), (4096, 96)])
+def test_m1_out_matches_structural_reference(gpu, dtype, o, g):
+    p = _payload(o, g, seed=o + g)
+    layout = _layout(p, "v5_p1024", gpu)
+    x = torch.randn(1, g * 128, generator=torch.Generator().manual_seed(o)).to(DT[dtype])
+    ref = _reference(x, p)
+    for gps in (1, 8, 1024):
+        ws = torch.full(d.workspace_shape(o, g * 128, gps), float("nan"), device=gpu)
+        y = torch.empty(1, o, dtype=DT[dtype], device=gpu)
+        d.m1_out(x.to(gpu), layout, y, ws, groups_per_split=gps, kernel="v5_p1024")
+        _check(y, ref)
+
+
+@pytest.mark.parametrize("kernel", ["v1", "v4", "v5", "v5_p256"])
+def test_interleaved_and_planar_kernels_agree(gpu, kernel):
+    o, g = 65, 10
+    p = _payload(o, g, seed=3)
+    x = torch.randn(1, g * 128, generator=torch.Generator().manual_seed(2)).to(torch.bfloat16).to(gpu)
+    planar = _layout(p, "v5_p1024", gpu)
+    ws = torch.empty(d.workspace_shape(o, g * 128, 8, kernel=kernel), device=gpu)
+    want = torch.empty(1, o, dtype=torch.bfloat16, device=gpu)
+    d.m1_out(x, planar, want, torch.empty(d.workspace_shape(o, g * 128, 8), device=gpu), kernel="v5_p1024")
+    y = torch.empty_like(want)
+    d.m1_out(x, _layout(p, kernel, gpu), y, ws, kernel=kernel)
+    assert torch.equal(y, want)
+
+
+def test_basis_vectors_hit_main_and_refinement_columns(gpu):
+    o, g = 48, 3
+    p = _payload(o, g, seed=7)
+    layout = _layout(p, "v5_p512", gpu)
+    w = tb.materialize_hybrid({k: v.numpy() for k, v in p.items()}).astype(np.float64)
+    cols = [0, 1, 7, 8, 100, 127, 128, 383] + [128 * gi + int(c) for gi in range(g) for c in p["refinement_indices"][gi][:2]]
+    ws = torch.empty(d.workspace_shape(o, g * 128), device=gpu)
+    for col in cols:
+        x = torch.zeros(1, g * 128, dtype=torch.bfloat16, device=gpu)
+        x[0, col] = 1.0
+        y = torch.empty(1, o, dtype=torch.bfloat16, device=gpu)
+        d.m1_out(x, layout, y, ws, kernel="v5_p512")
+        got = y.float().cpu().numpy()[0]
+        want = w[:, col]
+        assert np.max(np.abs(got - want)) <= 2 ** -7 * np.max(np.abs(w)), col
+
+
+def test_streams_graphs_and_repeated_calls(gpu):
+    o, g = 1025, 4
+    p = _payload(o, g, seed=5)
+    layout = _layout(p, "v5_p1024", gpu)
+    x = torch.randn(1, g * 128, device=gpu).to(torch.bfloat16)
+    ws = torch.full(d.workspace_shape(o, g * 128, 1), float("nan"), device=gpu)
+    y = torch.empty(1, o, dtype=torch.bfloat16, device=gpu)
+
+    def run():
+        d.m1_out(x, layout, y, ws, groups_per_split=1, kernel="v5_p1024")
+
+    run()
+    saved = y.clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        ws.fill_(float("nan"))
+        run()
+    torch.cuda.current_stream().wait_stream(side)
+    assert torch.equal(saved, y)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        run()
+    for _ in range(3):
+        y.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(saved, y)
+    with pytest.raises(RuntimeError):
+        d.m1_out(x.expand(2, -1).contiguous(), layout, y, ws, kernel="v5_p1024")
+
+
+@pytest.mark.parametrize("kernel", ["v1", "v5_p1024"])
+def test_packed_hybrid_linear_routes_and_prepared_decode(gpu, kernel):
+    o, g = 96, 4
+    p = _payload(o, g, seed=11)
+    bias = torch.randn(o).to(torch.bfloat16)
+    module = d.PackedHybridLinear(p, bias=bias, kernel=kernel).to(gpu)
+    x = torch.randn(1, 1, g * 128, generator=torch.Generator().manual_seed(1)).to(torch.bfloat16)
+    ref = _reference(x.view(1, -1), p)[0] + bias.float().numpy()
+    with torch.inference_mode():
+        y = module(x.to(gpu))
+        assert y.shape == (1, 1, o) and module.last_route == "packed_m1"
+        got = y.float().cpu().numpy()[0, 0]
+        assert np.max(np.abs(got - ref)) <= 2 ** -7 * np.max(np.abs(ref))
+        module.bind_prepared_decode(torch.bfloat16)
+        module._decode_audit = True
+        first = module(x.to(gpu)).clone()
+        second = module(x.to(gpu))
+        assert torch.equal(first, second) and torch.equal(first, y)
+        assert module.route_counts["packed_m1"] == 3
+        with pytest.raises(ValueError):
+            module(x.to(gpu).float())
+        module.clear_prepared_decode()
+        with pytest.raises(ValueError):
+            module(torch.randn(1, 2, g * 128, device=gpu, dtype=torch.bfloat16))
