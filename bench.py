@@ -189,8 +189,14 @@ def two_base_bench(device, steps, warmup, stream, o=12288, k=4096, salient=32, m
 
     ms_bf16 = time_graph(capture(bf16_arm, stream), steps, warmup, stream) / dense_copies
     gbps = nbytes / (ms / 1e3) / 1e9
+    traffic = None
+    traffic_file = ROOT / "profiles" / "w3_mfma_traffic.json"
+    if traffic_file.exists():
+        traffic = json.loads(traffic_file.read_text()).get("two_base", {}).get("rank_one_kernel", {}).get(
+            "traffic_bytes")
     return {
         "workload": f"config 4: rank-one two-base GEMV {o}x{k}, M=1, {salient} salient bf16 columns",
+        "traffic_bytes": traffic,
         "algorithmic_bytes": nbytes,
         "us": round(ms * 1e3, 3),
         "GBps": round(gbps, 1),
@@ -365,9 +371,10 @@ def decode_bench(layers=36, prefix=512, steps=32, replays=5, seed=0):
 def pmc_target():
     """Workload for ``rocprofv3 --pmc`` passes: the gate/up W3 GEMV (default plan)
     over 24 rotating payloads, twice; the LUT kernel (reference-style tables in
-    LDS) at the same shape, 8 launches; and torch's copy kernel over 16 distinct
-    20 MiB float32 buffers, whose FETCH_SIZE / WRITE_SIZE readings calibrate the
-    counters to bytes."""
+    LDS) at the same shape, 8 launches; the two-base GEMVs at the same shape (the
+    rank-one kernel over 24 payloads twice, the hybrid kernel 8 launches); and
+    torch's copy kernel over 16 distinct 20 MiB float32 buffers, whose FETCH_SIZE /
+    WRITE_SIZE readings calibrate the counters to bytes."""
     import torch
 
     from marlin_style_fluxbin_amd import W3Gemv
@@ -386,6 +393,38 @@ def pmc_target():
     partial = torch.empty(workspace_shape(o, k), dtype=torch.float32, device=device)
     for p in payloads[:8]:
         inline_main(x, p, partial, row_tile=256)
+    del gemvs, payloads
+    # the two-base GEMVs at the same shape: config 4's rank-one kernel, 24 rotating
+    # payloads twice, and the hybrid (reference layout) kernel, 8 payloads
+    from marlin_style_fluxbin_amd import deployment
+    from marlin_style_fluxbin_amd.two_base import TwoBaseGemv, pack_rank_one_planes
+
+    g = k // 128
+    rank_one = []
+    for _ in range(24):
+        bases = torch.randint(0, 2, (2, o, k), device=device, generator=gen, dtype=torch.int8) * 2 - 1
+        rank_one.append(TwoBaseGemv({
+            "planes": pack_rank_one_planes(bases),
+            "coef": (torch.rand(2, o, device=device, generator=gen) + 0.5).half(),
+            "srow": (torch.rand(o, device=device, generator=gen) * 0.015 + 0.005).half(),
+            "tcol": (torch.rand(k, device=device, generator=gen) * 0.4 + 0.8).half(),
+            "salient": (torch.randn(o, 32, device=device, generator=gen) * 0.05).bfloat16(),
+            "salient_idx": torch.randperm(k, device=device, generator=gen)[:32].sort().values.int()}))
+    for _ in range(2):
+        for gemv in rank_one:
+            gemv(x, out)
+    del rank_one
+    ws = torch.empty(deployment.workspace_shape(o, k), device=device)
+    for _ in range(8):
+        layout = {"codes": torch.randint(0, 256, (g, o, 2, 16), dtype=torch.uint8, device=device, generator=gen),
+                  "rows": torch.randn(g, o, 2, device=device, generator=gen) * 0.1,
+                  "columns": torch.randn(g, 128, 2, device=device, generator=gen),
+                  "indices": torch.arange(8, dtype=torch.int16, device=device).repeat(g, 1) * 16,
+                  "sparse_codes": torch.randint(0, 256, (g, o, 2, 1), dtype=torch.uint8, device=device,
+                                                generator=gen),
+                  "sparse_rows": torch.randn(g, o, 2, device=device, generator=gen) * 0.07,
+                  "sparse_columns": torch.randn(g, 8, 2, device=device, generator=gen)}
+        deployment.m1_out(x, layout, out, ws, kernel="v5_p1024")
     src = [torch.empty(CALIBRATION_BYTES // 4, device=device) for _ in range(16)]
     dst = [torch.empty_like(t) for t in src]
     for a, b in zip(src, dst):
@@ -409,7 +448,11 @@ def summarize_pmc(csv_paths, out_json):
             for row in csv.DictReader(f):
                 values[row["Kernel_Name"]][row["Counter_Name"]].append(float(row["Counter_Value"]))
     mean = {k: {c: sum(v) / len(v) for c, v in d.items()} for k, d in values.items()}
-    # the 20 MiB same-dtype copies run as the runtime's buffer-copy kernel
+    # the 16 copies of 20 MiB run as the runtime's buffer-copy kernel; smaller copies
+    # elsewhere in the workload share its name, so calibrate on the 16 largest
+    for k, d in values.items():
+        if "copyBuffer" in k:
+            mean[k] = {c: sum(sorted(v)[-16:]) / len(sorted(v)[-16:]) for c, v in d.items()}
     copy = [k for k in mean if "copyBuffer" in k and "FETCH_SIZE" in mean[k]]
     w3 = [k for k in mean if "w3_mfma_kernel" in k]
     if not copy or not w3:
@@ -431,8 +474,22 @@ def summarize_pmc(csv_paths, out_json):
         "traffic_bytes": int(round(fetch + write)),
         "algorithmic_bytes": algorithmic_bytes(o, k),
         "counters": {k.split("(")[0]: {c: round(v, 1) for c, v in d.items()} for k, d in mean.items()
-                     if "w3_" in k or "copyBuffer" in k},
+                     if "w3_" in k or "copyBuffer" in k or "rank_one" in k or "hybrid" in k},
     }
+    g = k // 128
+    two_base_bytes = {"rank_one_kernel": 2 * o * k // 8 + 6 * o + 2 * k + 64 * o + 128 + 2 * k + 2 * o,
+                      "hybrid_kernel": 32 * g * o + 8 * g * o + 1024 * g + 16 * g + 2 * g * o + 8 * g * o
+                                       + 64 * g + 2 * k + 2 * o}
+    for name, nbytes in two_base_bytes.items():
+        hit = [kk for kk in mean if name in kk and "FETCH_SIZE" in mean[kk]]
+        if hit:
+            m = mean[hit[0]]
+            summary.setdefault("two_base", {})[name] = {
+                "fetch_kib_raw": round(m["FETCH_SIZE"], 1),
+                "write_kib_raw": round(m.get("WRITE_SIZE", 0.0), 1),
+                "traffic_bytes": int(round(m["FETCH_SIZE"] * fetch_scale * 1024
+                                           + m.get("WRITE_SIZE", 0.0) * (write_scale or 1.0) * 1024)),
+                "algorithmic_bytes": nbytes}
     Path(out_json).write_text(json.dumps(summary, indent=1) + "\n")
     print(json.dumps(summary, indent=1))
 
