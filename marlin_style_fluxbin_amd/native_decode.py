@@ -55,6 +55,46 @@ class _Linear:
             out.add_(self.bias)
 
 
+class _FusedLinear:
+    """Linears that read the same activation, run as one GEMV over their
+    concatenated rows (q|k|v, gate|up): one launch instead of several.  W3 payloads
+    concatenate along O when K, arithmetic, scale dtype, zero-point presence and
+    the column permutation agree; dense weights concatenate along O.  Each output
+    row is computed exactly as it would be alone, so the outputs are bit-identical
+    to separate calls.  ``None`` from :meth:`build` when the modules do not fuse."""
+
+    def __init__(self, call, widths):
+        self.call = call
+        self.widths = widths
+
+    @staticmethod
+    def build(modules):
+        if all(isinstance(m, PackedW3Linear) for m in modules):
+            layouts = [m.layout() for m in modules]
+            first = layouts[0]
+            same = all(
+                m.in_features == modules[0].in_features and m.arithmetic == modules[0].arithmetic
+                and l["scales"].dtype == first["scales"].dtype and ("zeros" in l) == ("zeros" in first)
+                and torch.equal(l["perm"], first["perm"]) for m, l in zip(modules, layouts))
+            if not same or any(m.bias is not None for m in modules):
+                return None
+            fused = {"planes": torch.cat([l["planes"] for l in layouts], dim=2).contiguous(),
+                     "scales": torch.cat([l["scales"] for l in layouts], dim=1).contiguous(),
+                     "perm": first["perm"]}
+            if "zeros" in first:
+                fused["zeros"] = torch.cat([l["zeros"] for l in layouts], dim=1).contiguous()
+            gemv = W3Gemv(fused, arithmetic=modules[0].arithmetic)
+            return _FusedLinear(gemv, [m.out_features for m in modules])
+        if all(type(m) is torch.nn.Linear for m in modules) and all(m.bias is None for m in modules):
+            weight = torch.cat([m.weight for m in modules], dim=0).contiguous()
+            return _FusedLinear(lambda x, out: torch.matmul(x, weight.t(), out=out),
+                                [m.out_features for m in modules])
+        return None
+
+    def __call__(self, x, out):
+        self.call(x, out)
+
+
 class NativeDecodeSession:
     def __init__(self, model, input_ids: torch.Tensor, forced_tokens: torch.Tensor):
         from transformers import StaticCache
@@ -108,6 +148,9 @@ class NativeDecodeSession:
         self.final_norm = model.model.norm.weight
         self.lm_head = model.lm_head.weight
         self.lin = [{name: _Linear(block.get_submodule(name)) for name in _ATTN + _MLP} for block in self.layers]
+        # q|k|v and gate|up as one GEMV each where the payloads allow it
+        self.qkv = [_FusedLinear.build([b.get_submodule(n) for n in _ATTN[:3]]) for b in self.layers]
+        self.gate_up = [_FusedLinear.build([b.get_submodule(n) for n in _MLP[:2]]) for b in self.layers]
         self.in_norm = [b.input_layernorm.weight for b in self.layers]
         self.post_norm = [b.post_attention_layernorm.weight for b in self.layers]
         self.q_norm = [b.self_attn.q_norm.weight for b in self.layers]
@@ -120,8 +163,13 @@ class NativeDecodeSession:
         qd, kd = self.heads * self.head_dim, self.kv_heads * self.head_dim
         inter = cfg.intermediate_size
         self.residual, self.normed = buf(self.hidden), buf(self.hidden)
-        self.q, self.k, self.v, self.q_rot, self.attn = buf(qd), buf(kd), buf(kd), buf(qd), buf(qd)
-        self.o, self.gate, self.up, self.act, self.down = buf(self.hidden), buf(inter), buf(inter), buf(inter), buf(self.hidden)
+        # q|k|v and gate|up are views of one buffer each (what a fused GEMV writes)
+        self.qkv_out = buf(qd + 2 * kd)
+        self.q, self.k, self.v = self.qkv_out[:, :qd], self.qkv_out[:, qd:qd + kd], self.qkv_out[:, qd + kd:]
+        self.gate_up_out = buf(2 * inter)
+        self.gate, self.up = self.gate_up_out[:, :inter], self.gate_up_out[:, inter:]
+        self.q_rot, self.attn = buf(qd), buf(qd)
+        self.o, self.act, self.down = buf(self.hidden), buf(inter), buf(self.hidden)
         self.logits = torch.empty((self.steps, cfg.vocab_size), dtype=dtype, device=self.device)
         self.predictions = torch.empty((self.steps, 1), dtype=torch.int64, device=self.device)
         lib = _lib.library()
@@ -157,9 +205,12 @@ class NativeDecodeSession:
             if l > 0:
                 add_rms_norm(self.down, self.residual, self.in_norm[l], self.eps, out=self.normed,
                              residual_out=self.residual)
-            lin["self_attn.q_proj"](self.normed, self.q)
-            lin["self_attn.k_proj"](self.normed, self.k)
-            lin["self_attn.v_proj"](self.normed, self.v)
+            if self.qkv[l] is not None:
+                self.qkv[l](self.normed, self.qkv_out)
+            else:
+                lin["self_attn.q_proj"](self.normed, self.q)
+                lin["self_attn.k_proj"](self.normed, self.k)
+                lin["self_attn.v_proj"](self.normed, self.v)
             head_norm_rope([
                 dict(x=self.q.view(self.heads, d), out=self.q_rot.view(self.heads, d), weight=self.q_norm[l],
                      heads=self.heads, rope=True, in_strides=(0, d, 0), out_strides=(0, d, 0)),
@@ -172,8 +223,11 @@ class NativeDecodeSession:
             lin["self_attn.o_proj"](self.attn, self.o)
             add_rms_norm(self.o, self.residual, self.post_norm[l], self.eps, out=self.normed,
                          residual_out=self.residual)
-            lin["mlp.gate_proj"](self.normed, self.gate)
-            lin["mlp.up_proj"](self.normed, self.up)
+            if self.gate_up[l] is not None:
+                self.gate_up[l](self.normed, self.gate_up_out)
+            else:
+                lin["mlp.gate_proj"](self.normed, self.gate)
+                lin["mlp.up_proj"](self.normed, self.up)
             self._silu_mul()
             lin["mlp.down_proj"](self.act, self.down)
         add_rms_norm(self.down, self.residual, self.final_norm, self.eps, out=self.normed,
