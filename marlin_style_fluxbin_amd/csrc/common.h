@@ -105,14 +105,25 @@ __device__ __forceinline__ u32x4_t load_b128(__amdgpu_buffer_rsrc_t r, int offse
 
 constexpr int kOutOfRange = int(0x80000000u);  // > every record count: loads return 0
 
-// Workgroup index -> (row block, K split) so that the workgroups one XCD runs
-// (hardware dispatch deals consecutive workgroup ids round-robin over the XCDs)
+// Streaming load of weights that are read exactly once per launch: aux bit 1 is
+// the non-temporal policy, so the lines do not displace the activations and
+// per-row metadata that other workgroups still read from L2 (measured 0.3-0.7 us
+// per GEMV at the Qwen3-8B shapes on MI355X).
+__device__ __forceinline__ u32x4_t load_b128_stream(__amdgpu_buffer_rsrc_t r, int offset, int soffset) {
+  return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, offset, soffset, 2));
+}
+
+// Workgroup x index -> row block, so that the workgroups one XCD runs (hardware
+// dispatch deals consecutive workgroup ids round-robin over MI355X's 8 XCDs)
 // take consecutive row blocks and share the per-row metadata cache lines in
-// that XCD's L2.  A bijection for any grid size.
-__device__ __forceinline__ int xcd_local_index(int linear, int total, int xcds) {
-  const int xcd = linear % xcds, local = linear / xcds;
-  const int q = total / xcds, rem = total % xcds;
-  return xcd < rem ? xcd * (q + 1) + local : rem * (q + 1) + (xcd - rem) * q + local;
+// that XCD's L2.  A bijection for any grid size; the XCD count is a compile-time
+// constant (shifts and masks, no integer division ahead of the first load), and
+// a partition mode that exposes fewer XCDs only loses the locality.
+constexpr int kXcdCount = 8;
+__device__ __forceinline__ int xcd_local_index8(unsigned linear, unsigned total) {
+  const unsigned xcd = linear % kXcdCount, local = linear / kXcdCount;
+  const unsigned q = total / kXcdCount, rem = total % kXcdCount;
+  return int(xcd < rem ? xcd * (q + 1) + local : rem * (q + 1) + (xcd - rem) * q + local);
 }
 
 }  // namespace fx

@@ -65,11 +65,13 @@ __global__ __launch_bounds__(NT * NK * 64) void hybrid_kernel(HybridArgs a) {
   __shared__ float ug[kHybridMaxBatches][4][2];    // U per (batch, group slot, base)
   __shared__ float vg[kHybridMaxBatches][4][2];    // refinement U per (batch, slot, base)
   __shared__ float red[NK][16 * NT];
+  // one scalar-load round for every argument, before any branch
+  asm volatile("" ::"s"(a.x), "s"(a.codes), "s"(a.rows), "s"(a.cols), "s"(a.idx), "s"(a.scodes), "s"(a.srows),
+               "s"(a.scols), "s"(a.partial), "s"(a.out), "s"(a.O), "s"(a.G), "s"(a.gps), "s"(a.row_blocks));
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int O = a.O, G = a.G, K = G * 128;
-  const int block = xcd_local_index(blockIdx.x, gridDim.x, a.xcds);
-  const int split = block / a.row_blocks;
-  const int row0 = (block - split * a.row_blocks) * (16 * NT);
+  const int split = blockIdx.y;
+  const int row0 = xcd_local_index8(blockIdx.x, a.row_blocks) * (16 * NT);
   const int g0 = split * a.gps;
   const int g1 = min(G, g0 + a.gps);
   const int nbatch = (g1 - g0 + 3) >> 2;
@@ -115,8 +117,8 @@ __global__ __launch_bounds__(NT * NK * 64) void hybrid_kernel(HybridArgs a) {
     const int bt = kpart + i * NK;
     const int g = g0 + 4 * bt + kb;
     const int poff = (g * O + prow) * 32;  // past the end -> zeros
-    w0 = load_b128(rp, poff, 0);
-    w1 = load_b128(rp, poff + 16, 0);
+    w0 = load_b128_stream(rp, poff, 0);
+    w1 = load_b128_stream(rp, poff + 16, 0);
     sb = __builtin_amdgcn_raw_buffer_load_b16(rsp, (g * O + prow) * 2, 0, 0);
     // row scales of D rows drow .. +3 for this lane's group slot, both bases
     const int gd = g0 + 4 * bt + dslot;

@@ -71,11 +71,13 @@ __global__ __launch_bounds__(NT * NK * 64) void rank_one_kernel(RankOneArgs a) {
   __shared__ float bsum[kRankOneMaxBatches];    // U of each batch (real units)
   __shared__ float red[NK][16 * NT][2];
   __shared__ float sal_sum[16 * NT];
+  // one scalar-load round for every argument, before any branch
+  asm volatile("" ::"s"(a.x), "s"(a.planes), "s"(a.coef), "s"(a.srow), "s"(a.tcol), "s"(a.sal), "s"(a.sal_idx),
+               "s"(a.partial), "s"(a.out), "s"(a.O), "s"(a.G), "s"(a.S), "s"(a.gps), "s"(a.row_blocks));
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int O = a.O, G = a.G, K = G * 128;
-  const int block = xcd_local_index(blockIdx.x, gridDim.x, a.xcds);
-  const int split = block / a.row_blocks;
-  const int row0 = (block - split * a.row_blocks) * (16 * NT);
+  const int split = blockIdx.y;
+  const int row0 = xcd_local_index8(blockIdx.x, a.row_blocks) * (16 * NT);
   const int g0 = split * a.gps;
   const int g1 = min(G, g0 + a.gps);
   const int nbatch = (g1 - g0 + 3) >> 2;
@@ -128,8 +130,8 @@ __global__ __launch_bounds__(NT * NK * 64) void rank_one_kernel(RankOneArgs a) {
   auto issue = [&](int i, u32x4_t w[2]) __attribute__((always_inline)) {
     const int g = g0 + 4 * (kpart + i * NK) + kb;
     const int poff = (g * O + prow) * 32;  // past the end -> zeros
-    w[0] = load_b128(rp, poff, 0);
-    w[1] = load_b128(rp, poff + 16, 0);
+    w[0] = load_b128_stream(rp, poff, 0);
+    w[1] = load_b128_stream(rp, poff + 16, 0);
   };
   u32x4_t ring[PD][2];
 #pragma unroll

@@ -19,8 +19,7 @@ struct RankOneArgs {
   float* partial;          // null: write out directly (single K split)
   uint16_t* out;           // [O]
   int O, G, S, gps;
-  int row_blocks;  // ceil(O / (16 * tiles))
-  int xcds;
+  int row_blocks;  // ceil(O / (16 * tiles)); the grid is (row_blocks, K splits)
 };
 
 constexpr int kRankOneMaxBatches = 24;  // four-group batches one workgroup stages (48 KB LDS)
@@ -55,8 +54,7 @@ struct HybridArgs {
   float* partial;          // null: write out directly (single K split)
   uint16_t* out;           // [O]
   int O, G, gps;
-  int row_blocks;  // ceil(O / (16 * tiles))
-  int xcds;
+  int row_blocks;  // ceil(O / (16 * tiles)); the grid is (row_blocks, K splits)
 };
 
 constexpr int kHybridMaxBatches = 36;  // four-group batches one workgroup stages (117 KB LDS)

@@ -36,6 +36,12 @@
 // K splits across waves are reduced through LDS; across workgroups through
 // fp32 partials summed by w3_finish_kernel (stream-ordered, no device-scope
 // fences).
+//
+// Issue order per batch: activations, then the plane rows (non-temporal: read
+// once), then scales and zero-points.  A wave's loads complete in issue order,
+// so staging waits only for the L2-resident activations and overlaps the
+// weight stream; scheduling barriers keep the compiler from reordering them.
+// All kernel arguments are read in one scalar round before any branch.
 #pragma once
 #include "common.h"
 
@@ -107,36 +113,44 @@ struct BatchLoads {
   u32x4_t xv[MB];    // activation bits of rows 0..MB-1 (PERM: xv[0] = 8 int16 columns)
   unsigned s[RT][2]; // scales of rows erow..erow+3 of each tile, two per word
   unsigned z[RT];    // zero-points of rows erow..erow+3, one per byte
+  unsigned se[RT][4], ze[RT][4];  // the same as single elements when O % 4 != 0
 };
 
-// grid (ceil(O / (16 RT)) * splits) workgroups of NW*64 threads.  Workgroup:
-// rows [16 RT b, +16 RT), groups [gps*split, +gps) with gps a multiple of 4.
-// Rows past O and groups past G need no masking: padded groups have zero
-// activations (so D = 0 and sum(x) = 0), and rows past O are never stored.
-// x is [MB, 128 G] row-major; with PERM, sorted column k reads x column perm[k].
-template <int NW, int PD, int MB, int RT, bool PERM, int XDT, int SDT>
-__global__ __launch_bounds__(NW * 64) void w3_mfma_kernel(
-    const uint16_t* __restrict__ x, const int16_t* __restrict__ perm,
+// Workgroup LDS: per wave, B operands [k-block][step][row] (16 B each), zero
+// operands [step][row] read by the lanes whose column belongs to another
+// k-block, sum of x and subnormal exponent - E per (k-block group, row), and the
+// per-wave partial outputs.
+template <int NW, int MB, int RT>
+struct MfmaShared {
+  u32x4_t bstage[NW][64 * MB];
+  u32x4_t bzero[NW][16 * MB];
+  float gsum[NW][4 * MB];
+  int gexp[NW][4 * MB];
+  float red[NW][16 * RT * MB];
+};
+
+// VEC: O is a multiple of 4, so the four scales / zero-points of a lane are one
+// aligned load each.  A separate instantiation (rather than a runtime branch)
+// keeps the load count per batch fixed, so the wait before staging covers only
+// the activations.
+template <int NW, int PD, int MB, int RT, bool PERM, int XDT, int SDT, bool VEC>
+__device__ __forceinline__ void w3_mfma_body(
+    MfmaShared<NW, MB, RT>& sh, const uint16_t* __restrict__ x, const int16_t* __restrict__ perm,
     const uint8_t* __restrict__ planes, const uint16_t* __restrict__ scales,
     const uint8_t* __restrict__ zeros, float* __restrict__ partial,
-    uint16_t* __restrict__ out, int O, int G, int gps, int row_blocks, int xcds) {
-  // per wave: B operands [k-block][step][row] (16 B each), and zero operands
-  // [step][row] read by the lanes whose column belongs to another k-block
-  __shared__ u32x4_t bstage[NW][64 * MB];
-  __shared__ u32x4_t bzero[NW][16 * MB];
-  __shared__ float gsum[NW][4 * MB];   // sum of x per (k-block group, row)
-  __shared__ int gexp[NW][4 * MB];     // subnormal exponent - E per (k-block group, row)
-  __shared__ float red[NW][16 * RT * MB];
+    uint16_t* __restrict__ out, int O, int G, int gps, int row_blocks) {
+  auto& bstage = sh.bstage;
+  auto& bzero = sh.bzero;
+  auto& gsum = sh.gsum;
+  auto& gexp = sh.gexp;
+  auto& red = sh.red;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int K = G * 128;
-  const int block = xcd_local_index(blockIdx.x, gridDim.x, xcds);
-  const int split = block / row_blocks;
-  const int row0 = (block - split * row_blocks) * (16 * RT);
+  const int split = blockIdx.y;
+  const int row0 = xcd_local_index8(blockIdx.x, row_blocks) * (16 * RT);
   const int g0 = split * gps;
   const int g1 = min(G, g0 + gps);
   const int nbatch = (g1 - g0 + 3) >> 2;
-  // four consecutive scales / zero-points of a row block are one aligned load
-  const bool vec = (O & 3) == 0;
   // absent zero-points read as 0 (empty buffer) and become 4 through this OR
   const unsigned zero_default = zeros ? 0u : 0x04040404u;
 
@@ -166,13 +180,6 @@ __global__ __launch_bounds__(NW * 64) void w3_mfma_kernel(
 
   auto issue = [&](int batch, BatchLoads<MB, RT>& L) __attribute__((always_inline)) {
     const int gb = g0 + 4 * batch;
-    const int poff = ((gb + kb) * 3 * O + row0 + r) * 16;  // past the end -> zeros
-#pragma unroll
-    for (int tt = 0; tt < RT; ++tt) {
-      L.w[tt][0] = load_b128(rp, poff + tt * 256, 0);
-      L.w[tt][1] = load_b128(rp, poff + tt * 256, plane_stride);
-      L.w[tt][2] = load_b128(rp, poff + tt * 256, 2 * plane_stride);
-    }
     const int col = (gb + kb) * 128 + 8 * r;
     const bool real = gb + kb < G;
     if constexpr (PERM) {
@@ -181,25 +188,30 @@ __global__ __launch_bounds__(NW * 64) void w3_mfma_kernel(
 #pragma unroll
       for (int m = 0; m < MB; ++m) L.xv[m] = load_b128(rx, real ? (m * K + col) * 2 : kOutOfRange, 0);
     }
+    __builtin_amdgcn_sched_barrier(0);
+    const int poff = ((gb + kb) * 3 * O + row0 + r) * 16;  // past the end -> zeros
+#pragma unroll
+    for (int tt = 0; tt < RT; ++tt) {
+      L.w[tt][0] = load_b128_stream(rp, poff + tt * 256, 0);
+      L.w[tt][1] = load_b128_stream(rp, poff + tt * 256, plane_stride);
+      L.w[tt][2] = load_b128_stream(rp, poff + tt * 256, 2 * plane_stride);
+    }
+    __builtin_amdgcn_sched_barrier(0);
     const int eoff = (gb + cslot) * O + row0 + 4 * kb;
 #pragma unroll
     for (int tt = 0; tt < RT; ++tt) {
       const int e = eoff + 16 * tt;
-      if (vec) {
+      if constexpr (VEC) {
         const uint2 s4 = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rs, e * 2, 0, 0));
         L.s[tt][0] = s4.x;
         L.s[tt][1] = s4.y;
         L.z[tt] = __builtin_amdgcn_raw_buffer_load_b32(rz, e, 0, 0);
-      } else {  // O not a multiple of 4 (tests, tiny layers): element loads, same packing
-        unsigned sv[4], zv[4];
+      } else {  // O not a multiple of 4 (tests, tiny layers): element loads, packed in consume()
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          sv[j] = __builtin_amdgcn_raw_buffer_load_b16(rs, (e + j) * 2, 0, 0);
-          zv[j] = __builtin_amdgcn_raw_buffer_load_b8(rz, e + j, 0, 0);
+          L.se[tt][j] = __builtin_amdgcn_raw_buffer_load_b16(rs, (e + j) * 2, 0, 0);
+          L.ze[tt][j] = __builtin_amdgcn_raw_buffer_load_b8(rz, e + j, 0, 0);
         }
-        L.s[tt][0] = sv[0] | (sv[1] << 16);
-        L.s[tt][1] = sv[2] | (sv[3] << 16);
-        L.z[tt] = zv[0] | (zv[1] << 8) | (zv[2] << 16) | (zv[3] << 24);
       }
     }
   };
@@ -291,10 +303,16 @@ __global__ __launch_bounds__(NW * 64) void w3_mfma_kernel(
     const int fev = gexp[wave][cslot * MB + cmc];
 #pragma unroll
     for (int tt = 0; tt < RT; ++tt) {
-      const unsigned zw = L.z[tt] | zero_default;
+      unsigned sw[2] = {L.s[tt][0], L.s[tt][1]}, zw = L.z[tt];
+      if constexpr (!VEC) {
+        sw[0] = L.se[tt][0] | (L.se[tt][1] << 16);
+        sw[1] = L.se[tt][2] | (L.se[tt][3] << 16);
+        zw = L.ze[tt][0] | (L.ze[tt][1] << 8) | (L.ze[tt][2] << 16) | (L.ze[tt][3] << 24);
+      }
+      zw |= zero_default;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const unsigned sb = (j & 1) ? (L.s[tt][j >> 1] >> 16) : (L.s[tt][j >> 1] & 0xffffu);
+        const unsigned sb = (j & 1) ? (sw[j >> 1] >> 16) : (sw[j >> 1] & 0xffffu);
         const float se = to_f32<SDT>(uint16_t(sb));
         const float zf = float((zw >> (8 * j)) & 0xffu);
         acc[tt][j] += se * (ldexpf(d[tt][j], fev) - zf * sxv);
@@ -350,6 +368,32 @@ __global__ __launch_bounds__(NW * 64) void w3_mfma_kernel(
         out[size_t(m) * O + orow] = from_f32<XDT>(total);
     }
   }
+}
+
+
+// grid (row_blocks = ceil(O / (16 RT)), splits) workgroups of NW*64 threads.
+// Workgroup: rows [16 RT b, +16 RT), groups [gps*split, +gps) with gps a
+// multiple of 4.  Rows past O and groups past G need no masking: padded groups
+// have zero activations (so D = 0 and sum(x) = 0), and rows past O are never
+// stored.  x is [MB, 128 G] row-major; with PERM, sorted column k reads x
+// column perm[k].
+template <int NW, int PD, int MB, int RT, bool PERM, int XDT, int SDT>
+__global__ __launch_bounds__(NW * 64) void w3_mfma_kernel(
+    const uint16_t* __restrict__ x, const int16_t* __restrict__ perm,
+    const uint8_t* __restrict__ planes, const uint16_t* __restrict__ scales,
+    const uint8_t* __restrict__ zeros, float* __restrict__ partial,
+    uint16_t* __restrict__ out, int O, int G, int gps, int row_blocks) {
+  // one scalar-load round for every argument (otherwise the pointer loads sink
+  // below the first branch and add a second round trip before the first load)
+  asm volatile("" ::"s"(x), "s"(perm), "s"(planes), "s"(scales), "s"(zeros), "s"(partial), "s"(out),
+               "s"(O), "s"(G), "s"(gps), "s"(row_blocks));
+  __shared__ MfmaShared<NW, MB, RT> sh;
+  if ((O & 3) == 0)
+    w3_mfma_body<NW, PD, MB, RT, PERM, XDT, SDT, true>(sh, x, perm, planes, scales, zeros, partial, out, O, G,
+                                                       gps, row_blocks);
+  else
+    w3_mfma_body<NW, PD, MB, RT, PERM, XDT, SDT, false>(sh, x, perm, planes, scales, zeros, partial, out, O,
+                                                        G, gps, row_blocks);
 }
 
 }  // namespace fx

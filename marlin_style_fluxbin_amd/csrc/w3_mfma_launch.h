@@ -14,8 +14,7 @@ struct MfmaArgs {
   float* partial;  // null: write out directly (single K split)
   uint16_t* out;
   int O, G, gps;
-  int row_blocks;  // ceil(O / (16 * tiles))
-  int xcds;        // XCDs the hardware deals workgroups over
+  int row_blocks;  // ceil(O / (16 * tiles)); the grid is (row_blocks, K splits)
 };
 
 // nw waves per workgroup in {4, 8}; pd batches in flight per wave in {1, 2};
