@@ -702,8 +702,10 @@ int fx_head_norm_rope(int ntensors, const void* const* inputs, void* const* outp
 }
 
 size_t fx_decode_attention_workspace_bytes(int n_q_heads, int max_len, int head_dim) {
-  if (n_q_heads < 1 || max_len < 1 || head_dim < 1) return 0;
-  const size_t splits = (size_t(max_len) + 63) / 64;
+  if (n_q_heads < 1 || max_len < 1 || (head_dim != 64 && head_dim != 128 && head_dim != 256)) return 0;
+  // the most splits any position can use: one key per thread
+  const int keys = fx::attn_keys_per_block(head_dim, 1);
+  const size_t splits = (size_t(max_len) + keys - 1) / keys;
   return size_t(n_q_heads) * splits * (size_t(head_dim) + 2) * sizeof(float);
 }
 
@@ -735,7 +737,20 @@ int fx_decode_attention(const void* q, const void* k_cache, const void* v_cache,
   a.Hk = n_kv_heads;
   a.Lmax = max_len;
   a.pos = position;
-  a.splits = (max_len + 63) / 64;
+  // keys per thread: the most (fewest partials to combine) that still gives a
+  // workgroup per CU; one otherwise
+  const int n = position + 1, cus = device_cu_count();
+  a.kpt = 1;
+  for (int kpt : {4, 2}) {
+    const int keys = fx::attn_keys_per_block(head_dim, kpt);
+    if (long(n_kv_heads) * ((n + keys - 1) / keys) >= cus) {
+      a.kpt = kpt;
+      break;
+    }
+  }
+  const int keys = fx::attn_keys_per_block(head_dim, a.kpt);
+  a.splits = (n + keys - 1) / keys;
+  if (a.splits > 65535) return fail(FX_EINVAL, "position %d needs %d key splits (at most 65535)", position, a.splits);
   a.scale = scale;
   fx::launch_decode_attention(dtype, head_dim, a, static_cast<hipStream_t>(stream));
   return check_launch("attn_split_kernel");

@@ -12,105 +12,215 @@
 
 namespace fx {
 
-typedef unsigned u32x4d_t __attribute__((ext_vector_type(4)));
+// Query heads scored per pass over a KV head's chunk (the chunk's K and V stay
+// in registers across passes).
+constexpr int kAttnHeadsPerPass = 4;
 
-constexpr int kAttnChunk = 64;  // keys per workgroup (one per lane)
+// Sum over the DB lanes (8, 16 or 32) that hold one key row; every lane of the
+// group receives the same bits.
+template <int DB>
+__device__ __forceinline__ float key_row_sum(float v) {
+  v += dpp_move<kDppXor1>(v);
+  v += dpp_move<kDppXor2>(v);
+  v += dpp_move<kDppHalfMirror>(v);
+  if constexpr (DB >= 16) v += dpp_move<kDppMirror>(v);
+  if constexpr (DB == 32) v += __shfl_xor(v, 16, 64);
+  return v;
+}
 
-// grid (Hk, ceil(Lmax / 64)), 256 threads: wave w serves query heads
-// g*G + w, g*G + w + 4, ... (G = Hq / Hk).  Lane l scores key chunk*64 + l, then
-// the wave accumulates P.V with lane l owning output dims l, l + 64, ...
-// partial[(h * splits + chunk) * (D + 2)] = {running max m, sum l, o[0..D)}.
-template <int DT, int D>
+// grid (Hk, splits), 256 threads; splits = ceil((pos + 1) / (KS * KPT)).
+// Thread t holds dims [8 db, 8 db + 8) (db = t % DB, DB = D / 8) of keys
+// first + ks + KS i, i < KPT (ks = t / DB, KS = 256 / DB key rows per pass):
+// a key row is DB consecutive lanes reading 16 B each (coalesced), and every
+// K and V load of the chunk is issued before the first use.  Keys past pos
+// load zeros (out-of-range buffer offsets), so junk in future cache slots is
+// never read.  Per pass of up to 4 query heads: s = (q . k) * scale reduced over
+// the DB lanes of the row, chunk max over the workgroup, p = e^(s - m),
+// l = sum p, o = sum p v per thread, reduced over the key rows through LDS.
+// partial[(h * splits + chunk) * (D + 2)] = {m, l, o[0..D)}.
+template <int DT, int D, int KPT>
 __global__ __launch_bounds__(256) void attn_split_kernel(const uint16_t* __restrict__ q,
                                                          const uint16_t* __restrict__ kc,
                                                          const uint16_t* __restrict__ vc,
                                                          float* __restrict__ partial, int Hq, int Hk,
-                                                         int Lmax, int pos, float scale) {
-  __shared__ float qs[4][D];
-  __shared__ float ps[4][kAttnChunk];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int g = blockIdx.x, chunk = blockIdx.y, splits = gridDim.y;
+                                                         int Lmax, int pos, int splits, float scale) {
+  asm volatile("" ::"s"(q), "s"(kc), "s"(vc), "s"(partial), "s"(Hq), "s"(Hk), "s"(Lmax), "s"(pos),
+               "s"(splits), "s"(scale));
+  constexpr int DB = D / 8, KS = 256 / DB, HB = kAttnHeadsPerPass;
+  __shared__ float red_o[KS][HB][D];
+  __shared__ float red_l[KS][HB];
+  __shared__ float red_m[4][HB];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int db = t % DB, ks = t / DB;
+  const int g = blockIdx.x, chunk = blockIdx.y;
   const int G = Hq / Hk;
-  const int j = chunk * kAttnChunk + lane;
-  const bool live = j <= pos;
-  const int first = chunk * kAttnChunk;
-  for (int hl = wave; hl < G; hl += 4) {
-    const int h = g * G + hl;
-    float* out = partial + (size_t(h) * splits + chunk) * (D + 2);
-    if (first > pos) {  // chunk entirely in the future: empty partial
-      if (lane == 0) {
-        out[0] = -INFINITY;
-        out[1] = 0.f;
-      }
-      for (int d = lane; d < D; d += 64) out[2 + d] = 0.f;
-      continue;
+  const int first = chunk * (KS * KPT);
+  const auto rq = buffer_resource(q + size_t(g) * G * D, size_t(G) * D * 2);
+  const auto rk = buffer_resource(kc + size_t(g) * Lmax * D, size_t(Lmax) * D * 2);
+  const auto rv = buffer_resource(vc + size_t(g) * Lmax * D, size_t(Lmax) * D * 2);
+
+  // ---- loads: first pass's queries, then the chunk's keys and values
+  u32x4_t qr[HB], kr[KPT], vr[KPT];
+  bool live[KPT];
+#pragma unroll
+  for (int hh = 0; hh < HB; ++hh) qr[hh] = load_b128(rq, hh < G ? (hh * D + 8 * db) * 2 : kOutOfRange, 0);
+#pragma unroll
+  for (int i = 0; i < KPT; ++i) {
+    const int j = first + ks + KS * i;
+    live[i] = j <= pos;
+    kr[i] = load_b128(rk, live[i] ? (j * D + 8 * db) * 2 : kOutOfRange, 0);
+  }
+#pragma unroll
+  for (int i = 0; i < KPT; ++i) {
+    const int j = first + ks + KS * i;
+    vr[i] = load_b128(rv, live[i] ? (j * D + 8 * db) * 2 : kOutOfRange, 0);
+  }
+
+  for (int h0 = 0; h0 < G; h0 += HB) {
+    if (h0 > 0) {
+#pragma unroll
+      for (int hh = 0; hh < HB; ++hh)
+        qr[hh] = load_b128(rq, h0 + hh < G ? ((h0 + hh) * D + 8 * db) * 2 : kOutOfRange, 0);
     }
-    for (int d = lane; d < D; d += 64) qs[wave][d] = to_f32<DT>(q[size_t(h) * D + d]);
-    __builtin_amdgcn_wave_barrier();
-    float s = -INFINITY;
-    if (live) {
-      const uint16_t* krow = kc + (size_t(g) * Lmax + j) * D;
-      float acc = 0.f;
-#pragma unroll 4
-      for (int d = 0; d < D; d += 8) {
-        const u32x4d_t kv = *reinterpret_cast<const u32x4d_t*>(krow + d);
+    float kf[KPT][8];
 #pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          acc += qs[wave][d + 2 * w] * to_f32<DT>(uint16_t(kv[w]));
-          acc += qs[wave][d + 2 * w + 1] * to_f32<DT>(uint16_t(kv[w] >> 16));
-        }
+    for (int i = 0; i < KPT; ++i)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) kf[i][e] = to_f32<DT>(uint16_t(kr[i][e >> 1] >> (16 * (e & 1))));
+    float s[HB][KPT];
+    float mt[HB];
+#pragma unroll
+    for (int hh = 0; hh < HB; ++hh) {
+      float qf[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qf[e] = to_f32<DT>(uint16_t(qr[hh][e >> 1] >> (16 * (e & 1))));
+      mt[hh] = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < KPT; ++i) {
+        float acc = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc += qf[e] * kf[i][e];
+        acc = key_row_sum<DB>(acc) * scale;
+        s[hh][i] = live[i] ? acc : -INFINITY;
+        mt[hh] = fmaxf(mt[hh], s[hh][i]);
       }
-      s = acc * scale;
-    }
-    const float m = wave_max(s);  // finite: key `first` <= pos is live
-    const float p = live ? __expf(s - m) : 0.f;
-    const float l = wave_sum(p);
-    ps[wave][lane] = p;
-    __builtin_amdgcn_wave_barrier();
-    const int keys = min(kAttnChunk, pos - first + 1);
-    float o[D / 64];
-#pragma unroll
-    for (int i = 0; i < D / 64; ++i) o[i] = 0.f;
-    const uint16_t* vbase = vc + (size_t(g) * Lmax + first) * D;
-    for (int jj = 0; jj < keys; ++jj) {
-      const float pj = ps[wave][jj];
-#pragma unroll
-      for (int i = 0; i < D / 64; ++i) o[i] += pj * to_f32<DT>(vbase[size_t(jj) * D + lane + 64 * i]);
+      mt[hh] = wave_max(mt[hh]);
     }
     if (lane == 0) {
-      out[0] = m;
-      out[1] = l;
+#pragma unroll
+      for (int hh = 0; hh < HB; ++hh) red_m[wave][hh] = mt[hh];
+    }
+    __syncthreads();
+    float o[HB][8], lt[HB];
+#pragma unroll
+    for (int hh = 0; hh < HB; ++hh) {
+      // the chunk's first key is live, so m is finite
+      const float m = fmaxf(fmaxf(red_m[0][hh], red_m[1][hh]), fmaxf(red_m[2][hh], red_m[3][hh]));
+      mt[hh] = m;
+      lt[hh] = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[hh][e] = 0.f;
+#pragma unroll
+      for (int i = 0; i < KPT; ++i) {
+        const float p = live[i] ? __expf(s[hh][i] - m) : 0.f;
+        lt[hh] += p;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[hh][e] += p * to_f32<DT>(uint16_t(vr[i][e >> 1] >> (16 * (e & 1))));
+      }
     }
 #pragma unroll
-    for (int i = 0; i < D / 64; ++i) out[2 + lane + 64 * i] = o[i];
-    __builtin_amdgcn_wave_barrier();  // qs / ps reused by this wave's next head
+    for (int hh = 0; hh < HB; ++hh) {
+      float4* dst = reinterpret_cast<float4*>(&red_o[ks][hh][8 * db]);
+      dst[0] = make_float4(o[hh][0], o[hh][1], o[hh][2], o[hh][3]);
+      dst[1] = make_float4(o[hh][4], o[hh][5], o[hh][6], o[hh][7]);
+      if (db == 0) red_l[ks][hh] = lt[hh];
+    }
+    __syncthreads();
+    for (int idx = t; idx < HB * D; idx += 256) {
+      const int hh = idx / D, d = idx % D, h = h0 + hh;
+      float total = 0.f;
+#pragma unroll
+      for (int r = 0; r < KS; ++r) total += red_o[r][hh][d];
+      if (h < G) {
+        float* out = partial + (size_t(g * G + h) * splits + chunk) * (D + 2);
+        out[2 + d] = total;
+        if (d == 0) {
+          float l = 0.f;
+#pragma unroll
+          for (int r = 0; r < KS; ++r) l += red_l[r][hh];
+          out[0] = mt[hh];
+          out[1] = l;
+        }
+      }
+    }
+    __syncthreads();  // LDS reused by the next pass
   }
 }
 
-// grid Hq, 64 threads: o_h = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c.
+// grid Hq, 256 threads: o_h = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c over the
+// head's splits, taken in blocks of 256 (a running max rescales earlier blocks):
+// one load round for the block's maxima and sums, then each thread sums one
+// output dim over every (256 / D)-th split of the block with eight loads in
+// flight, and the 256 / D partial sums of a dim meet in LDS.
 template <int DT, int D>
-__global__ __launch_bounds__(64) void attn_combine_kernel(const float* __restrict__ partial,
+__global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restrict__ partial,
                                                           uint16_t* __restrict__ out, int splits) {
-  const int h = blockIdx.x, lane = threadIdx.x;
+  asm volatile("" ::"s"(partial), "s"(out), "s"(splits));
+  static_assert(D <= 256, "one output dim per thread");
+  constexpr int PARTS = 256 / D;  // threads per output dim
+  __shared__ float wsh[256];
+  __shared__ float wred[4];
+  __shared__ float ored[PARTS][D];
+  __shared__ float lred[4];
+  const int h = blockIdx.x, t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const float* base = partial + size_t(h) * splits * (D + 2);
-  float M = -INFINITY;
-  for (int c = 0; c < splits; ++c) M = fmaxf(M, base[size_t(c) * (D + 2)]);
-  float L = 0.f;
-  float o[D / 64];
+  float M = -INFINITY, L = 0.f, o = 0.f;
+  const int part = t / D, d0 = t % D;
+  for (int c0 = 0; c0 < splits; c0 += 256) {
+    const int n = min(256, splits - c0);
+    const bool mine = t < n;
+    const float mc = mine ? base[size_t(c0 + t) * (D + 2)] : -INFINITY;
+    const float lc = mine ? base[size_t(c0 + t) * (D + 2) + 1] : 0.f;
+    float bm = wave_max(mc);
+    if (lane == 0) wred[wave] = bm;
+    __syncthreads();
+    bm = fmaxf(fmaxf(wred[0], wred[1]), fmaxf(wred[2], wred[3]));
+    const float Mn = fmaxf(M, bm);
+    const float rescale = M == -INFINITY ? 0.f : __expf(M - Mn);
+    const float w = mine ? __expf(mc - Mn) : 0.f;
+    wsh[t] = w;
+    float lw = wave_sum(w * lc);
+    if (lane == 0) lred[wave] = lw;
+    __syncthreads();
+    L = L * rescale + (lred[0] + lred[1] + lred[2] + lred[3]);
+    o *= rescale;
+    // this thread: dim d0 over splits part, part + PARTS, ..., eight loads in flight
+    constexpr int U = 8;
+    for (int c = part; c < n; c += PARTS * U) {
+      float v[U];
 #pragma unroll
-  for (int i = 0; i < D / 64; ++i) o[i] = 0.f;
-  for (int c = 0; c < splits; ++c) {
-    const float* pc = base + size_t(c) * (D + 2);
-    const float mc = pc[0];
-    if (mc == -INFINITY) continue;
-    const float w = __expf(mc - M);
-    L += w * pc[1];
+      for (int u = 0; u < U; ++u) {
+        const int cc = c + u * PARTS;
+        v[u] = cc < n ? base[size_t(c0 + cc) * (D + 2) + 2 + d0] : 0.f;
+      }
 #pragma unroll
-    for (int i = 0; i < D / 64; ++i) o[i] += w * pc[2 + lane + 64 * i];
+      for (int u = 0; u < U; ++u) {
+        const int cc = c + u * PARTS;
+        o += (cc < n ? wsh[cc] : 0.f) * v[u];
+      }
+    }
+    M = Mn;
+    __syncthreads();  // wsh / wred / lred reused by the next block
   }
+  ored[part][d0] = o;
+  __syncthreads();
   const float inv = 1.f / L;
+  for (int d = t; d < D; d += 256) {
+    float total = 0.f;
 #pragma unroll
-  for (int i = 0; i < D / 64; ++i) out[size_t(h) * D + lane + 64 * i] = from_f32<DT>(o[i] * inv);
+    for (int p2 = 0; p2 < PARTS; ++p2) total += ored[p2][d];
+    out[size_t(h) * D + d] = from_f32<DT>(total * inv);
+  }
 }
 
 // SwiGLU of Qwen3MLP: act = round(round(silu(gate)) * up), silu(g) = g / (1 + e^-g).
@@ -125,22 +235,31 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* __restric
   out[i] = from_f32<DT>(s * to_f32<DT>(up[i]));
 }
 
+template <int DT, int D, int KPT>
+void attn_launch(const AttnArgs& a, hipStream_t s) {
+  hipLaunchKernelGGL((attn_split_kernel<DT, D, KPT>), dim3(a.Hk, a.splits), dim3(256), 0, s, a.q, a.k, a.v,
+                     a.partial, a.Hq, a.Hk, a.Lmax, a.pos, a.splits, a.scale);
+  hipLaunchKernelGGL((attn_combine_kernel<DT, D>), dim3(a.Hq), dim3(256), 0, s, a.partial, a.out, a.splits);
+}
+
+template <int DT, int D>
+bool attn_for_kpt(int kpt, const AttnArgs& a, hipStream_t s) {
+  switch (kpt) {
+    case 1: attn_launch<DT, D, 1>(a, s); return true;
+    case 2: attn_launch<DT, D, 2>(a, s); return true;
+    case 4: attn_launch<DT, D, 4>(a, s); return true;
+  }
+  return false;
+}
+
 template <int DT>
 bool attn_for_dim(int D, const AttnArgs& a, hipStream_t s) {
-  const dim3 grid(a.Hk, a.splits);
-  if (D == 128) {
-    hipLaunchKernelGGL((attn_split_kernel<DT, 128>), grid, dim3(256), 0, s, a.q, a.k, a.v, a.partial, a.Hq, a.Hk, a.Lmax, a.pos, a.scale);
-    hipLaunchKernelGGL((attn_combine_kernel<DT, 128>), dim3(a.Hq), dim3(64), 0, s, a.partial, a.out, a.splits);
-  } else if (D == 64) {
-    hipLaunchKernelGGL((attn_split_kernel<DT, 64>), grid, dim3(256), 0, s, a.q, a.k, a.v, a.partial, a.Hq, a.Hk, a.Lmax, a.pos, a.scale);
-    hipLaunchKernelGGL((attn_combine_kernel<DT, 64>), dim3(a.Hq), dim3(64), 0, s, a.partial, a.out, a.splits);
-  } else if (D == 256) {
-    hipLaunchKernelGGL((attn_split_kernel<DT, 256>), grid, dim3(256), 0, s, a.q, a.k, a.v, a.partial, a.Hq, a.Hk, a.Lmax, a.pos, a.scale);
-    hipLaunchKernelGGL((attn_combine_kernel<DT, 256>), dim3(a.Hq), dim3(64), 0, s, a.partial, a.out, a.splits);
-  } else {
-    return false;
+  switch (D) {
+    case 64: return attn_for_kpt<DT, 64>(a.kpt, a, s);
+    case 128: return attn_for_kpt<DT, 128>(a.kpt, a, s);
+    case 256: return attn_for_kpt<DT, 256>(a.kpt, a, s);
   }
-  return true;
+  return false;
 }
 
 bool launch_decode_attention(int dt, int D, const AttnArgs& a, hipStream_t s) {
