@@ -91,6 +91,17 @@ int fx_w3_gemv(const void *x, int x_dtype, const uint8_t *planes, const void *sc
                int scale_dtype, const uint8_t *zeros, const int16_t *perm, void *workspace,
                size_t workspace_bytes, void *out, int M, int O, int K, int arithmetic,
                void *stream);
+/* Fused gate|up projection and SwiGLU of a Qwen3 MLP for one activation row.  No
+ * single reference entry point: it replaces the reference's two PackedW3Linear
+ * calls (gate_proj, up_proj; w3_lut_deployment.py:250-359) followed by HF
+ * Qwen3MLP's act_fn(gate) * up, with bit-identical results.  The payload's O rows
+ * interleave the two projections (row 2r = gate row r, row 2r+1 = up row r, in
+ * planes, scales and zero-points alike); out receives O / 2 values
+ * round(round(silu(round(g))) * round(u)) in x's dtype, each round an RNE cast
+ * to that dtype.  Structural MFMA arithmetic, one launch, no workspace. */
+int fx_w3_gemv_swiglu(const void *x, int x_dtype, const uint8_t *planes, const void *scales,
+                      int scale_dtype, const uint8_t *zeros, const int16_t *perm, void *out, int O,
+                      int K, void *stream);
 /* Structural MFMA path with an explicit tiling (benchmark sweeps): waves per
  * workgroup in {4,8}, 4-group batches kept in flight per wave in {1,2},
  * groups per K split (rounded up to a multiple of 4, clamped to the padded group

@@ -245,7 +245,7 @@ size_t mfma_workspace(int M, int O, const MfmaPlan& p) {
 int run_mfma(const void* x, int x_dtype, const uint8_t* planes, const void* scales,
              int scale_dtype, const uint8_t* zeros, const int16_t* perm, void* workspace,
              size_t workspace_bytes, void* out, int M, int O, int K, const MfmaPlan& p,
-             hipStream_t s) {
+             hipStream_t s, int swiglu = 0) {
   const int G = K / 128;
   const size_t need = mfma_workspace(M, O, p);
   if (need > 0) {
@@ -271,6 +271,7 @@ int run_mfma(const void* x, int x_dtype, const uint8_t* planes, const void* scal
     a.G = G;
     a.gps = p.gps;
     a.row_blocks = p.row_blocks;
+    a.swiglu = swiglu;
     const dim3 grid(p.row_blocks, p.splits);
     if (!fx::dispatch_mfma(x_dtype, p.tiles, p.nw, p.pd, mb, scale_dtype, a, grid, s))
       return fail(FX_EINVAL, "no MFMA kernel for waves %d prefetch %d tiles %d rows %d", p.nw,
@@ -494,7 +495,7 @@ bool two_base_config(int O, int G, int waves, int prefetch, int groups_per_split
 
 extern "C" {
 
-int fx_abi_version(void) { return 4; }
+int fx_abi_version(void) { return 5; }
 
 const char* fx_last_error(void) { return g_error; }
 
@@ -570,6 +571,20 @@ int fx_w3_gemv(const void* x, int x_dtype, const uint8_t* planes, const void* sc
                          workspace_bytes, out, M, O, K, arithmetic, s);
   return run_mfma(x, x_dtype, planes, scales, scale_dtype, zeros, perm, workspace,
                   workspace_bytes, out, M, O, K, default_mfma_plan(O, K / 128), s);
+}
+
+int fx_w3_gemv_swiglu(const void* x, int x_dtype, const uint8_t* planes, const void* scales,
+                      int scale_dtype, const uint8_t* zeros, const int16_t* perm, void* out, int O,
+                      int K, void* stream) {
+  int rc = validate_payload(x, x_dtype, planes, scales, scale_dtype, 1, O, K, FX_ARITH_STRUCTURAL);
+  if (rc) return rc;
+  if (!out) return fail(FX_EINVAL, "out must be non-null");
+  if (O % 2) return fail(FX_EINVAL, "the interleaved gate|up payload needs an even row count, got %d", O);
+  const int G = K / 128;
+  MfmaPlan p = default_mfma_plan(O, G);
+  if (p.splits > 1) p = make_mfma_plan(O, G, 8, 1, G, 1);  // the fused epilogue needs one K split
+  return run_mfma(x, x_dtype, planes, scales, scale_dtype, zeros, perm, nullptr, 0, out, 1, O, K, p,
+                  static_cast<hipStream_t>(stream), 1);
 }
 
 size_t fx_w3_gemv_config_workspace_bytes(int M, int O, int K, int waves, int prefetch,

@@ -116,6 +116,14 @@ struct BatchLoads {
   unsigned se[RT][4], ze[RT][4];  // the same as single elements when O % 4 != 0
 };
 
+// The K reduction of a workgroup always runs in the order eight waves give it:
+// "virtual wave" k accumulates batches k, k + 8, k + 16, ... in turn, and the
+// eight sums are added in k order.  A 4-wave workgroup keeps two accumulator
+// sets per wave (k = w and k = w + 4), so the result depends only on the payload
+// and x, never on the tiling (a fused q|k|v or gate|up GEMV gives the same bits
+// as the separate projections whatever waves each plan picks).
+constexpr int kSumLanes = 8;
+
 // Workgroup LDS: per wave, B operands [k-block][step][row] (16 B each), zero
 // operands [step][row] read by the lanes whose column belongs to another
 // k-block, sum of x and subnormal exponent - E per (k-block group, row), and the
@@ -126,7 +134,7 @@ struct MfmaShared {
   u32x4_t bzero[NW][16 * MB];
   float gsum[NW][4 * MB];
   int gexp[NW][4 * MB];
-  float red[NW][16 * RT * MB];
+  float red[kSumLanes][16 * RT * MB];
 };
 
 // VEC: O is a multiple of 4, so the four scales / zero-points of a lane are one
@@ -138,7 +146,7 @@ __device__ __forceinline__ void w3_mfma_body(
     MfmaShared<NW, MB, RT>& sh, const uint16_t* __restrict__ x, const int16_t* __restrict__ perm,
     const uint8_t* __restrict__ planes, const uint16_t* __restrict__ scales,
     const uint8_t* __restrict__ zeros, float* __restrict__ partial,
-    uint16_t* __restrict__ out, int O, int G, int gps, int row_blocks) {
+    uint16_t* __restrict__ out, int O, int G, int gps, int row_blocks, int swiglu) {
   auto& bstage = sh.bstage;
   auto& bzero = sh.bzero;
   auto& gsum = sh.gsum;
@@ -239,13 +247,17 @@ __device__ __forceinline__ void w3_mfma_body(
     }
   };
 
-  float acc[RT][4];
+  static_assert(kSumLanes % NW == 0, "waves per workgroup must divide the reduction lanes");
+  constexpr int VS = kSumLanes / NW;  // accumulator sets per wave
+  float acc_sets[VS][RT][4];
 #pragma unroll
-  for (int tt = 0; tt < RT; ++tt)
+  for (int v = 0; v < VS; ++v)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[tt][j] = 0.f;
+    for (int tt = 0; tt < RT; ++tt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc_sets[v][tt][j] = 0.f;
   int cur_batch = 0;
-  auto consume = [&](const BatchLoads<MB, RT>& L) __attribute__((always_inline)) {
+  auto consume = [&](const BatchLoads<MB, RT>& L, float (&acc)[RT][4]) __attribute__((always_inline)) {
     const int gb = g0 + 4 * cur_batch;
     if constexpr (PERM) {
       const bool real = gb + kb < G;
@@ -322,43 +334,69 @@ __device__ __forceinline__ void w3_mfma_body(
   };
 
   // my batches: wave, wave + NW, ...; the i-th is batch wave + i*NW
+  // (the i-th batch of this wave feeds accumulator set i % VS, virtual wave
+  // wave + (i % VS) * NW)
   const int mine = wave < nbatch ? (nbatch - wave + NW - 1) / NW : 0;
   BatchLoads<MB, RT> ring[PD];
 #pragma unroll
   for (int i = 0; i < PD; ++i)
     if (i < mine) issue(wave + i * NW, ring[i]);
-  for (int base = 0; base < mine; base += PD) {
+  constexpr int STEP = PD > VS ? PD : VS;  // PD, VS in {1, 2}: a multiple of both
+  for (int base = 0; base < mine; base += STEP) {
 #pragma unroll
-    for (int i = 0; i < PD; ++i) {
+    for (int i = 0; i < STEP; ++i) {
       if (base + i < mine) {
         cur_batch = wave + (base + i) * NW;
-        consume(ring[i]);
-        if (base + i + PD < mine) issue(wave + (base + i + PD) * NW, ring[i]);
+        consume(ring[i % PD], acc_sets[i % VS]);
+        if (base + i + PD < mine) issue(wave + (base + i + PD) * NW, ring[i % PD]);
       }
     }
   }
 
   // sum the four group slots of each activation row (lanes c = 4m .. 4m+3)
 #pragma unroll
-  for (int tt = 0; tt < RT; ++tt)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      float v = acc[tt][j];
-      v += dpp_move<kDppXor1>(v);
-      v += dpp_move<kDppXor2>(v);
-      acc[tt][j] = v;
-    }
-  if (cslot == 0 && cm < MB) {
+  for (int v = 0; v < VS; ++v) {
 #pragma unroll
     for (int tt = 0; tt < RT; ++tt)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) red[wave][(16 * tt + 4 * kb + j) * MB + cm] = acc[tt][j];
+      for (int j = 0; j < 4; ++j) {
+        float a = acc_sets[v][tt][j];
+        a += dpp_move<kDppXor1>(a);
+        a += dpp_move<kDppXor2>(a);
+        acc_sets[v][tt][j] = a;
+      }
+    if (cslot == 0 && cm < MB) {
+#pragma unroll
+      for (int tt = 0; tt < RT; ++tt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) red[wave + v * NW][(16 * tt + 4 * kb + j) * MB + cm] = acc_sets[v][tt][j];
+    }
   }
   __syncthreads();
+  if (swiglu) {
+    // rows come in (gate, up) pairs (MB = 1, one K split): each pair is rounded
+    // to the activation dtype as a separate GEMV would store it, then
+    // act = round(round(silu(g)) * u) as Qwen3MLP computes it; out holds O / 2
+    for (int i = 2 * t; i < 16 * RT; i += 2 * NW * 64) {
+      float tg = 0.f, tu = 0.f;
+#pragma unroll
+      for (int k = 0; k < kSumLanes; ++k) {
+        tg += red[k][i];
+        tu += red[k][i + 1];
+      }
+      const int orow = row0 + i;
+      if (orow < O) {
+        const float g = round_to<XDT>(tg), u = round_to<XDT>(tu);
+        const float sg = round_to<XDT>(g / (1.f + __expf(-g)));
+        out[orow / 2] = from_f32<XDT>(sg * u);
+      }
+    }
+    return;
+  }
   for (int i = t; i < 16 * RT * MB; i += NW * 64) {
     float total = 0.f;
 #pragma unroll
-    for (int wv = 0; wv < NW; ++wv) total += red[wv][i];
+    for (int k = 0; k < kSumLanes; ++k) total += red[k][i];
     const int m = i % MB;
     const int orow = row0 + i / MB;
     if (orow < O) {
@@ -376,24 +414,25 @@ __device__ __forceinline__ void w3_mfma_body(
 // multiple of 4.  Rows past O and groups past G need no masking: padded groups
 // have zero activations (so D = 0 and sum(x) = 0), and rows past O are never
 // stored.  x is [MB, 128 G] row-major; with PERM, sorted column k reads x
-// column perm[k].
+// column perm[k].  swiglu != 0 (MB = 1, one split, O even): the payload's rows
+// interleave gate and up rows, and out receives SiLU(gate) * up, O / 2 values.
 template <int NW, int PD, int MB, int RT, bool PERM, int XDT, int SDT>
 __global__ __launch_bounds__(NW * 64) void w3_mfma_kernel(
     const uint16_t* __restrict__ x, const int16_t* __restrict__ perm,
     const uint8_t* __restrict__ planes, const uint16_t* __restrict__ scales,
     const uint8_t* __restrict__ zeros, float* __restrict__ partial,
-    uint16_t* __restrict__ out, int O, int G, int gps, int row_blocks) {
+    uint16_t* __restrict__ out, int O, int G, int gps, int row_blocks, int swiglu) {
   // one scalar-load round for every argument (otherwise the pointer loads sink
   // below the first branch and add a second round trip before the first load)
   asm volatile("" ::"s"(x), "s"(perm), "s"(planes), "s"(scales), "s"(zeros), "s"(partial), "s"(out),
-               "s"(O), "s"(G), "s"(gps), "s"(row_blocks));
+               "s"(O), "s"(G), "s"(gps), "s"(row_blocks), "s"(swiglu));
   __shared__ MfmaShared<NW, MB, RT> sh;
   if ((O & 3) == 0)
     w3_mfma_body<NW, PD, MB, RT, PERM, XDT, SDT, true>(sh, x, perm, planes, scales, zeros, partial, out, O, G,
-                                                       gps, row_blocks);
+                                                       gps, row_blocks, swiglu);
   else
     w3_mfma_body<NW, PD, MB, RT, PERM, XDT, SDT, false>(sh, x, perm, planes, scales, zeros, partial, out, O,
-                                                        G, gps, row_blocks);
+                                                        G, gps, row_blocks, swiglu);
 }
 
 }  // namespace fx

@@ -15,6 +15,7 @@ struct MfmaArgs {
   uint16_t* out;
   int O, G, gps;
   int row_blocks;  // ceil(O / (16 * tiles)); the grid is (row_blocks, K splits)
+  int swiglu;      // 1: rows interleave (gate, up); out gets SiLU(gate) * up (mb 1, one split)
 };
 
 // nw waves per workgroup in {4, 8}; pd batches in flight per wave in {1, 2};

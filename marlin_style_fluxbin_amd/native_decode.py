@@ -6,10 +6,10 @@ model and its dense fallback), keep the prefix KV, decode a fixed continuation,
 capture all steps in one hipGraph, time a replay.  What differs is the step:
 instead of the HF module tree (~27 kernels per layer) each decoder layer is
 
-    add+RMSNorm -> q, k, v GEMV -> q/k norm + RoPE + KV-cache write -> attention
-    (split + combine) -> o GEMV -> add+RMSNorm -> gate, up GEMV -> SwiGLU -> down GEMV
+    add+RMSNorm -> q|k|v GEMV -> q/k norm + RoPE + KV-cache write -> attention
+    (split + combine) -> o GEMV -> add+RMSNorm -> gate|up GEMV with SwiGLU -> down GEMV
 
-(12 launches with W3 Linears), followed once per token by the final add+RMSNorm,
+(9 launches with W3 Linears), followed once per token by the final add+RMSNorm,
 the bf16 LM head (hipBLASLt) and argmax.  The arithmetic and rounding points are
 the stock HF Qwen3 modules' (RMSNorm, RoPE, SDPA with fp32 softmax, SwiGLU); W3
 Linears run the MFMA GEMV, dense Linears ``torch.matmul`` (the bf16 arm).
@@ -95,6 +95,56 @@ class _FusedLinear:
         self.call(x, out)
 
 
+def interleave_gate_up(gate: dict, up: dict) -> dict:
+    """W3 payload whose rows alternate gate row r and up row r (planes, scales and
+    zero-points alike), the layout ``fx_w3_gemv_swiglu`` reads."""
+    def pair(a, b, dim):
+        return torch.stack([a, b], dim=dim + 1).flatten(dim, dim + 1).contiguous()
+
+    fused = {"planes": pair(gate["planes"], up["planes"], 2), "scales": pair(gate["scales"], up["scales"], 1),
+             "perm": gate["perm"]}
+    if "zeros" in gate:
+        fused["zeros"] = pair(gate["zeros"], up["zeros"], 1)
+    return fused
+
+
+class _GateUpSwiGLU:
+    """gate_proj, up_proj and SiLU(gate) * up of a Qwen3 MLP as one launch
+    (``fx_w3_gemv_swiglu`` over the row-interleaved payload), bit-identical to the
+    two GEMVs followed by the SwiGLU kernel.  ``None`` from :meth:`build` unless
+    both Linears are structural W3 with matching K, scale dtype, zero-point
+    presence and column permutation, equal widths and no bias."""
+
+    def __init__(self, layout, width):
+        self.layout = layout
+        self.width = width
+        self.lib = _lib.library()
+        perm = layout["perm"]
+        identity = torch.equal(perm.long(), torch.arange(perm.numel(), device=perm.device))
+        self.perm_ptr = None if identity else perm.data_ptr()
+        self.zeros_ptr = _lib.ptr(layout.get("zeros"))
+        self.scale_code = _lib.dtype_code(layout["scales"].dtype)
+        self.in_features = perm.numel()
+
+    @staticmethod
+    def build(gate, up):
+        if not (isinstance(gate, PackedW3Linear) and isinstance(up, PackedW3Linear)):
+            return None
+        g, u = gate.layout(), up.layout()
+        if (gate.arithmetic != "structural" or up.arithmetic != "structural" or gate.bias is not None
+                or up.bias is not None or gate.in_features != up.in_features
+                or gate.out_features != up.out_features or g["scales"].dtype != u["scales"].dtype
+                or ("zeros" in g) != ("zeros" in u) or not torch.equal(g["perm"], u["perm"])):
+            return None
+        return _GateUpSwiGLU(interleave_gate_up(g, u), gate.out_features)
+
+    def __call__(self, x, out):
+        _lib.check(self.lib.fx_w3_gemv_swiglu(
+            x.data_ptr(), _lib.dtype_code(x.dtype), self.layout["planes"].data_ptr(),
+            self.layout["scales"].data_ptr(), self.scale_code, self.zeros_ptr, self.perm_ptr, out.data_ptr(),
+            2 * self.width, self.in_features, _lib.stream_handle(x.device)), "fx_w3_gemv_swiglu")
+
+
 class NativeDecodeSession:
     def __init__(self, model, input_ids: torch.Tensor, forced_tokens: torch.Tensor):
         from transformers import StaticCache
@@ -150,7 +200,11 @@ class NativeDecodeSession:
         self.lin = [{name: _Linear(block.get_submodule(name)) for name in _ATTN + _MLP} for block in self.layers]
         # q|k|v and gate|up as one GEMV each where the payloads allow it
         self.qkv = [_FusedLinear.build([b.get_submodule(n) for n in _ATTN[:3]]) for b in self.layers]
-        self.gate_up = [_FusedLinear.build([b.get_submodule(n) for n in _MLP[:2]]) for b in self.layers]
+        # gate|up + SwiGLU as one launch where both are structural W3; else gate|up
+        # (fused where possible) and the SwiGLU kernel
+        self.swiglu = [_GateUpSwiGLU.build(*(b.get_submodule(n) for n in _MLP[:2])) for b in self.layers]
+        self.gate_up = [None if f is not None else _FusedLinear.build([b.get_submodule(n) for n in _MLP[:2]])
+                        for f, b in zip(self.swiglu, self.layers)]
         self.in_norm = [b.input_layernorm.weight for b in self.layers]
         self.post_norm = [b.post_attention_layernorm.weight for b in self.layers]
         self.q_norm = [b.self_attn.q_norm.weight for b in self.layers]
@@ -223,12 +277,15 @@ class NativeDecodeSession:
             lin["self_attn.o_proj"](self.attn, self.o)
             add_rms_norm(self.o, self.residual, self.post_norm[l], self.eps, out=self.normed,
                          residual_out=self.residual)
-            if self.gate_up[l] is not None:
-                self.gate_up[l](self.normed, self.gate_up_out)
+            if self.swiglu[l] is not None:
+                self.swiglu[l](self.normed, self.act)
             else:
-                lin["mlp.gate_proj"](self.normed, self.gate)
-                lin["mlp.up_proj"](self.normed, self.up)
-            self._silu_mul()
+                if self.gate_up[l] is not None:
+                    self.gate_up[l](self.normed, self.gate_up_out)
+                else:
+                    lin["mlp.gate_proj"](self.normed, self.gate)
+                    lin["mlp.up_proj"](self.normed, self.up)
+                self._silu_mul()
             lin["mlp.down_proj"](self.act, self.down)
         add_rms_norm(self.down, self.residual, self.final_norm, self.eps, out=self.normed,
                      residual_out=self.residual)

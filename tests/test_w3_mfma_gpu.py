@@ -91,3 +91,24 @@ def test_mfma_zero_activation(gpu):
     out = torch.full((1, 64), float("nan"), dtype=torch.bfloat16, device=gpu)
     _run_config(dl, torch.zeros(1, 256, dtype=torch.bfloat16, device=gpu), out, 4, 1, 4, 2)
     assert torch.equal(out, torch.zeros_like(out))
+
+
+@pytest.mark.parametrize("o,k", [(300, 2048), (96, 12288), (17, 640)])
+@pytest.mark.parametrize("m", [1, 3])
+def test_mfma_result_independent_of_waves_and_prefetch(gpu, o, k, m):
+    """With one K split the K reduction always runs in the eight-wave order, so
+    every (waves, prefetch, row tiles) tiling gives bitwise-equal outputs; a
+    fused q|k|v or gate|up payload therefore reproduces the separate projections
+    whatever plan each shape gets."""
+    codes, scales, zeros, perm = config_codes(o, k, seed=o + m, zeros=True, scale_dtype=torch.float16,
+                                              permute=True)
+    dl = {n: t.to(gpu) for n, t in layout_from_codes(codes, scales, zeros, perm).items()}
+    x = torch.randn(m, k, generator=torch.Generator().manual_seed(k)).to(torch.bfloat16).to(gpu)
+    padded = (k // 128 + 3) // 4 * 4
+    outs = []
+    for waves, prefetch, tiles in [(8, 1, 1), (4, 1, 1), (4, 2, 1), (8, 2, 2), (4, 1, 2)]:
+        out = torch.full((m, o), float("nan"), dtype=torch.bfloat16, device=gpu)
+        _run_config(dl, x, out, waves, prefetch, padded, tiles)
+        outs.append(out)
+    for out in outs[1:]:
+        assert torch.equal(out, outs[0])
