@@ -92,6 +92,32 @@ __device__ __forceinline__ float row16_max(float v) {
 
 typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
 
+// Sum over the 64 lanes of a wave (DPP within rows of 16, then lanes 16 and 32
+// apart); every lane gets the same bits.
+__device__ __forceinline__ float wave_total(float v) {
+  v = row16_sum(v);
+  v += __shfl_xor(v, 16, 64);
+  v += __shfl_xor(v, 32, 64);
+  return v;
+}
+
+// RMSNorm reductions run over 512-element batches: lane l of the wave serving
+// batch b holds elements [8 (64 b + l), +8), sums their squares with fused
+// multiply-adds in element order, and the batch total is wave_total of that.
+// The batch totals are added in batch order.
+constexpr int kNormBatch = 512;
+template <int DT>
+__device__ __forceinline__ float sum_sq8(const u32x4_t& v) {
+  float ss = 0.f;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const float lo = to_f32<DT>(uint16_t(v[w])), hi = to_f32<DT>(uint16_t(v[w] >> 16));
+    ss = fmaf(lo, lo, ss);
+    ss = fmaf(hi, hi, ss);
+  }
+  return ss;
+}
+
 // Buffer resource over [base, base + bytes): loads at offsets past the end
 // return zero instead of touching memory.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_resource(const void* base, size_t bytes) {

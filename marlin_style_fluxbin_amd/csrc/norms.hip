@@ -21,38 +21,98 @@ typedef unsigned u32x4n_t __attribute__((ext_vector_type(4)));
 template <int DT>
 __device__ __forceinline__ float rnd(float v) { return round_to<DT>(v); }
 
-// Sum over the 64 lanes of a wave; every lane gets the total.
-__device__ __forceinline__ float wave_total(float v) {
-  v = row16_sum(v);
-  v += __shfl_xor(v, 16, 64);
-  v += __shfl_xor(v, 32, 64);
-  return v;
-}
-
 // rows x hidden, hidden % 8 == 0.  TPR threads per row (64 or 256), 256 threads
-// per block.  Pass 1 forms s (and writes residual_out), accumulates sum(s^2);
-// pass 2 re-reads s (its own chunks, so in-place calls are safe) and writes y.
+// per block.  s = round(x + residual) (written to residual_out) or x; the sum of
+// s^2 in the shared 512-element batch order (wave w of a row takes batches
+// w, w + TPR/64, ...; lanes past the row read zeros); y = round(w * round(s * inv)).
+// When a lane's chunks fit in registers (hidden <= kNormRegChunks * 512 * TPR/64)
+// every load -- x, residual and weight -- is issued before the first use and y
+// is formed from registers: one global round trip.  Longer rows re-read s (their
+// own chunks, so in-place calls are safe).
+constexpr int kMaxNormBatches = (1 << 20) / kNormBatch;
+constexpr int kNormRegChunks = 4;
 template <int DT, int TPR>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* __restrict__ x,
                                                       const uint16_t* __restrict__ residual,
                                                       const uint16_t* __restrict__ weight,
                                                       uint16_t* out, uint16_t* residual_out,
                                                       int rows, int hidden, float eps) {
-  constexpr int kRowsPerBlock = 256 / TPR;
-  __shared__ float partial[kRowsPerBlock][TPR / 64];
+  asm volatile("" ::"s"(x), "s"(residual), "s"(weight), "s"(out), "s"(residual_out), "s"(rows), "s"(hidden),
+               "s"(eps));
+  constexpr int kRowsPerBlock = 256 / TPR, kWavesPerRow = TPR / 64;
+  __shared__ float bsum[kWavesPerRow > 1 ? kMaxNormBatches : 1];
   const int t = threadIdx.x;
   const int local = t / TPR, tl = t % TPR;
   const int row = blockIdx.x * kRowsPerBlock + local;
   const bool live = row < rows;
   const int chunks = hidden / 8;
+  const int nb = (hidden + kNormBatch - 1) / kNormBatch;
+  const int wr = tl / 64, lane = tl & 63;
   const size_t base = size_t(live ? row : 0) * hidden;
+
+  if (nb <= kNormRegChunks * kWavesPerRow) {
+    const auto rx = buffer_resource(x + base, size_t(hidden) * 2);
+    const auto rr = buffer_resource(residual ? residual + base : x, residual ? size_t(hidden) * 2 : 0);
+    const auto rw = buffer_resource(weight, size_t(hidden) * 2);
+    u32x4_t sv[kNormRegChunks], wv[kNormRegChunks], rv[kNormRegChunks];
+    bool ok[kNormRegChunks];
+#pragma unroll
+    for (int q = 0; q < kNormRegChunks; ++q) {
+      const int c = 64 * (wr + q * kWavesPerRow) + lane;
+      ok[q] = live && c < chunks;
+      const int off = ok[q] ? c * 16 : kOutOfRange;
+      sv[q] = load_b128(rx, off, 0);
+      rv[q] = load_b128(rr, off, 0);
+      wv[q] = load_b128(rw, off, 0);
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int q = 0; q < kNormRegChunks; ++q) {
+      const int b = wr + q * kWavesPerRow;
+      if (b >= nb) break;  // wave-uniform
+      if (residual) {
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const float lo = rnd<DT>(to_f32<DT>(uint16_t(sv[q][w])) + to_f32<DT>(uint16_t(rv[q][w])));
+          const float hi = rnd<DT>(to_f32<DT>(uint16_t(sv[q][w] >> 16)) + to_f32<DT>(uint16_t(rv[q][w] >> 16)));
+          sv[q][w] = unsigned(from_f32<DT>(lo)) | (unsigned(from_f32<DT>(hi)) << 16);
+        }
+        if (ok[q]) *reinterpret_cast<u32x4_t*>(residual_out + base + 8 * (64 * b + lane)) = sv[q];
+      }
+      const float bs = wave_total(sum_sq8<DT>(sv[q]));
+      if constexpr (kWavesPerRow == 1) ss += bs;  // batch order
+      else if (lane == 0) bsum[b] = bs;
+    }
+    if constexpr (kWavesPerRow > 1) {
+      __syncthreads();
+      for (int b = 0; b < nb; ++b) ss += bsum[b];
+    }
+    const float inv = rsqrtf(ss / float(hidden) + eps);
+#pragma unroll
+    for (int q = 0; q < kNormRegChunks; ++q) {
+      if (!ok[q]) continue;
+      u32x4_t yv;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const float n0 = rnd<DT>(to_f32<DT>(uint16_t(sv[q][w])) * inv);
+        const float n1 = rnd<DT>(to_f32<DT>(uint16_t(sv[q][w] >> 16)) * inv);
+        const float y0 = to_f32<DT>(uint16_t(wv[q][w])) * n0;
+        const float y1 = to_f32<DT>(uint16_t(wv[q][w] >> 16)) * n1;
+        yv[w] = unsigned(from_f32<DT>(y0)) | (unsigned(from_f32<DT>(y1)) << 16);
+      }
+      *reinterpret_cast<u32x4_t*>(out + base + 8 * (64 * (wr + q * kWavesPerRow) + lane)) = yv;
+    }
+    return;
+  }
+
   // with a residual, pass 2 reads the rounded sum back from residual_out
   const uint16_t* src = residual ? residual_out : x;
-
   float ss = 0.f;
-  if (live) {
-    for (int c = tl; c < chunks; c += TPR) {
-      u32x4n_t xv = *reinterpret_cast<const u32x4n_t*>(x + base + 8 * c);
+  for (int b = wr; b < nb; b += kWavesPerRow) {
+    const int c = 64 * b + lane;
+    u32x4n_t xv = {0u, 0u, 0u, 0u};
+    if (live && c < chunks) {
+      xv = *reinterpret_cast<const u32x4n_t*>(x + base + 8 * c);
       if (residual) {
         const u32x4n_t rv = *reinterpret_cast<const u32x4n_t*>(residual + base + 8 * c);
         u32x4n_t sv;
@@ -65,20 +125,14 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* __restrict
         *reinterpret_cast<u32x4n_t*>(residual_out + base + 8 * c) = sv;
         xv = sv;
       }
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        const float lo = to_f32<DT>(uint16_t(xv[w])), hi = to_f32<DT>(uint16_t(xv[w] >> 16));
-        ss += lo * lo + hi * hi;
-      }
     }
+    const float bs = wave_total(sum_sq8<DT>(__builtin_bit_cast(u32x4_t, xv)));
+    if constexpr (kWavesPerRow == 1) ss += bs;  // batch order
+    else if (lane == 0) bsum[b] = bs;
   }
-  ss = wave_total(ss);
-  if constexpr (TPR > 64) {
-    if ((tl & 63) == 0) partial[local][tl >> 6] = ss;
+  if constexpr (kWavesPerRow > 1) {
     __syncthreads();
-    ss = 0.f;
-#pragma unroll
-    for (int i = 0; i < TPR / 64; ++i) ss += partial[local][i];
+    for (int b = 0; b < nb; ++b) ss += bsum[b];
   }
   if (!live) return;
   const float inv = rsqrtf(ss / float(hidden) + eps);
