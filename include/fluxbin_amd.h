@@ -173,6 +173,22 @@ int fx_decode_attention(const void *q, const void *k_cache, const void *v_cache,
                         size_t workspace_bytes, void *out, int n_q_heads, int n_kv_heads,
                         int max_len, int head_dim, int position, float scale, int dtype,
                         void *stream);
+/*
+ * Decode attention with the per-head q/k RMSNorm + RoPE folded in: no single
+ * reference entry point; it replaces HF Qwen3Attention's q_norm / k_norm,
+ * apply_rotary_pos_emb (stock or the reference's fused_apply_rotary_pos_emb,
+ * fused_modules.py:66-85), the KV-cache update at `position` and the attention
+ * of fx_decode_attention.  q [Hq, D], k and v [Hk, D] are the raw projections of
+ * the current token; q_norm_weight / k_norm_weight [D]; cos / sin the RoPE rows
+ * [D] of `position`.  The key (normalised, rotated) and value of `position` are
+ * written into k_cache / v_cache and used; rounding points as fx_head_norm_rope
+ * (the per-head sum of squares may differ from it in the last bit).
+ */
+int fx_decode_attention_rope(const void *q, const void *k, const void *v, const void *q_norm_weight,
+                             const void *k_norm_weight, const void *cos, const void *sin, float eps,
+                             int rope_mode, void *k_cache, void *v_cache, void *workspace,
+                             size_t workspace_bytes, void *out, int n_q_heads, int n_kv_heads, int max_len,
+                             int head_dim, int position, float scale, int dtype, void *stream);
 
 /*
  * Qwen3MLP activation (transformers modeling_qwen3.py, run by the reference's

@@ -495,7 +495,7 @@ bool two_base_config(int O, int G, int waves, int prefetch, int groups_per_split
 
 extern "C" {
 
-int fx_abi_version(void) { return 5; }
+int fx_abi_version(void) { return 6; }
 
 const char* fx_last_error(void) { return g_error; }
 
@@ -724,10 +724,11 @@ size_t fx_decode_attention_workspace_bytes(int n_q_heads, int max_len, int head_
   return size_t(n_q_heads) * splits * (size_t(head_dim) + 2) * sizeof(float);
 }
 
-int fx_decode_attention(const void* q, const void* k_cache, const void* v_cache, void* workspace,
-                        size_t workspace_bytes, void* out, int n_q_heads, int n_kv_heads,
-                        int max_len, int head_dim, int position, float scale, int dtype,
-                        void* stream) {
+namespace {
+int decode_attention(const void* q, const void* k_cache, const void* v_cache, void* workspace,
+                     size_t workspace_bytes, void* out, int n_q_heads, int n_kv_heads, int max_len,
+                     int head_dim, int position, float scale, int dtype, void* stream,
+                     const fx::AttnPre& pre) {
   if (!q || !k_cache || !v_cache || !out) return fail(FX_EINVAL, "q, caches and out must be non-null");
   if (!is_half_dtype(dtype)) return fail(FX_EINVAL, "dtype must be fp16 or bf16");
   if (head_dim != 64 && head_dim != 128 && head_dim != 256)
@@ -742,7 +743,7 @@ int fx_decode_attention(const void* q, const void* k_cache, const void* v_cache,
   const size_t need = fx_decode_attention_workspace_bytes(n_q_heads, max_len, head_dim);
   if (!workspace || workspace_bytes < need)
     return fail(FX_EINVAL, "attention workspace needs %zu bytes, got %zu", need, workspace_bytes);
-  fx::AttnArgs a;
+  fx::AttnArgs a{};
   a.q = static_cast<const uint16_t*>(q);
   a.k = static_cast<const uint16_t*>(k_cache);
   a.v = static_cast<const uint16_t*>(v_cache);
@@ -767,8 +768,39 @@ int fx_decode_attention(const void* q, const void* k_cache, const void* v_cache,
   a.splits = (n + keys - 1) / keys;
   if (a.splits > 65535) return fail(FX_EINVAL, "position %d needs %d key splits (at most 65535)", position, a.splits);
   a.scale = scale;
+  a.pre = pre;
   fx::launch_decode_attention(dtype, head_dim, a, static_cast<hipStream_t>(stream));
   return check_launch("attn_split_kernel");
+}
+
+}  // namespace
+
+int fx_decode_attention(const void* q, const void* k_cache, const void* v_cache, void* workspace,
+                        size_t workspace_bytes, void* out, int n_q_heads, int n_kv_heads,
+                        int max_len, int head_dim, int position, float scale, int dtype,
+                        void* stream) {
+  return decode_attention(q, k_cache, v_cache, workspace, workspace_bytes, out, n_q_heads, n_kv_heads, max_len,
+                          head_dim, position, scale, dtype, stream, fx::AttnPre{});
+}
+
+int fx_decode_attention_rope(const void* q, const void* k, const void* v, const void* q_norm_weight,
+                             const void* k_norm_weight, const void* cos, const void* sin, float eps,
+                             int rope_mode, void* k_cache, void* v_cache, void* workspace,
+                             size_t workspace_bytes, void* out, int n_q_heads, int n_kv_heads, int max_len,
+                             int head_dim, int position, float scale, int dtype, void* stream) {
+  if (!k || !v || !q_norm_weight || !k_norm_weight || !cos || !sin)
+    return fail(FX_EINVAL, "raw k, v, norm weights, cos and sin must be non-null");
+  if (rope_mode != FX_ROPE_STOCK && rope_mode != FX_ROPE_FUSED)
+    return fail(FX_EINVAL, "rope_mode must be FX_ROPE_STOCK or FX_ROPE_FUSED");
+  const void* vec[6] = {k, v, q_norm_weight, k_norm_weight, cos, sin};
+  for (const void* p : vec)
+    if (reinterpret_cast<uintptr_t>(p) % 16 != 0)
+      return fail(FX_EINVAL, "raw k, v, norm weights, cos and sin must be 16-byte aligned");
+  fx::AttnPre pre{static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),
+                  static_cast<const uint16_t*>(q_norm_weight), static_cast<const uint16_t*>(k_norm_weight),
+                  static_cast<const uint16_t*>(cos), static_cast<const uint16_t*>(sin), eps, rope_mode};
+  return decode_attention(q, k_cache, v_cache, workspace, workspace_bytes, out, n_q_heads, n_kv_heads, max_len,
+                          head_dim, position, scale, dtype, stream, pre);
 }
 
 int fx_silu_mul(const void* gate, const void* up, void* out, int n, int dtype, void* stream) {

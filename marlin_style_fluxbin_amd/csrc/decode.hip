@@ -9,12 +9,14 @@
 // once to the activation dtype.  KV cache layout [Hk, Lmax, D].
 #include "common.h"
 #include "decode_launch.h"
+#include "norms_launch.h"
 
 namespace fx {
 
 // Query heads scored per pass over a KV head's chunk (the chunk's K and V stay
 // in registers across passes).
 constexpr int kAttnHeadsPerPass = 4;
+constexpr int kDppRowRor8 = 0x128;  // lane i <- lane (i + 8) mod 16 within each row
 
 // Sum over the DB lanes (8, 16 or 32) that hold one key row; every lane of the
 // group receives the same bits.
@@ -38,18 +40,63 @@ __device__ __forceinline__ float key_row_sum(float v) {
 // the DB lanes of the row, chunk max over the workgroup, p = e^(s - m),
 // l = sum p, o = sum p v per thread, reduced over the key rows through LDS.
 // partial[(h * splits + chunk) * (D + 2)] = {m, l, o[0..D)}.
-template <int DT, int D, int KPT>
+// PRE: q is the raw projection; each query head is normalised (q_norm) and
+// rotated before scoring, and the key and value of position pos are formed here
+// from the raw projections (k_norm, RoPE; v as is) -- by the workgroup whose
+// chunk holds pos, which also writes them into the caches.  Rounding points of
+// head_norm_rope_kernel: y = round(w * round(x * inv)), stock RoPE
+// round(round(y * cos) + round(rotate_half(y) * sin)) (fused: the second term
+// unrounded); the head's sum of squares is taken over the DB lanes of a row.
+template <int DT, int D>
+__device__ __forceinline__ u32x4_t head_norm_rope8(const u32x4_t& x, const u32x4_t& w, const u32x4_t& cs,
+                                                  const u32x4_t& sn, bool lower, float eps, int rope_mode) {
+  constexpr int DB = D / 8;
+  const float inv = rsqrtf(key_row_sum<DB>(sum_sq8<DT>(x)) / float(D) + eps);
+  float y[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float xv = to_f32<DT>(uint16_t(x[e >> 1] >> (16 * (e & 1))));
+    const float wv = to_f32<DT>(uint16_t(w[e >> 1] >> (16 * (e & 1))));
+    y[e] = round_to<DT>(wv * round_to<DT>(xv * inv));
+  }
+  u32x4_t o;
+#pragma unroll
+  for (int e = 0; e < 8; e += 2) {
+    float r[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      // rotate_half(y) = (-y[D/2:], y[:D/2]): the partner dim sits DB/2 lanes away
+      // (DB = 16: a DPP rotate by 8 within the row)
+      float partner;
+      if constexpr (DB == 16) partner = dpp_move<kDppRowRor8>(y[e + h]);
+      else partner = __shfl_xor(y[e + h], DB / 2, 64);
+      const float c = to_f32<DT>(uint16_t(cs[(e + h) >> 1] >> (16 * ((e + h) & 1))));
+      const float sv = to_f32<DT>(uint16_t(sn[(e + h) >> 1] >> (16 * ((e + h) & 1))));
+      float rot = (lower ? -partner : partner) * sv;
+      if (rope_mode == kRopeStock) rot = round_to<DT>(rot);
+      r[h] = round_to<DT>(y[e + h] * c) + rot;
+    }
+    o[e >> 1] = unsigned(from_f32<DT>(r[0])) | (unsigned(from_f32<DT>(r[1])) << 16);
+  }
+  return o;
+}
+
+template <int DT, int D, int KPT, bool PRE>
 __global__ __launch_bounds__(256) void attn_split_kernel(const uint16_t* __restrict__ q,
-                                                         const uint16_t* __restrict__ kc,
-                                                         const uint16_t* __restrict__ vc,
+                                                         const uint16_t* kc, const uint16_t* vc,
                                                          float* __restrict__ partial, int Hq, int Hk,
-                                                         int Lmax, int pos, int splits, float scale) {
+                                                         int Lmax, int pos, int splits, float scale,
+                                                         AttnPre pre) {
   asm volatile("" ::"s"(q), "s"(kc), "s"(vc), "s"(partial), "s"(Hq), "s"(Hk), "s"(Lmax), "s"(pos),
                "s"(splits), "s"(scale));
+  if constexpr (PRE)
+    asm volatile("" ::"s"(pre.k_raw), "s"(pre.v_raw), "s"(pre.q_weight), "s"(pre.k_weight), "s"(pre.cos),
+                 "s"(pre.sin), "s"(pre.eps), "s"(pre.rope_mode));
   constexpr int DB = D / 8, KS = 256 / DB, HB = kAttnHeadsPerPass;
   __shared__ float red_o[KS][HB][D];
   __shared__ float red_l[KS][HB];
   __shared__ float red_m[4][HB];
+  __shared__ u32x4_t qsh[PRE ? 4 : 1][HB][DB];  // PRE: normalised queries of each wave
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int db = t % DB, ks = t / DB;
   const int g = blockIdx.x, chunk = blockIdx.y;
@@ -59,11 +106,28 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const uint16_t* __restr
   const auto rk = buffer_resource(kc + size_t(g) * Lmax * D, size_t(Lmax) * D * 2);
   const auto rv = buffer_resource(vc + size_t(g) * Lmax * D, size_t(Lmax) * D * 2);
 
-  // ---- loads: first pass's queries, then the chunk's keys and values
+  // ---- loads: first pass's queries (PRE: with the norm weights, RoPE rows and,
+  // in the chunk holding pos, the raw key and value of pos), then the chunk's
+  // keys and values -- loads complete in issue order, so the query (and pos
+  // key) normalisation overlaps the K/V stream
   u32x4_t qr[HB], kr[KPT], vr[KPT];
   bool live[KPT];
+  const bool lower = db < DB / 2;
+  const bool has_pos = first <= pos && pos < first + KS * KPT;  // workgroup-uniform
+  u32x4_t qw, cs, sn, kraw, vraw, kw;
 #pragma unroll
   for (int hh = 0; hh < HB; ++hh) qr[hh] = load_b128(rq, hh < G ? (hh * D + 8 * db) * 2 : kOutOfRange, 0);
+  if constexpr (PRE) {
+    const auto rd = [&](const uint16_t* p, bool on) {
+      return load_b128(buffer_resource(p, D * 2), on ? 16 * db : kOutOfRange, 0);
+    };
+    qw = rd(pre.q_weight, true);
+    cs = rd(pre.cos, true);
+    sn = rd(pre.sin, true);
+    kraw = rd(pre.k_raw + size_t(g) * D, has_pos);
+    vraw = rd(pre.v_raw + size_t(g) * D, has_pos);
+    kw = rd(pre.k_weight, has_pos);
+  }
 #pragma unroll
   for (int i = 0; i < KPT; ++i) {
     const int j = first + ks + KS * i;
@@ -74,6 +138,44 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const uint16_t* __restr
   for (int i = 0; i < KPT; ++i) {
     const int j = first + ks + KS * i;
     vr[i] = load_b128(rv, live[i] ? (j * D + 8 * db) * 2 : kOutOfRange, 0);
+  }
+  // PRE: the rows of a wave split the pass's query heads (row r of the wave
+  // normalises heads r, r + rows, ...) and share them through the wave's LDS slot
+  constexpr int kRows = 64 / DB;
+  auto normalise_queries = [&]() __attribute__((always_inline)) {
+    const int row = lane / DB;
+#pragma unroll
+    for (int hh = 0; hh < HB; hh += kRows) {
+      const int mine_h = hh + row;
+      u32x4_t sel = qr[0];
+#pragma unroll
+      for (int c = 1; c < HB; ++c)
+        if (c == mine_h) sel = qr[c];
+      const u32x4_t o = head_norm_rope8<DT, D>(sel, qw, cs, sn, lower, pre.eps, pre.rope_mode);
+      if (mine_h < HB) qsh[wave][mine_h][db] = o;
+    }
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int hh = 0; hh < HB; ++hh) qr[hh] = qsh[wave][hh][db];
+    __builtin_amdgcn_wave_barrier();
+  };
+  if constexpr (PRE) {
+    // first pass's queries and the pos key: normalised and rotated while the
+    // chunk's K/V rows stream in
+    normalise_queries();
+    if (has_pos) {
+      const u32x4_t kpos = head_norm_rope8<DT, D>(kraw, kw, cs, sn, lower, pre.eps, pre.rope_mode);
+#pragma unroll
+      for (int i = 0; i < KPT; ++i) {
+        if (first + ks + KS * i == pos) {
+          kr[i] = kpos;
+          vr[i] = vraw;
+          const size_t at = (size_t(g) * Lmax + pos) * D + 8 * db;
+          *reinterpret_cast<u32x4_t*>(const_cast<uint16_t*>(kc) + at) = kpos;
+          *reinterpret_cast<u32x4_t*>(const_cast<uint16_t*>(vc) + at) = vraw;
+        }
+      }
+    }
   }
 
   for (int h0 = 0; h0 < G; h0 += HB) {
@@ -87,6 +189,9 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const uint16_t* __restr
     for (int i = 0; i < KPT; ++i)
 #pragma unroll
       for (int e = 0; e < 8; ++e) kf[i][e] = to_f32<DT>(uint16_t(kr[i][e >> 1] >> (16 * (e & 1))));
+    if constexpr (PRE) {
+      if (h0 > 0) normalise_queries();
+    }
     float s[HB][KPT];
     float mt[HB];
 #pragma unroll
@@ -237,8 +342,12 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* __restric
 
 template <int DT, int D, int KPT>
 void attn_launch(const AttnArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL((attn_split_kernel<DT, D, KPT>), dim3(a.Hk, a.splits), dim3(256), 0, s, a.q, a.k, a.v,
-                     a.partial, a.Hq, a.Hk, a.Lmax, a.pos, a.splits, a.scale);
+  if (a.pre.k_raw)
+    hipLaunchKernelGGL((attn_split_kernel<DT, D, KPT, true>), dim3(a.Hk, a.splits), dim3(256), 0, s, a.q, a.k,
+                       a.v, a.partial, a.Hq, a.Hk, a.Lmax, a.pos, a.splits, a.scale, a.pre);
+  else
+    hipLaunchKernelGGL((attn_split_kernel<DT, D, KPT, false>), dim3(a.Hk, a.splits), dim3(256), 0, s, a.q, a.k,
+                       a.v, a.partial, a.Hq, a.Hk, a.Lmax, a.pos, a.splits, a.scale, a.pre);
   hipLaunchKernelGGL((attn_combine_kernel<DT, D>), dim3(a.Hq), dim3(256), 0, s, a.partial, a.out, a.splits);
 }
 

@@ -4,6 +4,20 @@
 
 namespace fx {
 
+// Per-head q/k RMSNorm + RoPE folded into the attention (q is then the raw
+// projection); k_raw null: q is already normalised and rotated and the caches
+// already hold position pos.
+struct AttnPre {
+  const uint16_t* k_raw;     // [Hk, D] raw key projection of position pos
+  const uint16_t* v_raw;     // [Hk, D] value of position pos
+  const uint16_t* q_weight;  // [D] q_norm weight
+  const uint16_t* k_weight;  // [D] k_norm weight
+  const uint16_t* cos;       // [D] RoPE row of position pos
+  const uint16_t* sin;
+  float eps;
+  int rope_mode;             // 1 stock, 2 fused (addcmul)
+};
+
 struct AttnArgs {
   const uint16_t* q;   // [Hq, D]
   const uint16_t* k;   // [Hk, Lmax, D]
@@ -13,6 +27,7 @@ struct AttnArgs {
   int Hq, Hk, Lmax, pos;
   int kpt, splits;     // keys per thread (1, 2, 4); splits = ceil((pos + 1) / (keys per workgroup))
   float scale;
+  AttnPre pre;
 };
 
 // Keys one attention workgroup covers: 256 / (D / 8) key rows times keys per thread.

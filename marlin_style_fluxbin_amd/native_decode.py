@@ -6,10 +6,11 @@ model and its dense fallback), keep the prefix KV, decode a fixed continuation,
 capture all steps in one hipGraph, time a replay.  What differs is the step:
 instead of the HF module tree (~27 kernels per layer) each decoder layer is
 
-    add+RMSNorm -> q|k|v GEMV -> q/k norm + RoPE + KV-cache write -> attention
-    (split + combine) -> o GEMV -> add+RMSNorm -> gate|up GEMV with SwiGLU -> down GEMV
+    add+RMSNorm -> q|k|v GEMV -> attention with q/k norm, RoPE and the KV-cache
+    write folded in (split + combine) -> o GEMV -> add+RMSNorm -> gate|up GEMV
+    with SwiGLU -> down GEMV
 
-(9 launches with W3 Linears), followed once per token by the final add+RMSNorm,
+(8 launches with W3 Linears), followed once per token by the final add+RMSNorm,
 the bf16 LM head (hipBLASLt) and argmax.  The arithmetic and rounding points are
 the stock HF Qwen3 modules' (RMSNorm, RoPE, SDPA with fp32 softmax, SwiGLU); W3
 Linears run the MFMA GEMV, dense Linears ``torch.matmul`` (the bf16 arm).
@@ -22,7 +23,7 @@ import time
 import torch
 
 from . import _lib
-from .fused_modules import add_rms_norm, head_norm_rope
+from .fused_modules import add_rms_norm
 from .static_decode import graph_kernel_count
 from .w3_lut_deployment import PackedW3Linear, W3Gemv
 
@@ -222,7 +223,7 @@ class NativeDecodeSession:
         self.q, self.k, self.v = self.qkv_out[:, :qd], self.qkv_out[:, qd:qd + kd], self.qkv_out[:, qd + kd:]
         self.gate_up_out = buf(2 * inter)
         self.gate, self.up = self.gate_up_out[:, :inter], self.gate_up_out[:, inter:]
-        self.q_rot, self.attn = buf(qd), buf(qd)
+        self.attn = buf(qd)
         self.o, self.act, self.down = buf(self.hidden), buf(inter), buf(self.hidden)
         self.logits = torch.empty((self.steps, cfg.vocab_size), dtype=dtype, device=self.device)
         self.predictions = torch.empty((self.steps, 1), dtype=torch.int64, device=self.device)
@@ -236,12 +237,16 @@ class NativeDecodeSession:
 
     # -- one token -------------------------------------------------------------------
     def _attention(self, layer, pos):
+        """q/k RMSNorm + RoPE, the KV-cache write of position ``pos`` and the
+        attention, from the raw q|k|v projections (one split + one combine launch)."""
         lib = self.lib
-        _lib.check(lib.fx_decode_attention(
-            self.q_rot.data_ptr(), self.k_cache[layer].data_ptr(), self.v_cache[layer].data_ptr(),
+        _lib.check(lib.fx_decode_attention_rope(
+            self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), self.q_norm[layer].data_ptr(),
+            self.k_norm[layer].data_ptr(), self.cos[pos].data_ptr(), self.sin[pos].data_ptr(), self.eps,
+            _lib.ROPE_STOCK, self.k_cache[layer].data_ptr(), self.v_cache[layer].data_ptr(),
             self.attn_ws.data_ptr(), self.attn_ws.numel() * 4, self.attn.data_ptr(), self.heads, self.kv_heads,
             self.maximum_length, self.head_dim, pos, self.scale, _lib.dtype_code(self.dtype),
-            _lib.stream_handle(self.device)), "fx_decode_attention")
+            _lib.stream_handle(self.device)), "fx_decode_attention_rope")
 
     def _silu_mul(self):
         _lib.check(self.lib.fx_silu_mul(self.gate.data_ptr(), self.up.data_ptr(), self.act.data_ptr(),
@@ -250,7 +255,6 @@ class NativeDecodeSession:
 
     def _step(self, i):
         pos = self.prefix_length + i
-        d, lmax = self.head_dim, self.maximum_length
         torch.index_select(self.embed, 0, self.tokens[0, i:i + 1], out=self.residual)
         from .fused_modules import rms_norm
 
@@ -265,14 +269,6 @@ class NativeDecodeSession:
                 lin["self_attn.q_proj"](self.normed, self.q)
                 lin["self_attn.k_proj"](self.normed, self.k)
                 lin["self_attn.v_proj"](self.normed, self.v)
-            head_norm_rope([
-                dict(x=self.q.view(self.heads, d), out=self.q_rot.view(self.heads, d), weight=self.q_norm[l],
-                     heads=self.heads, rope=True, in_strides=(0, d, 0), out_strides=(0, d, 0)),
-                dict(x=self.k.view(self.kv_heads, d), out=self.k_cache[l, :, pos], weight=self.k_norm[l],
-                     heads=self.kv_heads, rope=True, in_strides=(0, d, 0), out_strides=(0, lmax * d, 0)),
-                dict(x=self.v.view(self.kv_heads, d), out=self.v_cache[l, :, pos], weight=None,
-                     heads=self.kv_heads, rope=False, in_strides=(0, d, 0), out_strides=(0, lmax * d, 0)),
-            ], cos=self.cos[pos], sin=self.sin[pos], eps=self.eps, rope_mode=_lib.ROPE_STOCK)
             self._attention(l, pos)
             lin["self_attn.o_proj"](self.attn, self.o)
             add_rms_norm(self.o, self.residual, self.post_norm[l], self.eps, out=self.normed,

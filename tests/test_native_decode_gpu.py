@@ -56,6 +56,59 @@ def test_decode_attention(gpu, dtype, hq, hk, d, lmax, pos):
     assert np.all(np.abs(got - exact) <= 2 * _ulp(exact, dtype) + 1e-6 * np.abs(exact).max())
 
 
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+@pytest.mark.parametrize("hq,hk,d,lmax,pos,rope_mode", [(32, 8, 128, 544, 543, 1), (32, 8, 128, 544, 300, 1),
+                                                        (4, 2, 64, 130, 0, 1), (12, 2, 128, 200, 150, 2),
+                                                        (8, 8, 256, 70, 69, 1)])
+def test_decode_attention_rope(gpu, dtype, hq, hk, d, lmax, pos, rope_mode):
+    """Attention with the q/k norm, RoPE and the KV-cache write of ``pos`` folded
+    in, against the float64 oracle of the same chain: per-head RMSNorm + RoPE
+    (oracle.norms, pinned to transformers), the cache update, exact attention."""
+    from oracle import norms
+
+    g = torch.Generator().manual_seed(pos + d + hq)
+    q = (torch.randn(hq, d, generator=g) * 2).to(DT[dtype])
+    k = (torch.randn(hk, d, generator=g) * 2).to(DT[dtype])
+    v = torch.randn(hk, d, generator=g).to(DT[dtype])
+    qw = (1 + 0.2 * torch.randn(d, generator=g)).to(DT[dtype])
+    kw = (1 + 0.2 * torch.randn(d, generator=g)).to(DT[dtype])
+    cos_t, sin_t = norms.rope_cos_sin([pos], d, 1e6, dtype)
+    kc = torch.randn(hk, lmax, d, generator=g).to(DT[dtype])
+    vc = torch.randn(hk, lmax, d, generator=g).to(DT[dtype])
+    kc[:, pos:] = 1e4  # position pos is written by the kernel; later slots hold junk
+    vc[:, pos:] = float("nan")
+    lib = _lib.library()
+    nbytes = lib.fx_decode_attention_workspace_bytes(hq, lmax, d)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=gpu)
+    out = torch.empty(hq, d, dtype=DT[dtype], device=gpu)
+    dev = {n: t.to(gpu) for n, t in dict(q=q, k=k, v=v, qw=qw, kw=kw, kc=kc, vc=vc).items()}
+    cos_d = torch.from_numpy(cos_t[0]).to(DT[dtype]).to(gpu)
+    sin_d = torch.from_numpy(sin_t[0]).to(DT[dtype]).to(gpu)
+    _lib.check(lib.fx_decode_attention_rope(
+        dev["q"].data_ptr(), dev["k"].data_ptr(), dev["v"].data_ptr(), dev["qw"].data_ptr(), dev["kw"].data_ptr(),
+        cos_d.data_ptr(), sin_d.data_ptr(), 1e-6, rope_mode, dev["kc"].data_ptr(), dev["vc"].data_ptr(),
+        ws.data_ptr(), nbytes, out.data_ptr(), hq, hk, lmax, d, pos, 1 / np.sqrt(d), _lib.dtype_code(DT[dtype]),
+        _lib.stream_handle(gpu)), "attention_rope")
+    qn = norms.rms_norm(q.float().numpy(), qw.float().numpy(), 1e-6, dtype)
+    kn = norms.rms_norm(k.float().numpy(), kw.float().numpy(), 1e-6, dtype)
+    qr = norms.apply_rope(qn, cos_t, sin_t, dtype, fused=rope_mode == 2)
+    kr = norms.apply_rope(kn, cos_t, sin_t, dtype, fused=rope_mode == 2)
+    kc_want, vc_want = kc.float().numpy().copy(), vc.float().numpy().copy()
+    kc_want[:, pos], vc_want[:, pos] = kr, v.float().numpy()
+    kc_got = dev["kc"].float().cpu().numpy()
+    # the cache row of pos: v exactly, k within one ulp (the per-head sum of
+    # squares is a different fp32 order than the oracle's float64 mean)
+    assert np.array_equal(dev["vc"].float().cpu().numpy()[:, pos], v.float().numpy())
+    assert np.all(np.abs(kc_got[:, pos] - kr) <= _ulp(kr, dtype))
+    assert np.array_equal(kc_got[:, :pos], kc.float().numpy()[:, :pos])
+    exact = decode.gqa_attention(qr, kc_want, vc_want, pos, 1 / np.sqrt(d))
+    got = out.float().cpu().numpy()
+    assert np.all(np.isfinite(got))
+    # two output ulps, plus what a one-ulp change of a normalised q/k element can move
+    assert np.all(np.abs(got - exact) <= 3 * _ulp(exact, dtype) + 1e-2 * np.abs(exact).max())
+    assert np.mean(np.abs(got - exact) <= 2 * _ulp(exact, dtype) + 1e-6 * np.abs(exact).max()) > 0.98
+
+
 def test_decode_attention_rejects_bad_position(gpu):
     lib = _lib.library()
     t = torch.empty(4096, dtype=torch.bfloat16, device=gpu)
@@ -171,8 +224,8 @@ def test_native_session_matches_hf_static_session(gpu, quantize):
     assert report["stepwise_normalized_rmse"][1] <= 0.01, report
     # launches per layer + embedding, first norm, final norm, LM head, argmax per token
     per_step = native.kernel_nodes / STEPS
-    # W3: 9 per layer (q|k|v and gate|up+SwiGLU fused) + 5 per token
-    assert per_step <= (9 if quantize else 13) * 3 + 5, per_step
+    # W3: 8 per layer (q|k|v and gate|up+SwiGLU fused, q/k norm + RoPE in the attention) + 5 per token
+    assert per_step <= (8 if quantize else 12) * 3 + 5, per_step
     for _ in range(2):
         timing, replay = native.measure("sequence_graph")
         assert torch.equal(replay["logits"], graph["logits"])
