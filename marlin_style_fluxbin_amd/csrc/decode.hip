@@ -115,8 +115,26 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const uint16_t* __restr
   const bool lower = db < DB / 2;
   const bool has_pos = first <= pos && pos < first + KS * KPT;  // workgroup-uniform
   u32x4_t qw, cs, sn, kraw, vraw, kw;
+  // PRE: the rows of a wave split the pass's query heads (row r of the wave
+  // normalises heads r, r + rows, ...; each row loads its own heads' raw slices)
+  // and share the results through the wave's LDS slot
+  constexpr int kRows = 64 / DB;
+  constexpr int kOwn = HB > kRows ? HB / kRows : 1;  // heads one row normalises per pass
+  const int qrow = lane / DB;
+  u32x4_t qown[kOwn];
+  auto load_own = [&](int h0) __attribute__((always_inline)) {
 #pragma unroll
-  for (int hh = 0; hh < HB; ++hh) qr[hh] = load_b128(rq, hh < G ? (hh * D + 8 * db) * 2 : kOutOfRange, 0);
+    for (int o = 0; o < kOwn; ++o) {
+      const int hh = o * kRows + qrow, h = h0 + hh;
+      qown[o] = load_b128(rq, hh < HB && h < G ? (h * D + 8 * db) * 2 : kOutOfRange, 0);
+    }
+  };
+  if constexpr (PRE) {
+    load_own(0);
+  } else {
+#pragma unroll
+    for (int hh = 0; hh < HB; ++hh) qr[hh] = load_b128(rq, hh < G ? (hh * D + 8 * db) * 2 : kOutOfRange, 0);
+  }
   if constexpr (PRE) {
     const auto rd = [&](const uint16_t* p, bool on) {
       return load_b128(buffer_resource(p, D * 2), on ? 16 * db : kOutOfRange, 0);
@@ -139,20 +157,12 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const uint16_t* __restr
     const int j = first + ks + KS * i;
     vr[i] = load_b128(rv, live[i] ? (j * D + 8 * db) * 2 : kOutOfRange, 0);
   }
-  // PRE: the rows of a wave split the pass's query heads (row r of the wave
-  // normalises heads r, r + rows, ...) and share them through the wave's LDS slot
-  constexpr int kRows = 64 / DB;
   auto normalise_queries = [&]() __attribute__((always_inline)) {
-    const int row = lane / DB;
 #pragma unroll
-    for (int hh = 0; hh < HB; hh += kRows) {
-      const int mine_h = hh + row;
-      u32x4_t sel = qr[0];
-#pragma unroll
-      for (int c = 1; c < HB; ++c)
-        if (c == mine_h) sel = qr[c];
-      const u32x4_t o = head_norm_rope8<DT, D>(sel, qw, cs, sn, lower, pre.eps, pre.rope_mode);
-      if (mine_h < HB) qsh[wave][mine_h][db] = o;
+    for (int o = 0; o < kOwn; ++o) {
+      const int hh = o * kRows + qrow;
+      const u32x4_t v = head_norm_rope8<DT, D>(qown[o], qw, cs, sn, lower, pre.eps, pre.rope_mode);
+      if (hh < HB) qsh[wave][hh][db] = v;
     }
     __builtin_amdgcn_wave_barrier();
 #pragma unroll
@@ -179,7 +189,7 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const uint16_t* __restr
   }
 
   for (int h0 = 0; h0 < G; h0 += HB) {
-    if (h0 > 0) {
+    if (!PRE && h0 > 0) {
 #pragma unroll
       for (int hh = 0; hh < HB; ++hh)
         qr[hh] = load_b128(rq, h0 + hh < G ? ((h0 + hh) * D + 8 * db) * 2 : kOutOfRange, 0);
@@ -190,7 +200,10 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const uint16_t* __restr
 #pragma unroll
       for (int e = 0; e < 8; ++e) kf[i][e] = to_f32<DT>(uint16_t(kr[i][e >> 1] >> (16 * (e & 1))));
     if constexpr (PRE) {
-      if (h0 > 0) normalise_queries();
+      if (h0 > 0) {
+        load_own(h0);
+        normalise_queries();
+      }
     }
     float s[HB][KPT];
     float mt[HB];
