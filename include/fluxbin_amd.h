@@ -102,6 +102,27 @@ int fx_w3_gemv(const void *x, int x_dtype, const uint8_t *planes, const void *sc
 int fx_w3_gemv_swiglu(const void *x, int x_dtype, const uint8_t *planes, const void *scales,
                       int scale_dtype, const uint8_t *zeros, const int16_t *perm, void *out, int O,
                       int K, void *stream);
+/* The decoder layer's residual stream threaded through its W3 GEMVs (one
+ * activation row, identity or permuted column order for the residual form,
+ * structural MFMA arithmetic).  No single reference entry point: together they
+ * replace HF Qwen3DecoderLayer's residual adds and Qwen3RMSNorm (as the reference
+ * patches them, fused_modules.py:30-63) around the PackedW3Linear calls
+ * (w3_lut_deployment.py:250-359).
+ * fx_w3_gemv_residual: out = round(residual + round(x @ W.T)) -- out may alias
+ * residual -- and tile_sumsq[t] = sum of out^2 over rows [16 t, 16 t + 16),
+ * ceil(O / 16) floats.
+ * fx_w3_gemv_rmsnormed: h is such an out (K = its O) and tile_sumsq its tile
+ * sums (n_tiles = ceil(K / 16), K <= 8192); the GEMV reads
+ * x = round(norm_weight * round(h * rsqrt(sum(tile_sumsq) / K + eps))), the
+ * RMSNorm of h, summing the tile sums in a fixed order; swiglu != 0 reads the
+ * row-interleaved gate|up payload of fx_w3_gemv_swiglu.  Identity column order. */
+int fx_w3_gemv_residual(const void *x, int x_dtype, const uint8_t *planes, const void *scales,
+                        int scale_dtype, const uint8_t *zeros, const int16_t *perm, const void *residual,
+                        void *out, float *tile_sumsq, int O, int K, void *stream);
+int fx_w3_gemv_rmsnormed(const void *h, int x_dtype, const uint8_t *planes, const void *scales,
+                         int scale_dtype, const uint8_t *zeros, const float *tile_sumsq, int n_tiles,
+                         const void *norm_weight, float eps, void *out, int O, int K, int swiglu,
+                         void *stream);
 /* Structural MFMA path with an explicit tiling (benchmark sweeps): waves per
  * workgroup in {4,8}, 4-group batches kept in flight per wave in {1,2},
  * groups per K split (rounded up to a multiple of 4, clamped to the padded group

@@ -272,6 +272,7 @@ int run_mfma(const void* x, int x_dtype, const uint8_t* planes, const void* scal
     a.gps = p.gps;
     a.row_blocks = p.row_blocks;
     a.swiglu = swiglu;
+    a.res = fx::ResidualArgs{};
     const dim3 grid(p.row_blocks, p.splits);
     if (!fx::dispatch_mfma(x_dtype, p.tiles, p.nw, p.pd, mb, scale_dtype, a, grid, s))
       return fail(FX_EINVAL, "no MFMA kernel for waves %d prefetch %d tiles %d rows %d", p.nw,
@@ -495,7 +496,7 @@ bool two_base_config(int O, int G, int waves, int prefetch, int groups_per_split
 
 extern "C" {
 
-int fx_abi_version(void) { return 6; }
+int fx_abi_version(void) { return 7; }
 
 const char* fx_last_error(void) { return g_error; }
 
@@ -585,6 +586,72 @@ int fx_w3_gemv_swiglu(const void* x, int x_dtype, const uint8_t* planes, const v
   if (p.splits > 1) p = make_mfma_plan(O, G, 8, 1, G, 1);  // the fused epilogue needs one K split
   return run_mfma(x, x_dtype, planes, scales, scale_dtype, zeros, perm, nullptr, 0, out, 1, O, K, p,
                   static_cast<hipStream_t>(stream), 1);
+}
+
+// One-row plan with one K split and one tile and batch in flight per wave (the
+// residual epilogue and the normalising prologue need all of K in one workgroup).
+MfmaPlan single_split_plan(int O, int G) {
+  MfmaPlan p = default_mfma_plan(O, G);
+  if (p.splits > 1 || p.pd != 1 || p.tiles != 1) p = make_mfma_plan(O, G, 8, 1, G, 1);
+  return p;
+}
+
+int fx_w3_gemv_residual(const void* x, int x_dtype, const uint8_t* planes, const void* scales,
+                        int scale_dtype, const uint8_t* zeros, const int16_t* perm, const void* residual,
+                        void* out, float* tile_sumsq, int O, int K, void* stream) {
+  int rc = validate_payload(x, x_dtype, planes, scales, scale_dtype, 1, O, K, FX_ARITH_STRUCTURAL);
+  if (rc) return rc;
+  if (!residual || !out || !tile_sumsq) return fail(FX_EINVAL, "residual, out and tile_sumsq must be non-null");
+  const int G = K / 128;
+  const MfmaPlan p = single_split_plan(O, G);
+  MfmaArgs a{};
+  a.x = static_cast<const uint16_t*>(x);
+  a.perm = perm;
+  a.planes = planes;
+  a.scales = static_cast<const uint16_t*>(scales);
+  a.zeros = zeros;
+  a.out = static_cast<uint16_t*>(out);
+  a.O = O;
+  a.G = G;
+  a.gps = p.gps;
+  a.row_blocks = p.row_blocks;
+  a.res.ep_residual = static_cast<const uint16_t*>(residual);
+  a.res.ep_partial = tile_sumsq;
+  if (!fx::dispatch_mfma(x_dtype, 1, p.nw, 1, 1, scale_dtype, a, dim3(p.row_blocks, 1), static_cast<hipStream_t>(stream)))
+    return fail(FX_EINVAL, "no MFMA kernel for waves %d", p.nw);
+  return check_launch("w3_mfma_kernel (residual epilogue)");
+}
+
+int fx_w3_gemv_rmsnormed(const void* h, int x_dtype, const uint8_t* planes, const void* scales, int scale_dtype,
+                         const uint8_t* zeros, const float* tile_sumsq, int n_tiles, const void* norm_weight,
+                         float eps, void* out, int O, int K, int swiglu, void* stream) {
+  int rc = validate_payload(h, x_dtype, planes, scales, scale_dtype, 1, O, K, FX_ARITH_STRUCTURAL);
+  if (rc) return rc;
+  if (!tile_sumsq || !norm_weight || !out) return fail(FX_EINVAL, "tile_sumsq, norm weight and out must be non-null");
+  if (n_tiles != (K + 15) / 16) return fail(FX_EINVAL, "n_tiles must be ceil(K / 16) = %d, got %d", (K + 15) / 16, n_tiles);
+  if (n_tiles > 64 * fx::kMaxNormPartialsPerLane) return fail(FX_EINVAL, "K = %d too large for the normalising prologue", K);
+  if (reinterpret_cast<uintptr_t>(norm_weight) % 16 != 0) return fail(FX_EINVAL, "norm weight must be 16-byte aligned");
+  if (swiglu && O % 2) return fail(FX_EINVAL, "the interleaved gate|up payload needs an even row count, got %d", O);
+  const int G = K / 128;
+  const MfmaPlan p = single_split_plan(O, G);
+  MfmaArgs a{};
+  a.x = static_cast<const uint16_t*>(h);
+  a.planes = planes;
+  a.scales = static_cast<const uint16_t*>(scales);
+  a.zeros = zeros;
+  a.out = static_cast<uint16_t*>(out);
+  a.O = O;
+  a.G = G;
+  a.gps = p.gps;
+  a.row_blocks = p.row_blocks;
+  a.swiglu = swiglu ? 1 : 0;
+  a.res.pro_partial = tile_sumsq;
+  a.res.pro_n = n_tiles;
+  a.res.pro_weight = static_cast<const uint16_t*>(norm_weight);
+  a.res.pro_eps = eps;
+  if (!fx::dispatch_mfma_normin(p.nw, x_dtype, scale_dtype, a, dim3(p.row_blocks, 1), static_cast<hipStream_t>(stream)))
+    return fail(FX_EINVAL, "no normalising MFMA kernel for waves %d", p.nw);
+  return check_launch("w3_mfma_kernel (normalising prologue)");
 }
 
 size_t fx_w3_gemv_config_workspace_bytes(int M, int O, int K, int waves, int prefetch,

@@ -44,6 +44,7 @@
 // All kernel arguments are read in one scalar round before any branch.
 #pragma once
 #include "common.h"
+#include "w3_mfma_launch.h"
 
 namespace fx {
 
@@ -114,6 +115,7 @@ struct BatchLoads {
   unsigned s[RT][2]; // scales of rows erow..erow+3 of each tile, two per word
   unsigned z[RT];    // zero-points of rows erow..erow+3, one per byte
   unsigned se[RT][4], ze[RT][4];  // the same as single elements when O % 4 != 0
+  u32x4_t wn;        // NORMIN: the RMSNorm weights of this lane's 8 columns
 };
 
 // The K reduction of a workgroup always runs in the order eight waves give it:
@@ -141,12 +143,12 @@ struct MfmaShared {
 // aligned load each.  A separate instantiation (rather than a runtime branch)
 // keeps the load count per batch fixed, so the wait before staging covers only
 // the activations.
-template <int NW, int PD, int MB, int RT, bool PERM, int XDT, int SDT, bool VEC>
+template <int NW, int PD, int MB, int RT, bool PERM, int XDT, int SDT, bool NORMIN, bool VEC>
 __device__ __forceinline__ void w3_mfma_body(
     MfmaShared<NW, MB, RT>& sh, const uint16_t* __restrict__ x, const int16_t* __restrict__ perm,
     const uint8_t* __restrict__ planes, const uint16_t* __restrict__ scales,
     const uint8_t* __restrict__ zeros, float* __restrict__ partial,
-    uint16_t* __restrict__ out, int O, int G, int gps, int row_blocks, int swiglu) {
+    uint16_t* out, int O, int G, int gps, int row_blocks, int swiglu, const ResidualArgs& ra) {
   auto& bstage = sh.bstage;
   auto& bzero = sh.bzero;
   auto& gsum = sh.gsum;
@@ -168,6 +170,21 @@ __device__ __forceinline__ void w3_mfma_body(
                                   zeros ? size_t(G) * O : 0);
   const auto rx = buffer_resource(x, size_t(MB) * K * 2);
   const auto rperm = buffer_resource(PERM ? (const void*)perm : (const void*)x, PERM ? size_t(K) * 2 : 0);
+  // NORMIN: the row's RMSNorm weights, and 1 / rms from the tile partials (each
+  // wave reduces them itself, in a fixed order: lane l adds partials l, l + 64,
+  // ..., then the wave total), loaded ahead of every other load
+  const auto rwn = buffer_resource(NORMIN ? (const void*)ra.pro_weight : (const void*)x, NORMIN ? size_t(K) * 2 : 0);
+  float norm_inv = 1.f;
+  float pp[kMaxNormPartialsPerLane];
+  if constexpr (NORMIN) {
+    const auto rpp = buffer_resource(ra.pro_partial, size_t(ra.pro_n) * 4);
+#pragma unroll
+    for (int k = 0; k < kMaxNormPartialsPerLane; ++k) {
+      const int idx = (lane & 63) + 64 * k;
+      pp[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rpp, idx < ra.pro_n ? idx * 4 : kOutOfRange, 0, 0));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
 
   const int r = lane & 15;    // A role: row within tile; x role: 8-column chunk
   const int kb = lane >> 4;   // A role: k-block = group slot; D role: row block
@@ -196,6 +213,7 @@ __device__ __forceinline__ void w3_mfma_body(
 #pragma unroll
       for (int m = 0; m < MB; ++m) L.xv[m] = load_b128(rx, real ? (m * K + col) * 2 : kOutOfRange, 0);
     }
+    if constexpr (NORMIN) L.wn = load_b128(rwn, real ? col * 2 : kOutOfRange, 0);
     __builtin_amdgcn_sched_barrier(0);
     const int poff = ((gb + kb) * 3 * O + row0 + r) * 16;  // past the end -> zeros
 #pragma unroll
@@ -281,6 +299,12 @@ __device__ __forceinline__ void w3_mfma_body(
         float v[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) v[i] = to_f32<XDT>(uint16_t(xw[i >> 1] >> (16 * (i & 1))));
+        if constexpr (NORMIN) {  // Qwen3RMSNorm: round(w * round(h * inv))
+#pragma unroll
+          for (int i = 0; i < 8; ++i)
+            v[i] = round_to<XDT>(to_f32<XDT>(uint16_t(L.wn[i >> 1] >> (16 * (i & 1)))) *
+                                 round_to<XDT>(v[i] * norm_inv));
+        }
         stage_row(m, v);
       }
     }
@@ -341,17 +365,36 @@ __device__ __forceinline__ void w3_mfma_body(
 #pragma unroll
   for (int i = 0; i < PD; ++i)
     if (i < mine) issue(wave + i * NW, ring[i]);
-  constexpr int STEP = PD > VS ? PD : VS;  // PD, VS in {1, 2}: a multiple of both
-  for (int base = 0; base < mine; base += STEP) {
+  if constexpr (NORMIN) {
+    float total = 0.f;
 #pragma unroll
-    for (int i = 0; i < STEP; ++i) {
+    for (int k = 0; k < kMaxNormPartialsPerLane; ++k) total += pp[k];
+    norm_inv = rsqrtf(wave_total(total) / float(K) + ra.pro_eps);
+  }
+  // batches always accumulate into set 0; with two sets they are swapped after
+  // every batch (register moves, not a second unrolled copy of the loop body),
+  // so after an odd count set 0 holds the wave's second virtual wave
+  for (int base = 0; base < mine; base += PD) {
+#pragma unroll
+    for (int i = 0; i < PD; ++i) {
       if (base + i < mine) {
         cur_batch = wave + (base + i) * NW;
-        consume(ring[i % PD], acc_sets[i % VS]);
-        if (base + i + PD < mine) issue(wave + (base + i + PD) * NW, ring[i % PD]);
+        consume(ring[i], acc_sets[0]);
+        if (base + i + PD < mine) issue(wave + (base + i + PD) * NW, ring[i]);
+        if constexpr (VS == 2) {
+#pragma unroll
+          for (int tt = 0; tt < RT; ++tt)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const float keep = acc_sets[0][tt][j];
+              acc_sets[0][tt][j] = acc_sets[1][tt][j];
+              acc_sets[1][tt][j] = keep;
+            }
+        }
       }
     }
   }
+  const bool odd = VS == 2 && (mine & 1);
 
   // sum the four group slots of each activation row (lanes c = 4m .. 4m+3)
 #pragma unroll
@@ -369,10 +412,30 @@ __device__ __forceinline__ void w3_mfma_body(
 #pragma unroll
       for (int tt = 0; tt < RT; ++tt)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) red[wave + v * NW][(16 * tt + 4 * kb + j) * MB + cm] = acc_sets[v][tt][j];
+        for (int j = 0; j < 4; ++j)
+          red[wave + (odd ? 1 - v : v) * NW][(16 * tt + 4 * kb + j) * MB + cm] = acc_sets[v][tt][j];
     }
   }
   __syncthreads();
+  if (ra.ep_residual) {
+    // MB = 1, RT = 1: out = round(residual + round(y)) for the tile's 16 rows
+    // (threads 0..15, wave 0), and the tile's sum of out^2 (DPP row sum)
+    if (wave == 0) {
+      float h2 = 0.f;
+      const int orow = row0 + lane;
+      if (lane < 16 && orow < O) {
+        float total = 0.f;
+#pragma unroll
+        for (int k = 0; k < kSumLanes; ++k) total += red[k][lane];
+        const float h = round_to<XDT>(to_f32<XDT>(ra.ep_residual[orow]) + round_to<XDT>(total));
+        out[orow] = from_f32<XDT>(h);
+        h2 = h * h;
+      }
+      h2 = row16_sum(h2);
+      if (lane == 0) ra.ep_partial[row0 / 16] = h2;
+    }
+    return;
+  }
   if (swiglu) {
     // rows come in (gate, up) pairs (MB = 1, one K split): each pair is rounded
     // to the activation dtype as a separate GEMV would store it, then
@@ -416,23 +479,25 @@ __device__ __forceinline__ void w3_mfma_body(
 // stored.  x is [MB, 128 G] row-major; with PERM, sorted column k reads x
 // column perm[k].  swiglu != 0 (MB = 1, one split, O even): the payload's rows
 // interleave gate and up rows, and out receives SiLU(gate) * up, O / 2 values.
-template <int NW, int PD, int MB, int RT, bool PERM, int XDT, int SDT>
+template <int NW, int PD, int MB, int RT, bool PERM, int XDT, int SDT, bool NORMIN = false>
 __global__ __launch_bounds__(NW * 64) void w3_mfma_kernel(
     const uint16_t* __restrict__ x, const int16_t* __restrict__ perm,
     const uint8_t* __restrict__ planes, const uint16_t* __restrict__ scales,
     const uint8_t* __restrict__ zeros, float* __restrict__ partial,
-    uint16_t* __restrict__ out, int O, int G, int gps, int row_blocks, int swiglu) {
+    uint16_t* out, int O, int G, int gps, int row_blocks, int swiglu, ResidualArgs ra) {
   // one scalar-load round for every argument (otherwise the pointer loads sink
   // below the first branch and add a second round trip before the first load)
   asm volatile("" ::"s"(x), "s"(perm), "s"(planes), "s"(scales), "s"(zeros), "s"(partial), "s"(out),
-               "s"(O), "s"(G), "s"(gps), "s"(row_blocks), "s"(swiglu));
+               "s"(O), "s"(G), "s"(gps), "s"(row_blocks), "s"(swiglu), "s"(ra.ep_residual), "s"(ra.ep_partial));
+  if constexpr (NORMIN)
+    asm volatile("" ::"s"(ra.pro_partial), "s"(ra.pro_n), "s"(ra.pro_weight), "s"(ra.pro_eps));
   __shared__ MfmaShared<NW, MB, RT> sh;
   if ((O & 3) == 0)
-    w3_mfma_body<NW, PD, MB, RT, PERM, XDT, SDT, true>(sh, x, perm, planes, scales, zeros, partial, out, O, G,
-                                                       gps, row_blocks, swiglu);
+    w3_mfma_body<NW, PD, MB, RT, PERM, XDT, SDT, NORMIN, true>(sh, x, perm, planes, scales, zeros, partial, out,
+                                                               O, G, gps, row_blocks, swiglu, ra);
   else
-    w3_mfma_body<NW, PD, MB, RT, PERM, XDT, SDT, false>(sh, x, perm, planes, scales, zeros, partial, out, O,
-                                                        G, gps, row_blocks, swiglu);
+    w3_mfma_body<NW, PD, MB, RT, PERM, XDT, SDT, NORMIN, false>(sh, x, perm, planes, scales, zeros, partial, out,
+                                                                O, G, gps, row_blocks, swiglu, ra);
 }
 
 }  // namespace fx

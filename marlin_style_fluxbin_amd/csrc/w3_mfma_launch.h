@@ -5,6 +5,23 @@
 
 namespace fx {
 
+// Decoder-layer residual stream around a one-row GEMV (one K split, one tile per
+// wave):
+// * epilogue (ep_residual set): out = round(residual + round(y)) -- the layer's
+//   residual add -- and ep_partial[tile] = sum over the tile's 16 rows of out^2;
+// * prologue (NORMIN instantiations): x holds h (such an epilogue's out); the
+//   GEMV reads x = round(weight * round(h * rsqrt(sum(pro_partial) / K + eps))),
+//   the RMSNorm of h, from the pro_n tile partials.
+struct ResidualArgs {
+  const uint16_t* ep_residual;  // null: plain epilogue
+  float* ep_partial;
+  const float* pro_partial;
+  int pro_n;
+  const uint16_t* pro_weight;
+  float pro_eps;
+};
+constexpr int kMaxNormPartialsPerLane = 8;  // prologue: K <= 8 * 64 * 16
+
 struct MfmaArgs {
   const uint16_t* x;     // [mb, K] activations of this launch
   const int16_t* perm;   // null: identity
@@ -16,6 +33,7 @@ struct MfmaArgs {
   int O, G, gps;
   int row_blocks;  // ceil(O / (16 * tiles)); the grid is (row_blocks, K splits)
   int swiglu;      // 1: rows interleave (gate, up); out gets SiLU(gate) * up (mb 1, one split)
+  ResidualArgs res;
 };
 
 // nw waves per workgroup in {4, 8}; pd batches in flight per wave in {1, 2};
@@ -33,6 +51,10 @@ FX_MFMA_DECL(dispatch_mfma_bf16_t2_perm)
 FX_MFMA_DECL(dispatch_mfma_f16_t1_perm)
 FX_MFMA_DECL(dispatch_mfma_f16_t2_perm)
 #undef FX_MFMA_DECL
+
+// The normalising-prologue instantiations: one activation row, one 16-row tile
+// and one batch in flight per wave, no permutation; nw in {4, 8}.
+bool dispatch_mfma_normin(int nw, int xdt, int sdt, const MfmaArgs& a, dim3 grid, hipStream_t s);
 
 inline bool dispatch_mfma(int xdt, int tiles, int nw, int pd, int mb, int sdt, const MfmaArgs& a,
                           dim3 grid, hipStream_t s) {

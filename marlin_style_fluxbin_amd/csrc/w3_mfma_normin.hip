@@ -1,0 +1,24 @@
+// MFMA W3 GEMV instantiations whose staging normalises the activation row
+// (RMSNorm from the previous GEMV's tile partial sums).
+#include "w3_mfma_inst.h"
+
+namespace fx {
+
+template <int NW, int XDT, int SDT>
+void launch_mfma_normin(const MfmaArgs& a, dim3 grid, hipStream_t s) {
+  hipLaunchKernelGGL((w3_mfma_kernel<NW, 1, 1, 1, false, XDT, SDT, true>), grid, dim3(NW * 64), 0, s, a.x,
+                     a.perm, a.planes, a.scales, a.zeros, a.partial, a.out, a.O, a.G, a.gps, a.row_blocks,
+                     a.swiglu, a.res);
+}
+
+bool dispatch_mfma_normin(int nw, int xdt, int sdt, const MfmaArgs& a, dim3 grid, hipStream_t s) {
+#define FX_NORMIN_CASE(W, X, S) \
+  if (nw == W && xdt == X && sdt == S) { launch_mfma_normin<W, X, S>(a, grid, s); return true; }
+  FX_NORMIN_CASE(4, kBF16, kBF16) FX_NORMIN_CASE(4, kBF16, kF16) FX_NORMIN_CASE(4, kF16, kBF16)
+  FX_NORMIN_CASE(4, kF16, kF16) FX_NORMIN_CASE(8, kBF16, kBF16) FX_NORMIN_CASE(8, kBF16, kF16)
+  FX_NORMIN_CASE(8, kF16, kBF16) FX_NORMIN_CASE(8, kF16, kF16)
+#undef FX_NORMIN_CASE
+  return false;
+}
+
+}  // namespace fx

@@ -146,6 +146,53 @@ class _GateUpSwiGLU:
             2 * self.width, self.in_features, _lib.stream_handle(x.device)), "fx_w3_gemv_swiglu")
 
 
+class _ResidualStream:
+    """The decoder layers' residual adds and RMSNorms threaded through the W3
+    GEMVs: the o and down GEMVs add their output into the residual in place and
+    write per-16-row sums of its squares (``fx_w3_gemv_residual``); the q|k|v and
+    gate|up GEMVs read the residual and normalise it on the fly from those sums
+    (``fx_w3_gemv_rmsnormed``).  ``None`` from :meth:`build` unless every layer's
+    o, down, q|k|v and gate|up are structural W3 (q|k|v and gate|up fused with
+    identity column order)."""
+
+    def __init__(self, lib, hidden, device):
+        self.lib = lib
+        self.tiles = (hidden + 15) // 16
+        self.partials = torch.zeros(self.tiles, dtype=torch.float32, device=device)
+
+    @staticmethod
+    def build(session):
+        def structural(m):
+            return isinstance(m, PackedW3Linear) and m.arithmetic == "structural" and m.bias is None
+
+        for layer, qkv, swiglu in zip(session.layers, session.qkv, session.swiglu):
+            o, down = layer.self_attn.o_proj, layer.mlp.down_proj
+            if not (structural(o) and structural(down)) or qkv is None or swiglu is None:
+                return None
+            gemv = qkv.call
+            if not (isinstance(gemv, W3Gemv) and gemv.perm_ptr is None and gemv.arith == _lib.ARITH_STRUCTURAL):
+                return None
+            if swiglu.perm_ptr is not None:
+                return None
+        return _ResidualStream(_lib.library(), session.hidden, session.device)
+
+    def residual(self, gemv: W3Gemv, x, residual):
+        """residual <- round(residual + round(x @ W.T)); tile sums of its squares."""
+        lay = gemv.layout
+        _lib.check(self.lib.fx_w3_gemv_residual(
+            x.data_ptr(), _lib.dtype_code(x.dtype), lay["planes"].data_ptr(), lay["scales"].data_ptr(),
+            gemv.scale_code, gemv.zeros_ptr, gemv.perm_ptr, residual.data_ptr(), residual.data_ptr(),
+            self.partials.data_ptr(), gemv.out_features, gemv.in_features, _lib.stream_handle(x.device)),
+            "fx_w3_gemv_residual")
+
+    def normed(self, layout, scale_code, zeros_ptr, rows, h, weight, eps, out, swiglu):
+        """out = GEMV (or SwiGLU) of RMSNorm(h) with the tile sums of h."""
+        _lib.check(self.lib.fx_w3_gemv_rmsnormed(
+            h.data_ptr(), _lib.dtype_code(h.dtype), layout["planes"].data_ptr(), layout["scales"].data_ptr(),
+            scale_code, zeros_ptr, self.partials.data_ptr(), self.tiles, weight.data_ptr(), eps, out.data_ptr(),
+            rows, h.shape[-1], int(swiglu), _lib.stream_handle(h.device)), "fx_w3_gemv_rmsnormed")
+
+
 class NativeDecodeSession:
     def __init__(self, model, input_ids: torch.Tensor, forced_tokens: torch.Tensor):
         from transformers import StaticCache
@@ -206,6 +253,7 @@ class NativeDecodeSession:
         self.swiglu = [_GateUpSwiGLU.build(*(b.get_submodule(n) for n in _MLP[:2])) for b in self.layers]
         self.gate_up = [None if f is not None else _FusedLinear.build([b.get_submodule(n) for n in _MLP[:2]])
                         for f, b in zip(self.swiglu, self.layers)]
+        self.stream = _ResidualStream.build(self)
         self.in_norm = [b.input_layernorm.weight for b in self.layers]
         self.post_norm = [b.post_attention_layernorm.weight for b in self.layers]
         self.q_norm = [b.self_attn.q_norm.weight for b in self.layers]
@@ -253,7 +301,33 @@ class NativeDecodeSession:
                                         self.act.shape[1], _lib.dtype_code(self.dtype),
                                         _lib.stream_handle(self.device)), "fx_silu_mul")
 
+    def _step_residual_stream(self, i):
+        from .fused_modules import rms_norm
+
+        rs = self.stream
+        torch.index_select(self.embed, 0, self.tokens[0, i:i + 1], out=self.residual)
+        pos = self.prefix_length + i
+        for l, lin in enumerate(self.lin):
+            gemv = self.qkv[l].call
+            if l == 0:
+                rms_norm(self.residual, self.in_norm[0], self.eps, out=self.normed)
+                gemv(self.normed, self.qkv_out)
+            else:
+                rs.normed(gemv.layout, gemv.scale_code, gemv.zeros_ptr, gemv.out_features, self.residual,
+                          self.in_norm[l], self.eps, self.qkv_out, False)
+            self._attention(l, pos)
+            rs.residual(lin["self_attn.o_proj"].gemv, self.attn, self.residual)
+            sw = self.swiglu[l]
+            rs.normed(sw.layout, sw.scale_code, sw.zeros_ptr, 2 * sw.width, self.residual, self.post_norm[l],
+                      self.eps, self.act, True)
+            rs.residual(lin["mlp.down_proj"].gemv, self.act, self.residual)
+        rms_norm(self.residual, self.final_norm, self.eps, out=self.normed)
+        torch.matmul(self.normed, self.lm_head.t(), out=self.logits[i:i + 1])
+        torch.argmax(self.logits[i:i + 1], dim=-1, keepdim=True, out=self.predictions[i:i + 1])
+
     def _step(self, i):
+        if self.stream is not None:
+            return self._step_residual_stream(i)
         pos = self.prefix_length + i
         torch.index_select(self.embed, 0, self.tokens[0, i:i + 1], out=self.residual)
         from .fused_modules import rms_norm

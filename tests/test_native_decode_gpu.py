@@ -179,6 +179,80 @@ def test_gemv_swiglu_matches_gemvs_then_silu_mul(gpu, inter, k, dtype, scale_dty
     assert rc == 1 and "even" in lib.fx_last_error().decode()
 
 
+@pytest.mark.parametrize("o,k,dtype,permute", [(4096, 4096, "bf16", False), (4096, 12288, "bf16", True),
+                                                (96, 384, "f16", False), (40, 256, "bf16", False)])
+def test_gemv_residual_epilogue(gpu, o, k, dtype, permute):
+    """fx_w3_gemv_residual: out = round(residual + round(x @ W.T)) bit for bit
+    (the plain GEMV, then the dtype's own add), in place, plus the sums of out^2
+    over 16-row tiles."""
+    from marlin_style_fluxbin_amd.w3_lut_deployment import W3Gemv
+    from payloads import config_codes, layout_from_codes
+
+    codes, scales, zero, perm = config_codes(o, k, seed=o + k, zeros=True, scale_dtype=torch.float16, permute=permute)
+    layout = {n: v.to(gpu) for n, v in layout_from_codes(codes, scales, zero, perm).items()}
+    gemv = W3Gemv(layout)
+    g = torch.Generator().manual_seed(o)
+    x = torch.randn(1, k, generator=g).to(DT[dtype]).to(gpu)
+    res = (torch.randn(1, o, generator=g) * 4).to(DT[dtype]).to(gpu)
+    y = torch.empty(1, o, dtype=DT[dtype], device=gpu)
+    gemv(x, y)
+    want = res + y
+    tiles = (o + 15) // 16
+    sums = torch.full((tiles,), float("nan"), device=gpu)
+    got = res.clone()
+    lib = _lib.library()
+    _lib.check(lib.fx_w3_gemv_residual(x.data_ptr(), _lib.dtype_code(DT[dtype]), layout["planes"].data_ptr(),
+                                       layout["scales"].data_ptr(), _lib.dtype_code(torch.float16),
+                                       layout["zeros"].data_ptr(), gemv.perm_ptr, got.data_ptr(), got.data_ptr(),
+                                       sums.data_ptr(), o, k, _lib.stream_handle(gpu)), "residual")
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    h = want.double().cpu().numpy()[0]
+    exact = np.array([np.sum(h[16 * t:16 * t + 16] ** 2) for t in range(tiles)])
+    assert np.allclose(sums.cpu().numpy(), exact, rtol=2e-6, atol=0)
+
+
+@pytest.mark.parametrize("rows,k,dtype,swiglu", [(6144, 4096, "bf16", False), (24576, 4096, "bf16", True),
+                                                 (96, 1024, "f16", True), (34, 512, "bf16", False)])
+def test_gemv_rmsnormed_prologue(gpu, rows, k, dtype, swiglu):
+    """fx_w3_gemv_rmsnormed equals the RMSNorm kernel followed by the plain GEMV
+    (or SwiGLU GEMV) bit for bit.  h holds small integers, so every order of the
+    fp32 sum of squares is exact and both paths form the same 1 / rms."""
+    from marlin_style_fluxbin_amd.fused_modules import rms_norm
+    from marlin_style_fluxbin_amd.native_decode import _GateUpSwiGLU
+    from marlin_style_fluxbin_amd.w3_lut_deployment import W3Gemv
+    from payloads import config_codes, layout_from_codes
+
+    codes, scales, zero, _ = config_codes(rows, k, seed=rows, zeros=True, scale_dtype=torch.float16)
+    layout = {n: v.to(gpu) for n, v in layout_from_codes(codes, scales, zero, None).items()}
+    g = torch.Generator().manual_seed(k)
+    h = torch.randint(-6, 7, (1, k), generator=g).to(DT[dtype]).to(gpu)
+    weight = (1 + 0.1 * torch.randn(k, generator=g)).to(DT[dtype]).to(gpu)
+    hs = h.double().cpu().numpy()[0]
+    sums = torch.tensor([np.sum(hs[16 * t:16 * t + 16] ** 2) for t in range((k + 15) // 16)],
+                        dtype=torch.float32, device=gpu)
+    normed = torch.empty_like(h)
+    rms_norm(h, weight, 1e-6, out=normed)
+    width = rows // 2 if swiglu else rows
+    want = torch.empty(1, width, dtype=DT[dtype], device=gpu)
+    if swiglu:
+        _GateUpSwiGLU(layout, width)(normed, want)
+    else:
+        W3Gemv(layout)(normed, want)
+    got = torch.full_like(want, float("nan"))
+    lib = _lib.library()
+    _lib.check(lib.fx_w3_gemv_rmsnormed(h.data_ptr(), _lib.dtype_code(DT[dtype]), layout["planes"].data_ptr(),
+                                        layout["scales"].data_ptr(), _lib.dtype_code(torch.float16),
+                                        layout["zeros"].data_ptr(), sums.data_ptr(), sums.numel(), weight.data_ptr(),
+                                        1e-6, got.data_ptr(), rows, k, int(swiglu), _lib.stream_handle(gpu)), "normed")
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    rc = lib.fx_w3_gemv_rmsnormed(h.data_ptr(), _lib.dtype_code(DT[dtype]), layout["planes"].data_ptr(),
+                                  layout["scales"].data_ptr(), _lib.dtype_code(torch.float16), None, sums.data_ptr(),
+                                  sums.numel() + 1, weight.data_ptr(), 1e-6, got.data_ptr(), rows, k, 0, None)
+    assert rc == 1 and "n_tiles" in lib.fx_last_error().decode()
+
+
 PREFIX, STEPS = 20, 8
 
 
@@ -224,8 +298,9 @@ def test_native_session_matches_hf_static_session(gpu, quantize):
     assert report["stepwise_normalized_rmse"][1] <= 0.01, report
     # launches per layer + embedding, first norm, final norm, LM head, argmax per token
     per_step = native.kernel_nodes / STEPS
-    # W3: 8 per layer (q|k|v and gate|up+SwiGLU fused, q/k norm + RoPE in the attention) + 5 per token
-    assert per_step <= (8 if quantize else 12) * 3 + 5, per_step
+    # W3: 6 per layer (the norms inside the GEMVs, q|k|v and gate|up+SwiGLU fused, q/k norm + RoPE
+    # in the attention) + 6 per token
+    assert per_step <= (6 if quantize else 12) * 3 + 6, per_step
     for _ in range(2):
         timing, replay = native.measure("sequence_graph")
         assert torch.equal(replay["logits"], graph["logits"])
