@@ -112,7 +112,7 @@ int fx_w3_gemv_swiglu(const void *x, int x_dtype, const uint8_t *planes, const v
  * residual -- and tile_sumsq[t] = sum of out^2 over rows [16 t, 16 t + 16),
  * ceil(O / 16) floats.
  * fx_w3_gemv_rmsnormed: h is such an out (K = its O) and tile_sumsq its tile
- * sums (n_tiles = ceil(K / 16), K <= 8192); the GEMV reads
+ * sums (n_tiles = ceil(K / 16), K <= 4096); the GEMV reads
  * x = round(norm_weight * round(h * rsqrt(sum(tile_sumsq) / K + eps))), the
  * RMSNorm of h, summing the tile sums in a fixed order; swiglu != 0 reads the
  * row-interleaved gate|up payload of fx_w3_gemv_swiglu.  Identity column order. */

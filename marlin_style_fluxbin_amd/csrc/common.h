@@ -13,11 +13,10 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) {
   return __uint_as_float(uint32_t(b) << 16);
 }
 
+// Round to nearest even in one instruction (v_cvt_pk_bf16_f32 on gfx950); NaN
+// stays NaN (quiet).
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return uint16_t(0x7fc0u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return uint16_t(u >> 16);
+  return __builtin_bit_cast(uint16_t, (__bf16)f);
 }
 
 __device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {

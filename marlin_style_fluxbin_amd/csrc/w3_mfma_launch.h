@@ -20,7 +20,7 @@ struct ResidualArgs {
   const uint16_t* pro_weight;
   float pro_eps;
 };
-constexpr int kMaxNormPartialsPerLane = 8;  // prologue: K <= 8 * 64 * 16
+constexpr int kMaxNormPartialsPerLane = 4;  // prologue: K <= 4 * 64 * 16
 
 struct MfmaArgs {
   const uint16_t* x;     // [mb, K] activations of this launch
