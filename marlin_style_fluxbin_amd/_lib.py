@@ -15,7 +15,7 @@ from pathlib import Path
 import torch
 
 LIBRARY_PATH = Path(__file__).resolve().parent / "libfluxbin_amd.so"
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 FX_F32, FX_F16, FX_BF16 = 0, 1, 2
 ARITH_STRUCTURAL, ARITH_DECODED_BF16 = 0, 1

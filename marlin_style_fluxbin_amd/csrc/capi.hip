@@ -496,7 +496,7 @@ bool two_base_config(int O, int G, int waves, int prefetch, int groups_per_split
 
 extern "C" {
 
-int fx_abi_version(void) { return 7; }
+int fx_abi_version(void) { return 8; }
 
 const char* fx_last_error(void) { return g_error; }
 
@@ -783,12 +783,16 @@ int fx_head_norm_rope(int ntensors, const void* const* inputs, void* const* outp
   return check_launch("head_norm_rope_kernel");
 }
 
+// Attention workspace: one arrival counter per KV head (at most n_q_heads),
+// padded to 256 bytes, then the fp32 partials [Hq, splits, D + 2].
+size_t attn_counter_bytes(int n_q_heads) { return (size_t(n_q_heads) * sizeof(unsigned) + 255) / 256 * 256; }
+
 size_t fx_decode_attention_workspace_bytes(int n_q_heads, int max_len, int head_dim) {
   if (n_q_heads < 1 || max_len < 1 || (head_dim != 64 && head_dim != 128 && head_dim != 256)) return 0;
   // the most splits any position can use: one key per thread
   const int keys = fx::attn_keys_per_block(head_dim, 1);
   const size_t splits = (size_t(max_len) + keys - 1) / keys;
-  return size_t(n_q_heads) * splits * (size_t(head_dim) + 2) * sizeof(float);
+  return attn_counter_bytes(n_q_heads) + size_t(n_q_heads) * splits * (size_t(head_dim) + 2) * sizeof(float);
 }
 
 namespace {
@@ -810,30 +814,48 @@ int decode_attention(const void* q, const void* k_cache, const void* v_cache, vo
   const size_t need = fx_decode_attention_workspace_bytes(n_q_heads, max_len, head_dim);
   if (!workspace || workspace_bytes < need)
     return fail(FX_EINVAL, "attention workspace needs %zu bytes, got %zu", need, workspace_bytes);
+  if (reinterpret_cast<uintptr_t>(workspace) % 16 != 0) return fail(FX_EINVAL, "workspace must be 16-byte aligned");
   fx::AttnArgs a{};
   a.q = static_cast<const uint16_t*>(q);
   a.k = static_cast<const uint16_t*>(k_cache);
   a.v = static_cast<const uint16_t*>(v_cache);
-  a.partial = static_cast<float*>(workspace);
+  a.arrivals = static_cast<unsigned*>(workspace);
+  a.partial = reinterpret_cast<float*>(static_cast<char*>(workspace) + attn_counter_bytes(n_q_heads));
   a.out = static_cast<uint16_t*>(out);
   a.Hq = n_q_heads;
   a.Hk = n_kv_heads;
   a.Lmax = max_len;
   a.pos = position;
-  // keys per thread: the most (fewest partials to combine) that still gives a
-  // workgroup per CU; one otherwise
-  const int n = position + 1, cus = device_cu_count();
-  a.kpt = 1;
-  for (int kpt : {4, 2}) {
+  // keys per thread: the fewest whose splits the last workgroup of each KV head
+  // can combine inline (one launch); beyond that, the most (fewest partials)
+  // that still gives a workgroup per CU, one otherwise, and the combine kernel
+  const int n = position + 1, cus = device_cu_count(), G = n_q_heads / n_kv_heads;
+  const auto splits_for = [&](int kpt) {
     const int keys = fx::attn_keys_per_block(head_dim, kpt);
-    if (long(n_kv_heads) * ((n + keys - 1) / keys) >= cus) {
-      a.kpt = kpt;
-      break;
-    }
+    return (n + keys - 1) / keys;
+  };
+  a.kpt = 0;
+  if (G * head_dim <= 256 * fx::kAttnInlineOutputs)
+    for (int kpt : {1, 2, 4})
+      if (splits_for(kpt) <= fx::kAttnInlineSplits && G * splits_for(kpt) <= 256) {
+        a.kpt = kpt;
+        break;
+      }
+  if (a.kpt == 0) {
+    a.kpt = 1;
+    for (int kpt : {4, 2})
+      if (long(n_kv_heads) * splits_for(kpt) >= cus) {
+        a.kpt = kpt;
+        break;
+      }
   }
-  const int keys = fx::attn_keys_per_block(head_dim, a.kpt);
-  a.splits = (n + keys - 1) / keys;
+  a.splits = splits_for(a.kpt);
   if (a.splits > 65535) return fail(FX_EINVAL, "position %d needs %d key splits (at most 65535)", position, a.splits);
+  a.combine = a.splits == 1 ? fx::kAttnDirect
+              : a.splits <= fx::kAttnInlineSplits && G * a.splits <= 256 &&
+                        G * head_dim <= 256 * fx::kAttnInlineOutputs
+                  ? fx::kAttnLastArrival
+                  : fx::kAttnCombineKernel;
   a.scale = scale;
   a.pre = pre;
   fx::launch_decode_attention(dtype, head_dim, a, static_cast<hipStream_t>(stream));

@@ -1,5 +1,7 @@
 // Batch-1 decode kernels for gfx950: grouped-query attention over a static KV
-// cache (split over key chunks, then combined), and the SwiGLU activation.
+// cache (split over key chunks, then combined in the same launch by the last
+// workgroup of each KV head, or by a second kernel for long contexts), and the
+// SwiGLU activation.
 //
 // Attention semantics (stock HF Qwen3 attention through SDPA with a boolean
 // mask): for query head h of KV head g = h / (Hq / Hk),
@@ -17,6 +19,16 @@ namespace fx {
 // in registers across passes).
 constexpr int kAttnHeadsPerPass = 4;
 constexpr int kDppRowRor8 = 0x128;  // lane i <- lane (i + 8) mod 16 within each row
+
+// Split partials are stored and read as relaxed device-scope atomics: coherent
+// across the XCDs' L2s without the L2 write-back a device-scope fence costs
+// (one per wave, measured ~19 us per layer at 272 workgroups).
+__device__ __forceinline__ void store_coherent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_coherent(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 // Sum over the DB lanes (8, 16 or 32) that hold one key row; every lane of the
 // group receives the same bits.
@@ -39,7 +51,9 @@ __device__ __forceinline__ float key_row_sum(float v) {
 // never read.  Per pass of up to 4 query heads: s = (q . k) * scale reduced over
 // the DB lanes of the row, chunk max over the workgroup, p = e^(s - m),
 // l = sum p, o = sum p v per thread, reduced over the key rows through LDS.
-// partial[(h * splits + chunk) * (D + 2)] = {m, l, o[0..D)}.
+// partial[(h * splits + chunk) * (D + 2)] = {m, l, o[0..D)}; with one split
+// the output o / l is written instead, and with combine == kAttnLastArrival the
+// KV head's last workgroup to finish combines the partials (arrival counter).
 // PRE: q is the raw projection; each query head is normalised (q_norm) and
 // rotated before scoring, and the key and value of position pos are formed here
 // from the raw projections (k_norm, RoPE; v as is) -- by the workgroup whose
@@ -84,11 +98,12 @@ __device__ __forceinline__ u32x4_t head_norm_rope8(const u32x4_t& x, const u32x4
 template <int DT, int D, int KPT, bool PRE>
 __global__ __launch_bounds__(256) void attn_split_kernel(const uint16_t* __restrict__ q,
                                                          const uint16_t* kc, const uint16_t* vc,
-                                                         float* __restrict__ partial, int Hq, int Hk,
-                                                         int Lmax, int pos, int splits, float scale,
-                                                         AttnPre pre) {
-  asm volatile("" ::"s"(q), "s"(kc), "s"(vc), "s"(partial), "s"(Hq), "s"(Hk), "s"(Lmax), "s"(pos),
-               "s"(splits), "s"(scale));
+                                                         float* partial, unsigned* arrivals,
+                                                         uint16_t* __restrict__ out, int Hq, int Hk,
+                                                         int Lmax, int pos, int splits, int combine,
+                                                         float scale, AttnPre pre) {
+  asm volatile("" ::"s"(q), "s"(kc), "s"(vc), "s"(partial), "s"(arrivals), "s"(out), "s"(Hq), "s"(Hk),
+               "s"(Lmax), "s"(pos), "s"(splits), "s"(combine), "s"(scale));
   if constexpr (PRE)
     asm volatile("" ::"s"(pre.k_raw), "s"(pre.v_raw), "s"(pre.q_weight), "s"(pre.k_weight), "s"(pre.cos),
                  "s"(pre.sin), "s"(pre.eps), "s"(pre.rope_mode));
@@ -260,18 +275,82 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const uint16_t* __restr
 #pragma unroll
       for (int r = 0; r < KS; ++r) total += red_o[r][hh][d];
       if (h < G) {
-        float* out = partial + (size_t(g * G + h) * splits + chunk) * (D + 2);
-        out[2 + d] = total;
-        if (d == 0) {
+        if (combine == kAttnDirect) {
+          // the whole context is this chunk: o = sum p v / sum p
           float l = 0.f;
 #pragma unroll
           for (int r = 0; r < KS; ++r) l += red_l[r][hh];
-          out[0] = mt[hh];
-          out[1] = l;
+          out[size_t(g * G + h) * D + d] = from_f32<DT>(total * (1.f / l));
+        } else {
+          float* dst = partial + (size_t(g * G + h) * splits + chunk) * (D + 2);
+          store_coherent(dst + 2 + d, total);
+          if (d == 0) {
+            float l = 0.f;
+#pragma unroll
+            for (int r = 0; r < KS; ++r) l += red_l[r][hh];
+            store_coherent(dst, mt[hh]);
+            store_coherent(dst + 1, l);
+          }
         }
       }
     }
     __syncthreads();  // LDS reused by the next pass
+  }
+  if (combine != kAttnLastArrival) return;
+
+  // ---- the last workgroup of this KV head to finish combines its G heads:
+  // o_h = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c over the S splits.
+  // Each wave waits for its device-scope partial stores to complete before the
+  // workgroup's arrival is counted (a device-scope atomic), and the last
+  // arrival reads the partials with device-scope loads issued after the count
+  // returned.  The counter is left at zero for the next call.
+  __shared__ int is_last;
+  __shared__ float cm[256], cl[256];
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (t == 0)
+    is_last = __hip_atomic_fetch_add(arrivals + g, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+              unsigned(splits - 1);
+  __syncthreads();
+  if (!is_last) return;
+  // one load round: every (split, dim) value this thread combines, issued
+  // behind the splits' maxima and sums (the host keeps S <= kAttnInlineSplits,
+  // G * S <= 256 and G * D <= 256 * kAttnInlineOutputs)
+  const int S = splits;
+  const float* base = partial + size_t(g) * G * S * (D + 2);  // [G, S, D + 2]
+  if (t < G * S) {
+    cm[t] = load_coherent(base + size_t(t) * (D + 2));
+    cl[t] = load_coherent(base + size_t(t) * (D + 2) + 1);
+  }
+  constexpr int R = kAttnInlineOutputs, C = kAttnInlineSplits;
+  float v[R][C];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int idx = t + 256 * r, hh = idx / D, d = idx % D;
+#pragma unroll
+    for (int c = 0; c < C; ++c)
+      v[r][c] = idx < G * D && c < S ? load_coherent(base + size_t(hh * S + c) * (D + 2) + 2 + d) : 0.f;
+  }
+  __syncthreads();
+  if (t == 0) __hip_atomic_store(arrivals + g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int idx = t + 256 * r, hh = idx / D, d = idx % D;
+    if (idx >= G * D) break;
+    const float* mh = cm + hh * S;
+    const float* lh = cl + hh * S;
+    float M = -INFINITY;
+    for (int c = 0; c < S; ++c) M = fmaxf(M, mh[c]);
+    float L = 0.f, o = 0.f;
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      if (c < S) {
+        const float w = __expf(mh[c] - M);
+        L += w * lh[c];
+        o += w * v[r][c];
+      }
+    }
+    out[size_t(g * G + hh) * D + d] = from_f32<DT>(o * (1.f / L));
   }
 }
 
@@ -357,11 +436,14 @@ template <int DT, int D, int KPT>
 void attn_launch(const AttnArgs& a, hipStream_t s) {
   if (a.pre.k_raw)
     hipLaunchKernelGGL((attn_split_kernel<DT, D, KPT, true>), dim3(a.Hk, a.splits), dim3(256), 0, s, a.q, a.k,
-                       a.v, a.partial, a.Hq, a.Hk, a.Lmax, a.pos, a.splits, a.scale, a.pre);
+                       a.v, a.partial, a.arrivals, a.out, a.Hq, a.Hk, a.Lmax, a.pos, a.splits, a.combine,
+                       a.scale, a.pre);
   else
     hipLaunchKernelGGL((attn_split_kernel<DT, D, KPT, false>), dim3(a.Hk, a.splits), dim3(256), 0, s, a.q, a.k,
-                       a.v, a.partial, a.Hq, a.Hk, a.Lmax, a.pos, a.splits, a.scale, a.pre);
-  hipLaunchKernelGGL((attn_combine_kernel<DT, D>), dim3(a.Hq), dim3(256), 0, s, a.partial, a.out, a.splits);
+                       a.v, a.partial, a.arrivals, a.out, a.Hq, a.Hk, a.Lmax, a.pos, a.splits, a.combine,
+                       a.scale, a.pre);
+  if (a.combine == kAttnCombineKernel)
+    hipLaunchKernelGGL((attn_combine_kernel<DT, D>), dim3(a.Hq), dim3(256), 0, s, a.partial, a.out, a.splits);
 }
 
 template <int DT, int D>

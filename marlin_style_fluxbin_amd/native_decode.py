@@ -278,7 +278,7 @@ class NativeDecodeSession:
         lib = _lib.library()
         self.lib = lib
         nbytes = lib.fx_decode_attention_workspace_bytes(self.heads, self.maximum_length, self.head_dim)
-        self.attn_ws = torch.empty(nbytes // 4 + 64, dtype=torch.float32, device=self.device)
+        self.attn_ws = torch.zeros(nbytes // 4 + 64, dtype=torch.float32, device=self.device)  # arrival counters start at zero
         self.graph = None
         self.kernel_nodes = None
         self.launches_per_step = None
@@ -286,7 +286,7 @@ class NativeDecodeSession:
     # -- one token -------------------------------------------------------------------
     def _attention(self, layer, pos):
         """q/k RMSNorm + RoPE, the KV-cache write of position ``pos`` and the
-        attention, from the raw q|k|v projections (one split + one combine launch)."""
+        attention, from the raw q|k|v projections (one launch at decode lengths)."""
         lib = self.lib
         _lib.check(lib.fx_decode_attention_rope(
             self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), self.q_norm[layer].data_ptr(),

@@ -44,7 +44,7 @@ def test_decode_attention(gpu, dtype, hq, hk, d, lmax, pos):
     vc[:, pos + 1:] = float("nan")
     lib = _lib.library()
     nbytes = lib.fx_decode_attention_workspace_bytes(hq, lmax, d)
-    ws = torch.empty(nbytes, dtype=torch.uint8, device=gpu)
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device=gpu)
     out = torch.empty(hq, d, dtype=DT[dtype], device=gpu)
     qd, kd, vd = q.to(gpu), kc.to(gpu), vc.to(gpu)
     _lib.check(lib.fx_decode_attention(qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), ws.data_ptr(), nbytes,
@@ -79,7 +79,7 @@ def test_decode_attention_rope(gpu, dtype, hq, hk, d, lmax, pos, rope_mode):
     vc[:, pos:] = float("nan")
     lib = _lib.library()
     nbytes = lib.fx_decode_attention_workspace_bytes(hq, lmax, d)
-    ws = torch.empty(nbytes, dtype=torch.uint8, device=gpu)
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device=gpu)
     out = torch.empty(hq, d, dtype=DT[dtype], device=gpu)
     dev = {n: t.to(gpu) for n, t in dict(q=q, k=k, v=v, qw=qw, kw=kw, kc=kc, vc=vc).items()}
     cos_d = torch.from_numpy(cos_t[0]).to(DT[dtype]).to(gpu)
@@ -107,6 +107,34 @@ def test_decode_attention_rope(gpu, dtype, hq, hk, d, lmax, pos, rope_mode):
     # two output ulps, plus what a one-ulp change of a normalised q/k element can move
     assert np.all(np.abs(got - exact) <= 3 * _ulp(exact, dtype) + 1e-2 * np.abs(exact).max())
     assert np.mean(np.abs(got - exact) <= 2 * _ulp(exact, dtype) + 1e-6 * np.abs(exact).max()) > 0.98
+
+
+@pytest.mark.parametrize("hq,hk", [(32, 8), (12, 2)])
+def test_decode_attention_workspace_reuse(gpu, hq, hk):
+    """One zero-filled workspace serves a run of calls whose split counts pick
+    every combine form: one chunk written directly (pos 0..15), partials combined
+    by the last workgroup of each KV head (up to 16 chunks), the combine kernel
+    beyond (pos 1099).  The arrival counters at the workspace's start are zero
+    after each call."""
+    d, lmax = 128, 1100
+    g = torch.Generator().manual_seed(7)
+    q = torch.randn(hq, d, generator=g).to(torch.bfloat16)
+    kc = torch.randn(hk, lmax, d, generator=g).to(torch.bfloat16)
+    vc = torch.randn(hk, lmax, d, generator=g).to(torch.bfloat16)
+    lib = _lib.library()
+    nbytes = lib.fx_decode_attention_workspace_bytes(hq, lmax, d)
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device=gpu)
+    out = torch.empty(hq, d, dtype=torch.bfloat16, device=gpu)
+    qd, kd, vd = q.to(gpu), kc.to(gpu), vc.to(gpu)
+    qf, kf, vf = q.float().numpy(), kc.float().numpy(), vc.float().numpy()
+    for pos in [5, 300, 15, 16, 900, 511, 1099, 40, 700]:
+        _lib.check(lib.fx_decode_attention(qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), ws.data_ptr(), nbytes,
+                                           out.data_ptr(), hq, hk, lmax, d, pos, 1 / np.sqrt(d),
+                                           _lib.dtype_code(torch.bfloat16), _lib.stream_handle(gpu)), "attention")
+        exact = decode.gqa_attention(qf, kf, vf, pos, 1 / np.sqrt(d))
+        got = out.float().cpu().numpy()
+        assert np.all(np.abs(got - exact) <= 2 * _ulp(exact, "bf16") + 1e-6 * np.abs(exact).max()), pos
+        assert not ws[:4 * hk].any().item(), pos
 
 
 def test_decode_attention_rejects_bad_position(gpu):
