@@ -221,6 +221,28 @@ int fx_decode_attention_rope(const void *q, const void *k, const void *v, const 
 int fx_silu_mul(const void *gate, const void *up, void *out, int n, int dtype, void *stream);
 
 /*
+ * End of a greedy decode step in one launch: the final RMSNorm, the LM head and
+ * the argmax that the reference's decode runs as model.norm, lm_head and
+ * logits.argmax(-1, keepdim=True) (static_decode.py:67-76).
+ *   x = round(norm_weight * round(hidden * rsqrt(mean(hidden^2) + eps)))
+ *       (norm_weight NULL: x = hidden, already normalised)
+ *   logits[v] = round(weight[v, :] . x), fp32 accumulation, v < vocab
+ *   *prediction = argmax of the rounded logits: the first index of the maximum,
+ *                 a NaN above every number (torch.argmax)
+ * hidden / norm_weight [hidden_size], weight [vocab, hidden_size] row-major,
+ * logits [vocab], all in `dtype`; hidden_size a multiple of 512 up to 8192;
+ * hidden, norm_weight, weight 16-byte aligned, logits 2-byte aligned.  The
+ * normalised x is bit-identical to fx_rmsnorm's.  `workspace`
+ * (fx_lm_head_argmax_workspace_bytes, 16-byte aligned): allocate it zero-filled
+ * once; every call leaves its arrival counter at zero.  Calls sharing a
+ * workspace must not overlap.
+ */
+size_t fx_lm_head_argmax_workspace_bytes(void);
+int fx_lm_head_argmax(const void *hidden, const void *norm_weight, float eps, const void *weight, void *logits,
+                      long long *prediction, void *workspace, size_t workspace_bytes, int vocab,
+                      int hidden_size, int dtype, void *stream);
+
+/*
  * Two-base binary-basis GEMV, rank-one format with salient columns, batch 1:
  * the benchmark's config-4 form of the reference's two-base M=1 GEMV
  * (deployment.py:168-179 m1_out -> csrc/m1_v5.cu:26-104 lut_m1; same

@@ -15,7 +15,7 @@ from pathlib import Path
 import torch
 
 LIBRARY_PATH = Path(__file__).resolve().parent / "libfluxbin_amd.so"
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 FX_F32, FX_F16, FX_BF16 = 0, 1, 2
 ARITH_STRUCTURAL, ARITH_DECODED_BF16 = 0, 1
@@ -49,6 +49,8 @@ SIGNATURES: dict[str, tuple] = {
     "fx_decode_attention": (_i, [_p, _p, _p, _p, _sz, _p, _i, _i, _i, _i, _i, _f, _i, _p]),
     "fx_decode_attention_rope": (_i, [_p, _p, _p, _p, _p, _p, _p, ctypes.c_float, _i, _p, _p, _p, _sz, _p, _i, _i, _i, _i, _i, ctypes.c_float, _i, _p]),
     "fx_silu_mul": (_i, [_p, _p, _p, _i, _i, _p]),
+    "fx_lm_head_argmax_workspace_bytes": (_sz, []),
+    "fx_lm_head_argmax": (_i, [_p, _p, _f, _p, _p, _p, _p, _sz, _i, _i, _i, _p]),
     "fx_two_base_gemv_workspace_bytes": (_sz, [_i, _i]),
     "fx_two_base_gemv": (_i, [_p, _i, _p, _p, _p, _p, _p, _p, _i, _p, _sz, _p, _i, _i, _p]),
     "fx_two_base_gemv_config_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _i]),

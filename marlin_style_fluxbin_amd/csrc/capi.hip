@@ -14,6 +14,7 @@
 #include "w3_mfma_launch.h"
 #include "norms_launch.h"
 #include "decode_launch.h"
+#include "lm_head_launch.h"
 #include "two_base_launch.h"
 
 using fx::LutArgs;
@@ -496,7 +497,7 @@ bool two_base_config(int O, int G, int waves, int prefetch, int groups_per_split
 
 extern "C" {
 
-int fx_abi_version(void) { return 8; }
+int fx_abi_version(void) { return 9; }
 
 const char* fx_last_error(void) { return g_error; }
 
@@ -890,6 +891,53 @@ int fx_decode_attention_rope(const void* q, const void* k, const void* v, const 
                   static_cast<const uint16_t*>(cos), static_cast<const uint16_t*>(sin), eps, rope_mode};
   return decode_attention(q, k_cache, v_cache, workspace, workspace_bytes, out, n_q_heads, n_kv_heads, max_len,
                           head_dim, position, scale, dtype, stream, pre);
+}
+
+// LM head: two workgroups per CU (8 waves, two 8 KB rows in flight per wave at
+// hidden 4096), fewer when the vocabulary has fewer row pairs.
+constexpr int kLmBlocksPerCu = 2;
+
+size_t fx_lm_head_argmax_workspace_bytes(void) {
+  return fx::kLmCounterBytes + size_t(fx::kLmMaxBlocks) * (sizeof(float) + sizeof(int));
+}
+
+int fx_lm_head_argmax(const void* hidden, const void* norm_weight, float eps, const void* weight, void* logits,
+                      long long* prediction, void* workspace, size_t workspace_bytes, int vocab,
+                      int hidden_size, int dtype, void* stream) {
+  if (!hidden || !weight || !logits || !prediction || !workspace)
+    return fail(FX_EINVAL, "hidden, weight, logits, prediction and workspace must be non-null");
+  if (!is_half_dtype(dtype)) return fail(FX_EINVAL, "dtype must be fp16 or bf16");
+  if (hidden_size < 512 || hidden_size > 512 * fx::kLmMaxChunks || hidden_size % 512)
+    return fail(FX_EINVAL, "hidden size must be a multiple of 512 in [512, %d], got %d", 512 * fx::kLmMaxChunks,
+                hidden_size);
+  if (vocab < 1) return fail(FX_EINVAL, "vocab must be positive, got %d", vocab);
+  const void* vec[3] = {hidden, norm_weight, weight};
+  for (const void* p : vec)
+    if (reinterpret_cast<uintptr_t>(p) % 16 != 0)
+      return fail(FX_EINVAL, "hidden, norm weight and weight must be 16-byte aligned");
+  if (reinterpret_cast<uintptr_t>(logits) % 2 != 0) return fail(FX_EINVAL, "logits must be 2-byte aligned");
+  if (reinterpret_cast<uintptr_t>(prediction) % 8 != 0) return fail(FX_EINVAL, "prediction must be 8-byte aligned");
+  if (reinterpret_cast<uintptr_t>(workspace) % 16 != 0) return fail(FX_EINVAL, "workspace must be 16-byte aligned");
+  const size_t need = fx_lm_head_argmax_workspace_bytes();
+  if (workspace_bytes < need)
+    return fail(FX_EINVAL, "LM-head workspace needs %zu bytes, got %zu", need, workspace_bytes);
+  fx::LmHeadArgs a{};
+  a.x = static_cast<const uint16_t*>(hidden);
+  a.norm_w = static_cast<const uint16_t*>(norm_weight);
+  a.eps = eps;
+  a.w = static_cast<const uint16_t*>(weight);
+  a.logits = static_cast<uint16_t*>(logits);
+  a.prediction = prediction;
+  a.arrival = static_cast<unsigned*>(workspace);
+  a.part_val = reinterpret_cast<float*>(static_cast<char*>(workspace) + fx::kLmCounterBytes);
+  a.part_idx = reinterpret_cast<int*>(a.part_val + fx::kLmMaxBlocks);
+  a.V = vocab;
+  a.K = hidden_size;
+  const long pairs = (long(vocab) + 1) / 2;
+  a.blocks = int(std::min<long>({long(fx::kLmMaxBlocks), long(kLmBlocksPerCu) * device_cu_count(),
+                                 (pairs + fx::kLmWaves - 1) / fx::kLmWaves}));
+  fx::launch_lm_head_argmax(dtype, a, static_cast<hipStream_t>(stream));
+  return check_launch("lm_head_argmax_kernel");
 }
 
 int fx_silu_mul(const void* gate, const void* up, void* out, int n, int dtype, void* stream) {

@@ -1,0 +1,213 @@
+// Batch-1 LM head of the greedy decode step for gfx950, with the final RMSNorm
+// and the argmax folded in: the reference's decode step ends in the model's
+// final norm, `lm_head` and `logits.argmax(-1, keepdim=True)`
+// (static_decode.py:67-76; HF Qwen3ForCausalLM with logits_to_keep=1).
+//
+//   x      = round(w_norm * round(h * rsqrt(mean(h^2) + eps)))   (Qwen3RMSNorm)
+//   logits = round(W x)          W [V, K] row-major, fp32 accumulation
+//   pred   = argmax(logits)      over the rounded logits, first index of the
+//                                maximum, NaN above every number (torch.argmax)
+//
+// HBM-bound: the weight (V K 2 bytes, 1.24 GB for Qwen3-8B) is streamed once per
+// token with non-temporal loads; everything else is a few KB.
+#include "common.h"
+#include "lm_head_launch.h"
+
+#include <climits>
+
+namespace fx {
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+
+// a.lo * b.lo + a.hi * b.hi + c in fp32 (v_dot2c_f32_bf16 / v_dot2c_f32_f16)
+template <int DT>
+__device__ __forceinline__ float dot2(unsigned a, unsigned b, float c) {
+  if constexpr (DT == kBF16)
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c,
+                                           false);
+  else
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, a), __builtin_bit_cast(f16x2_t, b), c, false);
+}
+
+// (v, i) ranks above (u, j): NaN above every number (the first NaN wins),
+// otherwise the larger value, ties to the lower index.  A strict total order
+// over distinct indices, so merges in any order give the same winner.
+__device__ __forceinline__ bool ranks_above(float v, int i, float u, int j) {
+  const bool vn = v != v, un = u != u;
+  if (vn || un) return vn && (!un || i < j);
+  return v > u || (v == u && i < j);
+}
+
+// grid `blocks` workgroups of 4 waves; wave w of the grid takes the row pairs
+// (2p, 2p + 1), p = w, w + waves, ... (neighbouring waves stream neighbouring
+// rows).  Lane l holds elements [8 (64 c + l), +8) of the activation for each
+// 512-element chunk c, so a weight row is NC loads of 16 B per lane, coalesced.
+// Every wave normalises the activation itself (the RMSNorm batch order of
+// rmsnorm_kernel: per-chunk wave totals added in chunk order; bit-identical
+// normalised values).  Each wave keeps its running argmax; the workgroup's
+// best goes to the workspace as a device-scope atomic store and the last
+// workgroup to arrive (device-scope counter) merges every workgroup's best in
+// one load round, writes the prediction and resets the counter to zero.
+template <int DT, int NC, bool NORM>
+__global__ __launch_bounds__(256) void lm_head_argmax_kernel(LmHeadArgs a) {
+  asm volatile("" ::"s"(a.x), "s"(a.norm_w), "s"(a.eps), "s"(a.w), "s"(a.logits), "s"(a.prediction),
+               "s"(a.arrival), "s"(a.part_val), "s"(a.part_idx), "s"(a.V));
+  constexpr int K = NC * 512;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+
+  u32x4_t xv[NC];
+  {
+    const u32x4_t* xp = reinterpret_cast<const u32x4_t*>(a.x) + lane;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) xv[c] = xp[64 * c];
+  }
+  if constexpr (NORM) {
+    const u32x4_t* wp = reinterpret_cast<const u32x4_t*>(a.norm_w) + lane;
+    u32x4_t wv[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) wv[c] = wp[64 * c];
+    float ss = 0.f;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) ss += wave_total(sum_sq8<DT>(xv[c]));
+    const float inv = rsqrtf(ss / float(K) + a.eps);
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const float n0 = round_to<DT>(to_f32<DT>(uint16_t(xv[c][w])) * inv);
+        const float n1 = round_to<DT>(to_f32<DT>(uint16_t(xv[c][w] >> 16)) * inv);
+        const float y0 = to_f32<DT>(uint16_t(wv[c][w])) * n0;
+        const float y1 = to_f32<DT>(uint16_t(wv[c][w] >> 16)) * n1;
+        xv[c][w] = unsigned(from_f32<DT>(y0)) | (unsigned(from_f32<DT>(y1)) << 16);
+      }
+    }
+  }
+
+  float best = -INFINITY;
+  int best_i = INT_MAX;
+  const int waves = gridDim.x * kLmWaves, pairs = (a.V + 1) / 2;
+  for (int p = blockIdx.x * kLmWaves + wave; p < pairs; p += waves) {
+    const int r0 = 2 * p, r1 = min(r0 + 1, a.V - 1);  // an odd V's last pair reads row V - 1 twice
+    const u32x4_t* w0 = reinterpret_cast<const u32x4_t*>(a.w + size_t(r0) * K) + lane;
+    const u32x4_t* w1 = reinterpret_cast<const u32x4_t*>(a.w + size_t(r1) * K) + lane;
+    u32x4_t b0[NC], b1[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) b0[c] = __builtin_nontemporal_load(w0 + 64 * c);
+#pragma unroll
+    for (int c = 0; c < NC; ++c) b1[c] = __builtin_nontemporal_load(w1 + 64 * c);
+    __builtin_amdgcn_sched_barrier(0);  // both rows' loads in flight before the first use
+    float s0[2] = {0.f, 0.f}, s1[2] = {0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        s0[w & 1] = dot2<DT>(b0[c][w], xv[c][w], s0[w & 1]);
+        s1[w & 1] = dot2<DT>(b1[c][w], xv[c][w], s1[w & 1]);
+      }
+    const float y0 = round_to<DT>(wave_total(s0[0] + s0[1]));
+    const float y1 = round_to<DT>(wave_total(s1[0] + s1[1]));
+    if (lane == 0) a.logits[r0] = from_f32<DT>(y0);
+    if (lane == 1 && r1 != r0) a.logits[r1] = from_f32<DT>(y1);
+    if (ranks_above(y0, r0, best, best_i)) {
+      best = y0;
+      best_i = r0;
+    }
+    if (r1 != r0 && ranks_above(y1, r1, best, best_i)) {
+      best = y1;
+      best_i = r1;
+    }
+  }
+
+  __shared__ float wbest[kLmWaves];
+  __shared__ int wbest_i[kLmWaves];
+  __shared__ int is_last;
+  if (lane == 0) {
+    wbest[wave] = best;
+    wbest_i[wave] = best_i;
+  }
+  __syncthreads();
+  if (t == 0) {
+    float v = wbest[0];
+    int i = wbest_i[0];
+#pragma unroll
+    for (int w = 1; w < kLmWaves; ++w)
+      if (ranks_above(wbest[w], wbest_i[w], v, i)) {
+        v = wbest[w];
+        i = wbest_i[w];
+      }
+    __hip_atomic_store(a.part_val + blockIdx.x, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(a.part_idx + blockIdx.x, i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);  // both stores complete before the arrival counts
+    is_last = __hip_atomic_fetch_add(a.arrival, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+              gridDim.x - 1;
+  }
+  __syncthreads();
+  if (!is_last) return;
+
+  constexpr int Q = kLmMaxBlocks / 256;
+  float pv[Q];
+  int pi[Q];
+#pragma unroll
+  for (int q = 0; q < Q; ++q) {
+    const int b = t + 256 * q;
+    const bool on = b < int(gridDim.x);
+    pv[q] = on ? __hip_atomic_load(a.part_val + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : -INFINITY;
+    pi[q] = on ? __hip_atomic_load(a.part_idx + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : INT_MAX;
+  }
+  float v = pv[0];
+  int i = pi[0];
+#pragma unroll
+  for (int q = 1; q < Q; ++q)
+    if (ranks_above(pv[q], pi[q], v, i)) {
+      v = pv[q];
+      i = pi[q];
+    }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(v, o, 64);
+    const int oi = __shfl_xor(i, o, 64);
+    if (ranks_above(ov, oi, v, i)) {
+      v = ov;
+      i = oi;
+    }
+  }
+  if (lane == 0) {
+    wbest[wave] = v;
+    wbest_i[wave] = i;
+  }
+  __syncthreads();
+  if (t == 0) {
+#pragma unroll
+    for (int w = 1; w < kLmWaves; ++w)
+      if (ranks_above(wbest[w], wbest_i[w], v, i)) {
+        v = wbest[w];
+        i = wbest_i[w];
+      }
+    *a.prediction = i;
+    __hip_atomic_store(a.arrival, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+template <int DT, int NC>
+bool lm_dispatch(int nc, const LmHeadArgs& a, hipStream_t s) {
+  if constexpr (NC > kLmMaxChunks) {
+    return false;
+  } else {
+    if (nc != NC) return lm_dispatch<DT, NC + 1>(nc, a, s);
+    if (a.norm_w)
+      hipLaunchKernelGGL((lm_head_argmax_kernel<DT, NC, true>), dim3(a.blocks), dim3(256), 0, s, a);
+    else
+      hipLaunchKernelGGL((lm_head_argmax_kernel<DT, NC, false>), dim3(a.blocks), dim3(256), 0, s, a);
+    return true;
+  }
+}
+
+bool launch_lm_head_argmax(int dt, const LmHeadArgs& a, hipStream_t s) {
+  if (a.K % 512 != 0) return false;
+  if (dt == kBF16) return lm_dispatch<kBF16, 1>(a.K / 512, a, s);
+  if (dt == kF16) return lm_dispatch<kF16, 1>(a.K / 512, a, s);
+  return false;
+}
+
+}  // namespace fx

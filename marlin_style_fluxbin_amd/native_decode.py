@@ -4,16 +4,19 @@ Same protocol and interface as :class:`static_decode.StaticDecodeSession`
 (reference ``static_decode.py:26-138``): prefill the real prefix (through the HF
 model and its dense fallback), keep the prefix KV, decode a fixed continuation,
 capture all steps in one hipGraph, time a replay.  What differs is the step:
-instead of the HF module tree (~27 kernels per layer) each decoder layer is
+instead of the HF module tree (~27 kernels per layer) each decoder layer is,
+with structural W3 Linears,
 
-    add+RMSNorm -> q|k|v GEMV -> attention with q/k norm, RoPE and the KV-cache
-    write folded in (split + combine) -> o GEMV -> add+RMSNorm -> gate|up GEMV
-    with SwiGLU -> down GEMV
+    q|k|v GEMV normalising the residual -> attention with q/k norm, RoPE, the
+    KV-cache write and the split combine folded in -> o GEMV adding into the
+    residual -> gate|up GEMV normalising, with SwiGLU -> down GEMV adding into
+    the residual
 
-(8 launches with W3 Linears), followed once per token by the final add+RMSNorm,
-the bf16 LM head (hipBLASLt) and argmax.  The arithmetic and rounding points are
-the stock HF Qwen3 modules' (RMSNorm, RoPE, SDPA with fp32 softmax, SwiGLU); W3
-Linears run the MFMA GEMV, dense Linears ``torch.matmul`` (the bf16 arm).
+(5 launches), followed once per token by one launch for the final RMSNorm, the
+bf16 LM head and the argmax.  Other Linears (the bf16 arm) take add+RMSNorm
+kernels and ``torch.matmul`` between the same attention launches.  The
+arithmetic and rounding points are the stock HF Qwen3 modules' (RMSNorm, RoPE,
+SDPA with fp32 softmax, SwiGLU).
 """
 from __future__ import annotations
 
@@ -277,6 +280,13 @@ class NativeDecodeSession:
         self.predictions = torch.empty((self.steps, 1), dtype=torch.int64, device=self.device)
         lib = _lib.library()
         self.lib = lib
+        # the final RMSNorm, LM head and argmax as one launch where the head allows it
+        head = self.lm_head
+        self.lm_ws = None
+        if (head.dtype == dtype and head.is_contiguous() and head.data_ptr() % 16 == 0
+                and self.hidden % 512 == 0 and self.hidden <= 8192):
+            self.lm_ws = torch.zeros(lib.fx_lm_head_argmax_workspace_bytes(), dtype=torch.uint8,
+                                     device=self.device)  # arrival counter starts at zero
         nbytes = lib.fx_decode_attention_workspace_bytes(self.heads, self.maximum_length, self.head_dim)
         self.attn_ws = torch.zeros(nbytes // 4 + 64, dtype=torch.float32, device=self.device)  # arrival counters start at zero
         self.graph = None
@@ -295,6 +305,26 @@ class NativeDecodeSession:
             self.attn_ws.data_ptr(), self.attn_ws.numel() * 4, self.attn.data_ptr(), self.heads, self.kv_heads,
             self.maximum_length, self.head_dim, pos, self.scale, _lib.dtype_code(self.dtype),
             _lib.stream_handle(self.device)), "fx_decode_attention_rope")
+
+    def _lm_head(self, i, hidden, norm_weight):
+        """Logits row ``i`` and its greedy token from the last hidden state
+        (``norm_weight`` set: RMS-normalised first).  One launch
+        (``fx_lm_head_argmax``) where the head allows it; else RMSNorm, the
+        hipBLASLt matmul and torch.argmax."""
+        if self.lm_ws is not None:
+            _lib.check(self.lib.fx_lm_head_argmax(
+                hidden.data_ptr(), None if norm_weight is None else norm_weight.data_ptr(), self.eps,
+                self.lm_head.data_ptr(), self.logits[i].data_ptr(), self.predictions[i].data_ptr(),
+                self.lm_ws.data_ptr(), self.lm_ws.numel(), self.logits.shape[1], self.hidden,
+                _lib.dtype_code(self.dtype), _lib.stream_handle(self.device)), "fx_lm_head_argmax")
+            return
+        from .fused_modules import rms_norm
+
+        if norm_weight is not None:
+            rms_norm(hidden, norm_weight, self.eps, out=self.normed)
+            hidden = self.normed
+        torch.matmul(hidden, self.lm_head.t(), out=self.logits[i:i + 1])
+        torch.argmax(self.logits[i:i + 1], dim=-1, keepdim=True, out=self.predictions[i:i + 1])
 
     def _silu_mul(self):
         _lib.check(self.lib.fx_silu_mul(self.gate.data_ptr(), self.up.data_ptr(), self.act.data_ptr(),
@@ -321,9 +351,7 @@ class NativeDecodeSession:
             rs.normed(sw.layout, sw.scale_code, sw.zeros_ptr, 2 * sw.width, self.residual, self.post_norm[l],
                       self.eps, self.act, True)
             rs.residual(lin["mlp.down_proj"].gemv, self.act, self.residual)
-        rms_norm(self.residual, self.final_norm, self.eps, out=self.normed)
-        torch.matmul(self.normed, self.lm_head.t(), out=self.logits[i:i + 1])
-        torch.argmax(self.logits[i:i + 1], dim=-1, keepdim=True, out=self.predictions[i:i + 1])
+        self._lm_head(i, self.residual, self.final_norm)
 
     def _step(self, i):
         if self.stream is not None:
@@ -359,8 +387,7 @@ class NativeDecodeSession:
             lin["mlp.down_proj"](self.act, self.down)
         add_rms_norm(self.down, self.residual, self.final_norm, self.eps, out=self.normed,
                      residual_out=self.residual)
-        torch.matmul(self.normed, self.lm_head.t(), out=self.logits[i:i + 1])
-        torch.argmax(self.logits[i:i + 1], dim=-1, keepdim=True, out=self.predictions[i:i + 1])
+        self._lm_head(i, self.normed, None)
 
     # -- session protocol --------------------------------------------------------------
     @torch.inference_mode()
