@@ -479,11 +479,11 @@ __device__ __forceinline__ void w3_mfma_body(
 // stored.  x is [MB, 128 G] row-major; with PERM, sorted column k reads x
 // column perm[k].  swiglu != 0 (MB = 1, one split, O even): the payload's rows
 // interleave gate and up rows, and out receives SiLU(gate) * up, O / 2 values.
-// One-row, one-tile instantiations (the decode shapes) are held to 80 VGPRs, six
-// waves per SIMD: a 24576-row gate|up grid of 4-wave workgroups then fits in one
-// residency round.
+// One-row, one-tile, single-prefetch instantiations (the decode shapes) are held
+// to 80 VGPRs, six waves per SIMD: a 24576-row gate|up grid of 4-wave workgroups
+// then fits in one residency round.
 template <int NW, int PD, int MB, int RT, bool PERM, int XDT, int SDT, bool NORMIN = false>
-__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(MB == 1 && RT == 1 ? 6 : 1)))
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(MB == 1 && RT == 1 && PD == 1 ? 6 : 1)))
 void w3_mfma_kernel(
     const uint16_t* __restrict__ x, const int16_t* __restrict__ perm,
     const uint8_t* __restrict__ planes, const uint16_t* __restrict__ scales,
