@@ -368,6 +368,88 @@ def decode_bench(layers=36, prefix=512, steps=32, replays=5, seed=0):
             "w3_speedup_vs_bf16_hf": round(w3["hf"]["tokens_per_s"] / bf16["hf"]["tokens_per_s"], 3)}
 
 
+def decode_native_only(layers=36, prefix=512, steps=32, replays=3, seed=0):
+    """The config-3 W3 native decode arm alone (no HF arms, no parity audit):
+    the workload for a kernel trace of the decode step.  Same model, prefix and
+    token protocol as decode_bench; the fed tokens are random instead of a
+    greedy trace (the kernels and their shapes are the same)."""
+    import statistics
+
+    import torch
+
+    from marlin_style_fluxbin_amd.native_decode import NativeDecodeSession
+    from marlin_style_fluxbin_amd.qwen3 import qwen3_config, random_qwen3_model, w3_quantize_qwen3_model
+
+    device = torch.device("cuda:0")
+    config = qwen3_config(num_hidden_layers=layers)
+    model = random_qwen3_model(config, device=device, dtype=torch.bfloat16, seed=seed)
+    w3_quantize_qwen3_model(model)
+    g = torch.Generator().manual_seed(seed)
+    ids = torch.randint(0, config.vocab_size, (1, prefix), generator=g).to(device)
+    tokens = torch.randint(0, config.vocab_size, (1, steps), generator=g).to(device)
+    with torch.inference_mode():
+        session = NativeDecodeSession(model, ids, tokens)
+        session.capture()
+        samples = [session.measure("sequence_graph")[0]["device_ms"] for _ in range(replays)]
+        head = lm_head_timing(session)
+    ms = statistics.median(samples)
+    return {"workload": f"config 3 W3 native arm: {layers} layers, prefill {prefix}, {steps} steps",
+            "tokens_per_s": round(steps / (ms / 1e3), 2), "ms_per_token": round(ms / steps, 4),
+            "graph_ms": [round(v, 3) for v in samples],
+            "kernels_per_token": round(session.kernel_nodes / steps, 1), "lm_head": head}
+
+
+def lm_head_timing(session, calls=20, reps=3):
+    """The decode step's last launch alone on the session's resident LM-head
+    weight: fx_lm_head_argmax (final RMSNorm + head + argmax) against hipBLASLt
+    torch.matmul + torch.argmax of the same normalised row; HIP events around
+    ``calls`` back-to-back calls on the current stream, best of ``reps``."""
+    import torch
+
+    from marlin_style_fluxbin_amd import _lib
+    from marlin_style_fluxbin_amd.fused_modules import rms_norm
+
+    weight, lib = session.lm_head, session.lib
+    vocab, hidden = weight.shape
+    h = session.residual
+    logits = torch.empty(vocab, dtype=weight.dtype, device=weight.device)
+    pred = torch.empty(1, dtype=torch.int64, device=weight.device)
+    ws = torch.zeros(lib.fx_lm_head_argmax_workspace_bytes(), dtype=torch.uint8, device=weight.device)
+    normed = rms_norm(h, session.final_norm, session.eps)
+    out = torch.empty(1, vocab, dtype=weight.dtype, device=weight.device)
+    p2 = torch.empty(1, 1, dtype=torch.int64, device=weight.device)
+    stream = _lib.stream_handle(weight.device)
+
+    def fused():
+        _lib.check(lib.fx_lm_head_argmax(h.data_ptr(), session.final_norm.data_ptr(), session.eps, weight.data_ptr(),
+                                         logits.data_ptr(), pred.data_ptr(), ws.data_ptr(), ws.numel(), vocab,
+                                         hidden, _lib.dtype_code(weight.dtype), stream), "fx_lm_head_argmax")
+
+    def library():
+        torch.matmul(normed, weight.t(), out=out)
+        torch.argmax(out, dim=-1, keepdim=True, out=p2)
+
+    result = {"shape": [vocab, hidden], "bytes": vocab * hidden * weight.element_size()}
+    for name, fn in (("fused_us", fused), ("hipblaslt_argmax_us", library)):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        best = float("inf")
+        for _ in range(reps):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            for _ in range(calls):
+                fn()
+            b.record()
+            torch.cuda.synchronize()
+            best = min(best, a.elapsed_time(b) * 1e3 / calls)
+        result[name] = round(best, 1)
+    result["fused_tb_per_s"] = round(result["bytes"] / (result["fused_us"] * 1e-6) / 1e12, 2)
+    if int(pred.item()) != int(torch.argmax(logits).item()):
+        raise RuntimeError("fx_lm_head_argmax prediction disagrees with its own logits")
+    return result
+
+
 def pmc_target():
     """Workload for ``rocprofv3 --pmc`` passes: the gate/up W3 GEMV (default plan)
     over 24 rotating payloads, twice; the LUT kernel (reference-style tables in
@@ -434,6 +516,32 @@ def pmc_target():
 
 
 CALIBRATION_BYTES = 20 * 1024 * 1024
+
+
+def summarize_trace(csv_path, last):
+    """Per-kernel duration summary of the last ``last`` dispatches (by start time)
+    of a rocprofv3 kernel-trace CSV: the span they cover, the sum of their
+    durations, and per (kernel, grid) count / total / mean / median in us."""
+    import csv
+    import statistics
+    from collections import defaultdict
+
+    rows = []
+    with open(csv_path, newline="") as f:
+        for r in csv.DictReader(f):
+            rows.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"], r.get("Grid_Size_X", "")))
+    rows.sort()
+    tail = rows[-last:]
+    groups = defaultdict(list)
+    for start, end, name, grid in tail:
+        groups[(name.split("(")[0], grid)].append((end - start) / 1000.0)
+    span = (tail[-1][1] - tail[0][0]) / 1000.0
+    busy = sum(sum(v) for v in groups.values())
+    print(f"last {len(tail)} dispatches: span {span:.1f} us, kernel time {busy:.1f} us ({100 * busy / span:.1f}%)")
+    print("| kernel | grid (threads) | dispatches | total us | mean us | median us |")
+    print("|---|---:|---:|---:|---:|---:|")
+    for (name, grid), v in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
+        print(f"| `{name}` | {grid} | {len(v)} | {sum(v):.1f} | {statistics.mean(v):.2f} | {statistics.median(v):.2f} |")
 
 
 def summarize_pmc(csv_paths, out_json):
@@ -504,17 +612,27 @@ def main():
     parser.add_argument("--shapes", default="all", help="comma list of q/o,k/v,gate/up,down or all")
     parser.add_argument("--pmc-target", action="store_true", help="run the counter-collection workload")
     parser.add_argument("--decode", action="store_true", help="run only the config-3 decode benchmark")
+    parser.add_argument("--decode-native", action="store_true",
+                        help="run only the config-3 W3 native decode arm (the kernel-trace workload)")
     parser.add_argument("--decode-layers", type=int, default=36)
     parser.add_argument("--no-decode", action="store_true", help="skip the config-3 decode benchmark")
     parser.add_argument("--no-two-base", action="store_true", help="skip the config-4 two-base benchmark")
     parser.add_argument("--summarize-pmc", nargs="+", metavar="CSV",
                         help="rocprofv3 counter CSVs -> profiles/w3_mfma_traffic.json")
+    parser.add_argument("--summarize-trace", nargs=2, metavar=("CSV", "LAST"),
+                        help="per-kernel summary of the last LAST dispatches of a kernel-trace CSV")
     args = parser.parse_args()
     if args.summarize_pmc:
         summarize_pmc(args.summarize_pmc, ROOT / "profiles" / "w3_mfma_traffic.json")
         return
+    if args.summarize_trace:
+        summarize_trace(args.summarize_trace[0], int(args.summarize_trace[1]))
+        return
     if args.pmc_target:
         pmc_target()
+        return
+    if args.decode_native:
+        print(json.dumps(decode_native_only(layers=args.decode_layers)), flush=True)
         return
     if args.decode:
         print(json.dumps(decode_bench(layers=args.decode_layers)), flush=True)
