@@ -91,6 +91,13 @@ __device__ __forceinline__ float row16_max(float v) {
 
 typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
 
+// Index of the calling wave in its workgroup, as a wave-uniform (scalar) value:
+// the compiler cannot tell that threadIdx.x / 64 is the same across a wave, and
+// treats everything derived from it (batch counts, loop guards, addresses) as
+// divergent -- vector compares, exec-masked branches, and loads sunk behind
+// guards that convergent cross-lane operations cannot follow.
+__device__ __forceinline__ int wave_index() { return __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6); }
+
 // Sum over the 64 lanes of a wave (DPP within rows of 16, then lanes 16 and 32
 // apart); every lane gets the same bits.
 __device__ __forceinline__ float wave_total(float v) {

@@ -154,7 +154,7 @@ __device__ __forceinline__ void w3_mfma_body(
   auto& gsum = sh.gsum;
   auto& gexp = sh.gexp;
   auto& red = sh.red;
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int t = threadIdx.x, lane = t & 63, wave = wave_index();
   const int K = G * 128;
   const int split = blockIdx.y;
   const int row0 = xcd_local_index8(blockIdx.x, row_blocks) * (16 * RT);
@@ -203,10 +203,12 @@ __device__ __forceinline__ void w3_mfma_body(
   const int xstep = 4 * (r >> 2);
   const int je = ((r >> 1) & 1) + 2 * (r & 1);
 
-  auto issue = [&](int batch, BatchLoads<MB, RT>& L) __attribute__((always_inline)) {
+  // live = false: every load of the batch is out of range (returns zeros, no
+  // memory access), so a wave issues the same loads whatever its batch count
+  auto issue = [&](int batch, BatchLoads<MB, RT>& L, bool live) __attribute__((always_inline)) {
     const int gb = g0 + 4 * batch;
     const int col = (gb + kb) * 128 + 8 * r;
-    const bool real = gb + kb < G;
+    const bool real = live && gb + kb < G;
     if constexpr (PERM) {
       L.xv[0] = load_b128(rperm, real ? col * 2 : kOutOfRange, 0);
     } else {
@@ -215,7 +217,7 @@ __device__ __forceinline__ void w3_mfma_body(
     }
     if constexpr (NORMIN) L.wn = load_b128(rwn, real ? col * 2 : kOutOfRange, 0);
     __builtin_amdgcn_sched_barrier(0);
-    const int poff = ((gb + kb) * 3 * O + row0 + r) * 16;  // past the end -> zeros
+    const int poff = live ? ((gb + kb) * 3 * O + row0 + r) * 16 : kOutOfRange;  // past the end -> zeros
 #pragma unroll
     for (int tt = 0; tt < RT; ++tt) {
       L.w[tt][0] = load_b128_stream(rp, poff + tt * 256, 0);
@@ -228,15 +230,16 @@ __device__ __forceinline__ void w3_mfma_body(
     for (int tt = 0; tt < RT; ++tt) {
       const int e = eoff + 16 * tt;
       if constexpr (VEC) {
-        const uint2 s4 = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rs, e * 2, 0, 0));
+        const uint2 s4 = __builtin_bit_cast(
+            uint2, __builtin_amdgcn_raw_buffer_load_b64(rs, live ? e * 2 : kOutOfRange, 0, 0));
         L.s[tt][0] = s4.x;
         L.s[tt][1] = s4.y;
-        L.z[tt] = __builtin_amdgcn_raw_buffer_load_b32(rz, e, 0, 0);
+        L.z[tt] = __builtin_amdgcn_raw_buffer_load_b32(rz, live ? e : kOutOfRange, 0, 0);
       } else {  // O not a multiple of 4 (tests, tiny layers): element loads, packed in consume()
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          L.se[tt][j] = __builtin_amdgcn_raw_buffer_load_b16(rs, (e + j) * 2, 0, 0);
-          L.ze[tt][j] = __builtin_amdgcn_raw_buffer_load_b8(rz, e + j, 0, 0);
+          L.se[tt][j] = __builtin_amdgcn_raw_buffer_load_b16(rs, live ? (e + j) * 2 : kOutOfRange, 0, 0);
+          L.ze[tt][j] = __builtin_amdgcn_raw_buffer_load_b8(rz, live ? e + j : kOutOfRange, 0, 0);
         }
       }
     }
@@ -277,6 +280,20 @@ __device__ __forceinline__ void w3_mfma_body(
   int cur_batch = 0;
   auto consume = [&](const BatchLoads<MB, RT>& L, float (&acc)[RT][4]) __attribute__((always_inline)) {
     const int gb = g0 + 4 * cur_batch;
+    if constexpr (NORMIN) {
+      // 1 / rms from the tile partials, at the wave's first batch: in the loop
+      // it follows the ring issue on every path, so the wait for the partials
+      // (issued before the ring) leaves the batch's loads in flight.  Computed
+      // ahead of the loop, it was placed between the activation and the plane
+      // loads, and the wait put a full round trip ahead of the weight stream
+      // (+1.3 us per call).
+      if (cur_batch == wave) {
+        float total = 0.f;
+#pragma unroll
+        for (int k = 0; k < kMaxNormPartialsPerLane; ++k) total += pp[k];
+        norm_inv = rsqrtf(wave_total(total) / float(K) + ra.pro_eps);
+      }
+    }
     if constexpr (PERM) {
       const bool real = gb + kb < G;
       const unsigned pw[4] = {L.xv[0].x, L.xv[0].y, L.xv[0].z, L.xv[0].w};
@@ -364,13 +381,7 @@ __device__ __forceinline__ void w3_mfma_body(
   BatchLoads<MB, RT> ring[PD];
 #pragma unroll
   for (int i = 0; i < PD; ++i)
-    if (i < mine) issue(wave + i * NW, ring[i]);
-  if constexpr (NORMIN) {
-    float total = 0.f;
-#pragma unroll
-    for (int k = 0; k < kMaxNormPartialsPerLane; ++k) total += pp[k];
-    norm_inv = rsqrtf(wave_total(total) / float(K) + ra.pro_eps);
-  }
+    issue(wave + i * NW, ring[i], i < mine);
   // batches always accumulate into set 0; with two sets they are swapped after
   // every batch (register moves, not a second unrolled copy of the loop body),
   // so after an odd count set 0 holds the wave's second virtual wave
@@ -380,7 +391,7 @@ __device__ __forceinline__ void w3_mfma_body(
       if (base + i < mine) {
         cur_batch = wave + (base + i) * NW;
         consume(ring[i], acc_sets[0]);
-        if (base + i + PD < mine) issue(wave + (base + i + PD) * NW, ring[i]);
+        if (base + i + PD < mine) issue(wave + (base + i + PD) * NW, ring[i], true);
         if constexpr (VS == 2) {
 #pragma unroll
           for (int tt = 0; tt < RT; ++tt)
@@ -482,7 +493,12 @@ __device__ __forceinline__ void w3_mfma_body(
 // One-row, one-tile, single-prefetch instantiations (the decode shapes) are held
 // to 80 VGPRs, six waves per SIMD: a 24576-row gate|up grid of 4-wave workgroups
 // then fits in one residency round.
-template <int NW, int PD, int MB, int RT, bool PERM, int XDT, int SDT, bool NORMIN = false>
+// VSEL picks the scale / zero-point load form: 0 at run time from O % 4, 1 the
+// vector form only (O % 4 == 0), 2 the element form only.  A kernel holding both
+// is allocated registers for the costlier element form, which may spill and
+// then needs a scratch segment on every launch; the normalising instantiations
+// are split.
+template <int NW, int PD, int MB, int RT, bool PERM, int XDT, int SDT, bool NORMIN = false, int VSEL = 0>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(MB == 1 && RT == 1 && PD == 1 ? 6 : 1)))
 void w3_mfma_kernel(
     const uint16_t* __restrict__ x, const int16_t* __restrict__ perm,
@@ -496,12 +512,12 @@ void w3_mfma_kernel(
   if constexpr (NORMIN)
     asm volatile("" ::"s"(ra.pro_partial), "s"(ra.pro_n), "s"(ra.pro_weight), "s"(ra.pro_eps));
   __shared__ MfmaShared<NW, MB, RT> sh;
-  if ((O & 3) == 0)
-    w3_mfma_body<NW, PD, MB, RT, PERM, XDT, SDT, NORMIN, true>(sh, x, perm, planes, scales, zeros, partial, out,
-                                                               O, G, gps, row_blocks, swiglu, ra);
+  if (VSEL == 1 || (VSEL == 0 && (O & 3) == 0))
+    w3_mfma_body<NW, PD, MB, RT, PERM, XDT, SDT, NORMIN, VSEL != 2>(sh, x, perm, planes, scales, zeros, partial,
+                                                                   out, O, G, gps, row_blocks, swiglu, ra);
   else
-    w3_mfma_body<NW, PD, MB, RT, PERM, XDT, SDT, NORMIN, false>(sh, x, perm, planes, scales, zeros, partial, out,
-                                                                O, G, gps, row_blocks, swiglu, ra);
+    w3_mfma_body<NW, PD, MB, RT, PERM, XDT, SDT, NORMIN, VSEL == 1>(sh, x, perm, planes, scales, zeros, partial,
+                                                                   out, O, G, gps, row_blocks, swiglu, ra);
 }
 
 }  // namespace fx

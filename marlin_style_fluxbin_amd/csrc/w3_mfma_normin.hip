@@ -4,11 +4,19 @@
 
 namespace fx {
 
+// Separate kernels for the vector (O % 4 == 0, the decode shapes) and element
+// scale / zero-point loads, so the vector one is allocated registers for its
+// own path only.
 template <int NW, int XDT, int SDT>
 void launch_mfma_normin(const MfmaArgs& a, dim3 grid, hipStream_t s) {
-  hipLaunchKernelGGL((w3_mfma_kernel<NW, 1, 1, 1, false, XDT, SDT, true>), grid, dim3(NW * 64), 0, s, a.x,
-                     a.perm, a.planes, a.scales, a.zeros, a.partial, a.out, a.O, a.G, a.gps, a.row_blocks,
-                     a.swiglu, a.res);
+  if (a.O % 4 == 0)
+    hipLaunchKernelGGL((w3_mfma_kernel<NW, 1, 1, 1, false, XDT, SDT, true, 1>), grid, dim3(NW * 64), 0, s, a.x,
+                       a.perm, a.planes, a.scales, a.zeros, a.partial, a.out, a.O, a.G, a.gps, a.row_blocks,
+                       a.swiglu, a.res);
+  else
+    hipLaunchKernelGGL((w3_mfma_kernel<NW, 1, 1, 1, false, XDT, SDT, true, 2>), grid, dim3(NW * 64), 0, s, a.x,
+                       a.perm, a.planes, a.scales, a.zeros, a.partial, a.out, a.O, a.G, a.gps, a.row_blocks,
+                       a.swiglu, a.res);
 }
 
 bool dispatch_mfma_normin(int nw, int xdt, int sdt, const MfmaArgs& a, dim3 grid, hipStream_t s) {
