@@ -127,7 +127,9 @@ __device__ __forceinline__ float sum_sq8(const u32x4_t& v) {
 // Buffer resource over [base, base + bytes): loads at offsets past the end
 // return zero instead of touching memory.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_resource(const void* base, size_t bytes) {
-  const int records = bytes > 0x7fffffffu ? 0x7fffffff : int(bytes);
+  // (a 64-bit unsigned compare has no scalar form on gfx9: as a vector compare
+  // it put the descriptor in VGPRs, and every load through it in a waterfall loop)
+  const int records = (bytes >> 31) != 0 ? 0x7fffffff : int(bytes);
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), short(0), records, 0x00020000);
 }
 

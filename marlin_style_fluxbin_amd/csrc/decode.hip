@@ -42,7 +42,10 @@ __device__ __forceinline__ float key_row_sum(float v) {
   return v;
 }
 
-// grid (Hk, splits), 256 threads; splits = ceil((pos + 1) / (KS * KPT)).
+// grid (Hk, splits), 256 threads; splits = ceil((pos + 1) / (KS * KPT)); G = Hq / Hk
+// query heads per KV head (from the host: a device-side divide runs on the VALU,
+// and the q / partial descriptors derived from it landed in VGPRs, every load
+// through them in a waterfall loop).
 // Thread t holds dims [8 db, 8 db + 8) (db = t % DB, DB = D / 8) of keys
 // first + ks + KS i, i < KPT (ks = t / DB, KS = 256 / DB key rows per pass):
 // a key row is DB consecutive lanes reading 16 B each (coalesced), and every
@@ -99,10 +102,10 @@ template <int DT, int D, int KPT, bool PRE>
 __global__ __launch_bounds__(256) void attn_split_kernel(const uint16_t* __restrict__ q,
                                                          const uint16_t* kc, const uint16_t* vc,
                                                          float* partial, unsigned* arrivals,
-                                                         uint16_t* __restrict__ out, int Hq, int Hk,
+                                                         uint16_t* __restrict__ out, int G,
                                                          int Lmax, int pos, int splits, int combine,
                                                          float scale, AttnPre pre) {
-  asm volatile("" ::"s"(q), "s"(kc), "s"(vc), "s"(partial), "s"(arrivals), "s"(out), "s"(Hq), "s"(Hk),
+  asm volatile("" ::"s"(q), "s"(kc), "s"(vc), "s"(partial), "s"(arrivals), "s"(out), "s"(G),
                "s"(Lmax), "s"(pos), "s"(splits), "s"(combine), "s"(scale));
   if constexpr (PRE)
     asm volatile("" ::"s"(pre.k_raw), "s"(pre.v_raw), "s"(pre.q_weight), "s"(pre.k_weight), "s"(pre.cos),
@@ -112,10 +115,9 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const uint16_t* __restr
   __shared__ float red_l[KS][HB];
   __shared__ float red_m[4][HB];
   __shared__ u32x4_t qsh[PRE ? 4 : 1][HB][DB];  // PRE: normalised queries of each wave
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int t = threadIdx.x, lane = t & 63, wave = wave_index();
   const int db = t % DB, ks = t / DB;
   const int g = blockIdx.x, chunk = blockIdx.y;
-  const int G = Hq / Hk;
   const int first = chunk * (KS * KPT);
   const auto rq = buffer_resource(q + size_t(g) * G * D, size_t(G) * D * 2);
   const auto rk = buffer_resource(kc + size_t(g) * Lmax * D, size_t(Lmax) * D * 2);
@@ -436,11 +438,11 @@ template <int DT, int D, int KPT>
 void attn_launch(const AttnArgs& a, hipStream_t s) {
   if (a.pre.k_raw)
     hipLaunchKernelGGL((attn_split_kernel<DT, D, KPT, true>), dim3(a.Hk, a.splits), dim3(256), 0, s, a.q, a.k,
-                       a.v, a.partial, a.arrivals, a.out, a.Hq, a.Hk, a.Lmax, a.pos, a.splits, a.combine,
+                       a.v, a.partial, a.arrivals, a.out, a.Hq / a.Hk, a.Lmax, a.pos, a.splits, a.combine,
                        a.scale, a.pre);
   else
     hipLaunchKernelGGL((attn_split_kernel<DT, D, KPT, false>), dim3(a.Hk, a.splits), dim3(256), 0, s, a.q, a.k,
-                       a.v, a.partial, a.arrivals, a.out, a.Hq, a.Hk, a.Lmax, a.pos, a.splits, a.combine,
+                       a.v, a.partial, a.arrivals, a.out, a.Hq / a.Hk, a.Lmax, a.pos, a.splits, a.combine,
                        a.scale, a.pre);
   if (a.combine == kAttnCombineKernel)
     hipLaunchKernelGGL((attn_combine_kernel<DT, D>), dim3(a.Hq), dim3(256), 0, s, a.partial, a.out, a.splits);

@@ -68,7 +68,7 @@ __global__ __launch_bounds__(NT * NK * 64) void hybrid_kernel(HybridArgs a) {
   // one scalar-load round for every argument, before any branch
   asm volatile("" ::"s"(a.x), "s"(a.codes), "s"(a.rows), "s"(a.cols), "s"(a.idx), "s"(a.scodes), "s"(a.srows),
                "s"(a.scols), "s"(a.partial), "s"(a.out), "s"(a.O), "s"(a.G), "s"(a.gps), "s"(a.row_blocks));
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int t = threadIdx.x, lane = t & 63, wave = wave_index();
   const int O = a.O, G = a.G, K = G * 128;
   const int split = blockIdx.y;
   const int row0 = xcd_local_index8(blockIdx.x, a.row_blocks) * (16 * NT);
@@ -122,10 +122,14 @@ __global__ __launch_bounds__(NT * NK * 64) void hybrid_kernel(HybridArgs a) {
     sb = __builtin_amdgcn_raw_buffer_load_b16(rsp, (g * O + prow) * 2, 0, 0);
     // row scales of D rows drow .. +3 for this lane's group slot, both bases
     const int gd = g0 + 4 * bt + dslot;
-    const auto& rr = is_ref ? rsrow : rrow;
+    // the lane picks the refinement or the main row scales: both descriptors
+    // stay scalar (one of the two loads out of range returns zeros), where a
+    // per-lane choice of descriptor cost a waterfall loop around each load
     const int roff = (gd * O + drow) * 8;
-    rv0 = load_b128(rr, roff, 0);
-    rv1 = load_b128(rr, roff + 16, 0);
+    const int moff = is_ref ? kOutOfRange : roff, soff = is_ref ? roff : kOutOfRange;
+    rv0 = load_b128(rrow, moff, 0) | load_b128(rsrow, soff, 0);
+    rv1 = load_b128(rrow, moff == kOutOfRange ? kOutOfRange : moff + 16, 0) |
+          load_b128(rsrow, soff == kOutOfRange ? kOutOfRange : soff + 16, 0);
   };
   if (mine > 0) issue(0);
 

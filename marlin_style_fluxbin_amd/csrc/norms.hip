@@ -42,7 +42,9 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* __restrict
   constexpr int kRowsPerBlock = 256 / TPR, kWavesPerRow = TPR / 64;
   __shared__ float bsum[kWavesPerRow > 1 ? kMaxNormBatches : 1];
   const int t = threadIdx.x;
-  const int local = t / TPR, tl = t % TPR;
+  // the row from the scalar wave index: t / TPR looks lane-dependent to the
+  // compiler, which then built the row's descriptors in VGPRs (waterfall loops)
+  const int local = wave_index() / (TPR / 64), tl = t % TPR;
   const int row = blockIdx.x * kRowsPerBlock + local;
   const bool live = row < rows;
   const int chunks = hidden / 8;
