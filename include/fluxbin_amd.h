@@ -39,6 +39,11 @@ extern "C" {
 #define FX_ARITH_STRUCTURAL 0  /* fp32 s*(q-z) grouped dot */
 #define FX_ARITH_DECODED_BF16 1 /* + per-weight bf16 rounding of s*(q-z) (bf16 scales, zero 3 or 4) */
 
+/* Payload formats of the one-row decode GEMVs: the reference's planar layout, or
+ * the library's field layout (fx_w3_planes_to_fields; identity column order). */
+#define FX_W3_PLANAR 0
+#define FX_W3_FIELDS 1
+
 /* ABI version of this header (bumped on any signature change). */
 int fx_abi_version(void);
 /* Last error message of the calling thread ("" if none). */
@@ -101,7 +106,7 @@ int fx_w3_gemv(const void *x, int x_dtype, const uint8_t *planes, const void *sc
  * to that dtype.  Structural MFMA arithmetic, one launch, no workspace. */
 int fx_w3_gemv_swiglu(const void *x, int x_dtype, const uint8_t *planes, const void *scales,
                       int scale_dtype, const uint8_t *zeros, const int16_t *perm, void *out, int O,
-                      int K, void *stream);
+                      int K, int payload_format, void *stream);
 /* The decoder layer's residual stream threaded through its W3 GEMVs (one
  * activation row, identity or permuted column order for the residual form,
  * structural MFMA arithmetic).  No single reference entry point: together they
@@ -115,14 +120,31 @@ int fx_w3_gemv_swiglu(const void *x, int x_dtype, const uint8_t *planes, const v
  * sums (n_tiles = ceil(K / 16), K <= 4096); the GEMV reads
  * x = round(norm_weight * round(h * rsqrt(sum(tile_sumsq) / K + eps))), the
  * RMSNorm of h, summing the tile sums in a fixed order; swiglu != 0 reads the
- * row-interleaved gate|up payload of fx_w3_gemv_swiglu.  Identity column order. */
+ * row-interleaved gate|up payload of fx_w3_gemv_swiglu.  Identity column order.
+ * payload_format (all three): FX_W3_PLANAR, or FX_W3_FIELDS with `planes` holding
+ * the field layout (perm NULL). */
 int fx_w3_gemv_residual(const void *x, int x_dtype, const uint8_t *planes, const void *scales,
                         int scale_dtype, const uint8_t *zeros, const int16_t *perm, const void *residual,
-                        void *out, float *tile_sumsq, int O, int K, void *stream);
+                        void *out, float *tile_sumsq, int O, int K, int payload_format, void *stream);
 int fx_w3_gemv_rmsnormed(const void *h, int x_dtype, const uint8_t *planes, const void *scales,
                          int scale_dtype, const uint8_t *zeros, const float *tile_sumsq, int n_tiles,
                          const void *norm_weight, float eps, void *out, int O, int K, int swiglu,
-                         void *stream);
+                         int payload_format, void *stream);
+/* The field layout: no reference counterpart; a bind-time repack of the
+ * reference's planar payload (gptq_deployment.py:199-244 layout, same sorted
+ * column order, same [G, 3, O, 16] byte shape, three bits per code) whose
+ * dequantization costs half the instructions.  The codes of sorted columns
+ * 32 w + t (t < 32) of a (group, row) sit in little-endian word w (bytes 4 w ..)
+ * of its three 16-byte member rows: i = t / 2, h = t % 2; for i < 15 the code
+ * occupies bits [16 h + 3 f, +3) of member i / 5 (f = i % 5); for i = 15 its
+ * bit k occupies bit 15 + 16 h of member k.  fields must not alias planes;
+ * both 16-byte aligned. */
+int fx_w3_planes_to_fields(const uint8_t *planes, uint8_t *fields, int O, int K, void *stream);
+/* One-row structural GEMV on the field layout (identity column order, one
+ * launch, no workspace): out [1, O] = x [1, K] @ W.T as fx_w3_gemv's structural
+ * arithmetic (fp32 accumulation of exact products; the sum order differs). */
+int fx_w3_gemv_fields(const void *x, int x_dtype, const uint8_t *fields, const void *scales, int scale_dtype,
+                      const uint8_t *zeros, void *out, int O, int K, void *stream);
 /* Structural MFMA path with an explicit tiling (benchmark sweeps): waves per
  * workgroup in {4,8}, 4-group batches kept in flight per wave in {1,2},
  * groups per K split (rounded up to a multiple of 4, clamped to the padded group

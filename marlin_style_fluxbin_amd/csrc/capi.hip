@@ -497,7 +497,7 @@ bool two_base_config(int O, int G, int waves, int prefetch, int groups_per_split
 
 extern "C" {
 
-int fx_abi_version(void) { return 9; }
+int fx_abi_version(void) { return 10; }
 
 const char* fx_last_error(void) { return g_error; }
 
@@ -575,20 +575,6 @@ int fx_w3_gemv(const void* x, int x_dtype, const uint8_t* planes, const void* sc
                   workspace_bytes, out, M, O, K, default_mfma_plan(O, K / 128), s);
 }
 
-int fx_w3_gemv_swiglu(const void* x, int x_dtype, const uint8_t* planes, const void* scales,
-                      int scale_dtype, const uint8_t* zeros, const int16_t* perm, void* out, int O,
-                      int K, void* stream) {
-  int rc = validate_payload(x, x_dtype, planes, scales, scale_dtype, 1, O, K, FX_ARITH_STRUCTURAL);
-  if (rc) return rc;
-  if (!out) return fail(FX_EINVAL, "out must be non-null");
-  if (O % 2) return fail(FX_EINVAL, "the interleaved gate|up payload needs an even row count, got %d", O);
-  const int G = K / 128;
-  MfmaPlan p = default_mfma_plan(O, G);
-  if (p.splits > 1) p = make_mfma_plan(O, G, 8, 1, G, 1);  // the fused epilogue needs one K split
-  return run_mfma(x, x_dtype, planes, scales, scale_dtype, zeros, perm, nullptr, 0, out, 1, O, K, p,
-                  static_cast<hipStream_t>(stream), 1);
-}
-
 // One-row plan with one K split and one tile and batch in flight per wave (the
 // residual epilogue and the normalising prologue need all of K in one workgroup).
 MfmaPlan single_split_plan(int O, int G) {
@@ -597,11 +583,60 @@ MfmaPlan single_split_plan(int O, int G) {
   return p;
 }
 
-int fx_w3_gemv_residual(const void* x, int x_dtype, const uint8_t* planes, const void* scales,
-                        int scale_dtype, const uint8_t* zeros, const int16_t* perm, const void* residual,
-                        void* out, float* tile_sumsq, int O, int K, void* stream) {
+// Payload format check of the one-row entry points: the field layout runs with
+// the identity column order only.
+int check_format(int payload_format, const int16_t* perm) {
+  if (payload_format != FX_W3_PLANAR && payload_format != FX_W3_FIELDS)
+    return fail(FX_EINVAL, "payload_format must be FX_W3_PLANAR or FX_W3_FIELDS, got %d", payload_format);
+  if (payload_format == FX_W3_FIELDS && perm)
+    return fail(FX_EINVAL, "the field layout takes no column permutation");
+  return FX_OK;
+}
+
+// One-row field-layout launch (one K split); epilogue and prologue from a.
+int run_fields(const MfmaArgs& base, int x_dtype, int scale_dtype, bool normin, hipStream_t s) {
+  const MfmaPlan p = single_split_plan(base.O, base.G);
+  MfmaArgs a = base;
+  a.gps = p.gps;
+  a.row_blocks = p.row_blocks;
+  if (!fx::dispatch_mfma_fields(p.nw, normin, x_dtype, scale_dtype, a, dim3(p.row_blocks, 1), s))
+    return fail(FX_EINVAL, "no field-layout MFMA kernel for waves %d", p.nw);
+  return check_launch("w3_mfma_kernel (field layout)");
+}
+
+int fx_w3_gemv_swiglu(const void* x, int x_dtype, const uint8_t* planes, const void* scales,
+                      int scale_dtype, const uint8_t* zeros, const int16_t* perm, void* out, int O,
+                      int K, int payload_format, void* stream) {
   int rc = validate_payload(x, x_dtype, planes, scales, scale_dtype, 1, O, K, FX_ARITH_STRUCTURAL);
   if (rc) return rc;
+  if ((rc = check_format(payload_format, perm))) return rc;
+  if (!out) return fail(FX_EINVAL, "out must be non-null");
+  if (O % 2) return fail(FX_EINVAL, "the interleaved gate|up payload needs an even row count, got %d", O);
+  const int G = K / 128;
+  if (payload_format == FX_W3_FIELDS) {
+    MfmaArgs a{};
+    a.x = static_cast<const uint16_t*>(x);
+    a.planes = planes;
+    a.scales = static_cast<const uint16_t*>(scales);
+    a.zeros = zeros;
+    a.out = static_cast<uint16_t*>(out);
+    a.O = O;
+    a.G = G;
+    a.swiglu = 1;
+    return run_fields(a, x_dtype, scale_dtype, false, static_cast<hipStream_t>(stream));
+  }
+  MfmaPlan p = default_mfma_plan(O, G);
+  if (p.splits > 1) p = make_mfma_plan(O, G, 8, 1, G, 1);  // the fused epilogue needs one K split
+  return run_mfma(x, x_dtype, planes, scales, scale_dtype, zeros, perm, nullptr, 0, out, 1, O, K, p,
+                  static_cast<hipStream_t>(stream), 1);
+}
+
+int fx_w3_gemv_residual(const void* x, int x_dtype, const uint8_t* planes, const void* scales,
+                        int scale_dtype, const uint8_t* zeros, const int16_t* perm, const void* residual,
+                        void* out, float* tile_sumsq, int O, int K, int payload_format, void* stream) {
+  int rc = validate_payload(x, x_dtype, planes, scales, scale_dtype, 1, O, K, FX_ARITH_STRUCTURAL);
+  if (rc) return rc;
+  if ((rc = check_format(payload_format, perm))) return rc;
   if (!residual || !out || !tile_sumsq) return fail(FX_EINVAL, "residual, out and tile_sumsq must be non-null");
   const int G = K / 128;
   const MfmaPlan p = single_split_plan(O, G);
@@ -618,6 +653,7 @@ int fx_w3_gemv_residual(const void* x, int x_dtype, const uint8_t* planes, const
   a.row_blocks = p.row_blocks;
   a.res.ep_residual = static_cast<const uint16_t*>(residual);
   a.res.ep_partial = tile_sumsq;
+  if (payload_format == FX_W3_FIELDS) return run_fields(a, x_dtype, scale_dtype, false, static_cast<hipStream_t>(stream));
   if (!fx::dispatch_mfma(x_dtype, 1, p.nw, 1, 1, scale_dtype, a, dim3(p.row_blocks, 1), static_cast<hipStream_t>(stream)))
     return fail(FX_EINVAL, "no MFMA kernel for waves %d", p.nw);
   return check_launch("w3_mfma_kernel (residual epilogue)");
@@ -625,9 +661,10 @@ int fx_w3_gemv_residual(const void* x, int x_dtype, const uint8_t* planes, const
 
 int fx_w3_gemv_rmsnormed(const void* h, int x_dtype, const uint8_t* planes, const void* scales, int scale_dtype,
                          const uint8_t* zeros, const float* tile_sumsq, int n_tiles, const void* norm_weight,
-                         float eps, void* out, int O, int K, int swiglu, void* stream) {
+                         float eps, void* out, int O, int K, int swiglu, int payload_format, void* stream) {
   int rc = validate_payload(h, x_dtype, planes, scales, scale_dtype, 1, O, K, FX_ARITH_STRUCTURAL);
   if (rc) return rc;
+  if ((rc = check_format(payload_format, nullptr))) return rc;
   if (!tile_sumsq || !norm_weight || !out) return fail(FX_EINVAL, "tile_sumsq, norm weight and out must be non-null");
   if (n_tiles != (K + 15) / 16) return fail(FX_EINVAL, "n_tiles must be ceil(K / 16) = %d, got %d", (K + 15) / 16, n_tiles);
   if (n_tiles > 64 * fx::kMaxNormPartialsPerLane) return fail(FX_EINVAL, "K = %d too large for the normalising prologue", K);
@@ -650,9 +687,36 @@ int fx_w3_gemv_rmsnormed(const void* h, int x_dtype, const uint8_t* planes, cons
   a.res.pro_n = n_tiles;
   a.res.pro_weight = static_cast<const uint16_t*>(norm_weight);
   a.res.pro_eps = eps;
+  if (payload_format == FX_W3_FIELDS) return run_fields(a, x_dtype, scale_dtype, true, static_cast<hipStream_t>(stream));
   if (!fx::dispatch_mfma_normin(p.nw, x_dtype, scale_dtype, a, dim3(p.row_blocks, 1), static_cast<hipStream_t>(stream)))
     return fail(FX_EINVAL, "no normalising MFMA kernel for waves %d", p.nw);
   return check_launch("w3_mfma_kernel (normalising prologue)");
+}
+
+int fx_w3_planes_to_fields(const uint8_t* planes, uint8_t* fields, int O, int K, void* stream) {
+  if (!planes || !fields) return fail(FX_EINVAL, "planes and fields must be non-null");
+  if (O < 1 || K < 128 || K % 128) return fail(FX_EINVAL, "O must be positive and K a multiple of 128");
+  if (reinterpret_cast<uintptr_t>(planes) % 16 != 0 || reinterpret_cast<uintptr_t>(fields) % 16 != 0)
+    return fail(FX_EINVAL, "planes and fields must be 16-byte aligned");
+  if (planes == fields) return fail(FX_EINVAL, "the repack cannot run in place");
+  fx::launch_planes_to_fields(planes, fields, O, K / 128, static_cast<hipStream_t>(stream));
+  return check_launch("w3_planes_to_fields_kernel");
+}
+
+int fx_w3_gemv_fields(const void* x, int x_dtype, const uint8_t* fields, const void* scales, int scale_dtype,
+                      const uint8_t* zeros, void* out, int O, int K, void* stream) {
+  int rc = validate_payload(x, x_dtype, fields, scales, scale_dtype, 1, O, K, FX_ARITH_STRUCTURAL);
+  if (rc) return rc;
+  if (!out) return fail(FX_EINVAL, "out must be non-null");
+  MfmaArgs a{};
+  a.x = static_cast<const uint16_t*>(x);
+  a.planes = fields;
+  a.scales = static_cast<const uint16_t*>(scales);
+  a.zeros = zeros;
+  a.out = static_cast<uint16_t*>(out);
+  a.O = O;
+  a.G = K / 128;
+  return run_fields(a, x_dtype, scale_dtype, false, static_cast<hipStream_t>(stream));
 }
 
 size_t fx_w3_gemv_config_workspace_bytes(int M, int O, int K, int waves, int prefetch,

@@ -104,6 +104,36 @@ __device__ __forceinline__ void dequant_word(unsigned p0, unsigned p1, unsigned 
   }
 }
 
+// Field layout (the bind-time repack of the planes, fx_w3_planes_to_fields): the
+// three 32-bit words of a 32-column word hold 10 codes each in 3-bit fields at
+// bits 0, 3, 6, 9, 12 of each half, and the last two codes' bits in bits 15 / 31
+// of the three words.  Register i of the 16 (step i / 4, component i % 4) takes
+// field i % 5 of word i / 5 (i < 15) or the spare bits (i = 15): masking leaves
+// the code in mantissa bits 0-2, 3-5 or 6-8 of each fp16 half, i.e. the exact
+// fp16 subnormals q * 2^(p - 24) for p = 0, 3, 6; fields 3 and 4 are shifted
+// down by 9 first.  One AND per two codes, a shift per word and four operations
+// for the spare pair: 24 per 32 codes (against 47 for the planes).
+__device__ __forceinline__ void dequant_fields(unsigned w0, unsigned w1, unsigned w2, u32x4_t a[4]) {
+  const unsigned M0 = 0x00070007u, M3 = 0x00380038u, M6 = 0x01c001c0u;
+  const unsigned h0 = w0 >> 9, h1 = w1 >> 9, h2 = w2 >> 9;
+  const unsigned spare = ((w0 >> 15) & 0x00010001u) | ((w1 >> 14) & 0x00020002u) | ((w2 >> 13) & 0x00040004u);
+  a[0] = u32x4_t{w0 & M0, w0 & M3, w0 & M6, h0 & M0};
+  a[1] = u32x4_t{h0 & M3, w1 & M0, w1 & M3, w1 & M6};
+  a[2] = u32x4_t{h1 & M0, h1 & M3, w2 & M0, w2 & M3};
+  a[3] = u32x4_t{w2 & M6, h2 & M0, h2 & M3, spare};
+}
+
+// Mantissa position p of register i's codes in the field layout (the B operand
+// carries the matching 2^-p).
+constexpr int kFieldShift[16] = {0, 3, 6, 0, 3, 0, 3, 6, 0, 3, 0, 3, 6, 0, 3, 0};
+// The same, a nibble per register (register i at bits 4 i): a lane reads its four
+// with shifts (a runtime index into the array would be a memory load).
+constexpr unsigned long long field_shift_nibbles() {
+  unsigned long long v = 0;
+  for (int i = 0; i < 16; ++i) v |= static_cast<unsigned long long>(kFieldShift[i]) << (4 * i);
+  return v;
+}
+
 // Everything one wave loads for one batch, kept as raw bits: this lane's plane
 // rows (one per row tile), its 8 activations per row (or, with a permutation,
 // its 8 column indices), and the epilogue's scales and zero-points.  Nothing
@@ -143,7 +173,7 @@ struct MfmaShared {
 // aligned load each.  A separate instantiation (rather than a runtime branch)
 // keeps the load count per batch fixed, so the wait before staging covers only
 // the activations.
-template <int NW, int PD, int MB, int RT, bool PERM, int XDT, int SDT, bool NORMIN, bool VEC>
+template <int NW, int PD, int MB, int RT, bool PERM, int XDT, int SDT, bool NORMIN, bool VEC, bool FIELDS>
 __device__ __forceinline__ void w3_mfma_body(
     MfmaShared<NW, MB, RT>& sh, const uint16_t* __restrict__ x, const int16_t* __restrict__ perm,
     const uint8_t* __restrict__ planes, const uint16_t* __restrict__ scales,
@@ -255,16 +285,41 @@ __device__ __forceinline__ void w3_mfma_body(
     }
     mx = row16_max(mx);
     sm = row16_sum(sm);
-    const int E = choose_exponent<XDT>(mx);
+    if constexpr (FIELDS) {
+      // fp16 operands (exact: x * 2^(E - p) keeps the activation's 8 or 11
+      // significant bits within fp16's range); the lane's 8 columns are elements
+      // 0..7 of step r, one 16-byte write
+      const int E = choose_exponent<kF16>(mx);
+      // the 2^-p of this lane's four element pairs (registers 4 (r % 4) + q),
+      // recomputed per batch (the asm keeps it from being hoisted and held
+      // across the batch loop, where it cost the 4-wave kernel a spill)
+      unsigned rr = unsigned(r & 3);
+      asm volatile("" : "+v"(rr));
+      const unsigned fsh = unsigned(field_shift_nibbles() >> (16 * rr)) & 0xffffu;
+      u32x4_t o;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      uint16_t* dst = stage16 + ((kb * 16 + xstep + s) * MB + m) * 8;
-      dst[je] = exact_bits<XDT>(ldexpf(v[s], E));
-      dst[je + 4] = exact_bits<XDT>(ldexpf(v[4 + s], E - 4));
-    }
-    if (r == 0) {
-      gsum[wave][kb * MB + m] = sm;
-      gexp[wave][kb * MB + m] = subnormal_exponent<XDT>() - E;
+      for (int q = 0; q < 4; ++q) {
+        const int e = E - int((fsh >> (4 * q)) & 0xfu);
+        o[q] = unsigned(f32_to_f16_bits(ldexpf(v[2 * q], e))) |
+               (unsigned(f32_to_f16_bits(ldexpf(v[2 * q + 1], e))) << 16);
+      }
+      my_stage[(kb * 16 + r) * MB + m] = o;
+      if (r == 0) {
+        gsum[wave][kb * MB + m] = sm;
+        gexp[wave][kb * MB + m] = subnormal_exponent<kF16>() - E;
+      }
+    } else {
+      const int E = choose_exponent<XDT>(mx);
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        uint16_t* dst = stage16 + ((kb * 16 + xstep + s) * MB + m) * 8;
+        dst[je] = exact_bits<XDT>(ldexpf(v[s], E));
+        dst[je + 4] = exact_bits<XDT>(ldexpf(v[4 + s], E - 4));
+      }
+      if (r == 0) {
+        gsum[wave][kb * MB + m] = sm;
+        gexp[wave][kb * MB + m] = subnormal_exponent<XDT>() - E;
+      }
     }
   };
 
@@ -336,14 +391,15 @@ __device__ __forceinline__ void w3_mfma_body(
 #pragma unroll
       for (int tt = 0; tt < RT; ++tt) {
         const u32x4_t* w = L.w[tt];
-        dequant_word(w[0][word], w[1][word], w[2][word], a[tt]);
+        if constexpr (FIELDS) dequant_fields(w[0][word], w[1][word], w[2][word], a[tt]);
+        else dequant_word(w[0][word], w[1][word], w[2][word], a[tt]);
       }
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
         const u32x4_t b = bsrc[(4 * word + s) * MB];
 #pragma unroll
         for (int tt = 0; tt < RT; ++tt) {
-          if constexpr (XDT == kBF16)
+          if constexpr (XDT == kBF16 && !FIELDS)
             d[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
                 __builtin_bit_cast(bf16x8_t, a[tt][s]), __builtin_bit_cast(bf16x8_t, b), d[tt], 0, 0, 0);
           else
@@ -498,7 +554,10 @@ __device__ __forceinline__ void w3_mfma_body(
 // is allocated registers for the costlier element form, which may spill and
 // then needs a scratch segment on every launch; the normalising instantiations
 // are split.
-template <int NW, int PD, int MB, int RT, bool PERM, int XDT, int SDT, bool NORMIN = false, int VSEL = 0>
+// FIELDS: the payload is the field layout (one activation row, identity column
+// order, one tile and one batch in flight per wave).
+template <int NW, int PD, int MB, int RT, bool PERM, int XDT, int SDT, bool NORMIN = false, int VSEL = 0,
+          bool FIELDS = false>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(MB == 1 && RT == 1 && PD == 1 ? 6 : 1)))
 void w3_mfma_kernel(
     const uint16_t* __restrict__ x, const int16_t* __restrict__ perm,
@@ -511,13 +570,16 @@ void w3_mfma_kernel(
                "s"(O), "s"(G), "s"(gps), "s"(row_blocks), "s"(swiglu), "s"(ra.ep_residual), "s"(ra.ep_partial));
   if constexpr (NORMIN)
     asm volatile("" ::"s"(ra.pro_partial), "s"(ra.pro_n), "s"(ra.pro_weight), "s"(ra.pro_eps));
+  static_assert(!FIELDS || (!PERM && MB == 1 && RT == 1 && PD == 1), "field layout: one row, identity order");
   __shared__ MfmaShared<NW, MB, RT> sh;
   if (VSEL == 1 || (VSEL == 0 && (O & 3) == 0))
-    w3_mfma_body<NW, PD, MB, RT, PERM, XDT, SDT, NORMIN, VSEL != 2>(sh, x, perm, planes, scales, zeros, partial,
-                                                                   out, O, G, gps, row_blocks, swiglu, ra);
+    w3_mfma_body<NW, PD, MB, RT, PERM, XDT, SDT, NORMIN, VSEL != 2, FIELDS>(sh, x, perm, planes, scales, zeros,
+                                                                           partial, out, O, G, gps, row_blocks,
+                                                                           swiglu, ra);
   else
-    w3_mfma_body<NW, PD, MB, RT, PERM, XDT, SDT, NORMIN, VSEL == 1>(sh, x, perm, planes, scales, zeros, partial,
-                                                                   out, O, G, gps, row_blocks, swiglu, ra);
+    w3_mfma_body<NW, PD, MB, RT, PERM, XDT, SDT, NORMIN, VSEL == 1, FIELDS>(sh, x, perm, planes, scales, zeros,
+                                                                           partial, out, O, G, gps, row_blocks,
+                                                                           swiglu, ra);
 }
 
 }  // namespace fx

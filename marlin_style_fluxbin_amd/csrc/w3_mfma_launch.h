@@ -56,6 +56,14 @@ FX_MFMA_DECL(dispatch_mfma_f16_t2_perm)
 // and one batch in flight per wave, no permutation; nw in {4, 8}.
 bool dispatch_mfma_normin(int nw, int xdt, int sdt, const MfmaArgs& a, dim3 grid, hipStream_t s);
 
+// The field-layout instantiations (a.planes holds fields, w3_fields.hip): one
+// activation row, one tile and one batch in flight per wave, identity order,
+// one K split; plain or normalising prologue; nw in {4, 8}.
+bool dispatch_mfma_fields(int nw, bool normin, int xdt, int sdt, const MfmaArgs& a, dim3 grid, hipStream_t s);
+
+// The bind-time repack planes [G, 3, O, 16] -> fields [G, 3, O, 16].
+void launch_planes_to_fields(const uint8_t* planes, uint8_t* fields, int O, int G, hipStream_t s);
+
 inline bool dispatch_mfma(int xdt, int tiles, int nw, int pd, int mb, int sdt, const MfmaArgs& a,
                           dim3 grid, hipStream_t s) {
   const bool p = a.perm != nullptr;

@@ -146,7 +146,8 @@ class _GateUpSwiGLU:
         _lib.check(self.lib.fx_w3_gemv_swiglu(
             x.data_ptr(), _lib.dtype_code(x.dtype), self.layout["planes"].data_ptr(),
             self.layout["scales"].data_ptr(), self.scale_code, self.zeros_ptr, self.perm_ptr, out.data_ptr(),
-            2 * self.width, self.in_features, _lib.stream_handle(x.device)), "fx_w3_gemv_swiglu")
+            2 * self.width, self.in_features, _lib.PAYLOAD_PLANAR, _lib.stream_handle(x.device)),
+            "fx_w3_gemv_swiglu")
 
 
 class _ResidualStream:
@@ -156,15 +157,50 @@ class _ResidualStream:
     gate|up GEMVs read the residual and normalise it on the fly from those sums
     (``fx_w3_gemv_rmsnormed``).  ``None`` from :meth:`build` unless every layer's
     o, down, q|k|v and gate|up are structural W3 (q|k|v and gate|up fused with
-    identity column order)."""
+    identity column order).  With ``payload_format`` fields (the default) every
+    layer's four payloads are repacked once into the field layout
+    (``fx_w3_planes_to_fields``), whose dequantization costs half the
+    instructions; the planar payloads stay as they are."""
 
-    def __init__(self, lib, hidden, device):
+    def __init__(self, lib, hidden, device, payload_format):
         self.lib = lib
         self.tiles = (hidden + 15) // 16
         self.partials = torch.zeros(self.tiles, dtype=torch.float32, device=device)
+        self.format = payload_format
+        # planes data_ptr -> (the planes tensor, its field-layout copy); holding the
+        # planes keeps their memory from being reused by another payload, and a
+        # lookup must find the same tensor object
+        self._fields = {}
+
+    def payload(self, layout):
+        """The weights the kernels read: the planes, or their field-layout copy."""
+        planes = layout["planes"]
+        if self.format == _lib.PAYLOAD_PLANAR:
+            return planes
+        entry = self._fields.get(planes.data_ptr())
+        if entry is None or entry[0] is not planes:
+            raise RuntimeError("no field-layout copy of this payload (repacked when the session is built)")
+        return entry[1]
+
+    def _repack(self, layout):
+        planes = layout["planes"]
+        if self.format == _lib.PAYLOAD_PLANAR:
+            return
+        entry = self._fields.get(planes.data_ptr())
+        if entry is not None:
+            if entry[0] is not planes:
+                raise RuntimeError("two payload tensors share one address")
+            return
+        if not planes.is_contiguous():
+            raise ValueError("W3 planes must be contiguous")
+        fields = torch.empty_like(planes)
+        g, _, o, _ = planes.shape
+        _lib.check(self.lib.fx_w3_planes_to_fields(planes.data_ptr(), fields.data_ptr(), o, 128 * g,
+                                                   _lib.stream_handle(planes.device)), "fx_w3_planes_to_fields")
+        self._fields[planes.data_ptr()] = (planes, fields)
 
     @staticmethod
-    def build(session):
+    def build(session, payload_format=None):
         def structural(m):
             return isinstance(m, PackedW3Linear) and m.arithmetic == "structural" and m.bias is None
 
@@ -177,27 +213,48 @@ class _ResidualStream:
                 return None
             if swiglu.perm_ptr is not None:
                 return None
-        return _ResidualStream(_lib.library(), session.hidden, session.device)
+        fmt = _lib.PAYLOAD_FIELDS if payload_format is None else payload_format
+        if any(lin["self_attn.o_proj"].gemv.perm_ptr is not None or lin["mlp.down_proj"].gemv.perm_ptr is not None
+               for lin in session.lin):
+            fmt = _lib.PAYLOAD_PLANAR  # the field layout takes the identity column order only
+        stream = _ResidualStream(_lib.library(), session.hidden, session.device, fmt)
+        for lin, qkv, swiglu in zip(session.lin, session.qkv, session.swiglu):
+            for layout in (qkv.call.layout, swiglu.layout, lin["self_attn.o_proj"].gemv.layout,
+                           lin["mlp.down_proj"].gemv.layout):
+                stream._repack(layout)
+        torch.cuda.synchronize(session.device)
+        return stream
+
+    def plain(self, gemv: W3Gemv, x, out):
+        """out = x @ W.T (the first layer's q|k|v, after the separate RMSNorm)."""
+        if self.format == _lib.PAYLOAD_PLANAR:
+            gemv(x, out)
+            return
+        lay = gemv.layout
+        _lib.check(self.lib.fx_w3_gemv_fields(
+            x.data_ptr(), _lib.dtype_code(x.dtype), self.payload(lay).data_ptr(), lay["scales"].data_ptr(),
+            gemv.scale_code, gemv.zeros_ptr, out.data_ptr(), gemv.out_features, gemv.in_features,
+            _lib.stream_handle(x.device)), "fx_w3_gemv_fields")
 
     def residual(self, gemv: W3Gemv, x, residual):
         """residual <- round(residual + round(x @ W.T)); tile sums of its squares."""
         lay = gemv.layout
         _lib.check(self.lib.fx_w3_gemv_residual(
-            x.data_ptr(), _lib.dtype_code(x.dtype), lay["planes"].data_ptr(), lay["scales"].data_ptr(),
+            x.data_ptr(), _lib.dtype_code(x.dtype), self.payload(lay).data_ptr(), lay["scales"].data_ptr(),
             gemv.scale_code, gemv.zeros_ptr, gemv.perm_ptr, residual.data_ptr(), residual.data_ptr(),
-            self.partials.data_ptr(), gemv.out_features, gemv.in_features, _lib.stream_handle(x.device)),
-            "fx_w3_gemv_residual")
+            self.partials.data_ptr(), gemv.out_features, gemv.in_features, self.format,
+            _lib.stream_handle(x.device)), "fx_w3_gemv_residual")
 
     def normed(self, layout, scale_code, zeros_ptr, rows, h, weight, eps, out, swiglu):
         """out = GEMV (or SwiGLU) of RMSNorm(h) with the tile sums of h."""
         _lib.check(self.lib.fx_w3_gemv_rmsnormed(
-            h.data_ptr(), _lib.dtype_code(h.dtype), layout["planes"].data_ptr(), layout["scales"].data_ptr(),
+            h.data_ptr(), _lib.dtype_code(h.dtype), self.payload(layout).data_ptr(), layout["scales"].data_ptr(),
             scale_code, zeros_ptr, self.partials.data_ptr(), self.tiles, weight.data_ptr(), eps, out.data_ptr(),
-            rows, h.shape[-1], int(swiglu), _lib.stream_handle(h.device)), "fx_w3_gemv_rmsnormed")
+            rows, h.shape[-1], int(swiglu), self.format, _lib.stream_handle(h.device)), "fx_w3_gemv_rmsnormed")
 
 
 class NativeDecodeSession:
-    def __init__(self, model, input_ids: torch.Tensor, forced_tokens: torch.Tensor):
+    def __init__(self, model, input_ids: torch.Tensor, forced_tokens: torch.Tensor, w3_payload: str = "fields"):
         from transformers import StaticCache
 
         if input_ids.ndim != 2 or input_ids.shape[0] != 1 or input_ids.shape[1] < 2:
@@ -256,7 +313,10 @@ class NativeDecodeSession:
         self.swiglu = [_GateUpSwiGLU.build(*(b.get_submodule(n) for n in _MLP[:2])) for b in self.layers]
         self.gate_up = [None if f is not None else _FusedLinear.build([b.get_submodule(n) for n in _MLP[:2]])
                         for f, b in zip(self.swiglu, self.layers)]
-        self.stream = _ResidualStream.build(self)
+        if w3_payload not in ("fields", "planar"):
+            raise ValueError(f"w3_payload must be 'fields' or 'planar', got {w3_payload!r}")
+        self.stream = _ResidualStream.build(
+            self, _lib.PAYLOAD_FIELDS if w3_payload == "fields" else _lib.PAYLOAD_PLANAR)
         self.in_norm = [b.input_layernorm.weight for b in self.layers]
         self.post_norm = [b.post_attention_layernorm.weight for b in self.layers]
         self.q_norm = [b.self_attn.q_norm.weight for b in self.layers]
@@ -341,7 +401,7 @@ class NativeDecodeSession:
             gemv = self.qkv[l].call
             if l == 0:
                 rms_norm(self.residual, self.in_norm[0], self.eps, out=self.normed)
-                gemv(self.normed, self.qkv_out)
+                rs.plain(gemv, self.normed, self.qkv_out)
             else:
                 rs.normed(gemv.layout, gemv.scale_code, gemv.zeros_ptr, gemv.out_features, self.residual,
                           self.in_norm[l], self.eps, self.qkv_out, False)

@@ -242,3 +242,61 @@ def layout_storage_bytes(layout) -> int:
     if layout.get("zeros") is not None:
         total += g * o
     return total
+
+
+# --------------------------------------------------------------------------- field layout
+# The library's bind-time repack of the planar payload (no reference counterpart;
+# written from its definition here, the kernel from the same definition in HIP).
+# Same array shape as the planes, [G, 3, O, 16] uint8 = per (group, row) three
+# "member" rows of four little-endian 32-bit words; the 32 sorted columns
+# 32 w + t (t < 32) of word w are spread over member word w of members 0..2:
+#   i = t // 2, h = t % 2 (low / high 16-bit half);
+#   i < 15: the whole code in bits [16 h + 3 f, +3) of member i // 5, f = i % 5;
+#   i = 15: bit k of the code in bit 15 + 16 h of member k.
+# Three bits per code, as the planes.
+def field_slots() -> list[list[tuple[int, int]]]:
+    """For t in 0..31: the (member, bit) of code bits 0, 1, 2 within word w."""
+    slots = []
+    for t in range(32):
+        i, h = t // 2, t % 2
+        if i < 15:
+            m, f = i // 5, i % 5
+            slots.append([(m, 16 * h + 3 * f + k) for k in range(3)])
+        else:
+            slots.append([(k, 15 + 16 * h) for k in range(3)])
+    return slots
+
+
+def fields_from_sorted_codes(sorted_codes: np.ndarray) -> np.ndarray:
+    """Sorted-order codes ``[K, O]`` -> field layout ``[G, 3, O, 16]``."""
+    codes = np.asarray(sorted_codes, dtype=np.uint32)
+    k, o = codes.shape
+    if k % GROUP:
+        raise ValueError("K must be a multiple of 128")
+    grouped = codes.reshape(k // GROUP, GROUP, o).transpose(0, 2, 1)  # [G, O, 128]
+    words = np.zeros((k // GROUP, 3, o, 4), dtype=np.uint32)
+    for c in range(GROUP):
+        w, t = divmod(c, 32)
+        for bit, (m, pos) in enumerate(field_slots()[t]):
+            words[:, m, :, w] |= ((grouped[:, :, c] >> bit) & 1) << np.uint32(pos)
+    return np.ascontiguousarray(words.astype("<u4").view(np.uint8).reshape(k // GROUP, 3, o, 16))
+
+
+def sorted_codes_from_fields(fields: np.ndarray) -> np.ndarray:
+    """Field layout ``[G, 3, O, 16]`` -> sorted-order codes ``[K, O]``."""
+    fields = np.asarray(fields, dtype=np.uint8)
+    g, three, o, sixteen = fields.shape
+    if three != 3 or sixteen != 16:
+        raise ValueError("fields must be [G,3,O,16]")
+    words = np.ascontiguousarray(fields).view("<u4").reshape(g, 3, o, 4).astype(np.uint32)
+    codes = np.zeros((g, o, GROUP), dtype=np.uint32)
+    for c in range(GROUP):
+        w, t = divmod(c, 32)
+        for bit, (m, pos) in enumerate(field_slots()[t]):
+            codes[:, :, c] |= ((words[:, m, :, w] >> np.uint32(pos)) & 1) << np.uint32(bit)
+    return np.ascontiguousarray(codes.transpose(0, 2, 1).reshape(g * GROUP, o).astype(np.uint8))
+
+
+def fields_from_planar(planes: np.ndarray) -> np.ndarray:
+    """The bind-time repack: planes ``[G,3,O,16]`` -> fields ``[G,3,O,16]`` (same sorted order)."""
+    return fields_from_sorted_codes(codes_from_planar(planes))

@@ -203,19 +203,40 @@ def test_gemv_swiglu_matches_gemvs_then_silu_mul(gpu, inter, k, dtype, scale_dty
     assert torch.equal(got, want)
     rc = lib.fx_w3_gemv_swiglu(x.data_ptr(), _lib.dtype_code(DT[dtype]), fused["planes"].data_ptr(),
                                fused["scales"].data_ptr(), _lib.dtype_code(scale_dtype), None, None,
-                               got.data_ptr(), 2 * inter + 1, k, None)
+                               got.data_ptr(), 2 * inter + 1, k, _lib.PAYLOAD_PLANAR, None)
     assert rc == 1 and "even" in lib.fx_last_error().decode()
 
 
+def _fields(planes):
+    """The field-layout copy of a planar payload (fx_w3_planes_to_fields)."""
+    lib = _lib.library()
+    fields = torch.empty_like(planes)
+    g, _, o, _ = planes.shape
+    _lib.check(lib.fx_w3_planes_to_fields(planes.data_ptr(), fields.data_ptr(), o, 128 * g,
+                                          _lib.stream_handle(planes.device)), "planes_to_fields")
+    return fields
+
+
+def _gemv_fields(x, fields, layout, out):
+    lib = _lib.library()
+    _lib.check(lib.fx_w3_gemv_fields(x.data_ptr(), _lib.dtype_code(x.dtype), fields.data_ptr(),
+                                     layout["scales"].data_ptr(), _lib.dtype_code(layout["scales"].dtype),
+                                     _lib.ptr(layout.get("zeros")), out.data_ptr(), out.shape[1], x.shape[1],
+                                     _lib.stream_handle(x.device)), "gemv_fields")
+
+
+@pytest.mark.parametrize("fmt", ["planar", "fields"])
 @pytest.mark.parametrize("o,k,dtype,permute", [(4096, 4096, "bf16", False), (4096, 12288, "bf16", True),
                                                 (96, 384, "f16", False), (40, 256, "bf16", False)])
-def test_gemv_residual_epilogue(gpu, o, k, dtype, permute):
+def test_gemv_residual_epilogue(gpu, o, k, dtype, permute, fmt):
     """fx_w3_gemv_residual: out = round(residual + round(x @ W.T)) bit for bit
-    (the plain GEMV, then the dtype's own add), in place, plus the sums of out^2
-    over 16-row tiles."""
+    (the plain GEMV of the same payload format, then the dtype's own add), in
+    place, plus the sums of out^2 over 16-row tiles."""
     from marlin_style_fluxbin_amd.w3_lut_deployment import W3Gemv
     from payloads import config_codes, layout_from_codes
 
+    if fmt == "fields" and permute:
+        pytest.skip("the field layout takes the identity column order only")
     codes, scales, zero, perm = config_codes(o, k, seed=o + k, zeros=True, scale_dtype=torch.float16, permute=permute)
     layout = {n: v.to(gpu) for n, v in layout_from_codes(codes, scales, zero, perm).items()}
     gemv = W3Gemv(layout)
@@ -223,16 +244,21 @@ def test_gemv_residual_epilogue(gpu, o, k, dtype, permute):
     x = torch.randn(1, k, generator=g).to(DT[dtype]).to(gpu)
     res = (torch.randn(1, o, generator=g) * 4).to(DT[dtype]).to(gpu)
     y = torch.empty(1, o, dtype=DT[dtype], device=gpu)
-    gemv(x, y)
+    payload = layout["planes"] if fmt == "planar" else _fields(layout["planes"])
+    if fmt == "planar":
+        gemv(x, y)
+    else:
+        _gemv_fields(x, payload, layout, y)
     want = res + y
     tiles = (o + 15) // 16
     sums = torch.full((tiles,), float("nan"), device=gpu)
     got = res.clone()
     lib = _lib.library()
-    _lib.check(lib.fx_w3_gemv_residual(x.data_ptr(), _lib.dtype_code(DT[dtype]), layout["planes"].data_ptr(),
+    _lib.check(lib.fx_w3_gemv_residual(x.data_ptr(), _lib.dtype_code(DT[dtype]), payload.data_ptr(),
                                        layout["scales"].data_ptr(), _lib.dtype_code(torch.float16),
                                        layout["zeros"].data_ptr(), gemv.perm_ptr, got.data_ptr(), got.data_ptr(),
-                                       sums.data_ptr(), o, k, _lib.stream_handle(gpu)), "residual")
+                                       sums.data_ptr(), o, k, 0 if fmt == "planar" else 1, _lib.stream_handle(gpu)),
+               "residual")
     torch.cuda.synchronize()
     assert torch.equal(got, want)
     h = want.double().cpu().numpy()[0]
@@ -240,12 +266,14 @@ def test_gemv_residual_epilogue(gpu, o, k, dtype, permute):
     assert np.allclose(sums.cpu().numpy(), exact, rtol=2e-6, atol=0)
 
 
+@pytest.mark.parametrize("fmt", ["planar", "fields"])
 @pytest.mark.parametrize("rows,k,dtype,swiglu", [(6144, 4096, "bf16", False), (24576, 4096, "bf16", True),
                                                  (96, 1024, "f16", True), (34, 512, "bf16", False)])
-def test_gemv_rmsnormed_prologue(gpu, rows, k, dtype, swiglu):
+def test_gemv_rmsnormed_prologue(gpu, rows, k, dtype, swiglu, fmt):
     """fx_w3_gemv_rmsnormed equals the RMSNorm kernel followed by the plain GEMV
-    (or SwiGLU GEMV) bit for bit.  h holds small integers, so every order of the
-    fp32 sum of squares is exact and both paths form the same 1 / rms."""
+    (or SwiGLU GEMV) of the same payload format bit for bit.  h holds small
+    integers, so every order of the fp32 sum of squares is exact and both paths
+    form the same 1 / rms."""
     from marlin_style_fluxbin_amd.fused_modules import rms_norm
     from marlin_style_fluxbin_amd.native_decode import _GateUpSwiGLU
     from marlin_style_fluxbin_amd.w3_lut_deployment import W3Gemv
@@ -263,21 +291,31 @@ def test_gemv_rmsnormed_prologue(gpu, rows, k, dtype, swiglu):
     rms_norm(h, weight, 1e-6, out=normed)
     width = rows // 2 if swiglu else rows
     want = torch.empty(1, width, dtype=DT[dtype], device=gpu)
-    if swiglu:
-        _GateUpSwiGLU(layout, width)(normed, want)
-    else:
-        W3Gemv(layout)(normed, want)
-    got = torch.full_like(want, float("nan"))
     lib = _lib.library()
-    _lib.check(lib.fx_w3_gemv_rmsnormed(h.data_ptr(), _lib.dtype_code(DT[dtype]), layout["planes"].data_ptr(),
+    fcode = 0 if fmt == "planar" else 1
+    payload = layout["planes"] if fmt == "planar" else _fields(layout["planes"])
+    if swiglu and fmt == "planar":
+        _GateUpSwiGLU(layout, width)(normed, want)
+    elif swiglu:
+        _lib.check(lib.fx_w3_gemv_swiglu(normed.data_ptr(), _lib.dtype_code(DT[dtype]), payload.data_ptr(),
+                                         layout["scales"].data_ptr(), _lib.dtype_code(torch.float16),
+                                         layout["zeros"].data_ptr(), None, want.data_ptr(), rows, k, fcode,
+                                         _lib.stream_handle(gpu)), "swiglu fields")
+    elif fmt == "planar":
+        W3Gemv(layout)(normed, want)
+    else:
+        _gemv_fields(normed, payload, layout, want)
+    got = torch.full_like(want, float("nan"))
+    _lib.check(lib.fx_w3_gemv_rmsnormed(h.data_ptr(), _lib.dtype_code(DT[dtype]), payload.data_ptr(),
                                         layout["scales"].data_ptr(), _lib.dtype_code(torch.float16),
                                         layout["zeros"].data_ptr(), sums.data_ptr(), sums.numel(), weight.data_ptr(),
-                                        1e-6, got.data_ptr(), rows, k, int(swiglu), _lib.stream_handle(gpu)), "normed")
+                                        1e-6, got.data_ptr(), rows, k, int(swiglu), fcode, _lib.stream_handle(gpu)),
+               "normed")
     torch.cuda.synchronize()
     assert torch.equal(got, want)
     rc = lib.fx_w3_gemv_rmsnormed(h.data_ptr(), _lib.dtype_code(DT[dtype]), layout["planes"].data_ptr(),
                                   layout["scales"].data_ptr(), _lib.dtype_code(torch.float16), None, sums.data_ptr(),
-                                  sums.numel() + 1, weight.data_ptr(), 1e-6, got.data_ptr(), rows, k, 0, None)
+                                  sums.numel() + 1, weight.data_ptr(), 1e-6, got.data_ptr(), rows, k, 0, fcode, None)
     assert rc == 1 and "n_tiles" in lib.fx_last_error().decode()
 
 
@@ -297,9 +335,12 @@ def _setup(gpu, quantize):
 
 
 @pytest.mark.parametrize("quantize", [True, False])
-def test_native_session_matches_hf_static_session(gpu, quantize):
+@pytest.mark.parametrize("payload", ["fields", "planar"])
+def test_native_session_matches_hf_static_session(gpu, quantize, payload):
     from torch.nn.attention import SDPBackend, sdpa_kernel
 
+    if payload == "planar" and not quantize:
+        pytest.skip("the W3 payload format only concerns the quantized model")
     model, ids, forced = _setup(gpu, quantize)
     # both prefills (the prefix KV) run the same attention backend
     with sdpa_kernel([SDPBackend.MATH]):
@@ -309,7 +350,7 @@ def test_native_session_matches_hf_static_session(gpu, quantize):
                 want = hf.audit()
         else:
             want = hf.audit()
-        native = NativeDecodeSession(model, ids, forced)
+        native = NativeDecodeSession(model, ids, forced, w3_payload=payload)
     eager = native.audit()
     graph = native.capture()
     assert torch.equal(graph["logits"], eager["logits"])

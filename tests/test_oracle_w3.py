@@ -231,3 +231,32 @@ def test_kernel_order_close_to_exact():
     assert np.abs(got - exact).max() <= bound
     decoded = w3_kernel_order(x, layout, decoded=True)
     assert np.abs(decoded - w3.matvec_decoded(x[None], layout)[0]).max() <= bound
+
+
+def test_field_layout_known_answer():
+    """Hand-built word images of the field layout (32 columns of one group row,
+    the rest zero): column 0 code 5 -> member 0 bits 0-2; column 1 (second half
+    of register 0) code 3 -> member 0 bits 16-18; column 8 (register 4 = member 0
+    field 4, low half) code 7 -> member 0 bits 12-14; column 10 (register 5 =
+    member 1 field 0) code 2 -> member 1 bits 0-2; column 30 code 6 = 0b110 ->
+    bit 15 of members 1 and 2; column 31 code 1 -> bit 31 of member 0."""
+    codes = np.zeros((128, 1), dtype=np.uint8)
+    codes[0, 0], codes[1, 0], codes[8, 0], codes[10, 0], codes[30, 0], codes[31, 0] = 5, 3, 7, 2, 6, 1
+    words = w3.fields_from_sorted_codes(codes).view("<u4").reshape(1, 3, 1, 4)
+    assert words[0, 0, 0, 0] == 5 | (3 << 16) | (7 << 12) | (1 << 31)
+    assert words[0, 1, 0, 0] == 2 | (1 << 15)
+    assert words[0, 2, 0, 0] == 1 << 15
+    assert not words[0, :, 0, 1:].any()
+
+
+def test_field_layout_bijection_and_roundtrip():
+    """Every one of the 96 bits of a word triple carries exactly one code bit,
+    so the layout keeps three bits per code; codes and planes round-trip."""
+    slots = [pos for t in w3.field_slots() for pos in t]
+    assert len(slots) == 96 and len(set(slots)) == 96
+    rng = np.random.default_rng(3)
+    codes = rng.integers(0, 8, (384, 21)).astype(np.uint8)
+    fields = w3.fields_from_sorted_codes(codes)
+    assert fields.shape == (3, 3, 21, 16)
+    assert np.array_equal(w3.sorted_codes_from_fields(fields), codes)
+    assert np.array_equal(w3.fields_from_planar(w3.planar_from_codes(codes)), fields)

@@ -1,0 +1,94 @@
+"""GPU parity of the W3 field layout: the bind-time repack (fx_w3_planes_to_fields)
+bit for bit against the oracle's restatement of the layout, and the field-layout
+GEMV (fx_w3_gemv_fields) against the float64 oracle of the planar payload it was
+repacked from.
+
+GEMV bar: half an output ulp of the exact x @ (s*(q-z)).T plus 3e-5 * max|y| --
+the field kernel runs the fp16 MFMA on fp16 subnormal codes, which rounds such
+products at ~2e-7 relative per instruction (the same bar as the planar kernel's
+fp16-activation path).
+"""
+import numpy as np
+import pytest
+import torch
+
+from marlin_style_fluxbin_amd import _lib
+from oracle import w3
+from tests.payloads import assert_half_ulp, config_codes, layout_from_codes, oracle_layout
+
+pytestmark = pytest.mark.gpu
+
+
+def _repack(planes):
+    lib = _lib.library()
+    fields = torch.full_like(planes, 0xA5)
+    g, _, o, _ = planes.shape
+    _lib.check(lib.fx_w3_planes_to_fields(planes.data_ptr(), fields.data_ptr(), o, 128 * g,
+                                          _lib.stream_handle(planes.device)), "planes_to_fields")
+    return fields
+
+
+@pytest.mark.parametrize("o,k", [(64, 512), (37, 1536), (300, 2048), (1, 128), (17, 384), (4096, 4096)])
+def test_planes_to_fields_matches_oracle(gpu, o, k):
+    codes, scales, zeros, perm = config_codes(o, k, seed=o * 7 + k, zeros=True, scale_dtype=torch.float16,
+                                              permute=True)
+    layout = layout_from_codes(codes, scales, zeros, perm)
+    fields = _repack(layout["planes"].to(gpu)).cpu().numpy()
+    assert np.array_equal(fields, w3.fields_from_planar(layout["planes"].numpy()))
+    # the sorted codes survive the repack
+    assert np.array_equal(w3.sorted_codes_from_fields(fields), w3.codes_from_planar(layout["planes"].numpy()))
+
+
+@pytest.mark.parametrize("o,k", [(4096, 4096), (12288, 4096), (4096, 12288), (37, 1536), (96, 384), (1, 128)])
+@pytest.mark.parametrize("xdtype,tag", [(torch.bfloat16, "bf16"), (torch.float16, "f16")])
+@pytest.mark.parametrize("scale_dtype,zeros", [(torch.float16, True), (torch.bfloat16, False)])
+def test_gemv_fields_matches_oracle(gpu, o, k, xdtype, tag, scale_dtype, zeros):
+    codes, scales, zero, _ = config_codes(o, k, seed=o + 3 * k, zeros=zeros, scale_dtype=scale_dtype)
+    layout = layout_from_codes(codes, scales, zero, None)
+    dl = {n: t.to(gpu) for n, t in layout.items()}
+    fields = _repack(dl["planes"])
+    x = torch.randn(1, k, generator=torch.Generator().manual_seed(o)).to(xdtype)
+    out = torch.full((1, o), float("nan"), dtype=xdtype, device=gpu)
+    lib = _lib.library()
+    _lib.check(lib.fx_w3_gemv_fields(x.to(gpu).data_ptr(), _lib.dtype_code(xdtype), fields.data_ptr(),
+                                     dl["scales"].data_ptr(), _lib.dtype_code(scale_dtype), _lib.ptr(dl.get("zeros")),
+                                     out.data_ptr(), o, k, _lib.stream_handle(gpu)), "gemv_fields")
+    exact = w3.matvec_exact(x.float().numpy(), oracle_layout(layout))
+    assert_half_ulp(out.float().cpu().numpy(), exact, tag, rel_slack=3e-5, what=f"fields {o}x{k}")
+
+
+@pytest.mark.parametrize("scale", [1e-30, 1e-3, 1.0, 1e4, 1e30])
+def test_gemv_fields_activation_range(gpu, scale):
+    """The fp16 operands are exact over the activation's whole range: each group's
+    power-of-two exponent puts its largest |x| near 2^14 whatever the scale."""
+    o, k = 256, 1024
+    codes, scales, zero, _ = config_codes(o, k, seed=9, zeros=True, scale_dtype=torch.float16)
+    layout = layout_from_codes(codes, scales, zero, None)
+    dl = {n: t.to(gpu) for n, t in layout.items()}
+    fields = _repack(dl["planes"])
+    x = (torch.randn(1, k, generator=torch.Generator().manual_seed(1)) * scale).to(torch.bfloat16)
+    out = torch.empty(1, o, dtype=torch.bfloat16, device=gpu)
+    lib = _lib.library()
+    _lib.check(lib.fx_w3_gemv_fields(x.to(gpu).data_ptr(), _lib.dtype_code(torch.bfloat16), fields.data_ptr(),
+                                     dl["scales"].data_ptr(), _lib.dtype_code(torch.float16), dl["zeros"].data_ptr(),
+                                     out.data_ptr(), o, k, _lib.stream_handle(gpu)), "gemv_fields")
+    exact = w3.matvec_exact(x.float().numpy(), oracle_layout(layout))
+    assert_half_ulp(out.float().cpu().numpy(), exact, "bf16", rel_slack=3e-5, what=f"scale {scale}")
+
+
+def test_field_layout_argument_checks(gpu):
+    lib = _lib.library()
+    t = torch.zeros(3 * 16 * 16, dtype=torch.uint8, device=gpu)
+    perm = torch.arange(128, dtype=torch.int16, device=gpu)
+    assert lib.fx_w3_planes_to_fields(t.data_ptr(), t.data_ptr(), 16, 128, None) == 1  # in place
+    assert "in place" in lib.fx_last_error().decode()
+    x = torch.zeros(1, 128, dtype=torch.bfloat16, device=gpu)
+    sc = torch.ones(1, 16, dtype=torch.float16, device=gpu)
+    out = torch.zeros(1, 16, dtype=torch.bfloat16, device=gpu)
+    part = torch.zeros(1, device=gpu)
+    rc = lib.fx_w3_gemv_residual(x.data_ptr(), 2, t.data_ptr(), sc.data_ptr(), 1, None, perm.data_ptr(),
+                                 out.data_ptr(), out.data_ptr(), part.data_ptr(), 16, 128, _lib.PAYLOAD_FIELDS, None)
+    assert rc == 1 and "permutation" in lib.fx_last_error().decode()
+    rc = lib.fx_w3_gemv_residual(x.data_ptr(), 2, t.data_ptr(), sc.data_ptr(), 1, None, None, out.data_ptr(),
+                                 out.data_ptr(), part.data_ptr(), 16, 128, 7, None)
+    assert rc == 1 and "payload_format" in lib.fx_last_error().decode()
