@@ -16,6 +16,9 @@ gives the average launch duration (one w3_mfma_kernel launch per call, plus a
 finish launch only for split-K plans); the same-run bf16 arm runs torch.matmul
 (hipBLASLt) on dequantized bf16 weights with the same rotation.  ``roofline``
 is the gate/up shape's measurement: the dominant kernel of a decode step.
+``config.field_layout`` (and each shape's ``fields_*``) times the same payloads
+after the library's bind-time repack into its field layout (same bytes, half
+the dequant instructions), the format the native decode reads.
 ``roofline.traffic`` is the HBM bytes per launch measured with rocprofv3 PMC
 counters (FETCH_SIZE + WRITE_SIZE, scaled by a plain read kernel of known size),
 read from ``profiles/w3_mfma_traffic.json`` when present.  The CPU baseline
@@ -95,6 +98,14 @@ def capture(fn, stream):
     return graph
 
 
+def dominant_fields_us(shapes):
+    return (shapes.get("gate/up") or next(iter(shapes.values()))).get("fields_us")
+
+
+def dominant_fields_frac(shapes):
+    return (shapes.get("gate/up") or next(iter(shapes.values()))).get("fields_frac_hbm")
+
+
 def bench_shape(o, k, device, steps, warmup, stream, min_bytes=320e6, min_copies=50):
     """Average launch time of the W3 GEMV and of the bf16 arm over rotating copies."""
     import torch
@@ -117,6 +128,35 @@ def bench_shape(o, k, device, steps, warmup, stream, min_bytes=320e6, min_copies
     ms = time_graph(graph, steps, warmup, stream)
     w3_us = ms * 1000 / copies
     del graph
+
+    # the same payloads repacked once into the field layout (fx_w3_planes_to_fields)
+    # and read by fx_w3_gemv_fields: the decode graph's weight format
+    from marlin_style_fluxbin_amd import _lib
+
+    lib = _lib.library()
+    fields = [torch.empty_like(p["planes"]) for p in payloads]
+    for p, f in zip(payloads, fields):
+        _lib.check(lib.fx_w3_planes_to_fields(p["planes"].data_ptr(), f.data_ptr(), o, k,
+                                              _lib.stream_handle(device)), "fx_w3_planes_to_fields")
+    fout = torch.empty_like(out)
+
+    def fields_all():
+        for p, f in zip(payloads, fields):
+            _lib.check(lib.fx_w3_gemv_fields(x.data_ptr(), _lib.dtype_code(x.dtype), f.data_ptr(),
+                                             p["scales"].data_ptr(), _lib.dtype_code(p["scales"].dtype),
+                                             p["zeros"].data_ptr(), fout.data_ptr(), o, k,
+                                             _lib.stream_handle(device)), "fx_w3_gemv_fields")
+
+    graph = capture(fields_all, stream)
+    fields_us = time_graph(graph, steps, warmup, stream) * 1000 / copies
+    del graph
+    # both formats compute the same GEMV of the last payload (fp32 sums in another
+    # order, fp16 MFMA): within two output ulps
+    gemvs[-1](x, out)
+    torch.cuda.synchronize()
+    if not torch.allclose(fout.float(), out.float(), rtol=2 ** -7, atol=1e-3 * float(out.float().abs().max())):
+        raise RuntimeError("field-layout GEMV disagrees with the planar GEMV")
+    del fields
 
     # same-run bf16 arm: dense bf16 weights (5.3x the bytes), same rotation rule
     bf16_bytes = 2 * o * k + 2 * k + 2 * o
@@ -141,6 +181,8 @@ def bench_shape(o, k, device, steps, warmup, stream, min_bytes=320e6, min_copies
         "w3_frac_hbm": round(nbytes / w3_us / 1e3 / HBM_PEAK_GBPS, 4),
         "bf16_us": round(bf16_us, 3), "bf16_GBps": round(bf16_bytes / bf16_us / 1e3, 1),
         "w3_speedup_vs_bf16": round(bf16_us / w3_us, 3),
+        "fields_us": round(fields_us, 3), "fields_GBps": round(nbytes / fields_us / 1e3, 1),
+        "fields_frac_hbm": round(nbytes / fields_us / 1e3 / HBM_PEAK_GBPS, 4),
     }
 
 
@@ -683,6 +725,32 @@ def main():
     step_bytes = args.layers * sum(algorithmic_bytes(o, k) for o, k in SHAPES.values())
     value = step_bytes / (ms / 1e3) / 1e9
 
+    # the same step on the field layout (the payloads repacked once, as the
+    # native decode session does): fx_w3_gemv_fields per GEMV
+    from marlin_style_fluxbin_amd import _lib
+
+    lib = _lib.library()
+    field_calls = []
+    for layer in layers:
+        for name, (o, k) in SHAPES.items():
+            lay = layer[name].layout
+            f = torch.empty_like(lay["planes"])
+            _lib.check(lib.fx_w3_planes_to_fields(lay["planes"].data_ptr(), f.data_ptr(), o, k,
+                                                  _lib.stream_handle(device)), "fx_w3_planes_to_fields")
+            field_calls.append((xs[k], f, lay, outs[name], o, k))
+
+    def field_step():
+        for x, f, lay, out, o, k in field_calls:
+            _lib.check(lib.fx_w3_gemv_fields(x.data_ptr(), _lib.dtype_code(x.dtype), f.data_ptr(),
+                                             lay["scales"].data_ptr(), _lib.dtype_code(lay["scales"].dtype),
+                                             lay["zeros"].data_ptr(), out.data_ptr(), o, k,
+                                             _lib.stream_handle(device)), "fx_w3_gemv_fields")
+
+    fgraph = capture(field_step, stream)
+    fms = time_graph(fgraph, args.steps, args.warmup, stream)
+    field_value = step_bytes / (fms / 1e3) / 1e9
+    del fgraph, field_calls
+
     dominant = shapes.get("gate/up") or next(iter(shapes.values()))
     traffic = None
     traffic_file = ROOT / "profiles" / "w3_mfma_traffic.json"
@@ -705,6 +773,13 @@ def main():
             "workload": f"config 1: 7 Qwen3-8B Linear shapes at M=1 x {args.layers} distinct layers per step",
             "frac_hbm_peak": round(value / HBM_PEAK_GBPS, 4),
             "shapes": shapes,
+            "field_layout": {
+                "note": "the same payloads repacked once by fx_w3_planes_to_fields (same bytes); "
+                        "value and roofline above are the planar payload, the reference's layout",
+                "step_GBps": round(field_value, 1), "ms_per_step": round(fms, 4),
+                "frac_hbm_peak": round(field_value / HBM_PEAK_GBPS, 4),
+                "gate_up_us": dominant_fields_us(shapes), "gate_up_frac_hbm": dominant_fields_frac(shapes),
+            },
         },
         "roofline": {
             "bound": "hbm",
