@@ -514,6 +514,21 @@ def pmc_target():
     for _ in range(2):
         for gemv in gemvs:
             gemv(x, out)
+    # the same payloads in the field layout, 24 launches twice
+    from marlin_style_fluxbin_amd import _lib
+
+    lib = _lib.library()
+    fields = [torch.empty_like(p["planes"]) for p in payloads]
+    for p, f in zip(payloads, fields):
+        _lib.check(lib.fx_w3_planes_to_fields(p["planes"].data_ptr(), f.data_ptr(), o, k,
+                                              _lib.stream_handle(device)), "fx_w3_planes_to_fields")
+    for _ in range(2):
+        for p, f in zip(payloads, fields):
+            _lib.check(lib.fx_w3_gemv_fields(x.data_ptr(), _lib.dtype_code(x.dtype), f.data_ptr(),
+                                             p["scales"].data_ptr(), _lib.dtype_code(p["scales"].dtype),
+                                             p["zeros"].data_ptr(), out.data_ptr(), o, k,
+                                             _lib.stream_handle(device)), "fx_w3_gemv_fields")
+    del fields
     partial = torch.empty(workspace_shape(o, k), dtype=torch.float32, device=device)
     for p in payloads[:8]:
         inline_main(x, p, partial, row_tile=256)
@@ -604,7 +619,10 @@ def summarize_pmc(csv_paths, out_json):
         if "copyBuffer" in k:
             mean[k] = {c: sum(sorted(v)[-16:]) / len(sorted(v)[-16:]) for c, v in d.items()}
     copy = [k for k in mean if "copyBuffer" in k and "FETCH_SIZE" in mean[k]]
-    w3 = [k for k in mean if "w3_mfma_kernel" in k]
+    # the planar kernel (FIELDS = false, the last template argument) and the
+    # field-layout one
+    w3 = [k for k in mean if "w3_mfma_kernel" in k and not k.split("(")[0].endswith("true>")]
+    w3_fields = [k for k in mean if "w3_mfma_kernel" in k and k.split("(")[0].endswith("true>")]
     if not copy or not w3:
         raise SystemExit("counter CSVs lack the copy kernel or the W3 kernel")
     kib = CALIBRATION_BYTES / 1024
@@ -626,6 +644,15 @@ def summarize_pmc(csv_paths, out_json):
         "counters": {k.split("(")[0]: {c: round(v, 1) for c, v in d.items()} for k, d in mean.items()
                      if "w3_" in k or "copyBuffer" in k or "rank_one" in k or "hybrid" in k},
     }
+    if w3_fields and "FETCH_SIZE" in mean[w3_fields[0]]:
+        m = mean[w3_fields[0]]
+        summary["field_layout"] = {
+            "kernel": w3_fields[0].split("(")[0],
+            "fetch_kib_raw": round(m["FETCH_SIZE"], 1),
+            "write_kib_raw": round(m.get("WRITE_SIZE", 0.0), 1),
+            "traffic_bytes": int(round(m["FETCH_SIZE"] * fetch_scale * 1024
+                                       + m.get("WRITE_SIZE", 0.0) * (write_scale or 1.0) * 1024)),
+            "algorithmic_bytes": algorithmic_bytes(o, k)}
     g = k // 128
     two_base_bytes = {"rank_one_kernel": 2 * o * k // 8 + 6 * o + 2 * k + 64 * o + 128 + 2 * k + 2 * o,
                       "hybrid_kernel": 32 * g * o + 8 * g * o + 1024 * g + 16 * g + 2 * g * o + 8 * g * o
@@ -793,6 +820,21 @@ def main():
                       f"(average launch over {dominant['copies']} rotating payloads)",
         },
     }
+    field_traffic = None
+    if traffic_file.exists() and "gate/up" in shapes:
+        field_traffic = json.loads(traffic_file.read_text()).get("field_layout", {}).get("traffic_bytes")
+    if dominant.get("fields_GBps") is not None:
+        result["roofline_field_layout"] = {
+            "bound": "hbm",
+            "achieved": dominant["fields_GBps"],
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": dominant["fields_frac_hbm"],
+            "traffic": field_traffic,
+            "algorithmic_bytes": dominant["algorithmic_bytes"],
+            "kernel": f"w3_mfma_kernel on the field layout (fx_w3_gemv_fields) at gate/up "
+                      f"{dominant['O']}x{dominant['K']}, M=1, same payloads repacked once",
+        }
     if not args.no_two_base:
         result["config"]["two_base"] = two_base_bench(device, max(args.steps, 10), args.warmup, stream)
         print(f"# two-base: {result['config']['two_base']}", file=sys.stderr, flush=True)
