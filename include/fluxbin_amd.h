@@ -207,12 +207,11 @@ int fx_head_norm_rope(int ntensors, const void *const *inputs, void *const *outp
  * [n_kv_heads, max_len, head_dim]; query head h reads KV head h / (n_q_heads /
  * n_kv_heads) at slots 0..position (later slots are never read); fp32 scores
  * scaled by `scale`, fp32 softmax and accumulation, out [n_q_heads, head_dim]
- * rounded to dtype.  One launch over key chunks whose partials the last
- * workgroup of each KV head combines (a second combine launch beyond 16 chunks
- * per KV head), through `workspace` (fx_decode_attention_workspace_bytes bytes,
- * 16-byte aligned): allocate it zero-filled once; its leading arrival counters
- * are left at zero by every call, so it is reused without clearing.  Calls that
- * share a workspace must not overlap.  head_dim in {64, 128, 256}.
+ * rounded to dtype.  One launch over key chunks and a second that combines
+ * their partials (one launch when one chunk covers the context), through
+ * `workspace` (fx_decode_attention_workspace_bytes bytes, 16-byte aligned, no
+ * initial contents needed).  Calls that share a workspace must not overlap.
+ * head_dim in {64, 128, 256}.
  */
 size_t fx_decode_attention_workspace_bytes(int n_q_heads, int max_len, int head_dim);
 int fx_decode_attention(const void *q, const void *k_cache, const void *v_cache, void *workspace,

@@ -848,16 +848,14 @@ int fx_head_norm_rope(int ntensors, const void* const* inputs, void* const* outp
   return check_launch("head_norm_rope_kernel");
 }
 
-// Attention workspace: one arrival counter per KV head (at most n_q_heads),
-// padded to 256 bytes, then the fp32 partials [Hq, splits, D + 2].
-size_t attn_counter_bytes(int n_q_heads) { return (size_t(n_q_heads) * sizeof(unsigned) + 255) / 256 * 256; }
-
+// Attention workspace: the fp32 partials, [Hq, splits, D] outputs then
+// [Hq, splits, 2] (max, sum).
 size_t fx_decode_attention_workspace_bytes(int n_q_heads, int max_len, int head_dim) {
   if (n_q_heads < 1 || max_len < 1 || (head_dim != 64 && head_dim != 128 && head_dim != 256)) return 0;
   // the most splits any position can use: one key per thread
   const int keys = fx::attn_keys_per_block(head_dim, 1);
   const size_t splits = (size_t(max_len) + keys - 1) / keys;
-  return attn_counter_bytes(n_q_heads) + size_t(n_q_heads) * splits * (size_t(head_dim) + 2) * sizeof(float);
+  return size_t(n_q_heads) * splits * (size_t(head_dim) + 2) * sizeof(float);
 }
 
 namespace {
@@ -884,43 +882,39 @@ int decode_attention(const void* q, const void* k_cache, const void* v_cache, vo
   a.q = static_cast<const uint16_t*>(q);
   a.k = static_cast<const uint16_t*>(k_cache);
   a.v = static_cast<const uint16_t*>(v_cache);
-  a.arrivals = static_cast<unsigned*>(workspace);
-  a.partial = reinterpret_cast<float*>(static_cast<char*>(workspace) + attn_counter_bytes(n_q_heads));
+  a.partial = static_cast<float*>(workspace);
   a.out = static_cast<uint16_t*>(out);
   a.Hq = n_q_heads;
   a.Hk = n_kv_heads;
   a.Lmax = max_len;
   a.pos = position;
-  // keys per thread: the fewest whose splits the last workgroup of each KV head
-  // can combine inline (one launch); beyond that, the most (fewest partials)
-  // that still gives a workgroup per CU, one otherwise, and the combine kernel
-  const int n = position + 1, cus = device_cu_count(), G = n_q_heads / n_kv_heads;
+  // keys per thread: one split (direct output) when some kpt covers the
+  // context in one workgroup; else the kpt with the fewest keys per CU
+  // (ceil(workgroups / CUs) * kpt, the split launch's bytes on its busiest CU),
+  // ties to the larger kpt (fewer partials for the combine launch)
+  const int n = position + 1, cus = device_cu_count();
   const auto splits_for = [&](int kpt) {
     const int keys = fx::attn_keys_per_block(head_dim, kpt);
     return (n + keys - 1) / keys;
   };
   a.kpt = 0;
-  if (G * head_dim <= 256 * fx::kAttnInlineOutputs)
-    for (int kpt : {1, 2, 4})
-      if (splits_for(kpt) <= fx::kAttnInlineSplits && G * splits_for(kpt) <= 256) {
-        a.kpt = kpt;
-        break;
-      }
+  for (int kpt : {1, 2, 4})
+    if (splits_for(kpt) == 1) {
+      a.kpt = kpt;
+      break;
+    }
   if (a.kpt == 0) {
-    a.kpt = 1;
-    for (int kpt : {4, 2})
-      if (long(n_kv_heads) * splits_for(kpt) >= cus) {
+    long best = 0;
+    for (int kpt : {4, 2, 1}) {
+      const long load = (long(n_kv_heads) * splits_for(kpt) + cus - 1) / cus * kpt;
+      if (a.kpt == 0 || load < best) {
         a.kpt = kpt;
-        break;
+        best = load;
       }
+    }
   }
   a.splits = splits_for(a.kpt);
   if (a.splits > 65535) return fail(FX_EINVAL, "position %d needs %d key splits (at most 65535)", position, a.splits);
-  a.combine = a.splits == 1 ? fx::kAttnDirect
-              : a.splits <= fx::kAttnInlineSplits && G * a.splits <= 256 &&
-                        G * head_dim <= 256 * fx::kAttnInlineOutputs
-                  ? fx::kAttnLastArrival
-                  : fx::kAttnCombineKernel;
   a.scale = scale;
   a.pre = pre;
   fx::launch_decode_attention(dtype, head_dim, a, static_cast<hipStream_t>(stream));

@@ -1,6 +1,5 @@
 // Batch-1 decode kernels for gfx950: grouped-query attention over a static KV
-// cache (split over key chunks, then combined in the same launch by the last
-// workgroup of each KV head, or by a second kernel for long contexts), and the
+// cache (split over key chunks, then combined by a second kernel), and the
 // SwiGLU activation.
 //
 // Attention semantics (stock HF Qwen3 attention through SDPA with a boolean
@@ -19,16 +18,6 @@ namespace fx {
 // in registers across passes).
 constexpr int kAttnHeadsPerPass = 4;
 constexpr int kDppRowRor8 = 0x128;  // lane i <- lane (i + 8) mod 16 within each row
-
-// Split partials are stored and read as relaxed device-scope atomics: coherent
-// across the XCDs' L2s without the L2 write-back a device-scope fence costs
-// (one per wave, measured ~19 us per layer at 272 workgroups).
-__device__ __forceinline__ void store_coherent(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float load_coherent(const float* p) {
-  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 
 // Sum over the DB lanes (8, 16 or 32) that hold one key row; every lane of the
 // group receives the same bits.
@@ -54,9 +43,9 @@ __device__ __forceinline__ float key_row_sum(float v) {
 // never read.  Per pass of up to 4 query heads: s = (q . k) * scale reduced over
 // the DB lanes of the row, chunk max over the workgroup, p = e^(s - m),
 // l = sum p, o = sum p v per thread, reduced over the key rows through LDS.
-// partial[(h * splits + chunk) * (D + 2)] = {m, l, o[0..D)}; with one split
-// the output o / l is written instead, and with combine == kAttnLastArrival the
-// KV head's last workgroup to finish combines the partials (arrival counter).
+// po[(h * splits + chunk) * D + d] = o[d] and pml[(h * splits + chunk) * 2] =
+// {m, l} (plain stores: the combine kernel reads them after this launch ends);
+// with one split the output o / l is written instead.
 // PRE: q is the raw projection; each query head is normalised (q_norm) and
 // rotated before scoring, and the key and value of position pos are formed here
 // from the raw projections (k_norm, RoPE; v as is) -- by the workgroup whose
@@ -101,12 +90,12 @@ __device__ __forceinline__ u32x4_t head_norm_rope8(const u32x4_t& x, const u32x4
 template <int DT, int D, int KPT, bool PRE>
 __global__ __launch_bounds__(256) void attn_split_kernel(const uint16_t* __restrict__ q,
                                                          const uint16_t* kc, const uint16_t* vc,
-                                                         float* partial, unsigned* arrivals,
+                                                         float* __restrict__ po, float* __restrict__ pml,
                                                          uint16_t* __restrict__ out, int G,
-                                                         int Lmax, int pos, int splits, int combine,
+                                                         int Lmax, int pos, int splits,
                                                          float scale, AttnPre pre) {
-  asm volatile("" ::"s"(q), "s"(kc), "s"(vc), "s"(partial), "s"(arrivals), "s"(out), "s"(G),
-               "s"(Lmax), "s"(pos), "s"(splits), "s"(combine), "s"(scale));
+  asm volatile("" ::"s"(q), "s"(kc), "s"(vc), "s"(po), "s"(pml), "s"(out), "s"(G),
+               "s"(Lmax), "s"(pos), "s"(splits), "s"(scale));
   if constexpr (PRE)
     asm volatile("" ::"s"(pre.k_raw), "s"(pre.v_raw), "s"(pre.q_weight), "s"(pre.k_weight), "s"(pre.cos),
                  "s"(pre.sin), "s"(pre.eps), "s"(pre.rope_mode));
@@ -277,109 +266,65 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const uint16_t* __restr
 #pragma unroll
       for (int r = 0; r < KS; ++r) total += red_o[r][hh][d];
       if (h < G) {
-        if (combine == kAttnDirect) {
+        if (splits == 1) {
           // the whole context is this chunk: o = sum p v / sum p
           float l = 0.f;
 #pragma unroll
           for (int r = 0; r < KS; ++r) l += red_l[r][hh];
           out[size_t(g * G + h) * D + d] = from_f32<DT>(total * (1.f / l));
         } else {
-          float* dst = partial + (size_t(g * G + h) * splits + chunk) * (D + 2);
-          store_coherent(dst + 2 + d, total);
+          const size_t slot = size_t(g * G + h) * splits + chunk;
+          po[slot * D + d] = total;
           if (d == 0) {
             float l = 0.f;
 #pragma unroll
             for (int r = 0; r < KS; ++r) l += red_l[r][hh];
-            store_coherent(dst, mt[hh]);
-            store_coherent(dst + 1, l);
+            pml[slot * 2] = mt[hh];
+            pml[slot * 2 + 1] = l;
           }
         }
       }
     }
     __syncthreads();  // LDS reused by the next pass
   }
-  if (combine != kAttnLastArrival) return;
-
-  // ---- the last workgroup of this KV head to finish combines its G heads:
-  // o_h = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c over the S splits.
-  // Each wave waits for its device-scope partial stores to complete before the
-  // workgroup's arrival is counted (a device-scope atomic), and the last
-  // arrival reads the partials with device-scope loads issued after the count
-  // returned.  The counter is left at zero for the next call.
-  __shared__ int is_last;
-  __shared__ float cm[256], cl[256];
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (t == 0)
-    is_last = __hip_atomic_fetch_add(arrivals + g, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-              unsigned(splits - 1);
-  __syncthreads();
-  if (!is_last) return;
-  // one load round: every (split, dim) value this thread combines, issued
-  // behind the splits' maxima and sums (the host keeps S <= kAttnInlineSplits,
-  // G * S <= 256 and G * D <= 256 * kAttnInlineOutputs)
-  const int S = splits;
-  const float* base = partial + size_t(g) * G * S * (D + 2);  // [G, S, D + 2]
-  if (t < G * S) {
-    cm[t] = load_coherent(base + size_t(t) * (D + 2));
-    cl[t] = load_coherent(base + size_t(t) * (D + 2) + 1);
-  }
-  constexpr int R = kAttnInlineOutputs, C = kAttnInlineSplits;
-  float v[R][C];
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const int idx = t + 256 * r, hh = idx / D, d = idx % D;
-#pragma unroll
-    for (int c = 0; c < C; ++c)
-      v[r][c] = idx < G * D && c < S ? load_coherent(base + size_t(hh * S + c) * (D + 2) + 2 + d) : 0.f;
-  }
-  __syncthreads();
-  if (t == 0) __hip_atomic_store(arrivals + g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const int idx = t + 256 * r, hh = idx / D, d = idx % D;
-    if (idx >= G * D) break;
-    const float* mh = cm + hh * S;
-    const float* lh = cl + hh * S;
-    float M = -INFINITY;
-    for (int c = 0; c < S; ++c) M = fmaxf(M, mh[c]);
-    float L = 0.f, o = 0.f;
-#pragma unroll
-    for (int c = 0; c < C; ++c) {
-      if (c < S) {
-        const float w = __expf(mh[c] - M);
-        L += w * lh[c];
-        o += w * v[r][c];
-      }
-    }
-    out[size_t(g * G + hh) * D + d] = from_f32<DT>(o * (1.f / L));
-  }
 }
 
 // grid Hq, 256 threads: o_h = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c over the
-// head's splits, taken in blocks of 256 (a running max rescales earlier blocks):
-// one load round for the block's maxima and sums, then each thread sums one
-// output dim over every (256 / D)-th split of the block with eight loads in
-// flight, and the 256 / D partial sums of a dim meet in LDS.
+// head's splits, taken in blocks of 256 (a running max rescales earlier blocks).
+// Thread t sums output dim t % D over the splits t / D, t / D + PARTS, ... of a
+// block (PARTS = 256 / D threads per dim, whose partial sums meet in LDS).  The
+// block's maxima and sums and this thread's first kPre split values are issued
+// in one load round (up to kPre * PARTS splits, 32 at D = 128: every block of a
+// decode length's splits), so the weights' reductions overlap the value loads;
+// further values follow eight in flight.
 template <int DT, int D>
-__global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restrict__ partial,
+__global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restrict__ po,
+                                                          const float* __restrict__ pml,
                                                           uint16_t* __restrict__ out, int splits) {
-  asm volatile("" ::"s"(partial), "s"(out), "s"(splits));
+  asm volatile("" ::"s"(po), "s"(pml), "s"(out), "s"(splits));
   static_assert(D <= 256, "one output dim per thread");
   constexpr int PARTS = 256 / D;  // threads per output dim
+  constexpr int kPre = 16, U = 8;
   __shared__ float wsh[256];
   __shared__ float wred[4];
   __shared__ float ored[PARTS][D];
   __shared__ float lred[4];
-  const int h = blockIdx.x, t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const float* base = partial + size_t(h) * splits * (D + 2);
+  const int h = blockIdx.x, t = threadIdx.x, lane = t & 63, wave = wave_index();
+  const float* vo = po + size_t(h) * splits * D;
+  const float* ml = pml + size_t(h) * splits * 2;
   float M = -INFINITY, L = 0.f, o = 0.f;
   const int part = t / D, d0 = t % D;
   for (int c0 = 0; c0 < splits; c0 += 256) {
     const int n = min(256, splits - c0);
     const bool mine = t < n;
-    const float mc = mine ? base[size_t(c0 + t) * (D + 2)] : -INFINITY;
-    const float lc = mine ? base[size_t(c0 + t) * (D + 2) + 1] : 0.f;
+    const float mc = mine ? ml[size_t(c0 + t) * 2] : -INFINITY;
+    const float lc = mine ? ml[size_t(c0 + t) * 2 + 1] : 0.f;
+    float v0[kPre];
+#pragma unroll
+    for (int u = 0; u < kPre; ++u) {
+      const int cc = part + u * PARTS;
+      v0[u] = cc < n ? vo[size_t(c0 + cc) * D + d0] : 0.f;
+    }
     float bm = wave_max(mc);
     if (lane == 0) wred[wave] = bm;
     __syncthreads();
@@ -393,14 +338,17 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
     __syncthreads();
     L = L * rescale + (lred[0] + lred[1] + lred[2] + lred[3]);
     o *= rescale;
-    // this thread: dim d0 over splits part, part + PARTS, ..., eight loads in flight
-    constexpr int U = 8;
-    for (int c = part; c < n; c += PARTS * U) {
+#pragma unroll
+    for (int u = 0; u < kPre; ++u) {
+      const int cc = part + u * PARTS;
+      o += (cc < n ? wsh[cc] : 0.f) * v0[u];
+    }
+    for (int c = part + kPre * PARTS; c < n; c += PARTS * U) {
       float v[U];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int cc = c + u * PARTS;
-        v[u] = cc < n ? base[size_t(c0 + cc) * (D + 2) + 2 + d0] : 0.f;
+        v[u] = cc < n ? vo[size_t(c0 + cc) * D + d0] : 0.f;
       }
 #pragma unroll
       for (int u = 0; u < U; ++u) {
@@ -436,16 +384,16 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* __restric
 
 template <int DT, int D, int KPT>
 void attn_launch(const AttnArgs& a, hipStream_t s) {
+  float* po = a.partial;
+  float* pml = a.partial + size_t(a.Hq) * a.splits * D;
   if (a.pre.k_raw)
     hipLaunchKernelGGL((attn_split_kernel<DT, D, KPT, true>), dim3(a.Hk, a.splits), dim3(256), 0, s, a.q, a.k,
-                       a.v, a.partial, a.arrivals, a.out, a.Hq / a.Hk, a.Lmax, a.pos, a.splits, a.combine,
-                       a.scale, a.pre);
+                       a.v, po, pml, a.out, a.Hq / a.Hk, a.Lmax, a.pos, a.splits, a.scale, a.pre);
   else
     hipLaunchKernelGGL((attn_split_kernel<DT, D, KPT, false>), dim3(a.Hk, a.splits), dim3(256), 0, s, a.q, a.k,
-                       a.v, a.partial, a.arrivals, a.out, a.Hq / a.Hk, a.Lmax, a.pos, a.splits, a.combine,
-                       a.scale, a.pre);
-  if (a.combine == kAttnCombineKernel)
-    hipLaunchKernelGGL((attn_combine_kernel<DT, D>), dim3(a.Hq), dim3(256), 0, s, a.partial, a.out, a.splits);
+                       a.v, po, pml, a.out, a.Hq / a.Hk, a.Lmax, a.pos, a.splits, a.scale, a.pre);
+  if (a.splits > 1)
+    hipLaunchKernelGGL((attn_combine_kernel<DT, D>), dim3(a.Hq), dim3(256), 0, s, po, pml, a.out, a.splits);
 }
 
 template <int DT, int D>

@@ -22,24 +22,20 @@ struct AttnArgs {
   const uint16_t* q;   // [Hq, D]
   const uint16_t* k;   // [Hk, Lmax, D]
   const uint16_t* v;   // [Hk, Lmax, D]
-  float* partial;      // [Hq, splits, D + 2]
-  unsigned* arrivals;  // [Hk] arrival counters (zero between calls)
+  float* partial;      // [Hq, splits, D] split outputs, then [Hq, splits, 2] their (max, sum)
   uint16_t* out;       // [Hq, D]
   int Hq, Hk, Lmax, pos;
   int kpt, splits;     // keys per thread (1, 2, 4); splits = ceil((pos + 1) / (keys per workgroup))
-  int combine;         // kAttnDirect, kAttnLastArrival or kAttnCombineKernel
   float scale;
   AttnPre pre;
 };
 
-// How the per-split partials become the output: one split writes it directly;
-// up to kAttnInlineSplits splits (with at most 256 (head, split) pairs and
-// 256 * kAttnInlineOutputs output values per KV head) are combined by the last
-// workgroup of the KV head to finish, in one load round; more go through the
-// separate combine kernel.
-enum : int { kAttnDirect = 0, kAttnLastArrival = 1, kAttnCombineKernel = 2 };
-constexpr int kAttnInlineSplits = 16;
-constexpr int kAttnInlineOutputs = 4;
+// One split writes the output directly; more write partials that a second
+// kernel (one workgroup per query head) combines.  A last-arriving-workgroup
+// combine inside the split kernel measured slower at every decode length: its
+// store wait, arrival atomic and coherent reloads form three dependent memory
+// round trips on one workgroup (9.55 vs 8.91 us at 544 keys, 10.3 vs 7.9 us at
+// 512, Qwen3-8B heads), more than the second launch.
 
 // Keys one attention workgroup covers: 256 / (D / 8) key rows times keys per thread.
 inline int attn_keys_per_block(int head_dim, int kpt) { return 256 / (head_dim / 8) * kpt; }

@@ -348,7 +348,7 @@ class NativeDecodeSession:
             self.lm_ws = torch.zeros(lib.fx_lm_head_argmax_workspace_bytes(), dtype=torch.uint8,
                                      device=self.device)  # arrival counter starts at zero
         nbytes = lib.fx_decode_attention_workspace_bytes(self.heads, self.maximum_length, self.head_dim)
-        self.attn_ws = torch.zeros(nbytes // 4 + 64, dtype=torch.float32, device=self.device)  # arrival counters start at zero
+        self.attn_ws = torch.empty(nbytes // 4 + 64, dtype=torch.float32, device=self.device)  # split partials
         self.graph = None
         self.kernel_nodes = None
         self.launches_per_step = None
