@@ -58,6 +58,7 @@ def test_decode_attention(gpu, dtype, hq, hk, d, lmax, pos):
 
 @pytest.mark.parametrize("dtype", ["bf16", "f16"])
 @pytest.mark.parametrize("hq,hk,d,lmax,pos,rope_mode", [(32, 8, 128, 544, 543, 1), (32, 8, 128, 544, 300, 1),
+                                                        (32, 8, 128, 544, 40, 1),
                                                         (4, 2, 64, 130, 0, 1), (12, 2, 128, 200, 150, 2),
                                                         (8, 8, 256, 70, 69, 1)])
 def test_decode_attention_rope(gpu, dtype, hq, hk, d, lmax, pos, rope_mode):
