@@ -7,12 +7,13 @@ capture all steps in one hipGraph, time a replay.  What differs is the step:
 instead of the HF module tree (~27 kernels per layer) each decoder layer is,
 with structural W3 Linears,
 
-    q|k|v GEMV normalising the residual -> attention with q/k norm, RoPE, the
-    KV-cache write and the split combine folded in -> o GEMV adding into the
-    residual -> gate|up GEMV normalising, with SwiGLU -> down GEMV adding into
-    the residual
+    q|k|v GEMV normalising the residual -> attention over key splits with q/k
+    norm, RoPE and the KV-cache write folded in -> the splits' combine -> o
+    GEMV adding into the residual -> gate|up GEMV normalising, with SwiGLU ->
+    down GEMV adding into the residual
 
-(5 launches), followed once per token by one launch for the final RMSNorm, the
+(6 launches; 5 while one split covers the context), followed once per token by
+one launch for the final RMSNorm, the
 bf16 LM head and the argmax.  Other Linears (the bf16 arm) take add+RMSNorm
 kernels and ``torch.matmul`` between the same attention launches.  The
 arithmetic and rounding points are the stock HF Qwen3 modules' (RMSNorm, RoPE,
