@@ -595,7 +595,9 @@ int check_format(int payload_format, const int16_t* perm) {
 
 // One-row field-layout launch (one K split); epilogue and prologue from a.
 int run_fields(const MfmaArgs& base, int x_dtype, int scale_dtype, bool normin, hipStream_t s) {
-  const MfmaPlan p = single_split_plan(base.O, base.G);
+  MfmaPlan p = single_split_plan(base.O, base.G);
+  const int tiles = fx::fields_row_tiles(normin, base.O);
+  if (tiles != p.tiles) p = make_mfma_plan(base.O, base.G, p.nw, 1, base.G, tiles);
   MfmaArgs a = base;
   a.gps = p.gps;
   a.row_blocks = p.row_blocks;

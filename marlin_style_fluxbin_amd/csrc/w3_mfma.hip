@@ -570,7 +570,7 @@ void w3_mfma_kernel(
                "s"(O), "s"(G), "s"(gps), "s"(row_blocks), "s"(swiglu), "s"(ra.ep_residual), "s"(ra.ep_partial));
   if constexpr (NORMIN)
     asm volatile("" ::"s"(ra.pro_partial), "s"(ra.pro_n), "s"(ra.pro_weight), "s"(ra.pro_eps));
-  static_assert(!FIELDS || (!PERM && MB == 1 && RT == 1 && PD == 1), "field layout: one row, identity order");
+  static_assert(!FIELDS || (!PERM && MB == 1 && PD == 1), "field layout: one row, identity order");
   __shared__ MfmaShared<NW, MB, RT> sh;
   if (VSEL == 1 || (VSEL == 0 && (O & 3) == 0))
     w3_mfma_body<NW, PD, MB, RT, PERM, XDT, SDT, NORMIN, VSEL != 2, FIELDS>(sh, x, perm, planes, scales, zeros,

@@ -57,9 +57,11 @@ FX_MFMA_DECL(dispatch_mfma_f16_t2_perm)
 bool dispatch_mfma_normin(int nw, int xdt, int sdt, const MfmaArgs& a, dim3 grid, hipStream_t s);
 
 // The field-layout instantiations (a.planes holds fields, w3_fields.hip): one
-// activation row, one tile and one batch in flight per wave, identity order,
-// one K split; plain or normalising prologue; nw in {4, 8}.
+// activation row and one batch in flight per wave, identity order, one K split;
+// plain or normalising prologue; nw in {4, 8}.  Row tiles per wave:
+// fields_row_tiles (a.row_blocks must count tiles of that many 16-row tiles).
 bool dispatch_mfma_fields(int nw, bool normin, int xdt, int sdt, const MfmaArgs& a, dim3 grid, hipStream_t s);
+inline int fields_row_tiles(bool normin, int O) { return normin && O % 4 == 0 ? 2 : 1; }
 
 // The bind-time repack planes [G, 3, O, 16] -> fields [G, 3, O, 16].
 void launch_planes_to_fields(const uint8_t* planes, uint8_t* fields, int O, int G, hipStream_t s);

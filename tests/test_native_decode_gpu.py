@@ -266,7 +266,8 @@ def test_gemv_residual_epilogue(gpu, o, k, dtype, permute, fmt):
 
 @pytest.mark.parametrize("fmt", ["planar", "fields"])
 @pytest.mark.parametrize("rows,k,dtype,swiglu", [(6144, 4096, "bf16", False), (24576, 4096, "bf16", True),
-                                                 (96, 1024, "f16", True), (34, 512, "bf16", False)])
+                                                 (96, 1024, "f16", True), (34, 512, "bf16", False),
+                                                 (48, 1024, "bf16", False), (40, 512, "bf16", True)])
 def test_gemv_rmsnormed_prologue(gpu, rows, k, dtype, swiglu, fmt):
     """fx_w3_gemv_rmsnormed equals the RMSNorm kernel followed by the plain GEMV
     (or SwiGLU GEMV) of the same payload format bit for bit.  h holds small
