@@ -34,8 +34,8 @@ struct AttnArgs {
 // kernel (one workgroup per query head) combines.  A last-arriving-workgroup
 // combine inside the split kernel measured slower at every decode length: its
 // store wait, arrival atomic and coherent reloads form three dependent memory
-// round trips on one workgroup (9.55 vs 8.91 us at 544 keys, 10.3 vs 7.9 us at
-// 512, Qwen3-8B heads), more than the second launch.
+// round trips on one workgroup (9.55 vs 7.46 us at 544 keys, 10.3 vs 7.5 us at
+// 512, Qwen3-8B heads with q/k norm and RoPE), more than the second launch.
 
 // Keys one attention workgroup covers: 256 / (D / 8) key rows times keys per thread.
 inline int attn_keys_per_block(int head_dim, int kpt) { return 256 / (head_dim / 8) * kpt; }
