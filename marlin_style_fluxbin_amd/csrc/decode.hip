@@ -290,13 +290,14 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const uint16_t* __restr
 }
 
 // grid Hq, 256 threads: o_h = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c over the
-// head's splits, taken in blocks of 256 (a running max rescales earlier blocks).
-// Thread t sums output dim t % D over the splits t / D, t / D + PARTS, ... of a
-// block (PARTS = 256 / D threads per dim, whose partial sums meet in LDS).  The
-// block's maxima and sums and this thread's first kPre split values are issued
-// in one load round (up to kPre * PARTS splits, 32 at D = 128: every block of a
-// decode length's splits), so the weights' reductions overlap the value loads;
-// further values follow eight in flight.
+// head's splits, taken in blocks of 64 (a running max rescales earlier blocks).
+// Every wave forms the block's maximum and weighted sum itself (lane c holds
+// split c's max and sum: no LDS round for them).  Thread t sums output dim
+// t % D over the splits t / D, t / D + PARTS, ... of the block (PARTS = 256 / D
+// threads per dim, whose partial sums meet in LDS once at the end), taking each
+// split's weight from its own load of that split's max.  The block's maxima and
+// sums and this thread's first kPre split values are issued in one load round
+// (kPre * PARTS splits: 32 at D = 128, every block of a decode length's splits).
 template <int DT, int D>
 __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restrict__ po,
                                                           const float* __restrict__ pml,
@@ -304,60 +305,36 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
   asm volatile("" ::"s"(po), "s"(pml), "s"(out), "s"(splits));
   static_assert(D <= 256, "one output dim per thread");
   constexpr int PARTS = 256 / D;  // threads per output dim
-  constexpr int kPre = 16, U = 8;
-  __shared__ float wsh[256];
-  __shared__ float wred[4];
+  constexpr int kPre = 16;
   __shared__ float ored[PARTS][D];
-  __shared__ float lred[4];
-  const int h = blockIdx.x, t = threadIdx.x, lane = t & 63, wave = wave_index();
+  const int h = blockIdx.x, t = threadIdx.x, lane = t & 63;
   const float* vo = po + size_t(h) * splits * D;
   const float* ml = pml + size_t(h) * splits * 2;
   float M = -INFINITY, L = 0.f, o = 0.f;
   const int part = t / D, d0 = t % D;
-  for (int c0 = 0; c0 < splits; c0 += 256) {
-    const int n = min(256, splits - c0);
-    const bool mine = t < n;
-    const float mc = mine ? ml[size_t(c0 + t) * 2] : -INFINITY;
-    const float lc = mine ? ml[size_t(c0 + t) * 2 + 1] : 0.f;
-    float v0[kPre];
+  for (int c0 = 0; c0 < splits; c0 += 64) {
+    const int n = min(64, splits - c0);
+    const float mc = lane < n ? ml[size_t(c0 + lane) * 2] : -INFINITY;
+    const float lc = lane < n ? ml[size_t(c0 + lane) * 2 + 1] : 0.f;
+    float v0[kPre], m0[kPre];
 #pragma unroll
     for (int u = 0; u < kPre; ++u) {
       const int cc = part + u * PARTS;
       v0[u] = cc < n ? vo[size_t(c0 + cc) * D + d0] : 0.f;
+      m0[u] = cc < n ? ml[size_t(c0 + cc) * 2] : -INFINITY;
     }
-    float bm = wave_max(mc);
-    if (lane == 0) wred[wave] = bm;
-    __syncthreads();
-    bm = fmaxf(fmaxf(wred[0], wred[1]), fmaxf(wred[2], wred[3]));
-    const float Mn = fmaxf(M, bm);
+    const float Mn = fmaxf(M, wave_max(mc));
     const float rescale = M == -INFINITY ? 0.f : __expf(M - Mn);
-    const float w = mine ? __expf(mc - Mn) : 0.f;
-    wsh[t] = w;
-    float lw = wave_sum(w * lc);
-    if (lane == 0) lred[wave] = lw;
-    __syncthreads();
-    L = L * rescale + (lred[0] + lred[1] + lred[2] + lred[3]);
+    L = L * rescale + wave_sum(lane < n ? __expf(mc - Mn) * lc : 0.f);
     o *= rescale;
 #pragma unroll
     for (int u = 0; u < kPre; ++u) {
       const int cc = part + u * PARTS;
-      o += (cc < n ? wsh[cc] : 0.f) * v0[u];
+      o += (cc < n ? __expf(m0[u] - Mn) : 0.f) * v0[u];
     }
-    for (int c = part + kPre * PARTS; c < n; c += PARTS * U) {
-      float v[U];
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int cc = c + u * PARTS;
-        v[u] = cc < n ? vo[size_t(c0 + cc) * D + d0] : 0.f;
-      }
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int cc = c + u * PARTS;
-        o += (cc < n ? wsh[cc] : 0.f) * v[u];
-      }
-    }
+    for (int cc = part + kPre * PARTS; cc < n; cc += PARTS)
+      o += __expf(ml[size_t(c0 + cc) * 2] - Mn) * vo[size_t(c0 + cc) * D + d0];
     M = Mn;
-    __syncthreads();  // wsh / wred / lred reused by the next block
   }
   ored[part][d0] = o;
   __syncthreads();
