@@ -48,13 +48,21 @@ def config_codes(o: int, k: int, *, seed: int = 0, zeros: bool = True, scale_dty
 
 
 def layout_from_codes(codes, scales, zeros, perm):
-    """Product-side planar layout (torch, CPU) for original-order codes."""
-    from marlin_style_fluxbin_amd.gptq_deployment import planar_from_codes
+    """Planar layout (torch, CPU) for original-order codes.
+
+    The planes come from the oracle's packer (``oracle.w3.planar_from_codes``,
+    pinned by brute force over every byte value and code position), not from
+    the product's, so a packer mistake in the product cannot hide behind planes
+    that both the kernels and the truth read; ``tests/test_gptq_deployment.py``
+    pins the product's packer against the oracle separately.
+    """
+    from oracle import w3
 
     k = codes.shape[0]
     perm_t = torch.arange(k, dtype=torch.int16) if perm is None else perm
+    planes = w3.planar_from_codes(codes.numpy(), perm_t.numpy().astype(np.int64))
     layout = {
-        "planes": planar_from_codes(codes, perm_t.to(torch.int64)),
+        "planes": torch.from_numpy(planes),
         "scales": scales.contiguous(),
         "perm": perm_t.contiguous(),
     }
