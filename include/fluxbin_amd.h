@@ -96,6 +96,19 @@ int fx_w3_gemv(const void *x, int x_dtype, const uint8_t *planes, const void *sc
                int scale_dtype, const uint8_t *zeros, const int16_t *perm, void *workspace,
                size_t workspace_bytes, void *out, int M, int O, int K, int arithmetic,
                void *stream);
+/* fx_w3_gemv without a workspace argument.  No counterpart in the reference: it is
+ * for callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  The K-split partials that
+ * fx_w3_gemv keeps in the caller's workspace live in a 4 MiB array of the library,
+ * one per GPU, held until the process ends; its device address is resolved on the
+ * first call on each device.  Calls whose fx_w3_gemv_workspace_bytes(M, O, K)
+ * exceeds 4 MiB fail with FX_EINVAL.  The array keeps the last call's contents and
+ * every call overwrites what it reads, so nothing needs clearing; calls that
+ * overlap on one GPU (different streams, or host threads) race on it and must be
+ * serialised by the caller.  Same kernels and results as fx_w3_gemv. */
+int fx_w3_gemv_noalloc(const void *x, int x_dtype, const uint8_t *planes, const void *scales,
+                       int scale_dtype, const uint8_t *zeros, const int16_t *perm, void *out, int M,
+                       int O, int K, int arithmetic, void *stream);
 /* Fused gate|up projection and SwiGLU of a Qwen3 MLP for one activation row.  No
  * single reference entry point: it replaces the reference's two PackedW3Linear
  * calls (gate_proj, up_proj; w3_lut_deployment.py:250-359) followed by HF

@@ -497,7 +497,7 @@ bool two_base_config(int O, int G, int waves, int prefetch, int groups_per_split
 
 extern "C" {
 
-int fx_abi_version(void) { return 10; }
+int fx_abi_version(void) { return 11; }
 
 const char* fx_last_error(void) { return g_error; }
 
@@ -573,6 +573,54 @@ int fx_w3_gemv(const void* x, int x_dtype, const uint8_t* planes, const void* sc
                          workspace_bytes, out, M, O, K, arithmetic, s);
   return run_mfma(x, x_dtype, planes, scales, scale_dtype, zeros, perm, workspace,
                   workspace_bytes, out, M, O, K, default_mfma_plan(O, K / 128), s);
+}
+
+// ------------------------------------------------------------------ allocation-free GEMV
+// Scratch of fx_w3_gemv_noalloc: the fp32 K-split partials that fx_w3_gemv keeps in
+// its caller's workspace.  One copy per GPU, held until the process ends.  Host
+// code never uses the array's name as an address (in host code it is a host-side
+// stand-in): each device's address comes from hipGetSymbolAddress, resolved once
+// per device with that device current, and only that address reaches kernels.
+constexpr size_t kNoallocScratchBytes = size_t(4) << 20;
+static __device__ __align__(256) unsigned char scratch[kNoallocScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_lock;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+int scratch_for_current_device(void** out) {
+  int device = -1;
+  hipError_t e = hipGetDevice(&device);
+  if (e != hipSuccess) return fail(FX_EHIP, "hipGetDevice: %s", hipGetErrorString(e));
+  if (device < 0 || device >= kMaxDevices) return fail(FX_EINVAL, "device %d out of range", device);
+  std::lock_guard<std::mutex> guard(g_scratch_lock);
+  if (!g_scratch_ptr[device]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(FX_EHIP, "hipGetSymbolAddress(scratch) on device %d: %s", device, hipGetErrorString(e));
+    g_scratch_ptr[device] = p;
+  }
+  *out = g_scratch_ptr[device];
+  return FX_OK;
+}
+}  // namespace
+
+int fx_w3_gemv_noalloc(const void* x, int x_dtype, const uint8_t* planes, const void* scales, int scale_dtype,
+                       const uint8_t* zeros, const int16_t* perm, void* out, int M, int O, int K, int arithmetic,
+                       void* stream) {
+  int rc = validate_payload(x, x_dtype, planes, scales, scale_dtype, M, O, K, arithmetic);
+  if (rc) return rc;
+  if (!out) return fail(FX_EINVAL, "out must be non-null");
+  const size_t need = fx_w3_gemv_workspace_bytes(M, O, K);
+  if (need > kNoallocScratchBytes)
+    return fail(FX_EINVAL, "M=%d O=%d K=%d needs %zu bytes of K-split scratch; the allocation-free entry "
+                "holds %zu (use fx_w3_gemv with a caller workspace)", M, O, K, need, kNoallocScratchBytes);
+  void* ws = nullptr;
+  if ((rc = scratch_for_current_device(&ws))) return rc;
+  return fx_w3_gemv(x, x_dtype, planes, scales, scale_dtype, zeros, perm, ws, kNoallocScratchBytes, out, M, O,
+                    K, arithmetic, stream);
 }
 
 // One-row plan with one K split and one tile and batch in flight per wave (the
