@@ -7,14 +7,13 @@ through its C ABI (``include/fluxbin_amd.h``).  There is no CPU substitute on th
 packed route: a missing library raises.
 
 Differences from the reference, all deliberate:
-* ``x`` may carry up to 8 rows on the packed route (config 1's small-M GEMV);
-  the reference sends M > 1 to the dense fallback.
 * The layout may carry ``zeros`` and fp16 scales (see ``gptq_deployment``).
-* ``row_tile`` / ``groups_per_split`` select rows per workgroup and the K split
-  of the reference-shaped functional ops (``inline_main``, ``finish``,
-  ``w3_lut_m1_out``) exactly; the module's own packed route and its prepared
-  decode binding use the single-launch kernel whose K split is reduced inside
-  the launch and whose tiling is chosen from the shape and CU count.
+* ``PackedW3Linear`` with ``structural`` arithmetic and one group per split runs
+  the one-launch MFMA kernel (the same structural sum, another fp32 order); every
+  other route runs the reference's split contract on the table kernel.
+* ``PackedW3Linear(max_packed_rows=n)`` opts 2..n-row inputs into the packed
+  route (config 1's small-M GEMV); by default they take the dense fallback, as
+  in the reference.
 """
 from __future__ import annotations
 
@@ -286,19 +285,45 @@ class W3Gemv:
         return out
 
 
+class _TableRoute:
+    """The reference contract's packed route for one payload: ``fx_w3_m1_out``
+    with the module's ``row_tile`` / ``groups_per_split`` and arithmetic (the
+    table kernel, fp32 split partials summed in split order), one preallocated
+    workspace.  Serves ``decoded_bf16`` and any ``groups_per_split > 1``."""
+
+    def __init__(self, module: "PackedW3Linear", device: torch.device):
+        self.module = module
+        self.ext = load_w3_lut_extension(module.row_tile)
+        shape = workspace_shape(module.out_features, module.in_features, module.groups_per_split)
+        self.workspace = torch.empty(shape, device=device, dtype=torch.float32)
+
+    def __call__(self, x: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
+        m = self.module
+        self.ext.m1_out(x, m.planes, m.scales, m.perm, self.workspace, out, m.groups_per_split,
+                        m.arithmetic == "decoded_bf16", zeros=getattr(m, "zeros", None))
+        return out
+
+
 class PackedW3Linear(nn.Module):
     """Decode-oriented W3 Linear with an explicit dense fallback.
 
-    Reference: ``w3_lut_deployment.py:190-359``.  The packed route serves GPU
-    fp16/bf16 inputs with 1..8 rows; anything else raises unless
-    ``fallback='dense'``, which dequantizes (HIP kernel on GPU) and calls
-    ``F.linear``.  ``route_counts`` counts packed calls under ``packed_m1`` for
-    one row and ``packed_small_m`` for 2..8 rows.
+    Reference: ``w3_lut_deployment.py:190-359``.  One-row GPU fp16/bf16 inputs
+    take the packed route and count under ``packed_m1``; anything else raises
+    unless ``fallback='dense'``, which dequantizes (HIP kernel on GPU) and calls
+    ``F.linear`` (``dense_fallback``), as in the reference.  The packed route is
+    the MFMA kernel for ``structural`` arithmetic with one group per split (one
+    launch), and the reference's table contract (``w3_lut_m1_out``: ``row_tile``,
+    ``groups_per_split``, split partials summed in order) otherwise, which is
+    how ``decoded_bf16`` routes such as ``fast_corrected`` and ``observed_exact``
+    run.
+
+    ``max_packed_rows`` (not in the reference; default 1) lets 2..8-row inputs
+    take the MFMA kernel too; they are then counted under ``packed_small_m``.
     """
 
     def __init__(self, layout: dict, *, bias: torch.Tensor | None = None, fallback: str = "error",
                  row_tile: int | None = None, groups_per_split: int = 1, arithmetic: str = "structural",
-                 route: str = "structural"):
+                 route: str = "structural", max_packed_rows: int = 1):
         super().__init__()
         if fallback not in {"error", "dense"}:
             raise ValueError("fallback must be error or dense")
@@ -314,16 +339,21 @@ class PackedW3Linear(nn.Module):
             zeros = layout.get("zeros")
             if zeros is not None and not bool(((zeros == 3) | (zeros == 4)).all()):
                 raise ValueError("decoded_bf16 arithmetic supports zero-points 3 and 4")
+        if not isinstance(max_packed_rows, int) or not 1 <= max_packed_rows <= MAX_PACKED_ROWS:
+            raise ValueError(f"max_packed_rows must be an integer in [1,{MAX_PACKED_ROWS}]")
         workspace_shape(self.out_features, self.in_features, groups_per_split)
         self.groups_per_split = groups_per_split
         self.arithmetic = arithmetic
         self.route = route
         self.fallback = fallback
+        self.max_packed_rows = max_packed_rows
         self.route_counts = {"packed_m1": 0, "dense_fallback": 0}
+        if max_packed_rows > 1:
+            self.route_counts["packed_small_m"] = 0
         self.last_route = "not_called"
         self._decode_binding = None
         self._decode_audit = False
-        self._gemv = None
+        self._packed = None
         perm = layout["perm"]
         self._perm_identity = bool(torch.equal(perm.long().cpu(), torch.arange(self.in_features)))
         self._fields = FIELDS + tuple(f for f in OPTIONAL_FIELDS if f in layout)
@@ -331,6 +361,12 @@ class PackedW3Linear(nn.Module):
             self.register_buffer(name, layout[name].detach().clone())
         self.register_buffer("bias", None if bias is None else bias.detach().clone())
         self.register_buffer("_decode_output", None, persistent=False)
+
+    @property
+    def uses_table_route(self) -> bool:
+        """True when the packed route is the reference's table contract rather
+        than the one-launch MFMA kernel."""
+        return self.arithmetic != "structural" or self.groups_per_split != 1
 
     def layout(self) -> dict:
         return {name: getattr(self, name) for name in self._fields}
@@ -342,13 +378,19 @@ class PackedW3Linear(nn.Module):
 
     def _apply(self, fn, recurse=True):
         self.clear_prepared_decode()
-        self._gemv = None
+        self._packed = None
         return super()._apply(fn, recurse=recurse)
 
-    def _kernel(self) -> W3Gemv:
-        if self._gemv is None or self._gemv.layout["planes"].data_ptr() != self.planes.data_ptr():
-            self._gemv = W3Gemv(self.layout(), arithmetic=self.arithmetic, perm_identity=self._perm_identity)
-        return self._gemv
+    def _route_for(self, rows: int, device: torch.device):
+        """The bound packed-route callable ``(x [rows, K], out [rows, O])``."""
+        if rows == 1 and self.uses_table_route:
+            if not isinstance(self._packed, _TableRoute) or self._packed.workspace.device != device:
+                self._packed = _TableRoute(self, device)
+            return self._packed
+        if not isinstance(self._packed, W3Gemv) or self._packed.layout["planes"].data_ptr() != self.planes.data_ptr():
+            self._packed = W3Gemv(self.layout(), arithmetic=self.arithmetic, perm_identity=self._perm_identity,
+                                  max_rows=self.max_packed_rows)
+        return self._packed
 
     def bind_prepared_decode(self, dtype: torch.dtype) -> None:
         if self._decode_binding is not None:
@@ -360,7 +402,7 @@ class PackedW3Linear(nn.Module):
         if device.type != "cuda":
             raise ValueError("prepared decode requires CUDA (a ROCm GPU)")
         validate_planar_w3(layout, check_values=False)
-        kernel = self._kernel()
+        kernel = self._route_for(1, device)
         self._decode_output = torch.empty((1, self.out_features), device=device, dtype=dtype)
         output = self._decode_output
         shaped = output.view(1, 1, self.out_features)
@@ -390,7 +432,7 @@ class PackedW3Linear(nn.Module):
         if x.ndim < 2 or x.shape[-1] != self.in_features:
             raise ValueError("expected [...,K] input")
         m = x.numel() // self.in_features
-        if not (1 <= m <= MAX_PACKED_ROWS) or not x.is_cuda or x.dtype not in (torch.float16, torch.bfloat16):
+        if not (1 <= m <= self.max_packed_rows) or not x.is_cuda or x.dtype not in (torch.float16, torch.bfloat16):
             if self.fallback != "dense":
                 raise ValueError("unsupported input; enable explicit dense fallback if needed")
             self.last_route = "dense_fallback"
@@ -398,10 +440,10 @@ class PackedW3Linear(nn.Module):
             return F.linear(x, restore_planar_w3(self.layout(), dtype=x.dtype), self.bias)
         route = "packed_m1" if m == 1 else "packed_small_m"
         self.last_route = route
-        self.route_counts[route] = self.route_counts.get(route, 0) + 1
+        self.route_counts[route] += 1
         flat = x.reshape(m, self.in_features).contiguous()
         output = torch.empty((m, self.out_features), device=x.device, dtype=x.dtype)
-        self._kernel()(flat, output)
+        self._route_for(m, x.device)(flat, output)
         if self.bias is not None:
             output.add_(self.bias)
         return output.reshape(*x.shape[:-1], self.out_features)

@@ -212,3 +212,52 @@ def test_dense_fallback_on_gpu_uses_device_restore(gpu):
     assert module.route_counts["dense_fallback"] == 1
     decoded = w3.matvec_decoded(x.float().cpu().numpy(), ol, "bf16")
     assert_rel(y.float().cpu().numpy(), decoded, 1e-2)
+
+
+@pytest.mark.parametrize("o,k", [(4096, 4096), (12288, 4096), (4096, 12288), (1024, 4096)])
+@pytest.mark.parametrize("route", ["fast_corrected", "observed_exact", "structural"])
+def test_module_routes_follow_the_reference_split_contract(gpu, o, k, route):
+    """PackedW3Linear carries its route's groups_per_split and arithmetic onto the
+    packed route (reference w3_lut_deployment.py:293-312): a decoded_bf16 or split
+    route is bit-equal to w3_lut_m1_out with the same row tile and split, in eager
+    and prepared form, and within the stated bars of its truth."""
+    from marlin_style_fluxbin_amd import qwen3_w3_route
+
+    layout, dl, ol = _setup(o, k, seed=5, zeros=True, scale_dtype=torch.bfloat16)
+    policy = qwen3_w3_route(route, o, k)
+    module = PackedW3Linear(dl, route=route, **policy)
+    x = _x(1, k, torch.bfloat16, seed=6).to(gpu)
+    with torch.inference_mode():
+        y = module(x)
+    assert module.route_counts == {"packed_m1": 1, "dense_fallback": 0}
+    truth = (w3.matvec_decoded(x.float().cpu().numpy(), ol, "bf16") if policy["arithmetic"] == "decoded_bf16"
+             else w3.matvec_exact(x.float().cpu().numpy(), ol))
+    assert_half_ulp(y.float().cpu().numpy(), truth, "bf16", rel_slack=1e-5)
+    if module.uses_table_route:
+        ws = torch.full(workspace_shape(o, k, policy["groups_per_split"]), float("nan"), device=gpu)
+        want = torch.empty(1, o, dtype=torch.bfloat16, device=gpu)
+        w3_lut_m1_out(x, dl, want, ws, row_tile=policy["row_tile"], groups_per_split=policy["groups_per_split"],
+                      arithmetic=policy["arithmetic"])
+        assert torch.equal(y.view(torch.int16), want.view(torch.int16))
+    module.bind_prepared_decode(torch.bfloat16)
+    module._decode_audit = True
+    with torch.inference_mode():
+        prepared = module(x.view(1, 1, k))
+    assert torch.equal(prepared.view(1, o).view(torch.int16), y.view(torch.int16))
+    assert module.route_counts == {"packed_m1": 2, "dense_fallback": 0}
+
+
+def test_module_small_m_opt_in(gpu):
+    layout, dl, ol = _setup(1024, 4096, seed=7, zeros=True, scale_dtype=torch.float16)
+    x = _x(4, 4096, torch.bfloat16, seed=7).to(gpu)
+    default = PackedW3Linear(dl, fallback="dense", row_tile=512)
+    opted = PackedW3Linear(dl, row_tile=512, max_packed_rows=8)
+    with torch.inference_mode():
+        dense = default(x)
+        packed = opted(x)
+    assert default.route_counts == {"packed_m1": 0, "dense_fallback": 1}
+    assert opted.route_counts == {"packed_m1": 0, "dense_fallback": 0, "packed_small_m": 1}
+    want = torch.empty(4, 1024, dtype=torch.bfloat16, device=gpu)
+    W3Gemv(dl)(x, want)
+    assert torch.equal(packed.view(torch.int16), want.view(torch.int16))
+    assert_rel(dense.float().cpu().numpy(), w3.matvec_decoded(x.float().cpu().numpy(), ol, "bf16"), 1e-2)
