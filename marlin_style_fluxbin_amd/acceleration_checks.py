@@ -1,58 +1,100 @@
 """Numerical gate and paired GPU timing protocol for decode comparisons.
 
-Reference: ``acceleration_checks.py`` (``numerical_gate`` :7-22,
-``stepwise_nrmse`` :25-41, ``paired_cuda_timing`` :44-64).  Same frozen
-thresholds and result keys, so reports from either implementation compare.
+Contract of the reference's ``acceleration_checks.py`` (``numerical_gate`` :7-22,
+``stepwise_nrmse`` :25-41, ``paired_cuda_timing`` :44-64): the frozen v1 gate
+thresholds (elementwise factor 0.02 against a bf16 reference, 0.002 otherwise;
+normalized RMSE limit a quarter of it), the result keys, and the timing schedule
+(warm-up per arm, alternating arm order per round, median, 10% stability bound)
+are kept so reports from either implementation compare.  The code is organised
+around an error-statistics record and a precomputed round schedule.
 """
 from __future__ import annotations
 
 import statistics
+from dataclasses import dataclass
 
 import torch
+
+GATE_FACTOR = {torch.bfloat16: 0.02}  # elementwise tolerance factor by reference dtype
+DEFAULT_GATE_FACTOR = 0.002
+STABLE_RELATIVE_RANGE = 0.10
+
+
+@dataclass(frozen=True)
+class _ErrorStats:
+    rms: float          # root mean square of the reference
+    max_abs: float
+    nrmse: float
+    within: bool        # every |a - b| <= factor * (rms + |b|) + 1e-6
+
+    @classmethod
+    def of(cls, actual: torch.Tensor, expected: torch.Tensor, factor: float) -> "_ErrorStats":
+        a = actual.detach().to(torch.float64)
+        b = expected.detach().to(torch.float64)
+        error = a - b
+        rms = float(torch.linalg.vector_norm(b) / b.numel() ** 0.5)
+        nrmse = float(torch.linalg.vector_norm(error) / error.numel() ** 0.5) / max(rms, 1e-12)
+        within = bool((error.abs() <= factor * (rms + b.abs()) + 1e-6).all())
+        return cls(rms, float(error.abs().max()), nrmse, within)
+
+
+def _finite(*tensors: torch.Tensor) -> bool:
+    return all(bool(torch.isfinite(t.detach()).all()) for t in tensors)
 
 
 def numerical_gate(actual: torch.Tensor, expected: torch.Tensor) -> dict:
     """Combined elementwise + normalized-RMSE gate (frozen v1 thresholds).
 
-    Elementwise: ``|a - b| <= tol * (rms(b) + |b|) + 1e-6`` everywhere, with
-    ``tol = 0.02`` for bf16 references and ``0.002`` otherwise; and
-    ``nrmse = rms(a - b) / rms(b) <= tol / 4``.  Computed in float64.
+    Passes when ``|a - b| <= f * (rms(b) + |b|) + 1e-6`` holds everywhere and
+    ``rms(a - b) / rms(b) <= f / 4``, with ``f = 0.02`` for a bf16 ``expected`` and
+    ``0.002`` otherwise; statistics in float64.
     """
     if actual.shape != expected.shape:
         return {"passed": False, "reason": "shape mismatch"}
-    a = actual.detach().double()
-    b = expected.detach().double()
-    if not bool(torch.isfinite(a).all()) or not bool(torch.isfinite(b).all()):
+    if not _finite(actual, expected):
         return {"passed": False, "reason": "nonfinite output"}
-    rms = b.square().mean().sqrt().item()
-    error = a - b
-    nrmse = error.square().mean().sqrt().item() / max(rms, 1e-12)
-    tol = 0.02 if expected.dtype == torch.bfloat16 else 0.002
-    elementwise = bool((error.abs() <= tol * (rms + b.abs()) + 1e-6).all())
-    return {"passed": elementwise and nrmse <= tol / 4, "max_abs_error": error.abs().max().item(),
-            "reference_rms": rms, "normalized_rmse": nrmse, "elementwise_tolerance_factor": tol,
-            "normalized_rmse_limit": tol / 4}
+    factor = GATE_FACTOR.get(expected.dtype, DEFAULT_GATE_FACTOR)
+    stats = _ErrorStats.of(actual, expected, factor)
+    limit = factor / 4
+    return {"passed": stats.within and stats.nrmse <= limit, "max_abs_error": stats.max_abs,
+            "reference_rms": stats.rms, "normalized_rmse": stats.nrmse,
+            "elementwise_tolerance_factor": factor, "normalized_rmse_limit": limit}
 
 
 def stepwise_nrmse(actual: torch.Tensor, expected: torch.Tensor):
-    """Per-step NRMSE of ``[1, steps, vocab]`` logits (report only); None otherwise."""
+    """Per-step NRMSE of ``[1, steps, vocab]`` logits (report only); None for any
+    other shape, mismatched shapes or non-finite values."""
     if actual.shape != expected.shape or actual.ndim != 3 or actual.shape[0] != 1:
         return None
-    a = actual.detach().double()
-    b = expected.detach().double()
-    if not bool(torch.isfinite(a).all()) or not bool(torch.isfinite(b).all()):
+    if not _finite(actual, expected):
         return None
-    rms = b.square().mean(dim=-1).sqrt().clamp_min(1e-12)
-    return [float(v) for v in ((a - b).square().mean(dim=-1).sqrt() / rms)[0]]
+    a = actual.detach().to(torch.float64)[0]
+    b = expected.detach().to(torch.float64)[0]
+    width = b.shape[-1] ** 0.5
+    error_rms = torch.linalg.vector_norm(a - b, dim=-1) / width
+    reference_rms = (torch.linalg.vector_norm(b, dim=-1) / width).clamp_min(1e-12)
+    return (error_rms / reference_rms).tolist()
+
+
+def _round_schedule(names: list[str], rounds: int) -> list[list[str]]:
+    """Arm order per round: forward on even rounds, reversed on odd ones (cancels
+    a systematic first-arm / last-arm bias)."""
+    return [names if r % 2 == 0 else names[::-1] for r in range(rounds)]
+
+
+def _summary(samples: list[float]) -> dict:
+    median = statistics.median(samples)
+    spread = (max(samples) - min(samples)) / median if median > 0 else float("inf")
+    return {"microseconds_per_call": samples, "median_us": median, "relative_range": spread,
+            "stable": spread <= STABLE_RELATIVE_RANGE}
 
 
 def paired_cuda_timing(functions: dict, *, warmup: int = 20, repeats: int = 100, rounds: int = 7) -> dict:
-    """Median microseconds per call of each function, arms alternated per round.
+    """Median microseconds per call of each arm, arms alternated per round.
 
-    Every arm gets ``warmup`` untimed calls; then ``rounds`` rounds, each timing
-    ``repeats`` back-to-back calls per arm with GPU events, in forward order on
-    even rounds and reversed order on odd rounds to cancel ordering bias.
-    ``stable`` flags a (max - min) / median spread of at most 10%.
+    Each arm gets ``warmup`` untimed calls; then each round times ``repeats``
+    back-to-back calls per arm between two events recorded on the current
+    stream.  ``stable`` flags a (max - min) / median spread of at most 10%.
     """
     if warmup < 1 or repeats < 1 or rounds < 3:
         raise ValueError("positive warmup/repeats and at least three rounds required")
@@ -60,22 +102,16 @@ def paired_cuda_timing(functions: dict, *, warmup: int = 20, repeats: int = 100,
         for _ in range(warmup):
             fn()
     torch.cuda.synchronize()
-    names = list(functions)
-    samples = {name: [] for name in names}
-    for index in range(rounds):
-        for name in (names if index % 2 == 0 else names[::-1]):
-            start = torch.cuda.Event(enable_timing=True)
-            end = torch.cuda.Event(enable_timing=True)
-            start.record()
+    samples: dict[str, list[float]] = {name: [] for name in functions}
+    for order in _round_schedule(list(functions), rounds):
+        for name in order:
+            fn = functions[name]
+            begin = torch.cuda.Event(enable_timing=True)
+            finish = torch.cuda.Event(enable_timing=True)
+            begin.record()
             for _ in range(repeats):
-                functions[name]()
-            end.record()
-            end.synchronize()
-            samples[name].append(start.elapsed_time(end) * 1000 / repeats)
-    result = {}
-    for name, values in samples.items():
-        median = statistics.median(values)
-        spread = (max(values) - min(values)) / median if median > 0 else float("inf")
-        result[name] = {"microseconds_per_call": values, "median_us": median, "relative_range": spread,
-                        "stable": spread <= 0.10}
-    return result
+                fn()
+            finish.record()
+            finish.synchronize()
+            samples[name].append(begin.elapsed_time(finish) * 1e3 / repeats)
+    return {name: _summary(values) for name, values in samples.items()}

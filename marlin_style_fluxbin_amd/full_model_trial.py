@@ -1,23 +1,94 @@
 """Dynamic-KV decode trace and trace comparison for HF Qwen3 models with packed Linears.
 
-Reference: ``full_model_trial.py`` (``packed_modules`` :10-12, ``decode_trace``
-:15-78, ``compare_trace`` :81-93, ``validate_routes`` :96-99).  The trace is the
-oracle side of a decode comparison: prefill through the dense fallback, then
-``steps`` single-token calls on one growing dynamic cache with the packed route
-enforced.
+Contract of the reference's ``full_model_trial.py`` (``packed_modules`` :10-12,
+``decode_trace`` :15-78, ``compare_trace`` :81-93, ``validate_routes`` :96-99):
+the same arguments, result keys, route expectations and error messages.  The
+trace is the oracle side of a decode comparison: the prompt runs once through
+the dense fallback, then exactly ``steps`` one-token calls on one growing dynamic
+cache must take the packed route (the fallback is switched to ``error`` for
+them).
+
+Organisation here: a ``_StageClock`` pairs a wall clock with GPU events for one
+timed stage, ``_fallback_policy`` owns the temporary fallback switch and its
+restoration, and ``_next_token`` is the one greedy step both stages share.
 """
 from __future__ import annotations
 
 import time
+from contextlib import contextmanager
 
 import torch
 
 from .acceleration_checks import numerical_gate, stepwise_nrmse
+from .deployment import PackedHybridLinear
 from .w3_lut_deployment import PackedW3Linear
+
+PACKED_TYPES = (PackedHybridLinear, PackedW3Linear)
 
 
 def packed_modules(model) -> dict:
-    return {name: m for name, m in model.named_modules() if isinstance(m, PackedW3Linear)}
+    """Every packed Linear of ``model`` (W3 and hybrid two-base), by module name."""
+    return {name: module for name, module in model.named_modules() if isinstance(module, PACKED_TYPES)}
+
+
+class _StageClock:
+    """Wall time of a stage plus, on GPU, its device time between two events."""
+
+    def __init__(self, device: torch.device):
+        self.device = device
+        self.gpu = device.type == "cuda"
+        self.wall_ms = 0.0
+        self._events = None
+
+    def __enter__(self):
+        if self.gpu:
+            torch.cuda.synchronize(self.device)
+            self._events = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+        self._t0 = time.perf_counter()
+        if self.gpu:
+            self._events[0].record()
+        return self
+
+    def __exit__(self, *exc):
+        if self.gpu:
+            self._events[1].record()
+            torch.cuda.synchronize(self.device)
+        self.wall_ms = (time.perf_counter() - self._t0) * 1e3
+        return False
+
+    @property
+    def device_ms(self):
+        return self._events[0].elapsed_time(self._events[1]) if self._events else None
+
+
+@contextmanager
+def _fallback_policy(modules: dict):
+    """Reset route counters; yield a setter for every module's fallback; restore
+    the original fallbacks on exit, whatever happened."""
+    original = {name: module.fallback for name, module in modules.items()}
+    for module in modules.values():
+        module.route_counts = {"packed_m1": 0, "dense_fallback": 0}
+
+    def set_all(policy: str) -> None:
+        for module in modules.values():
+            module.fallback = policy
+    try:
+        yield set_all
+    finally:
+        for name, module in modules.items():
+            module.fallback = original[name]
+
+
+def _next_token(model, input_ids, cache):
+    """One forward with the cache; (last logits, greedy token, cache)."""
+    output = model(input_ids=input_ids, past_key_values=cache, use_cache=True, logits_to_keep=1)
+    logits = output.logits[:, -1, :].detach()
+    return logits, logits.argmax(-1, keepdim=True), output.past_key_values
+
+
+def _cache_length(cache) -> int:
+    length = cache.get_seq_length()
+    return int(length.item()) if isinstance(length, torch.Tensor) else int(length)
 
 
 @torch.inference_mode()
@@ -33,102 +104,69 @@ def decode_trace(model, input_ids: torch.Tensor, *, steps: int, forced_tokens: t
         raise ValueError("batch1, prompt length>=2 and positive decode steps required")
     if forced_tokens is not None and tuple(forced_tokens.shape) != (1, steps):
         raise ValueError("forced continuation shape must be [1,steps]")
-    forced = None if forced_tokens is None else forced_tokens.to(input_ids.device)
+    device = input_ids.device
+    feed = None if forced_tokens is None else forced_tokens.to(device)
     modules = packed_modules(model)
-    saved = {n: m.fallback for n, m in modules.items()}
-    for m in modules.values():
-        m.route_counts = {"packed_m1": 0, "dense_fallback": 0}
-        m.fallback = "dense"
-    cuda = input_ids.is_cuda
-
-    def sync():
-        if cuda:
-            torch.cuda.synchronize(input_ids.device)
-
-    def event():
-        return torch.cuda.Event(enable_timing=True) if cuda else None
-
-    logits, predictions, fed, step_events = [], [], [], []
-    try:
-        sync()
-        wall = time.perf_counter()
-        pre_start, pre_end = event(), event()
-        if cuda:
-            pre_start.record()
-        output = model(input_ids=input_ids, use_cache=True, logits_to_keep=1)
-        cache = output.past_key_values
-        logits.append(output.logits[:, -1, :].detach())
-        current = logits[-1].argmax(-1, keepdim=True)
-        predictions.append(current)
-        if cuda:
-            pre_end.record()
-        sync()
-        prefill_wall = (time.perf_counter() - wall) * 1000
-        for m in modules.values():
-            m.fallback = "error"  # decode steps must take the packed route
-        dec_start, dec_end = event(), event()
-        wall = time.perf_counter()
-        if cuda:
-            dec_start.record()
-        for i in range(steps):
-            token = current if forced is None else forced[:, i:i + 1]
-            fed.append(token)
-            begin, end = event(), event()
-            if cuda:
-                begin.record()
-            output = model(input_ids=token, past_key_values=cache, use_cache=True, logits_to_keep=1)
-            cache = output.past_key_values
-            logits.append(output.logits[:, -1, :].detach())
-            current = logits[-1].argmax(-1, keepdim=True)
-            predictions.append(current)
-            if cuda:
-                end.record()
-                step_events.append((begin, end))
-        if cuda:
-            dec_end.record()
-        sync()
-        decode_wall = (time.perf_counter() - wall) * 1000
-        length = cache.get_seq_length()
-        length = int(length.item()) if isinstance(length, torch.Tensor) else int(length)
+    gpu = device.type == "cuda"
+    with _fallback_policy(modules) as set_fallback:
+        set_fallback("dense")
+        with _StageClock(device) as prefill:
+            logits, token, cache = _next_token(model, input_ids, None)
+        all_logits, predictions, fed, step_events = [logits], [token], [], []
+        set_fallback("error")  # every decode step must take the packed route
+        with _StageClock(device) as decode:
+            for i in range(steps):
+                token = token if feed is None else feed[:, i:i + 1]
+                fed.append(token)
+                events = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) if gpu else None
+                if events:
+                    events[0].record()
+                logits, token, cache = _next_token(model, token, cache)
+                if events:
+                    events[1].record()
+                    step_events.append(events)
+                all_logits.append(logits)
+                predictions.append(token)
+        length = _cache_length(cache)
         if length != input_ids.shape[1] + steps:
             raise RuntimeError("KV cache length drift")
         return {
-            "logits": torch.stack(logits, dim=1).cpu(),
+            "logits": torch.stack(all_logits, dim=1).cpu(),
             "predictions": torch.cat(predictions, dim=1).cpu(),
             "fed_tokens": torch.cat(fed, dim=1).cpu(),
             "cache_length": length,
-            "prefill_wall_ms": prefill_wall,
-            "decode_wall_ms": decode_wall,
-            "prefill_device_ms": pre_start.elapsed_time(pre_end) if cuda else None,
-            "decode_device_ms": dec_start.elapsed_time(dec_end) if cuda else None,
-            "step_device_ms": [a.elapsed_time(b) for a, b in step_events],
-            "routes": {n: dict(m.route_counts) for n, m in modules.items()},
+            "prefill_wall_ms": prefill.wall_ms,
+            "decode_wall_ms": decode.wall_ms,
+            "prefill_device_ms": prefill.device_ms,
+            "decode_device_ms": decode.device_ms,
+            "step_device_ms": [begin.elapsed_time(end) for begin, end in step_events],
+            "routes": {name: dict(module.route_counts) for name, module in modules.items()},
         }
-    finally:
-        for n, m in modules.items():
-            m.fallback = saved[n]
 
 
 def compare_trace(candidate: dict, reference: dict, *, logprob_tolerance: float) -> dict:
     """Pass iff the logits gate passes, greedy tokens and fed contexts are equal,
-    and the max |log-softmax difference| is within ``logprob_tolerance``."""
+    and the max |log-softmax difference| is finite and within ``logprob_tolerance``."""
     if logprob_tolerance < 0:
         raise ValueError("negative logprob tolerance")
-    gate = numerical_gate(candidate["logits"], reference["logits"])
-    if candidate["logits"].shape != reference["logits"].shape:
+    cand, ref = candidate["logits"], reference["logits"]
+    gate = numerical_gate(cand, ref)
+    if cand.shape != ref.shape:
         return {"passed": False, "reason": "shape drift"}
-    tokens_equal = torch.equal(candidate["predictions"], reference["predictions"])
-    contexts_equal = torch.equal(candidate["fed_tokens"], reference["fed_tokens"])
-    delta = (candidate["logits"].float().log_softmax(-1) - reference["logits"].float().log_softmax(-1)).abs()
-    maximum = float(delta.max())
-    finite = bool(torch.isfinite(delta).all())
-    return {"passed": gate["passed"] and tokens_equal and contexts_equal and finite and maximum <= logprob_tolerance,
-            "logits": gate, "greedy_tokens_equal": tokens_equal, "fed_tokens_equal": contexts_equal,
-            "max_abs_logprob_error": maximum, "logprob_tolerance": logprob_tolerance,
-            "stepwise_normalized_rmse": stepwise_nrmse(candidate["logits"], reference["logits"])}
+    checks = {
+        "greedy_tokens_equal": torch.equal(candidate["predictions"], reference["predictions"]),
+        "fed_tokens_equal": torch.equal(candidate["fed_tokens"], reference["fed_tokens"]),
+    }
+    gap = (torch.log_softmax(cand.float(), dim=-1) - torch.log_softmax(ref.float(), dim=-1)).abs()
+    worst = float(gap.max())
+    passed = (gate["passed"] and all(checks.values()) and bool(torch.isfinite(gap).all())
+              and worst <= logprob_tolerance)
+    return {"passed": passed, "logits": gate, **checks, "max_abs_logprob_error": worst,
+            "logprob_tolerance": logprob_tolerance, "stepwise_normalized_rmse": stepwise_nrmse(cand, ref)}
 
 
 def validate_routes(trace: dict, *, expected_linears: int, steps: int) -> bool:
-    """Every packed Linear served the prefill densely once and each decode step packed."""
-    return len(trace["routes"]) == expected_linears and all(
-        r == {"dense_fallback": 1, "packed_m1": steps} for r in trace["routes"].values())
+    """Every packed Linear served the prompt densely once and each decode step packed."""
+    want = {"dense_fallback": 1, "packed_m1": steps}
+    routes = trace["routes"]
+    return len(routes) == expected_linears and all(route == want for route in routes.values())

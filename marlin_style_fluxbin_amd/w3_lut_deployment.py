@@ -21,9 +21,9 @@ from functools import lru_cache
 
 import torch
 from torch import nn
-from torch.nn import functional as F
 
 from . import _lib
+from .packed_linear import PackedLinearBase, replace_linears_atomically
 from .gptq_deployment import FIELDS, OPTIONAL_FIELDS, restore_planar_w3, validate_planar_w3
 
 ROW_TILES = (256, 512, 1024)
@@ -304,18 +304,16 @@ class _TableRoute:
         return out
 
 
-class PackedW3Linear(nn.Module):
+class PackedW3Linear(PackedLinearBase):
     """Decode-oriented W3 Linear with an explicit dense fallback.
 
-    Reference: ``w3_lut_deployment.py:190-359``.  One-row GPU fp16/bf16 inputs
-    take the packed route and count under ``packed_m1``; anything else raises
-    unless ``fallback='dense'``, which dequantizes (HIP kernel on GPU) and calls
-    ``F.linear`` (``dense_fallback``), as in the reference.  The packed route is
-    the MFMA kernel for ``structural`` arithmetic with one group per split (one
-    launch), and the reference's table contract (``w3_lut_m1_out``: ``row_tile``,
-    ``groups_per_split``, split partials summed in order) otherwise, which is
-    how ``decoded_bf16`` routes such as ``fast_corrected`` and ``observed_exact``
-    run.
+    Reference: ``w3_lut_deployment.py:190-359``; the route / fallback / binding
+    protocol is ``packed_linear.PackedLinearBase``.  The packed route is the MFMA
+    kernel for ``structural`` arithmetic with one group per split (one launch),
+    and the reference's table contract (``w3_lut_m1_out``: ``row_tile``,
+    ``groups_per_split``, split partials summed in order) otherwise, which is how
+    ``decoded_bf16`` routes such as ``fast_corrected`` and ``observed_exact`` run.
+    The dense fallback dequantizes with the HIP restore kernel on GPU.
 
     ``max_packed_rows`` (not in the reference; default 1) lets 2..8-row inputs
     take the MFMA kernel too; they are then counted under ``packed_small_m``.
@@ -325,14 +323,11 @@ class PackedW3Linear(nn.Module):
                  row_tile: int | None = None, groups_per_split: int = 1, arithmetic: str = "structural",
                  route: str = "structural", max_packed_rows: int = 1):
         super().__init__()
-        if fallback not in {"error", "dense"}:
-            raise ValueError("fallback must be error or dense")
         self.out_features, self.in_features = validate_planar_w3(layout)
         self.row_tile = qwen3_row_tile(self.out_features, self.in_features) if row_tile is None else row_tile
         if self.row_tile not in ROW_TILES:
             raise ValueError(f"row_tile must be one of {ROW_TILES}")
-        if arithmetic not in ARITHMETIC_MODES:
-            raise ValueError(f"arithmetic must be one of {ARITHMETIC_MODES}")
+        _arith_code(arithmetic)
         if arithmetic == "decoded_bf16":
             if layout["scales"].dtype != torch.bfloat16:
                 raise ValueError("decoded_bf16 arithmetic requires bf16 scales")
@@ -342,25 +337,18 @@ class PackedW3Linear(nn.Module):
         if not isinstance(max_packed_rows, int) or not 1 <= max_packed_rows <= MAX_PACKED_ROWS:
             raise ValueError(f"max_packed_rows must be an integer in [1,{MAX_PACKED_ROWS}]")
         workspace_shape(self.out_features, self.in_features, groups_per_split)
+        self.max_packed_rows = max_packed_rows
+        self._init_protocol(fallback=fallback, bias=bias)
         self.groups_per_split = groups_per_split
         self.arithmetic = arithmetic
         self.route = route
-        self.fallback = fallback
-        self.max_packed_rows = max_packed_rows
-        self.route_counts = {"packed_m1": 0, "dense_fallback": 0}
-        if max_packed_rows > 1:
-            self.route_counts["packed_small_m"] = 0
-        self.last_route = "not_called"
-        self._decode_binding = None
-        self._decode_audit = False
-        self._packed = None
+        self._table = None
+        self._gemv = None
         perm = layout["perm"]
         self._perm_identity = bool(torch.equal(perm.long().cpu(), torch.arange(self.in_features)))
         self._fields = FIELDS + tuple(f for f in OPTIONAL_FIELDS if f in layout)
         for name in self._fields:
             self.register_buffer(name, layout[name].detach().clone())
-        self.register_buffer("bias", None if bias is None else bias.detach().clone())
-        self.register_buffer("_decode_output", None, persistent=False)
 
     @property
     def uses_table_route(self) -> bool:
@@ -371,122 +359,61 @@ class PackedW3Linear(nn.Module):
     def layout(self) -> dict:
         return {name: getattr(self, name) for name in self._fields}
 
-    def clear_prepared_decode(self) -> None:
-        self._decode_binding = None
-        self._decode_output = None
-        self._decode_audit = False
+    def _payload_device(self) -> torch.device:
+        return self.planes.device
 
-    def _apply(self, fn, recurse=True):
-        self.clear_prepared_decode()
-        self._packed = None
-        return super()._apply(fn, recurse=recurse)
+    def _dense_weight(self, dtype: torch.dtype) -> torch.Tensor:
+        return restore_planar_w3(self.layout(), dtype=dtype)
 
-    def _route_for(self, rows: int, device: torch.device):
-        """The bound packed-route callable ``(x [rows, K], out [rows, O])``."""
+    def _check_before_bind(self, device: torch.device) -> None:
+        validate_planar_w3(self.layout(), check_values=False)
+
+    def _forget_kernels(self) -> None:
+        self._table = None
+        self._gemv = None
+
+    def _packed_kernel(self, rows: int, device: torch.device):
         if rows == 1 and self.uses_table_route:
-            if not isinstance(self._packed, _TableRoute) or self._packed.workspace.device != device:
-                self._packed = _TableRoute(self, device)
-            return self._packed
-        if not isinstance(self._packed, W3Gemv) or self._packed.layout["planes"].data_ptr() != self.planes.data_ptr():
-            self._packed = W3Gemv(self.layout(), arithmetic=self.arithmetic, perm_identity=self._perm_identity,
-                                  max_rows=self.max_packed_rows)
-        return self._packed
-
-    def bind_prepared_decode(self, dtype: torch.dtype) -> None:
-        if self._decode_binding is not None:
-            raise ValueError("decode already bound")
-        if dtype not in (torch.float16, torch.bfloat16):
-            raise ValueError("FP16/BF16 required")
-        layout = self.layout()
-        device = layout["planes"].device
-        if device.type != "cuda":
-            raise ValueError("prepared decode requires CUDA (a ROCm GPU)")
-        validate_planar_w3(layout, check_values=False)
-        kernel = self._route_for(1, device)
-        self._decode_output = torch.empty((1, self.out_features), device=device, dtype=dtype)
-        output = self._decode_output
-        shaped = output.view(1, 1, self.out_features)
-        expected = (1, 1, self.in_features)
-        bias = self.bias
-
-        def apply(x: torch.Tensor) -> torch.Tensor:
-            if torch.is_grad_enabled():
-                raise RuntimeError("prepared decode is inference only")
-            if tuple(x.shape) != expected or x.dtype != dtype or x.device != device or not x.is_contiguous():
-                raise ValueError("prepared decode input shape/dtype/device/stride mismatch")
-            if self._decode_audit:
-                self.route_counts["packed_m1"] += 1
-                self.last_route = "packed_m1"
-            kernel(x.view(1, self.in_features), output)
-            if bias is not None:
-                output.add_(bias)
-            return shaped
-
-        self._decode_binding = apply
-
-    def forward(self, x: torch.Tensor) -> torch.Tensor:
-        if self._decode_binding is not None:
-            return self._decode_binding(x)
-        if torch.is_grad_enabled():
-            raise RuntimeError("packed inference requires no_grad/inference_mode")
-        if x.ndim < 2 or x.shape[-1] != self.in_features:
-            raise ValueError("expected [...,K] input")
-        m = x.numel() // self.in_features
-        if not (1 <= m <= self.max_packed_rows) or not x.is_cuda or x.dtype not in (torch.float16, torch.bfloat16):
-            if self.fallback != "dense":
-                raise ValueError("unsupported input; enable explicit dense fallback if needed")
-            self.last_route = "dense_fallback"
-            self.route_counts["dense_fallback"] += 1
-            return F.linear(x, restore_planar_w3(self.layout(), dtype=x.dtype), self.bias)
-        route = "packed_m1" if m == 1 else "packed_small_m"
-        self.last_route = route
-        self.route_counts[route] += 1
-        flat = x.reshape(m, self.in_features).contiguous()
-        output = torch.empty((m, self.out_features), device=x.device, dtype=x.dtype)
-        self._route_for(m, x.device)(flat, output)
-        if self.bias is not None:
-            output.add_(self.bias)
-        return output.reshape(*x.shape[:-1], self.out_features)
+            if self._table is None or self._table.workspace.device != device:
+                self._table = _TableRoute(self, device)
+            return self._table
+        if self._gemv is None or self._gemv.layout["planes"].data_ptr() != self.planes.data_ptr():
+            self._gemv = W3Gemv(self.layout(), arithmetic=self.arithmetic, perm_identity=self._perm_identity,
+                                max_rows=self.max_packed_rows)
+        return self._gemv
 
 
 def replace_w3_block_linears(block, layer_payload, *, fallback: str = "error",
                              row_tile_by_shape: dict | None = None, route: str = "structural") -> list[str]:
-    """Replace exactly the seven Qwen3 Linears of a block after validating all of them."""
+    """Replace exactly the seven Qwen3 Linears of a block (reference
+    ``w3_lut_deployment.py:362-417``); every payload is validated and every module
+    built before the block is touched."""
     from .qwen3 import QWEN3_LINEAR_MODULES
 
-    names_with_zeros = {name for name in QWEN3_LINEAR_MODULES if f"{name}.zeros" in layer_payload}
-    expected = {f"{module}.{field}" for module in QWEN3_LINEAR_MODULES for field in FIELDS}
-    expected |= {f"{module}.zeros" for module in names_with_zeros}
-    if set(layer_payload) != expected:
+    zero_names = {name for name in QWEN3_LINEAR_MODULES if f"{name}.zeros" in layer_payload}
+    wanted = {f"{name}.{field}" for name in QWEN3_LINEAR_MODULES for field in FIELDS}
+    wanted |= {f"{name}.zeros" for name in zero_names}
+    if set(layer_payload) != wanted:
         raise ValueError("layer must contain exactly seven complete W3 payloads")
     if route not in QWEN3_W3_ROUTE_POLICIES:
         raise ValueError(f"unknown Qwen3-8B W3 route: {route}")
-    row_policy = QWEN3_ROW_TILE_BY_SHAPE if row_tile_by_shape is None else row_tile_by_shape
-    replacements = []
-    for name in QWEN3_LINEAR_MODULES:
-        old = block.get_submodule(name)
-        fields = FIELDS + (("zeros",) if name in names_with_zeros else ())
-        layout = {field: layer_payload[f"{name}.{field}"] for field in fields}
-        out_features, in_features = validate_planar_w3(layout)
-        if not isinstance(old, nn.Linear) or (old.out_features, old.in_features) != (out_features, in_features):
+    tiles = QWEN3_ROW_TILE_BY_SHAPE if row_tile_by_shape is None else row_tile_by_shape
+
+    def build(name: str) -> PackedW3Linear:
+        linear = block.get_submodule(name)
+        names = FIELDS + (("zeros",) if name in zero_names else ())
+        layout = {field: layer_payload[f"{name}.{field}"] for field in names}
+        shape = validate_planar_w3(layout)
+        if not isinstance(linear, nn.Linear) or (linear.out_features, linear.in_features) != shape:
             raise ValueError(f"Linear shape/type mismatch: {name}")
-        try:
-            row_tile = row_policy[(out_features, in_features)]
-        except KeyError as exc:
-            raise ValueError(f"row-tile policy missing shape: {(out_features, in_features)}") from exc
+        if shape not in tiles:
+            raise ValueError(f"row-tile policy missing shape: {shape}")
+        policy = {"row_tile": tiles[shape], "groups_per_split": 1, "arithmetic": "structural"}
         if row_tile_by_shape is None:
-            route_policy = qwen3_w3_route(route, out_features, in_features)
-            if route_policy["row_tile"] != row_tile:
+            policy = qwen3_w3_route(route, *shape)
+            if policy["row_tile"] != tiles[shape]:
                 raise ValueError("route and row-tile policies disagree")
-        else:
-            route_policy = {"groups_per_split": 1, "arithmetic": "structural"}
-        replacement = PackedW3Linear(
-            layout, bias=old.bias, fallback=fallback, row_tile=row_tile,
-            groups_per_split=route_policy["groups_per_split"], arithmetic=route_policy["arithmetic"],
-            route=route,
-        ).to(old.weight.device)
-        replacements.append((name, replacement))
-    for name, replacement in replacements:
-        parent_name, attribute = name.rsplit(".", 1)
-        setattr(block.get_submodule(parent_name), attribute, replacement)
-    return [name for name, _ in replacements]
+        return PackedW3Linear(layout, bias=linear.bias, fallback=fallback, route=route,
+                              **policy).to(linear.weight.device)
+
+    return replace_linears_atomically(block, [(name, build(name)) for name in QWEN3_LINEAR_MODULES])

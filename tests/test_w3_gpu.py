@@ -261,3 +261,19 @@ def test_module_small_m_opt_in(gpu):
     W3Gemv(dl)(x, want)
     assert torch.equal(packed.view(torch.int16), want.view(torch.int16))
     assert_rel(dense.float().cpu().numpy(), w3.matvec_decoded(x.float().cpu().numpy(), ol, "bf16"), 1e-2)
+
+
+def test_engine_w3_backend_apply_out(gpu):
+    from marlin_style_fluxbin_amd.engine_interface import W3Backend
+
+    layout, dl, ol = _setup(4096, 4096, seed=8, zeros=True, scale_dtype=torch.float16, permute=True)
+    backend = W3Backend(allow_zeros=True, scale_dtype=torch.float16)
+    workspace = torch.empty(backend.workspace_shape(4096, 4096), dtype=torch.uint8, device=gpu)
+    for m in (1, 3):
+        x = _x(m, 4096, torch.bfloat16, seed=m).to(gpu)
+        out = torch.empty(m, 4096, dtype=torch.bfloat16, device=gpu)
+        backend.apply_out(x, dl, out, workspace)
+        want = torch.empty_like(out)
+        W3Gemv(dl)(x, want)
+        assert torch.equal(out.view(torch.int16), want.view(torch.int16))
+    assert_half_ulp(out.float().cpu().numpy(), w3.matvec_exact(x.float().cpu().numpy(), ol), "bf16")

@@ -183,3 +183,25 @@ def test_extension_loader_contract(monkeypatch):
             wl.load_w3_lut_extension(256)
     finally:
         wl.load_w3_lut_extension.cache_clear()
+
+
+def test_engine_backends_for_w3_and_hybrid_formats():
+    from marlin_style_fluxbin_amd import deployment as d
+    from marlin_style_fluxbin_amd.engine_interface import M1Backend, W3Backend, backend_for_format
+
+    raw, codes, _ = synthetic_raw()
+    backend = backend_for_format(gd.REFERENCE_FORMAT)
+    assert isinstance(backend, W3Backend) and backend.contract.target_arch == "gfx950"
+    layout = backend.convert(raw)
+    assert torch.equal(gd.decode_planar_w3_codes(layout), codes)
+    assert gd.layout_storage(layout)["format"] == backend.contract.format
+    zero3, _, _ = synthetic_raw(zero=3)
+    with_zeros = W3Backend(allow_zeros=True, scale_dtype=torch.float16)
+    converted = with_zeros.convert(zero3)
+    assert converted["scales"].dtype == torch.float16 and "zeros" in converted
+    assert gd.layout_storage(converted)["format"] == with_zeros.contract.format == gd.FORMAT
+    assert isinstance(backend_for_format(d.PLANAR_FORMAT), M1Backend)
+    assert backend_for_format(d.PLANAR_FORMAT).kernel == "v5_p1024"
+    assert backend_for_format(d.FORMAT).kernel == "v1"
+    with pytest.raises(ValueError):
+        backend_for_format("unknown-format")
