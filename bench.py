@@ -129,6 +129,24 @@ def bench_shape(o, k, device, steps, warmup, stream, min_bytes=320e6, min_copies
     w3_us = ms * 1000 / copies
     del graph
 
+    # config 1's small-M variants: M activation rows against the same payloads
+    small_m = {}
+    for m in (2, 4, 8):
+        xm = torch.randn(m, k, device=device, generator=gen).to(torch.bfloat16)
+        om = torch.empty(m, o, device=device, dtype=torch.bfloat16)
+
+        def w3_m(xm=xm, om=om):
+            for gemv in gemvs:
+                gemv(xm, om)
+
+        mgraph = capture(w3_m, stream)
+        m_us = time_graph(mgraph, steps, warmup, stream) * 1000 / copies
+        del mgraph
+        m_bytes = algorithmic_bytes(o, k, m)
+        small_m[f"M={m}"] = {"us": round(m_us, 3), "GBps": round(m_bytes / m_us / 1e3, 1),
+                             "frac_hbm": round(m_bytes / m_us / 1e3 / HBM_PEAK_GBPS, 4),
+                             "algorithmic_bytes": m_bytes}
+
     # the same payloads repacked once into the field layout (fx_w3_planes_to_fields)
     # and read by fx_w3_gemv_fields: the decode graph's weight format
     from marlin_style_fluxbin_amd import _lib
@@ -183,6 +201,7 @@ def bench_shape(o, k, device, steps, warmup, stream, min_bytes=320e6, min_copies
         "w3_speedup_vs_bf16": round(bf16_us / w3_us, 3),
         "fields_us": round(fields_us, 3), "fields_GBps": round(nbytes / fields_us / 1e3, 1),
         "fields_frac_hbm": round(nbytes / fields_us / 1e3 / HBM_PEAK_GBPS, 4),
+        "small_m": small_m,
     }
 
 
@@ -252,40 +271,78 @@ def two_base_bench(device, steps, warmup, stream, o=12288, k=4096, salient=32, m
     }
 
 
-def cpu_baseline(seconds_budget=15.0):
-    """Oracle restatement of the reference's dense CPU route (dequantize per call,
-    then matmul) on config 0's q_proj shape; one thread."""
-    import numpy as np
-    from threadpoolctl import threadpool_limits
+def _cpu_model_name() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
-    from oracle import w3
-    from oracle.bf16 import round_bf16
 
-    rng = np.random.default_rng(0)
-    o, k = 4096, 4096
-    g = k // 128
-    layout = {
-        "planes": rng.integers(0, 256, (g, 3, o, 16), dtype=np.uint8),
-        "scales": np.float16(rng.uniform(0.005, 0.02, (g, o))).astype(np.float32),
-        "scale_dtype": "f16", "perm": np.arange(k, dtype=np.int16),
-        "zeros": rng.integers(3, 5, (g, o), dtype=np.uint8),
+def cpu_baseline(warmup=3, repeats=10):
+    """The reference's CPU route on config 0 (q_proj 4096 x 4096, M = 1, fp16 scales,
+    zero-points U{3,4}), timed on this host's cores.
+
+    The reference runs ``PackedW3Linear(fallback='dense')`` on CPU tensors as
+    ``F.linear(x, restore_planar_w3(layout, x.dtype))`` (w3_lut_deployment.py:327-333,
+    gptq_deployment.py:247-260): the weight is dequantized on every call.  Its
+    restatement here is the product's CPU torch code for those two functions.
+    Arms: (1) dequantize + F.linear in bf16 per call (the reference's route, the
+    reported value); (2) ``structural_w3_matvec`` (the grouped fp32 form,
+    gptq_deployment.py:263-277); (3) F.linear on a weight dequantized once.  Each
+    arm at the host thread budget (``min(os.cpu_count(), OMP_NUM_THREADS)``) and at
+    one thread; ``warmup`` untimed calls, then the median of ``repeats``."""
+    import os
+    import statistics
+
+    import torch
+    import torch.nn.functional as F
+
+    from marlin_style_fluxbin_amd.gptq_deployment import planar_from_codes, restore_planar_w3, structural_w3_matvec
+
+    o = k = 4096
+    g = torch.Generator().manual_seed(0)
+    codes = torch.randint(0, 8, (k, o), generator=g, dtype=torch.uint8)
+    layout = {"planes": planar_from_codes(codes),
+              "scales": (torch.rand((k // 128, o), generator=g) * 0.015 + 0.005).to(torch.float16),
+              "perm": torch.arange(k, dtype=torch.int16),
+              "zeros": torch.randint(3, 5, (k // 128, o), generator=g, dtype=torch.uint8)}
+    x = torch.randn(1, k, generator=torch.Generator().manual_seed(0)).to(torch.bfloat16)
+    dense = restore_planar_w3(layout, dtype=torch.bfloat16)
+    arms = {
+        "dequantize_per_call_linear_bf16": lambda: F.linear(x, restore_planar_w3(layout, dtype=torch.bfloat16)),
+        "structural_fp32": lambda: structural_w3_matvec(x, layout),
+        "linear_bf16_predequantized": lambda: F.linear(x, dense),
     }
-    x = round_bf16(rng.standard_normal((1, k)).astype(np.float32))
-    calls = 0
-    with threadpool_limits(limits=1):
-        start = time.perf_counter()
-        while True:
-            weight = w3.restore_weight(layout, "bf16")
-            _ = x @ weight.T
-            calls += 1
-            elapsed = time.perf_counter() - start
-            if elapsed >= seconds_budget or calls >= 50:
-                break
-    per_call = elapsed / calls
-    nbytes = algorithmic_bytes(o, k)
-    return {"value": round(nbytes / per_call / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"config 0 q_proj 4096x4096 M=1: {calls} calls of oracle restore_weight(bf16) + "
-                      f"x@W.T, {per_call*1e3:.1f} ms/call, numpy single thread"}
+    budget = min(os.cpu_count() or 1, int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1)))
+    previous = torch.get_num_threads()
+    results = {}
+    try:
+        for threads in sorted({budget, 1}, reverse=True):
+            torch.set_num_threads(threads)
+            for name, fn in arms.items():
+                for _ in range(warmup):
+                    fn()
+                samples = []
+                for _ in range(repeats):
+                    t = time.perf_counter()
+                    fn()
+                    samples.append(time.perf_counter() - t)
+                ms = statistics.median(samples) * 1e3
+                results[f"{name}@{threads}t"] = {"median_ms": round(ms, 3),
+                                                  "GBps": round(algorithmic_bytes(o, k) / (ms / 1e3) / 1e9, 4)}
+    finally:
+        torch.set_num_threads(previous)
+    head = results[f"dequantize_per_call_linear_bf16@{budget}t"]
+    return {"value": head["GBps"], "unit": "GB/s", "cores": budget, "kind": "port",
+            "sample": f"config 0 q_proj 4096x4096 M=1: the reference's CPU route (restore_planar_w3 + F.linear "
+                      f"bf16 per call, product CPU torch code), median of {repeats} after {warmup} warm-ups, "
+                      f"{head['median_ms']} ms/call at {budget} threads",
+            "host": {"os_cpu_count": os.cpu_count(), "threads_used": budget, "model_name": _cpu_model_name(),
+                     "torch_threads_default": previous},
+            "arms": results}
 
 
 def decode_bench(layers=36, prefix=512, steps=32, replays=5, seed=0):

@@ -199,7 +199,7 @@ struct MfmaPlan {
   int gps, splits, row_blocks;
 };
 
-int mfma_chunk_for(int m) { return m >= 4 ? 4 : m >= 2 ? 2 : 1; }
+int mfma_chunk_for(int m) { return m >= 8 ? 8 : m >= 4 ? 4 : m >= 2 ? 2 : 1; }
 
 MfmaPlan make_mfma_plan(int O, int G, int nw, int pd, int gps, int tiles) {
   MfmaPlan p;

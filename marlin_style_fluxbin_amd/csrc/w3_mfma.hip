@@ -24,7 +24,9 @@
 //   subnormal codes (q * 2^-24) the same way.
 // * Columns: one MFMA chain covers 4 groups at once; k-block b of the
 //   instruction carries group 4i+b and column c = b + 4m only sees k-block b,
-//   so D[row][b + 4m] is the group's dot product for activation row m.
+//   so D[row][b + 4m] is the group's dot product for activation row m.  Eight
+//   activation rows run two such chains on the same dequantized A operands
+//   (rows 4h .. 4h+3 in chain h), so the weights are read once for all eight.
 // y[m,o] = sum_g s[g,o] * (D * 2^(133-E) - z[g,o] * sum_{k in g} x[m,k]).
 //
 // Each wave builds the B operands of its own batch from x: the 16 lanes of
@@ -52,7 +54,7 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
-constexpr int kMfmaMaxRows = 4;  // activation rows per launch (columns b + 4m)
+constexpr int kMfmaMaxRows = 8;  // activation rows per launch (columns b + 4m of NH = ceil(MB / 4) halves)
 
 // The A operand's bit pattern q (or 16q) is a subnormal of the operand type:
 // q * 2^-133 in bf16, q * 2^-24 in fp16.
@@ -156,14 +158,15 @@ struct BatchLoads {
 // as the separate projections whatever waves each plan picks).
 constexpr int kSumLanes = 8;
 
-// Workgroup LDS: per wave, B operands [k-block][step][row] (16 B each), zero
-// operands [step][row] read by the lanes whose column belongs to another
-// k-block, sum of x and subnormal exponent - E per (k-block group, row), and the
-// per-wave partial outputs.
+// Workgroup LDS: per wave, B operands [k-block][step][row] (16 B each); zero
+// operands [step][row] read by the lanes whose column belongs to another k-block
+// (one array for the workgroup: every wave writes all of it, with zeros only,
+// before its own first read, so no barrier orders the waves); sum of x and
+// subnormal exponent - E per (k-block group, row); the per-wave partial outputs.
 template <int NW, int MB, int RT>
 struct MfmaShared {
   u32x4_t bstage[NW][64 * MB];
-  u32x4_t bzero[NW][16 * MB];
+  u32x4_t bzero[16 * MB];
   float gsum[NW][4 * MB];
   int gexp[NW][4 * MB];
   float red[kSumLanes][16 * RT * MB];
@@ -220,13 +223,21 @@ __device__ __forceinline__ void w3_mfma_body(
   const int kb = lane >> 4;   // A role: k-block = group slot; D role: row block
   const int c = lane & 15;    // B / D role: column
   const int cslot = c & 3, cm = c >> 2;
-  const int cmc = cm < MB ? cm : 0;
-  const bool b_active = (cslot == kb) && (cm < MB);
+  // activation rows 4h .. 4h+3 sit in the D columns of half h (MB = 8: two MFMA
+  // chains share every dequantized A operand)
+  constexpr int NH = (MB + 3) / 4;
   u32x4_t* my_stage = bstage[wave];
   uint16_t* stage16 = reinterpret_cast<uint16_t*>(my_stage);
-  if (lane < 16 * MB) bzero[wave][lane] = u32x4_t{0u, 0u, 0u, 0u};
-  // operand of step st: bsrc[st * MB]
-  const u32x4_t* bsrc = (b_active ? my_stage + kb * 16 * MB : bzero[wave]) + cmc;
+  for (int i = lane; i < 16 * MB; i += 64) bzero[i] = u32x4_t{0u, 0u, 0u, 0u};
+  // operand of step st for half h: bsrc[h][st * MB]; rmc[h] the lane's activation row (clamped)
+  const u32x4_t* bsrc[NH];
+  int rmc[NH];
+#pragma unroll
+  for (int h = 0; h < NH; ++h) {
+    const int row = cm + 4 * h;
+    rmc[h] = row < MB ? row : 0;
+    bsrc[h] = ((cslot == kb && row < MB) ? my_stage + kb * 16 * MB : bzero) + rmc[h];
+  }
   const int plane_stride = O * 16;
   // x role: lane (kb, r) owns columns 8r .. 8r+7 of its group; they land in
   // steps 4(r>>2) + s, operand slots je (weight 1) and je + 4 (weight 16).
@@ -325,15 +336,17 @@ __device__ __forceinline__ void w3_mfma_body(
 
   static_assert(kSumLanes % NW == 0, "waves per workgroup must divide the reduction lanes");
   constexpr int VS = kSumLanes / NW;  // accumulator sets per wave
-  float acc_sets[VS][RT][4];
+  float acc_sets[VS][RT][NH][4];
 #pragma unroll
   for (int v = 0; v < VS; ++v)
 #pragma unroll
     for (int tt = 0; tt < RT; ++tt)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) acc_sets[v][tt][j] = 0.f;
+      for (int h = 0; h < NH; ++h)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc_sets[v][tt][h][j] = 0.f;
   int cur_batch = 0;
-  auto consume = [&](const BatchLoads<MB, RT>& L, float (&acc)[RT][4]) __attribute__((always_inline)) {
+  auto consume = [&](const BatchLoads<MB, RT>& L, float (&acc)[RT][NH][4]) __attribute__((always_inline)) {
     const int gb = g0 + 4 * cur_batch;
     if constexpr (NORMIN) {
       // 1 / rms from the tile partials, at the wave's first batch: in the loop
@@ -382,9 +395,11 @@ __device__ __forceinline__ void w3_mfma_body(
     }
     __builtin_amdgcn_wave_barrier();
 
-    f32x4_t d[RT];
+    f32x4_t d[RT][NH];
 #pragma unroll
-    for (int tt = 0; tt < RT; ++tt) d[tt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int tt = 0; tt < RT; ++tt)
+#pragma unroll
+      for (int h = 0; h < NH; ++h) d[tt][h] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int word = 0; word < 4; ++word) {
       u32x4_t a[RT][4];
@@ -396,20 +411,28 @@ __device__ __forceinline__ void w3_mfma_body(
       }
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        const u32x4_t b = bsrc[(4 * word + s) * MB];
 #pragma unroll
-        for (int tt = 0; tt < RT; ++tt) {
-          if constexpr (XDT == kBF16 && !FIELDS)
-            d[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                __builtin_bit_cast(bf16x8_t, a[tt][s]), __builtin_bit_cast(bf16x8_t, b), d[tt], 0, 0, 0);
-          else
-            d[tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                __builtin_bit_cast(f16x8_t, a[tt][s]), __builtin_bit_cast(f16x8_t, b), d[tt], 0, 0, 0);
+        for (int h = 0; h < NH; ++h) {
+          const u32x4_t b = bsrc[h][(4 * word + s) * MB];
+#pragma unroll
+          for (int tt = 0; tt < RT; ++tt) {
+            if constexpr (XDT == kBF16 && !FIELDS)
+              d[tt][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                  __builtin_bit_cast(bf16x8_t, a[tt][s]), __builtin_bit_cast(bf16x8_t, b), d[tt][h], 0, 0, 0);
+            else
+              d[tt][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                  __builtin_bit_cast(f16x8_t, a[tt][s]), __builtin_bit_cast(f16x8_t, b), d[tt][h], 0, 0, 0);
+          }
         }
       }
     }
-    const float sxv = gsum[wave][cslot * MB + cmc];
-    const int fev = gexp[wave][cslot * MB + cmc];
+    float sxv[NH];
+    int fev[NH];
+#pragma unroll
+    for (int h = 0; h < NH; ++h) {
+      sxv[h] = gsum[wave][cslot * MB + rmc[h]];
+      fev[h] = gexp[wave][cslot * MB + rmc[h]];
+    }
 #pragma unroll
     for (int tt = 0; tt < RT; ++tt) {
       unsigned sw[2] = {L.s[tt][0], L.s[tt][1]}, zw = L.z[tt];
@@ -424,7 +447,8 @@ __device__ __forceinline__ void w3_mfma_body(
         const unsigned sb = (j & 1) ? (sw[j >> 1] >> 16) : (sw[j >> 1] & 0xffffu);
         const float se = to_f32<SDT>(uint16_t(sb));
         const float zf = float((zw >> (8 * j)) & 0xffu);
-        acc[tt][j] += se * (ldexpf(d[tt][j], fev) - zf * sxv);
+#pragma unroll
+        for (int h = 0; h < NH; ++h) acc[tt][h][j] += se * (ldexpf(d[tt][h][j], fev[h]) - zf * sxv[h]);
       }
     }
     __builtin_amdgcn_wave_barrier();
@@ -452,11 +476,13 @@ __device__ __forceinline__ void w3_mfma_body(
 #pragma unroll
           for (int tt = 0; tt < RT; ++tt)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              const float keep = acc_sets[0][tt][j];
-              acc_sets[0][tt][j] = acc_sets[1][tt][j];
-              acc_sets[1][tt][j] = keep;
-            }
+            for (int h = 0; h < NH; ++h)
+#pragma unroll
+              for (int j = 0; j < 4; ++j) {
+                const float keep = acc_sets[0][tt][h][j];
+                acc_sets[0][tt][h][j] = acc_sets[1][tt][h][j];
+                acc_sets[1][tt][h][j] = keep;
+              }
         }
       }
     }
@@ -469,18 +495,23 @@ __device__ __forceinline__ void w3_mfma_body(
 #pragma unroll
     for (int tt = 0; tt < RT; ++tt)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        float a = acc_sets[v][tt][j];
-        a += dpp_move<kDppXor1>(a);
-        a += dpp_move<kDppXor2>(a);
-        acc_sets[v][tt][j] = a;
+      for (int h = 0; h < NH; ++h)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          float a = acc_sets[v][tt][h][j];
+          a += dpp_move<kDppXor1>(a);
+          a += dpp_move<kDppXor2>(a);
+          acc_sets[v][tt][h][j] = a;
+        }
+#pragma unroll
+    for (int h = 0; h < NH; ++h) {
+      if (cslot == 0 && cm + 4 * h < MB) {
+#pragma unroll
+        for (int tt = 0; tt < RT; ++tt)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            red[wave + (odd ? 1 - v : v) * NW][(16 * tt + 4 * kb + j) * MB + cm + 4 * h] = acc_sets[v][tt][h][j];
       }
-    if (cslot == 0 && cm < MB) {
-#pragma unroll
-      for (int tt = 0; tt < RT; ++tt)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          red[wave + (odd ? 1 - v : v) * NW][(16 * tt + 4 * kb + j) * MB + cm] = acc_sets[v][tt][j];
     }
   }
   __syncthreads();

@@ -25,6 +25,7 @@ bool mfma_mb(int mb, int sdt, const MfmaArgs& a, dim3 g, hipStream_t s) {
     case 1: return mfma_sdt<NW, PD, 1, RT, PERM, XDT>(sdt, a, g, s);
     case 2: return mfma_sdt<NW, PD, 2, RT, PERM, XDT>(sdt, a, g, s);
     case 4: return mfma_sdt<NW, PD, 4, RT, PERM, XDT>(sdt, a, g, s);
+    case 8: return mfma_sdt<NW, PD, 8, RT, PERM, XDT>(sdt, a, g, s);
     default: return false;
   }
 }

@@ -37,7 +37,7 @@ struct MfmaArgs {
 };
 
 // nw waves per workgroup in {4, 8}; pd batches in flight per wave in {1, 2};
-// mb activation rows in {1, 2, 4}; tiles 16-row tiles per wave in {1, 2};
+// mb activation rows in {1, 2, 4, 8}; tiles 16-row tiles per wave in {1, 2};
 // sdt the scale dtype; the permutation instantiations are used when a.perm is
 // set.  False if no instantiation matches.
 #define FX_MFMA_DECL(NAME) \

@@ -353,6 +353,9 @@ class NativeDecodeSession:
         self.graph = None
         self.kernel_nodes = None
         self.launches_per_step = None
+        # eager-only inspection: called as observer(step, layer, residual) after each
+        # decoder layer of the residual-stream chain (a graph capture must leave it None)
+        self.layer_observer = None
 
     # -- one token -------------------------------------------------------------------
     def _attention(self, layer, pos):
@@ -412,6 +415,8 @@ class NativeDecodeSession:
             rs.normed(sw.layout, sw.scale_code, sw.zeros_ptr, 2 * sw.width, self.residual, self.post_norm[l],
                       self.eps, self.act, True)
             rs.residual(lin["mlp.down_proj"].gemv, self.act, self.residual)
+            if self.layer_observer is not None:
+                self.layer_observer(i, l, self.residual)
         self._lm_head(i, self.residual, self.final_norm)
 
     def _step(self, i):
@@ -479,6 +484,8 @@ class NativeDecodeSession:
 
     @torch.inference_mode()
     def capture(self) -> dict:
+        if self.layer_observer is not None:
+            raise RuntimeError("clear layer_observer before graph capture")
         stream = torch.cuda.Stream()
         stream.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(stream):
