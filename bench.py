@@ -467,6 +467,43 @@ def decode_bench(layers=36, prefix=512, steps=32, replays=5, seed=0):
             "w3_speedup_vs_bf16_hf": round(w3["hf"]["tokens_per_s"] / bf16["hf"]["tokens_per_s"], 3)}
 
 
+def decode_hybrid_native(layers=36, prefix=512, steps=32, replays=3, seed=0):
+    """Config 3's architecture with the reference's hybrid two-base g128/s8 Linears
+    (random payloads of the Qwen3-8B shapes; ``PackedHybridLinear`` everywhere,
+    ``fx_hybrid_gemv``) through the native decode chain: tokens/s and kernels per
+    token of the two-base full-model route."""
+    import statistics
+
+    import torch
+
+    from marlin_style_fluxbin_amd.native_decode import NativeDecodeSession
+    from marlin_style_fluxbin_amd.qwen3 import hybrid_qwen3_model, qwen3_config, random_qwen3_model
+
+    device = torch.device("cuda:0")
+    config = qwen3_config(num_hidden_layers=layers)
+    model = random_qwen3_model(config, device=device, dtype=torch.bfloat16, seed=seed)
+    linears = hybrid_qwen3_model(model, seed=seed)
+    payload_bytes = sum(t.numel() * t.element_size() for m in model.model.layers
+                        for name, t in m.named_buffers() if not name.endswith(("_planar", "_workspace", "lookup")))
+    g = torch.Generator().manual_seed(seed)
+    ids = torch.randint(0, config.vocab_size, (1, prefix), generator=g).to(device)
+    tokens = torch.randint(0, config.vocab_size, (1, steps), generator=g).to(device)
+    with torch.inference_mode():
+        session = NativeDecodeSession(model, ids, tokens)
+        session.capture()
+        samples = [session.measure("sequence_graph")[0]["device_ms"] for _ in range(replays)]
+    ms = statistics.median(samples)
+    result = {"workload": f"config 3 architecture, hybrid two-base g128/s8 Linears (random payloads), {layers} "
+                          f"layers, prefill {prefix}, {steps} steps, native chain",
+              "linears": linears, "layer_payload_bytes_per_token": payload_bytes,
+              "tokens_per_s": round(steps / (ms / 1e3), 2), "ms_per_token": round(ms / steps, 4),
+              "graph_ms": [round(v, 3) for v in samples],
+              "kernels_per_token": round(session.kernel_nodes / steps, 1)}
+    del session, model
+    torch.cuda.empty_cache()
+    return result
+
+
 def decode_native_only(layers=36, prefix=512, steps=32, replays=3, seed=0):
     """The config-3 W3 native decode arm alone (no HF arms, no parity audit):
     the workload for a kernel trace of the decode step.  Same model, prefix and
@@ -900,6 +937,9 @@ def main():
         del graph, layers
         torch.cuda.empty_cache()
         result["config"]["decode"] = decode_bench(layers=args.decode_layers)
+        torch.cuda.empty_cache()
+        result["config"]["decode"]["hybrid_two_base_native"] = decode_hybrid_native(layers=args.decode_layers)
+        print(f"# decode hybrid: {result['config']['decode']['hybrid_two_base_native']}", file=sys.stderr, flush=True)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline()
     print(json.dumps(result), flush=True)

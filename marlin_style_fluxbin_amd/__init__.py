@@ -53,6 +53,7 @@ from .fused_modules import (  # noqa: F401
 from .packing import pack_two_bases, unpack_two_bases  # noqa: F401
 from .evaluation import materialize_global_two_base_weight, materialize_hybrid_s8_weight  # noqa: F401
 from .deployment import PackedHybridLinear  # noqa: F401
+from .w3_lut_artifacts import load_w3_lut_layer, replace_w3_model_linears, write_w3_lut_artifacts  # noqa: F401
 from .two_base import TwoBaseGemv, pack_rank_one_planes, two_base_gemv, unpack_rank_one_planes  # noqa: F401
 
 __version__ = "0.1.0"

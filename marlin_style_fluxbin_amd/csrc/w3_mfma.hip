@@ -163,9 +163,15 @@ constexpr int kSumLanes = 8;
 // (one array for the workgroup: every wave writes all of it, with zeros only,
 // before its own first read, so no barrier orders the waves); sum of x and
 // subnormal exponent - E per (k-block group, row); the per-wave partial outputs.
+// The four k-block stages of a wave are kStageStride<MB> 16-byte slots apart, one
+// more than they hold: without the extra slot every k-block started on the same
+// LDS bank, and the lanes staging or reading the four k-blocks at once collided.
+template <int MB>
+constexpr int kStageStride = 16 * MB + 1;
+
 template <int NW, int MB, int RT>
 struct MfmaShared {
-  u32x4_t bstage[NW][64 * MB];
+  u32x4_t bstage[NW][4 * kStageStride<MB>];
   u32x4_t bzero[16 * MB];
   float gsum[NW][4 * MB];
   int gexp[NW][4 * MB];
@@ -236,7 +242,7 @@ __device__ __forceinline__ void w3_mfma_body(
   for (int h = 0; h < NH; ++h) {
     const int row = cm + 4 * h;
     rmc[h] = row < MB ? row : 0;
-    bsrc[h] = ((cslot == kb && row < MB) ? my_stage + kb * 16 * MB : bzero) + rmc[h];
+    bsrc[h] = ((cslot == kb && row < MB) ? my_stage + kb * kStageStride<MB> : bzero) + rmc[h];
   }
   const int plane_stride = O * 16;
   // x role: lane (kb, r) owns columns 8r .. 8r+7 of its group; they land in
@@ -314,7 +320,7 @@ __device__ __forceinline__ void w3_mfma_body(
         o[q] = unsigned(f32_to_f16_bits(ldexpf(v[2 * q], e))) |
                (unsigned(f32_to_f16_bits(ldexpf(v[2 * q + 1], e))) << 16);
       }
-      my_stage[(kb * 16 + r) * MB + m] = o;
+      my_stage[kb * kStageStride<MB> + r * MB + m] = o;
       if (r == 0) {
         gsum[wave][kb * MB + m] = sm;
         gexp[wave][kb * MB + m] = subnormal_exponent<kF16>() - E;
@@ -323,7 +329,7 @@ __device__ __forceinline__ void w3_mfma_body(
       const int E = choose_exponent<XDT>(mx);
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        uint16_t* dst = stage16 + ((kb * 16 + xstep + s) * MB + m) * 8;
+        uint16_t* dst = stage16 + (kb * kStageStride<MB> + (xstep + s) * MB + m) * 8;
         dst[je] = exact_bits<XDT>(ldexpf(v[s], E));
         dst[je + 4] = exact_bits<XDT>(ldexpf(v[4 + s], E - 4));
       }

@@ -14,8 +14,10 @@ with structural W3 Linears,
 
 (6 launches; 5 while one split covers the context), followed once per token by
 one launch for the final RMSNorm, the
-bf16 LM head and the argmax.  Other Linears (the bf16 arm) take add+RMSNorm
-kernels and ``torch.matmul`` between the same attention launches.  The
+bf16 LM head and the argmax.  Other Linears -- the hybrid two-base g128/s8
+format of ``PackedHybridLinear`` (``fx_hybrid_gemv``) or dense bf16 (the bf16
+arm, ``torch.matmul``) -- run between add+RMSNorm kernels and the same attention
+launches.  The
 arithmetic and rounding points are the stock HF Qwen3 modules' (RMSNorm, RoPE,
 SDPA with fp32 softmax, SwiGLU).
 """
@@ -29,6 +31,7 @@ import torch
 from . import _lib
 from .fused_modules import add_rms_norm
 from .static_decode import graph_kernel_count
+from .deployment import PackedHybridLinear
 from .w3_lut_deployment import PackedW3Linear, W3Gemv
 
 _ATTN = ("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj", "self_attn.o_proj")
@@ -36,26 +39,28 @@ _MLP = ("mlp.gate_proj", "mlp.up_proj", "mlp.down_proj")
 
 
 class _Linear:
-    """One decode Linear: W3 MFMA GEMV or a dense bf16 matmul, writing ``out``."""
+    """One decode Linear writing ``out``: the W3 MFMA GEMV, the hybrid two-base GEMV
+    (``fx_hybrid_gemv`` through the module's own packed kernel and workspace), or a
+    dense matmul."""
 
     def __init__(self, module):
+        self.gemv = None
+        self.call = None
         if isinstance(module, PackedW3Linear):
             self.gemv = W3Gemv(module.layout(), arithmetic=module.arithmetic)
-            self.weight = None
-            self.packed = True
+            self.call = self.gemv
+        elif isinstance(module, PackedHybridLinear):
+            self.call = module._packed_kernel(1, module.codes.device)
         elif isinstance(module, torch.nn.Linear):
-            self.gemv = None
-            self.weight = module.weight
-            self.packed = False
+            weight = module.weight
+            self.call = lambda x, out: torch.matmul(x, weight.t(), out=out)
         else:
             raise TypeError(f"unsupported Linear type {type(module).__name__}")
+        self.packed = not isinstance(module, torch.nn.Linear)
         self.bias = module.bias
 
     def __call__(self, x, out):
-        if self.packed:
-            self.gemv(x, out)
-        else:
-            torch.matmul(x, self.weight.t(), out=out)
+        self.call(x, out)
         if self.bias is not None:
             out.add_(self.bias)
 

@@ -151,3 +151,53 @@ def w3_quantize_qwen3_model(model, *, fallback: str = "dense", row_tile_by_shape
             policy = None if shapes <= set(QWEN3_ROW_TILE_BY_SHAPE) else {s: 256 for s in shapes}
         count += len(replace_w3_block_linears(block, payload, fallback=fallback, row_tile_by_shape=policy))
     return count
+
+
+def random_hybrid_payload(out_features: int, in_features: int, *, device, generator, row_scale: float = 0.01) -> dict:
+    """A random hybrid g128/s8 two-base payload of one Linear (the seven fields of
+    ``deployment.FIELDS``): uniform random signs, row scales ~ N(0, row_scale),
+    column scales ~ N(0, 1), sorted distinct refinement columns.  The reference
+    builds these payloads offline from real weights (out of scope here); random
+    ones exercise the same kernels at the same shapes and byte counts."""
+    import torch
+
+    from .packing import pack_two_bases
+
+    g = in_features // 128
+    kw = {"device": device, "generator": generator}
+
+    def signs(k):
+        return pack_two_bases(torch.randint(0, 2, (2, out_features, k), **kw) * 2 - 1)
+
+    idx = torch.sort(torch.rand(g, 128, **kw).argsort(dim=1)[:, :8], dim=1).values.to(torch.int16)
+    return {
+        "global_sign_codes": signs(in_features),
+        "global_row_scales": torch.randn(2, out_features, g, **kw) * row_scale,
+        "global_column_scales": torch.randn(2, g, 128, **kw),
+        "refinement_indices": idx,
+        "refinement_sign_codes": signs(g * 8),
+        "refinement_row_scales": torch.randn(2, out_features, g, **kw) * (0.7 * row_scale),
+        "refinement_column_scales": torch.randn(2, g, 8, **kw),
+    }
+
+
+def hybrid_qwen3_model(model, *, seed: int = 0, kernel: str = "v5_p1024", groups_per_split: int = 8,
+                       fallback: str = "dense") -> int:
+    """Replace every decoder block's seven Linears by ``PackedHybridLinear`` with
+    random hybrid payloads of the same shapes (in place); returns the count."""
+    import torch
+
+    from .deployment import replace_block_linears
+
+    device = model.model.embed_tokens.weight.device
+    generator = torch.Generator(device=device).manual_seed(seed)
+    count = 0
+    for block in model.model.layers:
+        payload = {}
+        for name in QWEN3_LINEAR_MODULES:
+            o, k = block.get_submodule(name).weight.shape
+            for field, value in random_hybrid_payload(o, k, device=device, generator=generator).items():
+                payload[f"{name}.{field}"] = value
+        count += len(replace_block_linears(block, payload, fallback=fallback, groups_per_split=groups_per_split,
+                                           kernel=kernel))
+    return count
