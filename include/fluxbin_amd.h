@@ -266,10 +266,11 @@ int fx_silu_mul(const void *gate, const void *up, void *out, int n, int dtype, v
  * hidden / norm_weight [hidden_size], weight [vocab, hidden_size] row-major,
  * logits [vocab], all in `dtype`; hidden_size a multiple of 512 up to 8192;
  * hidden, norm_weight, weight 16-byte aligned, logits 2-byte aligned.  The
- * normalised x is bit-identical to fx_rmsnorm's.  `workspace`
- * (fx_lm_head_argmax_workspace_bytes, 16-byte aligned): allocate it zero-filled
- * once; every call leaves its arrival counter at zero.  Calls sharing a
- * workspace must not overlap.
+ * normalised x is bit-identical to fx_rmsnorm's.  Two launches: the streaming
+ * kernel leaves each workgroup's best logit in `workspace`
+ * (fx_lm_head_argmax_workspace_bytes, 16-byte aligned, no initial contents
+ * needed) and a one-workgroup launch merges them into *prediction.  Calls sharing
+ * a workspace must not overlap.
  */
 size_t fx_lm_head_argmax_workspace_bytes(void);
 int fx_lm_head_argmax(const void *hidden, const void *norm_weight, float eps, const void *weight, void *logits,

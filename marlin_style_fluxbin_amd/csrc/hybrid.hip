@@ -16,10 +16,14 @@
 //   c >= 8 the same for the refinement; an operand is non-zero only in the lanes
 //   of its own column and k-block (the others read a shared zero block).
 // * Activations u_b = x * cols[.., b] are rounded to v = rint(u_b 2^F) with F per
-//   (batch, base), |v| <= 2^14, and split into digits 256 hi + lo.  Per batch the
-//   int32 products are folded: acc += rows[g,o,b] (2 S - U_g,b) with S the
-//   weighted digit sum and U the exact sum of the same v (per group and base);
-//   the refinement the same with its own scales.
+//   (group, base) -- |v| <= 2^14 over the group's 128 columns -- and split into
+//   digits 256 hi + lo.  Every D column holds one group, so each column is folded
+//   with its own 2^-F: an outlier coarsens only its own group, whose row scale
+//   multiplies it anyway.  Per batch the int32 products are folded:
+//   acc += rows[g,o,b] (2 S - U_g,b) 2^-F_g,b with S the weighted digit sum and U
+//   the exact sum of the same v; the refinement the same with its own scales and
+//   exponents.  A refinement index outside [0, 128) makes the output NaN (its U
+//   is NaN), as the reference's lookup does.
 //
 // Work split as in the rank-one kernel: a workgroup owns NT 16-row tiles and a K
 // range; wave w stages batches w, w + NW, ... (one 8-column unit per lane and
@@ -34,13 +38,6 @@ typedef int hy_i32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr float kHyMagic = 12583040.0f;  // 1.5 * 2^23 + 128: low 16 bits of the sum are v + 128
 constexpr int kHyMaxUnits = 4;           // staged batches per wave
-
-__device__ __forceinline__ float hy_wave_max(float v) {
-  v = row16_max(v);
-  v = fmaxf(v, __shfl_xor(v, 16, 64));
-  v = fmaxf(v, __shfl_xor(v, 32, 64));
-  return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v)));
-}
 
 __device__ __forceinline__ int hy_exponent(float max_abs) {
   if (!(max_abs > 0.f)) return 0;
@@ -60,8 +57,8 @@ __global__ __launch_bounds__(NT * NK * 64) void hybrid_kernel(HybridArgs a) {
   constexpr int NW = NT * NK;
   extern __shared__ u32x4_t hy_dyn[];
   __shared__ u32x4_t zero16;
-  __shared__ float fsc[kHybridMaxBatches][2];      // 2^-F per (batch, base)
-  __shared__ float fref[kHybridMaxBatches];        // 2^-F of the refinement operands
+  __shared__ float fsc[kHybridMaxBatches][4][2];   // 2^-F per (batch, group slot, base)
+  __shared__ float fref[kHybridMaxBatches][4][2];  // the same for the refinement operands
   __shared__ float ug[kHybridMaxBatches][4][2];    // U per (batch, group slot, base)
   __shared__ float vg[kHybridMaxBatches][4][2];    // refinement U per (batch, slot, base)
   __shared__ float red[NK][16 * NT];
@@ -152,7 +149,7 @@ __global__ __launch_bounds__(NT * NK * 64) void hybrid_kernel(HybridArgs a) {
           u[j] = xv[j] * __uint_as_float(sc[q][(2 * j + b) >> 2][(2 * j + b) & 3]);
           mx = fmaxf(mx, fabsf(u[j]));
         }
-        const int F = hy_exponent(hy_wave_max(mx));
+        const int F = hy_exponent(row16_max(mx));  // the group's 16 lanes
         const float scale = ldexpf(1.f, F);
         int vsum = 0;
 #pragma unroll
@@ -165,26 +162,36 @@ __global__ __launch_bounds__(NT * NK * 64) void hybrid_kernel(HybridArgs a) {
           dst[16] = uint8_t(wv ^ 0x80u);      // lo digit
         }
         const float us = row16_sum(float(vsum));  // group slot kb; |sum| < 2^22: exact
-        if (r == 0) ug[bt][kb][b] = ldexpf(us, -F);
-        if (lane == 0) fsc[bt][b] = ldexpf(1.f, -F);
+        if (r == 0) {
+          ug[bt][kb][b] = ldexpf(us, -F);
+          fsc[bt][kb][b] = ldexpf(1.f, -F);
+        }
       }
       __builtin_amdgcn_wave_barrier();  // xs of this batch written by this wave
       // refinement: lane (kb, r) takes column idx[g][r & 7] of base r >> 3
       const int j = r & 7, b = r >> 3;
-      const int cc = int(int16_t(uint16_t(sidx[q]))) & 127;
+      const int index = int(int16_t(uint16_t(sidx[q])));
+      const bool bad_index = index < 0 || index > 127;
+      const int cc = index & 127;  // the read stays inside the group; a bad index poisons U below
       const uint16_t* xs16 = reinterpret_cast<const uint16_t*>(xs + bt * 64 + kb * 16);
       const float v = to_f32<XDT>(xs16[cc]) * __uint_as_float(sscol[q]);
-      const int F = hy_exponent(hy_wave_max(fabsf(v)));
+      float m8 = fabsf(v);  // max over the 8 lanes of this (group, base)
+      m8 = fmaxf(m8, dpp_move<kDppXor1>(m8));
+      m8 = fmaxf(m8, dpp_move<kDppXor2>(m8));
+      m8 = fmaxf(m8, dpp_move<kDppHalfMirror>(m8));
+      const int F = hy_exponent(m8);
       const unsigned wv = __float_as_uint(fmaf(v, ldexpf(1.f, F), kHyMagic));
       uint8_t* dst = rslot + (((bt * 2 + b) * 4 + kb) * 2) * 16 + j;
       dst[0] = uint8_t(wv >> 8);
       dst[16] = uint8_t(wv ^ 0x80u);
-      float vs = float(int(int16_t(uint16_t(wv))) - 128);
+      float vs = bad_index ? __builtin_nanf("") : float(int(int16_t(uint16_t(wv))) - 128);
       vs += dpp_move<kDppXor1>(vs);
       vs += dpp_move<kDppXor2>(vs);
       vs += dpp_move<kDppHalfMirror>(vs);  // lanes j and 7 - j: completes the 8-lane sum
-      if (j == 0) vg[bt][kb][b] = ldexpf(vs, -F);
-      if (lane == 0) fref[bt] = ldexpf(1.f, -F);
+      if (j == 0) {
+        vg[bt][kb][b] = ldexpf(vs, -F);
+        fref[bt][kb][b] = ldexpf(1.f, -F);
+      }
     }
   }
   __syncthreads();
@@ -223,8 +230,8 @@ __global__ __launch_bounds__(NT * NK * 64) void hybrid_kernel(HybridArgs a) {
                                                 __builtin_bit_cast(hy_i32x4_t, bop1), d1, 0, 0, 0);
     }
     // fold: this lane's column is (group slot, digit) of the main or the refinement product
-    const float s0 = dw * (is_ref ? fref[bt] : fsc[bt][0]);
-    const float s1 = dw * (is_ref ? fref[bt] : fsc[bt][1]);
+    const float s0 = dw * (is_ref ? fref[bt][dslot][0] : fsc[bt][dslot][0]);
+    const float s1 = dw * (is_ref ? fref[bt][dslot][1] : fsc[bt][dslot][1]);
     const float u0 = digit ? 0.f : (is_ref ? vg[bt][dslot][0] : ug[bt][dslot][0]);
     const float u1 = digit ? 0.f : (is_ref ? vg[bt][dslot][1] : ug[bt][dslot][1]);
     // rv: rows drow + j, base b at float 2 j + b

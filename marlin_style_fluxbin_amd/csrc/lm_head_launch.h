@@ -8,7 +8,7 @@ namespace fx {
 constexpr int kLmWaves = 4;             // waves per workgroup (256 threads)
 constexpr int kLmMaxChunks = 16;        // hidden <= 16 * 512
 constexpr int kLmMaxBlocks = 4096;      // workgroups (argmax partials) per launch
-constexpr size_t kLmCounterBytes = 256; // the arrival counter, padded
+constexpr size_t kLmCounterBytes = 256; // reserved head of the workspace (kept for the ABI's size)
 
 struct LmHeadArgs {
   const uint16_t* x;       // [K] hidden state (normalised here when norm_w is set)
@@ -17,7 +17,7 @@ struct LmHeadArgs {
   const uint16_t* w;       // [V, K] LM-head weight, row-major
   uint16_t* logits;        // [V]
   long long* prediction;   // [1] argmax of the rounded logits (first index of the maximum)
-  unsigned* arrival;       // workspace: counter (zero between calls), then partials
+  unsigned* arrival;       // workspace head (unused), then the partials
   float* part_val;         // [blocks]
   int* part_idx;           // [blocks]
   int V, K, blocks;

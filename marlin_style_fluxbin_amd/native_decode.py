@@ -351,8 +351,8 @@ class NativeDecodeSession:
         self.lm_ws = None
         if (head.dtype == dtype and head.is_contiguous() and head.data_ptr() % 16 == 0
                 and self.hidden % 512 == 0 and self.hidden <= 8192):
-            self.lm_ws = torch.zeros(lib.fx_lm_head_argmax_workspace_bytes(), dtype=torch.uint8,
-                                     device=self.device)  # arrival counter starts at zero
+            self.lm_ws = torch.empty(lib.fx_lm_head_argmax_workspace_bytes(), dtype=torch.uint8,
+                                     device=self.device)  # per-workgroup argmax partials
         nbytes = lib.fx_decode_attention_workspace_bytes(self.heads, self.maximum_length, self.head_dim)
         self.attn_ws = torch.empty(nbytes // 4 + 64, dtype=torch.float32, device=self.device)  # split partials
         self.graph = None

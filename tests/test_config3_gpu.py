@@ -148,7 +148,7 @@ def test_lm_head_argmax_at_vocab_151936(gpu):
     logits = torch.empty(vocab, dtype=torch.bfloat16, device=gpu)
     pred = torch.full((1,), -1, dtype=torch.int64, device=gpu)
     wg, hg, ng = weight.to(gpu), hidden.to(gpu), norm_w.to(gpu)
-    for _ in range(2):  # the second call finds the arrival counter back at zero
+    for _ in range(2):  # a second call on the same workspace
         _lib.check(lib.fx_lm_head_argmax(hg.data_ptr(), ng.data_ptr(), 1e-6, wg.data_ptr(),
                                          logits.data_ptr(), pred.data_ptr(), ws.data_ptr(), ws.numel(), vocab, k,
                                          _lib.FX_BF16, _lib.stream_handle(gpu)), "fx_lm_head_argmax")
@@ -183,4 +183,4 @@ def test_config3_36_layers_graph_replay_equals_eager(gpu):
     assert torch.equal(eager["predictions"][0, 1:], torch.argmax(logits, dim=-1))
     per_token = native.kernel_nodes / 32
     print(f"kernels per token: {per_token}", flush=True)
-    assert per_token <= 6 * 36 + 3
+    assert per_token <= 6 * 36 + 4  # + embedding, first RMSNorm, LM head, argmax merge

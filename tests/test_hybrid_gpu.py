@@ -145,3 +145,39 @@ def test_packed_hybrid_linear_routes_and_prepared_decode(gpu, kernel):
         module.clear_prepared_decode()
         with pytest.raises(ValueError):
             module(torch.randn(1, 2, g * 128, device=gpu, dtype=torch.bfloat16))
+
+
+@pytest.mark.parametrize("gps", [1, 8])
+def test_outlier_activation_per_element_bound(gpu, gps):
+    """An activation outlier (~1e3 in a group with tiny row scales, the rest ~1e-2):
+    every output row within the per-group fixed-point bound 2^-7 B_o of the float64
+    truth plus its bf16 rounding (the emulation in tests/test_hybrid_numerics.py
+    shows a batch-wide exponent breaking this bound)."""
+    from tests.test_hybrid_numerics import outlier_case, row_bound
+
+    p, layout_np, x = outlier_case()
+    o = layout_np["codes"].shape[1]
+    layout = _layout({k: torch.from_numpy(v) for k, v in p.items()}, "v5_p1024", gpu)
+    exact = tb.structural_reference(x, layout_np)[0]
+    bound = row_bound(x, layout_np) + 2.0 ** -8 * np.abs(exact)
+    xt = torch.from_numpy(x).to(torch.bfloat16).to(gpu)
+    ws = torch.full(d.workspace_shape(o, x.shape[1], gps), float("nan"), device=gpu)
+    y = torch.empty(1, o, dtype=torch.bfloat16, device=gpu)
+    d.m1_out(xt, layout, y, ws, groups_per_split=gps, kernel="v5_p1024")
+    got = y.float().cpu().numpy()[0].astype(np.float64)
+    assert np.all(np.abs(got - exact) <= bound), float(np.max(np.abs(got - exact) / bound))
+
+
+def test_out_of_range_refinement_index_gives_nan(gpu):
+    p = _payload(24, 3, seed=8)
+    layout = _layout(p, "v5_p1024", gpu)
+    layout["indices"] = layout["indices"].clone()
+    layout["indices"][1, 5] = 200
+    x = torch.randn(1, 384, generator=torch.Generator().manual_seed(8)).to(torch.bfloat16).to(gpu)
+    y = torch.zeros(1, 24, dtype=torch.bfloat16, device=gpu)
+    ws = torch.empty(d.workspace_shape(24, 384, 8), device=gpu)
+    d.m1_out(x, layout, y, ws, kernel="v5_p1024")
+    assert torch.isnan(y.float()).all()
+    layout["indices"][1, 5] = -3
+    d.m1_out(x, layout, y, ws, kernel="v5_p1024")
+    assert torch.isnan(y.float()).all()

@@ -100,17 +100,17 @@ def test_lm_head_argmax_ties_and_nan(gpu):
 
 
 def test_lm_head_argmax_workspace_reuse(gpu):
-    """One zero-filled workspace across calls with different grids (1 to 512
-    workgroups): every prediction is right and the arrival counter is zero
-    after each call."""
+    """One workspace, filled with junk first, across calls with different grids (1
+    to 512 workgroups): every prediction is right (the merge reads only the
+    partials the same call wrote; nothing needs clearing between calls)."""
     head = _Head(gpu)
+    head.ws.fill_(0xA5)
     g = torch.Generator().manual_seed(5)
     for vocab in [151936, 3, 20000, 1, 4097]:
         x = torch.randn(1, 1024, generator=g).to(torch.bfloat16).to(gpu)
         w = torch.randn(vocab, 1024, generator=g).to(torch.bfloat16).to(gpu)
         logits, pred = head(x, None, w)
         assert pred.item() == torch.argmax(logits.cpu()).item(), vocab
-        assert not head.ws[:4].any().item(), vocab
 
 
 def test_lm_head_argmax_rejects_bad_shapes(gpu):
