@@ -1001,9 +1001,13 @@ int fx_decode_attention_rope(const void* q, const void* k, const void* v, const 
                           head_dim, position, scale, dtype, stream, pre);
 }
 
-// LM head: two workgroups per CU (8 waves, two 8 KB rows in flight per wave at
-// hidden 4096), fewer when the vocabulary has fewer row pairs.
-constexpr int kLmBlocksPerCu = 2;
+// LM head: one workgroup per CU (4 waves, one 8 KB row in flight per wave at
+// hidden 4096: 32 KB per CU), fewer when the vocabulary has fewer rows.  Measured
+// at 151936 x 4096 (HIP events, 20 calls): 177.0 us against 189.8 us for two
+// workgroups per CU with two rows per wave (128 KB per CU in flight); a plain
+// streaming read of the same 1.24 GB peaks at 24-32 KB per CU in flight too
+// (7.3 TB/s) and falls to 5-6 TB/s at 64-128 KB.
+constexpr int kLmBlocksPerCu = 1;
 
 size_t fx_lm_head_argmax_workspace_bytes(void) {
   return fx::kLmCounterBytes + size_t(fx::kLmMaxBlocks) * (sizeof(float) + sizeof(int));
@@ -1041,9 +1045,9 @@ int fx_lm_head_argmax(const void* hidden, const void* norm_weight, float eps, co
   a.part_idx = reinterpret_cast<int*>(a.part_val + fx::kLmMaxBlocks);
   a.V = vocab;
   a.K = hidden_size;
-  const long pairs = (long(vocab) + 1) / 2;
+  const long groups = (long(vocab) + fx::kLmRowsInFlight - 1) / fx::kLmRowsInFlight;  // one wave's rows at a time
   a.blocks = int(std::min<long>({long(fx::kLmMaxBlocks), long(kLmBlocksPerCu) * device_cu_count(),
-                                 (pairs + fx::kLmWaves - 1) / fx::kLmWaves}));
+                                 (groups + fx::kLmWaves - 1) / fx::kLmWaves}));
   fx::launch_lm_head_argmax(dtype, a, static_cast<hipStream_t>(stream));
   return check_launch("lm_head_argmax_kernel");
 }

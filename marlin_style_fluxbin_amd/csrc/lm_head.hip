@@ -39,10 +39,11 @@ __device__ __forceinline__ bool ranks_above(float v, int i, float u, int j) {
   return v > u || (v == u && i < j);
 }
 
-// grid `blocks` workgroups of 4 waves; wave w of the grid takes the row pairs
-// (2p, 2p + 1), p = w, w + waves, ... (neighbouring waves stream neighbouring
-// rows).  Lane l holds elements [8 (64 c + l), +8) of the activation for each
-// 512-element chunk c, so a weight row is NC loads of 16 B per lane, coalesced.
+// grid `blocks` workgroups of 4 waves; wave w of the grid takes the row groups
+// (RPI p .. RPI p + RPI - 1), p = w, w + waves, ... (neighbouring waves stream
+// neighbouring rows).  Lane l holds elements [8 (64 c + l), +8) of the activation
+// for each 512-element chunk c, so a weight row is NC loads of 16 B per lane,
+// coalesced, and a wave keeps RPI rows (RPI * 8 KB at K = 4096) in flight.
 // Every wave normalises the activation itself (the RMSNorm batch order of
 // rmsnorm_kernel: per-chunk wave totals added in chunk order; bit-identical
 // normalised values).  Each wave keeps its running argmax; the workgroup's
@@ -50,8 +51,10 @@ __device__ __forceinline__ bool ranks_above(float v, int i, float u, int j) {
 // next launch on the stream, so the kernel boundary orders every block's stores
 // before its loads -- merges them and writes the prediction.  (Merging inside this
 // launch needs a device-scope release per block, which writes back the block's
-// XCD L2: 191.5 -> 207.1 us per call at 151936 x 4096.)
-template <int DT, int NC, bool NORM>
+// XCD L2: 191.5 -> 207.1 us per call at 151936 x 4096.)  A row's logit does not
+// depend on RPI or the grid: each row is one wave's two dot2 chains and one
+// wave total.
+template <int DT, int NC, bool NORM, int RPI>
 __global__ __launch_bounds__(256) void lm_head_argmax_kernel(LmHeadArgs a) {
   asm volatile("" ::"s"(a.x), "s"(a.norm_w), "s"(a.eps), "s"(a.w), "s"(a.logits), "s"(a.part_val),
                "s"(a.part_idx), "s"(a.V));
@@ -88,36 +91,36 @@ __global__ __launch_bounds__(256) void lm_head_argmax_kernel(LmHeadArgs a) {
 
   float best = -INFINITY;
   int best_i = INT_MAX;
-  const int waves = gridDim.x * kLmWaves, pairs = (a.V + 1) / 2;
-  for (int p = blockIdx.x * kLmWaves + wave; p < pairs; p += waves) {
-    const int r0 = 2 * p, r1 = min(r0 + 1, a.V - 1);  // an odd V's last pair reads row V - 1 twice
-    const u32x4_t* w0 = reinterpret_cast<const u32x4_t*>(a.w + size_t(r0) * K) + lane;
-    const u32x4_t* w1 = reinterpret_cast<const u32x4_t*>(a.w + size_t(r1) * K) + lane;
-    u32x4_t b0[NC], b1[NC];
+  const int waves = gridDim.x * kLmWaves, groups = (a.V + RPI - 1) / RPI;
+  for (int p = blockIdx.x * kLmWaves + wave; p < groups; p += waves) {
+    int r[RPI];
+    u32x4_t b[RPI][NC];
 #pragma unroll
-    for (int c = 0; c < NC; ++c) b0[c] = __builtin_nontemporal_load(w0 + 64 * c);
+    for (int j = 0; j < RPI; ++j) {
+      r[j] = min(RPI * p + j, a.V - 1);  // the last group of a ragged V re-reads row V - 1
+      const u32x4_t* wr = reinterpret_cast<const u32x4_t*>(a.w + size_t(r[j]) * K) + lane;
 #pragma unroll
-    for (int c = 0; c < NC; ++c) b1[c] = __builtin_nontemporal_load(w1 + 64 * c);
-    __builtin_amdgcn_sched_barrier(0);  // both rows' loads in flight before the first use
-    float s0[2] = {0.f, 0.f}, s1[2] = {0.f, 0.f};
+      for (int c = 0; c < NC; ++c) b[j][c] = __builtin_nontemporal_load(wr + 64 * c);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // every row's loads in flight before the first use
+    float sacc[RPI][2];
+#pragma unroll
+    for (int j = 0; j < RPI; ++j) sacc[j][0] = sacc[j][1] = 0.f;
 #pragma unroll
     for (int c = 0; c < NC; ++c)
 #pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        s0[w & 1] = dot2<DT>(b0[c][w], xv[c][w], s0[w & 1]);
-        s1[w & 1] = dot2<DT>(b1[c][w], xv[c][w], s1[w & 1]);
+      for (int w = 0; w < 4; ++w)
+#pragma unroll
+        for (int j = 0; j < RPI; ++j) sacc[j][w & 1] = dot2<DT>(b[j][c][w], xv[c][w], sacc[j][w & 1]);
+#pragma unroll
+    for (int j = 0; j < RPI; ++j) {
+      const float y = round_to<DT>(wave_total(sacc[j][0] + sacc[j][1]));
+      const bool fresh = j == 0 || r[j] != r[j - 1];
+      if (lane == j && fresh) a.logits[r[j]] = from_f32<DT>(y);
+      if (fresh && ranks_above(y, r[j], best, best_i)) {
+        best = y;
+        best_i = r[j];
       }
-    const float y0 = round_to<DT>(wave_total(s0[0] + s0[1]));
-    const float y1 = round_to<DT>(wave_total(s1[0] + s1[1]));
-    if (lane == 0) a.logits[r0] = from_f32<DT>(y0);
-    if (lane == 1 && r1 != r0) a.logits[r1] = from_f32<DT>(y1);
-    if (ranks_above(y0, r0, best, best_i)) {
-      best = y0;
-      best_i = r0;
-    }
-    if (r1 != r0 && ranks_above(y1, r1, best, best_i)) {
-      best = y1;
-      best_i = r1;
     }
   }
 
@@ -190,9 +193,10 @@ bool lm_dispatch(int nc, const LmHeadArgs& a, hipStream_t s) {
   } else {
     if (nc != NC) return lm_dispatch<DT, NC + 1>(nc, a, s);
     if (a.norm_w)
-      hipLaunchKernelGGL((lm_head_argmax_kernel<DT, NC, true>), dim3(a.blocks), dim3(256), 0, s, a);
+      hipLaunchKernelGGL((lm_head_argmax_kernel<DT, NC, true, kLmRowsInFlight>), dim3(a.blocks), dim3(256), 0, s, a);
     else
-      hipLaunchKernelGGL((lm_head_argmax_kernel<DT, NC, false>), dim3(a.blocks), dim3(256), 0, s, a);
+      hipLaunchKernelGGL((lm_head_argmax_kernel<DT, NC, false, kLmRowsInFlight>), dim3(a.blocks), dim3(256), 0, s,
+                         a);
     hipLaunchKernelGGL(lm_head_merge_kernel, dim3(1), dim3(256), 0, s, a.part_val, a.part_idx, a.blocks,
                        a.prediction);
     return true;

@@ -8,6 +8,7 @@ namespace fx {
 constexpr int kLmWaves = 4;             // waves per workgroup (256 threads)
 constexpr int kLmMaxChunks = 16;        // hidden <= 16 * 512
 constexpr int kLmMaxBlocks = 4096;      // workgroups (argmax partials) per launch
+constexpr int kLmRowsInFlight = 1;      // weight rows a wave loads before its first dot product
 constexpr size_t kLmCounterBytes = 256; // reserved head of the workspace (kept for the ABI's size)
 
 struct LmHeadArgs {
