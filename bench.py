@@ -21,9 +21,14 @@ after the library's bind-time repack into its field layout (same bytes, half
 the dequant instructions), the format the native decode reads.
 ``roofline.traffic`` is the HBM bytes per launch measured with rocprofv3 PMC
 counters (FETCH_SIZE + WRITE_SIZE, scaled by a plain read kernel of known size),
-read from ``profiles/w3_mfma_traffic.json`` when present.  The CPU baseline
-times the oracle's dequantize-then-matmul restatement of the reference's dense
-CPU route on a bounded sample.
+read from ``profiles/w3_mfma_traffic.json`` when present.
+
+Also in the line: ``config.fused_ops`` (config 2: RMSNorm, residual add + RMSNorm,
+q/k norm + RoPE per launch beside HF's eager ops), ``config.two_base`` (config 4),
+``config.decode`` (config 3: W3 and bf16, HF module tree and native chain, plus
+the hybrid two-base native arm) and ``cpu_baseline``: the reference's CPU route
+(dequantize + ``F.linear`` per call, as the product's CPU torch code restates it)
+on config 0, at the host's thread budget and at one thread.
 """
 from __future__ import annotations
 
@@ -204,6 +209,126 @@ def bench_shape(o, k, device, steps, warmup, stream, min_bytes=320e6, min_copies
         "fields_frac_hbm": round(nbytes / fields_us / 1e3 / HBM_PEAK_GBPS, 4),
         "small_m": small_m,
     }
+
+
+def fused_ops_bench(device, steps, warmup, stream, launches=64, seed=0):
+    """Config 2: the fused non-Linear decode ops at Qwen3-8B shapes, batch 1, one
+    token.  Per launch (a graph of ``launches`` calls over distinct inputs and
+    positions): RMSNorm over hidden 4096; the residual add fused with RMSNorm;
+    per-head q/k RMSNorm + RoPE (32 query and 8 KV heads of 128, theta 1e6,
+    positions uniform in [0, 4095]) with the value copied into its cache slot,
+    one launch.  Beside each: the HF eager ops they replace (Qwen3RMSNorm's
+    arithmetic, q_norm / k_norm + apply_rotary_pos_emb), graph-captured the same
+    way, and the largest ulp distance between the two outputs."""
+    import torch
+    from transformers.models.qwen3.modeling_qwen3 import Qwen3RotaryEmbedding, apply_rotary_pos_emb
+
+    from marlin_style_fluxbin_amd import _lib
+    from marlin_style_fluxbin_amd.fused_modules import add_rms_norm, head_norm_rope, rms_norm, rms_norm_reference
+    from marlin_style_fluxbin_amd.qwen3 import qwen3_config
+
+    g = torch.Generator(device=device).manual_seed(seed)
+    bf = torch.bfloat16
+    eps = 1e-6
+
+    def bf16_ulps(a, b):
+        ia = a.contiguous().view(torch.int16).int()
+        ib = b.contiguous().view(torch.int16).int()
+        ia = torch.where(ia < 0, -32768 - ia, ia)  # sign-magnitude -> ordered integers
+        ib = torch.where(ib < 0, -32768 - ib, ib)
+        return int((ia - ib).abs().max())
+
+    def timed(fn):
+        graph = capture(fn, stream)
+        us = time_graph(graph, steps, warmup, stream) * 1000 / launches
+        del graph
+        return round(us, 3)
+
+    # RMSNorm and residual add + RMSNorm, hidden 4096
+    xs = [torch.randn(1, 4096, device=device, generator=g).to(bf) for _ in range(launches)]
+    res = [torch.randn(1, 4096, device=device, generator=g).to(bf) for _ in range(launches)]
+    w = (1 + 0.02 * torch.randn(4096, device=device, generator=g)).to(bf)
+    outs = [torch.empty_like(x) for x in xs]
+    res_out = [torch.empty_like(x) for x in xs]
+    ref_outs = [torch.empty_like(x) for x in xs]
+
+    def norm_fused():
+        for x, o in zip(xs, outs):
+            rms_norm(x, w, eps, out=o)
+
+    def norm_eager():
+        for x, o in zip(xs, ref_outs):
+            o.copy_(rms_norm_reference(x, w, eps))
+
+    def add_norm_fused():
+        for x, r, o, ro in zip(xs, res, outs, res_out):
+            add_rms_norm(x, r, w, eps, out=o, residual_out=ro)
+
+    def add_norm_eager():
+        for x, r, o, ro in zip(xs, res, ref_outs, res_out):
+            ro.copy_(x + r)
+            o.copy_(rms_norm_reference(ro, w, eps))
+
+    result = {"rmsnorm_4096": {"fused_us": timed(norm_fused), "hf_eager_us": timed(norm_eager)}}
+    norm_fused()
+    norm_eager()
+    torch.cuda.synchronize()
+    result["rmsnorm_4096"]["max_ulps_vs_hf"] = max(bf16_ulps(a, b) for a, b in zip(outs, ref_outs))
+    result["add_rmsnorm_4096"] = {"fused_us": timed(add_norm_fused), "hf_eager_us": timed(add_norm_eager)}
+    add_norm_fused()
+    fused_add = [o.clone() for o in outs]
+    add_norm_eager()
+    torch.cuda.synchronize()
+    result["add_rmsnorm_4096"]["max_ulps_vs_hf"] = max(bf16_ulps(a, b) for a, b in zip(fused_add, ref_outs))
+
+    # per-head q/k RMSNorm + RoPE (+ v into its cache slot), HF's rotary rows
+    config = qwen3_config()
+    rotary = Qwen3RotaryEmbedding(config=config).to(device)
+    positions = torch.randint(0, 4096, (launches,), device=device, generator=g)
+    cos, sin = rotary(xs[0], positions[None])  # [1, launches, 128] in bf16
+    cos, sin = cos[0].contiguous(), sin[0].contiguous()
+    qs = [torch.randn(32, 128, device=device, generator=g).to(bf) for _ in range(launches)]
+    ks = [torch.randn(8, 128, device=device, generator=g).to(bf) for _ in range(launches)]
+    vs = [torch.randn(8, 128, device=device, generator=g).to(bf) for _ in range(launches)]
+    qw = (1 + 0.02 * torch.randn(128, device=device, generator=g)).to(bf)
+    kw = (1 + 0.02 * torch.randn(128, device=device, generator=g)).to(bf)
+    q_out = [torch.empty_like(q) for q in qs]
+    k_cache = torch.zeros(8, launches, 128, device=device, dtype=bf)
+    v_cache = torch.zeros(8, launches, 128, device=device, dtype=bf)
+    q_ref = [torch.empty_like(q) for q in qs]
+    k_ref = torch.zeros_like(k_cache)
+    v_ref = torch.zeros_like(v_cache)
+    strides = dict(in_strides=(0, 128, 0))
+
+    def rope_fused():
+        for i in range(launches):
+            head_norm_rope([
+                dict(x=qs[i], out=q_out[i], weight=qw, heads=32, rope=True, out_strides=(0, 128, 0), **strides),
+                dict(x=ks[i], out=k_cache[:, i], weight=kw, heads=8, rope=True,
+                     out_strides=(0, launches * 128, 0), **strides),
+                dict(x=vs[i], out=v_cache[:, i], weight=None, heads=8, rope=False,
+                     out_strides=(0, launches * 128, 0), **strides),
+            ], cos=cos[i], sin=sin[i], eps=eps, rope_mode=_lib.ROPE_STOCK)
+
+    def rope_eager():
+        for i in range(launches):
+            qn = rms_norm_reference(qs[i], qw, eps)[None, :, None]  # [1, 32, 1, 128]
+            kn = rms_norm_reference(ks[i], kw, eps)[None, :, None]
+            qr, kr = apply_rotary_pos_emb(qn, kn, cos[i][None, None], sin[i][None, None])
+            q_ref[i].copy_(qr[0, :, 0])
+            k_ref[:, i].copy_(kr[0, :, 0])
+            v_ref[:, i].copy_(vs[i])
+
+    result["qk_norm_rope_32q_8kv"] = {"fused_us": timed(rope_fused), "hf_eager_us": timed(rope_eager)}
+    rope_fused()
+    rope_eager()
+    torch.cuda.synchronize()
+    result["qk_norm_rope_32q_8kv"]["max_ulps_vs_hf"] = max(
+        max(bf16_ulps(a, b) for a, b in zip(q_out, q_ref)), bf16_ulps(k_cache, k_ref))
+    result["qk_norm_rope_32q_8kv"]["v_slots_equal"] = bool(torch.equal(v_cache, v_ref))
+    result["note"] = ("launch-bound: each call moves under 25 KB; the fused launch replaces the eager ops' "
+                      "kernels (the norm in the decode graph is further folded into the GEMV staging)")
+    return result
 
 
 def two_base_bench(device, steps, warmup, stream, o=12288, k=4096, salient=32, min_bytes=640e6):
@@ -787,6 +912,8 @@ def main():
     parser.add_argument("--decode-layers", type=int, default=36)
     parser.add_argument("--no-decode", action="store_true", help="skip the config-3 decode benchmark")
     parser.add_argument("--no-two-base", action="store_true", help="skip the config-4 two-base benchmark")
+    parser.add_argument("--no-fused-ops", action="store_true", help="skip the config-2 fused-ops benchmark")
+    parser.add_argument("--fused-ops", action="store_true", help="run only the config-2 fused-ops benchmark")
     parser.add_argument("--summarize-pmc", nargs="+", metavar="CSV",
                         help="rocprofv3 counter CSVs -> profiles/w3_mfma_traffic.json")
     parser.add_argument("--summarize-trace", nargs=2, metavar=("CSV", "LAST"),
@@ -806,6 +933,12 @@ def main():
         return
     if args.decode:
         print(json.dumps(decode_bench(layers=args.decode_layers)), flush=True)
+        return
+    if args.fused_ops:
+        import torch
+
+        device = torch.device("cuda:0")
+        print(json.dumps(fused_ops_bench(device, args.steps, args.warmup, torch.cuda.Stream(device))), flush=True)
         return
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -936,6 +1069,9 @@ def main():
             "kernel": f"w3_mfma_kernel on the field layout (fx_w3_gemv_fields) at gate/up "
                       f"{dominant['O']}x{dominant['K']}, M=1, same payloads repacked once",
         }
+    if not args.no_fused_ops:
+        result["config"]["fused_ops"] = fused_ops_bench(device, max(args.steps, 10), args.warmup, stream)
+        print(f"# fused ops (config 2): {result['config']['fused_ops']}", file=sys.stderr, flush=True)
     if not args.no_two_base:
         result["config"]["two_base"] = two_base_bench(device, max(args.steps, 10), args.warmup, stream)
         print(f"# two-base: {result['config']['two_base']}", file=sys.stderr, flush=True)
