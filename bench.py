@@ -909,6 +909,8 @@ def main():
     parser.add_argument("--decode", action="store_true", help="run only the config-3 decode benchmark")
     parser.add_argument("--decode-native", action="store_true",
                         help="run only the config-3 W3 native decode arm (the kernel-trace workload)")
+    parser.add_argument("--decode-hybrid", action="store_true",
+                        help="run only the config-3 architecture with hybrid two-base Linears, native chain")
     parser.add_argument("--decode-layers", type=int, default=36)
     parser.add_argument("--no-decode", action="store_true", help="skip the config-3 decode benchmark")
     parser.add_argument("--no-two-base", action="store_true", help="skip the config-4 two-base benchmark")
@@ -930,6 +932,9 @@ def main():
         return
     if args.decode_native:
         print(json.dumps(decode_native_only(layers=args.decode_layers)), flush=True)
+        return
+    if args.decode_hybrid:
+        print(json.dumps(decode_hybrid_native(layers=args.decode_layers)), flush=True)
         return
     if args.decode:
         print(json.dumps(decode_bench(layers=args.decode_layers)), flush=True)

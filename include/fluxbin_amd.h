@@ -330,6 +330,23 @@ int fx_hybrid_gemv(const void *x, int x_dtype, const uint8_t *codes, const float
                    const float *columns, const int16_t *indices, const uint8_t *sparse_codes,
                    const float *sparse_rows, const float *sparse_columns, void *workspace,
                    size_t workspace_bytes, void *out, int O, int K, void *stream);
+/*
+ * fx_hybrid_gemv over n_segments (1..4) layouts that read the same activation,
+ * in one launch: no single reference entry point; it replaces the reference
+ * decode's separate m1_out calls for q_proj, k_proj, v_proj (or gate_proj,
+ * up_proj) (deployment.py:168-179) and gives each row the bits of its own
+ * fx_hybrid_gemv call.  codes, rows, sparse_codes and sparse_rows are the
+ * segments' arrays concatenated along O ([G, O_total, ...]); columns, indices
+ * and sparse_columns hold one pointer per segment (its [G, 128, 2], [G, 8],
+ * [G, 8, 2] arrays); segment_rows[s] is segment s's row count, a multiple of 16
+ * when n_segments > 1; out [O_total], O_total = sum of segment_rows (<= 65536).
+ * Workspace as fx_hybrid_gemv_workspace_bytes(O_total, K).
+ */
+int fx_hybrid_gemv_segments(const void *x, int x_dtype, int n_segments, const int *segment_rows,
+                            const uint8_t *codes, const float *rows, const float *const *columns,
+                            const int16_t *const *indices, const uint8_t *sparse_codes, const float *sparse_rows,
+                            const float *const *sparse_columns, void *workspace, size_t workspace_bytes, void *out,
+                            int K, void *stream);
 
 #ifdef __cplusplus
 }

@@ -405,11 +405,11 @@ int run_rank_one(const void* x, int x_dtype, const uint8_t* planes, const void* 
 
 // Hybrid layout: the rank-one tiling rules with a smaller staging cap (3.3 KB of
 // LDS per batch) and at most `max_splits` K splits (the caller's workspace).
-TwoBasePlan default_hybrid_plan(int O, int G, int max_splits) {
+TwoBasePlan default_hybrid_plan(int O, int G, int max_splits, int max_tiles = 3) {
   const int cus = device_cu_count();
   const int tiles_total = (O + 15) / 16;
   int nt = tiles_total / cus;
-  nt = nt < 1 ? 1 : (nt > 3 ? 3 : nt);
+  nt = nt < 1 ? 1 : (nt > max_tiles ? max_tiles : nt);
   const int row_blocks = (tiles_total + nt - 1) / nt;
   const int batches = (G + 3) / 4;
   int splits = 1;
@@ -437,23 +437,46 @@ TwoBasePlan default_hybrid_plan(int O, int G, int max_splits) {
   return p;
 }
 
-int run_hybrid(const void* x, int x_dtype, const uint8_t* codes, const float* rows, const float* cols,
-               const int16_t* idx, const uint8_t* scodes, const float* srows, const float* scols,
-               void* workspace, size_t workspace_bytes, void* out, int O, int K, hipStream_t s) {
-  if (!x || !codes || !rows || !cols || !idx || !scodes || !srows || !scols || !out)
+// One launch over n_seg layouts concatenated along O (n_seg = 1: one layout).
+int run_hybrid(const void* x, int x_dtype, int n_seg, const int* seg_rows, const uint8_t* codes, const float* rows,
+               const float* const* cols, const int16_t* const* idx, const uint8_t* scodes, const float* srows,
+               const float* const* scols, void* workspace, size_t workspace_bytes, void* out, int K,
+               hipStream_t s) {
+  if (n_seg < 1 || n_seg > fx::kHybridMaxSegments)
+    return fail(FX_EINVAL, "n_segments must be in [1, %d], got %d", fx::kHybridMaxSegments, n_seg);
+  if (!seg_rows || !cols || !idx || !scols) return fail(FX_EINVAL, "segment arrays must be non-null");
+  long total = 0;
+  for (int i = 0; i < n_seg; ++i) {
+    if (seg_rows[i] < 1) return fail(FX_EINVAL, "segment %d has %d rows", i, seg_rows[i]);
+    if (n_seg > 1 && seg_rows[i] % 16)
+      return fail(FX_EINVAL, "segment %d has %d rows: concatenated segments must be multiples of 16", i,
+                  seg_rows[i]);
+    if (!cols[i] || !idx[i] || !scols[i]) return fail(FX_EINVAL, "segment %d: columns, indices and sparse columns "
+                                                      "must be non-null", i);
+    if (reinterpret_cast<uintptr_t>(cols[i]) % 16) return fail(FX_EINVAL, "segment %d: columns must be 16-byte "
+                                                                "aligned", i);
+    total += seg_rows[i];
+  }
+  if (total > 65536) return fail(FX_EINVAL, "O must be in [1, 65536], got %ld", total);
+  const int O = int(total);
+  if (!x || !codes || !rows || !scodes || !srows || !out)
     return fail(FX_EINVAL, "x, every layout field and out must be non-null");
   if (!is_half_dtype(x_dtype)) return fail(FX_EINVAL, "x dtype must be fp16 or bf16");
-  if (O < 1 || O > 65536) return fail(FX_EINVAL, "O must be in [1, 65536], got %d", O);
   if (K < 128 || K % 128 != 0 || K > 131072)
     return fail(FX_EINVAL, "K must be a multiple of 128 in [128, 131072], got %d", K);
   if (reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(codes) % 16 ||
-      reinterpret_cast<uintptr_t>(cols) % 16 || reinterpret_cast<uintptr_t>(rows) % 16 ||
-      reinterpret_cast<uintptr_t>(srows) % 16)
+      reinterpret_cast<uintptr_t>(rows) % 16 || reinterpret_cast<uintptr_t>(srows) % 16)
     return fail(FX_EINVAL, "x, codes, rows, columns and sparse rows must be 16-byte aligned");
   const int G = K / 128;
   if (size_t(G) * size_t(O) * 32 > 0x7fffffffu) return fail(FX_EINVAL, "payload exceeds 2 GiB");
   const int max_splits = int(std::min<size_t>(workspace ? workspace_bytes / (size_t(O) * 4) : 0, 1 << 20));
-  const TwoBasePlan p = default_hybrid_plan(O, G, max_splits < 1 ? 1 : max_splits);
+  TwoBasePlan p = default_hybrid_plan(O, G, max_splits < 1 ? 1 : max_splits);
+  // a workgroup's rows must lie in one segment: starts on its 16 * tiles grid
+  for (int i = 1, start = seg_rows[0]; i < n_seg; start += seg_rows[i], ++i)
+    if (start % (16 * p.nt)) {
+      p = default_hybrid_plan(O, G, max_splits < 1 ? 1 : max_splits, 1);
+      break;
+    }
   const size_t need = two_base_workspace(O, p);
   if (need > 0) {
     if (!workspace || workspace_bytes < need)
@@ -461,21 +484,30 @@ int run_hybrid(const void* x, int x_dtype, const uint8_t* codes, const float* ro
     if (reinterpret_cast<uintptr_t>(workspace) % 16 != 0)
       return fail(FX_EINVAL, "workspace must be 16-byte aligned");
   }
-  fx::HybridArgs a;
+  fx::HybridArgs a{};
   a.x = static_cast<const uint16_t*>(x);
   a.codes = codes;
   a.rows = rows;
-  a.cols = cols;
-  a.idx = idx;
+  a.cols = cols[0];
+  a.idx = idx[0];
   a.scodes = scodes;
   a.srows = srows;
-  a.scols = scols;
+  a.scols = scols[0];
   a.partial = p.splits > 1 ? static_cast<float*>(workspace) : nullptr;
   a.out = static_cast<uint16_t*>(out);
   a.O = O;
   a.G = G;
   a.gps = p.gps;
   a.row_blocks = p.row_blocks;
+  a.nseg = n_seg;
+  for (int i = 0, start = 0; i < fx::kHybridMaxSegments; ++i) {
+    const bool used = i < n_seg;
+    a.seg_start[i] = used ? start : O;
+    a.seg_cols[i] = used ? cols[i] : cols[0];
+    a.seg_idx[i] = used ? idx[i] : idx[0];
+    a.seg_scols[i] = used ? scols[i] : scols[0];
+    if (used) start += seg_rows[i];
+  }
   if (!fx::dispatch_hybrid(x_dtype, p.nt, p.nk, a, dim3(p.row_blocks, p.splits), s))
     return fail(FX_EINVAL, "no hybrid kernel for tiles %d kparts %d", p.nt, p.nk);
   int rc = check_launch("hybrid_kernel");
@@ -497,7 +529,7 @@ bool two_base_config(int O, int G, int waves, int prefetch, int groups_per_split
 
 extern "C" {
 
-int fx_abi_version(void) { return 11; }
+int fx_abi_version(void) { return 12; }
 
 const char* fx_last_error(void) { return g_error; }
 
@@ -1108,8 +1140,20 @@ int fx_hybrid_gemv(const void* x, int x_dtype, const uint8_t* codes, const float
                    const float* columns, const int16_t* indices, const uint8_t* sparse_codes,
                    const float* sparse_rows, const float* sparse_columns, void* workspace,
                    size_t workspace_bytes, void* out, int O, int K, void* stream) {
-  return run_hybrid(x, x_dtype, codes, rows, columns, indices, sparse_codes, sparse_rows, sparse_columns,
-                    workspace, workspace_bytes, out, O, K, static_cast<hipStream_t>(stream));
+  if (O < 1 || O > 65536) return fail(FX_EINVAL, "O must be in [1, 65536], got %d", O);
+  if (!columns || !indices || !sparse_columns)
+    return fail(FX_EINVAL, "x, every layout field and out must be non-null");
+  return run_hybrid(x, x_dtype, 1, &O, codes, rows, &columns, &indices, sparse_codes, sparse_rows, &sparse_columns,
+                    workspace, workspace_bytes, out, K, static_cast<hipStream_t>(stream));
+}
+
+int fx_hybrid_gemv_segments(const void* x, int x_dtype, int n_segments, const int* segment_rows,
+                            const uint8_t* codes, const float* rows, const float* const* columns,
+                            const int16_t* const* indices, const uint8_t* sparse_codes, const float* sparse_rows,
+                            const float* const* sparse_columns, void* workspace, size_t workspace_bytes, void* out,
+                            int K, void* stream) {
+  return run_hybrid(x, x_dtype, n_segments, segment_rows, codes, rows, columns, indices, sparse_codes, sparse_rows,
+                    sparse_columns, workspace, workspace_bytes, out, K, static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

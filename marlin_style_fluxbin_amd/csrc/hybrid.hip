@@ -25,6 +25,12 @@
 //   exponents.  A refinement index outside [0, 128) makes the output NaN (its U
 //   is NaN), as the reference's lookup does.
 //
+// Several layouts that read the same x (q|k|v, gate|up) can run as one launch:
+// their row-side arrays concatenated along O, their column-side arrays (column
+// scales, refinement indices and refinement column scales) one per segment; a
+// workgroup takes its segment's from the segment table.  Every row is computed
+// as in a launch of its own layout.
+//
 // Work split as in the rank-one kernel: a workgroup owns NT 16-row tiles and a K
 // range; wave w stages batches w, w + NW, ... (one 8-column unit per lane and
 // base, the refinement columns one per lane); after one barrier wave (tile,
@@ -64,11 +70,28 @@ __global__ __launch_bounds__(NT * NK * 64) void hybrid_kernel(HybridArgs a) {
   __shared__ float red[NK][16 * NT];
   // one scalar-load round for every argument, before any branch
   asm volatile("" ::"s"(a.x), "s"(a.codes), "s"(a.rows), "s"(a.cols), "s"(a.idx), "s"(a.scodes), "s"(a.srows),
-               "s"(a.scols), "s"(a.partial), "s"(a.out), "s"(a.O), "s"(a.G), "s"(a.gps), "s"(a.row_blocks));
+               "s"(a.scols), "s"(a.partial), "s"(a.out), "s"(a.O), "s"(a.G), "s"(a.gps), "s"(a.row_blocks),
+               "s"(a.nseg));
+  asm volatile("" ::"s"(a.seg_start[1]), "s"(a.seg_start[2]), "s"(a.seg_start[3]), "s"(a.seg_cols[1]),
+               "s"(a.seg_cols[2]), "s"(a.seg_cols[3]), "s"(a.seg_idx[1]), "s"(a.seg_idx[2]), "s"(a.seg_idx[3]),
+               "s"(a.seg_scols[1]), "s"(a.seg_scols[2]), "s"(a.seg_scols[3]));
   const int t = threadIdx.x, lane = t & 63, wave = wave_index();
   const int O = a.O, G = a.G, K = G * 128;
   const int split = blockIdx.y;
   const int row0 = xcd_local_index8(blockIdx.x, a.row_blocks) * (16 * NT);
+  // the workgroup's segment: scalar selects over the segment table (no indexing
+  // into the argument array, which would be a second scalar load round)
+  const float* cols = a.cols;
+  const int16_t* idxp = a.idx;
+  const float* scols = a.scols;
+#pragma unroll
+  for (int s = 1; s < kHybridMaxSegments; ++s) {
+    if (s < a.nseg && row0 >= a.seg_start[s]) {
+      cols = a.seg_cols[s];
+      idxp = a.seg_idx[s];
+      scols = a.seg_scols[s];
+    }
+  }
   const int g0 = split * a.gps;
   const int g1 = min(G, g0 + a.gps);
   const int nbatch = (g1 - g0 + 3) >> 2;
@@ -78,9 +101,9 @@ __global__ __launch_bounds__(NT * NK * 64) void hybrid_kernel(HybridArgs a) {
   u32x4_t* xs = reinterpret_cast<u32x4_t*>(rslot + size_t(maxb) * 256);  // [batch][64 units]
 
   const auto rx = buffer_resource(a.x, size_t(K) * 2);
-  const auto rcol = buffer_resource(a.cols, size_t(G) * 128 * 2 * 4);
-  const auto ridx = buffer_resource(a.idx, size_t(G) * 8 * 2);
-  const auto rscol = buffer_resource(a.scols, size_t(G) * 8 * 2 * 4);
+  const auto rcol = buffer_resource(cols, size_t(G) * 128 * 2 * 4);
+  const auto ridx = buffer_resource(idxp, size_t(G) * 8 * 2);
+  const auto rscol = buffer_resource(scols, size_t(G) * 8 * 2 * 4);
   const auto rp = buffer_resource(a.codes, size_t(G) * O * 32);
   const auto rsp = buffer_resource(a.scodes, size_t(G) * O * 2);
   const auto rrow = buffer_resource(a.rows, size_t(G) * O * 2 * 4);

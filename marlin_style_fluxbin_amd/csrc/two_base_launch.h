@@ -42,19 +42,29 @@ namespace fx {
 //   y[o] = sum_g sum_b rows[g,o,b] (B_b[o, g, :] . (x_g * cols[g, :, b]))
 //        + sum_g sum_b srows[g,o,b] (R_b[o, g, :] . (x[128 g + idx[g, :]] * scols[g, :, b]))
 // with B, R in {-1, +1} stored as bits (1 = +1).
+constexpr int kHybridMaxSegments = 4;  // layouts one launch may concatenate along O (q|k|v, gate|up)
+
 struct HybridArgs {
   const uint16_t* x;       // [K] activations (fp16 / bf16)
   const uint8_t* codes;    // [G, O, 2, 16]: bit j of byte c of base b = column 8 c + j
   const float* rows;       // [G, O, 2]
-  const float* cols;       // [G, 128, 2]
-  const int16_t* idx;      // [G, 8] refinement columns inside each group
+  const float* cols;       // [G, 128, 2]        of segment 0
+  const int16_t* idx;      // [G, 8] refinement columns inside each group, segment 0
   const uint8_t* scodes;   // [G, O, 2, 1]: bit j = refinement column j
   const float* srows;      // [G, O, 2]
-  const float* scols;      // [G, 8, 2]
+  const float* scols;      // [G, 8, 2]          of segment 0
   float* partial;          // null: write out directly (single K split)
   uint16_t* out;           // [O]
   int O, G, gps;
   int row_blocks;  // ceil(O / (16 * tiles)); the grid is (row_blocks, K splits)
+  // Rows [seg_start[s], seg_start[s + 1]) use segment s's column-side arrays
+  // (segment 0: cols / idx / scols above); every start is a multiple of the
+  // workgroup's 16 * tiles rows, so a workgroup lies in one segment.
+  int nseg;
+  int seg_start[kHybridMaxSegments];
+  const float* seg_cols[kHybridMaxSegments];
+  const int16_t* seg_idx[kHybridMaxSegments];
+  const float* seg_scols[kHybridMaxSegments];
 };
 
 constexpr int kHybridMaxBatches = 36;  // four-group batches one workgroup stages (117 KB LDS)

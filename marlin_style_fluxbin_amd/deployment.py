@@ -355,6 +355,76 @@ class PackedHybridLinear(PackedLinearBase):
         return run
 
 
+class HybridSegmentsGemv:
+    """Hybrid Linears that read the same activation (a decoder layer's q|k|v or
+    gate|up) as one launch, ``fx_hybrid_gemv_segments``: the modules' codes, row
+    scales, refinement codes and refinement row scales are concatenated along O
+    once here; their column scales, refinement indices and refinement column
+    scales stay per module.  ``out`` is ``[1, sum(out_features)]``, the modules'
+    outputs side by side, each row with the bits of its module's own call.
+    Raises ``ValueError`` unless 1..4 GPU modules share ``in_features``, carry no
+    bias, and (for several) have row counts that are multiples of 16."""
+
+    MAX_SEGMENTS = 4
+
+    def __init__(self, modules):
+        import ctypes
+
+        modules = list(modules)
+        if not 1 <= len(modules) <= self.MAX_SEGMENTS:
+            raise ValueError(f"1..{self.MAX_SEGMENTS} hybrid Linears per launch, got {len(modules)}")
+        if not all(isinstance(m, PackedHybridLinear) for m in modules):
+            raise ValueError("every module must be a PackedHybridLinear")
+        first = modules[0]
+        device = first.codes.device
+        if device.type != "cuda":
+            raise ValueError("fused hybrid GEMV runs on a GPU")
+        if any(m.in_features != first.in_features or m.bias is not None or m.codes.device != device
+               for m in modules):
+            raise ValueError("fused hybrid Linears need one in_features, one device and no bias")
+        if len(modules) > 1 and any(m.out_features % 16 for m in modules):
+            raise ValueError("concatenated hybrid Linears need row counts that are multiples of 16")
+        for m in modules:
+            m._check_before_call()
+
+        def planar(m, name):
+            copy = getattr(m, f"_{name}_planar")
+            return getattr(m, name) if copy is None else copy
+
+        self.in_features = first.in_features
+        self.out_features = sum(m.out_features for m in modules)
+        self.codes = torch.cat([planar(m, "codes") for m in modules], dim=1).contiguous()
+        self.rows = torch.cat([m.rows for m in modules], dim=1).contiguous()
+        self.sparse_codes = torch.cat([planar(m, "sparse_codes") for m in modules], dim=1).contiguous()
+        self.sparse_rows = torch.cat([m.sparse_rows for m in modules], dim=1).contiguous()
+        self._columns = [m.columns.contiguous() for m in modules]
+        self._indices = [HybridExtension._sorted_columns(m.indices) for m in modules]
+        self._sparse_columns = [m.sparse_columns.contiguous() for m in modules]
+        n = len(modules)
+        vp = ctypes.c_void_p
+        self._n = n
+        self._segment_rows = (ctypes.c_int * n)(*[m.out_features for m in modules])
+        self._cols_ptrs = (vp * n)(*[t.data_ptr() for t in self._columns])
+        self._idx_ptrs = (vp * n)(*[t.data_ptr() for t in self._indices])
+        self._scols_ptrs = (vp * n)(*[t.data_ptr() for t in self._sparse_columns])
+        self.lib = _lib.library()
+        nbytes = self.lib.fx_hybrid_gemv_workspace_bytes(self.out_features, self.in_features)
+        self.workspace = torch.empty(max(nbytes, 4) // 4, dtype=torch.float32, device=device) if nbytes else None
+        self._workspace_view = (self.workspace if self.workspace is not None
+                                else torch.empty(0, dtype=torch.float32, device=device))
+
+    def __call__(self, x: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
+        _check_m1_args(x, out, self._workspace_view, self.out_features, self.in_features)
+        ws = self.workspace
+        _lib.check(self.lib.fx_hybrid_gemv_segments(
+            x.data_ptr(), _lib.dtype_code(x.dtype), self._n, self._segment_rows, self.codes.data_ptr(),
+            self.rows.data_ptr(), self._cols_ptrs, self._idx_ptrs, self.sparse_codes.data_ptr(),
+            self.sparse_rows.data_ptr(), self._scols_ptrs, None if ws is None else ws.data_ptr(),
+            0 if ws is None else ws.numel() * 4, out.data_ptr(), self.in_features, _lib.stream_handle(x.device)),
+            "fx_hybrid_gemv_segments")
+        return out
+
+
 def replace_block_linears(block, layer_payload, *, fallback="error", groups_per_split=8, kernel="v1"):
     """Replace the seven Qwen3 Linears of one block; every payload is validated and
     every replacement built before the block is touched."""

@@ -31,7 +31,7 @@ import torch
 from . import _lib
 from .fused_modules import add_rms_norm
 from .static_decode import graph_kernel_count
-from .deployment import PackedHybridLinear
+from .deployment import HybridSegmentsGemv, PackedHybridLinear
 from .w3_lut_deployment import PackedW3Linear, W3Gemv
 
 _ATTN = ("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj", "self_attn.o_proj")
@@ -69,7 +69,8 @@ class _FusedLinear:
     """Linears that read the same activation, run as one GEMV over their
     concatenated rows (q|k|v, gate|up): one launch instead of several.  W3 payloads
     concatenate along O when K, arithmetic, scale dtype, zero-point presence and
-    the column permutation agree; dense weights concatenate along O.  Each output
+    the column permutation agree; hybrid two-base payloads run as one
+    ``fx_hybrid_gemv_segments`` launch; dense weights concatenate along O.  Each output
     row is computed exactly as it would be alone, so the outputs are bit-identical
     to separate calls.  ``None`` from :meth:`build` when the modules do not fuse."""
 
@@ -94,6 +95,12 @@ class _FusedLinear:
             if "zeros" in first:
                 fused["zeros"] = torch.cat([l["zeros"] for l in layouts], dim=1).contiguous()
             gemv = W3Gemv(fused, arithmetic=modules[0].arithmetic)
+            return _FusedLinear(gemv, [m.out_features for m in modules])
+        if all(isinstance(m, PackedHybridLinear) for m in modules):
+            try:
+                gemv = HybridSegmentsGemv(modules)
+            except ValueError:
+                return None
             return _FusedLinear(gemv, [m.out_features for m in modules])
         if all(type(m) is torch.nn.Linear for m in modules) and all(m.bias is None for m in modules):
             weight = torch.cat([m.weight for m in modules], dim=0).contiguous()

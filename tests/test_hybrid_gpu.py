@@ -181,3 +181,58 @@ def test_out_of_range_refinement_index_gives_nan(gpu):
     layout["indices"][1, 5] = -3
     d.m1_out(x, layout, y, ws, kernel="v5_p1024")
     assert torch.isnan(y.float()).all()
+
+
+@pytest.mark.parametrize("widths,g", [((64, 32, 32), 3), ((4096, 1024, 1024), 32), ((12288, 12288), 32),
+                                      ((48,), 5), ((16, 48, 32, 64), 2)])
+def test_segments_launch_equals_separate_calls(gpu, widths, g):
+    """q|k|v / gate|up as one fx_hybrid_gemv_segments launch: every row has the bits
+    of its own module's fx_hybrid_gemv call (segment starts that do not sit on the
+    tall-tile grid, 48 | 16-multiples, fall back to 16-row tiles)."""
+    modules = [d.PackedHybridLinear(_payload(o, g, seed=31 + i), kernel="v5_p1024").to(gpu)
+               for i, o in enumerate(widths)]
+    x = torch.randn(1, g * 128, generator=torch.Generator().manual_seed(4)).to(torch.bfloat16).to(gpu)
+    fused = d.HybridSegmentsGemv(modules)
+    out = torch.full((1, sum(widths)), float("nan"), dtype=torch.bfloat16, device=gpu)
+    fused(x, out)
+    want = []
+    with torch.inference_mode():
+        for m in modules:
+            y = torch.empty(1, m.out_features, dtype=torch.bfloat16, device=gpu)
+            m._packed_kernel(1, gpu)(x, y)
+            want.append(y)
+    assert torch.equal(out, torch.cat(want, 1))
+    # graph replay of the fused launch, twice, against the eager result
+    graph = torch.cuda.CUDAGraph()
+    replay = torch.empty_like(out)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        fused(x, replay)
+    torch.cuda.current_stream().wait_stream(stream)
+    with torch.cuda.graph(graph, stream=stream):
+        fused(x, replay)
+    for _ in range(2):
+        replay.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(replay, out)
+
+
+def test_segments_argument_checks(gpu):
+    from marlin_style_fluxbin_amd import _lib
+
+    a = d.PackedHybridLinear(_payload(40, 2, seed=1), kernel="v5_p1024").to(gpu)
+    b = d.PackedHybridLinear(_payload(32, 2, seed=2), kernel="v5_p1024").to(gpu)
+    with pytest.raises(ValueError, match="multiples of 16"):
+        d.HybridSegmentsGemv([a, b])
+    c = d.PackedHybridLinear(_payload(32, 3, seed=3), kernel="v5_p1024").to(gpu)
+    with pytest.raises(ValueError, match="in_features"):
+        d.HybridSegmentsGemv([b, c])
+    with pytest.raises(ValueError, match="1..4"):
+        d.HybridSegmentsGemv([b] * 5)
+    lib = _lib.library()
+    rows = (__import__("ctypes").c_int * 1)(32)
+    rc = lib.fx_hybrid_gemv_segments(None, 2, 0, rows, None, None, None, None, None, None, None, None, 0, None,
+                                     256, None)
+    assert rc == 1 and b"n_segments" in lib.fx_last_error()  # FX_EINVAL
