@@ -255,7 +255,7 @@ int fx_decode_attention_rope(const void *q, const void *k, const void *v, const 
 int fx_silu_mul(const void *gate, const void *up, void *out, int n, int dtype, void *stream);
 
 /*
- * End of a greedy decode step in one launch: the final RMSNorm, the LM head and
+ * End of a greedy decode step: the final RMSNorm, the LM head and
  * the argmax that the reference's decode runs as model.norm, lm_head and
  * logits.argmax(-1, keepdim=True) (static_decode.py:67-76).
  *   x = round(norm_weight * round(hidden * rsqrt(mean(hidden^2) + eps)))
@@ -276,6 +276,32 @@ size_t fx_lm_head_argmax_workspace_bytes(void);
 int fx_lm_head_argmax(const void *hidden, const void *norm_weight, float eps, const void *weight, void *logits,
                       long long *prediction, void *workspace, size_t workspace_bytes, int vocab,
                       int hidden_size, int dtype, void *stream);
+/*
+ * fx_lm_head_argmax's two launches one at a time (no reference counterpart: the
+ * decode chain splits them so the merge can ride in the next step's first
+ * launch).  fx_lm_head_logits: the streaming launch (logits, and the
+ * per-workgroup maxima left in `workspace`).  fx_lm_head_merge: their merge into
+ * *prediction; `vocab` must be the one the streaming call was given (it fixes
+ * how many maxima there are).  Together bit-identical to fx_lm_head_argmax.
+ */
+int fx_lm_head_logits(const void *hidden, const void *norm_weight, float eps, const void *weight, void *logits,
+                      void *workspace, size_t workspace_bytes, int vocab, int hidden_size, int dtype, void *stream);
+int fx_lm_head_merge(void *workspace, size_t workspace_bytes, int vocab, long long *prediction, void *stream);
+
+/*
+ * Start of a decode step (no single reference counterpart: it replaces the
+ * embedding lookup of the step's token and the first decoder layer's
+ * input RMSNorm statistics, static_decode.py:67-76 / HF Qwen3Model.forward).  One
+ * workgroup: out [hidden] = table[*token] (row-major [vocab, hidden], bit copy),
+ * tile_sumsq [hidden / 16] = per 16-element tile the fp32 sum of squares, the
+ * partials fx_w3_gemv_rmsnormed reads; a token outside [0, vocab) writes NaNs.
+ * prediction non-null: also merges the previous step's fx_lm_head_logits maxima
+ * (lm_workspace, lm_vocab) into *prediction, as fx_lm_head_merge does.  hidden a
+ * multiple of 16; table and out 16-byte aligned, token 8-byte aligned.
+ */
+int fx_decode_embed(const long long *token, const void *table, int vocab, int hidden, void *out, float *tile_sumsq,
+                    void *lm_workspace, size_t lm_workspace_bytes, int lm_vocab, long long *prediction, int dtype,
+                    void *stream);
 
 /*
  * Two-base binary-basis GEMV, rank-one format with salient columns, batch 1:

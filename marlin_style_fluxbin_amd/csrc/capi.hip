@@ -529,7 +529,7 @@ bool two_base_config(int O, int G, int waves, int prefetch, int groups_per_split
 
 extern "C" {
 
-int fx_abi_version(void) { return 12; }
+int fx_abi_version(void) { return 13; }
 
 const char* fx_last_error(void) { return g_error; }
 
@@ -1045,43 +1045,108 @@ size_t fx_lm_head_argmax_workspace_bytes(void) {
   return fx::kLmCounterBytes + size_t(fx::kLmMaxBlocks) * (sizeof(float) + sizeof(int));
 }
 
-int fx_lm_head_argmax(const void* hidden, const void* norm_weight, float eps, const void* weight, void* logits,
-                      long long* prediction, void* workspace, size_t workspace_bytes, int vocab,
-                      int hidden_size, int dtype, void* stream) {
-  if (!hidden || !weight || !logits || !prediction || !workspace)
-    return fail(FX_EINVAL, "hidden, weight, logits, prediction and workspace must be non-null");
+namespace {
+// The workspace's partial arrays and the grid of a vocab-row LM head (the same
+// for the streaming launch and a later merge of its partials).
+int lm_head_workspace(void* workspace, size_t workspace_bytes, int vocab, fx::LmHeadArgs* a) {
+  if (!workspace) return fail(FX_EINVAL, "workspace must be non-null");
+  if (reinterpret_cast<uintptr_t>(workspace) % 16 != 0) return fail(FX_EINVAL, "workspace must be 16-byte aligned");
+  const size_t need = fx_lm_head_argmax_workspace_bytes();
+  if (workspace_bytes < need)
+    return fail(FX_EINVAL, "LM-head workspace needs %zu bytes, got %zu", need, workspace_bytes);
+  if (vocab < 1) return fail(FX_EINVAL, "vocab must be positive, got %d", vocab);
+  a->arrival = static_cast<unsigned*>(workspace);
+  a->part_val = reinterpret_cast<float*>(static_cast<char*>(workspace) + fx::kLmCounterBytes);
+  a->part_idx = reinterpret_cast<int*>(a->part_val + fx::kLmMaxBlocks);
+  a->V = vocab;
+  const long groups = (long(vocab) + fx::kLmRowsInFlight - 1) / fx::kLmRowsInFlight;  // one wave's rows at a time
+  a->blocks = int(std::min<long>({long(fx::kLmMaxBlocks), long(kLmBlocksPerCu) * device_cu_count(),
+                                  (groups + fx::kLmWaves - 1) / fx::kLmWaves}));
+  return FX_OK;
+}
+
+int lm_head_args(const void* hidden, const void* norm_weight, float eps, const void* weight, void* logits,
+                 void* workspace, size_t workspace_bytes, int vocab, int hidden_size, int dtype, fx::LmHeadArgs* a) {
+  if (!hidden || !weight || !logits) return fail(FX_EINVAL, "hidden, weight, logits and workspace must be non-null");
   if (!is_half_dtype(dtype)) return fail(FX_EINVAL, "dtype must be fp16 or bf16");
   if (hidden_size < 512 || hidden_size > 512 * fx::kLmMaxChunks || hidden_size % 512)
     return fail(FX_EINVAL, "hidden size must be a multiple of 512 in [512, %d], got %d", 512 * fx::kLmMaxChunks,
                 hidden_size);
-  if (vocab < 1) return fail(FX_EINVAL, "vocab must be positive, got %d", vocab);
   const void* vec[3] = {hidden, norm_weight, weight};
   for (const void* p : vec)
     if (reinterpret_cast<uintptr_t>(p) % 16 != 0)
       return fail(FX_EINVAL, "hidden, norm weight and weight must be 16-byte aligned");
   if (reinterpret_cast<uintptr_t>(logits) % 2 != 0) return fail(FX_EINVAL, "logits must be 2-byte aligned");
+  int rc = lm_head_workspace(workspace, workspace_bytes, vocab, a);
+  if (rc) return rc;
+  a->x = static_cast<const uint16_t*>(hidden);
+  a->norm_w = static_cast<const uint16_t*>(norm_weight);
+  a->eps = eps;
+  a->w = static_cast<const uint16_t*>(weight);
+  a->logits = static_cast<uint16_t*>(logits);
+  a->K = hidden_size;
+  return FX_OK;
+}
+}  // namespace
+
+int fx_lm_head_argmax(const void* hidden, const void* norm_weight, float eps, const void* weight, void* logits,
+                      long long* prediction, void* workspace, size_t workspace_bytes, int vocab,
+                      int hidden_size, int dtype, void* stream) {
+  if (!prediction) return fail(FX_EINVAL, "hidden, weight, logits, prediction and workspace must be non-null");
   if (reinterpret_cast<uintptr_t>(prediction) % 8 != 0) return fail(FX_EINVAL, "prediction must be 8-byte aligned");
-  if (reinterpret_cast<uintptr_t>(workspace) % 16 != 0) return fail(FX_EINVAL, "workspace must be 16-byte aligned");
-  const size_t need = fx_lm_head_argmax_workspace_bytes();
-  if (workspace_bytes < need)
-    return fail(FX_EINVAL, "LM-head workspace needs %zu bytes, got %zu", need, workspace_bytes);
   fx::LmHeadArgs a{};
-  a.x = static_cast<const uint16_t*>(hidden);
-  a.norm_w = static_cast<const uint16_t*>(norm_weight);
-  a.eps = eps;
-  a.w = static_cast<const uint16_t*>(weight);
-  a.logits = static_cast<uint16_t*>(logits);
+  int rc = lm_head_args(hidden, norm_weight, eps, weight, logits, workspace, workspace_bytes, vocab, hidden_size,
+                        dtype, &a);
+  if (rc) return rc;
   a.prediction = prediction;
-  a.arrival = static_cast<unsigned*>(workspace);
-  a.part_val = reinterpret_cast<float*>(static_cast<char*>(workspace) + fx::kLmCounterBytes);
-  a.part_idx = reinterpret_cast<int*>(a.part_val + fx::kLmMaxBlocks);
-  a.V = vocab;
-  a.K = hidden_size;
-  const long groups = (long(vocab) + fx::kLmRowsInFlight - 1) / fx::kLmRowsInFlight;  // one wave's rows at a time
-  a.blocks = int(std::min<long>({long(fx::kLmMaxBlocks), long(kLmBlocksPerCu) * device_cu_count(),
-                                 (groups + fx::kLmWaves - 1) / fx::kLmWaves}));
   fx::launch_lm_head_argmax(dtype, a, static_cast<hipStream_t>(stream));
   return check_launch("lm_head_argmax_kernel");
+}
+
+int fx_lm_head_logits(const void* hidden, const void* norm_weight, float eps, const void* weight, void* logits,
+                      void* workspace, size_t workspace_bytes, int vocab, int hidden_size, int dtype, void* stream) {
+  fx::LmHeadArgs a{};
+  int rc = lm_head_args(hidden, norm_weight, eps, weight, logits, workspace, workspace_bytes, vocab, hidden_size,
+                        dtype, &a);
+  if (rc) return rc;
+  fx::launch_lm_head_partials(dtype, a, static_cast<hipStream_t>(stream));
+  return check_launch("lm_head_argmax_kernel");
+}
+
+int fx_lm_head_merge(void* workspace, size_t workspace_bytes, int vocab, long long* prediction, void* stream) {
+  if (!prediction) return fail(FX_EINVAL, "prediction must be non-null");
+  if (reinterpret_cast<uintptr_t>(prediction) % 8 != 0) return fail(FX_EINVAL, "prediction must be 8-byte aligned");
+  fx::LmHeadArgs a{};
+  int rc = lm_head_workspace(workspace, workspace_bytes, vocab, &a);
+  if (rc) return rc;
+  a.prediction = prediction;
+  fx::launch_lm_head_merge(a, static_cast<hipStream_t>(stream));
+  return check_launch("lm_head_merge_kernel");
+}
+
+int fx_decode_embed(const long long* token, const void* table, int vocab, int hidden, void* out, float* tile_sumsq,
+                    void* lm_workspace, size_t lm_workspace_bytes, int lm_vocab, long long* prediction, int dtype,
+                    void* stream) {
+  if (!token || !table || !out || !tile_sumsq) return fail(FX_EINVAL, "token, table, out and tile_sumsq must be non-null");
+  if (!is_half_dtype(dtype)) return fail(FX_EINVAL, "dtype must be fp16 or bf16");
+  if (vocab < 1) return fail(FX_EINVAL, "vocab must be positive, got %d", vocab);
+  if (hidden < 16 || hidden % 16 || hidden > (1 << 20))
+    return fail(FX_EINVAL, "hidden must be a positive multiple of 16, got %d", hidden);
+  if (reinterpret_cast<uintptr_t>(table) % 16 || reinterpret_cast<uintptr_t>(out) % 16 ||
+      reinterpret_cast<uintptr_t>(token) % 8 || reinterpret_cast<uintptr_t>(tile_sumsq) % 4)
+    return fail(FX_EINVAL, "table and out must be 16-byte aligned, token 8-byte and tile_sumsq 4-byte aligned");
+  fx::LmHeadArgs merge{};
+  if (prediction) {
+    if (reinterpret_cast<uintptr_t>(prediction) % 8 != 0)
+      return fail(FX_EINVAL, "prediction must be 8-byte aligned");
+    int rc = lm_head_workspace(lm_workspace, lm_workspace_bytes, lm_vocab, &merge);
+    if (rc) return rc;
+    merge.prediction = prediction;
+  }
+  if (!fx::launch_decode_embed(dtype, token, static_cast<const uint16_t*>(table), vocab, hidden,
+                               static_cast<uint16_t*>(out), tile_sumsq, merge, static_cast<hipStream_t>(stream)))
+    return fail(FX_EINVAL, "no embedding kernel for dtype %d", dtype);
+  return check_launch("decode_embed_kernel");
 }
 
 int fx_silu_mul(const void* gate, const void* up, void* out, int n, int dtype, void* stream) {

@@ -10,6 +10,7 @@
 // once to the activation dtype.  KV cache layout [Hk, Lmax, D].
 #include "common.h"
 #include "decode_launch.h"
+#include "lm_head_launch.h"
 #include "norms_launch.h"
 
 namespace fx {
@@ -357,6 +358,63 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* __restric
   const float g = to_f32<DT>(gate[i]);
   const float s = round_to<DT>(g / (1.f + __expf(-g)));
   out[i] = from_f32<DT>(s * to_f32<DT>(up[i]));
+}
+
+// Start of a decode step on the residual-stream chain (one workgroup of 256
+// threads): the embedding row of *token into `out`, and per 16-element tile of
+// it the sum of squares (elements in order, fp32) into `tile_sumsq` -- the
+// partials the first layer's normalising q|k|v GEMV reads, as every later layer
+// reads its predecessor's residual epilogue; then, when `merge` is set, the
+// argmax merge of the previous step's LM-head partials into its prediction.
+// One launch in place of the embedding gather, the first RMSNorm and the
+// previous step's merge.  A token outside [0, vocab) gives a NaN row (and NaN
+// tile sums), so the step's logits are NaN rather than another token's.
+template <int DT>
+__global__ __launch_bounds__(256) void decode_embed_kernel(const long long* __restrict__ token,
+                                                           const uint16_t* __restrict__ table, int vocab,
+                                                           int hidden, uint16_t* __restrict__ out,
+                                                           float* __restrict__ tile_sumsq, LmHeadArgs merge) {
+  asm volatile("" ::"s"(token), "s"(table), "s"(vocab), "s"(hidden), "s"(out), "s"(tile_sumsq));
+  const long long tok = *token;
+  const bool valid = tok >= 0 && tok < vocab;
+  const auto rt = buffer_resource(table + (valid ? size_t(tok) * hidden : 0), size_t(hidden) * 2);
+  const int tiles = hidden / 16;
+  for (int tile = threadIdx.x; tile < tiles; tile += 256) {
+    const u32x4_t a = load_b128(rt, tile * 32, 0), b = load_b128(rt, tile * 32 + 16, 0);
+    u32x4_t* dst = reinterpret_cast<u32x4_t*>(out + size_t(tile) * 16);
+    float ss = 0.f;
+    if (valid) {
+      dst[0] = a;
+      dst[1] = b;
+      const u32x4_t v[2] = {a, b};
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float x = to_f32<DT>(uint16_t(v[h][e >> 1] >> (16 * (e & 1))));
+          ss = fmaf(x, x, ss);
+        }
+    } else {
+      const unsigned nan2 = DT == kBF16 ? 0x7fc07fc0u : 0x7e007e00u;
+      dst[0] = dst[1] = u32x4_t{nan2, nan2, nan2, nan2};
+      ss = __builtin_nanf("");
+    }
+    tile_sumsq[tile] = ss;
+  }
+  if (merge.prediction) merge_argmax_partials(merge.part_val, merge.part_idx, merge.blocks, merge.prediction);
+}
+
+bool launch_decode_embed(int dt, const long long* token, const uint16_t* table, int vocab, int hidden,
+                         uint16_t* out, float* tile_sumsq, const LmHeadArgs& merge, hipStream_t s) {
+  if (dt == kBF16)
+    hipLaunchKernelGGL(decode_embed_kernel<kBF16>, dim3(1), dim3(256), 0, s, token, table, vocab, hidden, out,
+                       tile_sumsq, merge);
+  else if (dt == kF16)
+    hipLaunchKernelGGL(decode_embed_kernel<kF16>, dim3(1), dim3(256), 0, s, token, table, vocab, hidden, out,
+                       tile_sumsq, merge);
+  else
+    return false;
+  return true;
 }
 
 template <int DT, int D, int KPT>

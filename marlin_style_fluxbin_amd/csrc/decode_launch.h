@@ -1,6 +1,7 @@
 // Launch plumbing for the decode attention and SwiGLU kernels (decode.hip).
 #pragma once
 #include "common.h"
+#include "lm_head_launch.h"
 
 namespace fx {
 
@@ -43,5 +44,9 @@ inline int attn_keys_per_block(int head_dim, int kpt) { return 256 / (head_dim /
 bool launch_decode_attention(int dt, int head_dim, const AttnArgs& a, hipStream_t s);
 bool launch_silu_mul(int dt, const uint16_t* gate, const uint16_t* up, uint16_t* out, int n,
                      hipStream_t s);
+// Embedding row of *token + its 16-element tile sums of squares; merge.prediction
+// set: also the argmax merge of merge.part_val / part_idx (merge.blocks of them).
+bool launch_decode_embed(int dt, const long long* token, const uint16_t* table, int vocab, int hidden,
+                         uint16_t* out, float* tile_sumsq, const LmHeadArgs& merge, hipStream_t s);
 
 }  // namespace fx

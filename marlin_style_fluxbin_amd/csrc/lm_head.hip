@@ -30,15 +30,6 @@ __device__ __forceinline__ float dot2(unsigned a, unsigned b, float c) {
     return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, a), __builtin_bit_cast(f16x2_t, b), c, false);
 }
 
-// (v, i) ranks above (u, j): NaN above every number (the first NaN wins),
-// otherwise the larger value, ties to the lower index.  A strict total order
-// over distinct indices, so merges in any order give the same winner.
-__device__ __forceinline__ bool ranks_above(float v, int i, float u, int j) {
-  const bool vn = v != v, un = u != u;
-  if (vn || un) return vn && (!un || i < j);
-  return v > u || (v == u && i < j);
-}
-
 // grid `blocks` workgroups of 4 waves; wave w of the grid takes the row groups
 // (RPI p .. RPI p + RPI - 1), p = w, w + waves, ... (neighbouring waves stream
 // neighbouring rows).  Lane l holds elements [8 (64 c + l), +8) of the activation
@@ -149,41 +140,7 @@ __global__ __launch_bounds__(256) void lm_head_argmax_kernel(LmHeadArgs a) {
 // total order, so the result does not depend on the merge order) -> *prediction.
 __global__ __launch_bounds__(256) void lm_head_merge_kernel(const float* part_val, const int* part_idx, int blocks,
                                                             long long* prediction) {
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  float v = -INFINITY;
-  int i = INT_MAX;
-  for (int b = t; b < blocks; b += 256) {
-    const float pv = part_val[b];
-    const int pi = part_idx[b];
-    if (ranks_above(pv, pi, v, i)) {
-      v = pv;
-      i = pi;
-    }
-  }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const float ov = __shfl_xor(v, o, 64);
-    const int oi = __shfl_xor(i, o, 64);
-    if (ranks_above(ov, oi, v, i)) {
-      v = ov;
-      i = oi;
-    }
-  }
-  __shared__ float wv[kLmWaves];
-  __shared__ int wi[kLmWaves];
-  if (lane == 0) {
-    wv[wave] = v;
-    wi[wave] = i;
-  }
-  __syncthreads();
-  if (t == 0) {
-    for (int w = 1; w < kLmWaves; ++w)
-      if (ranks_above(wv[w], wi[w], v, i)) {
-        v = wv[w];
-        i = wi[w];
-      }
-    *prediction = i;
-  }
+  merge_argmax_partials(part_val, part_idx, blocks, prediction);
 }
 
 template <int DT, int NC>
@@ -197,17 +154,26 @@ bool lm_dispatch(int nc, const LmHeadArgs& a, hipStream_t s) {
     else
       hipLaunchKernelGGL((lm_head_argmax_kernel<DT, NC, false, kLmRowsInFlight>), dim3(a.blocks), dim3(256), 0, s,
                          a);
-    hipLaunchKernelGGL(lm_head_merge_kernel, dim3(1), dim3(256), 0, s, a.part_val, a.part_idx, a.blocks,
-                       a.prediction);
     return true;
   }
 }
 
-bool launch_lm_head_argmax(int dt, const LmHeadArgs& a, hipStream_t s) {
+bool launch_lm_head_partials(int dt, const LmHeadArgs& a, hipStream_t s) {
   if (a.K % 512 != 0) return false;
   if (dt == kBF16) return lm_dispatch<kBF16, 1>(a.K / 512, a, s);
   if (dt == kF16) return lm_dispatch<kF16, 1>(a.K / 512, a, s);
   return false;
+}
+
+void launch_lm_head_merge(const LmHeadArgs& a, hipStream_t s) {
+  hipLaunchKernelGGL(lm_head_merge_kernel, dim3(1), dim3(256), 0, s, a.part_val, a.part_idx, a.blocks,
+                     a.prediction);
+}
+
+bool launch_lm_head_argmax(int dt, const LmHeadArgs& a, hipStream_t s) {
+  if (!launch_lm_head_partials(dt, a, s)) return false;
+  launch_lm_head_merge(a, s);
+  return true;
 }
 
 }  // namespace fx

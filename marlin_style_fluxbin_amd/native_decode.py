@@ -12,9 +12,10 @@ with structural W3 Linears,
     GEMV adding into the residual -> gate|up GEMV normalising, with SwiGLU ->
     down GEMV adding into the residual
 
-(6 launches; 5 while one split covers the context), followed once per token by
-one launch for the final RMSNorm, the
-bf16 LM head and the argmax.  Other Linears -- the hybrid two-base g128/s8
+(6 launches; 5 while one split covers the context).  Each token starts with one
+launch for the embedding row and its RMSNorm statistics (which also merges the
+previous token's argmax partials) and ends with the final RMSNorm + bf16 LM head
+launch; the last token's argmax merge is one more launch per sequence.  Other Linears -- the hybrid two-base g128/s8
 format of ``PackedHybridLinear`` (``fx_hybrid_gemv``) or dense bf16 (the bf16
 arm, ``torch.matmul``) -- run between add+RMSNorm kernels and the same attention
 launches.  The
@@ -226,6 +227,10 @@ class _ResidualStream:
                 return None
             if swiglu.perm_ptr is not None:
                 return None
+        table = session.embed
+        if not (table.is_contiguous() and table.data_ptr() % 16 == 0 and table.dtype == session.dtype
+                and session.hidden % 16 == 0):
+            return None  # the step's first launch reads the embedding rows as 16-byte vectors
         fmt = _lib.PAYLOAD_FIELDS if payload_format is None else payload_format
         if any(lin["self_attn.o_proj"].gemv.perm_ptr is not None or lin["mlp.down_proj"].gemv.perm_ptr is not None
                for lin in session.lin):
@@ -238,17 +243,6 @@ class _ResidualStream:
         torch.cuda.synchronize(session.device)
         return stream
 
-    def plain(self, gemv: W3Gemv, x, out):
-        """out = x @ W.T (the first layer's q|k|v, after the separate RMSNorm)."""
-        if self.format == _lib.PAYLOAD_PLANAR:
-            gemv(x, out)
-            return
-        lay = gemv.layout
-        _lib.check(self.lib.fx_w3_gemv_fields(
-            x.data_ptr(), _lib.dtype_code(x.dtype), self.payload(lay).data_ptr(), lay["scales"].data_ptr(),
-            gemv.scale_code, gemv.zeros_ptr, out.data_ptr(), gemv.out_features, gemv.in_features,
-            _lib.stream_handle(x.device)), "fx_w3_gemv_fields")
-
     def residual(self, gemv: W3Gemv, x, residual):
         """residual <- round(residual + round(x @ W.T)); tile sums of its squares."""
         lay = gemv.layout
@@ -257,6 +251,15 @@ class _ResidualStream:
             gemv.scale_code, gemv.zeros_ptr, gemv.perm_ptr, residual.data_ptr(), residual.data_ptr(),
             self.partials.data_ptr(), gemv.out_features, gemv.in_features, self.format,
             _lib.stream_handle(x.device)), "fx_w3_gemv_residual")
+
+    def embed(self, token, table, out, lm_ws=None, lm_vocab=0, prediction=None):
+        """out = table[*token], and the tile sums of its squares (the first layer's
+        normalising GEMV reads them); with ``prediction``, also the merge of the
+        previous step's LM-head maxima in ``lm_ws`` into it (one launch)."""
+        _lib.check(self.lib.fx_decode_embed(
+            token.data_ptr(), table.data_ptr(), table.shape[0], table.shape[1], out.data_ptr(),
+            self.partials.data_ptr(), _lib.ptr(lm_ws), 0 if lm_ws is None else lm_ws.numel(), lm_vocab,
+            _lib.ptr(prediction), _lib.dtype_code(table.dtype), _lib.stream_handle(out.device)), "fx_decode_embed")
 
     def normed(self, layout, scale_code, zeros_ptr, rows, h, weight, eps, out, swiglu):
         """out = GEMV (or SwiGLU) of RMSNorm(h) with the tile sums of h."""
@@ -382,12 +385,20 @@ class NativeDecodeSession:
             self.maximum_length, self.head_dim, pos, self.scale, _lib.dtype_code(self.dtype),
             _lib.stream_handle(self.device)), "fx_decode_attention_rope")
 
-    def _lm_head(self, i, hidden, norm_weight):
+    def _lm_head(self, i, hidden, norm_weight, merge=True):
         """Logits row ``i`` and its greedy token from the last hidden state
-        (``norm_weight`` set: RMS-normalised first).  One launch
-        (``fx_lm_head_argmax``) where the head allows it; else RMSNorm, the
-        hipBLASLt matmul and torch.argmax."""
+        (``norm_weight`` set: RMS-normalised first).  ``fx_lm_head_argmax`` where
+        the head allows it (``merge`` False: ``fx_lm_head_logits`` only, the
+        maxima merged by the next step's first launch or by :meth:`_merge_last`);
+        else RMSNorm, the hipBLASLt matmul and torch.argmax."""
         if self.lm_ws is not None:
+            if not merge:
+                _lib.check(self.lib.fx_lm_head_logits(
+                    hidden.data_ptr(), None if norm_weight is None else norm_weight.data_ptr(), self.eps,
+                    self.lm_head.data_ptr(), self.logits[i].data_ptr(), self.lm_ws.data_ptr(), self.lm_ws.numel(),
+                    self.logits.shape[1], self.hidden, _lib.dtype_code(self.dtype),
+                    _lib.stream_handle(self.device)), "fx_lm_head_logits")
+                return
             _lib.check(self.lib.fx_lm_head_argmax(
                 hidden.data_ptr(), None if norm_weight is None else norm_weight.data_ptr(), self.eps,
                 self.lm_head.data_ptr(), self.logits[i].data_ptr(), self.predictions[i].data_ptr(),
@@ -408,19 +419,19 @@ class NativeDecodeSession:
                                         _lib.stream_handle(self.device)), "fx_silu_mul")
 
     def _step_residual_stream(self, i):
-        from .fused_modules import rms_norm
-
         rs = self.stream
-        torch.index_select(self.embed, 0, self.tokens[0, i:i + 1], out=self.residual)
+        # the step's first launch: embedding row, its tile sums, and the merge of
+        # the previous step's LM-head maxima into that step's prediction
+        split_head = self.lm_ws is not None
+        merge_prev = split_head and i > 0
+        rs.embed(self.tokens[0, i:i + 1], self.embed, self.residual,
+                 self.lm_ws if merge_prev else None, self.logits.shape[1] if merge_prev else 0,
+                 self.predictions[i - 1] if merge_prev else None)
         pos = self.prefix_length + i
         for l, lin in enumerate(self.lin):
             gemv = self.qkv[l].call
-            if l == 0:
-                rms_norm(self.residual, self.in_norm[0], self.eps, out=self.normed)
-                rs.plain(gemv, self.normed, self.qkv_out)
-            else:
-                rs.normed(gemv.layout, gemv.scale_code, gemv.zeros_ptr, gemv.out_features, self.residual,
-                          self.in_norm[l], self.eps, self.qkv_out, False)
+            rs.normed(gemv.layout, gemv.scale_code, gemv.zeros_ptr, gemv.out_features, self.residual,
+                      self.in_norm[l], self.eps, self.qkv_out, False)
             self._attention(l, pos)
             rs.residual(lin["self_attn.o_proj"].gemv, self.attn, self.residual)
             sw = self.swiglu[l]
@@ -429,7 +440,15 @@ class NativeDecodeSession:
             rs.residual(lin["mlp.down_proj"].gemv, self.act, self.residual)
             if self.layer_observer is not None:
                 self.layer_observer(i, l, self.residual)
-        self._lm_head(i, self.residual, self.final_norm)
+        self._lm_head(i, self.residual, self.final_norm, merge=not split_head)
+
+    def _merge_last(self):
+        """The last step's LM-head maxima into its prediction (the residual-stream
+        chain merges every other step's in the next step's first launch)."""
+        if self.stream is not None and self.lm_ws is not None:
+            _lib.check(self.lib.fx_lm_head_merge(
+                self.lm_ws.data_ptr(), self.lm_ws.numel(), self.logits.shape[1],
+                self.predictions[self.steps - 1].data_ptr(), _lib.stream_handle(self.device)), "fx_lm_head_merge")
 
     def _step(self, i):
         if self.stream is not None:
@@ -479,6 +498,7 @@ class NativeDecodeSession:
     def run(self):
         for i in range(self.steps):
             self._step(i)
+        self._merge_last()
         return self.logits, self.predictions
 
     def trace(self, outputs=None) -> dict:

@@ -125,3 +125,63 @@ def test_lm_head_argmax_rejects_bad_shapes(gpu):
     rc = lib.fx_lm_head_argmax(t.data_ptr(), None, 1e-6, t.data_ptr(), t.data_ptr(), p.data_ptr(),
                                head.ws.data_ptr(), 16, 2, 512, 2, None)
     assert rc == 1 and "workspace" in lib.fx_last_error().decode()
+
+
+@pytest.mark.parametrize("vocab,k", [(12289, 4096), (7, 512), (151936, 4096)])
+def test_split_launches_equal_the_fused_call(gpu, vocab, k):
+    """fx_lm_head_logits then fx_lm_head_merge (or the merge inside fx_decode_embed,
+    the decode chain's next-step launch) give fx_lm_head_argmax's logits and prediction."""
+    lib = _lib.library()
+    g = torch.Generator().manual_seed(vocab)
+    h = torch.randn(1, k, generator=g).to(torch.bfloat16).to(gpu)
+    w = (1 + 0.02 * torch.randn(k, generator=g)).to(torch.bfloat16).to(gpu)
+    weight = (torch.randn(vocab, k, generator=g) * 0.05).to(torch.bfloat16).to(gpu)
+    want_logits, want_pred = _Head(gpu)(h, w, weight)
+    ws = torch.full((lib.fx_lm_head_argmax_workspace_bytes(),), 0xAB, dtype=torch.uint8, device=gpu)
+    logits = torch.empty(vocab, dtype=torch.bfloat16, device=gpu)
+    _lib.check(lib.fx_lm_head_logits(h.data_ptr(), w.data_ptr(), 1e-6, weight.data_ptr(), logits.data_ptr(),
+                                     ws.data_ptr(), ws.numel(), vocab, k, _lib.FX_BF16, _lib.stream_handle(gpu)),
+               "lm_head_logits")
+    pred = torch.full((1,), -1, dtype=torch.int64, device=gpu)
+    _lib.check(lib.fx_lm_head_merge(ws.data_ptr(), ws.numel(), vocab, pred.data_ptr(), _lib.stream_handle(gpu)),
+               "lm_head_merge")
+    assert torch.equal(logits, want_logits) and torch.equal(pred, want_pred)
+    # the same merge inside the next step's embedding launch
+    table = torch.randn(5, 256, generator=g).to(torch.bfloat16).to(gpu)
+    token = torch.tensor([3], dtype=torch.int64, device=gpu)
+    row = torch.empty(1, 256, dtype=torch.bfloat16, device=gpu)
+    sums = torch.empty(16, dtype=torch.float32, device=gpu)
+    pred2 = torch.full((1,), -1, dtype=torch.int64, device=gpu)
+    _lib.check(lib.fx_decode_embed(token.data_ptr(), table.data_ptr(), 5, 256, row.data_ptr(), sums.data_ptr(),
+                                   ws.data_ptr(), ws.numel(), vocab, pred2.data_ptr(), _lib.FX_BF16,
+                                   _lib.stream_handle(gpu)), "decode_embed")
+    assert torch.equal(pred2, want_pred)
+
+
+def test_decode_embed_row_and_tile_sums(gpu):
+    """fx_decode_embed: the token's row bit for bit, each 16-element tile's sum of
+    squares against float64, NaNs for a token outside the table, no merge when
+    prediction is NULL."""
+    lib = _lib.library()
+    g = torch.Generator().manual_seed(3)
+    for dtype, code in ((torch.bfloat16, _lib.FX_BF16), (torch.float16, _lib.FX_F16)):
+        table = (torch.randn(40, 4096, generator=g) * 2).to(dtype).to(gpu)
+        out = torch.empty(1, 4096, dtype=dtype, device=gpu)
+        sums = torch.empty(256, dtype=torch.float32, device=gpu)
+        for tok in (0, 17, 39):
+            token = torch.tensor([tok], dtype=torch.int64, device=gpu)
+            _lib.check(lib.fx_decode_embed(token.data_ptr(), table.data_ptr(), 40, 4096, out.data_ptr(),
+                                           sums.data_ptr(), None, 0, 0, None, code, _lib.stream_handle(gpu)),
+                       "decode_embed")
+            assert torch.equal(out[0], table[tok])
+            want = (table[tok].double().cpu().view(256, 16) ** 2).sum(1)
+            np.testing.assert_allclose(sums.double().cpu().numpy(), want.numpy(), rtol=1e-5, atol=0)
+        for bad in (-1, 40):
+            token = torch.tensor([bad], dtype=torch.int64, device=gpu)
+            _lib.check(lib.fx_decode_embed(token.data_ptr(), table.data_ptr(), 40, 4096, out.data_ptr(),
+                                           sums.data_ptr(), None, 0, 0, None, code, _lib.stream_handle(gpu)),
+                       "decode_embed")
+            assert torch.isnan(out.float()).all() and torch.isnan(sums).all()
+    rc = lib.fx_decode_embed(token.data_ptr(), table.data_ptr(), 40, 4004, out.data_ptr(), sums.data_ptr(), None, 0,
+                             0, None, _lib.FX_BF16, _lib.stream_handle(gpu))
+    assert rc == 1 and b"multiple of 16" in lib.fx_last_error()
