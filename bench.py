@@ -187,7 +187,8 @@ def bench_shape(o, k, device, steps, warmup, stream, min_bytes=320e6, min_copies
     bcopies = max(min_copies // 5, int(min_bytes // bf16_bytes) + 1)
     from marlin_style_fluxbin_amd.gptq_deployment import restore_planar_w3
 
-    weights = [restore_planar_w3(payloads[i % copies], dtype=torch.bfloat16) for i in range(bcopies)]
+    weights = [restore_planar_w3(payloads[i % copies], dtype=torch.bfloat16, perm_identity=True)
+               for i in range(bcopies)]
     bout = torch.empty(1, o, device=device, dtype=torch.bfloat16)
 
     def bf16_all():
@@ -197,7 +198,20 @@ def bench_shape(o, k, device, steps, warmup, stream, min_bytes=320e6, min_copies
     bgraph = capture(bf16_all, stream)
     bms = time_graph(bgraph, steps, warmup, stream)
     bf16_us = bms * 1000 / bcopies
-    del bgraph, weights, payloads, gemvs
+    del bgraph
+
+    # the dense fallback's dequantize (fx_w3_restore, identity order) into the bf16
+    # arm's buffers: reads the payload, writes the 2OK-byte weight
+    from marlin_style_fluxbin_amd.w3_lut_deployment import restore_planar_w3_into
+
+    def restore_all():
+        for i, w in enumerate(weights):
+            restore_planar_w3_into(payloads[i % copies], w, perm_identity=True)
+
+    rgraph = capture(restore_all, stream)
+    restore_us = time_graph(rgraph, steps, warmup, stream) * 1000 / bcopies
+    restore_bytes = algorithmic_bytes(o, k, m=0) + 2 * o * k
+    del rgraph, weights, payloads, gemvs
     torch.cuda.empty_cache()
     return {
         "O": o, "K": k, "copies": copies, "algorithmic_bytes": nbytes,
@@ -208,6 +222,7 @@ def bench_shape(o, k, device, steps, warmup, stream, min_bytes=320e6, min_copies
         "fields_us": round(fields_us, 3), "fields_GBps": round(nbytes / fields_us / 1e3, 1),
         "fields_frac_hbm": round(nbytes / fields_us / 1e3 / HBM_PEAK_GBPS, 4),
         "small_m": small_m,
+        "restore_us": round(restore_us, 3), "restore_GBps": round(restore_bytes / restore_us / 1e3, 1),
     }
 
 

@@ -172,7 +172,12 @@ int fx_w3_gemv_config(const void *x, int x_dtype, const uint8_t *planes, const v
 /*
  * Reference: restore_planar_w3 (gptq_deployment.py:247-260), the dequantize
  * step of the dense fallback (w3_lut_deployment.py:327-333).  weight [O,K] in
- * weight_dtype: round_weight_dtype(round_scale_dtype(s * (q - z))).
+ * weight_dtype: round_weight_dtype(round_scale_dtype(s * (q - z))); sorted
+ * column s of row o lands at weight[o, perm[s]].  perm NULL is the identity
+ * order (row-ordered 16-byte stores; pass NULL when the order is known to be
+ * the identity); a permutation stages whole rows in LDS and needs K <= 32768.
+ * perm entries outside [0, K) are skipped and a column that no entry names is
+ * zero.
  */
 int fx_w3_restore(const uint8_t *planes, const void *scales, int scale_dtype,
                   const uint8_t *zeros, const int16_t *perm, void *weight, int weight_dtype,

@@ -828,6 +828,23 @@ int fx_w3_gemv_config(const void* x, int x_dtype, const uint8_t* planes, const v
                   static_cast<hipStream_t>(stream));
 }
 
+namespace {
+
+// Kernel pointers of the restore instantiations, indexed [scale bf16][weight bf16].
+using RestoreFn = void (*)(const uint8_t*, const uint16_t*, const uint8_t*, uint16_t*, int, int, int);
+using RestorePermutedFn = void (*)(const uint8_t*, const uint16_t*, const uint8_t*, const int16_t*,
+                                   uint16_t*, int, int, int, int, int);
+constexpr RestoreFn kRestore[2][2] = {
+    {fx::w3_restore_kernel<fx::kF16, fx::kF16>, fx::w3_restore_kernel<fx::kF16, fx::kBF16>},
+    {fx::w3_restore_kernel<fx::kBF16, fx::kF16>, fx::w3_restore_kernel<fx::kBF16, fx::kBF16>}};
+constexpr RestorePermutedFn kRestorePermuted[2][2] = {
+    {fx::w3_restore_permuted_kernel<fx::kF16, fx::kF16>,
+     fx::w3_restore_permuted_kernel<fx::kF16, fx::kBF16>},
+    {fx::w3_restore_permuted_kernel<fx::kBF16, fx::kF16>,
+     fx::w3_restore_permuted_kernel<fx::kBF16, fx::kBF16>}};
+
+}  // namespace
+
 int fx_w3_restore(const uint8_t* planes, const void* scales, int scale_dtype,
                   const uint8_t* zeros, const int16_t* perm, void* weight, int weight_dtype,
                   int O, int K, void* stream) {
@@ -835,26 +852,31 @@ int fx_w3_restore(const uint8_t* planes, const void* scales, int scale_dtype,
   if (!is_half_dtype(scale_dtype) || !is_half_dtype(weight_dtype))
     return fail(FX_EINVAL, "scale and weight dtypes must be fp16 or bf16");
   if (O < 1 || K < 128 || K % 128) return fail(FX_EINVAL, "bad O/K");
+  if (perm && K > 32768) return fail(FX_EINVAL, "int16 permutation entries address K <= 32768");
   if (reinterpret_cast<uintptr_t>(planes) % 16 != 0)
     return fail(FX_EINVAL, "planes must be 16-byte aligned");
   const int G = K / 128;
-  const dim3 grid((O * G + 255) / 256);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const uint16_t* sc = static_cast<const uint16_t*>(scales);
   uint16_t* w = static_cast<uint16_t*>(weight);
-  if (scale_dtype == FX_BF16 && weight_dtype == FX_BF16)
-    hipLaunchKernelGGL((fx::w3_restore_kernel<fx::kBF16, fx::kBF16>), grid, dim3(256), 0, s,
-                       planes, sc, zeros, perm, w, O, G);
-  else if (scale_dtype == FX_BF16 && weight_dtype == FX_F16)
-    hipLaunchKernelGGL((fx::w3_restore_kernel<fx::kBF16, fx::kF16>), grid, dim3(256), 0, s,
-                       planes, sc, zeros, perm, w, O, G);
-  else if (scale_dtype == FX_F16 && weight_dtype == FX_BF16)
-    hipLaunchKernelGGL((fx::w3_restore_kernel<fx::kF16, fx::kBF16>), grid, dim3(256), 0, s,
-                       planes, sc, zeros, perm, w, O, G);
-  else
-    hipLaunchKernelGGL((fx::w3_restore_kernel<fx::kF16, fx::kF16>), grid, dim3(256), 0, s, planes,
-                       sc, zeros, perm, w, O, G);
-  return check_launch("w3_restore_kernel");
+  const int sb = scale_dtype == FX_BF16, wb = weight_dtype == FX_BF16;
+  const int weight16 = reinterpret_cast<uintptr_t>(weight) % 16 == 0;
+  if (!perm) {
+    // one workgroup per (16-row block, kRestoreGroups groups)
+    const size_t blocks =
+        size_t((O + 15) / 16) * size_t((G + fx::kRestoreGroups - 1) / fx::kRestoreGroups);
+    if (blocks > size_t(INT32_MAX)) return fail(FX_EINVAL, "O * K too large");
+    hipLaunchKernelGGL(kRestore[sb][wb], dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s,
+                       planes, sc, zeros, w, O, G, weight16);
+    return check_launch("w3_restore_kernel");
+  }
+  // whole rows staged in LDS: at most 32 KB for K <= 16384, one row (<= 64 KB) above
+  const int rows = std::max(1, fx::kRestoreStageBytes / (2 * K));
+  const int perm16 = reinterpret_cast<uintptr_t>(perm) % 16 == 0;
+  hipLaunchKernelGGL(kRestorePermuted[sb][wb], dim3((O + rows - 1) / rows),
+                     dim3(fx::kRestoreStageThreads), size_t(rows) * K * 2, s, planes, sc, zeros,
+                     perm, w, O, G, rows, weight16, perm16);
+  return check_launch("w3_restore_permuted_kernel");
 }
 
 int fx_rmsnorm(const void* x, const void* residual, const void* weight, void* out,

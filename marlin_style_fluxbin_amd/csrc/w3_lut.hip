@@ -218,32 +218,124 @@ __global__ __launch_bounds__(256) void w3_finish_kernel(const float* __restrict_
 
 // Dequantize to a dense [O,K] weight with the reference's rounding points
 // (restore_planar_w3, gptq_deployment.py:247-260): round_scale_dtype(s*(q-z)),
-// then round to the weight dtype.  One thread per (group, row).
+// then round to the weight dtype.  Sorted column s = 128g+8c+j of row o lands
+// at weight[o, perm[s]].
+//
+// The eight values of byte c of a row's three plane vectors (sorted columns
+// 128g+8c .. 128g+8c+7), two per word in column order.
+template <int SDT, int WDT>
+__device__ __forceinline__ void restore_eight(unsigned b0, unsigned b1, unsigned b2, float s, int z,
+                                              unsigned (&pair)[4]) {
+#pragma unroll
+  for (int j = 0; j < 8; j += 2) {
+    unsigned two = 0;
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int b = j + e;
+      const int q = int((b0 >> b) & 1u) | (int((b1 >> b) & 1u) << 1) | ((1 - int((b2 >> b) & 1u)) << 2);
+      two |= unsigned(from_f32<WDT>(round_to<SDT>(s * float(q - z)))) << (16 * e);
+    }
+    pair[j >> 1] = two;
+  }
+}
+
+// Identity order.  A workgroup owns 16 rows and kRestoreGroups consecutive
+// groups (consecutive workgroups: the next groups of the same rows); per group
+// lane c of a row's 16 lanes expands byte c of the row's plane vectors and
+// writes its eight columns as one 16-byte store (element stores when the
+// weight is not 16-byte aligned), so the 16 lanes of a row store the group's
+// 256 bytes of that row together.
+constexpr int kRestoreGroups = 2;
+
 template <int SDT, int WDT>
 __global__ __launch_bounds__(256) void w3_restore_kernel(
     const uint8_t* __restrict__ planes, const uint16_t* __restrict__ scales,
-    const uint8_t* __restrict__ zeros, const int16_t* __restrict__ perm,
-    uint16_t* __restrict__ weight, int O, int G) {
-  const int idx = int(blockIdx.x) * 256 + threadIdx.x;
-  if (idx >= O * G) return;
-  const int g = idx / O, o = idx % O;
-  const int K = G * 128;
-  uint4 w[3];
+    const uint8_t* __restrict__ zeros, uint16_t* __restrict__ weight, int O, int G, int weight16) {
+  const unsigned group_blocks = unsigned((G + kRestoreGroups - 1) / kRestoreGroups);
+  const int g0 = int(blockIdx.x % group_blocks) * kRestoreGroups;
+  const int o = int(blockIdx.x / group_blocks) * 16 + int(threadIdx.x >> 4);
+  const int c = int(threadIdx.x & 15u);
+  if (o >= O) return;
+  const size_t plane = size_t(O) * 16;
+  uint16_t* row = weight + size_t(o) * G * 128;
 #pragma unroll
-  for (int p = 0; p < 3; ++p)
-    w[p] = *reinterpret_cast<const uint4*>(planes + ((size_t(g) * 3 + p) * O + o) * 16);
-  const float s = to_f32<SDT>(scales[size_t(g) * O + o]);
-  const int z = zeros ? int(zeros[size_t(g) * O + o]) : 4;
-  for (int c = 0; c < 16; ++c) {
-    const unsigned b0 = plane_byte(w[0], c), b1 = plane_byte(w[1], c), b2 = plane_byte(w[2], c);
+  for (int i = 0; i < kRestoreGroups; ++i) {
+    const int g = g0 + i;
+    if (g >= G) break;
+    const size_t at = size_t(g) * 3 * plane + size_t(o) * 16 + c;
+    unsigned pair[4];
+    restore_eight<SDT, WDT>(planes[at], planes[at + plane], planes[at + 2 * plane],
+                            to_f32<SDT>(scales[size_t(g) * O + o]),
+                            zeros ? int(zeros[size_t(g) * O + o]) : 4, pair);
+    uint16_t* dst = row + g * 128 + c * 8;
+    if (weight16) {
+      *reinterpret_cast<uint4*>(dst) = make_uint4(pair[0], pair[1], pair[2], pair[3]);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) dst[j] = uint16_t(pair[j >> 1] >> (16 * (j & 1)));
+    }
+  }
+}
+
+// With a column permutation.  A workgroup stages `rows_per_block` whole rows
+// in LDS (rows_per_block * K * 2 bytes, zeroed first), scatters each expanded
+// value to its permuted column there, and then writes the rows out in order
+// with 16-byte stores, so a scattered permutation costs LDS scatter and not
+// scattered HBM stores.  Entries outside [0, K) are skipped; a column no entry
+// names stays zero.  The eight entries of a lane are one 16-byte load when perm
+// is 16-byte aligned.
+constexpr int kRestoreStageThreads = 512;
+constexpr int kRestoreStageBytes = 32768;  // rows_per_block = max(1, this / (2K))
+
+template <int SDT, int WDT>
+__global__ __launch_bounds__(kRestoreStageThreads) void w3_restore_permuted_kernel(
+    const uint8_t* __restrict__ planes, const uint16_t* __restrict__ scales,
+    const uint8_t* __restrict__ zeros, const int16_t* __restrict__ perm,
+    uint16_t* __restrict__ weight, int O, int G, int rows_per_block, int weight16, int perm16) {
+  extern __shared__ uint4 stage_vec[];
+  uint16_t* stage = reinterpret_cast<uint16_t*>(stage_vec);
+  const int K = G * 128;
+  const int o0 = int(blockIdx.x) * rows_per_block;
+  const int rows = min(rows_per_block, O - o0);
+  const int vecs = rows * K / 8;
+  for (int i = threadIdx.x; i < vecs; i += kRestoreStageThreads) stage_vec[i] = make_uint4(0, 0, 0, 0);
+  __syncthreads();
+  const size_t plane = size_t(O) * 16;
+  // items (g, r, c): 16 consecutive lanes read one row's 16 plane bytes
+  const int items = G * rows * 16;
+  for (int it = threadIdx.x; it < items; it += kRestoreStageThreads) {
+    const int c = it & 15;
+    const int r = (it >> 4) % rows;
+    const int g = (it >> 4) / rows;
+    const int o = o0 + r;
+    const size_t at = size_t(g) * 3 * plane + size_t(o) * 16 + c;
+    unsigned pair[4];
+    restore_eight<SDT, WDT>(planes[at], planes[at + plane], planes[at + 2 * plane],
+                            to_f32<SDT>(scales[size_t(g) * O + o]),
+                            zeros ? int(zeros[size_t(g) * O + o]) : 4, pair);
+    const int sorted = g * 128 + c * 8;
+    unsigned cols[4];  // perm[sorted .. sorted+7], two per word
+    if (perm16) {
+      const uint4 p = *reinterpret_cast<const uint4*>(perm + sorted);
+      cols[0] = p.x, cols[1] = p.y, cols[2] = p.z, cols[3] = p.w;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        cols[j] = unsigned(uint16_t(perm[sorted + 2 * j])) | (unsigned(uint16_t(perm[sorted + 2 * j + 1])) << 16);
+    }
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const int q = int((b0 >> j) & 1u) | (int((b1 >> j) & 1u) << 1) | ((1 - int((b2 >> j) & 1u)) << 2);
-      const float product = round_to<SDT>(s * float(q - z));
-      const int sorted = g * 128 + c * 8 + j;
-      const int col = perm ? int(perm[sorted]) : sorted;
-      weight[size_t(o) * K + col] = from_f32<WDT>(product);
+      const int col = int(int16_t(cols[j >> 1] >> (16 * (j & 1))));
+      if (unsigned(col) < unsigned(K)) stage[r * K + col] = uint16_t(pair[j >> 1] >> (16 * (j & 1)));
     }
+  }
+  __syncthreads();
+  uint16_t* dst = weight + size_t(o0) * K;
+  if (weight16) {
+    uint4* dst_vec = reinterpret_cast<uint4*>(dst);
+    for (int i = threadIdx.x; i < vecs; i += kRestoreStageThreads) dst_vec[i] = stage_vec[i];
+  } else {
+    for (int i = threadIdx.x; i < rows * K; i += kRestoreStageThreads) dst[i] = stage[i];
   }
 }
 

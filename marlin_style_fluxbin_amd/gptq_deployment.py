@@ -273,17 +273,20 @@ def _signed_sorted(layout) -> torch.Tensor:
     return codes - zero.unsqueeze(-1)
 
 
-def restore_planar_w3(layout: Mapping[str, torch.Tensor], *, dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+def restore_planar_w3(layout: Mapping[str, torch.Tensor], *, dtype: torch.dtype = torch.bfloat16,
+                      perm_identity: bool | None = None) -> torch.Tensor:
     """Dense ``[O, K]`` weight ``round_dtype(round_scale_dtype(s * (q - z)))``.
 
-    GPU layouts are dequantized by the HIP kernel (``fx_w3_restore``).
+    GPU layouts are dequantized by the HIP kernel (``fx_w3_restore``);
+    ``perm_identity`` (known to the caller, else compared on the device) picks
+    its identity-order form.  CPU layouts ignore it.
     """
     out_features, in_features = validate_planar_w3(layout, check_values=False)
     if dtype not in (torch.float16, torch.bfloat16, torch.float32):
         raise ValueError("dtype must be float16, bfloat16 or float32")
     if layout["planes"].is_cuda and dtype != torch.float32:
         from .w3_lut_deployment import restore_planar_w3_device
-        return restore_planar_w3_device(layout, dtype=dtype)
+        return restore_planar_w3_device(layout, dtype=dtype, perm_identity=perm_identity)
     signed = _signed_sorted(layout)
     # scale dtype x int16 rounds once to the scale dtype, as the bf16 GPTQ dequantizer does
     product = layout["scales"].unsqueeze(-1) * signed

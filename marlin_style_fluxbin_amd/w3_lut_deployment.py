@@ -207,23 +207,32 @@ def qwen3_w3_route(route: str, out_features: int, in_features: int) -> dict:
 
 
 # --------------------------------------------------------------------------- device helpers
-def restore_planar_w3_device(layout: dict, *, dtype: torch.dtype) -> torch.Tensor:
+def restore_planar_w3_device(layout: dict, *, dtype: torch.dtype,
+                             perm_identity: bool | None = None) -> torch.Tensor:
     """HIP dequantize of a GPU layout into a new dense ``[O, K]`` weight."""
     out_features, in_features = validate_planar_w3(layout, check_values=False)
     weight = torch.empty(out_features, in_features, dtype=dtype, device=layout["planes"].device)
-    restore_planar_w3_into(layout, weight)
+    restore_planar_w3_into(layout, weight, perm_identity=perm_identity)
     return weight
 
 
-def restore_planar_w3_into(layout: dict, weight: torch.Tensor) -> torch.Tensor:
+def restore_planar_w3_into(layout: dict, weight: torch.Tensor, *,
+                           perm_identity: bool | None = None) -> torch.Tensor:
+    """``fx_w3_restore`` into ``weight``.  An identity permutation goes to the
+    kernel as NULL (row-ordered 16-byte stores); any other stages whole rows in
+    LDS.  ``perm_identity`` None compares the permutation on the device (one
+    host synchronisation); callers that know it pass it."""
     out_features, in_features = validate_planar_w3(layout, check_values=False)
     if tuple(weight.shape) != (out_features, in_features) or not weight.is_contiguous():
         raise ValueError("weight must be a contiguous [O,K] tensor")
     _check_layout_device(layout, weight)
+    perm = layout["perm"]
+    if perm_identity is None:
+        perm_identity = bool(torch.equal(perm.long(), torch.arange(in_features, device=perm.device)))
     lib = _lib.library()
     _lib.check(lib.fx_w3_restore(
         layout["planes"].data_ptr(), layout["scales"].data_ptr(), _lib.dtype_code(layout["scales"].dtype),
-        _lib.ptr(layout.get("zeros")), layout["perm"].data_ptr(), weight.data_ptr(),
+        _lib.ptr(layout.get("zeros")), None if perm_identity else perm.data_ptr(), weight.data_ptr(),
         _lib.dtype_code(weight.dtype), out_features, in_features, _lib.stream_handle(weight.device)),
         "fx_w3_restore")
     return weight
@@ -363,7 +372,7 @@ class PackedW3Linear(PackedLinearBase):
         return self.planes.device
 
     def _dense_weight(self, dtype: torch.dtype) -> torch.Tensor:
-        return restore_planar_w3(self.layout(), dtype=dtype)
+        return restore_planar_w3(self.layout(), dtype=dtype, perm_identity=self._perm_identity)
 
     def _check_before_bind(self, device: torch.device) -> None:
         validate_planar_w3(self.layout(), check_values=False)

@@ -196,11 +196,65 @@ def test_config0_q_proj_seed0(gpu):
 @pytest.mark.parametrize("scale_dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("weight_dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("zeros", [False, True])
-def test_restore_kernel_bitwise(gpu, scale_dtype, weight_dtype, zeros):
-    layout, dl, ol = _setup(96, 384, seed=9, zeros=zeros, scale_dtype=scale_dtype, permute=True)
+@pytest.mark.parametrize("o,k,order", [(96, 384, "random"), (37, 256, "identity"), (1041, 1024, "mixed")])
+def test_restore_kernel_bitwise(gpu, scale_dtype, weight_dtype, zeros, o, k, order):
+    """The dense weight bit for bit against the oracle's restore.  Orders: a
+    scattered permutation (every value stored alone), the identity (16-byte row
+    stores), and one that moves columns inside a few 8-column runs only (both
+    store forms in one launch); row counts off the 16-row workgroup tile."""
+    codes, scales, z, perm = config_codes(o, k, seed=o + k, zeros=zeros, scale_dtype=scale_dtype,
+                                          permute=order == "random")
+    if order == "mixed":
+        perm = torch.arange(k, dtype=torch.int16)
+        for start in (8, 136, 520, 1000):
+            perm[start:start + 8] = perm[start:start + 8].flip(0)
+        perm[300], perm[700] = 700, 300
+    layout = layout_from_codes(codes, scales, z, perm)
+    dl = {name: t.to(gpu) for name, t in layout.items()}
     got = restore_planar_w3(dl, dtype=weight_dtype).float().cpu().numpy()
-    expected = w3.restore_weight(ol, "bf16" if weight_dtype == torch.bfloat16 else "f16")
+    expected = w3.restore_weight(oracle_layout(layout), "bf16" if weight_dtype == torch.bfloat16 else "f16")
     assert np.array_equal(got, expected)
+
+
+def test_restore_kernel_permutation_edge_entries(gpu):
+    """The permuted form: an identity order passed as a permutation gives the
+    NULL form's bits; an entry outside [0, K) is skipped, so the column that no
+    entry names is zero."""
+    from marlin_style_fluxbin_amd.w3_lut_deployment import restore_planar_w3_into
+
+    layout, dl, ol = _setup(33, 768, seed=6, zeros=True)
+    want = w3.restore_weight(ol, "bf16")
+    as_perm = torch.empty(33, 768, dtype=torch.bfloat16, device=gpu)
+    restore_planar_w3_into(dl, as_perm, perm_identity=False)
+    assert np.array_equal(as_perm.float().cpu().numpy(), want)
+    bad = dl["perm"].clone()
+    bad[5], bad[600] = -3, 30000
+    skipped = torch.full((33, 768), 7.0, dtype=torch.bfloat16, device=gpu)
+    restore_planar_w3_into(dict(dl, perm=bad), skipped, perm_identity=False)
+    want[:, [5, 600]] = 0
+    assert np.array_equal(skipped.float().cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("order", ["identity", "random"])
+def test_restore_kernel_unaligned_pointers(gpu, order):
+    """A weight, then a permutation, 2 bytes off 16-byte alignment (element stores,
+    element permutation loads): the same bits."""
+    from marlin_style_fluxbin_amd.w3_lut_deployment import restore_planar_w3_into
+
+    layout, dl, ol = _setup(40, 512, seed=2, zeros=True, permute=order == "random")
+    want = w3.restore_weight(ol, "bf16")
+    buf = torch.empty(40 * 512 + 1, dtype=torch.bfloat16, device=gpu)
+    weight = buf[1:].view(40, 512)
+    assert weight.data_ptr() % 16 == 2
+    restore_planar_w3_into(dl, weight)
+    assert np.array_equal(weight.float().cpu().numpy(), want)
+    pbuf = torch.empty(513, dtype=torch.int16, device=gpu)
+    pbuf[1:].copy_(dl["perm"])
+    shifted = dict(dl, perm=pbuf[1:])
+    assert shifted["perm"].data_ptr() % 16 == 2
+    aligned = torch.empty(40, 512, dtype=torch.bfloat16, device=gpu)
+    restore_planar_w3_into(shifted, aligned)
+    assert np.array_equal(aligned.float().cpu().numpy(), want)
 
 
 def test_dense_fallback_on_gpu_uses_device_restore(gpu):
