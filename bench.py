@@ -211,7 +211,18 @@ def bench_shape(o, k, device, steps, warmup, stream, min_bytes=320e6, min_copies
     rgraph = capture(restore_all, stream)
     restore_us = time_graph(rgraph, steps, warmup, stream) * 1000 / bcopies
     restore_bytes = algorithmic_bytes(o, k, m=0) + 2 * o * k
-    del rgraph, weights, payloads, gemvs
+    del rgraph
+    # the same with a scattered (desc_act-style) column permutation: the LDS-staged form
+    shuffled = [dict(payloads[i % copies], perm=torch.randperm(k, generator=gen, device=device).to(torch.int16))
+                for i in range(bcopies)]
+
+    def restore_permuted_all():
+        for p, w in zip(shuffled, weights):
+            restore_planar_w3_into(p, w, perm_identity=False)
+
+    rgraph = capture(restore_permuted_all, stream)
+    restore_perm_us = time_graph(rgraph, steps, warmup, stream) * 1000 / bcopies
+    del rgraph, shuffled, weights, payloads, gemvs
     torch.cuda.empty_cache()
     return {
         "O": o, "K": k, "copies": copies, "algorithmic_bytes": nbytes,
@@ -223,6 +234,8 @@ def bench_shape(o, k, device, steps, warmup, stream, min_bytes=320e6, min_copies
         "fields_frac_hbm": round(nbytes / fields_us / 1e3 / HBM_PEAK_GBPS, 4),
         "small_m": small_m,
         "restore_us": round(restore_us, 3), "restore_GBps": round(restore_bytes / restore_us / 1e3, 1),
+        "restore_permuted_us": round(restore_perm_us, 3),
+        "restore_permuted_GBps": round((restore_bytes + 2 * k) / restore_perm_us / 1e3, 1),
     }
 
 

@@ -36,7 +36,12 @@ struct AttnArgs {
 // combine inside the split kernel measured slower at every decode length: its
 // store wait, arrival atomic and coherent reloads form three dependent memory
 // round trips on one workgroup (9.55 vs 7.46 us at 544 keys, 10.3 vs 7.5 us at
-// 512, Qwen3-8B heads with q/k norm and RoPE), more than the second launch.
+// 512, Qwen3-8B heads with q/k norm and RoPE), more than the second launch.  A
+// single-pass kernel (one 512-thread workgroup per query head over all keys,
+// every load issued up front, no partials) is faster only while the cache is
+// hot (4.9 us in a loop over one layer's cache): in the 36-layer decode graph,
+// where each layer's cache comes from HBM, its 32 workgroups stream 278 KB each
+// at ~30 GB/s per CU and the step took 1.513 against 1.441 ms per token.
 
 // Keys one attention workgroup covers: 256 / (D / 8) key rows times keys per thread.
 inline int attn_keys_per_block(int head_dim, int kpt) { return 256 / (head_dim / 8) * kpt; }

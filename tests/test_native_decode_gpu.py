@@ -34,7 +34,9 @@ def _ulp(v, dtype):
 
 @pytest.mark.parametrize("dtype", ["bf16", "f16"])
 @pytest.mark.parametrize("hq,hk,d,lmax,pos", [(32, 8, 128, 544, 543), (32, 8, 128, 544, 511), (4, 2, 64, 130, 0),
-                                              (4, 2, 64, 130, 64), (8, 8, 256, 70, 69), (12, 2, 128, 200, 150)])
+                                              (4, 2, 64, 130, 64), (8, 8, 256, 70, 69), (12, 2, 128, 200, 150),
+                                              (32, 8, 128, 1300, 1200), (4, 2, 64, 2100, 2099),
+                                              (8, 8, 256, 600, 599)])
 def test_decode_attention(gpu, dtype, hq, hk, d, lmax, pos):
     g = torch.Generator().manual_seed(pos + d)
     q = torch.randn(hq, d, generator=g).to(DT[dtype])
@@ -60,7 +62,8 @@ def test_decode_attention(gpu, dtype, hq, hk, d, lmax, pos):
 @pytest.mark.parametrize("hq,hk,d,lmax,pos,rope_mode", [(32, 8, 128, 544, 543, 1), (32, 8, 128, 544, 300, 1),
                                                         (32, 8, 128, 544, 40, 1),
                                                         (4, 2, 64, 130, 0, 1), (12, 2, 128, 200, 150, 2),
-                                                        (8, 8, 256, 70, 69, 1)])
+                                                        (8, 8, 256, 70, 69, 1), (32, 8, 128, 1300, 1100, 1),
+                                                        (4, 2, 64, 2100, 2047, 2)])
 def test_decode_attention_rope(gpu, dtype, hq, hk, d, lmax, pos, rope_mode):
     """Attention with the q/k norm, RoPE and the KV-cache write of ``pos`` folded
     in, against the float64 oracle of the same chain: per-head RMSNorm + RoPE
