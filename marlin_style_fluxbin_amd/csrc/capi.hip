@@ -403,12 +403,23 @@ int run_rank_one(const void* x, int x_dtype, const uint8_t* planes, const void* 
   return launch_finish(a.partial, out, x_dtype, p.splits, O, s);
 }
 
-// Hybrid layout: the rank-one tiling rules with a smaller staging cap (3.3 KB of
-// LDS per batch) and at most `max_splits` K splits (the caller's workspace).
-TwoBasePlan default_hybrid_plan(int O, int G, int max_splits, int max_tiles = 3) {
+// Hybrid layout.  The kernel holds 134 VGPRs per lane, so a CU runs 12 of its
+// waves; a plan keeps every workgroup resident in one round where the rows
+// allow it: nt = ceil(tiles / CUs) 16-row tiles per workgroup (at most
+// max_tiles), and K parts nk = 4 for nt = 2..3, 2 for nt = 4..6 (8 or 12 waves
+// per workgroup), nt = 1: 8 (4 when the split has fewer than 8 batches).  The
+// results do not depend on the plan (the kernel sums eight virtual K parts in a
+// fixed order).  Measured at the Qwen3-8B decode launches (rotating payloads,
+// HIP graph): q|k|v 6144 x 4096 11.5 -> 8.4 us ((1, 8) -> (2, 4)), gate|up
+// 24576 x 4096 17.8 -> 13.7 us ((3, 4) -> (6, 2)); o and down stay (1, 8).
+// At most `max_splits` K splits (the caller's workspace); staging holds 3.3 KB
+// of LDS per batch.
+constexpr int kHybridMaxTiles = 6;
+
+TwoBasePlan default_hybrid_plan(int O, int G, int max_splits, int max_tiles = kHybridMaxTiles) {
   const int cus = device_cu_count();
   const int tiles_total = (O + 15) / 16;
-  int nt = tiles_total / cus;
+  int nt = (tiles_total + cus - 1) / cus;
   nt = nt < 1 ? 1 : (nt > max_tiles ? max_tiles : nt);
   const int row_blocks = (tiles_total + nt - 1) / nt;
   const int batches = (G + 3) / 4;
@@ -416,7 +427,7 @@ TwoBasePlan default_hybrid_plan(int O, int G, int max_splits, int max_tiles = 3)
   if (row_blocks < 32) splits = (64 + row_blocks - 1) / row_blocks;
   if (splits > batches) splits = batches;
   int per_split = (batches + splits - 1) / splits;
-  const int nk = (nt == 1 && per_split >= 8) ? 8 : 4;
+  const int nk = nt == 1 ? (per_split >= 8 ? 8 : 4) : (nt <= 3 ? 4 : 2);
   const int cap = std::min(fx::kHybridMaxBatches, 4 * nt * nk);
   if (per_split > cap) {
     splits = (batches + cap - 1) / cap;
@@ -470,13 +481,15 @@ int run_hybrid(const void* x, int x_dtype, int n_seg, const int* seg_rows, const
   const int G = K / 128;
   if (size_t(G) * size_t(O) * 32 > 0x7fffffffu) return fail(FX_EINVAL, "payload exceeds 2 GiB");
   const int max_splits = int(std::min<size_t>(workspace ? workspace_bytes / (size_t(O) * 4) : 0, 1 << 20));
+  // a workgroup's rows must lie in one segment: every segment start on its
+  // 16 * tiles grid (fewer tiles per workgroup until they are)
   TwoBasePlan p = default_hybrid_plan(O, G, max_splits < 1 ? 1 : max_splits);
-  // a workgroup's rows must lie in one segment: starts on its 16 * tiles grid
-  for (int i = 1, start = seg_rows[0]; i < n_seg; start += seg_rows[i], ++i)
-    if (start % (16 * p.nt)) {
-      p = default_hybrid_plan(O, G, max_splits < 1 ? 1 : max_splits, 1);
-      break;
-    }
+  for (;;) {
+    bool aligned = true;
+    for (int i = 1, start = seg_rows[0]; i < n_seg; start += seg_rows[i], ++i) aligned = aligned && start % (16 * p.nt) == 0;
+    if (aligned || p.nt == 1) break;
+    p = default_hybrid_plan(O, G, max_splits < 1 ? 1 : max_splits, p.nt - 1);
+  }
   const size_t need = two_base_workspace(O, p);
   if (need > 0) {
     if (!workspace || workspace_bytes < need)

@@ -44,6 +44,13 @@ typedef int hy_i32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr float kHyMagic = 12583040.0f;  // 1.5 * 2^23 + 128: low 16 bits of the sum are v + 128
 constexpr int kHyMaxUnits = 4;           // staged batches per wave
+// The K reduction always runs in the order of eight K parts: batch b of a split
+// feeds virtual part b % 8, each part accumulates its batches in order, and the
+// eight part sums are added in part order.  A plan with NK < 8 waves per tile
+// keeps 8 / NK accumulator sets per wave, so every plan (tiles, K parts) gives
+// the same bits and a fused q|k|v launch matches the separate projections
+// whatever plan each one picks.
+constexpr int kHyVirtualParts = 8;
 
 __device__ __forceinline__ int hy_exponent(float max_abs) {
   if (!(max_abs > 0.f)) return 0;
@@ -67,7 +74,9 @@ __global__ __launch_bounds__(NT * NK * 64) void hybrid_kernel(HybridArgs a) {
   __shared__ float fref[kHybridMaxBatches][4][2];  // the same for the refinement operands
   __shared__ float ug[kHybridMaxBatches][4][2];    // U per (batch, group slot, base)
   __shared__ float vg[kHybridMaxBatches][4][2];    // refinement U per (batch, slot, base)
-  __shared__ float red[NK][16 * NT];
+  __shared__ float red[kHyVirtualParts][16 * NT];
+  static_assert(kHyVirtualParts % NK == 0, "K parts must divide the virtual parts");
+  constexpr int VS = kHyVirtualParts / NK;  // accumulator sets per wave
   // one scalar-load round for every argument, before any branch
   asm volatile("" ::"s"(a.x), "s"(a.codes), "s"(a.rows), "s"(a.cols), "s"(a.idx), "s"(a.scodes), "s"(a.srows),
                "s"(a.scols), "s"(a.partial), "s"(a.out), "s"(a.O), "s"(a.G), "s"(a.gps), "s"(a.row_blocks),
@@ -219,8 +228,15 @@ __global__ __launch_bounds__(NT * NK * 64) void hybrid_kernel(HybridArgs a) {
   }
   __syncthreads();
 
-  // ---- main loop: eight bit positions + the refinement per batch and base
-  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  // ---- main loop: eight bit positions + the refinement per batch and base.
+  // Batch i of this wave (virtual part kpart + NK (i % VS)) accumulates into
+  // acc[0]; with VS > 1 the sets rotate after every batch (register moves), so
+  // after `mine` batches set p holds virtual part kpart + NK ((p + mine) % VS).
+  float acc[VS][4];
+#pragma unroll
+  for (int v = 0; v < VS; ++v)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[v][j] = 0.f;
   const u32x4_t* zp = &zero16;
   const bool main_lane = !is_ref && dslot == kb;
   const bool ref_lane = is_ref && dslot == kb;
@@ -262,23 +278,37 @@ __global__ __launch_bounds__(NT * NK * 64) void hybrid_kernel(HybridArgs a) {
                          __uint_as_float(r1.x), __uint_as_float(r1.y), __uint_as_float(r1.z), __uint_as_float(r1.w)};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      acc[j] = fmaf(rs[2 * j], fmaf(2.f * float(d0[j]), s0, -u0), acc[j]);
-      acc[j] = fmaf(rs[2 * j + 1], fmaf(2.f * float(d1[j]), s1, -u1), acc[j]);
+      acc[0][j] = fmaf(rs[2 * j], fmaf(2.f * float(d0[j]), s0, -u0), acc[0][j]);
+      acc[0][j] = fmaf(rs[2 * j + 1], fmaf(2.f * float(d1[j]), s1, -u1), acc[0][j]);
+    }
+    if constexpr (VS > 1) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float first = acc[0][j];
+#pragma unroll
+        for (int v = 0; v + 1 < VS; ++v) acc[v][j] = acc[v + 1][j];
+        acc[VS - 1][j] = first;
+      }
     }
   }
 
-  // ---- rows 4 kb + j: sum over the 16 columns of the quad, then over the K parts
+  // ---- rows 4 kb + j: sum over the 16 columns of the quad, then over the
+  // virtual K parts in order
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const float s = row16_sum(acc[j]);
-    if (c == 0) red[kpart][16 * tile + 4 * kb + j] = s;
+  for (int v = 0; v < VS; ++v) {
+    const int part = kpart + NK * ((v + mine) % VS);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float s = row16_sum(acc[v][j]);
+      if (c == 0) red[part][16 * tile + 4 * kb + j] = s;
+    }
   }
   __syncthreads();
   const int orow = row0 + t;
   if (t < 16 * NT && orow < O) {
     float y = 0.f;
 #pragma unroll
-    for (int q = 0; q < NK; ++q) y += red[q][t];
+    for (int q = 0; q < kHyVirtualParts; ++q) y += red[q][t];
     if (a.partial)
       a.partial[size_t(split) * O + orow] = y;
     else
@@ -310,6 +340,9 @@ bool dispatch_hybrid(int xdt, int tiles, int kparts, const HybridArgs& a, dim3 g
   if (tiles == 1 && kparts == 8) return hybrid_for_dtype<1, 8>(xdt, a, grid, s);
   if (tiles == 2 && kparts == 4) return hybrid_for_dtype<2, 4>(xdt, a, grid, s);
   if (tiles == 3 && kparts == 4) return hybrid_for_dtype<3, 4>(xdt, a, grid, s);
+  if (tiles == 4 && kparts == 2) return hybrid_for_dtype<4, 2>(xdt, a, grid, s);
+  if (tiles == 5 && kparts == 2) return hybrid_for_dtype<5, 2>(xdt, a, grid, s);
+  if (tiles == 6 && kparts == 2) return hybrid_for_dtype<6, 2>(xdt, a, grid, s);
   return false;
 }
 

@@ -73,7 +73,7 @@ constexpr int kHybridMaxBatches = 36;  // four-group batches one workgroup stage
 // (256 B) and activations (1 KB) per staged batch.
 inline size_t hybrid_lds_bytes(int gps) { return size_t(gps / 4) * (2048 + 256 + 1024); }
 
-// Instantiated (tiles, kparts): (1,4) (1,8) (2,4) (3,4).  False otherwise.
+// Instantiated (tiles, kparts): (1,4) (1,8) (2,4) (3,4) (4,2) (5,2) (6,2).  False otherwise.
 bool dispatch_hybrid(int xdt, int tiles, int kparts, const HybridArgs& a, dim3 grid, hipStream_t s);
 
 }  // namespace fx

@@ -187,8 +187,10 @@ def test_out_of_range_refinement_index_gives_nan(gpu):
                                       ((48,), 5), ((16, 48, 32, 64), 2)])
 def test_segments_launch_equals_separate_calls(gpu, widths, g):
     """q|k|v / gate|up as one fx_hybrid_gemv_segments launch: every row has the bits
-    of its own module's fx_hybrid_gemv call (segment starts that do not sit on the
-    tall-tile grid, 48 | 16-multiples, fall back to 16-row tiles)."""
+    of its own module's fx_hybrid_gemv call although the plans differ (q|k|v 6144
+    rows: 2 tiles x 4 K parts per workgroup, q alone 1 x 8; gate|up 24576 rows:
+    6 x 2, gate alone 3 x 4), since the kernel sums eight virtual K parts in a
+    fixed order; segment starts off the tall-tile grid fall back to fewer tiles."""
     modules = [d.PackedHybridLinear(_payload(o, g, seed=31 + i), kernel="v5_p1024").to(gpu)
                for i, o in enumerate(widths)]
     x = torch.randn(1, g * 128, generator=torch.Generator().manual_seed(4)).to(torch.bfloat16).to(gpu)
