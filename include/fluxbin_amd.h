@@ -378,6 +378,32 @@ int fx_hybrid_gemv_segments(const void *x, int x_dtype, int n_segments, const in
                             const int16_t *const *indices, const uint8_t *sparse_codes, const float *sparse_rows,
                             const float *const *sparse_columns, void *workspace, size_t workspace_bytes, void *out,
                             int K, void *stream);
+/*
+ * fx_hybrid_gemv with the decoder layer's residual add folded in (no single
+ * reference entry point: it replaces m1_out for o_proj / down_proj plus the
+ * following add of HF Qwen3DecoderLayer): out = round(residual + round(y)) in
+ * x_dtype (residual may alias out) and tile_sumsq[i] = the fp32 sum of out^2 over
+ * rows 16i .. 16i+15, the partials the next fx_hybrid_gemv_segments_rmsnormed
+ * reads.  One K split (no workspace): fails when K needs more.
+ */
+int fx_hybrid_gemv_residual(const void *x, int x_dtype, const uint8_t *codes, const float *rows,
+                            const float *columns, const int16_t *indices, const uint8_t *sparse_codes,
+                            const float *sparse_rows, const float *sparse_columns, const void *residual, void *out,
+                            float *tile_sumsq, int O, int K, void *stream);
+/*
+ * fx_hybrid_gemv_segments of RMSNorm(h): no single reference entry point; it
+ * replaces the input_layernorm / post_attention_layernorm of HF Qwen3DecoderLayer
+ * plus the projections' m1_out calls.  The kernel normalises h [K] on the fly as
+ * Qwen3RMSNorm does, x = round(w * round(h * rsqrt(sum(tile_sumsq) / K + eps))),
+ * from n_tiles = ceil(K / 16) partial sums of h^2 (fx_hybrid_gemv_residual's or
+ * fx_decode_embed's), norm_weight [K] 16-byte aligned, K <= 4096.
+ */
+int fx_hybrid_gemv_segments_rmsnormed(const void *h, int x_dtype, int n_segments, const int *segment_rows,
+                                      const uint8_t *codes, const float *rows, const float *const *columns,
+                                      const int16_t *const *indices, const uint8_t *sparse_codes,
+                                      const float *sparse_rows, const float *const *sparse_columns,
+                                      const float *tile_sumsq, int n_tiles, const void *norm_weight, float eps,
+                                      void *workspace, size_t workspace_bytes, void *out, int K, void *stream);
 
 #ifdef __cplusplus
 }

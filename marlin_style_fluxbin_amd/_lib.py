@@ -15,7 +15,7 @@ from pathlib import Path
 import torch
 
 LIBRARY_PATH = Path(__file__).resolve().parent / "libfluxbin_amd.so"
-ABI_VERSION = 13
+ABI_VERSION = 14
 PAYLOAD_PLANAR, PAYLOAD_FIELDS = 0, 1  # FX_W3_PLANAR / FX_W3_FIELDS
 
 FX_F32, FX_F16, FX_BF16 = 0, 1, 2
@@ -66,6 +66,9 @@ SIGNATURES: dict[str, tuple] = {
     "fx_hybrid_gemv_workspace_bytes": (_sz, [_i, _i]),
     "fx_hybrid_gemv": (_i, [_p, _i, _p, _p, _p, _p, _p, _p, _p, _p, _sz, _p, _i, _i, _p]),
     "fx_hybrid_gemv_segments": (_i, [_p, _i, _i, _p, _p, _p, _p, _p, _p, _p, _p, _p, _sz, _p, _i, _p]),
+    "fx_hybrid_gemv_residual": (_i, [_p, _i, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _p]),
+    "fx_hybrid_gemv_segments_rmsnormed": (_i, [_p, _i, _i, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i, _p, _f, _p, _sz,
+                                                _p, _i, _p]),
 }
 
 _lock = threading.Lock()

@@ -452,7 +452,7 @@ TwoBasePlan default_hybrid_plan(int O, int G, int max_splits, int max_tiles = kH
 int run_hybrid(const void* x, int x_dtype, int n_seg, const int* seg_rows, const uint8_t* codes, const float* rows,
                const float* const* cols, const int16_t* const* idx, const uint8_t* scodes, const float* srows,
                const float* const* scols, void* workspace, size_t workspace_bytes, void* out, int K,
-               hipStream_t s) {
+               const fx::ResidualArgs& res, hipStream_t s) {
   if (n_seg < 1 || n_seg > fx::kHybridMaxSegments)
     return fail(FX_EINVAL, "n_segments must be in [1, %d], got %d", fx::kHybridMaxSegments, n_seg);
   if (!seg_rows || !cols || !idx || !scols) return fail(FX_EINVAL, "segment arrays must be non-null");
@@ -480,7 +480,9 @@ int run_hybrid(const void* x, int x_dtype, int n_seg, const int* seg_rows, const
     return fail(FX_EINVAL, "x, codes, rows, columns and sparse rows must be 16-byte aligned");
   const int G = K / 128;
   if (size_t(G) * size_t(O) * 32 > 0x7fffffffu) return fail(FX_EINVAL, "payload exceeds 2 GiB");
-  const int max_splits = int(std::min<size_t>(workspace ? workspace_bytes / (size_t(O) * 4) : 0, 1 << 20));
+  // the residual epilogue writes the output itself: one K split
+  const int max_splits = res.ep_residual ? 1
+                                         : int(std::min<size_t>(workspace ? workspace_bytes / (size_t(O) * 4) : 0, 1 << 20));
   // a workgroup's rows must lie in one segment: every segment start on its
   // 16 * tiles grid (fewer tiles per workgroup until they are)
   TwoBasePlan p = default_hybrid_plan(O, G, max_splits < 1 ? 1 : max_splits);
@@ -490,6 +492,8 @@ int run_hybrid(const void* x, int x_dtype, int n_seg, const int* seg_rows, const
     if (aligned || p.nt == 1) break;
     p = default_hybrid_plan(O, G, max_splits < 1 ? 1 : max_splits, p.nt - 1);
   }
+  if (res.ep_residual && p.splits > 1)
+    return fail(FX_EINVAL, "K = %d needs %d K splits; the residual epilogue takes one", K, p.splits);
   const size_t need = two_base_workspace(O, p);
   if (need > 0) {
     if (!workspace || workspace_bytes < need)
@@ -498,6 +502,7 @@ int run_hybrid(const void* x, int x_dtype, int n_seg, const int* seg_rows, const
       return fail(FX_EINVAL, "workspace must be 16-byte aligned");
   }
   fx::HybridArgs a{};
+  a.res = res;
   a.x = static_cast<const uint16_t*>(x);
   a.codes = codes;
   a.rows = rows;
@@ -521,7 +526,7 @@ int run_hybrid(const void* x, int x_dtype, int n_seg, const int* seg_rows, const
     a.seg_scols[i] = used ? scols[i] : scols[0];
     if (used) start += seg_rows[i];
   }
-  if (!fx::dispatch_hybrid(x_dtype, p.nt, p.nk, a, dim3(p.row_blocks, p.splits), s))
+  if (!fx::dispatch_hybrid(x_dtype, p.nt, p.nk, res.pro_partial != nullptr, a, dim3(p.row_blocks, p.splits), s))
     return fail(FX_EINVAL, "no hybrid kernel for tiles %d kparts %d", p.nt, p.nk);
   int rc = check_launch("hybrid_kernel");
   if (rc || p.splits == 1) return rc;
@@ -542,7 +547,7 @@ bool two_base_config(int O, int G, int waves, int prefetch, int groups_per_split
 
 extern "C" {
 
-int fx_abi_version(void) { return 13; }
+int fx_abi_version(void) { return 14; }
 
 const char* fx_last_error(void) { return g_error; }
 
@@ -1244,7 +1249,7 @@ int fx_hybrid_gemv(const void* x, int x_dtype, const uint8_t* codes, const float
   if (!columns || !indices || !sparse_columns)
     return fail(FX_EINVAL, "x, every layout field and out must be non-null");
   return run_hybrid(x, x_dtype, 1, &O, codes, rows, &columns, &indices, sparse_codes, sparse_rows, &sparse_columns,
-                    workspace, workspace_bytes, out, K, static_cast<hipStream_t>(stream));
+                    workspace, workspace_bytes, out, K, fx::ResidualArgs{}, static_cast<hipStream_t>(stream));
 }
 
 int fx_hybrid_gemv_segments(const void* x, int x_dtype, int n_segments, const int* segment_rows,
@@ -1253,7 +1258,42 @@ int fx_hybrid_gemv_segments(const void* x, int x_dtype, int n_segments, const in
                             const float* const* sparse_columns, void* workspace, size_t workspace_bytes, void* out,
                             int K, void* stream) {
   return run_hybrid(x, x_dtype, n_segments, segment_rows, codes, rows, columns, indices, sparse_codes, sparse_rows,
-                    sparse_columns, workspace, workspace_bytes, out, K, static_cast<hipStream_t>(stream));
+                    sparse_columns, workspace, workspace_bytes, out, K, fx::ResidualArgs{},
+                    static_cast<hipStream_t>(stream));
+}
+
+int fx_hybrid_gemv_residual(const void* x, int x_dtype, const uint8_t* codes, const float* rows,
+                            const float* columns, const int16_t* indices, const uint8_t* sparse_codes,
+                            const float* sparse_rows, const float* sparse_columns, const void* residual, void* out,
+                            float* tile_sumsq, int O, int K, void* stream) {
+  if (O < 1 || O > 65536) return fail(FX_EINVAL, "O must be in [1, 65536], got %d", O);
+  if (!columns || !indices || !sparse_columns)
+    return fail(FX_EINVAL, "x, every layout field and out must be non-null");
+  if (!residual || !out || !tile_sumsq) return fail(FX_EINVAL, "residual, out and tile_sumsq must be non-null");
+  fx::ResidualArgs res{};
+  res.ep_residual = static_cast<const uint16_t*>(residual);
+  res.ep_partial = tile_sumsq;
+  return run_hybrid(x, x_dtype, 1, &O, codes, rows, &columns, &indices, sparse_codes, sparse_rows, &sparse_columns,
+                    nullptr, 0, out, K, res, static_cast<hipStream_t>(stream));
+}
+
+int fx_hybrid_gemv_segments_rmsnormed(const void* h, int x_dtype, int n_segments, const int* segment_rows,
+                                      const uint8_t* codes, const float* rows, const float* const* columns,
+                                      const int16_t* const* indices, const uint8_t* sparse_codes,
+                                      const float* sparse_rows, const float* const* sparse_columns,
+                                      const float* tile_sumsq, int n_tiles, const void* norm_weight, float eps,
+                                      void* workspace, size_t workspace_bytes, void* out, int K, void* stream) {
+  if (!tile_sumsq || !norm_weight) return fail(FX_EINVAL, "tile_sumsq and norm weight must be non-null");
+  if (n_tiles != (K + 15) / 16) return fail(FX_EINVAL, "n_tiles must be ceil(K / 16) = %d, got %d", (K + 15) / 16, n_tiles);
+  if (n_tiles > 64 * fx::kMaxNormPartialsPerLane) return fail(FX_EINVAL, "K = %d too large for the normalising prologue", K);
+  if (reinterpret_cast<uintptr_t>(norm_weight) % 16 != 0) return fail(FX_EINVAL, "norm weight must be 16-byte aligned");
+  fx::ResidualArgs res{};
+  res.pro_partial = tile_sumsq;
+  res.pro_n = n_tiles;
+  res.pro_weight = static_cast<const uint16_t*>(norm_weight);
+  res.pro_eps = eps;
+  return run_hybrid(h, x_dtype, n_segments, segment_rows, codes, rows, columns, indices, sparse_codes, sparse_rows,
+                    sparse_columns, workspace, workspace_bytes, out, K, res, static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

@@ -65,7 +65,7 @@ __device__ __forceinline__ u32x4_t refine_operand(unsigned byte) {
                  0u, 0u};
 }
 
-template <int NT, int NK, int XDT>
+template <int NT, int NK, int XDT, bool NORMIN>
 __global__ __launch_bounds__(NT * NK * 64) void hybrid_kernel(HybridArgs a) {
   constexpr int NW = NT * NK;
   extern __shared__ u32x4_t hy_dyn[];
@@ -119,9 +119,21 @@ __global__ __launch_bounds__(NT * NK * 64) void hybrid_kernel(HybridArgs a) {
   const auto rsrow = buffer_resource(a.srows, size_t(G) * O * 2 * 4);
   const int r = lane & 15, kb = lane >> 4, c = lane & 15;
 
-  // ---- loads in consumption order (raw bits; nothing waits until all are issued)
+  // ---- loads in consumption order (raw bits; nothing waits until all are issued):
+  // NORMIN first the tile partials of h (each wave reduces them itself, in a
+  // fixed order: lane l adds partials l, l + 64, ..., then the wave total)
+  float pp[kMaxNormPartialsPerLane];
+  if constexpr (NORMIN) {
+    const auto rpp = buffer_resource(a.res.pro_partial, size_t(a.res.pro_n) * 4);
+#pragma unroll
+    for (int k = 0; k < kMaxNormPartialsPerLane; ++k) {
+      const int i = lane + 64 * k;
+      pp[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rpp, i < a.res.pro_n ? i * 4 : kOutOfRange, 0, 0));
+    }
+  }
+  const auto rwn = buffer_resource(NORMIN ? (const void*)a.res.pro_weight : (const void*)a.x, NORMIN ? size_t(K) * 2 : 0);
   const int staged = wave < nbatch ? (nbatch - wave + NW - 1) / NW : 0;
-  u32x4_t sx[kHyMaxUnits], sc[kHyMaxUnits][4];
+  u32x4_t sx[kHyMaxUnits], sc[kHyMaxUnits][4], swn[kHyMaxUnits];
   unsigned sidx[kHyMaxUnits], sscol[kHyMaxUnits];
 #pragma unroll
   for (int q = 0; q < kHyMaxUnits; ++q) {
@@ -129,6 +141,7 @@ __global__ __launch_bounds__(NT * NK * 64) void hybrid_kernel(HybridArgs a) {
     const bool real = q < staged && g < g1;
     const int col = g * 128 + 8 * r;
     sx[q] = load_b128(rx, real ? col * 2 : kOutOfRange, 0);
+    if constexpr (NORMIN) swn[q] = load_b128(rwn, real ? col * 2 : kOutOfRange, 0);
 #pragma unroll
     for (int h = 0; h < 4; ++h) sc[q][h] = load_b128(rcol, real ? (col * 2 + 4 * h) * 4 : kOutOfRange, 0);
     sidx[q] = __builtin_amdgcn_raw_buffer_load_b16(ridx, real ? (g * 8 + (r & 7)) * 2 : kOutOfRange, 0, 0);
@@ -164,14 +177,34 @@ __global__ __launch_bounds__(NT * NK * 64) void hybrid_kernel(HybridArgs a) {
 
   // ---- staging: wave w stages batches w, w + NW, ...
   if (t == 0) zero16 = u32x4_t{0u, 0u, 0u, 0u};
+  float norm_inv = 1.f;
+  if constexpr (NORMIN) {
+    float total = 0.f;
+#pragma unroll
+    for (int k = 0; k < kMaxNormPartialsPerLane; ++k) total += pp[k];
+    norm_inv = rsqrtf(wave_total(total) / float(K) + a.res.pro_eps);
+  }
 #pragma unroll
   for (int q = 0; q < kHyMaxUnits; ++q) {
     if (q < staged) {
       const int bt = wave + q * NW;
-      xs[bt * 64 + lane] = sx[q];
       float xv[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) xv[j] = to_f32<XDT>(uint16_t(sx[q][j >> 1] >> (16 * (j & 1))));
+      if constexpr (NORMIN) {  // Qwen3RMSNorm: round(w * round(h * inv)), staged as the activation
+        u32x4_t nb;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          xv[j] = round_to<XDT>(to_f32<XDT>(uint16_t(swn[q][j >> 1] >> (16 * (j & 1)))) *
+                                round_to<XDT>(xv[j] * norm_inv));
+          const unsigned bits = from_f32<XDT>(xv[j]);
+          if (j & 1) nb[j >> 1] |= bits << 16;
+          else nb[j >> 1] = bits;
+        }
+        xs[bt * 64 + lane] = nb;
+      } else {
+        xs[bt * 64 + lane] = sx[q];
+      }
 #pragma unroll
       for (int b = 0; b < 2; ++b) {
         float u[8], mx = 0.f;
@@ -305,6 +338,24 @@ __global__ __launch_bounds__(NT * NK * 64) void hybrid_kernel(HybridArgs a) {
   }
   __syncthreads();
   const int orow = row0 + t;
+  if (a.res.ep_residual) {
+    // one K split: out = round(residual + round(y)) for the workgroup's rows and,
+    // per 16-row tile (16 consecutive lanes), the sum of out^2 (DPP row sum)
+    if (t < (16 * NT + 63) / 64 * 64) {
+      float h2 = 0.f;
+      if (t < 16 * NT && orow < O) {
+        float y = 0.f;
+#pragma unroll
+        for (int q = 0; q < kHyVirtualParts; ++q) y += red[q][t];
+        const float h = round_to<XDT>(to_f32<XDT>(a.res.ep_residual[orow]) + round_to<XDT>(y));
+        a.out[orow] = from_f32<XDT>(h);
+        h2 = h * h;
+      }
+      h2 = row16_sum(h2);
+      if ((t & 15) == 0 && t < 16 * NT && orow < O) a.res.ep_partial[orow / 16] = h2;
+    }
+    return;
+  }
   if (t < 16 * NT && orow < O) {
     float y = 0.f;
 #pragma unroll
@@ -317,32 +368,34 @@ __global__ __launch_bounds__(NT * NK * 64) void hybrid_kernel(HybridArgs a) {
 }
 
 // Dynamic LDS beyond the default 64 KB must be allowed per kernel, once.
-template <int NT, int NK, int XDT>
+template <int NT, int NK, int XDT, bool NORMIN>
 bool hybrid_launch(const HybridArgs& a, dim3 grid, hipStream_t s) {
   static const bool allowed =
-      hipFuncSetAttribute(reinterpret_cast<const void*>(&hybrid_kernel<NT, NK, XDT>),
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&hybrid_kernel<NT, NK, XDT, NORMIN>),
                           hipFuncAttributeMaxDynamicSharedMemorySize,
                           int(hybrid_lds_bytes(4 * kHybridMaxBatches))) == hipSuccess;
   if (!allowed) return false;
-  hipLaunchKernelGGL((hybrid_kernel<NT, NK, XDT>), grid, dim3(NT * NK * 64), hybrid_lds_bytes(a.gps), s, a);
+  hipLaunchKernelGGL((hybrid_kernel<NT, NK, XDT, NORMIN>), grid, dim3(NT * NK * 64), hybrid_lds_bytes(a.gps), s, a);
   return true;
 }
 
 template <int NT, int NK>
-bool hybrid_for_dtype(int xdt, const HybridArgs& a, dim3 grid, hipStream_t s) {
-  if (xdt == kBF16) return hybrid_launch<NT, NK, kBF16>(a, grid, s);
-  if (xdt == kF16) return hybrid_launch<NT, NK, kF16>(a, grid, s);
+bool hybrid_for_dtype(int xdt, bool normin, const HybridArgs& a, dim3 grid, hipStream_t s) {
+  if (xdt == kBF16) return normin ? hybrid_launch<NT, NK, kBF16, true>(a, grid, s)
+                                  : hybrid_launch<NT, NK, kBF16, false>(a, grid, s);
+  if (xdt == kF16) return normin ? hybrid_launch<NT, NK, kF16, true>(a, grid, s)
+                                 : hybrid_launch<NT, NK, kF16, false>(a, grid, s);
   return false;
 }
 
-bool dispatch_hybrid(int xdt, int tiles, int kparts, const HybridArgs& a, dim3 grid, hipStream_t s) {
-  if (tiles == 1 && kparts == 4) return hybrid_for_dtype<1, 4>(xdt, a, grid, s);
-  if (tiles == 1 && kparts == 8) return hybrid_for_dtype<1, 8>(xdt, a, grid, s);
-  if (tiles == 2 && kparts == 4) return hybrid_for_dtype<2, 4>(xdt, a, grid, s);
-  if (tiles == 3 && kparts == 4) return hybrid_for_dtype<3, 4>(xdt, a, grid, s);
-  if (tiles == 4 && kparts == 2) return hybrid_for_dtype<4, 2>(xdt, a, grid, s);
-  if (tiles == 5 && kparts == 2) return hybrid_for_dtype<5, 2>(xdt, a, grid, s);
-  if (tiles == 6 && kparts == 2) return hybrid_for_dtype<6, 2>(xdt, a, grid, s);
+bool dispatch_hybrid(int xdt, int tiles, int kparts, bool normin, const HybridArgs& a, dim3 grid, hipStream_t s) {
+  if (tiles == 1 && kparts == 4) return hybrid_for_dtype<1, 4>(xdt, normin, a, grid, s);
+  if (tiles == 1 && kparts == 8) return hybrid_for_dtype<1, 8>(xdt, normin, a, grid, s);
+  if (tiles == 2 && kparts == 4) return hybrid_for_dtype<2, 4>(xdt, normin, a, grid, s);
+  if (tiles == 3 && kparts == 4) return hybrid_for_dtype<3, 4>(xdt, normin, a, grid, s);
+  if (tiles == 4 && kparts == 2) return hybrid_for_dtype<4, 2>(xdt, normin, a, grid, s);
+  if (tiles == 5 && kparts == 2) return hybrid_for_dtype<5, 2>(xdt, normin, a, grid, s);
+  if (tiles == 6 && kparts == 2) return hybrid_for_dtype<6, 2>(xdt, normin, a, grid, s);
   return false;
 }
 

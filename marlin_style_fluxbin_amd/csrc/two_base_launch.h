@@ -2,6 +2,7 @@
 // the C ABI.
 #pragma once
 #include "common.h"
+#include "w3_mfma_launch.h"  // ResidualArgs: the decoder residual stream around a GEMV
 
 namespace fx {
 
@@ -65,6 +66,11 @@ struct HybridArgs {
   const float* seg_cols[kHybridMaxSegments];
   const int16_t* seg_idx[kHybridMaxSegments];
   const float* seg_scols[kHybridMaxSegments];
+  // Decoder residual stream (one K split): res.ep_residual set: out =
+  // round(residual + round(y)) and per-16-row sums of out^2 into res.ep_partial;
+  // the normalising instantiations read x = round(w * round(h * rsqrt(sum(
+  // res.pro_partial) / K + eps))), the RMSNorm of h, as the W3 kernel does.
+  ResidualArgs res;
 };
 
 constexpr int kHybridMaxBatches = 36;  // four-group batches one workgroup stages (117 KB LDS)
@@ -73,7 +79,9 @@ constexpr int kHybridMaxBatches = 36;  // four-group batches one workgroup stage
 // (256 B) and activations (1 KB) per staged batch.
 inline size_t hybrid_lds_bytes(int gps) { return size_t(gps / 4) * (2048 + 256 + 1024); }
 
-// Instantiated (tiles, kparts): (1,4) (1,8) (2,4) (3,4) (4,2) (5,2) (6,2).  False otherwise.
-bool dispatch_hybrid(int xdt, int tiles, int kparts, const HybridArgs& a, dim3 grid, hipStream_t s);
+// Instantiated (tiles, kparts): (1,4) (1,8) (2,4) (3,4) (4,2) (5,2) (6,2), each
+// plain and normalising (normin: a.x holds h, a.res the prologue's partials,
+// weight and eps).  False otherwise.
+bool dispatch_hybrid(int xdt, int tiles, int kparts, bool normin, const HybridArgs& a, dim3 grid, hipStream_t s);
 
 }  // namespace fx

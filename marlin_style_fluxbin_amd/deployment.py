@@ -391,12 +391,15 @@ class HybridSegmentsGemv:
             copy = getattr(m, f"_{name}_planar")
             return getattr(m, name) if copy is None else copy
 
+        def joined(tensors):  # one module: its own (contiguous) buffer, no copy
+            return tensors[0].contiguous() if len(tensors) == 1 else torch.cat(tensors, dim=1).contiguous()
+
         self.in_features = first.in_features
         self.out_features = sum(m.out_features for m in modules)
-        self.codes = torch.cat([planar(m, "codes") for m in modules], dim=1).contiguous()
-        self.rows = torch.cat([m.rows for m in modules], dim=1).contiguous()
-        self.sparse_codes = torch.cat([planar(m, "sparse_codes") for m in modules], dim=1).contiguous()
-        self.sparse_rows = torch.cat([m.sparse_rows for m in modules], dim=1).contiguous()
+        self.codes = joined([planar(m, "codes") for m in modules])
+        self.rows = joined([m.rows for m in modules])
+        self.sparse_codes = joined([planar(m, "sparse_codes") for m in modules])
+        self.sparse_rows = joined([m.sparse_rows for m in modules])
         self._columns = [m.columns.contiguous() for m in modules]
         self._indices = [HybridExtension._sorted_columns(m.indices) for m in modules]
         self._sparse_columns = [m.sparse_columns.contiguous() for m in modules]
@@ -422,6 +425,46 @@ class HybridSegmentsGemv:
             self.sparse_rows.data_ptr(), self._scols_ptrs, None if ws is None else ws.data_ptr(),
             0 if ws is None else ws.numel() * 4, out.data_ptr(), self.in_features, _lib.stream_handle(x.device)),
             "fx_hybrid_gemv_segments")
+        return out
+
+    def rmsnormed(self, h: torch.Tensor, tile_sumsq: torch.Tensor, weight: torch.Tensor, eps: float,
+                  out: torch.Tensor) -> torch.Tensor:
+        """The GEMV of RMSNorm(h) (``fx_hybrid_gemv_segments_rmsnormed``): the kernel
+        normalises h from ``tile_sumsq``, the fp32 sums of h^2 over its 16-element
+        tiles, and the norm ``weight`` [K]."""
+        _check_m1_args(h, out, self._workspace_view, self.out_features, self.in_features)
+        if (tile_sumsq.dtype != torch.float32 or tile_sumsq.device != h.device or not tile_sumsq.is_contiguous()
+                or weight.dtype != h.dtype or weight.device != h.device or not weight.is_contiguous()):
+            raise RuntimeError("tile sums must be contiguous fp32 and the norm weight contiguous in h's dtype")
+        ws = self.workspace
+        _lib.check(self.lib.fx_hybrid_gemv_segments_rmsnormed(
+            h.data_ptr(), _lib.dtype_code(h.dtype), self._n, self._segment_rows, self.codes.data_ptr(),
+            self.rows.data_ptr(), self._cols_ptrs, self._idx_ptrs, self.sparse_codes.data_ptr(),
+            self.sparse_rows.data_ptr(), self._scols_ptrs, tile_sumsq.data_ptr(), tile_sumsq.numel(),
+            weight.data_ptr(), eps, None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel() * 4,
+            out.data_ptr(), self.in_features, _lib.stream_handle(h.device)), "fx_hybrid_gemv_segments_rmsnormed")
+        return out
+
+    def residual(self, x: torch.Tensor, residual: torch.Tensor, tile_sumsq: torch.Tensor,
+                 out: torch.Tensor | None = None) -> torch.Tensor:
+        """One module: out = round(residual + round(x @ W.T)) (``out`` None: in
+        place) and the fp32 sums of out^2 over 16-row tiles into ``tile_sumsq``
+        (``fx_hybrid_gemv_residual``)."""
+        if self._n != 1:
+            raise ValueError("the residual epilogue takes one hybrid Linear")
+        out = residual if out is None else out
+        _check_m1_args(x, out, self._workspace_view, self.out_features, self.in_features)
+        if residual.shape != out.shape or residual.dtype != out.dtype or not residual.is_contiguous():
+            raise RuntimeError("residual must match out")
+        if (tile_sumsq.dtype != torch.float32 or tile_sumsq.numel() != (self.out_features + 15) // 16
+                or not tile_sumsq.is_contiguous() or tile_sumsq.device != x.device):
+            raise RuntimeError("tile_sumsq must be contiguous fp32 [ceil(O / 16)]")
+        _lib.check(self.lib.fx_hybrid_gemv_residual(
+            x.data_ptr(), _lib.dtype_code(x.dtype), self.codes.data_ptr(), self.rows.data_ptr(),
+            self._columns[0].data_ptr(), self._indices[0].data_ptr(), self.sparse_codes.data_ptr(),
+            self.sparse_rows.data_ptr(), self._sparse_columns[0].data_ptr(), residual.data_ptr(), out.data_ptr(),
+            tile_sumsq.data_ptr(), self.out_features, self.in_features, _lib.stream_handle(x.device)),
+            "fx_hybrid_gemv_residual")
         return out
 
 

@@ -15,12 +15,14 @@ with structural W3 Linears,
 (6 launches; 5 while one split covers the context).  Each token starts with one
 launch for the embedding row and its RMSNorm statistics (which also merges the
 previous token's argmax partials) and ends with the final RMSNorm + bf16 LM head
-launch; the last token's argmax merge is one more launch per sequence.  Other Linears -- the hybrid two-base g128/s8
-format of ``PackedHybridLinear`` (``fx_hybrid_gemv``) or dense bf16 (the bf16
-arm, ``torch.matmul``) -- run between add+RMSNorm kernels and the same attention
-launches.  The
-arithmetic and rounding points are the stock HF Qwen3 modules' (RMSNorm, RoPE,
-SDPA with fp32 softmax, SwiGLU).
+launch; the last token's argmax merge is one more launch per sequence.  With
+the hybrid two-base g128/s8 Linears of ``PackedHybridLinear`` the chain is the
+same with the hybrid GEMV's normalising prologue and residual epilogue
+(``fx_hybrid_gemv_segments_rmsnormed``, ``fx_hybrid_gemv_residual``) and the
+SwiGLU as its own launch (7 per layer).  Other Linears (dense bf16, the bf16
+arm, ``torch.matmul``) run between add+RMSNorm kernels and the same attention
+launches.  The arithmetic and rounding points are the stock HF Qwen3 modules'
+(RMSNorm, RoPE, SDPA with fp32 softmax, SwiGLU).
 """
 from __future__ import annotations
 
@@ -165,22 +167,27 @@ class _GateUpSwiGLU:
 
 
 class _ResidualStream:
-    """The decoder layers' residual adds and RMSNorms threaded through the W3
-    GEMVs: the o and down GEMVs add their output into the residual in place and
-    write per-16-row sums of its squares (``fx_w3_gemv_residual``); the q|k|v and
-    gate|up GEMVs read the residual and normalise it on the fly from those sums
-    (``fx_w3_gemv_rmsnormed``).  ``None`` from :meth:`build` unless every layer's
-    o, down, q|k|v and gate|up are structural W3 (q|k|v and gate|up fused with
-    identity column order).  With ``payload_format`` fields (the default) every
-    layer's four payloads are repacked once into the field layout
-    (``fx_w3_planes_to_fields``), whose dequantization costs half the
-    instructions; the planar payloads stay as they are."""
+    """The decoder layers' residual adds and RMSNorms threaded through the GEMVs:
+    the o and down GEMVs add their output into the residual in place and write
+    per-16-row sums of its squares; the q|k|v and gate|up GEMVs read the residual
+    and normalise it on the fly from those sums.  W3 (``kind`` "w3"):
+    ``fx_w3_gemv_residual`` / ``fx_w3_gemv_rmsnormed``, gate|up with the SwiGLU
+    epilogue, when every layer's o, down, q|k|v and gate|up are structural W3
+    (q|k|v and gate|up fused with identity column order); with
+    ``payload_format`` fields (the default) every layer's four payloads are
+    repacked once into the field layout (``fx_w3_planes_to_fields``), whose
+    dequantization costs half the instructions.  Hybrid two-base (``kind``
+    "hybrid"): ``fx_hybrid_gemv_residual`` / ``fx_hybrid_gemv_segments_rmsnormed``
+    and the SwiGLU kernel, when every layer's four are hybrid Linears without
+    bias (q|k|v and gate|up fused).  ``None`` from :meth:`build` otherwise."""
 
-    def __init__(self, lib, hidden, device, payload_format):
+    def __init__(self, lib, hidden, device, payload_format, kind="w3"):
         self.lib = lib
+        self.kind = kind
         self.tiles = (hidden + 15) // 16
         self.partials = torch.zeros(self.tiles, dtype=torch.float32, device=device)
         self.format = payload_format
+        self.o_out = self.down_out = None  # hybrid: per-layer single-module launches
         # planes data_ptr -> (the planes tensor, its field-layout copy); holding the
         # planes keeps their memory from being reused by another payload, and a
         # lookup must find the same tensor object
@@ -215,6 +222,46 @@ class _ResidualStream:
 
     @staticmethod
     def build(session, payload_format=None):
+        if all(isinstance(l.self_attn.o_proj, PackedHybridLinear) for l in session.layers):
+            return _ResidualStream._build_hybrid(session)
+        return _ResidualStream._build_w3(session, payload_format)
+
+    @staticmethod
+    def _embed_ok(session):
+        table = session.embed
+        # the step's first launch reads the embedding rows as 16-byte vectors
+        return (table.is_contiguous() and table.data_ptr() % 16 == 0 and table.dtype == session.dtype
+                and session.hidden % 16 == 0)
+
+    @staticmethod
+    def _build_hybrid(session):
+        def bare(m):
+            return isinstance(m, PackedHybridLinear) and m.bias is None
+
+        if session.hidden > 4096 or not _ResidualStream._embed_ok(session):
+            return None  # the normalising prologue reads at most 256 tile sums
+        for layer, qkv, gate_up in zip(session.layers, session.qkv, session.gate_up):
+            if not (bare(layer.self_attn.o_proj) and bare(layer.mlp.down_proj)):
+                return None
+            if not all(f is not None and isinstance(f.call, HybridSegmentsGemv) for f in (qkv, gate_up)):
+                return None
+        stream = _ResidualStream(_lib.library(), session.hidden, session.device, None, kind="hybrid")
+        stream.o_out = [HybridSegmentsGemv([l.self_attn.o_proj]) for l in session.layers]
+        stream.down_out = [HybridSegmentsGemv([l.mlp.down_proj]) for l in session.layers]
+        # the residual epilogue needs one K split: try each shape once on scratch
+        for gemv in (stream.o_out[0], stream.down_out[0]):
+            x = torch.zeros(1, gemv.in_features, dtype=session.dtype, device=session.device)
+            res = torch.zeros(1, gemv.out_features, dtype=session.dtype, device=session.device)
+            sums = torch.empty((gemv.out_features + 15) // 16, dtype=torch.float32, device=session.device)
+            try:
+                gemv.residual(x, res, sums)
+            except RuntimeError:
+                return None
+        torch.cuda.synchronize(session.device)
+        return stream
+
+    @staticmethod
+    def _build_w3(session, payload_format=None):
         def structural(m):
             return isinstance(m, PackedW3Linear) and m.arithmetic == "structural" and m.bias is None
 
@@ -227,10 +274,8 @@ class _ResidualStream:
                 return None
             if swiglu.perm_ptr is not None:
                 return None
-        table = session.embed
-        if not (table.is_contiguous() and table.data_ptr() % 16 == 0 and table.dtype == session.dtype
-                and session.hidden % 16 == 0):
-            return None  # the step's first launch reads the embedding rows as 16-byte vectors
+        if not _ResidualStream._embed_ok(session):
+            return None
         fmt = _lib.PAYLOAD_FIELDS if payload_format is None else payload_format
         if any(lin["self_attn.o_proj"].gemv.perm_ptr is not None or lin["mlp.down_proj"].gemv.perm_ptr is not None
                for lin in session.lin):
@@ -267,6 +312,42 @@ class _ResidualStream:
             h.data_ptr(), _lib.dtype_code(h.dtype), self.payload(layout).data_ptr(), layout["scales"].data_ptr(),
             scale_code, zeros_ptr, self.partials.data_ptr(), self.tiles, weight.data_ptr(), eps, out.data_ptr(),
             rows, h.shape[-1], int(swiglu), self.format, _lib.stream_handle(h.device)), "fx_w3_gemv_rmsnormed")
+
+    # -- one decoder layer's four launches around the attention and the SwiGLU ------
+    def qkv_in(self, session, l):
+        """q|k|v of RMSNorm(residual) into session.qkv_out."""
+        if self.kind == "hybrid":
+            session.qkv[l].call.rmsnormed(session.residual, self.partials, session.in_norm[l], session.eps,
+                                          session.qkv_out)
+            return
+        gemv = session.qkv[l].call
+        self.normed(gemv.layout, gemv.scale_code, gemv.zeros_ptr, gemv.out_features, session.residual,
+                    session.in_norm[l], session.eps, session.qkv_out, False)
+
+    def attn_out(self, session, l):
+        """residual += o_proj(attn), with its tile sums."""
+        if self.kind == "hybrid":
+            self.o_out[l].residual(session.attn, session.residual, self.partials)
+            return
+        self.residual(session.lin[l]["self_attn.o_proj"].gemv, session.attn, session.residual)
+
+    def mlp_in(self, session, l):
+        """SiLU(gate) * up of RMSNorm(residual) into session.act."""
+        if self.kind == "hybrid":
+            session.gate_up[l].call.rmsnormed(session.residual, self.partials, session.post_norm[l], session.eps,
+                                              session.gate_up_out)
+            session._silu_mul()
+            return
+        sw = session.swiglu[l]
+        self.normed(sw.layout, sw.scale_code, sw.zeros_ptr, 2 * sw.width, session.residual, session.post_norm[l],
+                    session.eps, session.act, True)
+
+    def mlp_out(self, session, l):
+        """residual += down_proj(act), with its tile sums."""
+        if self.kind == "hybrid":
+            self.down_out[l].residual(session.act, session.residual, self.partials)
+            return
+        self.residual(session.lin[l]["mlp.down_proj"].gemv, session.act, session.residual)
 
 
 class NativeDecodeSession:
@@ -428,16 +509,12 @@ class NativeDecodeSession:
                  self.lm_ws if merge_prev else None, self.logits.shape[1] if merge_prev else 0,
                  self.predictions[i - 1] if merge_prev else None)
         pos = self.prefix_length + i
-        for l, lin in enumerate(self.lin):
-            gemv = self.qkv[l].call
-            rs.normed(gemv.layout, gemv.scale_code, gemv.zeros_ptr, gemv.out_features, self.residual,
-                      self.in_norm[l], self.eps, self.qkv_out, False)
+        for l in range(len(self.lin)):
+            rs.qkv_in(self, l)
             self._attention(l, pos)
-            rs.residual(lin["self_attn.o_proj"].gemv, self.attn, self.residual)
-            sw = self.swiglu[l]
-            rs.normed(sw.layout, sw.scale_code, sw.zeros_ptr, 2 * sw.width, self.residual, self.post_norm[l],
-                      self.eps, self.act, True)
-            rs.residual(lin["mlp.down_proj"].gemv, self.act, self.residual)
+            rs.attn_out(self, l)
+            rs.mlp_in(self, l)
+            rs.mlp_out(self, l)
             if self.layer_observer is not None:
                 self.layer_observer(i, l, self.residual)
         self._lm_head(i, self.residual, self.final_norm, merge=not split_head)

@@ -59,7 +59,9 @@ def test_hybrid_native_session_matches_hf(gpu):
         with prepared_linears(model, torch.bfloat16):
             want = hf.audit()
         native = NativeDecodeSession(model, ids, forced)
-    assert native.stream is None  # hybrid Linears take the generic chain
+    # hybrid Linears take the residual-stream chain: normalising q|k|v and gate|up
+    # launches, o and down adding into the residual, the SwiGLU kernel
+    assert native.stream is not None and native.stream.kind == "hybrid"
     eager = native.audit()
     graph = native.capture()
     assert torch.equal(graph["logits"], eager["logits"])

@@ -238,3 +238,80 @@ def test_segments_argument_checks(gpu):
     rc = lib.fx_hybrid_gemv_segments(None, 2, 0, rows, None, None, None, None, None, None, None, None, 0, None,
                                      256, None)
     assert rc == 1 and b"n_segments" in lib.fx_last_error()  # FX_EINVAL
+
+
+def _single_split_gemv(module, x):
+    """The module's GEMV with no workspace: one K split, the plan the residual
+    epilogue runs."""
+    from marlin_style_fluxbin_amd import _lib
+
+    fused = d.HybridSegmentsGemv([module])
+    y = torch.empty(1, module.out_features, dtype=x.dtype, device=x.device)
+    _lib.check(fused.lib.fx_hybrid_gemv(
+        x.data_ptr(), _lib.dtype_code(x.dtype), fused.codes.data_ptr(), fused.rows.data_ptr(),
+        fused._columns[0].data_ptr(), fused._indices[0].data_ptr(), fused.sparse_codes.data_ptr(),
+        fused.sparse_rows.data_ptr(), fused._sparse_columns[0].data_ptr(), None, 0, y.data_ptr(),
+        module.out_features, module.in_features, _lib.stream_handle(x.device)), "fx_hybrid_gemv")
+    return fused, y
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+@pytest.mark.parametrize("o,g", [(4096, 32), (4096, 96), (40, 32), (96, 3), (1040, 8)])
+def test_residual_epilogue(gpu, dtype, o, g):
+    """fx_hybrid_gemv_residual: out = round(residual + round(y)) bit for bit (the
+    single-split GEMV, then the dtype's own add), in place, and the sums of out^2
+    over 16-row tiles against float64."""
+    module = d.PackedHybridLinear(_payload(o, g, seed=o + g), kernel="v5_p1024").to(gpu)
+    gen = torch.Generator().manual_seed(o)
+    x = torch.randn(1, g * 128, generator=gen).to(DT[dtype]).to(gpu)
+    res = (torch.randn(1, o, generator=gen) * 4).to(DT[dtype]).to(gpu)
+    fused, y = _single_split_gemv(module, x)
+    want = res + y
+    tiles = (o + 15) // 16
+    sums = torch.full((tiles,), float("nan"), device=gpu)
+    got = res.clone()
+    fused.residual(x, got, sums)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    h = want.double().cpu().numpy()[0]
+    exact = np.array([np.sum(h[16 * t:16 * t + 16] ** 2) for t in range(tiles)])
+    assert np.allclose(sums.cpu().numpy(), exact, rtol=2e-6, atol=0)
+    with pytest.raises(ValueError):
+        d.HybridSegmentsGemv([module, module]).residual(x, got, sums)
+
+
+@pytest.mark.parametrize("widths,g,dtype", [((4096, 1024, 1024), 32, "bf16"), ((12288, 12288), 32, "bf16"),
+                                            ((48,), 8, "f16"), ((16, 48, 32, 64), 2, "bf16")])
+def test_rmsnormed_prologue(gpu, widths, g, dtype):
+    """fx_hybrid_gemv_segments_rmsnormed equals the RMSNorm kernel followed by the
+    plain segments launch bit for bit.  h holds small integers, so every order of
+    the fp32 sum of squares is exact and both paths form the same 1 / rms; the
+    refinement columns read the normalised activations too."""
+    from marlin_style_fluxbin_amd import _lib
+    from marlin_style_fluxbin_amd.fused_modules import rms_norm
+
+    k = g * 128
+    modules = [d.PackedHybridLinear(_payload(o, g, seed=5 + i), kernel="v5_p1024").to(gpu)
+               for i, o in enumerate(widths)]
+    fused = d.HybridSegmentsGemv(modules)
+    gen = torch.Generator().manual_seed(k)
+    h = torch.randint(-6, 7, (1, k), generator=gen).to(DT[dtype]).to(gpu)
+    weight = (1 + 0.1 * torch.randn(k, generator=gen)).to(DT[dtype]).to(gpu)
+    hs = h.double().cpu().numpy()[0]
+    sums = torch.tensor([np.sum(hs[16 * t:16 * t + 16] ** 2) for t in range((k + 15) // 16)],
+                        dtype=torch.float32, device=gpu)
+    normed = torch.empty_like(h)
+    rms_norm(h, weight, 1e-6, out=normed)
+    want = torch.empty(1, sum(widths), dtype=DT[dtype], device=gpu)
+    fused(normed, want)
+    got = torch.full_like(want, float("nan"))
+    fused.rmsnormed(h, sums, weight, 1e-6, got)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    lib = fused.lib
+    rc = lib.fx_hybrid_gemv_segments_rmsnormed(
+        h.data_ptr(), _lib.dtype_code(h.dtype), fused._n, fused._segment_rows, fused.codes.data_ptr(),
+        fused.rows.data_ptr(), fused._cols_ptrs, fused._idx_ptrs, fused.sparse_codes.data_ptr(),
+        fused.sparse_rows.data_ptr(), fused._scols_ptrs, sums.data_ptr(), sums.numel() + 1, weight.data_ptr(), 1e-6,
+        None, 0, got.data_ptr(), k, None)
+    assert rc == 1 and "n_tiles" in lib.fx_last_error().decode()
