@@ -384,12 +384,14 @@ int fx_hybrid_gemv_segments(const void *x, int x_dtype, int n_segments, const in
  * following add of HF Qwen3DecoderLayer): out = round(residual + round(y)) in
  * x_dtype (residual may alias out) and tile_sumsq[i] = the fp32 sum of out^2 over
  * rows 16i .. 16i+15, the partials the next fx_hybrid_gemv_segments_rmsnormed
- * reads.  One K split (no workspace): fails when K needs more.
+ * reads.  swiglu != 0 (down_proj, replacing also the SwiGLU of Qwen3MLP): x holds
+ * gate | up, 2K values, and the GEMV reads round(round(silu(gate)) * up), bit for
+ * bit what fx_silu_mul writes.  One K split (no workspace): fails when K needs more.
  */
 int fx_hybrid_gemv_residual(const void *x, int x_dtype, const uint8_t *codes, const float *rows,
                             const float *columns, const int16_t *indices, const uint8_t *sparse_codes,
                             const float *sparse_rows, const float *sparse_columns, const void *residual, void *out,
-                            float *tile_sumsq, int O, int K, void *stream);
+                            float *tile_sumsq, int O, int K, int swiglu, void *stream);
 /*
  * fx_hybrid_gemv_segments of RMSNorm(h): no single reference entry point; it
  * replaces the input_layernorm / post_attention_layernorm of HF Qwen3DecoderLayer

@@ -66,7 +66,7 @@ SIGNATURES: dict[str, tuple] = {
     "fx_hybrid_gemv_workspace_bytes": (_sz, [_i, _i]),
     "fx_hybrid_gemv": (_i, [_p, _i, _p, _p, _p, _p, _p, _p, _p, _p, _sz, _p, _i, _i, _p]),
     "fx_hybrid_gemv_segments": (_i, [_p, _i, _i, _p, _p, _p, _p, _p, _p, _p, _p, _p, _sz, _p, _i, _p]),
-    "fx_hybrid_gemv_residual": (_i, [_p, _i, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _p]),
+    "fx_hybrid_gemv_residual": (_i, [_p, _i, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _p]),
     "fx_hybrid_gemv_segments_rmsnormed": (_i, [_p, _i, _i, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i, _p, _f, _p, _sz,
                                                 _p, _i, _p]),
 }

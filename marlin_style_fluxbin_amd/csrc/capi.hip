@@ -452,7 +452,7 @@ TwoBasePlan default_hybrid_plan(int O, int G, int max_splits, int max_tiles = kH
 int run_hybrid(const void* x, int x_dtype, int n_seg, const int* seg_rows, const uint8_t* codes, const float* rows,
                const float* const* cols, const int16_t* const* idx, const uint8_t* scodes, const float* srows,
                const float* const* scols, void* workspace, size_t workspace_bytes, void* out, int K,
-               const fx::ResidualArgs& res, hipStream_t s) {
+               const fx::ResidualArgs& res, bool swiglu_in, hipStream_t s) {
   if (n_seg < 1 || n_seg > fx::kHybridMaxSegments)
     return fail(FX_EINVAL, "n_segments must be in [1, %d], got %d", fx::kHybridMaxSegments, n_seg);
   if (!seg_rows || !cols || !idx || !scols) return fail(FX_EINVAL, "segment arrays must be non-null");
@@ -526,7 +526,8 @@ int run_hybrid(const void* x, int x_dtype, int n_seg, const int* seg_rows, const
     a.seg_scols[i] = used ? scols[i] : scols[0];
     if (used) start += seg_rows[i];
   }
-  if (!fx::dispatch_hybrid(x_dtype, p.nt, p.nk, res.pro_partial != nullptr, a, dim3(p.row_blocks, p.splits), s))
+  const int prologue = res.pro_partial ? fx::kHyProNorm : swiglu_in ? fx::kHyProSwiglu : fx::kHyProPlain;
+  if (!fx::dispatch_hybrid(x_dtype, p.nt, p.nk, prologue, a, dim3(p.row_blocks, p.splits), s))
     return fail(FX_EINVAL, "no hybrid kernel for tiles %d kparts %d", p.nt, p.nk);
   int rc = check_launch("hybrid_kernel");
   if (rc || p.splits == 1) return rc;
@@ -1249,7 +1250,7 @@ int fx_hybrid_gemv(const void* x, int x_dtype, const uint8_t* codes, const float
   if (!columns || !indices || !sparse_columns)
     return fail(FX_EINVAL, "x, every layout field and out must be non-null");
   return run_hybrid(x, x_dtype, 1, &O, codes, rows, &columns, &indices, sparse_codes, sparse_rows, &sparse_columns,
-                    workspace, workspace_bytes, out, K, fx::ResidualArgs{}, static_cast<hipStream_t>(stream));
+                    workspace, workspace_bytes, out, K, fx::ResidualArgs{}, false, static_cast<hipStream_t>(stream));
 }
 
 int fx_hybrid_gemv_segments(const void* x, int x_dtype, int n_segments, const int* segment_rows,
@@ -1258,14 +1259,14 @@ int fx_hybrid_gemv_segments(const void* x, int x_dtype, int n_segments, const in
                             const float* const* sparse_columns, void* workspace, size_t workspace_bytes, void* out,
                             int K, void* stream) {
   return run_hybrid(x, x_dtype, n_segments, segment_rows, codes, rows, columns, indices, sparse_codes, sparse_rows,
-                    sparse_columns, workspace, workspace_bytes, out, K, fx::ResidualArgs{},
+                    sparse_columns, workspace, workspace_bytes, out, K, fx::ResidualArgs{}, false,
                     static_cast<hipStream_t>(stream));
 }
 
 int fx_hybrid_gemv_residual(const void* x, int x_dtype, const uint8_t* codes, const float* rows,
                             const float* columns, const int16_t* indices, const uint8_t* sparse_codes,
                             const float* sparse_rows, const float* sparse_columns, const void* residual, void* out,
-                            float* tile_sumsq, int O, int K, void* stream) {
+                            float* tile_sumsq, int O, int K, int swiglu, void* stream) {
   if (O < 1 || O > 65536) return fail(FX_EINVAL, "O must be in [1, 65536], got %d", O);
   if (!columns || !indices || !sparse_columns)
     return fail(FX_EINVAL, "x, every layout field and out must be non-null");
@@ -1274,7 +1275,7 @@ int fx_hybrid_gemv_residual(const void* x, int x_dtype, const uint8_t* codes, co
   res.ep_residual = static_cast<const uint16_t*>(residual);
   res.ep_partial = tile_sumsq;
   return run_hybrid(x, x_dtype, 1, &O, codes, rows, &columns, &indices, sparse_codes, sparse_rows, &sparse_columns,
-                    nullptr, 0, out, K, res, static_cast<hipStream_t>(stream));
+                    nullptr, 0, out, K, res, swiglu != 0, static_cast<hipStream_t>(stream));
 }
 
 int fx_hybrid_gemv_segments_rmsnormed(const void* h, int x_dtype, int n_segments, const int* segment_rows,
@@ -1293,7 +1294,7 @@ int fx_hybrid_gemv_segments_rmsnormed(const void* h, int x_dtype, int n_segments
   res.pro_weight = static_cast<const uint16_t*>(norm_weight);
   res.pro_eps = eps;
   return run_hybrid(h, x_dtype, n_segments, segment_rows, codes, rows, columns, indices, sparse_codes, sparse_rows,
-                    sparse_columns, workspace, workspace_bytes, out, K, res, static_cast<hipStream_t>(stream));
+                    sparse_columns, workspace, workspace_bytes, out, K, res, false, static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

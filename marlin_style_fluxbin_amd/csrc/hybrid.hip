@@ -65,8 +65,9 @@ __device__ __forceinline__ u32x4_t refine_operand(unsigned byte) {
                  0u, 0u};
 }
 
-template <int NT, int NK, int XDT, bool NORMIN>
+template <int NT, int NK, int XDT, int PRO>
 __global__ __launch_bounds__(NT * NK * 64) void hybrid_kernel(HybridArgs a) {
+  constexpr bool NORMIN = PRO == kHyProNorm, SWIGLU = PRO == kHyProSwiglu;
   constexpr int NW = NT * NK;
   extern __shared__ u32x4_t hy_dyn[];
   __shared__ u32x4_t zero16;
@@ -109,7 +110,7 @@ __global__ __launch_bounds__(NT * NK * 64) void hybrid_kernel(HybridArgs a) {
   uint8_t* rslot = mslot + size_t(maxb) * 2048;                 // [batch][base][slot][digit][16]
   u32x4_t* xs = reinterpret_cast<u32x4_t*>(rslot + size_t(maxb) * 256);  // [batch][64 units]
 
-  const auto rx = buffer_resource(a.x, size_t(K) * 2);
+  const auto rx = buffer_resource(a.x, size_t(SWIGLU ? 2 : 1) * K * 2);
   const auto rcol = buffer_resource(cols, size_t(G) * 128 * 2 * 4);
   const auto ridx = buffer_resource(idxp, size_t(G) * 8 * 2);
   const auto rscol = buffer_resource(scols, size_t(G) * 8 * 2 * 4);
@@ -133,7 +134,7 @@ __global__ __launch_bounds__(NT * NK * 64) void hybrid_kernel(HybridArgs a) {
   }
   const auto rwn = buffer_resource(NORMIN ? (const void*)a.res.pro_weight : (const void*)a.x, NORMIN ? size_t(K) * 2 : 0);
   const int staged = wave < nbatch ? (nbatch - wave + NW - 1) / NW : 0;
-  u32x4_t sx[kHyMaxUnits], sc[kHyMaxUnits][4], swn[kHyMaxUnits];
+  u32x4_t sx[kHyMaxUnits], sc[kHyMaxUnits][4], swn[kHyMaxUnits], sup[kHyMaxUnits];
   unsigned sidx[kHyMaxUnits], sscol[kHyMaxUnits];
 #pragma unroll
   for (int q = 0; q < kHyMaxUnits; ++q) {
@@ -142,6 +143,7 @@ __global__ __launch_bounds__(NT * NK * 64) void hybrid_kernel(HybridArgs a) {
     const int col = g * 128 + 8 * r;
     sx[q] = load_b128(rx, real ? col * 2 : kOutOfRange, 0);
     if constexpr (NORMIN) swn[q] = load_b128(rwn, real ? col * 2 : kOutOfRange, 0);
+    if constexpr (SWIGLU) sup[q] = load_b128(rx, real ? (K + col) * 2 : kOutOfRange, 0);
 #pragma unroll
     for (int h = 0; h < 4; ++h) sc[q][h] = load_b128(rcol, real ? (col * 2 + 4 * h) * 4 : kOutOfRange, 0);
     sidx[q] = __builtin_amdgcn_raw_buffer_load_b16(ridx, real ? (g * 8 + (r & 7)) * 2 : kOutOfRange, 0, 0);
@@ -191,12 +193,18 @@ __global__ __launch_bounds__(NT * NK * 64) void hybrid_kernel(HybridArgs a) {
       float xv[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) xv[j] = to_f32<XDT>(uint16_t(sx[q][j >> 1] >> (16 * (j & 1))));
-      if constexpr (NORMIN) {  // Qwen3RMSNorm: round(w * round(h * inv)), staged as the activation
+      if constexpr (NORMIN || SWIGLU) {  // the activation the GEMV reads, staged for the refinement too
         u32x4_t nb;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          xv[j] = round_to<XDT>(to_f32<XDT>(uint16_t(swn[q][j >> 1] >> (16 * (j & 1)))) *
-                                round_to<XDT>(xv[j] * norm_inv));
+          if constexpr (NORMIN) {  // Qwen3RMSNorm: round(w * round(h * inv))
+            xv[j] = round_to<XDT>(to_f32<XDT>(uint16_t(swn[q][j >> 1] >> (16 * (j & 1)))) *
+                                  round_to<XDT>(xv[j] * norm_inv));
+          } else {  // Qwen3MLP: round(round(silu(gate)) * up), silu(g) = g / (1 + e^-g)
+            const float gv = xv[j];
+            const float sg = round_to<XDT>(gv / (1.f + __expf(-gv)));
+            xv[j] = round_to<XDT>(sg * to_f32<XDT>(uint16_t(sup[q][j >> 1] >> (16 * (j & 1)))));
+          }
           const unsigned bits = from_f32<XDT>(xv[j]);
           if (j & 1) nb[j >> 1] |= bits << 16;
           else nb[j >> 1] = bits;
@@ -368,34 +376,40 @@ __global__ __launch_bounds__(NT * NK * 64) void hybrid_kernel(HybridArgs a) {
 }
 
 // Dynamic LDS beyond the default 64 KB must be allowed per kernel, once.
-template <int NT, int NK, int XDT, bool NORMIN>
+template <int NT, int NK, int XDT, int PRO>
 bool hybrid_launch(const HybridArgs& a, dim3 grid, hipStream_t s) {
   static const bool allowed =
-      hipFuncSetAttribute(reinterpret_cast<const void*>(&hybrid_kernel<NT, NK, XDT, NORMIN>),
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&hybrid_kernel<NT, NK, XDT, PRO>),
                           hipFuncAttributeMaxDynamicSharedMemorySize,
                           int(hybrid_lds_bytes(4 * kHybridMaxBatches))) == hipSuccess;
   if (!allowed) return false;
-  hipLaunchKernelGGL((hybrid_kernel<NT, NK, XDT, NORMIN>), grid, dim3(NT * NK * 64), hybrid_lds_bytes(a.gps), s, a);
+  hipLaunchKernelGGL((hybrid_kernel<NT, NK, XDT, PRO>), grid, dim3(NT * NK * 64), hybrid_lds_bytes(a.gps), s, a);
   return true;
 }
 
-template <int NT, int NK>
-bool hybrid_for_dtype(int xdt, bool normin, const HybridArgs& a, dim3 grid, hipStream_t s) {
-  if (xdt == kBF16) return normin ? hybrid_launch<NT, NK, kBF16, true>(a, grid, s)
-                                  : hybrid_launch<NT, NK, kBF16, false>(a, grid, s);
-  if (xdt == kF16) return normin ? hybrid_launch<NT, NK, kF16, true>(a, grid, s)
-                                 : hybrid_launch<NT, NK, kF16, false>(a, grid, s);
+template <int NT, int NK, int XDT>
+bool hybrid_for_prologue(int pro, const HybridArgs& a, dim3 grid, hipStream_t s) {
+  if (pro == kHyProPlain) return hybrid_launch<NT, NK, XDT, kHyProPlain>(a, grid, s);
+  if (pro == kHyProNorm) return hybrid_launch<NT, NK, XDT, kHyProNorm>(a, grid, s);
+  if (pro == kHyProSwiglu) return hybrid_launch<NT, NK, XDT, kHyProSwiglu>(a, grid, s);
   return false;
 }
 
-bool dispatch_hybrid(int xdt, int tiles, int kparts, bool normin, const HybridArgs& a, dim3 grid, hipStream_t s) {
-  if (tiles == 1 && kparts == 4) return hybrid_for_dtype<1, 4>(xdt, normin, a, grid, s);
-  if (tiles == 1 && kparts == 8) return hybrid_for_dtype<1, 8>(xdt, normin, a, grid, s);
-  if (tiles == 2 && kparts == 4) return hybrid_for_dtype<2, 4>(xdt, normin, a, grid, s);
-  if (tiles == 3 && kparts == 4) return hybrid_for_dtype<3, 4>(xdt, normin, a, grid, s);
-  if (tiles == 4 && kparts == 2) return hybrid_for_dtype<4, 2>(xdt, normin, a, grid, s);
-  if (tiles == 5 && kparts == 2) return hybrid_for_dtype<5, 2>(xdt, normin, a, grid, s);
-  if (tiles == 6 && kparts == 2) return hybrid_for_dtype<6, 2>(xdt, normin, a, grid, s);
+template <int NT, int NK>
+bool hybrid_for_dtype(int xdt, int pro, const HybridArgs& a, dim3 grid, hipStream_t s) {
+  if (xdt == kBF16) return hybrid_for_prologue<NT, NK, kBF16>(pro, a, grid, s);
+  if (xdt == kF16) return hybrid_for_prologue<NT, NK, kF16>(pro, a, grid, s);
+  return false;
+}
+
+bool dispatch_hybrid(int xdt, int tiles, int kparts, int pro, const HybridArgs& a, dim3 grid, hipStream_t s) {
+  if (tiles == 1 && kparts == 4) return hybrid_for_dtype<1, 4>(xdt, pro, a, grid, s);
+  if (tiles == 1 && kparts == 8) return hybrid_for_dtype<1, 8>(xdt, pro, a, grid, s);
+  if (tiles == 2 && kparts == 4) return hybrid_for_dtype<2, 4>(xdt, pro, a, grid, s);
+  if (tiles == 3 && kparts == 4) return hybrid_for_dtype<3, 4>(xdt, pro, a, grid, s);
+  if (tiles == 4 && kparts == 2) return hybrid_for_dtype<4, 2>(xdt, pro, a, grid, s);
+  if (tiles == 5 && kparts == 2) return hybrid_for_dtype<5, 2>(xdt, pro, a, grid, s);
+  if (tiles == 6 && kparts == 2) return hybrid_for_dtype<6, 2>(xdt, pro, a, grid, s);
   return false;
 }
 

@@ -79,9 +79,14 @@ constexpr int kHybridMaxBatches = 36;  // four-group batches one workgroup stage
 // (256 B) and activations (1 KB) per staged batch.
 inline size_t hybrid_lds_bytes(int gps) { return size_t(gps / 4) * (2048 + 256 + 1024); }
 
+// Activation prologues of the hybrid GEMV: plain x; normalising (a.x holds h,
+// a.res the partials, weight and eps of its RMSNorm); SwiGLU (a.x holds gate |
+// up, 2K values, and the GEMV reads round(round(silu(gate)) * up), as the SwiGLU
+// kernel computes it).
+enum : int { kHyProPlain = 0, kHyProNorm = 1, kHyProSwiglu = 2 };
+
 // Instantiated (tiles, kparts): (1,4) (1,8) (2,4) (3,4) (4,2) (5,2) (6,2), each
-// plain and normalising (normin: a.x holds h, a.res the prologue's partials,
-// weight and eps).  False otherwise.
-bool dispatch_hybrid(int xdt, int tiles, int kparts, bool normin, const HybridArgs& a, dim3 grid, hipStream_t s);
+// with every prologue.  False otherwise.
+bool dispatch_hybrid(int xdt, int tiles, int kparts, int prologue, const HybridArgs& a, dim3 grid, hipStream_t s);
 
 }  // namespace fx

@@ -446,14 +446,23 @@ class HybridSegmentsGemv:
         return out
 
     def residual(self, x: torch.Tensor, residual: torch.Tensor, tile_sumsq: torch.Tensor,
-                 out: torch.Tensor | None = None) -> torch.Tensor:
+                 out: torch.Tensor | None = None, swiglu: bool = False) -> torch.Tensor:
         """One module: out = round(residual + round(x @ W.T)) (``out`` None: in
         place) and the fp32 sums of out^2 over 16-row tiles into ``tile_sumsq``
-        (``fx_hybrid_gemv_residual``)."""
+        (``fx_hybrid_gemv_residual``).  ``swiglu``: x is gate | up ``[1, 2K]`` and
+        the GEMV reads round(round(silu(gate)) * up), the SwiGLU of Qwen3MLP."""
         if self._n != 1:
             raise ValueError("the residual epilogue takes one hybrid Linear")
         out = residual if out is None else out
-        _check_m1_args(x, out, self._workspace_view, self.out_features, self.in_features)
+        k = self.in_features
+        if swiglu:
+            if tuple(x.shape) != (1, 2 * k):
+                raise RuntimeError("x must be gate | up [1, 2K] for the SwiGLU prologue")
+            _check_m1_args(x[:, :k].contiguous(), out, self._workspace_view, self.out_features, k)
+            if not x.is_contiguous():
+                raise RuntimeError("x must be contiguous")
+        else:
+            _check_m1_args(x, out, self._workspace_view, self.out_features, k)
         if residual.shape != out.shape or residual.dtype != out.dtype or not residual.is_contiguous():
             raise RuntimeError("residual must match out")
         if (tile_sumsq.dtype != torch.float32 or tile_sumsq.numel() != (self.out_features + 15) // 16
@@ -463,7 +472,7 @@ class HybridSegmentsGemv:
             x.data_ptr(), _lib.dtype_code(x.dtype), self.codes.data_ptr(), self.rows.data_ptr(),
             self._columns[0].data_ptr(), self._indices[0].data_ptr(), self.sparse_codes.data_ptr(),
             self.sparse_rows.data_ptr(), self._sparse_columns[0].data_ptr(), residual.data_ptr(), out.data_ptr(),
-            tile_sumsq.data_ptr(), self.out_features, self.in_features, _lib.stream_handle(x.device)),
+            tile_sumsq.data_ptr(), self.out_features, self.in_features, int(swiglu), _lib.stream_handle(x.device)),
             "fx_hybrid_gemv_residual")
         return out
 

@@ -18,8 +18,8 @@ previous token's argmax partials) and ends with the final RMSNorm + bf16 LM head
 launch; the last token's argmax merge is one more launch per sequence.  With
 the hybrid two-base g128/s8 Linears of ``PackedHybridLinear`` the chain is the
 same with the hybrid GEMV's normalising prologue and residual epilogue
-(``fx_hybrid_gemv_segments_rmsnormed``, ``fx_hybrid_gemv_residual``) and the
-SwiGLU as its own launch (7 per layer).  Other Linears (dense bf16, the bf16
+(``fx_hybrid_gemv_segments_rmsnormed``, ``fx_hybrid_gemv_residual``), the
+SwiGLU formed in the down GEMV's prologue (6 per layer).  Other Linears (dense bf16, the bf16
 arm, ``torch.matmul``) run between add+RMSNorm kernels and the same attention
 launches.  The arithmetic and rounding points are the stock HF Qwen3 modules'
 (RMSNorm, RoPE, SDPA with fp32 softmax, SwiGLU).
@@ -178,8 +178,9 @@ class _ResidualStream:
     repacked once into the field layout (``fx_w3_planes_to_fields``), whose
     dequantization costs half the instructions.  Hybrid two-base (``kind``
     "hybrid"): ``fx_hybrid_gemv_residual`` / ``fx_hybrid_gemv_segments_rmsnormed``
-    and the SwiGLU kernel, when every layer's four are hybrid Linears without
-    bias (q|k|v and gate|up fused).  ``None`` from :meth:`build` otherwise."""
+    with the SwiGLU formed in the down launch's prologue, when every layer's four
+    are hybrid Linears without bias (q|k|v and gate|up fused).  ``None`` from
+    :meth:`build` otherwise."""
 
     def __init__(self, lib, hidden, device, payload_format, kind="w3"):
         self.lib = lib
@@ -249,12 +250,12 @@ class _ResidualStream:
         stream.o_out = [HybridSegmentsGemv([l.self_attn.o_proj]) for l in session.layers]
         stream.down_out = [HybridSegmentsGemv([l.mlp.down_proj]) for l in session.layers]
         # the residual epilogue needs one K split: try each shape once on scratch
-        for gemv in (stream.o_out[0], stream.down_out[0]):
-            x = torch.zeros(1, gemv.in_features, dtype=session.dtype, device=session.device)
+        for gemv, swiglu in ((stream.o_out[0], False), (stream.down_out[0], True)):
+            x = torch.zeros(1, (2 if swiglu else 1) * gemv.in_features, dtype=session.dtype, device=session.device)
             res = torch.zeros(1, gemv.out_features, dtype=session.dtype, device=session.device)
             sums = torch.empty((gemv.out_features + 15) // 16, dtype=torch.float32, device=session.device)
             try:
-                gemv.residual(x, res, sums)
+                gemv.residual(x, res, sums, swiglu=swiglu)
             except RuntimeError:
                 return None
         torch.cuda.synchronize(session.device)
@@ -332,11 +333,11 @@ class _ResidualStream:
         self.residual(session.lin[l]["self_attn.o_proj"].gemv, session.attn, session.residual)
 
     def mlp_in(self, session, l):
-        """SiLU(gate) * up of RMSNorm(residual) into session.act."""
+        """SiLU(gate) * up of RMSNorm(residual) into session.act (hybrid: gate | up
+        into session.gate_up_out; the down launch forms the SwiGLU)."""
         if self.kind == "hybrid":
             session.gate_up[l].call.rmsnormed(session.residual, self.partials, session.post_norm[l], session.eps,
                                               session.gate_up_out)
-            session._silu_mul()
             return
         sw = session.swiglu[l]
         self.normed(sw.layout, sw.scale_code, sw.zeros_ptr, 2 * sw.width, session.residual, session.post_norm[l],
@@ -345,7 +346,7 @@ class _ResidualStream:
     def mlp_out(self, session, l):
         """residual += down_proj(act), with its tile sums."""
         if self.kind == "hybrid":
-            self.down_out[l].residual(session.act, session.residual, self.partials)
+            self.down_out[l].residual(session.gate_up_out, session.residual, self.partials, swiglu=True)
             return
         self.residual(session.lin[l]["mlp.down_proj"].gemv, session.act, session.residual)
 

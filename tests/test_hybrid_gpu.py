@@ -256,21 +256,32 @@ def _single_split_gemv(module, x):
 
 
 @pytest.mark.parametrize("dtype", ["bf16", "f16"])
-@pytest.mark.parametrize("o,g", [(4096, 32), (4096, 96), (40, 32), (96, 3), (1040, 8)])
-def test_residual_epilogue(gpu, dtype, o, g):
+@pytest.mark.parametrize("o,g,swiglu", [(4096, 32, False), (4096, 96, True), (40, 32, False), (96, 3, True),
+                                        (1040, 8, False), (1040, 8, True)])
+def test_residual_epilogue(gpu, dtype, o, g, swiglu):
     """fx_hybrid_gemv_residual: out = round(residual + round(y)) bit for bit (the
     single-split GEMV, then the dtype's own add), in place, and the sums of out^2
-    over 16-row tiles against float64."""
+    over 16-row tiles against float64.  swiglu: x is gate | up and the GEMV's
+    input equals fx_silu_mul's output bit for bit."""
+    from marlin_style_fluxbin_amd import _lib
+
     module = d.PackedHybridLinear(_payload(o, g, seed=o + g), kernel="v5_p1024").to(gpu)
+    k = g * 128
     gen = torch.Generator().manual_seed(o)
-    x = torch.randn(1, g * 128, generator=gen).to(DT[dtype]).to(gpu)
+    x = (torch.randn(1, (2 if swiglu else 1) * k, generator=gen) * 3).to(DT[dtype]).to(gpu)
     res = (torch.randn(1, o, generator=gen) * 4).to(DT[dtype]).to(gpu)
-    fused, y = _single_split_gemv(module, x)
+    act = x
+    if swiglu:
+        act = torch.empty(1, k, dtype=x.dtype, device=gpu)
+        lib = _lib.library()
+        _lib.check(lib.fx_silu_mul(x.data_ptr(), x[:, k:].data_ptr(), act.data_ptr(), k, _lib.dtype_code(x.dtype),
+                                   _lib.stream_handle(gpu)), "silu_mul")
+    fused, y = _single_split_gemv(module, act)
     want = res + y
     tiles = (o + 15) // 16
     sums = torch.full((tiles,), float("nan"), device=gpu)
     got = res.clone()
-    fused.residual(x, got, sums)
+    fused.residual(x, got, sums, swiglu=swiglu)
     torch.cuda.synchronize()
     assert torch.equal(got, want)
     h = want.double().cpu().numpy()[0]
