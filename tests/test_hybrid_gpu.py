@@ -257,7 +257,7 @@ def _single_split_gemv(module, x):
 
 @pytest.mark.parametrize("dtype", ["bf16", "f16"])
 @pytest.mark.parametrize("o,g,swiglu", [(4096, 32, False), (4096, 96, True), (40, 32, False), (96, 3, True),
-                                        (1040, 8, False), (1040, 8, True)])
+                                        (1040, 8, False), (1040, 8, True), (17, 1, False), (4112, 4, True)])
 def test_residual_epilogue(gpu, dtype, o, g, swiglu):
     """fx_hybrid_gemv_residual: out = round(residual + round(y)) bit for bit (the
     single-split GEMV, then the dtype's own add), in place, and the sums of out^2
@@ -292,7 +292,8 @@ def test_residual_epilogue(gpu, dtype, o, g, swiglu):
 
 
 @pytest.mark.parametrize("widths,g,dtype", [((4096, 1024, 1024), 32, "bf16"), ((12288, 12288), 32, "bf16"),
-                                            ((48,), 8, "f16"), ((16, 48, 32, 64), 2, "bf16")])
+                                            ((48,), 8, "f16"), ((16, 48, 32, 64), 2, "bf16"), ((37,), 1, "bf16"),
+                                            ((4112, 4112), 4, "f16")])
 def test_rmsnormed_prologue(gpu, widths, g, dtype):
     """fx_hybrid_gemv_segments_rmsnormed equals the RMSNorm kernel followed by the
     plain segments launch bit for bit.  h holds small integers, so every order of
