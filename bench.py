@@ -609,18 +609,47 @@ def decode_bench(layers=36, prefix=512, steps=32, replays=5, seed=0):
 
     floor = noise_floor()
     print(f"# decode: HF default vs HF math attention (noise floor) {floor}", file=sys.stderr, flush=True)
+    prefill = {"bf16": prefill_timing(model, ids)}
     bf16 = arms("bf16", packed=False)
     t = time.perf_counter()
     w3_quantize_qwen3_model(model)
     torch.cuda.empty_cache()
     print(f"# decode: W3 quantization {time.perf_counter() - t:.1f}s", file=sys.stderr, flush=True)
+    prefill["w3_dense_fallback"] = prefill_timing(model, ids)
+    print(f"# decode: prefill {prefill}", file=sys.stderr, flush=True)
     w3 = arms("w3", packed=True)
     return {"workload": f"config 3: Qwen3-8B arch random init, {layers} layers, prefill {prefix}, "
                         f"{steps} greedy steps in one hipGraph, batch 1",
             "w3": w3, "bf16": bf16, "noise_floor_hf_default_vs_hf_math": floor,
+            "prefill": prefill,
             "w3_native_tokens_per_s": w3["native"]["tokens_per_s"],
             "w3_speedup_vs_bf16_native": round(w3["native"]["tokens_per_s"] / bf16["native"]["tokens_per_s"], 3),
             "w3_speedup_vs_bf16_hf": round(w3["hf"]["tokens_per_s"] / bf16["hf"]["tokens_per_s"], 3)}
+
+
+def prefill_timing(model, ids, reps=3):
+    """One prefill forward of the prompt through the HF module tree (packed W3
+    Linears take their dense fallback at M > 8: the HIP restore of the weight,
+    then a hipBLASLt GEMM): HIP events around the forward, median of ``reps``
+    after one untimed run."""
+    import statistics
+
+    import torch
+    from transformers import StaticCache
+
+    samples = []
+    with torch.inference_mode():
+        for _ in range(reps + 1):
+            cache = StaticCache(config=model.config, max_cache_len=ids.shape[1])
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record()
+            model(input_ids=ids, past_key_values=cache, use_cache=True, logits_to_keep=1)
+            end.record()
+            torch.cuda.synchronize()
+            samples.append(start.elapsed_time(end))
+            del cache
+    ms = statistics.median(samples[1:])
+    return {"ms": round(ms, 2), "tokens_per_s": round(ids.shape[1] / (ms / 1e3), 1)}
 
 
 def decode_hybrid_native(layers=36, prefix=512, steps=32, replays=3, seed=0):
