@@ -223,7 +223,19 @@ MfmaPlan make_mfma_plan(int O, int G, int nw, int pd, int gps, int tiles) {
 // this kernel per SIMD): a second residency round costs more than the longer
 // per-wave K loop (fused gate|up, 24576 x 4096: 10.3 us with 4 waves, 11.7 us
 // with 8).
-MfmaPlan default_mfma_plan(int O, int G) {
+// mb: activation rows per launch.  Eight rows: two 16-row tiles per wave share
+// each staged batch of the eight rows where the grid still covers the CUs (the
+// wide gate/up shape, 4 waves; with 16+ batches per row block, two K splits and
+// 8 waves), measured at Qwen3-8B shapes (graph-timed, rotating payloads): gate/up
+// 13.95 -> 13.09 us, down 15.11 -> 12.50 us; q/o keeps the one-row plan (7.0 us).
+MfmaPlan default_mfma_plan(int O, int G, int mb = 1) {
+  if (mb == 8) {
+    const int batches = (G + 3) / 4;
+    const int cus = device_cu_count();
+    const int blocks2 = (O + 31) / 32;  // row blocks of two 16-row tiles
+    if (batches >= 16 && blocks2 < cus) return make_mfma_plan(O, G, 8, 1, (batches + 1) / 2 * 4, 2);
+    if (batches <= 8 && blocks2 >= cus) return make_mfma_plan(O, G, 4, 1, batches * 4, 2);
+  }
   const int tiles = 1;
   const int row_blocks = (O + 15) / 16;
   const int batches = (G + 3) / 4;
@@ -606,7 +618,7 @@ int fx_w3_m1_out(const void* x, int x_dtype, const uint8_t* planes, const void* 
 size_t fx_w3_gemv_workspace_bytes(int M, int O, int K) {
   if (M < 1 || O < 1 || K < 128 || K % 128) return 0;
   const int G = K / 128;
-  const size_t mfma = mfma_workspace(M, O, default_mfma_plan(O, G));
+  const size_t mfma = mfma_workspace(M, O, default_mfma_plan(O, G, mfma_chunk_for(M)));
   const size_t lut = lut_route_workspace(M, O, K);
   return mfma > lut ? mfma : lut;
 }
@@ -623,7 +635,7 @@ int fx_w3_gemv(const void* x, int x_dtype, const uint8_t* planes, const void* sc
     return run_lut_route(x, x_dtype, planes, scales, scale_dtype, zeros, perm, workspace,
                          workspace_bytes, out, M, O, K, arithmetic, s);
   return run_mfma(x, x_dtype, planes, scales, scale_dtype, zeros, perm, workspace,
-                  workspace_bytes, out, M, O, K, default_mfma_plan(O, K / 128), s);
+                  workspace_bytes, out, M, O, K, default_mfma_plan(O, K / 128, mfma_chunk_for(M)), s);
 }
 
 // ------------------------------------------------------------------ allocation-free GEMV
