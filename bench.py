@@ -884,6 +884,74 @@ def summarize_trace(csv_path, last):
         print(f"| `{name}` | {grid} | {len(v)} | {sum(v):.1f} | {statistics.mean(v):.2f} | {statistics.median(v):.2f} |")
 
 
+def pmc_hybrid_target(copies=4, reps=8):
+    """Workload for ``rocprofv3 --pmc`` passes over the hybrid decode launches:
+    one Qwen3-8B layer's hybrid two-base Linears (random payloads, ``copies``
+    rotating copies) run as the native decode chain runs them -- q|k|v and gate|up
+    normalising the residual, o adding into it, down forming the SwiGLU and adding
+    into it -- ``reps`` times each, with a progress line per round."""
+    import torch
+
+    from marlin_style_fluxbin_amd.deployment import HybridSegmentsGemv, PackedHybridLinear
+    from marlin_style_fluxbin_amd.qwen3 import random_hybrid_payload
+
+    device = torch.device("cuda:0")
+    gen = torch.Generator(device=device).manual_seed(0)
+    hidden, inter, kv = 4096, 12288, 1024
+
+    def module(o, k):
+        return PackedHybridLinear(random_hybrid_payload(o, k, device=device, generator=gen), kernel="v5_p1024",
+                                  groups_per_split=8).to(device)
+
+    layers = []
+    for _ in range(copies):
+        layers.append({"qkv": HybridSegmentsGemv([module(hidden, hidden), module(kv, hidden), module(kv, hidden)]),
+                       "o": HybridSegmentsGemv([module(hidden, hidden)]),
+                       "gate_up": HybridSegmentsGemv([module(inter, hidden), module(inter, hidden)]),
+                       "down": HybridSegmentsGemv([module(hidden, inter)])})
+    residual = torch.randn(1, hidden, device=device, generator=gen).to(torch.bfloat16)
+    sums = torch.rand(hidden // 16, device=device, generator=gen) * 16
+    weight = (1 + 0.02 * torch.randn(hidden, device=device, generator=gen)).to(torch.bfloat16)
+    qkv_out = torch.empty(1, hidden + 2 * kv, dtype=torch.bfloat16, device=device)
+    attn = torch.randn(1, hidden, device=device, generator=gen).to(torch.bfloat16)
+    gate_up = torch.empty(1, 2 * inter, dtype=torch.bfloat16, device=device)
+    for r in range(reps):
+        for layer in layers:
+            layer["qkv"].rmsnormed(residual, sums, weight, 1e-6, qkv_out)
+            layer["o"].residual(attn, residual, sums)
+            layer["gate_up"].rmsnormed(residual, sums, weight, 1e-6, gate_up)
+            layer["down"].residual(gate_up, residual, sums, swiglu=True)
+        torch.cuda.synchronize()
+        print(f"# pmc-hybrid round {r + 1}/{reps}", flush=True)
+
+
+def summarize_sq(csv_path, name_filter):
+    """Per-kernel (and grid) SQ instruction mix from a rocprofv3 counter CSV:
+    waves, cycles, VALU / MFMA / LDS / VMEM instructions per wave and LDS bank
+    conflicts per active LDS cycle, for kernels whose name contains name_filter."""
+    import csv
+    from collections import defaultdict
+
+    vals = defaultdict(lambda: defaultdict(list))
+    with open(csv_path, newline="") as f:
+        for row in csv.DictReader(f):
+            name = row["Kernel_Name"].split("(")[0]
+            if name_filter not in name:
+                continue
+            key = (name, row.get("Grid_Size") or row.get("Grid_Size_X", ""))
+            vals[key][row["Counter_Name"]].append(float(row["Counter_Value"]))
+    print("| kernel | grid | waves | cycles / wave | VALU / wave | MFMA / wave | LDS / wave | VMEM / wave | "
+          "bank conflicts / active LDS |")
+    print("|---|---:|---:|---:|---:|---:|---:|---:|---:|")
+    for (name, grid), d in sorted(vals.items()):
+        m = {c: sum(v) / len(v) for c, v in d.items()}
+        w = max(m.get("SQ_WAVES", 1.0), 1.0)
+        conflicts = m.get("SQ_LDS_BANK_CONFLICT", 0.0) / max(m.get("SQ_ACTIVE_INST_LDS", 1.0), 1.0)
+        print(f"| `{name}` | {grid} | {w:.0f} | {m.get('SQ_WAVE_CYCLES', 0) / w:.0f} | "
+              f"{m.get('SQ_INSTS_VALU', 0) / w:.1f} | {m.get('SQ_INSTS_MFMA', 0) / w:.1f} | "
+              f"{m.get('SQ_INSTS_LDS', 0) / w:.1f} | {m.get('SQ_INSTS_VMEM', 0) / w:.1f} | {conflicts:.2f} |")
+
+
 def summarize_pmc(csv_paths, out_json):
     """Average rocprofv3 counter CSVs per kernel; scale FETCH_SIZE / WRITE_SIZE
     (KiB per dispatch) by what they read for the copy kernel of known size."""
@@ -963,6 +1031,10 @@ def main():
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--shapes", default="all", help="comma list of q/o,k/v,gate/up,down or all")
     parser.add_argument("--pmc-target", action="store_true", help="run the counter-collection workload")
+    parser.add_argument("--pmc-hybrid", action="store_true",
+                        help="run the counter-collection workload of the hybrid decode launches")
+    parser.add_argument("--summarize-sq", nargs=2, metavar=("CSV", "NAME"),
+                        help="per-kernel SQ instruction mix of a counter CSV (kernels matching NAME)")
     parser.add_argument("--decode", action="store_true", help="run only the config-3 decode benchmark")
     parser.add_argument("--decode-native", action="store_true",
                         help="run only the config-3 W3 native decode arm (the kernel-trace workload)")
@@ -986,6 +1058,12 @@ def main():
         return
     if args.pmc_target:
         pmc_target()
+        return
+    if args.pmc_hybrid:
+        pmc_hybrid_target()
+        return
+    if args.summarize_sq:
+        summarize_sq(args.summarize_sq[0], args.summarize_sq[1])
         return
     if args.decode_native:
         print(json.dumps(decode_native_only(layers=args.decode_layers)), flush=True)
