@@ -47,6 +47,53 @@ def config_codes(o: int, k: int, *, seed: int = 0, zeros: bool = True, scale_dty
     return codes, scales, zero, perm
 
 
+def outlier_activations(m: int, k: int, *, ratio: float, seed: int, channels, dtype=torch.bfloat16):
+    """[m, k] activations N(0, 1) * 1e-2 with `channels` at +-ratio * 1e-2 (sign and
+    size varying per row) and the two columns after the first channel exactly
+    zero: Qwen3's massive activations sit in a few channels of otherwise small rows."""
+    generator = torch.Generator().manual_seed(seed)
+    x = torch.randn(m, k, generator=generator) * 1e-2
+    for i, c in enumerate(channels):
+        sign = torch.where(torch.rand(m, generator=generator) < 0.5, -1.0, 1.0)
+        x[:, c] = sign * ratio * 1e-2 * (1.0 - 0.25 * (i % 3))
+    x[:, channels[0] + 1: channels[0] + 3] = 0.0
+    return x.to(dtype)
+
+
+def silence_columns(codes, zeros, perm, columns, rows) -> None:
+    """Make the weights of original columns `columns` exactly zero in output rows
+    `rows` (code = the zero-point of the column's sorted group, 4 without
+    zero-points), in place on the [K, O] codes."""
+    k = codes.shape[0]
+    position = np.empty(k, dtype=np.int64)
+    order = np.arange(k) if perm is None else perm.numpy().astype(np.int64)
+    position[order] = np.arange(k)
+    for c in columns:
+        g = int(position[c]) // 128
+        z = torch.full((len(rows),), 4, dtype=torch.uint8) if zeros is None else zeros[g, rows]
+        codes[c, rows] = z
+
+
+def assert_within_terms(actual, exact, dtype: str, x, scales, factor: float, what: str = "") -> None:
+    """Element-wise: |actual - exact| <= half an ulp of the output dtype at exact,
+    plus factor * 11 * max(s) * sum_k |x[m, k]| for activation row m.  The kernels
+    apply the zero-point as z * sum(x) beside the unsigned dot sum(q x) of each
+    (group, row), so their fp32 rounding scales with those terms (bounded by
+    11 max(s) sum|x|, q <= 7 and z <= 4), not with |y|: a row whose weights
+    cancel an outlier channel is held to its terms' scale, not to the outlier
+    rows' max|y|."""
+    a = np.asarray(actual, dtype=np.float64)
+    e = np.asarray(exact, dtype=np.float64)
+    mantissa = 7 if dtype == "bf16" else 10
+    exponent = np.floor(np.log2(np.maximum(np.abs(e), 1e-30)))
+    terms = 11.0 * float(scales.float().abs().max()) * np.abs(x.float().numpy()).sum(axis=1, keepdims=True)
+    bound = 2.0 ** (exponent - mantissa - 1) + factor * terms
+    excess = np.abs(a - e) - bound
+    worst = int(np.argmax(excess))
+    assert excess.max() <= 0, (f"{what} element {worst}: |{a.flat[worst]} - {e.flat[worst]}| exceeds "
+                               f"bound {bound.flat[worst]:.3g}")
+
+
 def layout_from_codes(codes, scales, zeros, perm):
     """Planar layout (torch, CPU) for original-order codes.
 

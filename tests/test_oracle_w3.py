@@ -260,3 +260,40 @@ def test_field_layout_bijection_and_roundtrip():
     assert fields.shape == (3, 3, 21, 16)
     assert np.array_equal(w3.sorted_codes_from_fields(fields), codes)
     assert np.array_equal(w3.fields_from_planar(w3.planar_from_codes(codes)), fields)
+
+
+@pytest.mark.parametrize("permute", [False, True])
+@pytest.mark.parametrize("ratio", [10.0, 1e3, 1e4, 2.0 ** 20])
+def test_outlier_case_quiet_rows_and_sensitivity(permute, ratio):
+    """The outlier parity case of the GPU suites: silenced rows do not depend on
+    the outlier channels at all, and a kernel that flushed the small elements of
+    an outlier's group (a per-batch or normal-only fp16 exponent would) misses the
+    terms-scaled bar those suites hold every row to, so the bar can see the loss."""
+    from tests.payloads import (assert_within_terms, config_codes, layout_from_codes, oracle_layout,
+                                outlier_activations, silence_columns)
+
+    o, k = 96, 1024
+    codes, scales, zeros, perm = config_codes(o, k, seed=11, zeros=True, permute=permute)
+    channels = [5, 300, 301, 777]
+    quiet = np.arange(0, o, 2)
+    silence_columns(codes, zeros, perm, channels, quiet)
+    layout = oracle_layout(layout_from_codes(codes, scales, zeros, perm))
+    x = outlier_activations(3, k, ratio=ratio, seed=3, channels=channels)
+    exact = w3.matvec_exact(x.float().numpy(), layout)
+    cut = x.clone()
+    cut[:, channels] = 0
+    assert np.array_equal(exact[:, quiet], w3.matvec_exact(cut.float().numpy(), layout)[:, quiet])
+    # the exact values pass their own bar at the loosest factor the suites use
+    assert_within_terms(exact, exact, "bf16", x, scales, 2.0 ** -18)
+    # planted loss: the outlier groups' other elements flushed to zero
+    flushed = x.float().clone()
+    position = np.empty(k, dtype=np.int64)
+    position[np.arange(k) if perm is None else perm.numpy().astype(np.int64)] = np.arange(k)
+    for c in channels:
+        group = position // 128 == position[c] // 128
+        keep = flushed[:, c].clone()
+        flushed[:, torch.from_numpy(group)] = 0
+        flushed[:, c] = keep
+    lossy = w3.matvec_exact(flushed.numpy(), layout)
+    with pytest.raises(AssertionError):
+        assert_within_terms(lossy, exact, "bf16", x, scales, 2.0 ** -18)

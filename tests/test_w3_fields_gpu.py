@@ -14,7 +14,8 @@ import torch
 
 from marlin_style_fluxbin_amd import _lib
 from oracle import w3
-from tests.payloads import assert_half_ulp, config_codes, layout_from_codes, oracle_layout
+from tests.payloads import (assert_half_ulp, assert_within_terms, config_codes, layout_from_codes, oracle_layout,
+                            outlier_activations, silence_columns)
 
 pytestmark = pytest.mark.gpu
 
@@ -74,6 +75,35 @@ def test_gemv_fields_activation_range(gpu, scale):
                                      out.data_ptr(), o, k, _lib.stream_handle(gpu)), "gemv_fields")
     exact = w3.matvec_exact(x.float().numpy(), oracle_layout(layout))
     assert_half_ulp(out.float().cpu().numpy(), exact, "bf16", rel_slack=3e-5, what=f"scale {scale}")
+
+
+@pytest.mark.parametrize("xdtype,tag", [(torch.bfloat16, "bf16"), (torch.float16, "f16")])
+@pytest.mark.parametrize("ratio", [10.0, 1e3, 1e4])
+def test_gemv_fields_outlier_channels(gpu, xdtype, tag, ratio):
+    """A few channels `ratio` times larger than the rest of their group (Qwen3's
+    massive activations), with half of the rows' weights on those channels
+    exactly zero.  The group's exponent follows the outlier; the fp16 operands
+    x * 2^(E - p) keep the other elements' 8 (bf16) or 11 (fp16) significant bits
+    while they lie within 2^24 (bf16) or 2^21 (fp16) of the group's largest |x|
+    (the largest lands in [2^7, 2^14) after the 2^-p, and fp16 subnormals end at
+    2^-24).  Every row lies within half an ulp plus 2^-18 of its terms' scale
+    (11 max(s) sum|x|; the fp16 MFMA rounds products of subnormal codes at ~2e-7
+    relative)."""
+    o, k = 96, 1024
+    codes, scales, zero, _ = config_codes(o, k, seed=12, zeros=True, scale_dtype=torch.float16)
+    channels = [5, 300, 301, 777]
+    silence_columns(codes, zero, None, channels, np.arange(0, o, 2))
+    layout = layout_from_codes(codes, scales, zero, None)
+    dl = {n: t.to(gpu) for n, t in layout.items()}
+    fields = _repack(dl["planes"])
+    x = outlier_activations(1, k, ratio=ratio, seed=3, channels=channels, dtype=xdtype)
+    out = torch.full((1, o), float("nan"), dtype=xdtype, device=gpu)
+    lib = _lib.library()
+    _lib.check(lib.fx_w3_gemv_fields(x.to(gpu).data_ptr(), _lib.dtype_code(xdtype), fields.data_ptr(),
+                                     dl["scales"].data_ptr(), _lib.dtype_code(torch.float16), dl["zeros"].data_ptr(),
+                                     out.data_ptr(), o, k, _lib.stream_handle(gpu)), "gemv_fields")
+    exact = w3.matvec_exact(x.float().numpy(), oracle_layout(layout))
+    assert_within_terms(out.float().cpu().numpy(), exact, tag, x, scales, 2.0 ** -18, what=f"ratio {ratio}")
 
 
 def test_field_layout_argument_checks(gpu):

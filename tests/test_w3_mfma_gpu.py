@@ -12,7 +12,8 @@ import torch
 
 from marlin_style_fluxbin_amd import _lib
 from oracle import w3
-from tests.payloads import assert_half_ulp, config_codes, layout_from_codes, oracle_layout
+from tests.payloads import (assert_half_ulp, assert_within_terms, config_codes, layout_from_codes, oracle_layout,
+                            outlier_activations, silence_columns)
 
 pytestmark = pytest.mark.gpu
 
@@ -82,6 +83,32 @@ def test_mfma_activation_range(gpu, scale):
     exact = w3.matvec_exact(x.float().numpy(), oracle_layout(layout))
     assert np.all(np.isfinite(out.float().cpu().numpy()))
     assert_half_ulp(out.float().cpu().numpy(), exact, "bf16", what=f"scale {scale}")
+
+
+@pytest.mark.parametrize("ratio", [10.0, 1e3, 1e4, 2.0 ** 20])
+@pytest.mark.parametrize("plan,m,permute", [((8, 1, 32, 1), 1, False), ((4, 2, 8, 2), 3, True),
+                                            ((8, 1, 4, 1), 8, True)])
+def test_mfma_outlier_channels(gpu, ratio, plan, m, permute):
+    """A few channels `ratio` times larger than the rest of their group (Qwen3's
+    massive activations), with half of the rows' weights on those channels
+    exactly zero.  Each (group, row) exponent follows the outlier and the bf16
+    operands keep every other element exact, so every row, the small ones
+    included, lies within half an ulp plus 2^-20 of its terms' scale
+    (11 max(s) sum|x|, the scale of the unsigned dot and the zero-point term the
+    kernel adds); a flush of the outlier groups' small elements misses that bar
+    (pinned on the CPU in tests/test_oracle_w3.py)."""
+    o, k = 96, 1024
+    codes, scales, zeros, perm = config_codes(o, k, seed=11, zeros=True, scale_dtype=torch.float16,
+                                              permute=permute)
+    channels = [5, 300, 301, 777]
+    silence_columns(codes, zeros, perm, channels, np.arange(0, o, 2))
+    layout = layout_from_codes(codes, scales, zeros, perm)
+    dl = {n: t.to(gpu) for n, t in layout.items()}
+    x = outlier_activations(m, k, ratio=ratio, seed=m, channels=channels)
+    out = torch.full((m, o), float("nan"), dtype=torch.bfloat16, device=gpu)
+    _run_config(dl, x.to(gpu), out, *plan, use_perm=permute)
+    exact = w3.matvec_exact(x.float().numpy(), oracle_layout(layout))
+    assert_within_terms(out.float().cpu().numpy(), exact, "bf16", x, scales, 2.0 ** -20, what=f"ratio {ratio}")
 
 
 def test_mfma_zero_activation(gpu):
