@@ -8,6 +8,7 @@ one argument of an otherwise valid call, so the message shows which check fired.
 """
 import ctypes
 import re
+import threading
 from pathlib import Path
 
 import pytest
@@ -302,3 +303,30 @@ def test_every_compute_entry_point_has_a_case():
                                         "fx_head_norm_rope"}
     queries = {n for n in PARAMS if n.endswith("_workspace_bytes")} | {"fx_abi_version"}
     assert set(PARAMS) - queries - covered == set()
+
+
+def test_error_text_is_per_thread():
+    """fx_last_error() is the calling thread's: two threads failing at once each
+    read their own message, and the main thread's stays as it was."""
+    lib = _lib.library()
+    assert lib.fx_lm_head_merge(None, 0, 1, None, None) == 1
+    mine = lib.fx_last_error().decode()
+    seen = {}
+    barrier = threading.Barrier(2)
+
+    def fail(tag, call):
+        barrier.wait()
+        rc = call()
+        seen[tag] = (rc, lib.fx_last_error().decode())
+
+    threads = [
+        threading.Thread(target=fail, args=("finish", lambda: lib.fx_w3_finish(None, None, 2, 1, 1, 1, None))),
+        threading.Thread(target=fail, args=("silu", lambda: lib.fx_silu_mul(None, None, None, 0, 2, None))),
+    ]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=60)
+    assert seen["finish"][0] == 1 and "partial and out" in seen["finish"][1]
+    assert seen["silu"][0] == 1 and "gate, up and out" in seen["silu"][1]
+    assert lib.fx_last_error().decode() == mine and "prediction" in mine
