@@ -367,11 +367,13 @@ def test_native_session_matches_hf_static_session(gpu, quantize, payload):
     assert report["logits"]["normalized_rmse"] <= 0.02, report
     # the first decode step sees identical inputs and a single layer stack pass
     assert report["stepwise_normalized_rmse"][1] <= 0.01, report
-    # launches per layer + embedding, first norm, final norm, LM head, argmax per token
+    # W3: 5 launches per layer here (q|k|v normalising, one attention launch -- at most 28
+    # keys fit one chunk at head_dim 64 -- o, gate|up + SwiGLU, down) and a few per token:
+    # at hidden 256 the fused LM-head launch does not apply (it takes hidden sizes that
+    # are multiples of 512), so the head runs as RMSNorm, hipBLASLt and argmax; the exact
+    # count at the Qwen3-8B shapes is pinned in tests/test_config3_gpu.py
     per_step = native.kernel_nodes / STEPS
-    # W3: 6 per layer (the norms inside the GEMVs, q|k|v and gate|up+SwiGLU fused, q/k norm + RoPE
-    # in the attention) + 6 per token
-    assert per_step <= (6 if quantize else 12) * 3 + 6, per_step
+    assert per_step <= (5 if quantize else 12) * 3 + 6, per_step
     for _ in range(2):
         timing, replay = native.measure("sequence_graph")
         assert torch.equal(replay["logits"], graph["logits"])
