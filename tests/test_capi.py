@@ -59,3 +59,32 @@ def test_check_raises_runtime_error_with_message():
     rc = lib.fx_w3_finish(None, None, 2, 1, 1, 1, None)
     with pytest.raises(RuntimeError, match="non-null"):
         _lib.check(rc, "fx_w3_finish")
+
+
+def test_plain_c_caller(tmp_path):
+    """The header compiles as C99 and as C++, and a C program linked against the
+    library calls it (host-only calls: ABI version, workspace query, fail-closed
+    argument checks)."""
+    import shutil
+    import subprocess
+
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("no gcc")
+    root = HEADER.parents[1]
+    libdir = root / "marlin_style_fluxbin_amd"
+    exe = tmp_path / "caller"
+    subprocess.run([gcc, "-std=c99", "-Wall", "-Wextra", "-Werror", "-I", str(root / "include"),
+                    str(root / "tests" / "c_abi" / "caller.c"), "-L", str(libdir), "-lfluxbin_amd",
+                    f"-Wl,-rpath,{libdir}", "-o", str(exe)], check=True)
+    run = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
+    assert run.returncode == 0, run.stdout + run.stderr
+    assert f"abi {_lib.ABI_VERSION}" in run.stdout
+    assert f"workspace {_lib.library().fx_w3_gemv_workspace_bytes(1, 4096, 4096)}" in run.stdout
+    gxx = shutil.which("g++")
+    if gxx is not None:  # the extern "C" block keeps the names unmangled for C++ callers
+        src = tmp_path / "probe.cc"
+        src.write_text('#include "fluxbin_amd.h"\nint main() { return fx_abi_version() > 0 ? 0 : 1; }\n')
+        subprocess.run([gxx, "-Wall", "-Werror", "-I", str(root / "include"), str(src), "-L", str(libdir),
+                        "-lfluxbin_amd", f"-Wl,-rpath,{libdir}", "-o", str(tmp_path / "probe")], check=True)
+        assert subprocess.run([str(tmp_path / "probe")], timeout=120).returncode == 0
