@@ -90,6 +90,26 @@ def time_graph(graph, steps, warmup, stream):
     return start.elapsed_time(end) / steps
 
 
+PAIRED_WARMUP, PAIRED_ROUNDS = 20, 7  # the reference's protocol (acceleration_checks.py:42-64)
+
+
+def paired_graph_timing(graphs: dict, stream, repeats: int) -> dict:
+    """µs per launch of each arm: ``graphs`` maps an arm name to (graph, launches
+    per replay).  The product's ``paired_cuda_timing`` -- 20 untimed replays per
+    arm, then 7 rounds of ``repeats`` replays per arm with the arm order reversed
+    on every other round, HIP events on ``stream`` -- and the median round."""
+    import torch
+
+    from marlin_style_fluxbin_amd.acceleration_checks import paired_cuda_timing
+
+    with torch.cuda.stream(stream):
+        timing = paired_cuda_timing({name: graph.replay for name, (graph, _) in graphs.items()},
+                                    warmup=PAIRED_WARMUP, repeats=repeats, rounds=PAIRED_ROUNDS)
+    return {name: {"us": timing[name]["median_us"] / launches,
+                   "relative_range": round(timing[name]["relative_range"], 4)}
+            for name, (_, launches) in graphs.items()}
+
+
 def capture(fn, stream):
     import torch
 
@@ -113,50 +133,49 @@ def dominant_fields_frac(shapes):
 
 
 def bench_shape(o, k, device, steps, warmup, stream, min_bytes=320e6, min_copies=50):
-    """Average launch time of the W3 GEMV and of the bf16 arm over rotating copies."""
+    """Average launch time of the W3 GEMV arms and of the bf16 arm over rotating
+    copies, every arm timed by :func:`paired_graph_timing` (alternating rounds,
+    median): the planar kernel (identity order, as config 1 draws it), the same
+    payloads with a desc_act column permutation (the reference's real artifacts;
+    the kernel gathers x[perm]), the field layout, M = 2 / 4 / 8, the bf16 arm,
+    and the dense fallback's restore (identity and permuted)."""
     import torch
 
-    from marlin_style_fluxbin_amd import W3Gemv
+    from marlin_style_fluxbin_amd import W3Gemv, _lib
+    from marlin_style_fluxbin_amd.gptq_deployment import restore_planar_w3
+    from marlin_style_fluxbin_amd.qwen3 import desc_act_perm
+    from marlin_style_fluxbin_amd.w3_lut_deployment import restore_planar_w3_into
 
     gen = torch.Generator(device=device).manual_seed(o * 7 + k)
+    cpu_gen = torch.Generator().manual_seed(o + k)
     nbytes = algorithmic_bytes(o, k)
+    perm_bytes = algorithmic_bytes(o, k, perm=True)
     copies = max(min_copies, int(min_bytes // nbytes) + 1)
     payloads = [make_payload(o, k, device, gen) for _ in range(copies)]
     gemvs = [W3Gemv(p, perm_identity=True) for p in payloads]
+    # desc_act: each copy its own group-preserving order (perm = argsort(g_idx))
+    permuted = [W3Gemv(dict(p, perm=desc_act_perm(k, cpu_gen, device)), perm_identity=False) for p in payloads]
     x = torch.randn(1, k, device=device, generator=gen).to(torch.bfloat16)
     out = torch.empty(1, o, device=device, dtype=torch.bfloat16)
+    graphs = {}
 
-    def w3_all():
-        for gemv in gemvs:
-            gemv(x, out)
+    def over(calls):
+        def run():
+            for call in calls:
+                call()
+        return run
 
-    graph = capture(w3_all, stream)
-    ms = time_graph(graph, steps, warmup, stream)
-    w3_us = ms * 1000 / copies
-    del graph
-
+    graphs["w3"] = (capture(over([lambda g=g: g(x, out) for g in gemvs]), stream), copies)
+    pout = torch.empty_like(out)
+    graphs["w3_perm"] = (capture(over([lambda g=g: g(x, pout) for g in permuted]), stream), copies)
     # config 1's small-M variants: M activation rows against the same payloads
-    small_m = {}
+    xm = {m: torch.randn(m, k, device=device, generator=gen).to(torch.bfloat16) for m in (2, 4, 8)}
+    om = {m: torch.empty(m, o, device=device, dtype=torch.bfloat16) for m in (2, 4, 8)}
     for m in (2, 4, 8):
-        xm = torch.randn(m, k, device=device, generator=gen).to(torch.bfloat16)
-        om = torch.empty(m, o, device=device, dtype=torch.bfloat16)
-
-        def w3_m(xm=xm, om=om):
-            for gemv in gemvs:
-                gemv(xm, om)
-
-        mgraph = capture(w3_m, stream)
-        m_us = time_graph(mgraph, steps, warmup, stream) * 1000 / copies
-        del mgraph
-        m_bytes = algorithmic_bytes(o, k, m)
-        small_m[f"M={m}"] = {"us": round(m_us, 3), "GBps": round(m_bytes / m_us / 1e3, 1),
-                             "frac_hbm": round(m_bytes / m_us / 1e3 / HBM_PEAK_GBPS, 4),
-                             "algorithmic_bytes": m_bytes}
+        graphs[f"M={m}"] = (capture(over([lambda g=g, m=m: g(xm[m], om[m]) for g in gemvs]), stream), copies)
 
     # the same payloads repacked once into the field layout (fx_w3_planes_to_fields)
     # and read by fx_w3_gemv_fields: the decode graph's weight format
-    from marlin_style_fluxbin_amd import _lib
-
     lib = _lib.library()
     fields = [torch.empty_like(p["planes"]) for p in payloads]
     for p, f in zip(payloads, fields):
@@ -164,70 +183,66 @@ def bench_shape(o, k, device, steps, warmup, stream, min_bytes=320e6, min_copies
                                               _lib.stream_handle(device)), "fx_w3_planes_to_fields")
     fout = torch.empty_like(out)
 
-    def fields_all():
-        for p, f in zip(payloads, fields):
-            _lib.check(lib.fx_w3_gemv_fields(x.data_ptr(), _lib.dtype_code(x.dtype), f.data_ptr(),
-                                             p["scales"].data_ptr(), _lib.dtype_code(p["scales"].dtype),
-                                             p["zeros"].data_ptr(), fout.data_ptr(), o, k,
-                                             _lib.stream_handle(device)), "fx_w3_gemv_fields")
+    def field_call(p, f):
+        _lib.check(lib.fx_w3_gemv_fields(x.data_ptr(), _lib.dtype_code(x.dtype), f.data_ptr(),
+                                         p["scales"].data_ptr(), _lib.dtype_code(p["scales"].dtype),
+                                         p["zeros"].data_ptr(), fout.data_ptr(), o, k,
+                                         _lib.stream_handle(device)), "fx_w3_gemv_fields")
 
-    graph = capture(fields_all, stream)
-    fields_us = time_graph(graph, steps, warmup, stream) * 1000 / copies
-    del graph
-    # both formats compute the same GEMV of the last payload (fp32 sums in another
-    # order, fp16 MFMA): within two output ulps
-    gemvs[-1](x, out)
-    torch.cuda.synchronize()
-    if not torch.allclose(fout.float(), out.float(), rtol=2 ** -7, atol=1e-3 * float(out.float().abs().max())):
-        raise RuntimeError("field-layout GEMV disagrees with the planar GEMV")
-    del fields
+    graphs["fields"] = (capture(over([lambda p=p, f=f: field_call(p, f) for p, f in zip(payloads, fields)]),
+                                stream), copies)
 
     # same-run bf16 arm: dense bf16 weights (5.3x the bytes), same rotation rule
     bf16_bytes = 2 * o * k + 2 * k + 2 * o
     bcopies = max(min_copies // 5, int(min_bytes // bf16_bytes) + 1)
-    from marlin_style_fluxbin_amd.gptq_deployment import restore_planar_w3
-
     weights = [restore_planar_w3(payloads[i % copies], dtype=torch.bfloat16, perm_identity=True)
                for i in range(bcopies)]
     bout = torch.empty(1, o, device=device, dtype=torch.bfloat16)
-
-    def bf16_all():
-        for w in weights:
-            torch.matmul(x, w.t(), out=bout)
-
-    bgraph = capture(bf16_all, stream)
-    bms = time_graph(bgraph, steps, warmup, stream)
-    bf16_us = bms * 1000 / bcopies
-    del bgraph
-
-    # the dense fallback's dequantize (fx_w3_restore, identity order) into the bf16
-    # arm's buffers: reads the payload, writes the 2OK-byte weight
-    from marlin_style_fluxbin_amd.w3_lut_deployment import restore_planar_w3_into
-
-    def restore_all():
-        for i, w in enumerate(weights):
-            restore_planar_w3_into(payloads[i % copies], w, perm_identity=True)
-
-    rgraph = capture(restore_all, stream)
-    restore_us = time_graph(rgraph, steps, warmup, stream) * 1000 / bcopies
+    graphs["bf16"] = (capture(over([lambda w=w: torch.matmul(x, w.t(), out=bout) for w in weights]), stream),
+                      bcopies)
+    # the dense fallback's dequantize (fx_w3_restore) into the bf16 arm's buffers:
+    # reads the payload, writes the 2OK-byte weight; identity order, then with a
+    # scattered column permutation (the LDS-staged form)
     restore_bytes = algorithmic_bytes(o, k, m=0) + 2 * o * k
-    del rgraph
-    # the same with a scattered (desc_act-style) column permutation: the LDS-staged form
+    graphs["restore"] = (capture(over([lambda i=i, w=w: restore_planar_w3_into(payloads[i % copies], w,
+                                                                                 perm_identity=True)
+                                       for i, w in enumerate(weights)]), stream), bcopies)
     shuffled = [dict(payloads[i % copies], perm=torch.randperm(k, generator=gen, device=device).to(torch.int16))
                 for i in range(bcopies)]
+    graphs["restore_permuted"] = (capture(over([lambda p=p, w=w: restore_planar_w3_into(p, w, perm_identity=False)
+                                                for p, w in zip(shuffled, weights)]), stream), bcopies)
 
-    def restore_permuted_all():
-        for p, w in zip(shuffled, weights):
-            restore_planar_w3_into(p, w, perm_identity=False)
-
-    rgraph = capture(restore_permuted_all, stream)
-    restore_perm_us = time_graph(rgraph, steps, warmup, stream) * 1000 / bcopies
-    del rgraph, shuffled, weights, payloads, gemvs
+    t = paired_graph_timing(graphs, stream, repeats=max(steps, 10))
+    # the arms compute the same GEMV of the last payload: the field layout within
+    # two output ulps (fp32 sums in another order, fp16 MFMA); the permuted arm
+    # bit-equal to the identity kernel on the gathered row
+    gemvs[-1](x, out)
+    field_call(payloads[-1], fields[-1])
+    permuted[-1](x, pout)
+    gathered = torch.empty_like(out)
+    gemvs[-1](x[:, permuted[-1].layout["perm"].long()].contiguous(), gathered)
+    torch.cuda.synchronize()
+    if not torch.allclose(fout.float(), out.float(), rtol=2 ** -7, atol=1e-3 * float(out.float().abs().max())):
+        raise RuntimeError("field-layout GEMV disagrees with the planar GEMV")
+    if not torch.equal(pout, gathered):
+        raise RuntimeError("permuted GEMV differs from the identity GEMV on the gathered activations")
+    small_m = {}
+    for m in (2, 4, 8):
+        m_us = t[f"M={m}"]["us"]
+        m_bytes = algorithmic_bytes(o, k, m)
+        small_m[f"M={m}"] = {"us": round(m_us, 3), "GBps": round(m_bytes / m_us / 1e3, 1),
+                             "frac_hbm": round(m_bytes / m_us / 1e3 / HBM_PEAK_GBPS, 4),
+                             "algorithmic_bytes": m_bytes, "vs_M=1": round(m_us / t["w3"]["us"], 3)}
+    w3_us, fields_us, bf16_us, perm_us = t["w3"]["us"], t["fields"]["us"], t["bf16"]["us"], t["w3_perm"]["us"]
+    restore_us, restore_perm_us = t["restore"]["us"], t["restore_permuted"]["us"]
+    del graphs, shuffled, weights, payloads, gemvs, permuted, fields
     torch.cuda.empty_cache()
     return {
         "O": o, "K": k, "copies": copies, "algorithmic_bytes": nbytes,
         "w3_us": round(w3_us, 3), "w3_GBps": round(nbytes / w3_us / 1e3, 1),
         "w3_frac_hbm": round(nbytes / w3_us / 1e3 / HBM_PEAK_GBPS, 4),
+        "w3_perm_us": round(perm_us, 3), "w3_perm_GBps": round(perm_bytes / perm_us / 1e3, 1),
+        "w3_perm_frac_hbm": round(perm_bytes / perm_us / 1e3 / HBM_PEAK_GBPS, 4),
         "bf16_us": round(bf16_us, 3), "bf16_GBps": round(bf16_bytes / bf16_us / 1e3, 1),
         "w3_speedup_vs_bf16": round(bf16_us / w3_us, 3),
         "fields_us": round(fields_us, 3), "fields_GBps": round(nbytes / fields_us / 1e3, 1),
@@ -236,6 +251,9 @@ def bench_shape(o, k, device, steps, warmup, stream, min_bytes=320e6, min_copies
         "restore_us": round(restore_us, 3), "restore_GBps": round(restore_bytes / restore_us / 1e3, 1),
         "restore_permuted_us": round(restore_perm_us, 3),
         "restore_permuted_GBps": round((restore_bytes + 2 * k) / restore_perm_us / 1e3, 1),
+        "timing": {"protocol": f"alternating arm order, {PAIRED_WARMUP} warm-up replays per arm, median of "
+                               f"{PAIRED_ROUNDS} rounds of {max(steps, 10)} replays",
+                   "relative_range": {name: v["relative_range"] for name, v in t.items()}},
     }
 
 
@@ -266,11 +284,11 @@ def fused_ops_bench(device, steps, warmup, stream, launches=64, seed=0):
         ib = torch.where(ib < 0, -32768 - ib, ib)
         return int((ia - ib).abs().max())
 
-    def timed(fn):
-        graph = capture(fn, stream)
-        us = time_graph(graph, steps, warmup, stream) * 1000 / launches
-        del graph
-        return round(us, 3)
+    def paired(fused, eager):
+        """Fused launch vs HF's eager ops, alternating rounds (paired_graph_timing)."""
+        t = paired_graph_timing({"fused_us": (capture(fused, stream), launches),
+                                 "hf_eager_us": (capture(eager, stream), launches)}, stream, repeats=steps)
+        return {name: round(v["us"], 3) for name, v in t.items()}
 
     # RMSNorm and residual add + RMSNorm, hidden 4096
     xs = [torch.randn(1, 4096, device=device, generator=g).to(bf) for _ in range(launches)]
@@ -297,12 +315,12 @@ def fused_ops_bench(device, steps, warmup, stream, launches=64, seed=0):
             ro.copy_(x + r)
             o.copy_(rms_norm_reference(ro, w, eps))
 
-    result = {"rmsnorm_4096": {"fused_us": timed(norm_fused), "hf_eager_us": timed(norm_eager)}}
+    result = {"rmsnorm_4096": paired(norm_fused, norm_eager)}
     norm_fused()
     norm_eager()
     torch.cuda.synchronize()
     result["rmsnorm_4096"]["max_ulps_vs_hf"] = max(bf16_ulps(a, b) for a, b in zip(outs, ref_outs))
-    result["add_rmsnorm_4096"] = {"fused_us": timed(add_norm_fused), "hf_eager_us": timed(add_norm_eager)}
+    result["add_rmsnorm_4096"] = paired(add_norm_fused, add_norm_eager)
     add_norm_fused()
     fused_add = [o.clone() for o in outs]
     add_norm_eager()
@@ -347,7 +365,7 @@ def fused_ops_bench(device, steps, warmup, stream, launches=64, seed=0):
             k_ref[:, i].copy_(kr[0, :, 0])
             v_ref[:, i].copy_(vs[i])
 
-    result["qk_norm_rope_32q_8kv"] = {"fused_us": timed(rope_fused), "hf_eager_us": timed(rope_eager)}
+    result["qk_norm_rope_32q_8kv"] = paired(rope_fused, rope_eager)
     rope_fused()
     rope_eager()
     torch.cuda.synchronize()
@@ -355,7 +373,8 @@ def fused_ops_bench(device, steps, warmup, stream, launches=64, seed=0):
         max(bf16_ulps(a, b) for a, b in zip(q_out, q_ref)), bf16_ulps(k_cache, k_ref))
     result["qk_norm_rope_32q_8kv"]["v_slots_equal"] = bool(torch.equal(v_cache, v_ref))
     result["note"] = ("launch-bound: each call moves under 25 KB; the fused launch replaces the eager ops' "
-                      "kernels (the norm in the decode graph is further folded into the GEMV staging)")
+                      "kernels (the norm in the decode graph is further folded into the GEMV staging); "
+                      f"paired timing: {PAIRED_WARMUP} warm-up replays, median of {PAIRED_ROUNDS} alternating rounds")
     return result
 
 
@@ -394,7 +413,6 @@ def two_base_bench(device, steps, warmup, stream, o=12288, k=4096, salient=32, m
         for gemv, out in zip(gemvs, outs):
             gemv(x, out)
 
-    ms = time_graph(capture(run, stream), steps, warmup, stream) / copies
     dense_copies = max(4, int(min_bytes // (2 * o * k)) + 1)
     dense = [rank_one_reference_weight(layouts[i % copies], torch.bfloat16) for i in range(dense_copies)]
 
@@ -402,7 +420,9 @@ def two_base_bench(device, steps, warmup, stream, o=12288, k=4096, salient=32, m
         for i, w in enumerate(dense):
             torch.matmul(x, w.t(), out=outs[i % copies])
 
-    ms_bf16 = time_graph(capture(bf16_arm, stream), steps, warmup, stream) / dense_copies
+    t = paired_graph_timing({"two_base": (capture(run, stream), copies),
+                             "bf16": (capture(bf16_arm, stream), dense_copies)}, stream, repeats=max(steps, 10))
+    ms, ms_bf16 = t["two_base"]["us"] / 1e3, t["bf16"]["us"] / 1e3
     gbps = nbytes / (ms / 1e3) / 1e9
     traffic = None
     traffic_file = ROOT / "profiles" / "w3_mfma_traffic.json"
@@ -419,6 +439,8 @@ def two_base_bench(device, steps, warmup, stream, o=12288, k=4096, salient=32, m
         "bf16_arm_us": round(ms_bf16 * 1e3, 3),
         "speedup_vs_bf16": round(ms_bf16 / ms, 3),
         "copies": copies,
+        "timing": {"protocol": f"paired, {PAIRED_WARMUP} warm-up replays, median of {PAIRED_ROUNDS} rounds",
+                   "relative_range": {name: v["relative_range"] for name, v in t.items()}},
         "parity_max_rel_vs_fp32_dequant_matmul": round(max_rel, 6),
         "data": "synthetic: random +-1 bases, a1,a2 ~U[0.5,1.5], s_r ~U[0.005,0.02], t_c ~U[0.8,1.2] (fp16), "
                 "salient bf16 ~N(0,0.05), x bf16 ~N(0,1)",
@@ -499,7 +521,7 @@ def cpu_baseline(warmup=3, repeats=10):
             "arms": results}
 
 
-def decode_bench(layers=36, prefix=512, steps=32, replays=5, seed=0):
+def decode_bench(layers=36, prefix=512, steps=32, replays=7, seed=0):
     """Config 3: random-init Qwen3-8B architecture, batch-1 greedy decode of
     ``steps`` tokens after a ``prefix``-token prefill, every step in one hipGraph.
 
@@ -686,6 +708,63 @@ def decode_hybrid_native(layers=36, prefix=512, steps=32, replays=3, seed=0):
               "tokens_per_s": round(steps / (ms / 1e3), 2), "ms_per_token": round(ms / steps, 4),
               "graph_ms": [round(v, 3) for v in samples],
               "kernels_per_token": round(session.kernel_nodes / steps, 1)}
+    del session, model
+    torch.cuda.empty_cache()
+    return result
+
+
+def decode_desc_act_native(layers=36, prefix=512, steps=32, replays=7, seed=0, desc_act_seed=1):
+    """Config 3 on the reference's real payload structure: every Linear's W3
+    payload carries a desc_act column permutation (one per input group and layer:
+    q|k|v share one, gate|up one, o and down their own; ``qwen3.desc_act_perm``).
+    The native chain runs them fused -- each producer writes the next GEMV's
+    sorted column order -- at the identity order's launch count; its tokens are
+    checked against the HF module tree on the same payloads (stock modules, SDPA
+    math, the packed Linears gathering x[perm] themselves)."""
+    import statistics
+
+    import torch
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    from marlin_style_fluxbin_amd.full_model_trial import compare_trace
+    from marlin_style_fluxbin_amd.native_decode import NativeDecodeSession
+    from marlin_style_fluxbin_amd.qwen3 import qwen3_config, random_qwen3_model, w3_quantize_qwen3_model
+    from marlin_style_fluxbin_amd.static_decode import StaticDecodeSession, prepared_linears
+
+    device = torch.device("cuda:0")
+    config = qwen3_config(num_hidden_layers=layers)
+    model = random_qwen3_model(config, device=device, dtype=torch.bfloat16, seed=seed)
+    w3_quantize_qwen3_model(model, desc_act_seed=desc_act_seed)
+    g = torch.Generator().manual_seed(seed)
+    ids = torch.randint(0, config.vocab_size, (1, prefix), generator=g).to(device)
+    tokens = torch.randint(0, config.vocab_size, (1, steps), generator=g).to(device)
+    with sdpa_kernel([SDPBackend.MATH]):
+        ref = StaticDecodeSession(model, ids, tokens)
+        with prepared_linears(model, torch.bfloat16):
+            ref_trace = ref.audit()
+        del ref
+        session = NativeDecodeSession(model, ids, tokens)
+    fused = session.stream is not None
+    with torch.inference_mode():
+        trace = session.capture()
+        for _ in range(DECODE_WARMUP_REPLAYS):
+            session.measure("sequence_graph")
+        samples = [session.measure("sequence_graph")[0]["device_ms"] for _ in range(replays)]
+    ms = statistics.median(samples)
+    vs_ref = compare_trace(trace, ref_trace, logprob_tolerance=0.1)
+    same = int((trace["predictions"] == ref_trace["predictions"]).sum())
+    result = {"workload": f"config 3 W3 native arm on desc_act payloads: {layers} layers, prefill {prefix}, "
+                          f"{steps} steps (random fed tokens)",
+              "fused_residual_stream": fused,
+              "tokens_per_s": round(steps / (ms / 1e3), 2), "ms_per_token": round(ms / steps, 4),
+              "graph_ms": [round(v, 3) for v in samples],
+              "kernels_per_token": round(session.kernel_nodes / steps, 1),
+              "parity_vs_hf_math_stock": {
+                  "greedy_tokens_equal": f"{same}/{trace['predictions'].numel()}",
+                  "max_abs_logprob_error": round(vs_ref["max_abs_logprob_error"], 5),
+                  "logits_normalized_rmse": vs_ref["logits"].get("normalized_rmse"),
+                  "first_step_normalized_rmse": vs_ref["stepwise_normalized_rmse"][1]}}
+    session.graph = None
     del session, model
     torch.cuda.empty_cache()
     return result
@@ -1040,6 +1119,8 @@ def main():
                         help="run only the config-3 W3 native decode arm (the kernel-trace workload)")
     parser.add_argument("--decode-hybrid", action="store_true",
                         help="run only the config-3 architecture with hybrid two-base Linears, native chain")
+    parser.add_argument("--decode-desc-act", action="store_true",
+                        help="run only the config-3 W3 native arm on desc_act (column-permuted) payloads")
     parser.add_argument("--decode-layers", type=int, default=36)
     parser.add_argument("--no-decode", action="store_true", help="skip the config-3 decode benchmark")
     parser.add_argument("--no-two-base", action="store_true", help="skip the config-4 two-base benchmark")
@@ -1070,6 +1151,9 @@ def main():
         return
     if args.decode_hybrid:
         print(json.dumps(decode_hybrid_native(layers=args.decode_layers)), flush=True)
+        return
+    if args.decode_desc_act:
+        print(json.dumps(decode_desc_act_native(layers=args.decode_layers)), flush=True)
         return
     if args.decode:
         print(json.dumps(decode_bench(layers=args.decode_layers)), flush=True)
@@ -1223,6 +1307,9 @@ def main():
         torch.cuda.empty_cache()
         result["config"]["decode"]["hybrid_two_base_native"] = decode_hybrid_native(layers=args.decode_layers)
         print(f"# decode hybrid: {result['config']['decode']['hybrid_two_base_native']}", file=sys.stderr, flush=True)
+        torch.cuda.empty_cache()
+        result["config"]["decode"]["w3_desc_act_native"] = decode_desc_act_native(layers=args.decode_layers)
+        print(f"# decode desc_act: {result['config']['decode']['w3_desc_act_native']}", file=sys.stderr, flush=True)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline()
     print(json.dumps(result), flush=True)

@@ -40,7 +40,7 @@ extern "C" {
 #define FX_ARITH_DECODED_BF16 1 /* + per-weight bf16 rounding of s*(q-z) (bf16 scales, zero 3 or 4) */
 
 /* Payload formats of the one-row decode GEMVs: the reference's planar layout, or
- * the library's field layout (fx_w3_planes_to_fields; identity column order). */
+ * the library's field layout (fx_w3_planes_to_fields; the same sorted column order). */
 #define FX_W3_PLANAR 0
 #define FX_W3_FIELDS 1
 
@@ -118,11 +118,10 @@ int fx_w3_gemv_noalloc(const void *x, int x_dtype, const uint8_t *planes, const 
  * round(round(silu(round(g))) * round(u)) in x's dtype, each round an RNE cast
  * to that dtype.  Structural MFMA arithmetic, one launch, no workspace. */
 int fx_w3_gemv_swiglu(const void *x, int x_dtype, const uint8_t *planes, const void *scales,
-                      int scale_dtype, const uint8_t *zeros, const int16_t *perm, void *out, int O,
-                      int K, int payload_format, void *stream);
+                      int scale_dtype, const uint8_t *zeros, const int16_t *perm, const int16_t *out_index,
+                      void *out, int O, int K, int payload_format, void *stream);
 /* The decoder layer's residual stream threaded through its W3 GEMVs (one
- * activation row, identity or permuted column order for the residual form,
- * structural MFMA arithmetic).  No single reference entry point: together they
+ * activation row, structural MFMA arithmetic).  No single reference entry point: together they
  * replace HF Qwen3DecoderLayer's residual adds and Qwen3RMSNorm (as the reference
  * patches them, fused_modules.py:30-63) around the PackedW3Linear calls
  * (w3_lut_deployment.py:250-359).
@@ -133,16 +132,31 @@ int fx_w3_gemv_swiglu(const void *x, int x_dtype, const uint8_t *planes, const v
  * sums (n_tiles = ceil(K / 16), K <= 4096); the GEMV reads
  * x = round(norm_weight * round(h * rsqrt(sum(tile_sumsq) / K + eps))), the
  * RMSNorm of h, summing the tile sums in a fixed order; swiglu != 0 reads the
- * row-interleaved gate|up payload of fx_w3_gemv_swiglu.  Identity column order.
- * payload_format (all three): FX_W3_PLANAR, or FX_W3_FIELDS with `planes` holding
- * the field layout (perm NULL). */
+ * row-interleaved gate|up payload of fx_w3_gemv_swiglu.  It takes no permutation:
+ * with a column-permuted payload, h and norm_weight come in the payload's sorted
+ * column order (h[k] = residual[perm[k]], norm_weight[k] = w[perm[k]]); the
+ * tile sums are order-free.
+ * Column order for permuted consumers (the reference's desc_act payloads carry
+ * perm = argsort(g_idx), gptq_deployment.py:199-227): out_index (int16, NULL =
+ * none) names where each output value goes, so the producer writes the next
+ * GEMV's activations in that GEMV's sorted order and it reads them contiguously.
+ * fx_w3_gemv_residual: out row o is also written to sorted_out[out_index[o]]
+ * (both NULL or both set; sorted_out [O] must not alias out or residual).
+ * fx_w3_gemv_swiglu / fx_w3_gemv_rmsnormed (swiglu = 1 only): SwiGLU value r goes
+ * to out[out_index[r]] instead of out[r].  With out_index the inverse of the next
+ * GEMV's perm, that GEMV's result is bit-identical to the same GEMV given the
+ * row-ordered activation and the perm.  Entries outside [0, outputs) are not
+ * written.
+ * payload_format (all): FX_W3_PLANAR, or FX_W3_FIELDS with `planes` holding the
+ * field layout. */
 int fx_w3_gemv_residual(const void *x, int x_dtype, const uint8_t *planes, const void *scales,
                         int scale_dtype, const uint8_t *zeros, const int16_t *perm, const void *residual,
-                        void *out, float *tile_sumsq, int O, int K, int payload_format, void *stream);
+                        void *out, float *tile_sumsq, const int16_t *out_index, void *sorted_out, int O, int K,
+                        int payload_format, void *stream);
 int fx_w3_gemv_rmsnormed(const void *h, int x_dtype, const uint8_t *planes, const void *scales,
                          int scale_dtype, const uint8_t *zeros, const float *tile_sumsq, int n_tiles,
-                         const void *norm_weight, float eps, void *out, int O, int K, int swiglu,
-                         int payload_format, void *stream);
+                         const void *norm_weight, float eps, const int16_t *out_index, void *out, int O, int K,
+                         int swiglu, int payload_format, void *stream);
 /* The field layout: no reference counterpart; a bind-time repack of the
  * reference's planar payload (gptq_deployment.py:199-244 layout, same sorted
  * column order, same [G, 3, O, 16] byte shape, three bits per code) whose
@@ -229,12 +243,15 @@ int fx_head_norm_rope(int ntensors, const void *const *inputs, void *const *outp
  * their partials (one launch when one chunk covers the context), through
  * `workspace` (fx_decode_attention_workspace_bytes bytes, 16-byte aligned, no
  * initial contents needed).  Calls that share a workspace must not overlap.
- * head_dim in {64, 128, 256}.
+ * head_dim in {64, 128, 256}.  out_index (int16 [n_q_heads * head_dim], NULL =
+ * none): value i of the output goes to out[out_index[i]] (the o projection's
+ * sorted column order when its payload carries a permutation; entries outside
+ * the output are not written).
  */
 size_t fx_decode_attention_workspace_bytes(int n_q_heads, int max_len, int head_dim);
 int fx_decode_attention(const void *q, const void *k_cache, const void *v_cache, void *workspace,
-                        size_t workspace_bytes, void *out, int n_q_heads, int n_kv_heads,
-                        int max_len, int head_dim, int position, float scale, int dtype,
+                        size_t workspace_bytes, const int16_t *out_index, void *out, int n_q_heads,
+                        int n_kv_heads, int max_len, int head_dim, int position, float scale, int dtype,
                         void *stream);
 /*
  * Decode attention with the per-head q/k RMSNorm + RoPE folded in: no single
@@ -250,8 +267,9 @@ int fx_decode_attention(const void *q, const void *k_cache, const void *v_cache,
 int fx_decode_attention_rope(const void *q, const void *k, const void *v, const void *q_norm_weight,
                              const void *k_norm_weight, const void *cos, const void *sin, float eps,
                              int rope_mode, void *k_cache, void *v_cache, void *workspace,
-                             size_t workspace_bytes, void *out, int n_q_heads, int n_kv_heads, int max_len,
-                             int head_dim, int position, float scale, int dtype, void *stream);
+                             size_t workspace_bytes, const int16_t *out_index, void *out, int n_q_heads,
+                             int n_kv_heads, int max_len, int head_dim, int position, float scale, int dtype,
+                             void *stream);
 
 /*
  * Qwen3MLP activation (transformers modeling_qwen3.py, run by the reference's
@@ -303,10 +321,13 @@ int fx_lm_head_merge(void *workspace, size_t workspace_bytes, int vocab, long lo
  * prediction non-null: also merges the previous step's fx_lm_head_logits maxima
  * (lm_workspace, lm_vocab) into *prediction, as fx_lm_head_merge does.  hidden a
  * multiple of 16; table and out 16-byte aligned, token 8-byte aligned.
+ * out_index (int16 [hidden], 16-byte aligned) and sorted_out [hidden], both NULL
+ * or both set: element i of the row is also written to sorted_out[out_index[i]]
+ * (the first layer's q|k|v sorted column order, as fx_w3_gemv_residual's).
  */
 int fx_decode_embed(const long long *token, const void *table, int vocab, int hidden, void *out, float *tile_sumsq,
-                    void *lm_workspace, size_t lm_workspace_bytes, int lm_vocab, long long *prediction, int dtype,
-                    void *stream);
+                    const int16_t *out_index, void *sorted_out, void *lm_workspace, size_t lm_workspace_bytes,
+                    int lm_vocab, long long *prediction, int dtype, void *stream);
 
 /*
  * Two-base binary-basis GEMV, rank-one format with salient columns, batch 1:

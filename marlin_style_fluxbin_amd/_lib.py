@@ -15,7 +15,7 @@ from pathlib import Path
 import torch
 
 LIBRARY_PATH = Path(__file__).resolve().parent / "libfluxbin_amd.so"
-ABI_VERSION = 14
+ABI_VERSION = 15
 PAYLOAD_PLANAR, PAYLOAD_FIELDS = 0, 1  # FX_W3_PLANAR / FX_W3_FIELDS
 
 FX_F32, FX_F16, FX_BF16 = 0, 1, 2
@@ -39,9 +39,9 @@ SIGNATURES: dict[str, tuple] = {
     "fx_w3_gemv_workspace_bytes": (_sz, [_i, _i, _i]),
     "fx_w3_gemv": (_i, [_p, _i, _p, _p, _i, _p, _p, _p, _sz, _p, _i, _i, _i, _i, _p]),
     "fx_w3_gemv_noalloc": (_i, [_p, _i, _p, _p, _i, _p, _p, _p, _i, _i, _i, _i, _p]),
-    "fx_w3_gemv_swiglu": (_i, [_p, _i, _p, _p, _i, _p, _p, _p, _i, _i, _i, _p]),
-    "fx_w3_gemv_residual": (_i, [_p, _i, _p, _p, _i, _p, _p, _p, _p, _p, _i, _i, _i, _p]),
-    "fx_w3_gemv_rmsnormed": (_i, [_p, _i, _p, _p, _i, _p, _p, _i, _p, ctypes.c_float, _p, _i, _i, _i, _i, _p]),
+    "fx_w3_gemv_swiglu": (_i, [_p, _i, _p, _p, _i, _p, _p, _p, _p, _i, _i, _i, _p]),
+    "fx_w3_gemv_residual": (_i, [_p, _i, _p, _p, _i, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _p]),
+    "fx_w3_gemv_rmsnormed": (_i, [_p, _i, _p, _p, _i, _p, _p, _i, _p, ctypes.c_float, _p, _p, _i, _i, _i, _i, _p]),
     "fx_w3_planes_to_fields": (_i, [_p, _p, _i, _i, _p]),
     "fx_w3_gemv_fields": (_i, [_p, _i, _p, _p, _i, _p, _p, _i, _i, _p]),
     "fx_w3_gemv_config_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _i, _i]),
@@ -50,14 +50,14 @@ SIGNATURES: dict[str, tuple] = {
     "fx_rmsnorm": (_i, [_p, _p, _p, _p, _p, _i, _i, _f, _i, _p]),
     "fx_head_norm_rope": (_i, [_i, _p, _p, _p, _p, _p, _p, _i, _i, _i, _p, _p, _p, _p, _f, _i, _i, _p]),
     "fx_decode_attention_workspace_bytes": (_sz, [_i, _i, _i]),
-    "fx_decode_attention": (_i, [_p, _p, _p, _p, _sz, _p, _i, _i, _i, _i, _i, _f, _i, _p]),
-    "fx_decode_attention_rope": (_i, [_p, _p, _p, _p, _p, _p, _p, ctypes.c_float, _i, _p, _p, _p, _sz, _p, _i, _i, _i, _i, _i, ctypes.c_float, _i, _p]),
+    "fx_decode_attention": (_i, [_p, _p, _p, _p, _sz, _p, _p, _i, _i, _i, _i, _i, _f, _i, _p]),
+    "fx_decode_attention_rope": (_i, [_p, _p, _p, _p, _p, _p, _p, ctypes.c_float, _i, _p, _p, _p, _sz, _p, _p, _i, _i, _i, _i, _i, ctypes.c_float, _i, _p]),
     "fx_silu_mul": (_i, [_p, _p, _p, _i, _i, _p]),
     "fx_lm_head_argmax_workspace_bytes": (_sz, []),
     "fx_lm_head_argmax": (_i, [_p, _p, _f, _p, _p, _p, _p, _sz, _i, _i, _i, _p]),
     "fx_lm_head_logits": (_i, [_p, _p, _f, _p, _p, _p, _sz, _i, _i, _i, _p]),
     "fx_lm_head_merge": (_i, [_p, _sz, _i, _p, _p]),
-    "fx_decode_embed": (_i, [_p, _p, _i, _i, _p, _p, _p, _sz, _i, _p, _i, _p]),
+    "fx_decode_embed": (_i, [_p, _p, _i, _i, _p, _p, _p, _p, _p, _sz, _i, _p, _i, _p]),
     "fx_two_base_gemv_workspace_bytes": (_sz, [_i, _i]),
     "fx_two_base_gemv": (_i, [_p, _i, _p, _p, _p, _p, _p, _p, _i, _p, _sz, _p, _i, _i, _p]),
     "fx_two_base_gemv_config_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _i]),

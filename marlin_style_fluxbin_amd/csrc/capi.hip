@@ -258,7 +258,7 @@ size_t mfma_workspace(int M, int O, const MfmaPlan& p) {
 int run_mfma(const void* x, int x_dtype, const uint8_t* planes, const void* scales,
              int scale_dtype, const uint8_t* zeros, const int16_t* perm, void* workspace,
              size_t workspace_bytes, void* out, int M, int O, int K, const MfmaPlan& p,
-             hipStream_t s, int swiglu = 0) {
+             hipStream_t s, int swiglu = 0, const int16_t* out_index = nullptr) {
   const int G = K / 128;
   const size_t need = mfma_workspace(M, O, p);
   if (need > 0) {
@@ -286,6 +286,7 @@ int run_mfma(const void* x, int x_dtype, const uint8_t* planes, const void* scal
     a.row_blocks = p.row_blocks;
     a.swiglu = swiglu;
     a.res = fx::ResidualArgs{};
+    a.res.ep_index = out_index;
     const dim3 grid(p.row_blocks, p.splits);
     if (!fx::dispatch_mfma(x_dtype, p.tiles, p.nw, p.pd, mb, scale_dtype, a, grid, s))
       return fail(FX_EINVAL, "no MFMA kernel for waves %d prefetch %d tiles %d rows %d", p.nw,
@@ -560,7 +561,7 @@ bool two_base_config(int O, int G, int waves, int prefetch, int groups_per_split
 
 extern "C" {
 
-int fx_abi_version(void) { return 14; }
+int fx_abi_version(void) { return 15; }
 
 const char* fx_last_error(void) { return g_error; }
 
@@ -694,13 +695,18 @@ MfmaPlan single_split_plan(int O, int G) {
   return p;
 }
 
-// Payload format check of the one-row entry points: the field layout runs with
-// the identity column order only.
-int check_format(int payload_format, const int16_t* perm) {
+// Payload format check of the one-row entry points.
+int check_format(int payload_format) {
   if (payload_format != FX_W3_PLANAR && payload_format != FX_W3_FIELDS)
     return fail(FX_EINVAL, "payload_format must be FX_W3_PLANAR or FX_W3_FIELDS, got %d", payload_format);
-  if (payload_format == FX_W3_FIELDS && perm)
-    return fail(FX_EINVAL, "the field layout takes no column permutation");
+  return FX_OK;
+}
+
+// An output index (int16, one entry per output value) must be 2-byte aligned;
+// its entries are bounds-checked by the kernels.
+int check_out_index(const int16_t* out_index) {
+  if (out_index && reinterpret_cast<uintptr_t>(out_index) % 2 != 0)
+    return fail(FX_EINVAL, "out_index must be 2-byte aligned");
   return FX_OK;
 }
 
@@ -718,17 +724,19 @@ int run_fields(const MfmaArgs& base, int x_dtype, int scale_dtype, bool normin, 
 }
 
 int fx_w3_gemv_swiglu(const void* x, int x_dtype, const uint8_t* planes, const void* scales,
-                      int scale_dtype, const uint8_t* zeros, const int16_t* perm, void* out, int O,
-                      int K, int payload_format, void* stream) {
+                      int scale_dtype, const uint8_t* zeros, const int16_t* perm, const int16_t* out_index,
+                      void* out, int O, int K, int payload_format, void* stream) {
   int rc = validate_payload(x, x_dtype, planes, scales, scale_dtype, 1, O, K, FX_ARITH_STRUCTURAL);
   if (rc) return rc;
-  if ((rc = check_format(payload_format, perm))) return rc;
+  if ((rc = check_format(payload_format))) return rc;
+  if ((rc = check_out_index(out_index))) return rc;
   if (!out) return fail(FX_EINVAL, "out must be non-null");
   if (O % 2) return fail(FX_EINVAL, "the interleaved gate|up payload needs an even row count, got %d", O);
   const int G = K / 128;
   if (payload_format == FX_W3_FIELDS) {
     MfmaArgs a{};
     a.x = static_cast<const uint16_t*>(x);
+    a.perm = perm;
     a.planes = planes;
     a.scales = static_cast<const uint16_t*>(scales);
     a.zeros = zeros;
@@ -736,21 +744,27 @@ int fx_w3_gemv_swiglu(const void* x, int x_dtype, const uint8_t* planes, const v
     a.O = O;
     a.G = G;
     a.swiglu = 1;
+    a.res.ep_index = out_index;
     return run_fields(a, x_dtype, scale_dtype, false, static_cast<hipStream_t>(stream));
   }
   MfmaPlan p = default_mfma_plan(O, G);
   if (p.splits > 1) p = make_mfma_plan(O, G, 8, 1, G, 1);  // the fused epilogue needs one K split
   return run_mfma(x, x_dtype, planes, scales, scale_dtype, zeros, perm, nullptr, 0, out, 1, O, K, p,
-                  static_cast<hipStream_t>(stream), 1);
+                  static_cast<hipStream_t>(stream), 1, out_index);
 }
 
 int fx_w3_gemv_residual(const void* x, int x_dtype, const uint8_t* planes, const void* scales,
                         int scale_dtype, const uint8_t* zeros, const int16_t* perm, const void* residual,
-                        void* out, float* tile_sumsq, int O, int K, int payload_format, void* stream) {
+                        void* out, float* tile_sumsq, const int16_t* out_index, void* sorted_out, int O, int K,
+                        int payload_format, void* stream) {
   int rc = validate_payload(x, x_dtype, planes, scales, scale_dtype, 1, O, K, FX_ARITH_STRUCTURAL);
   if (rc) return rc;
-  if ((rc = check_format(payload_format, perm))) return rc;
+  if ((rc = check_format(payload_format))) return rc;
   if (!residual || !out || !tile_sumsq) return fail(FX_EINVAL, "residual, out and tile_sumsq must be non-null");
+  if ((rc = check_out_index(out_index))) return rc;
+  if (!out_index != !sorted_out) return fail(FX_EINVAL, "out_index and sorted_out are given together or not at all");
+  if (sorted_out && (sorted_out == out || sorted_out == residual))
+    return fail(FX_EINVAL, "sorted_out must not alias out or residual");
   const int G = K / 128;
   const MfmaPlan p = single_split_plan(O, G);
   MfmaArgs a{};
@@ -766,6 +780,8 @@ int fx_w3_gemv_residual(const void* x, int x_dtype, const uint8_t* planes, const
   a.row_blocks = p.row_blocks;
   a.res.ep_residual = static_cast<const uint16_t*>(residual);
   a.res.ep_partial = tile_sumsq;
+  a.res.ep_index = out_index;
+  a.res.ep_sorted = static_cast<uint16_t*>(sorted_out);
   if (payload_format == FX_W3_FIELDS) return run_fields(a, x_dtype, scale_dtype, false, static_cast<hipStream_t>(stream));
   if (!fx::dispatch_mfma(x_dtype, 1, p.nw, 1, 1, scale_dtype, a, dim3(p.row_blocks, 1), static_cast<hipStream_t>(stream)))
     return fail(FX_EINVAL, "no MFMA kernel for waves %d", p.nw);
@@ -774,10 +790,13 @@ int fx_w3_gemv_residual(const void* x, int x_dtype, const uint8_t* planes, const
 
 int fx_w3_gemv_rmsnormed(const void* h, int x_dtype, const uint8_t* planes, const void* scales, int scale_dtype,
                          const uint8_t* zeros, const float* tile_sumsq, int n_tiles, const void* norm_weight,
-                         float eps, void* out, int O, int K, int swiglu, int payload_format, void* stream) {
+                         float eps, const int16_t* out_index, void* out, int O, int K, int swiglu,
+                         int payload_format, void* stream) {
   int rc = validate_payload(h, x_dtype, planes, scales, scale_dtype, 1, O, K, FX_ARITH_STRUCTURAL);
   if (rc) return rc;
-  if ((rc = check_format(payload_format, nullptr))) return rc;
+  if ((rc = check_format(payload_format))) return rc;
+  if ((rc = check_out_index(out_index))) return rc;
+  if (out_index && !swiglu) return fail(FX_EINVAL, "out_index applies to the SwiGLU output (swiglu = 1)");
   if (!tile_sumsq || !norm_weight || !out) return fail(FX_EINVAL, "tile_sumsq, norm weight and out must be non-null");
   if (n_tiles != (K + 15) / 16) return fail(FX_EINVAL, "n_tiles must be ceil(K / 16) = %d, got %d", (K + 15) / 16, n_tiles);
   if (n_tiles > 64 * fx::kMaxNormPartialsPerLane) return fail(FX_EINVAL, "K = %d too large for the normalising prologue", K);
@@ -800,6 +819,7 @@ int fx_w3_gemv_rmsnormed(const void* h, int x_dtype, const uint8_t* planes, cons
   a.res.pro_n = n_tiles;
   a.res.pro_weight = static_cast<const uint16_t*>(norm_weight);
   a.res.pro_eps = eps;
+  a.res.ep_index = out_index;
   if (payload_format == FX_W3_FIELDS) return run_fields(a, x_dtype, scale_dtype, true, static_cast<hipStream_t>(stream));
   if (!fx::dispatch_mfma_normin(p.nw, x_dtype, scale_dtype, a, dim3(p.row_blocks, 1), static_cast<hipStream_t>(stream)))
     return fail(FX_EINVAL, "no normalising MFMA kernel for waves %d", p.nw);
@@ -997,8 +1017,9 @@ namespace {
 int decode_attention(const void* q, const void* k_cache, const void* v_cache, void* workspace,
                      size_t workspace_bytes, void* out, int n_q_heads, int n_kv_heads, int max_len,
                      int head_dim, int position, float scale, int dtype, void* stream,
-                     const fx::AttnPre& pre) {
+                     const fx::AttnPre& pre, const int16_t* out_index) {
   if (!q || !k_cache || !v_cache || !out) return fail(FX_EINVAL, "q, caches and out must be non-null");
+  if (int rc = check_out_index(out_index)) return rc;
   if (!is_half_dtype(dtype)) return fail(FX_EINVAL, "dtype must be fp16 or bf16");
   if (head_dim != 64 && head_dim != 128 && head_dim != 256)
     return fail(FX_EINVAL, "head_dim must be 64, 128 or 256, got %d", head_dim);
@@ -1019,6 +1040,7 @@ int decode_attention(const void* q, const void* k_cache, const void* v_cache, vo
   a.v = static_cast<const uint16_t*>(v_cache);
   a.partial = static_cast<float*>(workspace);
   a.out = static_cast<uint16_t*>(out);
+  a.out_index = out_index;
   a.Hq = n_q_heads;
   a.Hk = n_kv_heads;
   a.Lmax = max_len;
@@ -1059,18 +1081,19 @@ int decode_attention(const void* q, const void* k_cache, const void* v_cache, vo
 }  // namespace
 
 int fx_decode_attention(const void* q, const void* k_cache, const void* v_cache, void* workspace,
-                        size_t workspace_bytes, void* out, int n_q_heads, int n_kv_heads,
-                        int max_len, int head_dim, int position, float scale, int dtype,
+                        size_t workspace_bytes, const int16_t* out_index, void* out, int n_q_heads,
+                        int n_kv_heads, int max_len, int head_dim, int position, float scale, int dtype,
                         void* stream) {
   return decode_attention(q, k_cache, v_cache, workspace, workspace_bytes, out, n_q_heads, n_kv_heads, max_len,
-                          head_dim, position, scale, dtype, stream, fx::AttnPre{});
+                          head_dim, position, scale, dtype, stream, fx::AttnPre{}, out_index);
 }
 
 int fx_decode_attention_rope(const void* q, const void* k, const void* v, const void* q_norm_weight,
                              const void* k_norm_weight, const void* cos, const void* sin, float eps,
                              int rope_mode, void* k_cache, void* v_cache, void* workspace,
-                             size_t workspace_bytes, void* out, int n_q_heads, int n_kv_heads, int max_len,
-                             int head_dim, int position, float scale, int dtype, void* stream) {
+                             size_t workspace_bytes, const int16_t* out_index, void* out, int n_q_heads,
+                             int n_kv_heads, int max_len, int head_dim, int position, float scale, int dtype,
+                             void* stream) {
   if (!k || !v || !q_norm_weight || !k_norm_weight || !cos || !sin)
     return fail(FX_EINVAL, "raw k, v, norm weights, cos and sin must be non-null");
   if (rope_mode != FX_ROPE_STOCK && rope_mode != FX_ROPE_FUSED)
@@ -1083,7 +1106,7 @@ int fx_decode_attention_rope(const void* q, const void* k, const void* v, const 
                   static_cast<const uint16_t*>(q_norm_weight), static_cast<const uint16_t*>(k_norm_weight),
                   static_cast<const uint16_t*>(cos), static_cast<const uint16_t*>(sin), eps, rope_mode};
   return decode_attention(q, k_cache, v_cache, workspace, workspace_bytes, out, n_q_heads, n_kv_heads, max_len,
-                          head_dim, position, scale, dtype, stream, pre);
+                          head_dim, position, scale, dtype, stream, pre, out_index);
 }
 
 // LM head: one workgroup per CU (4 waves, one 8 KB row in flight per wave at
@@ -1178,9 +1201,14 @@ int fx_lm_head_merge(void* workspace, size_t workspace_bytes, int vocab, long lo
 }
 
 int fx_decode_embed(const long long* token, const void* table, int vocab, int hidden, void* out, float* tile_sumsq,
-                    void* lm_workspace, size_t lm_workspace_bytes, int lm_vocab, long long* prediction, int dtype,
-                    void* stream) {
+                    const int16_t* out_index, void* sorted_out, void* lm_workspace, size_t lm_workspace_bytes,
+                    int lm_vocab, long long* prediction, int dtype, void* stream) {
   if (!token || !table || !out || !tile_sumsq) return fail(FX_EINVAL, "token, table, out and tile_sumsq must be non-null");
+  if (!out_index != !sorted_out) return fail(FX_EINVAL, "out_index and sorted_out are given together or not at all");
+  if (out_index && reinterpret_cast<uintptr_t>(out_index) % 16 != 0)
+    return fail(FX_EINVAL, "out_index must be 16-byte aligned");
+  if (sorted_out && (sorted_out == out || reinterpret_cast<uintptr_t>(sorted_out) % 2 != 0))
+    return fail(FX_EINVAL, "sorted_out must be 2-byte aligned and must not alias out");
   if (!is_half_dtype(dtype)) return fail(FX_EINVAL, "dtype must be fp16 or bf16");
   if (vocab < 1) return fail(FX_EINVAL, "vocab must be positive, got %d", vocab);
   if (hidden < 16 || hidden % 16 || hidden > (1 << 20))
@@ -1197,7 +1225,8 @@ int fx_decode_embed(const long long* token, const void* table, int vocab, int hi
     merge.prediction = prediction;
   }
   if (!fx::launch_decode_embed(dtype, token, static_cast<const uint16_t*>(table), vocab, hidden,
-                               static_cast<uint16_t*>(out), tile_sumsq, merge, static_cast<hipStream_t>(stream)))
+                               static_cast<uint16_t*>(out), tile_sumsq, out_index, static_cast<uint16_t*>(sorted_out),
+                               merge, static_cast<hipStream_t>(stream)))
     return fail(FX_EINVAL, "no embedding kernel for dtype %d", dtype);
   return check_launch("decode_embed_kernel");
 }

@@ -92,10 +92,11 @@ template <int DT, int D, int KPT, bool PRE>
 __global__ __launch_bounds__(256) void attn_split_kernel(const uint16_t* __restrict__ q,
                                                          const uint16_t* kc, const uint16_t* vc,
                                                          float* __restrict__ po, float* __restrict__ pml,
-                                                         uint16_t* __restrict__ out, int G,
+                                                         uint16_t* __restrict__ out,
+                                                         const int16_t* __restrict__ out_index, int G,
                                                          int Lmax, int pos, int splits,
                                                          float scale, AttnPre pre) {
-  asm volatile("" ::"s"(q), "s"(kc), "s"(vc), "s"(po), "s"(pml), "s"(out), "s"(G),
+  asm volatile("" ::"s"(q), "s"(kc), "s"(vc), "s"(po), "s"(pml), "s"(out), "s"(out_index), "s"(G),
                "s"(Lmax), "s"(pos), "s"(splits), "s"(scale));
   if constexpr (PRE)
     asm volatile("" ::"s"(pre.k_raw), "s"(pre.v_raw), "s"(pre.q_weight), "s"(pre.k_weight), "s"(pre.cos),
@@ -272,7 +273,10 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const uint16_t* __restr
           float l = 0.f;
 #pragma unroll
           for (int r = 0; r < KS; ++r) l += red_l[r][hh];
-          out[size_t(g * G + h) * D + d] = from_f32<DT>(total * (1.f / l));
+          const int n_out = int(gridDim.x) * G * D;
+          int at = (g * G + h) * D + d;
+          if (out_index) at = out_index[at];
+          if (unsigned(at) < unsigned(n_out)) out[at] = from_f32<DT>(total * (1.f / l));
         } else {
           const size_t slot = size_t(g * G + h) * splits + chunk;
           po[slot * D + d] = total;
@@ -302,13 +306,17 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const uint16_t* __restr
 template <int DT, int D>
 __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restrict__ po,
                                                           const float* __restrict__ pml,
-                                                          uint16_t* __restrict__ out, int splits) {
-  asm volatile("" ::"s"(po), "s"(pml), "s"(out), "s"(splits));
+                                                          uint16_t* __restrict__ out,
+                                                          const int16_t* __restrict__ out_index, int splits) {
+  asm volatile("" ::"s"(po), "s"(pml), "s"(out), "s"(out_index), "s"(splits));
   static_assert(D <= 256, "one output dim per thread");
   constexpr int PARTS = 256 / D;  // threads per output dim
   constexpr int kPre = 16;
   __shared__ float ored[PARTS][D];
   const int h = blockIdx.x, t = threadIdx.x, lane = t & 63;
+  // where this thread's output dim goes, loaded ahead of the partials
+  const int n_out = int(gridDim.x) * D;
+  const int at = out_index ? (t < D ? int(out_index[h * D + t]) : -1) : h * D + t;
   const float* vo = po + size_t(h) * splits * D;
   const float* ml = pml + size_t(h) * splits * 2;
   float M = -INFINITY, L = 0.f, o = 0.f;
@@ -340,11 +348,11 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
   ored[part][d0] = o;
   __syncthreads();
   const float inv = 1.f / L;
-  for (int d = t; d < D; d += 256) {
+  if (t < D) {  // D <= 256: thread t holds output dim t
     float total = 0.f;
 #pragma unroll
-    for (int p2 = 0; p2 < PARTS; ++p2) total += ored[p2][d];
-    out[size_t(h) * D + d] = from_f32<DT>(total * inv);
+    for (int p2 = 0; p2 < PARTS; ++p2) total += ored[p2][t];
+    if (unsigned(at) < unsigned(n_out)) out[at] = from_f32<DT>(total * inv);
   }
 }
 
@@ -373,19 +381,39 @@ template <int DT>
 __global__ __launch_bounds__(256) void decode_embed_kernel(const long long* __restrict__ token,
                                                            const uint16_t* __restrict__ table, int vocab,
                                                            int hidden, uint16_t* __restrict__ out,
-                                                           float* __restrict__ tile_sumsq, LmHeadArgs merge) {
-  asm volatile("" ::"s"(token), "s"(table), "s"(vocab), "s"(hidden), "s"(out), "s"(tile_sumsq));
+                                                           float* __restrict__ tile_sumsq,
+                                                           const int16_t* __restrict__ out_index,
+                                                           uint16_t* __restrict__ sorted_out, LmHeadArgs merge) {
+  asm volatile("" ::"s"(token), "s"(table), "s"(vocab), "s"(hidden), "s"(out), "s"(tile_sumsq), "s"(out_index),
+               "s"(sorted_out));
   const long long tok = *token;
   const bool valid = tok >= 0 && tok < vocab;
   const auto rt = buffer_resource(table + (valid ? size_t(tok) * hidden : 0), size_t(hidden) * 2);
+  const auto ri = buffer_resource(out_index ? (const void*)out_index : (const void*)table,
+                                  out_index ? size_t(hidden) * 2 : 0);
   const int tiles = hidden / 16;
   for (int tile = threadIdx.x; tile < tiles; tile += 256) {
     const u32x4_t a = load_b128(rt, tile * 32, 0), b = load_b128(rt, tile * 32 + 16, 0);
+    u32x4_t ia{}, ib{};
+    if (out_index) {
+      ia = load_b128(ri, tile * 32, 0);
+      ib = load_b128(ri, tile * 32 + 16, 0);
+    }
     u32x4_t* dst = reinterpret_cast<u32x4_t*>(out + size_t(tile) * 16);
     float ss = 0.f;
     if (valid) {
       dst[0] = a;
       dst[1] = b;
+      if (out_index) {  // the same row in the next GEMV's sorted column order
+        const u32x4_t v[2] = {a, b}, ix[2] = {ia, ib};
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const int to = int(int16_t(ix[h][e >> 1] >> (16 * (e & 1))));
+            if (unsigned(to) < unsigned(hidden)) sorted_out[to] = uint16_t(v[h][e >> 1] >> (16 * (e & 1)));
+          }
+      }
       const u32x4_t v[2] = {a, b};
 #pragma unroll
       for (int h = 0; h < 2; ++h)
@@ -397,6 +425,16 @@ __global__ __launch_bounds__(256) void decode_embed_kernel(const long long* __re
     } else {
       const unsigned nan2 = DT == kBF16 ? 0x7fc07fc0u : 0x7e007e00u;
       dst[0] = dst[1] = u32x4_t{nan2, nan2, nan2, nan2};
+      if (out_index) {
+        const u32x4_t ix[2] = {ia, ib};
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const int to = int(int16_t(ix[h][e >> 1] >> (16 * (e & 1))));
+            if (unsigned(to) < unsigned(hidden)) sorted_out[to] = uint16_t(nan2);
+          }
+      }
       ss = __builtin_nanf("");
     }
     tile_sumsq[tile] = ss;
@@ -405,13 +443,14 @@ __global__ __launch_bounds__(256) void decode_embed_kernel(const long long* __re
 }
 
 bool launch_decode_embed(int dt, const long long* token, const uint16_t* table, int vocab, int hidden,
-                         uint16_t* out, float* tile_sumsq, const LmHeadArgs& merge, hipStream_t s) {
+                         uint16_t* out, float* tile_sumsq, const int16_t* out_index, uint16_t* sorted_out,
+                         const LmHeadArgs& merge, hipStream_t s) {
   if (dt == kBF16)
     hipLaunchKernelGGL(decode_embed_kernel<kBF16>, dim3(1), dim3(256), 0, s, token, table, vocab, hidden, out,
-                       tile_sumsq, merge);
+                       tile_sumsq, out_index, sorted_out, merge);
   else if (dt == kF16)
     hipLaunchKernelGGL(decode_embed_kernel<kF16>, dim3(1), dim3(256), 0, s, token, table, vocab, hidden, out,
-                       tile_sumsq, merge);
+                       tile_sumsq, out_index, sorted_out, merge);
   else
     return false;
   return true;
@@ -423,12 +462,13 @@ void attn_launch(const AttnArgs& a, hipStream_t s) {
   float* pml = a.partial + size_t(a.Hq) * a.splits * D;
   if (a.pre.k_raw)
     hipLaunchKernelGGL((attn_split_kernel<DT, D, KPT, true>), dim3(a.Hk, a.splits), dim3(256), 0, s, a.q, a.k,
-                       a.v, po, pml, a.out, a.Hq / a.Hk, a.Lmax, a.pos, a.splits, a.scale, a.pre);
+                       a.v, po, pml, a.out, a.out_index, a.Hq / a.Hk, a.Lmax, a.pos, a.splits, a.scale, a.pre);
   else
     hipLaunchKernelGGL((attn_split_kernel<DT, D, KPT, false>), dim3(a.Hk, a.splits), dim3(256), 0, s, a.q, a.k,
-                       a.v, po, pml, a.out, a.Hq / a.Hk, a.Lmax, a.pos, a.splits, a.scale, a.pre);
+                       a.v, po, pml, a.out, a.out_index, a.Hq / a.Hk, a.Lmax, a.pos, a.splits, a.scale, a.pre);
   if (a.splits > 1)
-    hipLaunchKernelGGL((attn_combine_kernel<DT, D>), dim3(a.Hq), dim3(256), 0, s, po, pml, a.out, a.splits);
+    hipLaunchKernelGGL((attn_combine_kernel<DT, D>), dim3(a.Hq), dim3(256), 0, s, po, pml, a.out, a.out_index,
+                       a.splits);
 }
 
 template <int DT, int D>

@@ -25,6 +25,7 @@ struct AttnArgs {
   const uint16_t* v;   // [Hk, Lmax, D]
   float* partial;      // [Hq, splits, D] split outputs, then [Hq, splits, 2] their (max, sum)
   uint16_t* out;       // [Hq, D]
+  const int16_t* out_index;  // null: out in head order; else value i goes to out[out_index[i]]
   int Hq, Hk, Lmax, pos;
   int kpt, splits;     // keys per thread (1, 2, 4); splits = ceil((pos + 1) / (keys per workgroup))
   float scale;
@@ -49,9 +50,11 @@ inline int attn_keys_per_block(int head_dim, int kpt) { return 256 / (head_dim /
 bool launch_decode_attention(int dt, int head_dim, const AttnArgs& a, hipStream_t s);
 bool launch_silu_mul(int dt, const uint16_t* gate, const uint16_t* up, uint16_t* out, int n,
                      hipStream_t s);
-// Embedding row of *token + its 16-element tile sums of squares; merge.prediction
-// set: also the argmax merge of merge.part_val / part_idx (merge.blocks of them).
+// Embedding row of *token + its 16-element tile sums of squares; out_index set:
+// element i also goes to sorted_out[out_index[i]]; merge.prediction set: also the
+// argmax merge of merge.part_val / part_idx (merge.blocks of them).
 bool launch_decode_embed(int dt, const long long* token, const uint16_t* table, int vocab, int hidden,
-                         uint16_t* out, float* tile_sumsq, const LmHeadArgs& merge, hipStream_t s);
+                         uint16_t* out, float* tile_sumsq, const int16_t* out_index, uint16_t* sorted_out,
+                         const LmHeadArgs& merge, hipStream_t s);
 
 }  // namespace fx

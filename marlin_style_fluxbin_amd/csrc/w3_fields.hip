@@ -1,6 +1,6 @@
 // The W3 field layout: its bind-time repack from the reference's planar payload,
-// and the MFMA GEMV instantiations that read it (one activation row, identity
-// column order).  Layout: same array shape as the planes, [G, 3, O, 16] bytes =
+// and the MFMA GEMV instantiations that read it (one activation row; identity or
+// permuted column order, the normalising prologue identity only).  Layout: same array shape as the planes, [G, 3, O, 16] bytes =
 // per (group, row) three member rows of four little-endian 32-bit words.  The
 // codes of sorted columns 32 w + t (t < 32) sit in word w of the members:
 // i = t / 2, h = t % 2; for i < 15 the code occupies bits [16 h + 3 f, +3) of
@@ -55,25 +55,29 @@ void launch_planes_to_fields(const uint8_t* planes, uint8_t* fields, int O, int 
 // wave (fields_row_tiles): each normalised, staged batch of activations then
 // feeds 32 rows, which halves the per-row cost of the RMSNorm arithmetic
 // (24576 x 4096 gate|up with SwiGLU 11.6 -> 10.7 us, 6144 x 4096 5.5 -> 5.1 us).
-template <int NW, int XDT, int SDT, bool NORMIN>
+// PERM (plain and residual forms only): sorted column k reads x[perm[k]], one
+// 2-byte gather per value in the staging, as the planar kernel's permuted form.
+template <int NW, int XDT, int SDT, bool NORMIN, bool PERM>
 void launch_fields(const MfmaArgs& a, dim3 grid, hipStream_t s) {
   if (a.O % 4 == 0) {
     constexpr int RT = NORMIN ? 2 : 1;  // fields_row_tiles
-    hipLaunchKernelGGL((w3_mfma_kernel<NW, 1, 1, RT, false, XDT, SDT, NORMIN, 1, true>), grid, dim3(NW * 64), 0, s,
+    hipLaunchKernelGGL((w3_mfma_kernel<NW, 1, 1, RT, PERM, XDT, SDT, NORMIN, 1, true>), grid, dim3(NW * 64), 0, s,
                        a.x, a.perm, a.planes, a.scales, a.zeros, a.partial, a.out, a.O, a.G, a.gps, a.row_blocks,
                        a.swiglu, a.res);
   } else {
-    hipLaunchKernelGGL((w3_mfma_kernel<NW, 1, 1, 1, false, XDT, SDT, NORMIN, 2, true>), grid, dim3(NW * 64), 0, s,
+    hipLaunchKernelGGL((w3_mfma_kernel<NW, 1, 1, 1, PERM, XDT, SDT, NORMIN, 2, true>), grid, dim3(NW * 64), 0, s,
                        a.x, a.perm, a.planes, a.scales, a.zeros, a.partial, a.out, a.O, a.G, a.gps, a.row_blocks,
                        a.swiglu, a.res);
   }
 }
 
 bool dispatch_mfma_fields(int nw, bool normin, int xdt, int sdt, const MfmaArgs& a, dim3 grid, hipStream_t s) {
+  if (normin && a.perm) return false;
 #define FX_FIELDS_CASE(W, X, S)                                                     \
   if (nw == W && xdt == X && sdt == S) {                                            \
-    if (normin) launch_fields<W, X, S, true>(a, grid, s);                           \
-    else launch_fields<W, X, S, false>(a, grid, s);                                 \
+    if (normin) launch_fields<W, X, S, true, false>(a, grid, s);                    \
+    else if (a.perm) launch_fields<W, X, S, false, true>(a, grid, s);               \
+    else launch_fields<W, X, S, false, false>(a, grid, s);                          \
     return true;                                                                    \
   }
   FX_FIELDS_CASE(4, kBF16, kBF16) FX_FIELDS_CASE(4, kBF16, kF16) FX_FIELDS_CASE(4, kF16, kBF16)

@@ -224,6 +224,17 @@ __device__ __forceinline__ void w3_mfma_body(
     }
     __builtin_amdgcn_sched_barrier(0);
   }
+  // the output index of this thread's epilogue row (residual: lanes 0..15 of wave
+  // 0, row row0 + lane; SwiGLU: thread t, pair row0 / 2 + t), loaded ahead of the
+  // weight stream so the epilogue does not wait a round trip for it
+  int ep_to = -1;
+  if (ra.ep_index) {
+    const int n_idx = ra.ep_residual ? O : O / 2;
+    const int at = ra.ep_residual ? (wave == 0 && lane < 16 ? row0 + lane : n_idx)
+                                   : (2 * t < 16 * RT ? row0 / 2 + t : n_idx);
+    const auto rix = buffer_resource(ra.ep_index, size_t(n_idx) * 2);
+    ep_to = int(int16_t(__builtin_amdgcn_raw_buffer_load_b16(rix, at < n_idx ? at * 2 : kOutOfRange, 0, 0)));
+  }
 
   const int r = lane & 15;    // A role: row within tile; x role: 8-column chunk
   const int kb = lane >> 4;   // A role: k-block = group slot; D role: row block
@@ -533,6 +544,7 @@ __device__ __forceinline__ void w3_mfma_body(
         for (int k = 0; k < kSumLanes; ++k) total += red[k][lane];
         const float h = round_to<XDT>(to_f32<XDT>(ra.ep_residual[orow]) + round_to<XDT>(total));
         out[orow] = from_f32<XDT>(h);
+        if (ra.ep_index && unsigned(ep_to) < unsigned(O)) ra.ep_sorted[ep_to] = from_f32<XDT>(h);
         h2 = h * h;
       }
       h2 = row16_sum(h2);
@@ -555,7 +567,8 @@ __device__ __forceinline__ void w3_mfma_body(
       if (orow < O) {
         const float g = round_to<XDT>(tg), u = round_to<XDT>(tu);
         const float sg = round_to<XDT>(g / (1.f + __expf(-g)));
-        out[orow / 2] = from_f32<XDT>(sg * u);
+        if (!ra.ep_index) out[orow / 2] = from_f32<XDT>(sg * u);
+        else if (unsigned(ep_to) < unsigned(O / 2)) out[ep_to] = from_f32<XDT>(sg * u);
       }
     }
     return;
@@ -591,8 +604,10 @@ __device__ __forceinline__ void w3_mfma_body(
 // is allocated registers for the costlier element form, which may spill and
 // then needs a scratch segment on every launch; the normalising instantiations
 // are split.
-// FIELDS: the payload is the field layout (one activation row, identity column
-// order, one tile and one batch in flight per wave).
+// FIELDS: the payload is the field layout (one activation row, one batch in
+// flight per wave).  NORMIN takes no permutation: its caller hands it h and the
+// norm weights in the payload's sorted column order (a producer epilogue's
+// ep_index output, weights reordered once at bind time).
 template <int NW, int PD, int MB, int RT, bool PERM, int XDT, int SDT, bool NORMIN = false, int VSEL = 0,
           bool FIELDS = false>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(MB == 1 && RT == 1 && PD == 1 ? 6 : 1)))
@@ -604,10 +619,12 @@ void w3_mfma_kernel(
   // one scalar-load round for every argument (otherwise the pointer loads sink
   // below the first branch and add a second round trip before the first load)
   asm volatile("" ::"s"(x), "s"(perm), "s"(planes), "s"(scales), "s"(zeros), "s"(partial), "s"(out),
-               "s"(O), "s"(G), "s"(gps), "s"(row_blocks), "s"(swiglu), "s"(ra.ep_residual), "s"(ra.ep_partial));
+               "s"(O), "s"(G), "s"(gps), "s"(row_blocks), "s"(swiglu), "s"(ra.ep_residual), "s"(ra.ep_partial),
+               "s"(ra.ep_index), "s"(ra.ep_sorted));
   if constexpr (NORMIN)
     asm volatile("" ::"s"(ra.pro_partial), "s"(ra.pro_n), "s"(ra.pro_weight), "s"(ra.pro_eps));
-  static_assert(!FIELDS || (!PERM && MB == 1 && PD == 1), "field layout: one row, identity order");
+  static_assert(!FIELDS || (MB == 1 && PD == 1), "field layout: one activation row, one batch in flight");
+  static_assert(!(PERM && NORMIN), "the normalising prologue reads its activations in sorted order");
   __shared__ MfmaShared<NW, MB, RT> sh;
   if (VSEL == 1 || (VSEL == 0 && (O & 3) == 0))
     w3_mfma_body<NW, PD, MB, RT, PERM, XDT, SDT, NORMIN, VSEL != 2, FIELDS>(sh, x, perm, planes, scales, zeros,

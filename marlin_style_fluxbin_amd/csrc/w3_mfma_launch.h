@@ -12,6 +12,12 @@ namespace fx {
 // * prologue (NORMIN instantiations): x holds h (such an epilogue's out); the
 //   GEMV reads x = round(weight * round(h * rsqrt(sum(pro_partial) / K + eps))),
 //   the RMSNorm of h, from the pro_n tile partials.
+// * output order for a column-permuted consumer (ep_index set): the residual
+//   epilogue also writes row o of out to ep_sorted[ep_index[o]], and the SwiGLU
+//   epilogue writes value r to out[ep_index[r]] instead of out[r].  With
+//   ep_index = the inverse of the next GEMV's permutation, that GEMV reads its
+//   activations in its own sorted column order, contiguous, with no gather.
+//   Entries outside the output's range are not written.
 struct ResidualArgs {
   const uint16_t* ep_residual;  // null: plain epilogue
   float* ep_partial;
@@ -19,6 +25,8 @@ struct ResidualArgs {
   int pro_n;
   const uint16_t* pro_weight;
   float pro_eps;
+  const int16_t* ep_index;  // null: outputs in row order only
+  uint16_t* ep_sorted;      // residual epilogue: the reordered copy of out
 };
 constexpr int kMaxNormPartialsPerLane = 4;  // prologue: K <= 4 * 64 * 16
 
@@ -57,8 +65,9 @@ FX_MFMA_DECL(dispatch_mfma_f16_t2_perm)
 bool dispatch_mfma_normin(int nw, int xdt, int sdt, const MfmaArgs& a, dim3 grid, hipStream_t s);
 
 // The field-layout instantiations (a.planes holds fields, w3_fields.hip): one
-// activation row and one batch in flight per wave, identity order, one K split;
-// plain or normalising prologue; nw in {4, 8}.  Row tiles per wave:
+// activation row and one batch in flight per wave, one K split; plain (identity
+// or permuted column order, a.perm) or normalising prologue (identity order
+// only: false when a.perm is set); nw in {4, 8}.  Row tiles per wave:
 // fields_row_tiles (a.row_blocks must count tiles of that many 16-row tiles).
 bool dispatch_mfma_fields(int nw, bool normin, int xdt, int sdt, const MfmaArgs& a, dim3 grid, hipStream_t s);
 inline int fields_row_tiles(bool normin, int O) { return normin && O % 4 == 0 ? 2 : 1; }

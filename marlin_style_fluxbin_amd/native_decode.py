@@ -41,15 +41,27 @@ _ATTN = ("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj", "self_attn.
 _MLP = ("mlp.gate_proj", "mlp.up_proj", "mlp.down_proj")
 
 
+def _one_launch_w3(module) -> bool:
+    """A W3 Linear whose packed route is the one-launch MFMA GEMV (structural
+    arithmetic, one group per split, no bias): the form the decode chain fuses.
+    Table-route modules (``decoded_bf16``, ``groups_per_split > 1``) keep their
+    own split contract and summation order."""
+    return isinstance(module, PackedW3Linear) and not module.uses_table_route and module.bias is None
+
+
 class _Linear:
-    """One decode Linear writing ``out``: the W3 MFMA GEMV, the hybrid two-base GEMV
-    (``fx_hybrid_gemv`` through the module's own packed kernel and workspace), or a
-    dense matmul."""
+    """One decode Linear writing ``out``: the W3 MFMA GEMV, the module's own table
+    route (``decoded_bf16`` or ``groups_per_split > 1``: ``fx_w3_m1_out`` with its
+    row tile and split, as ``PackedW3Linear.forward`` runs it), the hybrid two-base
+    GEMV (``fx_hybrid_gemv`` through the module's own packed kernel and
+    workspace), or a dense matmul."""
 
     def __init__(self, module):
         self.gemv = None
         self.call = None
-        if isinstance(module, PackedW3Linear):
+        if isinstance(module, PackedW3Linear) and module.uses_table_route:
+            self.call = module._packed_kernel(1, module.planes.device)
+        elif isinstance(module, PackedW3Linear):
             self.gemv = W3Gemv(module.layout(), arithmetic=module.arithmetic)
             self.call = self.gemv
         elif isinstance(module, PackedHybridLinear):
@@ -83,6 +95,8 @@ class _FusedLinear:
 
     @staticmethod
     def build(modules):
+        if any(isinstance(m, PackedW3Linear) and m.uses_table_route for m in modules):
+            return None  # each keeps its own split contract
         if all(isinstance(m, PackedW3Linear) for m in modules):
             layouts = [m.layout() for m in modules]
             first = layouts[0]
@@ -148,11 +162,10 @@ class _GateUpSwiGLU:
 
     @staticmethod
     def build(gate, up):
-        if not (isinstance(gate, PackedW3Linear) and isinstance(up, PackedW3Linear)):
+        if not (_one_launch_w3(gate) and _one_launch_w3(up)):
             return None
         g, u = gate.layout(), up.layout()
-        if (gate.arithmetic != "structural" or up.arithmetic != "structural" or gate.bias is not None
-                or up.bias is not None or gate.in_features != up.in_features
+        if (gate.in_features != up.in_features
                 or gate.out_features != up.out_features or g["scales"].dtype != u["scales"].dtype
                 or ("zeros" in g) != ("zeros" in u) or not torch.equal(g["perm"], u["perm"])):
             return None
@@ -161,9 +174,25 @@ class _GateUpSwiGLU:
     def __call__(self, x, out):
         _lib.check(self.lib.fx_w3_gemv_swiglu(
             x.data_ptr(), _lib.dtype_code(x.dtype), self.layout["planes"].data_ptr(),
-            self.layout["scales"].data_ptr(), self.scale_code, self.zeros_ptr, self.perm_ptr, out.data_ptr(),
+            self.layout["scales"].data_ptr(), self.scale_code, self.zeros_ptr, self.perm_ptr, None, out.data_ptr(),
             2 * self.width, self.in_features, _lib.PAYLOAD_PLANAR, _lib.stream_handle(x.device)),
             "fx_w3_gemv_swiglu")
+
+
+def inverse_index(perm: torch.Tensor) -> torch.Tensor | None:
+    """``inv`` with ``inv[perm[k]] = k`` (int16, on perm's device), or None for the
+    identity: where a producer writes value i so that a GEMV whose sorted column
+    k reads activation ``perm[k]`` finds it at position k."""
+    k = perm.numel()
+    order = torch.arange(k, device=perm.device)
+    p = perm.long()
+    if torch.equal(p, order):
+        return None
+    if not torch.equal(torch.sort(p).values, order):
+        raise ValueError("column permutation is not a bijection of [0, K)")
+    inv = torch.empty(k, dtype=torch.int16, device=perm.device)
+    inv[p] = order.to(torch.int16)
+    return inv
 
 
 class _ResidualStream:
@@ -172,15 +201,25 @@ class _ResidualStream:
     per-16-row sums of its squares; the q|k|v and gate|up GEMVs read the residual
     and normalise it on the fly from those sums.  W3 (``kind`` "w3"):
     ``fx_w3_gemv_residual`` / ``fx_w3_gemv_rmsnormed``, gate|up with the SwiGLU
-    epilogue, when every layer's o, down, q|k|v and gate|up are structural W3
-    (q|k|v and gate|up fused with identity column order); with
+    epilogue, when every layer's o, down, q|k|v and gate|up are one-launch W3
+    (q|k|v sharing one column permutation, gate|up another); with
     ``payload_format`` fields (the default) every layer's four payloads are
     repacked once into the field layout (``fx_w3_planes_to_fields``), whose
     dequantization costs half the instructions.  Hybrid two-base (``kind``
     "hybrid"): ``fx_hybrid_gemv_residual`` / ``fx_hybrid_gemv_segments_rmsnormed``
     with the SwiGLU formed in the down launch's prologue, when every layer's four
     are hybrid Linears without bias (q|k|v and gate|up fused).  ``None`` from
-    :meth:`build` otherwise."""
+    :meth:`build` otherwise.
+
+    Column-permuted W3 payloads (the reference's desc_act artifacts,
+    ``perm = argsort(g_idx)``, ``gptq_deployment.py:199-227``): every producer
+    writes its output in the next GEMV's sorted column order -- the step's first
+    launch and the o / down residual epilogues a sorted copy of the residual
+    (``sorted_residual``), the attention its output in o's order, the SwiGLU
+    epilogue its output in down's order -- so every GEMV reads its activations
+    contiguously with no gather; the normalising GEMVs read the RMSNorm weights
+    reordered once here.  The results are bit-identical to the GEMVs gathering
+    ``x[perm]`` themselves."""
 
     def __init__(self, lib, hidden, device, payload_format, kind="w3"):
         self.lib = lib
@@ -193,6 +232,11 @@ class _ResidualStream:
         # planes keeps their memory from being reused by another payload, and a
         # lookup must find the same tensor object
         self._fields = {}
+        # per layer: where each producer writes (None = row order), and the norm
+        # weights in the normalising GEMVs' sorted order
+        self.qkv_index = self.o_index = self.gate_up_index = self.down_index = None
+        self.in_norm = self.post_norm = None
+        self.sorted_residual = None
 
     def payload(self, layout):
         """The weights the kernels read: the planes, or their field-layout copy."""
@@ -263,56 +307,82 @@ class _ResidualStream:
 
     @staticmethod
     def _build_w3(session, payload_format=None):
-        def structural(m):
-            return isinstance(m, PackedW3Linear) and m.arithmetic == "structural" and m.bias is None
-
         for layer, qkv, swiglu in zip(session.layers, session.qkv, session.swiglu):
             o, down = layer.self_attn.o_proj, layer.mlp.down_proj
-            if not (structural(o) and structural(down)) or qkv is None or swiglu is None:
+            if not (_one_launch_w3(o) and _one_launch_w3(down)) or qkv is None or swiglu is None:
                 return None
             gemv = qkv.call
-            if not (isinstance(gemv, W3Gemv) and gemv.perm_ptr is None and gemv.arith == _lib.ARITH_STRUCTURAL):
-                return None
-            if swiglu.perm_ptr is not None:
+            if not (isinstance(gemv, W3Gemv) and gemv.arith == _lib.ARITH_STRUCTURAL):
                 return None
         if not _ResidualStream._embed_ok(session):
             return None
         fmt = _lib.PAYLOAD_FIELDS if payload_format is None else payload_format
-        if any(lin["self_attn.o_proj"].gemv.perm_ptr is not None or lin["mlp.down_proj"].gemv.perm_ptr is not None
-               for lin in session.lin):
-            fmt = _lib.PAYLOAD_PLANAR  # the field layout takes the identity column order only
         stream = _ResidualStream(_lib.library(), session.hidden, session.device, fmt)
         for lin, qkv, swiglu in zip(session.lin, session.qkv, session.swiglu):
             for layout in (qkv.call.layout, swiglu.layout, lin["self_attn.o_proj"].gemv.layout,
                            lin["mlp.down_proj"].gemv.layout):
                 stream._repack(layout)
+        stream._orders(session)
         torch.cuda.synchronize(session.device)
         return stream
 
-    def residual(self, gemv: W3Gemv, x, residual):
-        """residual <- round(residual + round(x @ W.T)); tile sums of its squares."""
+    def _orders(self, session):
+        """Each producer's output order and the sorted norm weights (W3 chain)."""
+        self.qkv_index = [inverse_index(q.call.layout["perm"]) for q in session.qkv]
+        self.o_index = [inverse_index(lin["self_attn.o_proj"].gemv.layout["perm"]) for lin in session.lin]
+        self.gate_up_index = [inverse_index(sw.layout["perm"]) for sw in session.swiglu]
+        self.down_index = [inverse_index(lin["mlp.down_proj"].gemv.layout["perm"]) for lin in session.lin]
+
+        def sort(weight, qkv_or_gu):
+            return weight if qkv_or_gu is None else weight[qkv_or_gu.layout["perm"].long()].contiguous()
+
+        self.in_norm = [w if i is None else sort(w, q.call)
+                        for w, i, q in zip(session.in_norm, self.qkv_index, session.qkv)]
+        self.post_norm = [w if i is None else sort(w, sw)
+                          for w, i, sw in zip(session.post_norm, self.gate_up_index, session.swiglu)]
+        if any(i is not None for i in self.qkv_index + self.gate_up_index):
+            self.sorted_residual = torch.zeros_like(session.residual)
+
+    def _residual_input(self, session, index):
+        """What a normalising GEMV reads: the residual, or its sorted copy."""
+        return session.residual if index is None else self.sorted_residual
+
+    def residual(self, gemv: W3Gemv, x, residual, next_index=None, x_sorted=False):
+        """residual <- round(residual + round(x @ W.T)); tile sums of its squares;
+        with ``next_index`` also the residual in the next GEMV's sorted order.
+        ``x_sorted``: x already comes in the payload's sorted column order."""
         lay = gemv.layout
         _lib.check(self.lib.fx_w3_gemv_residual(
             x.data_ptr(), _lib.dtype_code(x.dtype), self.payload(lay).data_ptr(), lay["scales"].data_ptr(),
-            gemv.scale_code, gemv.zeros_ptr, gemv.perm_ptr, residual.data_ptr(), residual.data_ptr(),
-            self.partials.data_ptr(), gemv.out_features, gemv.in_features, self.format,
-            _lib.stream_handle(x.device)), "fx_w3_gemv_residual")
+            gemv.scale_code, gemv.zeros_ptr, None if x_sorted else gemv.perm_ptr, residual.data_ptr(),
+            residual.data_ptr(), self.partials.data_ptr(), _lib.ptr(next_index),
+            None if next_index is None else self.sorted_residual.data_ptr(), gemv.out_features, gemv.in_features,
+            self.format, _lib.stream_handle(x.device)), "fx_w3_gemv_residual")
 
     def embed(self, token, table, out, lm_ws=None, lm_vocab=0, prediction=None):
         """out = table[*token], and the tile sums of its squares (the first layer's
-        normalising GEMV reads them); with ``prediction``, also the merge of the
-        previous step's LM-head maxima in ``lm_ws`` into it (one launch)."""
+        normalising GEMV reads them) and, for a permuted first q|k|v, the row in its
+        sorted order; with ``prediction``, also the merge of the previous step's
+        LM-head maxima in ``lm_ws`` into it (one launch)."""
+        index = self.qkv_index[0] if self.qkv_index else None
         _lib.check(self.lib.fx_decode_embed(
             token.data_ptr(), table.data_ptr(), table.shape[0], table.shape[1], out.data_ptr(),
-            self.partials.data_ptr(), _lib.ptr(lm_ws), 0 if lm_ws is None else lm_ws.numel(), lm_vocab,
+            self.partials.data_ptr(), _lib.ptr(index), None if index is None else self.sorted_residual.data_ptr(),
+            _lib.ptr(lm_ws), 0 if lm_ws is None else lm_ws.numel(), lm_vocab,
             _lib.ptr(prediction), _lib.dtype_code(table.dtype), _lib.stream_handle(out.device)), "fx_decode_embed")
 
-    def normed(self, layout, scale_code, zeros_ptr, rows, h, weight, eps, out, swiglu):
-        """out = GEMV (or SwiGLU) of RMSNorm(h) with the tile sums of h."""
+    def normed(self, layout, scale_code, zeros_ptr, rows, h, weight, eps, out, swiglu, out_index=None):
+        """out = GEMV (or SwiGLU, written in ``out_index`` order) of RMSNorm(h) with
+        the tile sums of h."""
         _lib.check(self.lib.fx_w3_gemv_rmsnormed(
             h.data_ptr(), _lib.dtype_code(h.dtype), self.payload(layout).data_ptr(), layout["scales"].data_ptr(),
-            scale_code, zeros_ptr, self.partials.data_ptr(), self.tiles, weight.data_ptr(), eps, out.data_ptr(),
-            rows, h.shape[-1], int(swiglu), self.format, _lib.stream_handle(h.device)), "fx_w3_gemv_rmsnormed")
+            scale_code, zeros_ptr, self.partials.data_ptr(), self.tiles, weight.data_ptr(), eps, _lib.ptr(out_index),
+            out.data_ptr(), rows, h.shape[-1], int(swiglu), self.format, _lib.stream_handle(h.device)),
+            "fx_w3_gemv_rmsnormed")
+
+    def attention_index(self, l):
+        """Where the attention of layer l writes its output (o's sorted order)."""
+        return self.o_index[l] if self.o_index else None
 
     # -- one decoder layer's four launches around the attention and the SwiGLU ------
     def qkv_in(self, session, l):
@@ -322,33 +392,41 @@ class _ResidualStream:
                                           session.qkv_out)
             return
         gemv = session.qkv[l].call
-        self.normed(gemv.layout, gemv.scale_code, gemv.zeros_ptr, gemv.out_features, session.residual,
-                    session.in_norm[l], session.eps, session.qkv_out, False)
+        self.normed(gemv.layout, gemv.scale_code, gemv.zeros_ptr, gemv.out_features,
+                    self._residual_input(session, self.qkv_index[l]), self.in_norm[l], session.eps,
+                    session.qkv_out, False)
 
     def attn_out(self, session, l):
-        """residual += o_proj(attn), with its tile sums."""
+        """residual += o_proj(attn), with its tile sums (and the sorted copy for a
+        permuted gate|up)."""
         if self.kind == "hybrid":
             self.o_out[l].residual(session.attn, session.residual, self.partials)
             return
-        self.residual(session.lin[l]["self_attn.o_proj"].gemv, session.attn, session.residual)
+        self.residual(session.lin[l]["self_attn.o_proj"].gemv, session.attn, session.residual,
+                      next_index=self.gate_up_index[l], x_sorted=True)
 
     def mlp_in(self, session, l):
-        """SiLU(gate) * up of RMSNorm(residual) into session.act (hybrid: gate | up
-        into session.gate_up_out; the down launch forms the SwiGLU)."""
+        """SiLU(gate) * up of RMSNorm(residual) into session.act, in down's sorted
+        order (hybrid: gate | up into session.gate_up_out; the down launch forms the
+        SwiGLU)."""
         if self.kind == "hybrid":
             session.gate_up[l].call.rmsnormed(session.residual, self.partials, session.post_norm[l], session.eps,
                                               session.gate_up_out)
             return
         sw = session.swiglu[l]
-        self.normed(sw.layout, sw.scale_code, sw.zeros_ptr, 2 * sw.width, session.residual, session.post_norm[l],
-                    session.eps, session.act, True)
+        self.normed(sw.layout, sw.scale_code, sw.zeros_ptr, 2 * sw.width,
+                    self._residual_input(session, self.gate_up_index[l]), self.post_norm[l], session.eps,
+                    session.act, True, out_index=self.down_index[l])
 
     def mlp_out(self, session, l):
-        """residual += down_proj(act), with its tile sums."""
+        """residual += down_proj(act), with its tile sums (and the sorted copy for
+        the next layer's permuted q|k|v)."""
         if self.kind == "hybrid":
             self.down_out[l].residual(session.gate_up_out, session.residual, self.partials, swiglu=True)
             return
-        self.residual(session.lin[l]["mlp.down_proj"].gemv, session.act, session.residual)
+        nxt = self.qkv_index[l + 1] if l + 1 < len(self.qkv_index) else None
+        self.residual(session.lin[l]["mlp.down_proj"].gemv, session.act, session.residual, next_index=nxt,
+                      x_sorted=True)
 
 
 class NativeDecodeSession:
@@ -413,8 +491,6 @@ class NativeDecodeSession:
                         for f, b in zip(self.swiglu, self.layers)]
         if w3_payload not in ("fields", "planar"):
             raise ValueError(f"w3_payload must be 'fields' or 'planar', got {w3_payload!r}")
-        self.stream = _ResidualStream.build(
-            self, _lib.PAYLOAD_FIELDS if w3_payload == "fields" else _lib.PAYLOAD_PLANAR)
         self.in_norm = [b.input_layernorm.weight for b in self.layers]
         self.post_norm = [b.post_attention_layernorm.weight for b in self.layers]
         self.q_norm = [b.self_attn.q_norm.weight for b in self.layers]
@@ -436,6 +512,8 @@ class NativeDecodeSession:
         self.o, self.act, self.down = buf(self.hidden), buf(inter), buf(self.hidden)
         self.logits = torch.empty((self.steps, cfg.vocab_size), dtype=dtype, device=self.device)
         self.predictions = torch.empty((self.steps, 1), dtype=torch.int64, device=self.device)
+        self.stream = _ResidualStream.build(
+            self, _lib.PAYLOAD_FIELDS if w3_payload == "fields" else _lib.PAYLOAD_PLANAR)
         lib = _lib.library()
         self.lib = lib
         # the final RMSNorm, LM head and argmax as one launch where the head allows it
@@ -455,17 +533,18 @@ class NativeDecodeSession:
         self.layer_observer = None
 
     # -- one token -------------------------------------------------------------------
-    def _attention(self, layer, pos):
+    def _attention(self, layer, pos, out_index=None):
         """q/k RMSNorm + RoPE, the KV-cache write of position ``pos`` and the
-        attention, from the raw q|k|v projections (one launch at decode lengths)."""
+        attention, from the raw q|k|v projections (one launch at decode lengths);
+        ``out_index``: the output in the o projection's sorted column order."""
         lib = self.lib
         _lib.check(lib.fx_decode_attention_rope(
             self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), self.q_norm[layer].data_ptr(),
             self.k_norm[layer].data_ptr(), self.cos[pos].data_ptr(), self.sin[pos].data_ptr(), self.eps,
             _lib.ROPE_STOCK, self.k_cache[layer].data_ptr(), self.v_cache[layer].data_ptr(),
-            self.attn_ws.data_ptr(), self.attn_ws.numel() * 4, self.attn.data_ptr(), self.heads, self.kv_heads,
-            self.maximum_length, self.head_dim, pos, self.scale, _lib.dtype_code(self.dtype),
-            _lib.stream_handle(self.device)), "fx_decode_attention_rope")
+            self.attn_ws.data_ptr(), self.attn_ws.numel() * 4, _lib.ptr(out_index), self.attn.data_ptr(),
+            self.heads, self.kv_heads, self.maximum_length, self.head_dim, pos, self.scale,
+            _lib.dtype_code(self.dtype), _lib.stream_handle(self.device)), "fx_decode_attention_rope")
 
     def _lm_head(self, i, hidden, norm_weight, merge=True):
         """Logits row ``i`` and its greedy token from the last hidden state
@@ -512,7 +591,7 @@ class NativeDecodeSession:
         pos = self.prefix_length + i
         for l in range(len(self.lin)):
             rs.qkv_in(self, l)
-            self._attention(l, pos)
+            self._attention(l, pos, rs.attention_index(l))
             rs.attn_out(self, l)
             rs.mlp_in(self, l)
             rs.mlp_out(self, l)

@@ -85,8 +85,15 @@ class PackedLinearBase(nn.Module):
         """Drop cached kernel bindings that hold device pointers."""
 
     def _count(self, route: str) -> None:
-        self.route_counts[route] += 1
+        self.route_counts[route] = self.route_counts.get(route, 0) + 1
         self.last_route = route
+
+    def reset_route_counts(self) -> None:
+        """Zero every route counter this module keeps (``packed_small_m`` too,
+        when the module opts into small-M inputs)."""
+        self.route_counts = {key: 0 for key in self.route_counts}
+        for key in (PACKED_M1, DENSE_FALLBACK):
+            self.route_counts.setdefault(key, 0)
 
     def bind_prepared_decode(self, dtype: torch.dtype) -> None:
         if self._decode_binding is not None:

@@ -141,7 +141,7 @@ class _TransitionScorer:
 
 def _reset_routes(modules: dict) -> None:
     for module in modules.values():
-        module.route_counts = {key: 0 for key in module.route_counts}
+        module.reset_route_counts()
 
 
 @torch.inference_mode()

@@ -88,14 +88,30 @@ def random_qwen3_model(config, *, device, dtype, seed: int = 0):
     return model.eval()
 
 
-def quantize_w3_rtn(weight, *, scale_dtype=None, zeros: bool = True) -> dict:
+def desc_act_perm(k: int, generator, device=None):
+    """The column permutation a GPTQ ``desc_act=True`` checkpoint carries after the
+    reference's conversion (``gptq_deployment.py:199-227``): columns are quantized
+    in a random activation order, group ``g`` holds the columns ranked
+    ``[128 g, 128 g + 128)`` in it (``g_idx``), and ``perm = stable_argsort(g_idx)``
+    lists each group's columns in ascending index order.  int16 ``[k]``."""
+    import torch
+
+    order = torch.randperm(k, generator=generator)
+    g_idx = torch.empty(k, dtype=torch.int64)
+    g_idx[order] = torch.arange(k) // 128
+    return torch.argsort(g_idx, stable=True).to(torch.int16).to(device)
+
+
+def quantize_w3_rtn(weight, *, scale_dtype=None, zeros: bool = True, perm=None) -> dict:
     """Round-to-nearest W3 g128 planar payload of a dense ``[O, K]`` weight.
 
     Asymmetric per (row, 128-column group): ``s = (max - min) / 7`` rounded to
     ``scale_dtype`` (fp16 by default), ``z = clamp(round(-min / s), 0, 7)``,
-    ``q = clamp(round(w / s) + z, 0, 7)``; identity permutation.  With
-    ``zeros=False`` the GPTQ-symmetric convention ``s = 2 max|w| / 7``, ``z = 4``
-    is used and no ``zeros`` field is stored.  Runs on the weight's device.
+    ``q = clamp(round(w / s) + z, 0, 7)``.  With ``zeros=False`` the
+    GPTQ-symmetric convention ``s = 2 max|w| / 7``, ``z = 4`` is used and no
+    ``zeros`` field is stored.  ``perm`` (int ``[K]``, default the identity): the
+    groups are formed over the sorted columns ``weight[:, perm]``, as a desc_act
+    checkpoint's are, and the payload stores it.  Runs on the weight's device.
     """
     import torch
 
@@ -105,7 +121,12 @@ def quantize_w3_rtn(weight, *, scale_dtype=None, zeros: bool = True) -> dict:
     o, k = weight.shape
     if k % 128:
         raise ValueError("K must be a multiple of 128")
-    w = weight.detach().float().reshape(o, k // 128, 128)
+    w = weight.detach().float()
+    if perm is not None:
+        if perm.numel() != k:
+            raise ValueError("perm must have K entries")
+        w = w[:, perm.to(device=w.device, dtype=torch.int64)]
+    w = w.reshape(o, k // 128, 128)
     if zeros:
         lo = w.amin(-1)
         hi = w.amax(-1)
@@ -117,34 +138,55 @@ def quantize_w3_rtn(weight, *, scale_dtype=None, zeros: bool = True) -> dict:
         scale = torch.where(scale > 0, scale, torch.ones_like(scale))
         zero = torch.full_like(scale, 4.0)
     q = torch.clamp(torch.round(w / scale[..., None]) + zero[..., None], 0, 7).to(torch.uint8)
-    codes = q.reshape(o, k).t().contiguous()  # [K, O]
+    codes = q.reshape(o, k).t().contiguous()  # [K, O], sorted column order
     layout = {
         "planes": planar_from_codes(codes),
         "scales": scale.t().contiguous().to(scale_dtype),          # [G, O]
-        "perm": torch.arange(k, dtype=torch.int16, device=weight.device),
+        "perm": (torch.arange(k, dtype=torch.int16, device=weight.device) if perm is None
+                 else perm.to(device=weight.device, dtype=torch.int16).contiguous()),
     }
     if zeros:
         layout["zeros"] = zero.t().contiguous().to(torch.uint8)
     return layout
 
 
-def quantize_qwen3_block(block, **kwargs) -> dict:
-    """W3 payload ``{"<module>.<field>": tensor}`` for the seven Linears of a block."""
+# Linears that read the same activation, and so share one desc_act column order
+# (GPTQ orders columns by the Hessian of their common input).
+QWEN3_INPUT_GROUPS = (("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj"), ("self_attn.o_proj",),
+                      ("mlp.gate_proj", "mlp.up_proj"), ("mlp.down_proj",))
+
+
+def quantize_qwen3_block(block, *, desc_act_generator=None, **kwargs) -> dict:
+    """W3 payload ``{"<module>.<field>": tensor}`` for the seven Linears of a block.
+    ``desc_act_generator`` (a CPU ``torch.Generator``): each input group of
+    ``QWEN3_INPUT_GROUPS`` gets one random desc_act column order
+    (:func:`desc_act_perm`), the structure of the reference's real artifacts."""
+    perms = {}
+    if desc_act_generator is not None:
+        for group in QWEN3_INPUT_GROUPS:
+            k = block.get_submodule(group[0]).weight.shape[1]
+            perm = desc_act_perm(k, desc_act_generator)
+            perms.update({name: perm for name in group})
     payload = {}
     for name in QWEN3_LINEAR_MODULES:
-        layout = quantize_w3_rtn(block.get_submodule(name).weight, **kwargs)
+        layout = quantize_w3_rtn(block.get_submodule(name).weight, perm=perms.get(name), **kwargs)
         payload.update({f"{name}.{field}": value for field, value in layout.items()})
     return payload
 
 
-def w3_quantize_qwen3_model(model, *, fallback: str = "dense", row_tile_by_shape=None, **kwargs) -> int:
+def w3_quantize_qwen3_model(model, *, fallback: str = "dense", row_tile_by_shape=None, desc_act_seed=None,
+                            **kwargs) -> int:
     """Replace every decoder block's seven Linears by ``PackedW3Linear`` (in place).
-    Returns the number of replaced Linears."""
+    ``desc_act_seed``: payloads with desc_act column orders drawn from that seed
+    (one per input group and block).  Returns the number of replaced Linears."""
+    import torch
+
     from .w3_lut_deployment import QWEN3_ROW_TILE_BY_SHAPE, replace_w3_block_linears
 
+    generator = None if desc_act_seed is None else torch.Generator().manual_seed(desc_act_seed)
     count = 0
     for block in model.model.layers:
-        payload = quantize_qwen3_block(block, **kwargs)
+        payload = quantize_qwen3_block(block, desc_act_generator=generator, **kwargs)
         policy = row_tile_by_shape
         if policy is None:
             shapes = {tuple(block.get_submodule(n).weight.shape) for n in QWEN3_LINEAR_MODULES}

@@ -174,7 +174,7 @@ class StaticDecodeSession:
     def set_audit(self, enabled: bool):
         for module in packed_modules(self.model).values():
             module._decode_audit = enabled
-            module.route_counts = {"dense_fallback": 0, "packed_m1": 0}
+            module.reset_route_counts()
 
     def routes(self) -> dict:
         return {name: dict(module.route_counts) for name, module in packed_modules(self.model).items()}

@@ -42,7 +42,7 @@ def _ints(*values):
 
 W3 = dict(x=D, x_dtype=2, planes=D, scales=D, scale_dtype=2, zeros=None, perm=None, partial=D, workspace=None,
           workspace_bytes=0, out=D, M=1, O=64, K=256, groups_per_split=2, row_tile=256, arithmetic=0,
-          residual=D, tile_sumsq=D, payload_format=0, stream=None)
+          residual=D, tile_sumsq=D, payload_format=0, out_index=None, sorted_out=None, stream=None)
 HYBRID = dict(x=D, h=D, x_dtype=2, codes=D, rows=D, columns=D, indices=D, sparse_codes=D, sparse_rows=D,
               sparse_columns=D, workspace=None, workspace_bytes=0, out=D, O=64, K=256, residual=D, tile_sumsq=D,
               swiglu=0, n_segments=2, n_tiles=16, norm_weight=D, eps=1e-6, stream=None)
@@ -63,14 +63,15 @@ DEFAULTS = {
                           O=64, K=256, stream=None),
     "fx_rmsnorm": dict(x=D, residual=None, weight=D, out=D, residual_out=None, rows=1, hidden=4096, eps=1e-6,
                        dtype=2, stream=None),
-    "fx_decode_attention": dict(q=D, k_cache=D, v_cache=D, workspace=D, workspace_bytes=1 << 24, out=D,
+    "fx_decode_attention": dict(q=D, k_cache=D, v_cache=D, workspace=D, workspace_bytes=1 << 24, out_index=None, out=D,
                                 n_q_heads=32, n_kv_heads=8, max_len=1024, head_dim=128, position=100,
                                 scale=0.088, dtype=2, stream=None),
     "fx_silu_mul": dict(gate=D, up=D, out=D, n=4096, dtype=2, stream=None),
     "fx_lm_head_argmax": dict(hidden=D, norm_weight=D, eps=1e-6, weight=D, logits=D, prediction=D, workspace=D,
                               workspace_bytes=1 << 20, vocab=1000, hidden_size=4096, dtype=2, stream=None),
     "fx_lm_head_merge": dict(workspace=D, workspace_bytes=1 << 20, vocab=1000, prediction=D, stream=None),
-    "fx_decode_embed": dict(token=D, table=D, vocab=1000, hidden=4096, out=D, tile_sumsq=D, lm_workspace=None,
+    "fx_decode_embed": dict(token=D, table=D, vocab=1000, hidden=4096, out=D, tile_sumsq=D, out_index=None,
+                            sorted_out=None, lm_workspace=None,
                             lm_workspace_bytes=0, lm_vocab=0, prediction=None, dtype=2, stream=None),
     "fx_two_base_gemv": dict(x=D, x_dtype=2, planes=D, coef=D, srow=D, tcol=D, salient=None, salient_idx=None,
                              n_salient=0, workspace=None, workspace_bytes=0, out=D, O=64, K=256, stream=None),
@@ -148,8 +149,13 @@ CASES = [
     ("fx_w3_gemv_swiglu", dict(out=None), "out must be non-null"),
     ("fx_w3_gemv_residual", dict(residual=None), "residual, out and tile_sumsq must be non-null"),
     ("fx_w3_gemv_residual", dict(tile_sumsq=None), "residual, out and tile_sumsq must be non-null"),
-    ("fx_w3_gemv_residual", dict(payload_format=1, perm=D), "the field layout takes no column permutation"),
     ("fx_w3_gemv_residual", dict(payload_format=7), "payload_format"),
+    ("fx_w3_gemv_residual", dict(out_index=D), "given together"),
+    ("fx_w3_gemv_residual", dict(sorted_out=D + 4096), "given together"),
+    ("fx_w3_gemv_residual", dict(out_index=D + 1, sorted_out=D + 4096), "out_index must be 2-byte aligned"),
+    ("fx_w3_gemv_residual", dict(out_index=D + 4096, sorted_out=D), "must not alias"),
+    ("fx_w3_gemv_swiglu", dict(out_index=D + 1), "out_index must be 2-byte aligned"),
+    ("fx_w3_gemv_rmsnormed", dict(out_index=D + 4096, swiglu=0), "out_index applies to the SwiGLU output"),
     ("fx_w3_gemv_rmsnormed", dict(n_tiles=15), "n_tiles must be ceil(K / 16)"),
     ("fx_w3_gemv_rmsnormed", dict(norm_weight=D + 2), "norm weight must be 16-byte aligned"),
     ("fx_w3_gemv_rmsnormed", dict(tile_sumsq=None), "must be non-null"),
@@ -195,6 +201,7 @@ CASES = [
     ("fx_decode_attention_rope", dict(rope_mode=9), "rope_mode must be FX_ROPE_STOCK or FX_ROPE_FUSED"),
     ("fx_decode_attention_rope", dict(k=D + 8), "16-byte aligned"),
     ("fx_decode_attention_rope", dict(cos=None), "non-null"),
+    ("fx_decode_attention", dict(out_index=D + 1), "out_index must be 2-byte aligned"),
     ("fx_silu_mul", dict(n=0), "n must be positive"),
     ("fx_silu_mul", dict(dtype=0), "dtype must be fp16 or bf16"),
     ("fx_silu_mul", dict(up=None), "non-null"),
@@ -216,6 +223,9 @@ CASES = [
     ("fx_decode_embed", dict(table=D + 8), "aligned"),
     ("fx_decode_embed", dict(dtype=0), "dtype must be fp16 or bf16"),
     ("fx_decode_embed", dict(out=None), "non-null"),
+    ("fx_decode_embed", dict(out_index=D + 8192), "given together"),
+    ("fx_decode_embed", dict(out_index=D + 8200, sorted_out=D + 16384), "out_index must be 16-byte aligned"),
+    ("fx_decode_embed", dict(out_index=D + 8192, sorted_out=D), "must not alias"),
     # two-base GEMVs
     ("fx_two_base_gemv", dict(O=0), "O must be positive and K a positive multiple of 128"),
     ("fx_two_base_gemv", dict(K=200), "O must be positive and K a positive multiple of 128"),

@@ -118,3 +118,27 @@ def test_w3_decode_close_to_bf16_model(gpu):
     # ~0.88 cosine similarity; a broken packing or scale would be near 0
     cos = torch.nn.functional.cosine_similarity(got.flatten(), want.flatten(), dim=0)
     assert cos > 0.75, cos
+
+
+def test_decode_trace_short_prompt_on_small_m_modules(gpu):
+    """Modules that opt into 2..8-row inputs (max_packed_rows=8) serve a 4-token
+    prompt on the small-M packed route inside decode_trace, whose counter reset
+    keeps that route's key; the trace equals the same trace with the prompt served
+    densely within the bars of test_dynamic_static_graph_agree."""
+    from marlin_style_fluxbin_amd.w3_lut_deployment import PackedW3Linear
+
+    model = _model(gpu)
+    ids, forced = _inputs(gpu)
+    short = ids[:, :4]
+    dense = decode_trace(model, short, steps=STEPS, forced_tokens=forced)
+    for block in model.model.layers:
+        for name, module in list(block.named_modules()):
+            if isinstance(module, PackedW3Linear):
+                parent, attr = name.rsplit(".", 1)
+                setattr(block.get_submodule(parent), attr,
+                        PackedW3Linear(module.layout(), fallback="dense", row_tile=256, max_packed_rows=8))
+    small = decode_trace(model, short, steps=STEPS, forced_tokens=forced)
+    assert all(r == {"packed_m1": STEPS, "dense_fallback": 0, "packed_small_m": 1} for r in small["routes"].values())
+    assert validate_routes(small, expected_linears=14, steps=STEPS)
+    report = compare_trace(small, dense, logprob_tolerance=0.05)
+    assert report["passed"], report

@@ -153,7 +153,7 @@ def test_split_launches_equal_the_fused_call(gpu, vocab, k):
     sums = torch.empty(16, dtype=torch.float32, device=gpu)
     pred2 = torch.full((1,), -1, dtype=torch.int64, device=gpu)
     _lib.check(lib.fx_decode_embed(token.data_ptr(), table.data_ptr(), 5, 256, row.data_ptr(), sums.data_ptr(),
-                                   ws.data_ptr(), ws.numel(), vocab, pred2.data_ptr(), _lib.FX_BF16,
+                                   None, None, ws.data_ptr(), ws.numel(), vocab, pred2.data_ptr(), _lib.FX_BF16,
                                    _lib.stream_handle(gpu)), "decode_embed")
     assert torch.equal(pred2, want_pred)
 
@@ -161,27 +161,38 @@ def test_split_launches_equal_the_fused_call(gpu, vocab, k):
 def test_decode_embed_row_and_tile_sums(gpu):
     """fx_decode_embed: the token's row bit for bit, each 16-element tile's sum of
     squares against float64, NaNs for a token outside the table, no merge when
-    prediction is NULL."""
+    prediction is NULL; with an output index, the row also in the first q|k|v's
+    sorted column order (sorted[k] = row[P[k]] for out_index = P^-1)."""
+    from marlin_style_fluxbin_amd.native_decode import inverse_index
+
     lib = _lib.library()
     g = torch.Generator().manual_seed(3)
+    nxt = torch.randperm(4096, generator=g).to(torch.int16).to(gpu)
+    index = inverse_index(nxt)
     for dtype, code in ((torch.bfloat16, _lib.FX_BF16), (torch.float16, _lib.FX_F16)):
         table = (torch.randn(40, 4096, generator=g) * 2).to(dtype).to(gpu)
         out = torch.empty(1, 4096, dtype=dtype, device=gpu)
+        sorted_out = torch.empty(1, 4096, dtype=dtype, device=gpu)
         sums = torch.empty(256, dtype=torch.float32, device=gpu)
         for tok in (0, 17, 39):
             token = torch.tensor([tok], dtype=torch.int64, device=gpu)
-            _lib.check(lib.fx_decode_embed(token.data_ptr(), table.data_ptr(), 40, 4096, out.data_ptr(),
-                                           sums.data_ptr(), None, 0, 0, None, code, _lib.stream_handle(gpu)),
-                       "decode_embed")
-            assert torch.equal(out[0], table[tok])
-            want = (table[tok].double().cpu().view(256, 16) ** 2).sum(1)
-            np.testing.assert_allclose(sums.double().cpu().numpy(), want.numpy(), rtol=1e-5, atol=0)
+            for idx, so in ((None, None), (index, sorted_out)):
+                sorted_out.fill_(float("nan"))
+                _lib.check(lib.fx_decode_embed(token.data_ptr(), table.data_ptr(), 40, 4096, out.data_ptr(),
+                                               sums.data_ptr(), _lib.ptr(idx), _lib.ptr(so), None, 0, 0, None, code,
+                                               _lib.stream_handle(gpu)), "decode_embed")
+                assert torch.equal(out[0], table[tok])
+                if idx is not None:
+                    assert torch.equal(sorted_out[0], table[tok][nxt.long()])
+                want = (table[tok].double().cpu().view(256, 16) ** 2).sum(1)
+                np.testing.assert_allclose(sums.double().cpu().numpy(), want.numpy(), rtol=1e-5, atol=0)
         for bad in (-1, 40):
             token = torch.tensor([bad], dtype=torch.int64, device=gpu)
             _lib.check(lib.fx_decode_embed(token.data_ptr(), table.data_ptr(), 40, 4096, out.data_ptr(),
-                                           sums.data_ptr(), None, 0, 0, None, code, _lib.stream_handle(gpu)),
-                       "decode_embed")
+                                           sums.data_ptr(), index.data_ptr(), sorted_out.data_ptr(), None, 0, 0, None,
+                                           code, _lib.stream_handle(gpu)), "decode_embed")
             assert torch.isnan(out.float()).all() and torch.isnan(sums).all()
-    rc = lib.fx_decode_embed(token.data_ptr(), table.data_ptr(), 40, 4004, out.data_ptr(), sums.data_ptr(), None, 0,
-                             0, None, _lib.FX_BF16, _lib.stream_handle(gpu))
+            assert torch.isnan(sorted_out.float()).all()
+    rc = lib.fx_decode_embed(token.data_ptr(), table.data_ptr(), 40, 4004, out.data_ptr(), sums.data_ptr(), None,
+                             None, None, 0, 0, None, _lib.FX_BF16, _lib.stream_handle(gpu))
     assert rc == 1 and b"multiple of 16" in lib.fx_last_error()

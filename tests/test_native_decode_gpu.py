@@ -49,7 +49,7 @@ def test_decode_attention(gpu, dtype, hq, hk, d, lmax, pos):
     ws = torch.full((nbytes,), 0xFF, dtype=torch.uint8, device=gpu)  # NaN partials until written
     out = torch.empty(hq, d, dtype=DT[dtype], device=gpu)
     qd, kd, vd = q.to(gpu), kc.to(gpu), vc.to(gpu)
-    _lib.check(lib.fx_decode_attention(qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), ws.data_ptr(), nbytes,
+    _lib.check(lib.fx_decode_attention(qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), ws.data_ptr(), nbytes, None,
                                        out.data_ptr(), hq, hk, lmax, d, pos, 1 / np.sqrt(d),
                                        _lib.dtype_code(DT[dtype]), _lib.stream_handle(gpu)), "attention")
     exact = decode.gqa_attention(q.float().numpy(), kc.float().numpy(), vc.float().numpy(), pos, 1 / np.sqrt(d))
@@ -91,8 +91,8 @@ def test_decode_attention_rope(gpu, dtype, hq, hk, d, lmax, pos, rope_mode):
     _lib.check(lib.fx_decode_attention_rope(
         dev["q"].data_ptr(), dev["k"].data_ptr(), dev["v"].data_ptr(), dev["qw"].data_ptr(), dev["kw"].data_ptr(),
         cos_d.data_ptr(), sin_d.data_ptr(), 1e-6, rope_mode, dev["kc"].data_ptr(), dev["vc"].data_ptr(),
-        ws.data_ptr(), nbytes, out.data_ptr(), hq, hk, lmax, d, pos, 1 / np.sqrt(d), _lib.dtype_code(DT[dtype]),
-        _lib.stream_handle(gpu)), "attention_rope")
+        ws.data_ptr(), nbytes, None, out.data_ptr(), hq, hk, lmax, d, pos, 1 / np.sqrt(d),
+        _lib.dtype_code(DT[dtype]), _lib.stream_handle(gpu)), "attention_rope")
     qn = norms.rms_norm(q.float().numpy(), qw.float().numpy(), 1e-6, dtype)
     kn = norms.rms_norm(k.float().numpy(), kw.float().numpy(), 1e-6, dtype)
     qr = norms.apply_rope(qn, cos_t, sin_t, dtype, fused=rope_mode == 2)
@@ -131,7 +131,7 @@ def test_decode_attention_workspace_reuse(gpu, hq, hk):
     qf, kf, vf = q.float().numpy(), kc.float().numpy(), vc.float().numpy()
     for pos in [5, 300, 15, 16, 900, 511, 1099, 40, 63, 64, 543, 700]:
         _lib.check(lib.fx_decode_attention(qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), ws.data_ptr(), nbytes,
-                                           out.data_ptr(), hq, hk, lmax, d, pos, 1 / np.sqrt(d),
+                                           None, out.data_ptr(), hq, hk, lmax, d, pos, 1 / np.sqrt(d),
                                            _lib.dtype_code(torch.bfloat16), _lib.stream_handle(gpu)), "attention")
         exact = decode.gqa_attention(qf, kf, vf, pos, 1 / np.sqrt(d))
         got = out.float().cpu().numpy()
@@ -141,7 +141,7 @@ def test_decode_attention_workspace_reuse(gpu, hq, hk):
 def test_decode_attention_rejects_bad_position(gpu):
     lib = _lib.library()
     t = torch.empty(4096, dtype=torch.bfloat16, device=gpu)
-    rc = lib.fx_decode_attention(t.data_ptr(), t.data_ptr(), t.data_ptr(), t.data_ptr(), 8192, t.data_ptr(),
+    rc = lib.fx_decode_attention(t.data_ptr(), t.data_ptr(), t.data_ptr(), t.data_ptr(), 8192, None, t.data_ptr(),
                                  4, 2, 16, 64, 16, 0.125, 2, None)
     assert rc == 1 and "position" in lib.fx_last_error().decode()
 
@@ -203,7 +203,7 @@ def test_gemv_swiglu_matches_gemvs_then_silu_mul(gpu, inter, k, dtype, scale_dty
     torch.cuda.synchronize()
     assert torch.equal(got, want)
     rc = lib.fx_w3_gemv_swiglu(x.data_ptr(), _lib.dtype_code(DT[dtype]), fused["planes"].data_ptr(),
-                               fused["scales"].data_ptr(), _lib.dtype_code(scale_dtype), None, None,
+                               fused["scales"].data_ptr(), _lib.dtype_code(scale_dtype), None, None, None,
                                got.data_ptr(), 2 * inter + 1, k, _lib.PAYLOAD_PLANAR, None)
     assert rc == 1 and "even" in lib.fx_last_error().decode()
 
@@ -232,12 +232,14 @@ def _gemv_fields(x, fields, layout, out):
 def test_gemv_residual_epilogue(gpu, o, k, dtype, permute, fmt):
     """fx_w3_gemv_residual: out = round(residual + round(x @ W.T)) bit for bit
     (the plain GEMV of the same payload format, then the dtype's own add), in
-    place, plus the sums of out^2 over 16-row tiles."""
+    place, plus the sums of out^2 over 16-row tiles; with an output index, the
+    same out also in the next GEMV's sorted order (sorted[k] = out[P[k]] for
+    out_index = P^-1).  The field layout gathers a permuted x as the planar
+    kernel does."""
+    from marlin_style_fluxbin_amd.native_decode import inverse_index
     from marlin_style_fluxbin_amd.w3_lut_deployment import W3Gemv
     from payloads import config_codes, layout_from_codes
 
-    if fmt == "fields" and permute:
-        pytest.skip("the field layout takes the identity column order only")
     codes, scales, zero, perm = config_codes(o, k, seed=o + k, zeros=True, scale_dtype=torch.float16, permute=permute)
     layout = {n: v.to(gpu) for n, v in layout_from_codes(codes, scales, zero, perm).items()}
     gemv = W3Gemv(layout)
@@ -248,20 +250,25 @@ def test_gemv_residual_epilogue(gpu, o, k, dtype, permute, fmt):
     payload = layout["planes"] if fmt == "planar" else _fields(layout["planes"])
     if fmt == "planar":
         gemv(x, y)
-    else:
-        _gemv_fields(x, payload, layout, y)
+    else:  # the gather gives the same staged operands as the pre-gathered row
+        _gemv_fields(x if perm is None else x[:, layout["perm"].long()].contiguous(), payload, layout, y)
     want = res + y
     tiles = (o + 15) // 16
     sums = torch.full((tiles,), float("nan"), device=gpu)
-    got = res.clone()
     lib = _lib.library()
-    _lib.check(lib.fx_w3_gemv_residual(x.data_ptr(), _lib.dtype_code(DT[dtype]), payload.data_ptr(),
-                                       layout["scales"].data_ptr(), _lib.dtype_code(torch.float16),
-                                       layout["zeros"].data_ptr(), gemv.perm_ptr, got.data_ptr(), got.data_ptr(),
-                                       sums.data_ptr(), o, k, 0 if fmt == "planar" else 1, _lib.stream_handle(gpu)),
-               "residual")
-    torch.cuda.synchronize()
-    assert torch.equal(got, want)
+    nxt = torch.randperm(o, generator=g).to(torch.int16).to(gpu)  # the next GEMV's column order
+    for index in (None, inverse_index(nxt)):
+        got = res.clone()
+        sorted_out = None if index is None else torch.full_like(res, float("nan"))
+        _lib.check(lib.fx_w3_gemv_residual(x.data_ptr(), _lib.dtype_code(DT[dtype]), payload.data_ptr(),
+                                           layout["scales"].data_ptr(), _lib.dtype_code(torch.float16),
+                                           layout["zeros"].data_ptr(), gemv.perm_ptr, got.data_ptr(), got.data_ptr(),
+                                           sums.data_ptr(), _lib.ptr(index), _lib.ptr(sorted_out), o, k,
+                                           0 if fmt == "planar" else 1, _lib.stream_handle(gpu)), "residual")
+        torch.cuda.synchronize()
+        assert torch.equal(got, want)
+        if index is not None:
+            assert torch.equal(sorted_out, got[:, nxt.long()])
     h = want.double().cpu().numpy()[0]
     exact = np.array([np.sum(h[16 * t:16 * t + 16] ** 2) for t in range(tiles)])
     assert np.allclose(sums.cpu().numpy(), exact, rtol=2e-6, atol=0)
@@ -301,7 +308,7 @@ def test_gemv_rmsnormed_prologue(gpu, rows, k, dtype, swiglu, fmt):
     elif swiglu:
         _lib.check(lib.fx_w3_gemv_swiglu(normed.data_ptr(), _lib.dtype_code(DT[dtype]), payload.data_ptr(),
                                          layout["scales"].data_ptr(), _lib.dtype_code(torch.float16),
-                                         layout["zeros"].data_ptr(), None, want.data_ptr(), rows, k, fcode,
+                                         layout["zeros"].data_ptr(), None, None, want.data_ptr(), rows, k, fcode,
                                          _lib.stream_handle(gpu)), "swiglu fields")
     elif fmt == "planar":
         W3Gemv(layout)(normed, want)
@@ -311,13 +318,26 @@ def test_gemv_rmsnormed_prologue(gpu, rows, k, dtype, swiglu, fmt):
     _lib.check(lib.fx_w3_gemv_rmsnormed(h.data_ptr(), _lib.dtype_code(DT[dtype]), payload.data_ptr(),
                                         layout["scales"].data_ptr(), _lib.dtype_code(torch.float16),
                                         layout["zeros"].data_ptr(), sums.data_ptr(), sums.numel(), weight.data_ptr(),
-                                        1e-6, got.data_ptr(), rows, k, int(swiglu), fcode, _lib.stream_handle(gpu)),
-               "normed")
+                                        1e-6, None, got.data_ptr(), rows, k, int(swiglu), fcode,
+                                        _lib.stream_handle(gpu)), "normed")
     torch.cuda.synchronize()
     assert torch.equal(got, want)
+    if swiglu:  # the SwiGLU output in the next GEMV's sorted order: got[k] = want[P[k]]
+        from marlin_style_fluxbin_amd.native_decode import inverse_index
+
+        nxt = torch.randperm(width, generator=g).to(torch.int16).to(gpu)
+        got = torch.full_like(want, float("nan"))
+        _lib.check(lib.fx_w3_gemv_rmsnormed(h.data_ptr(), _lib.dtype_code(DT[dtype]), payload.data_ptr(),
+                                            layout["scales"].data_ptr(), _lib.dtype_code(torch.float16),
+                                            layout["zeros"].data_ptr(), sums.data_ptr(), sums.numel(),
+                                            weight.data_ptr(), 1e-6, inverse_index(nxt).data_ptr(), got.data_ptr(),
+                                            rows, k, 1, fcode, _lib.stream_handle(gpu)), "normed, output index")
+        torch.cuda.synchronize()
+        assert torch.equal(got, want[:, nxt.long()])
     rc = lib.fx_w3_gemv_rmsnormed(h.data_ptr(), _lib.dtype_code(DT[dtype]), layout["planes"].data_ptr(),
                                   layout["scales"].data_ptr(), _lib.dtype_code(torch.float16), None, sums.data_ptr(),
-                                  sums.numel() + 1, weight.data_ptr(), 1e-6, got.data_ptr(), rows, k, 0, fcode, None)
+                                  sums.numel() + 1, weight.data_ptr(), 1e-6, None, got.data_ptr(), rows, k, 0, fcode,
+                                  None)
     assert rc == 1 and "n_tiles" in lib.fx_last_error().decode()
 
 

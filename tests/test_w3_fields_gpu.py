@@ -117,8 +117,9 @@ def test_field_layout_argument_checks(gpu):
     out = torch.zeros(1, 16, dtype=torch.bfloat16, device=gpu)
     part = torch.zeros(1, device=gpu)
     rc = lib.fx_w3_gemv_residual(x.data_ptr(), 2, t.data_ptr(), sc.data_ptr(), 1, None, perm.data_ptr(),
-                                 out.data_ptr(), out.data_ptr(), part.data_ptr(), 16, 128, _lib.PAYLOAD_FIELDS, None)
-    assert rc == 1 and "permutation" in lib.fx_last_error().decode()
+                                 out.data_ptr(), out.data_ptr(), part.data_ptr(), perm.data_ptr(), None, 16, 128,
+                                 _lib.PAYLOAD_FIELDS, None)
+    assert rc == 1 and "together" in lib.fx_last_error().decode()
     rc = lib.fx_w3_gemv_residual(x.data_ptr(), 2, t.data_ptr(), sc.data_ptr(), 1, None, None, out.data_ptr(),
-                                 out.data_ptr(), part.data_ptr(), 16, 128, 7, None)
+                                 out.data_ptr(), part.data_ptr(), None, None, 16, 128, 7, None)
     assert rc == 1 and "payload_format" in lib.fx_last_error().decode()

@@ -205,3 +205,27 @@ def test_engine_backends_for_w3_and_hybrid_formats():
     assert backend_for_format(d.FORMAT).kernel == "v1"
     with pytest.raises(ValueError):
         backend_for_format("unknown-format")
+
+
+def test_route_counter_reset_keeps_the_small_m_key():
+    """The trial and session resets zero every counter a module keeps: a module
+    that opts into 2..8-row inputs keeps ``packed_small_m`` across a reset (a
+    reset to the two reference keys made its next small-M call a KeyError), and
+    the route check accepts a short prompt served on that route."""
+    from marlin_style_fluxbin_amd.full_model_trial import _fallback_policy, validate_routes
+
+    module = wl.PackedW3Linear(tiny_layout(), row_tile=256, max_packed_rows=8)
+    module._count("packed_small_m")
+    with _fallback_policy({"m": module}):
+        assert module.route_counts == {"packed_m1": 0, "dense_fallback": 0, "packed_small_m": 0}
+        module._count("packed_small_m")
+        module._count("packed_m1")
+    plain = wl.PackedW3Linear(tiny_layout(), row_tile=256)
+    plain.reset_route_counts()
+    assert plain.route_counts == {"packed_m1": 0, "dense_fallback": 0}
+    plain._count("dense_fallback")
+    plain._count("packed_m1")
+    trace = {"routes": {"a": dict(module.route_counts), "b": dict(plain.route_counts)}}
+    assert validate_routes(trace, expected_linears=2, steps=1)
+    trace["routes"]["a"]["dense_fallback"] = 1  # the prompt served twice
+    assert not validate_routes(trace, expected_linears=2, steps=1)
