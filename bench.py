@@ -1031,6 +1031,70 @@ def summarize_sq(csv_path, name_filter):
               f"{m.get('SQ_INSTS_LDS', 0) / w:.1f} | {m.get('SQ_INSTS_VMEM', 0) / w:.1f} | {conflicts:.2f} |")
 
 
+def summarize_counters(csv_paths, name_filter):
+    """Every counter of one or more rocprofv3 counter CSVs, averaged per dispatch
+    for each (kernel, grid) whose name contains name_filter; per wave too where
+    the CSV holds SQ_WAVES.  FETCH_SIZE / WRITE_SIZE are KiB per dispatch, unscaled."""
+    import csv
+    from collections import defaultdict
+
+    vals = defaultdict(lambda: defaultdict(list))
+    for path in csv_paths:
+        with open(path, newline="") as f:
+            for row in csv.DictReader(f):
+                name = row["Kernel_Name"].split("(")[0]
+                if name_filter in name:
+                    key = (name, row.get("Grid_Size") or row.get("Grid_Size_X", ""))
+                    vals[key][row["Counter_Name"]].append(float(row["Counter_Value"]))
+    for (name, grid), d in sorted(vals.items()):
+        m = {c: sum(v) / len(v) for c, v in d.items()}
+        waves = m.get("SQ_WAVES")
+        print(f"`{name}` grid {grid}, {max(len(v) for v in d.values())} dispatches")
+        print("| counter | mean per dispatch | per wave |")
+        print("|---|---:|---:|")
+        for c in sorted(m):
+            per_wave = f"{m[c] / waves:.1f}" if waves and c.startswith("SQ_") and c != "SQ_WAVES" else ""
+            print(f"| {c} | {m[c]:.1f} | {per_wave} |")
+
+
+def pmc_attention_target(layers=36, position=543, rounds=8):
+    """Workload for ``rocprofv3 --pmc`` passes over the decode attention: Qwen3-8B
+    heads (32 query / 8 KV heads of 128), the native decode's call
+    (``fx_decode_attention_rope``: q/k norm, RoPE and the cache write folded in;
+    its combine launch), over ``layers`` distinct 544-slot KV caches (as the decode
+    graph walks them) at ``position``, ``rounds`` times, a progress line per round."""
+    import math
+
+    import torch
+
+    from marlin_style_fluxbin_amd import _lib
+
+    device = torch.device("cuda:0")
+    gen = torch.Generator(device=device).manual_seed(0)
+    hq, hk, d, lmax = 32, 8, 128, position + 1
+    lib = _lib.library()
+    bf = torch.bfloat16
+    kc = [torch.randn(hk, lmax, d, device=device, generator=gen).to(bf) for _ in range(layers)]
+    vc = [torch.randn(hk, lmax, d, device=device, generator=gen).to(bf) for _ in range(layers)]
+    qkv = torch.randn(hq * d + 2 * hk * d, device=device, generator=gen).to(bf)
+    q, k, v = qkv[:hq * d], qkv[hq * d:(hq + hk) * d], qkv[(hq + hk) * d:]
+    w = (1 + 0.02 * torch.randn(2, d, device=device, generator=gen)).to(bf)
+    cos = torch.randn(d, device=device, generator=gen).to(bf)
+    sin = torch.randn(d, device=device, generator=gen).to(bf)
+    nbytes = lib.fx_decode_attention_workspace_bytes(hq, lmax, d)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
+    out = torch.empty(hq * d, dtype=bf, device=device)
+    for r in range(rounds):
+        for kl, vl in zip(kc, vc):
+            _lib.check(lib.fx_decode_attention_rope(
+                q.data_ptr(), k.data_ptr(), v.data_ptr(), w[0].data_ptr(), w[1].data_ptr(), cos.data_ptr(),
+                sin.data_ptr(), 1e-6, _lib.ROPE_STOCK, kl.data_ptr(), vl.data_ptr(), ws.data_ptr(), nbytes, None,
+                out.data_ptr(), hq, hk, lmax, d, position, 1 / math.sqrt(d), _lib.FX_BF16,
+                _lib.stream_handle(device)), "fx_decode_attention_rope")
+        torch.cuda.synchronize()
+        print(f"# pmc-attention round {r + 1}/{rounds}", flush=True)
+
+
 def summarize_pmc(csv_paths, out_json):
     """Average rocprofv3 counter CSVs per kernel; scale FETCH_SIZE / WRITE_SIZE
     (KiB per dispatch) by what they read for the copy kernel of known size."""
@@ -1128,6 +1192,10 @@ def main():
     parser.add_argument("--fused-ops", action="store_true", help="run only the config-2 fused-ops benchmark")
     parser.add_argument("--summarize-pmc", nargs="+", metavar="CSV",
                         help="rocprofv3 counter CSVs -> profiles/w3_mfma_traffic.json")
+    parser.add_argument("--pmc-attention", action="store_true",
+                        help="run the counter-collection workload of the decode attention")
+    parser.add_argument("--summarize-counters", nargs="+", metavar="ARG",
+                        help="NAME CSV [CSV ...]: every counter per dispatch of kernels matching NAME")
     parser.add_argument("--summarize-trace", nargs=2, metavar=("CSV", "LAST"),
                         help="per-kernel summary of the last LAST dispatches of a kernel-trace CSV")
     args = parser.parse_args()
@@ -1142,6 +1210,12 @@ def main():
         return
     if args.pmc_hybrid:
         pmc_hybrid_target()
+        return
+    if args.pmc_attention:
+        pmc_attention_target()
+        return
+    if args.summarize_counters:
+        summarize_counters(args.summarize_counters[1:], args.summarize_counters[0])
         return
     if args.summarize_sq:
         summarize_sq(args.summarize_sq[0], args.summarize_sq[1])

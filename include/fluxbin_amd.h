@@ -6,7 +6,9 @@
  * Every entry point is asynchronous on that stream, allocates nothing and never
  * synchronises, so all of them may be captured into a HIP graph.  Return value:
  * FX_OK, or an FX_E* code with a message available from fx_last_error() (per
- * calling thread).
+ * calling thread).  Host threads may call concurrently on their own streams (a
+ * call's state lives in its arguments) with one exception: fx_w3_gemv_noalloc's
+ * calls share a per-GPU scratch array and must not overlap on one GPU.
  *
  * dtype codes: FX_F32 = 0, FX_F16 = 1, FX_BF16 = 2.
  *
