@@ -158,3 +158,33 @@ def test_rank_one_rejects_bad_arguments(gpu):
     need = lib.fx_two_base_gemv_workspace_bytes(16, 8192)
     assert need > 0
     assert call(args(o=16, k=8192)) == 1 and "workspace" in lib.fx_last_error().decode()
+
+
+@pytest.mark.parametrize("tiling", [None, (8, 2, 16, 1), (12, 1, 64, 3)])
+def test_rank_one_outlier_activation(gpu, tiling):
+    """One activation column ~1e3 among ~1e-2 (tests/test_two_base_numerics.py's
+    case: in half the rows the outlier cancels and the small columns are the whole
+    output).  The kernel equals the CPU emulation of its fixed point (one exponent
+    per 512-column batch, two int8 digits) up to the bf16 output rounding and fp32
+    sums, and so stays within the stated per-row bound of the float64 truth."""
+    from tests.test_two_base_numerics import outlier_case, emulate
+
+    p, x = outlier_case()
+    layout = _layout(p, gpu)
+    xt = torch.from_numpy(x).to(torch.bfloat16)
+    o, k = p["planes"].shape[1], 128 * p["planes"].shape[0]
+    out = torch.full((1, o), float("nan"), dtype=torch.bfloat16, device=gpu)
+    if tiling is None:
+        TwoBaseGemv(layout)(xt.to(gpu), out)
+    else:
+        nbytes = _lib.library().fx_two_base_gemv_config_workspace_bytes(o, k, *tiling)
+        ws = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=gpu)
+        two_base_gemv(xt.to(gpu), layout, out, ws, tiling=tiling)
+    got = out.float().cpu().numpy()[0].astype(np.float64)
+    exact = tb.rank_one_matvec(x, p)[0]
+    emulated, bound = emulate(x, p)
+    u_abs = np.abs(x[0].astype(np.float64) * p["tcol"].astype(np.float64)).sum()
+    coef = np.abs(p["srow"].astype(np.float64)) * (np.abs(p["coef"][0]) + np.abs(p["coef"][1])).astype(np.float64)
+    slack = 2.0 ** -9 * np.abs(got) + 2e-6 * coef * u_abs  # bf16 output rounding, fp32 sums of ~1e3 terms
+    assert np.all(np.abs(got - emulated) <= slack), np.max(np.abs(got - emulated) / slack)
+    assert np.all(np.abs(got - exact) <= bound + slack)
