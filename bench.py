@@ -62,6 +62,39 @@ def algorithmic_bytes(o: int, k: int, m: int = 1, zeros: bool = True, perm: bool
     return total
 
 
+def make_payloads(o, k, device, generator, copies):
+    """``copies`` payloads stored back to back (planes [copies, G, 3, O, 16], scales,
+    zeros), returned as the stacked tensors and per-copy views: one strided-batch
+    launch walks the stacked tensors, the per-launch arms take the views."""
+    import torch
+
+    g = k // 128
+    stacked = {
+        "planes": torch.randint(0, 256, (copies, g, 3, o, 16), dtype=torch.uint8, device=device, generator=generator),
+        "scales": (torch.rand((copies, g, o), device=device, generator=generator) * 0.015 + 0.005).half(),
+        "zeros": torch.randint(3, 5, (copies, g, o), dtype=torch.uint8, device=device, generator=generator),
+    }
+    perm = torch.arange(k, dtype=torch.int16, device=device)
+    views = [{"planes": stacked["planes"][i], "scales": stacked["scales"][i], "perm": perm,
+              "zeros": stacked["zeros"][i]} for i in range(copies)]
+    return stacked, views
+
+
+def batched_call(lib, x, weights, stacked, out, o, k, fmt, device):
+    """One fx_w3_gemv_strided_batched launch over every stacked payload (x row p
+    for payload p)."""
+    from marlin_style_fluxbin_amd import _lib
+
+    n = weights.shape[0]
+    if x.numel() < n * k or out.numel() < n * o or not (x.is_contiguous() and out.is_contiguous()):
+        raise ValueError(f"strided batch of {n}: x needs {n} x {k} and out {n} x {o} contiguous elements")
+    _lib.check(lib.fx_w3_gemv_strided_batched(
+        x.data_ptr(), _lib.dtype_code(x.dtype), k, weights.data_ptr(), weights[0].numel(),
+        stacked["scales"].data_ptr(), _lib.dtype_code(stacked["scales"].dtype), stacked["scales"][0].numel(),
+        stacked["zeros"].data_ptr(), stacked["zeros"][0].numel(), out.data_ptr(), o, n, o, k, fmt,
+        _lib.stream_handle(device)), "fx_w3_gemv_strided_batched")
+
+
 def make_payload(o, k, device, generator):
     import torch
 
@@ -151,7 +184,7 @@ def bench_shape(o, k, device, steps, warmup, stream, min_bytes=320e6, min_copies
     nbytes = algorithmic_bytes(o, k)
     perm_bytes = algorithmic_bytes(o, k, perm=True)
     copies = max(min_copies, int(min_bytes // nbytes) + 1)
-    payloads = [make_payload(o, k, device, gen) for _ in range(copies)]
+    stacked, payloads = make_payloads(o, k, device, gen, copies)
     gemvs = [W3Gemv(p, perm_identity=True) for p in payloads]
     # desc_act: each copy its own group-preserving order (perm = argsort(g_idx))
     permuted = [W3Gemv(dict(p, perm=desc_act_perm(k, cpu_gen, device)), perm_identity=False) for p in payloads]
@@ -191,6 +224,17 @@ def bench_shape(o, k, device, steps, warmup, stream, min_bytes=320e6, min_copies
 
     graphs["fields"] = (capture(over([lambda p=p, f=f: field_call(p, f) for p, f in zip(payloads, fields)]),
                                 stream), copies)
+    # steady state: the same payloads walked by one launch (fx_w3_gemv_strided_batched),
+    # planar and field layout -- the kernel without the per-launch cost
+    fields_stacked = torch.stack(fields)
+    # (default arguments bind the tensors now: the graphs hold their addresses, and
+    # a later rebinding of a name must not free what a graph writes)
+    xs = x.expand(copies, k).contiguous()
+    batch_out = torch.empty(copies, o, device=device, dtype=torch.bfloat16)
+    graphs["w3_batched"] = (capture(lambda xs=xs, w=stacked["planes"], y=batch_out: batched_call(
+        lib, xs, w, stacked, y, o, k, _lib.PAYLOAD_PLANAR, device), stream), copies)
+    graphs["fields_batched"] = (capture(lambda xs=xs, w=fields_stacked, y=batch_out: batched_call(
+        lib, xs, w, stacked, y, o, k, _lib.PAYLOAD_FIELDS, device), stream), copies)
 
     # same-run bf16 arm: dense bf16 weights (5.3x the bytes), same rotation rule
     bf16_bytes = 2 * o * k + 2 * k + 2 * o
@@ -226,6 +270,10 @@ def bench_shape(o, k, device, steps, warmup, stream, min_bytes=320e6, min_copies
         raise RuntimeError("field-layout GEMV disagrees with the planar GEMV")
     if not torch.equal(pout, gathered):
         raise RuntimeError("permuted GEMV differs from the identity GEMV on the gathered activations")
+    batched_call(lib, xs, stacked["planes"], stacked, batch_out, o, k, _lib.PAYLOAD_PLANAR, device)
+    torch.cuda.synchronize()
+    if not torch.equal(batch_out[-1:], out):
+        raise RuntimeError("strided-batch GEMV differs from the single launch")
     small_m = {}
     for m in (2, 4, 8):
         m_us = t[f"M={m}"]["us"]
@@ -235,7 +283,14 @@ def bench_shape(o, k, device, steps, warmup, stream, min_bytes=320e6, min_copies
                              "algorithmic_bytes": m_bytes, "vs_M=1": round(m_us / t["w3"]["us"], 3)}
     w3_us, fields_us, bf16_us, perm_us = t["w3"]["us"], t["fields"]["us"], t["bf16"]["us"], t["w3_perm"]["us"]
     restore_us, restore_perm_us = t["restore"]["us"], t["restore_permuted"]["us"]
-    del graphs, shuffled, weights, payloads, gemvs, permuted, fields
+    steady = {}
+    for name, arm in (("planar", "w3_batched"), ("fields", "fields_batched")):
+        us = t[arm]["us"]
+        steady[name] = {"us_per_gemv": round(us, 3), "GBps": round(nbytes / us / 1e3, 1),
+                        "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBPS, 4)}
+    steady["note"] = (f"one fx_w3_gemv_strided_batched launch over the {copies} payloads (bit-identical "
+                      "outputs): the kernel's rate without the per-launch cost")
+    del graphs, shuffled, weights, payloads, gemvs, permuted, fields, fields_stacked, stacked, batch_out
     torch.cuda.empty_cache()
     return {
         "O": o, "K": k, "copies": copies, "algorithmic_bytes": nbytes,
@@ -248,6 +303,7 @@ def bench_shape(o, k, device, steps, warmup, stream, min_bytes=320e6, min_copies
         "fields_us": round(fields_us, 3), "fields_GBps": round(nbytes / fields_us / 1e3, 1),
         "fields_frac_hbm": round(nbytes / fields_us / 1e3 / HBM_PEAK_GBPS, 4),
         "small_m": small_m,
+        "steady_state": steady,
         "restore_us": round(restore_us, 3), "restore_GBps": round(restore_bytes / restore_us / 1e3, 1),
         "restore_permuted_us": round(restore_perm_us, 3),
         "restore_permuted_GBps": round((restore_bytes + 2 * k) / restore_perm_us / 1e3, 1),
@@ -1366,6 +1422,20 @@ def main():
             "algorithmic_bytes": dominant["algorithmic_bytes"],
             "kernel": f"w3_mfma_kernel on the field layout (fx_w3_gemv_fields) at gate/up "
                       f"{dominant['O']}x{dominant['K']}, M=1, same payloads repacked once",
+        }
+    if dominant.get("steady_state"):
+        st = dominant["steady_state"]
+        result["roofline_steady_state"] = {
+            "bound": "hbm", "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+            "planar": {"achieved": st["planar"]["GBps"], "frac": st["planar"]["frac_hbm"]},
+            "field_layout": {"achieved": st["fields"]["GBps"], "frac": st["fields"]["frac_hbm"]},
+            "algorithmic_bytes_per_gemv": dominant["algorithmic_bytes"],
+            "kernel": f"w3_mfma_kernel at gate/up {dominant['O']}x{dominant['K']}, M=1, one strided-batch launch "
+                      f"over {dominant['copies']} payloads (the same payloads as roofline): the kernel without the "
+                      "per-launch cost",
+            "per_shape_frac": {name: {"planar": sh["steady_state"]["planar"]["frac_hbm"],
+                                      "fields": sh["steady_state"]["fields"]["frac_hbm"]}
+                               for name, sh in shapes.items() if sh.get("steady_state")},
         }
     if not args.no_fused_ops:
         result["config"]["fused_ops"] = fused_ops_bench(device, max(args.steps, 10), args.warmup, stream)

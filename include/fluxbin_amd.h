@@ -159,6 +159,20 @@ int fx_w3_gemv_rmsnormed(const void *h, int x_dtype, const uint8_t *planes, cons
                          int scale_dtype, const uint8_t *zeros, const float *tile_sumsq, int n_tiles,
                          const void *norm_weight, float eps, const int16_t *out_index, void *out, int O, int K,
                          int swiglu, int payload_format, void *stream);
+/* A strided batch of one-row structural GEMVs in one launch: no reference
+ * counterpart (the reference runs one PackedW3Linear call per payload).  Payload
+ * p (0 <= p < batch) reads x + p * x_stride, planes + p * planes_stride (bytes),
+ * scales + p * scales_stride, zeros + p * zeros_stride (elements; zeros NULL =
+ * every zero-point 4) and writes out + p * out_stride: out_p [1, O] = x_p [1, K] @
+ * W_p.T, each bit-identical to the same payload's single call of the same format
+ * (fx_w3_gemv's one-split plan, or fx_w3_gemv_fields).  Identity column order; with
+ * batch > 1, O / 16 a multiple of 8 and each stride at least one payload / row.
+ * For the same-shape Linears of many layers, and to measure the kernel without
+ * the per-launch cost. */
+int fx_w3_gemv_strided_batched(const void *x, int x_dtype, long long x_stride, const uint8_t *planes,
+                               long long planes_stride, const void *scales, int scale_dtype,
+                               long long scales_stride, const uint8_t *zeros, long long zeros_stride, void *out,
+                               long long out_stride, int batch, int O, int K, int payload_format, void *stream);
 /* The field layout: no reference counterpart; a bind-time repack of the
  * reference's planar payload (gptq_deployment.py:199-244 layout, same sorted
  * column order, same [G, 3, O, 16] byte shape, three bits per code) whose

@@ -15,7 +15,7 @@ from pathlib import Path
 import torch
 
 LIBRARY_PATH = Path(__file__).resolve().parent / "libfluxbin_amd.so"
-ABI_VERSION = 15
+ABI_VERSION = 16
 PAYLOAD_PLANAR, PAYLOAD_FIELDS = 0, 1  # FX_W3_PLANAR / FX_W3_FIELDS
 
 FX_F32, FX_F16, FX_BF16 = 0, 1, 2
@@ -42,6 +42,8 @@ SIGNATURES: dict[str, tuple] = {
     "fx_w3_gemv_swiglu": (_i, [_p, _i, _p, _p, _i, _p, _p, _p, _p, _i, _i, _i, _p]),
     "fx_w3_gemv_residual": (_i, [_p, _i, _p, _p, _i, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _p]),
     "fx_w3_gemv_rmsnormed": (_i, [_p, _i, _p, _p, _i, _p, _p, _i, _p, ctypes.c_float, _p, _p, _i, _i, _i, _i, _p]),
+    "fx_w3_gemv_strided_batched": (_i, [_p, _i, ctypes.c_longlong, _p, ctypes.c_longlong, _p, _i, ctypes.c_longlong,
+                                        _p, ctypes.c_longlong, _p, ctypes.c_longlong, _i, _i, _i, _i, _p]),
     "fx_w3_planes_to_fields": (_i, [_p, _p, _i, _i, _p]),
     "fx_w3_gemv_fields": (_i, [_p, _i, _p, _p, _i, _p, _p, _i, _i, _p]),
     "fx_w3_gemv_config_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _i, _i]),

@@ -288,6 +288,7 @@ int run_mfma(const void* x, int x_dtype, const uint8_t* planes, const void* scal
     a.res = fx::ResidualArgs{};
     a.res.ep_index = out_index;
     a.x_lds = perm && fx::x_lds_fits(mb, K, p.nw);
+    a.batch = fx::StridedArgs{};
     const dim3 grid(p.row_blocks, p.splits);
     if (!fx::dispatch_mfma(x_dtype, p.tiles, p.nw, p.pd, mb, scale_dtype, a, grid, s))
       return fail(FX_EINVAL, "no MFMA kernel for waves %d prefetch %d tiles %d rows %d", p.nw,
@@ -562,7 +563,7 @@ bool two_base_config(int O, int G, int waves, int prefetch, int groups_per_split
 
 extern "C" {
 
-int fx_abi_version(void) { return 15; }
+int fx_abi_version(void) { return 16; }
 
 const char* fx_last_error(void) { return g_error; }
 
@@ -827,6 +828,52 @@ int fx_w3_gemv_rmsnormed(const void* h, int x_dtype, const uint8_t* planes, cons
   if (!fx::dispatch_mfma_normin(p.nw, x_dtype, scale_dtype, a, dim3(p.row_blocks, 1), static_cast<hipStream_t>(stream)))
     return fail(FX_EINVAL, "no normalising MFMA kernel for waves %d", p.nw);
   return check_launch("w3_mfma_kernel (normalising prologue)");
+}
+
+int fx_w3_gemv_strided_batched(const void* x, int x_dtype, long long x_stride, const uint8_t* planes,
+                               long long planes_stride, const void* scales, int scale_dtype, long long scales_stride,
+                               const uint8_t* zeros, long long zeros_stride, void* out, long long out_stride,
+                               int batch, int O, int K, int payload_format, void* stream) {
+  int rc = validate_payload(x, x_dtype, planes, scales, scale_dtype, 1, O, K, FX_ARITH_STRUCTURAL);
+  if (rc) return rc;
+  if ((rc = check_format(payload_format))) return rc;
+  if (!out) return fail(FX_EINVAL, "out must be non-null");
+  if (batch < 1 || batch > 65535) return fail(FX_EINVAL, "batch must be in [1, 65535], got %d", batch);
+  const int G = K / 128;
+  const long long planes_bytes = 3LL * G * O * 16;
+  if (batch > 1 && (planes_stride < planes_bytes || scales_stride < 1LL * G * O || (zeros && zeros_stride < 1LL * G * O) ||
+                    x_stride < K || out_stride < O))
+    return fail(FX_EINVAL, "strides must cover one payload, activation row and output row each");
+  if (planes_stride % 16 || x_stride % 8)
+    return fail(FX_EINVAL, "planes stride must be a multiple of 16 bytes and x stride of 8 elements");
+  MfmaPlan p = single_split_plan(O, G);
+  if (payload_format == FX_W3_FIELDS) {
+    const int tiles = fx::fields_row_tiles(false, O);
+    if (tiles != p.tiles) p = make_mfma_plan(O, G, p.nw, 1, G, tiles);
+  }
+  if (batch > 1 && p.row_blocks % 8)
+    return fail(FX_EINVAL, "a batch needs O / 16 to be a multiple of 8 (XCD-aligned row blocks), got O = %d", O);
+  MfmaArgs a{};
+  a.x = static_cast<const uint16_t*>(x);
+  a.planes = planes;
+  a.scales = static_cast<const uint16_t*>(scales);
+  a.zeros = zeros;
+  a.out = static_cast<uint16_t*>(out);
+  a.O = O;
+  a.G = G;
+  a.gps = p.gps;
+  a.row_blocks = p.row_blocks;
+  if (batch > 1) a.batch = fx::StridedArgs{x_stride, planes_stride, scales_stride, zeros_stride, out_stride};
+  const dim3 grid(p.row_blocks, batch);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (payload_format == FX_W3_FIELDS) {
+    if (!fx::dispatch_mfma_fields(p.nw, false, x_dtype, scale_dtype, a, grid, s))
+      return fail(FX_EINVAL, "no field-layout MFMA kernel for waves %d", p.nw);
+    return check_launch("w3_mfma_kernel (field layout, strided batch)");
+  }
+  if (!fx::dispatch_mfma(x_dtype, 1, p.nw, 1, 1, scale_dtype, a, grid, s))
+    return fail(FX_EINVAL, "no MFMA kernel for waves %d", p.nw);
+  return check_launch("w3_mfma_kernel (strided batch)");
 }
 
 int fx_w3_planes_to_fields(const uint8_t* planes, uint8_t* fields, int O, int K, void* stream) {

@@ -63,11 +63,11 @@ void launch_fields(const MfmaArgs& a, dim3 grid, hipStream_t s) {
     constexpr int RT = NORMIN ? 2 : 1;  // fields_row_tiles
     hipLaunchKernelGGL((w3_mfma_kernel<NW, 1, 1, RT, PERM, XDT, SDT, NORMIN, 1, true>), grid, dim3(NW * 64),
                        PERM ? x_lds_bytes(a, 1) : 0, s, a.x, a.perm, a.planes, a.scales, a.zeros, a.partial, a.out,
-                       a.O, a.G, a.gps, a.row_blocks, a.swiglu, a.res, PERM ? a.x_lds : 0);
+                       a.O, a.G, a.gps, a.row_blocks, a.swiglu, a.res, PERM ? a.x_lds : 0, a.batch);
   } else {
     hipLaunchKernelGGL((w3_mfma_kernel<NW, 1, 1, 1, PERM, XDT, SDT, NORMIN, 2, true>), grid, dim3(NW * 64),
                        PERM ? x_lds_bytes(a, 1) : 0, s, a.x, a.perm, a.planes, a.scales, a.zeros, a.partial, a.out,
-                       a.O, a.G, a.gps, a.row_blocks, a.swiglu, a.res, PERM ? a.x_lds : 0);
+                       a.O, a.G, a.gps, a.row_blocks, a.swiglu, a.res, PERM ? a.x_lds : 0, a.batch);
   }
 }
 

@@ -188,7 +188,7 @@ __device__ __forceinline__ void w3_mfma_body(
     const uint8_t* __restrict__ planes, const uint16_t* __restrict__ scales,
     const uint8_t* __restrict__ zeros, float* __restrict__ partial,
     uint16_t* out, int O, int G, int gps, int row_blocks, int swiglu, const ResidualArgs& ra, int x_lds,
-    u32x4_t* x_stage) {
+    u32x4_t* x_stage, int split) {
   auto& bstage = sh.bstage;
   auto& bzero = sh.bzero;
   auto& gsum = sh.gsum;
@@ -196,7 +196,6 @@ __device__ __forceinline__ void w3_mfma_body(
   auto& red = sh.red;
   const int t = threadIdx.x, lane = t & 63, wave = wave_index();
   const int K = G * 128;
-  const int split = blockIdx.y;
   const int row0 = xcd_local_index8(blockIdx.x, row_blocks) * (16 * RT);
   const int g0 = split * gps;
   const int g1 = min(G, g0 + gps);
@@ -650,12 +649,27 @@ void w3_mfma_kernel(
     const uint16_t* __restrict__ x, const int16_t* __restrict__ perm,
     const uint8_t* __restrict__ planes, const uint16_t* __restrict__ scales,
     const uint8_t* __restrict__ zeros, float* __restrict__ partial,
-    uint16_t* out, int O, int G, int gps, int row_blocks, int swiglu, ResidualArgs ra, int x_lds) {
+    uint16_t* out, int O, int G, int gps, int row_blocks, int swiglu, ResidualArgs ra, int x_lds,
+    StridedArgs sb) {
   // one scalar-load round for every argument (otherwise the pointer loads sink
   // below the first branch and add a second round trip before the first load)
   asm volatile("" ::"s"(x), "s"(perm), "s"(planes), "s"(scales), "s"(zeros), "s"(partial), "s"(out),
                "s"(O), "s"(G), "s"(gps), "s"(row_blocks), "s"(swiglu), "s"(ra.ep_residual), "s"(ra.ep_partial),
-               "s"(ra.ep_index), "s"(ra.ep_sorted), "s"(x_lds));
+               "s"(ra.ep_index), "s"(ra.ep_sorted), "s"(x_lds), "s"(sb.x), "s"(sb.planes), "s"(sb.scales),
+               "s"(sb.zeros), "s"(sb.out));
+  // a strided batch: grid.y walks the payloads (one K split each); row blocks
+  // per payload are a multiple of 8 at the batched shapes, so the XCD mapping of
+  // blockIdx.x holds within every payload
+  int split = blockIdx.y;
+  if (sb.planes) {
+    const long long p = blockIdx.y;
+    x += p * sb.x;
+    planes += p * sb.planes;
+    scales += p * sb.scales;
+    if (zeros) zeros += p * sb.zeros;
+    out += p * sb.out;
+    split = 0;
+  }
   if constexpr (NORMIN)
     asm volatile("" ::"s"(ra.pro_partial), "s"(ra.pro_n), "s"(ra.pro_weight), "s"(ra.pro_eps));
   static_assert(!FIELDS || (MB == 1 && PD == 1), "field layout: one activation row, one batch in flight");
@@ -665,11 +679,11 @@ void w3_mfma_kernel(
   if (VSEL == 1 || (VSEL == 0 && (O & 3) == 0))
     w3_mfma_body<NW, PD, MB, RT, PERM, XDT, SDT, NORMIN, VSEL != 2, FIELDS>(sh, x, perm, planes, scales, zeros,
                                                                            partial, out, O, G, gps, row_blocks,
-                                                                           swiglu, ra, x_lds, x_stage);
+                                                                           swiglu, ra, x_lds, x_stage, split);
   else
     w3_mfma_body<NW, PD, MB, RT, PERM, XDT, SDT, NORMIN, VSEL == 1, FIELDS>(sh, x, perm, planes, scales, zeros,
                                                                            partial, out, O, G, gps, row_blocks,
-                                                                           swiglu, ra, x_lds, x_stage);
+                                                                           swiglu, ra, x_lds, x_stage, split);
 }
 
 }  // namespace fx

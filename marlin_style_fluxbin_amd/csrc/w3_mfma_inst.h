@@ -9,7 +9,7 @@ template <int NW, int PD, int MB, int RT, bool PERM, int XDT, int SDT>
 void launch_mfma(const MfmaArgs& a, dim3 grid, hipStream_t s) {
   hipLaunchKernelGGL((w3_mfma_kernel<NW, PD, MB, RT, PERM, XDT, SDT>), grid, dim3(NW * 64),
                      PERM ? x_lds_bytes(a, MB) : 0, s, a.x, a.perm, a.planes, a.scales, a.zeros, a.partial,
-                     a.out, a.O, a.G, a.gps, a.row_blocks, a.swiglu, a.res, PERM ? a.x_lds : 0);
+                     a.out, a.O, a.G, a.gps, a.row_blocks, a.swiglu, a.res, PERM ? a.x_lds : 0, a.batch);
 }
 
 template <int NW, int PD, int MB, int RT, bool PERM, int XDT>

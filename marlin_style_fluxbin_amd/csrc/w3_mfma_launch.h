@@ -30,6 +30,13 @@ struct ResidualArgs {
 };
 constexpr int kMaxNormPartialsPerLane = 4;  // prologue: K <= 4 * 64 * 16
 
+// Strided batch of one-row GEMVs in one launch (grid.y = payloads, one K split):
+// payload p reads x + p * x, planes + p * planes, ... (element strides) and writes
+// out + p * out.  All zero: a single GEMV (grid.y counts K splits).
+struct StridedArgs {
+  long long x, planes, scales, zeros, out;
+};
+
 struct MfmaArgs {
   const uint16_t* x;     // [mb, K] activations of this launch
   const int16_t* perm;   // null: identity
@@ -43,6 +50,7 @@ struct MfmaArgs {
   int swiglu;      // 1: rows interleave (gate, up); out gets SiLU(gate) * up (mb 1, one split)
   ResidualArgs res;
   int x_lds;       // permuted kernels: 1 = gather from an LDS copy of x (x_lds_fits)
+  StridedArgs batch;
 };
 
 // The permuted kernels gather x[perm] from an LDS copy of x when the activation

@@ -12,11 +12,11 @@ void launch_mfma_normin(const MfmaArgs& a, dim3 grid, hipStream_t s) {
   if (a.O % 4 == 0)
     hipLaunchKernelGGL((w3_mfma_kernel<NW, 1, 1, 1, false, XDT, SDT, true, 1>), grid, dim3(NW * 64), 0, s, a.x,
                        a.perm, a.planes, a.scales, a.zeros, a.partial, a.out, a.O, a.G, a.gps, a.row_blocks,
-                       a.swiglu, a.res, 0);
+                       a.swiglu, a.res, 0, a.batch);
   else
     hipLaunchKernelGGL((w3_mfma_kernel<NW, 1, 1, 1, false, XDT, SDT, true, 2>), grid, dim3(NW * 64), 0, s, a.x,
                        a.perm, a.planes, a.scales, a.zeros, a.partial, a.out, a.O, a.G, a.gps, a.row_blocks,
-                       a.swiglu, a.res, 0);
+                       a.swiglu, a.res, 0, a.batch);
 }
 
 bool dispatch_mfma_normin(int nw, int xdt, int sdt, const MfmaArgs& a, dim3 grid, hipStream_t s) {

@@ -57,6 +57,8 @@ DEFAULTS = {
     "fx_w3_gemv_residual": W3,
     "fx_w3_gemv_rmsnormed": dict(W3, h=D, n_tiles=16, norm_weight=D, eps=1e-6, swiglu=0),
     "fx_w3_planes_to_fields": dict(planes=D, fields=D + 4096, O=64, K=256, stream=None),
+    "fx_w3_gemv_strided_batched": dict(W3, O=128, x_stride=256, planes_stride=3 * 2 * 128 * 16, scales_stride=256,
+                                       zeros_stride=256, out_stride=128, batch=4),
     "fx_w3_gemv_fields": dict(W3, fields=D),
     "fx_w3_gemv_config": dict(W3, waves=8, prefetch=1, tiles=1),
     "fx_w3_restore": dict(planes=D, scales=D, scale_dtype=2, zeros=None, perm=None, weight=D, weight_dtype=2,
@@ -161,6 +163,15 @@ CASES = [
     ("fx_w3_gemv_rmsnormed", dict(tile_sumsq=None), "must be non-null"),
     ("fx_w3_gemv_rmsnormed", dict(swiglu=1, O=63), "even row count"),
     ("fx_w3_gemv_rmsnormed", dict(K=131072, n_tiles=8192), "too large for the normalising prologue"),
+    # strided batch
+    ("fx_w3_gemv_strided_batched", dict(batch=0), "batch must be in [1, 65535]"),
+    ("fx_w3_gemv_strided_batched", dict(planes_stride=1024), "strides must cover"),
+    ("fx_w3_gemv_strided_batched", dict(out_stride=64), "strides must cover"),
+    ("fx_w3_gemv_strided_batched", dict(planes_stride=3 * 2 * 128 * 16 + 8), "multiple of 16 bytes"),
+    ("fx_w3_gemv_strided_batched", dict(O=64, scales_stride=128, zeros_stride=128, out_stride=64,
+                                        planes_stride=3 * 2 * 64 * 16), "multiple of 8"),
+    ("fx_w3_gemv_strided_batched", dict(payload_format=5), "payload_format"),
+    ("fx_w3_gemv_strided_batched", dict(out=None), "out must be non-null"),
     # field layout
     ("fx_w3_planes_to_fields", dict(fields=D), "cannot run in place"),
     ("fx_w3_planes_to_fields", dict(O=0), "O must be positive and K a multiple of 128"),

@@ -123,3 +123,50 @@ def test_field_layout_argument_checks(gpu):
     rc = lib.fx_w3_gemv_residual(x.data_ptr(), 2, t.data_ptr(), sc.data_ptr(), 1, None, None, out.data_ptr(),
                                  out.data_ptr(), part.data_ptr(), None, None, 16, 128, 7, None)
     assert rc == 1 and "payload_format" in lib.fx_last_error().decode()
+
+
+@pytest.mark.parametrize("fmt", ["planar", "fields"])
+@pytest.mark.parametrize("o,k,batch", [(4096, 4096, 3), (1024, 4096, 5), (12288, 4096, 2), (4096, 12288, 2),
+                                        (128, 256, 1)])
+def test_strided_batch_equals_single_calls(gpu, fmt, o, k, batch):
+    """fx_w3_gemv_strided_batched: payload p of one launch is bit-identical to the
+    same payload's single call of the same format (fx_w3_gemv / fx_w3_gemv_fields)."""
+    from marlin_style_fluxbin_amd.w3_lut_deployment import W3Gemv
+
+    print(f"strided batch {fmt} {o}x{k} x{batch}", flush=True)
+    lib = _lib.library()
+    layouts = []
+    for p in range(batch):
+        codes, scales, zeros, _ = config_codes(o, k, seed=o + k + p, zeros=p % 2 == 0 or batch == 1,
+                                               scale_dtype=torch.float16)
+        if zeros is None:
+            zeros = torch.full((k // 128, o), 4, dtype=torch.uint8)
+        layouts.append({n: t.to(gpu) for n, t in layout_from_codes(codes, scales, zeros, None).items()})
+    planes = torch.stack([l["planes"] for l in layouts]).contiguous()
+    if fmt == "fields":
+        fields = torch.empty_like(planes)
+        for p in range(batch):
+            _lib.check(lib.fx_w3_planes_to_fields(planes[p].data_ptr(), fields[p].data_ptr(), o, k,
+                                                  _lib.stream_handle(gpu)), "planes_to_fields")
+        weights = fields
+    else:
+        weights = planes
+    scales = torch.stack([l["scales"] for l in layouts]).contiguous()
+    zeros = torch.stack([l["zeros"] for l in layouts]).contiguous()
+    x = torch.randn(batch, k, generator=torch.Generator().manual_seed(k)).to(torch.bfloat16).to(gpu)
+    got = torch.full((batch, o), float("nan"), dtype=torch.bfloat16, device=gpu)
+    _lib.check(lib.fx_w3_gemv_strided_batched(
+        x.data_ptr(), _lib.FX_BF16, k, weights.data_ptr(), weights[0].numel(), scales.data_ptr(), _lib.FX_F16,
+        scales[0].numel(), zeros.data_ptr(), zeros[0].numel(), got.data_ptr(), o, batch, o, k,
+        _lib.PAYLOAD_PLANAR if fmt == "planar" else _lib.PAYLOAD_FIELDS, _lib.stream_handle(gpu)),
+        "strided batch")
+    for p in range(batch):
+        want = torch.full((1, o), float("nan"), dtype=torch.bfloat16, device=gpu)
+        if fmt == "planar":
+            W3Gemv(layouts[p], perm_identity=True)(x[p:p + 1], want)
+        else:
+            _lib.check(lib.fx_w3_gemv_fields(x[p:p + 1].data_ptr(), _lib.FX_BF16, weights[p].data_ptr(),
+                                             scales[p].data_ptr(), _lib.FX_F16, zeros[p].data_ptr(), want.data_ptr(),
+                                             o, k, _lib.stream_handle(gpu)), "gemv_fields")
+        torch.cuda.synchronize()
+        assert torch.equal(got[p:p + 1], want), p
