@@ -201,6 +201,22 @@ def bench_shape(o, k, device, steps, warmup, stream, min_bytes=320e6, min_copies
     graphs["w3"] = (capture(over([lambda g=g: g(x, out) for g in gemvs]), stream), copies)
     pout = torch.empty_like(out)
     graphs["w3_perm"] = (capture(over([lambda g=g: g(x, pout) for g in permuted]), stream), copies)
+    # decoded_bf16 (the fast_corrected route: bf16 scales, zero-points 3 / 4): the
+    # MFMA kernel with the +-3 correction chain, and the reference's table kernel
+    # (w3_lut_m1_out, one group per split) on the same payloads
+    from marlin_style_fluxbin_amd.w3_lut_deployment import load_w3_lut_extension
+
+    scales16 = stacked["scales"].to(torch.bfloat16)
+    decoded_views = [dict(p, scales=scales16[i]) for i, p in enumerate(payloads)]
+    decoded = [W3Gemv(p, arithmetic="decoded_bf16", perm_identity=True) for p in decoded_views]
+    dout = torch.empty_like(out)
+    graphs["w3_decoded"] = (capture(over([lambda g=g: g(x, dout) for g in decoded]), stream), copies)
+    table = load_w3_lut_extension(1024)
+    table_ws = torch.empty(k // 128, o, dtype=torch.float32, device=device)
+    tout = torch.empty_like(out)
+    graphs["table_decoded"] = (capture(over([lambda p=p: table.m1_out(
+        x, p["planes"], p["scales"], None, table_ws, tout, 1, True, zeros=p["zeros"]) for p in decoded_views]), stream),
+        copies)
     # config 1's small-M variants: M activation rows against the same payloads
     xm = {m: torch.randn(m, k, device=device, generator=gen).to(torch.bfloat16) for m in (2, 4, 8)}
     om = {m: torch.empty(m, o, device=device, dtype=torch.bfloat16) for m in (2, 4, 8)}
@@ -270,6 +286,12 @@ def bench_shape(o, k, device, steps, warmup, stream, min_bytes=320e6, min_copies
         raise RuntimeError("field-layout GEMV disagrees with the planar GEMV")
     if not torch.equal(pout, gathered):
         raise RuntimeError("permuted GEMV differs from the identity GEMV on the gathered activations")
+    decoded[-1](x, dout)
+    table.m1_out(x, decoded_views[-1]["planes"], decoded_views[-1]["scales"], None, table_ws, tout, 1, True,
+                 zeros=decoded_views[-1]["zeros"])
+    torch.cuda.synchronize()
+    if not torch.allclose(dout.float(), tout.float(), rtol=2 ** -7, atol=1e-3 * float(tout.float().abs().max())):
+        raise RuntimeError("decoded_bf16 MFMA GEMV disagrees with the table kernel")
     batched_call(lib, xs, stacked["planes"], stacked, batch_out, o, k, _lib.PAYLOAD_PLANAR, device)
     torch.cuda.synchronize()
     if not torch.equal(batch_out[-1:], out):
@@ -282,6 +304,7 @@ def bench_shape(o, k, device, steps, warmup, stream, min_bytes=320e6, min_copies
                              "frac_hbm": round(m_bytes / m_us / 1e3 / HBM_PEAK_GBPS, 4),
                              "algorithmic_bytes": m_bytes, "vs_M=1": round(m_us / t["w3"]["us"], 3)}
     w3_us, fields_us, bf16_us, perm_us = t["w3"]["us"], t["fields"]["us"], t["bf16"]["us"], t["w3_perm"]["us"]
+    decoded_us, table_us = t["w3_decoded"]["us"], t["table_decoded"]["us"]
     restore_us, restore_perm_us = t["restore"]["us"], t["restore_permuted"]["us"]
     steady = {}
     for name, arm in (("planar", "w3_batched"), ("fields", "fields_batched")):
@@ -290,7 +313,8 @@ def bench_shape(o, k, device, steps, warmup, stream, min_bytes=320e6, min_copies
                         "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBPS, 4)}
     steady["note"] = (f"one fx_w3_gemv_strided_batched launch over the {copies} payloads (bit-identical "
                       "outputs): the kernel's rate without the per-launch cost")
-    del graphs, shuffled, weights, payloads, gemvs, permuted, fields, fields_stacked, stacked, batch_out
+    del graphs, shuffled, weights, payloads, gemvs, permuted, fields, fields_stacked, stacked, batch_out, decoded
+    del decoded_views, scales16, table_ws
     torch.cuda.empty_cache()
     return {
         "O": o, "K": k, "copies": copies, "algorithmic_bytes": nbytes,
@@ -298,6 +322,8 @@ def bench_shape(o, k, device, steps, warmup, stream, min_bytes=320e6, min_copies
         "w3_frac_hbm": round(nbytes / w3_us / 1e3 / HBM_PEAK_GBPS, 4),
         "w3_perm_us": round(perm_us, 3), "w3_perm_GBps": round(perm_bytes / perm_us / 1e3, 1),
         "w3_perm_frac_hbm": round(perm_bytes / perm_us / 1e3 / HBM_PEAK_GBPS, 4),
+        "decoded_bf16_us": round(decoded_us, 3), "decoded_bf16_vs_structural": round(decoded_us / w3_us, 3),
+        "table_decoded_bf16_us": round(table_us, 3),
         "bf16_us": round(bf16_us, 3), "bf16_GBps": round(bf16_bytes / bf16_us / 1e3, 1),
         "w3_speedup_vs_bf16": round(bf16_us / w3_us, 3),
         "fields_us": round(fields_us, 3), "fields_GBps": round(nbytes / fields_us / 1e3, 1),

@@ -228,7 +228,7 @@ MfmaPlan make_mfma_plan(int O, int G, int nw, int pd, int gps, int tiles) {
 // wide gate/up shape, 4 waves; with 16+ batches per row block, two K splits and
 // 8 waves), measured at Qwen3-8B shapes (graph-timed, rotating payloads): gate/up
 // 13.95 -> 13.09 us, down 15.11 -> 12.50 us; q/o keeps the one-row plan (7.0 us).
-MfmaPlan default_mfma_plan(int O, int G, int mb = 1) {
+MfmaPlan default_mfma_plan(int O, int G, int mb = 1, int waves_per_simd = 6) {
   if (mb == 8) {
     const int batches = (G + 3) / 4;
     const int cus = device_cu_count();
@@ -243,7 +243,7 @@ MfmaPlan default_mfma_plan(int O, int G, int mb = 1) {
   if (row_blocks < 32) splits = (64 + row_blocks - 1) / row_blocks;
   if (splits > batches) splits = batches;
   const int per_split = (batches + splits - 1) / splits;  // batches per workgroup
-  const long resident_waves = 24L * device_cu_count();
+  const long resident_waves = 4L * waves_per_simd * device_cu_count();
   const int nw = per_split >= 8 && long(row_blocks) * splits * 8 <= resident_waves ? 8 : 4;
   return make_mfma_plan(O, G, nw, 1, per_split * 4, tiles);
 }
@@ -258,7 +258,7 @@ size_t mfma_workspace(int M, int O, const MfmaPlan& p) {
 int run_mfma(const void* x, int x_dtype, const uint8_t* planes, const void* scales,
              int scale_dtype, const uint8_t* zeros, const int16_t* perm, void* workspace,
              size_t workspace_bytes, void* out, int M, int O, int K, const MfmaPlan& p,
-             hipStream_t s, int swiglu = 0, const int16_t* out_index = nullptr) {
+             hipStream_t s, int swiglu = 0, const int16_t* out_index = nullptr, bool corrected = false) {
   const int G = K / 128;
   const size_t need = mfma_workspace(M, O, p);
   if (need > 0) {
@@ -290,9 +290,14 @@ int run_mfma(const void* x, int x_dtype, const uint8_t* planes, const void* scal
     a.x_lds = perm && fx::x_lds_fits(mb, K, p.nw);
     a.batch = fx::StridedArgs{};
     const dim3 grid(p.row_blocks, p.splits);
-    if (!fx::dispatch_mfma(x_dtype, p.tiles, p.nw, p.pd, mb, scale_dtype, a, grid, s))
+    if (corrected) {
+      if (mb != 1 || p.tiles != 1 || p.pd != 1 || scale_dtype != FX_BF16 ||
+          !fx::dispatch_mfma_corr(p.nw, x_dtype, a, grid, s))
+        return fail(FX_EINVAL, "no decoded_bf16 MFMA kernel for waves %d tiles %d rows %d", p.nw, p.tiles, mb);
+    } else if (!fx::dispatch_mfma(x_dtype, p.tiles, p.nw, p.pd, mb, scale_dtype, a, grid, s)) {
       return fail(FX_EINVAL, "no MFMA kernel for waves %d prefetch %d tiles %d rows %d", p.nw,
                   p.pd, p.tiles, mb);
+    }
     int rc = check_launch("w3_mfma_kernel");
     if (rc) return rc;
     if (partial) {
@@ -618,12 +623,16 @@ int fx_w3_m1_out(const void* x, int x_dtype, const uint8_t* planes, const void* 
   return launch_finish(workspace, out, x_dtype, tile.splits, M * O, s);
 }
 
+// The decoded_bf16 kernel holds ~90 VGPRs: five of its waves fit per SIMD.
+constexpr int kCorrWavesPerSimd = 5;
+
 size_t fx_w3_gemv_workspace_bytes(int M, int O, int K) {
   if (M < 1 || O < 1 || K < 128 || K % 128) return 0;
   const int G = K / 128;
   const size_t mfma = mfma_workspace(M, O, default_mfma_plan(O, G, mfma_chunk_for(M)));
+  const size_t corr = M == 1 ? mfma_workspace(1, O, default_mfma_plan(O, G, 1, kCorrWavesPerSimd)) : 0;
   const size_t lut = lut_route_workspace(M, O, K);
-  return mfma > lut ? mfma : lut;
+  return std::max({mfma, corr, lut});
 }
 
 int fx_w3_gemv(const void* x, int x_dtype, const uint8_t* planes, const void* scales,
@@ -634,6 +643,11 @@ int fx_w3_gemv(const void* x, int x_dtype, const uint8_t* planes, const void* sc
   if (rc) return rc;
   if (!out) return fail(FX_EINVAL, "out must be non-null");
   hipStream_t s = static_cast<hipStream_t>(stream);
+  // decoded_bf16: one activation row on the matrix cores (the +-3 correction as a
+  // second MFMA chain); more rows on the table kernel
+  if (arithmetic == FX_ARITH_DECODED_BF16 && M == 1)
+    return run_mfma(x, x_dtype, planes, scales, scale_dtype, zeros, perm, workspace, workspace_bytes, out, 1, O,
+                    K, default_mfma_plan(O, K / 128, 1, kCorrWavesPerSimd), s, 0, nullptr, true);
   if (arithmetic == FX_ARITH_DECODED_BF16)
     return run_lut_route(x, x_dtype, planes, scales, scale_dtype, zeros, perm, workspace,
                          workspace_bytes, out, M, O, K, arithmetic, s);

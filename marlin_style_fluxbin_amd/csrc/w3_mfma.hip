@@ -148,7 +148,26 @@ struct BatchLoads {
   unsigned z[RT];    // zero-points of rows erow..erow+3, one per byte
   unsigned se[RT][4], ze[RT][4];  // the same as single elements when O % 4 != 0
   u32x4_t wn;        // NORMIN: the RMSNorm weights of this lane's 8 columns
+  unsigned za[RT];   // CORR: the zero-point of this lane's A row (row r of each tile, group 4i + k-block)
 };
+
+// decoded_bf16 arithmetic (the reference's +-3 correction, csrc/w3_lut.cu:105-122):
+// each weight is bf16(s (q - z)), which differs from s (q - z) only where
+// |q - z| = 3, by sign(q - z) (bf16(3 s) - 3 s).  So y = sum_g s D_g - s z sum(x) +
+// e_g C_g with e_g = bf16(3 s) - 3 s and C_g = sum_k ([q - z = 3] - [q - z = -3]) x_k.
+// C comes from the same dequantizer and B operands: the planes are transformed
+// bitwise into g(q) = q - c(q) (z = 4: q = 7 -> 6, q = 1 -> 2; z = 3: q = 6 -> 5,
+// q = 0 -> 1; every other code unchanged), so C = D - sum_k g(q_k) x_k from a second
+// MFMA chain.  In plane bits (b0 = P0, b1 = P1, b2 = ~P2, e = P1 ^ P2 = ~(b1 ^ b2)):
+//   z = 4: g0 = b0 & ~e,  g1 = b1 | (b0 & ~b2)      z = 3: g0 = b0 | e,  g1 = b1 & (~b2 | b0)
+// and g2 = b2; zmask (all ones where z = 4) selects per lane.  Zero-points must be
+// 3 or 4 (the route's contract).
+__device__ __forceinline__ void corrected_planes(unsigned p0, unsigned p1, unsigned p2, unsigned zmask,
+                                                 unsigned& g0, unsigned& g1) {
+  const unsigned e = p1 ^ p2;
+  g0 = bitfield_insert(zmask, p0 & ~e, p0 | e);
+  g1 = bitfield_insert(zmask, p1 | (p0 & p2), p1 & (p2 | p0));
+}
 
 // The K reduction of a workgroup always runs in the order eight waves give it:
 // "virtual wave" k accumulates batches k, k + 8, k + 16, ... in turn, and the
@@ -182,7 +201,8 @@ struct MfmaShared {
 // aligned load each.  A separate instantiation (rather than a runtime branch)
 // keeps the load count per batch fixed, so the wait before staging covers only
 // the activations.
-template <int NW, int PD, int MB, int RT, bool PERM, int XDT, int SDT, bool NORMIN, bool VEC, bool FIELDS>
+template <int NW, int PD, int MB, int RT, bool PERM, int XDT, int SDT, bool NORMIN, bool VEC, bool FIELDS,
+          bool CORR>
 __device__ __forceinline__ void w3_mfma_body(
     MfmaShared<NW, MB, RT>& sh, const uint16_t* __restrict__ x, const int16_t* __restrict__ perm,
     const uint8_t* __restrict__ planes, const uint16_t* __restrict__ scales,
@@ -274,6 +294,12 @@ __device__ __forceinline__ void w3_mfma_body(
       for (int m = 0; m < MB; ++m) L.xv[m] = load_b128(rx, real ? (m * K + col) * 2 : kOutOfRange, 0);
     }
     if constexpr (NORMIN) L.wn = load_b128(rwn, real ? col * 2 : kOutOfRange, 0);
+    if constexpr (CORR) {  // the A row's zero-point (needed by the dequant, ahead of the planes)
+#pragma unroll
+      for (int tt = 0; tt < RT; ++tt)
+        L.za[tt] = __builtin_amdgcn_raw_buffer_load_b8(rz, real ? (gb + kb) * O + row0 + 16 * tt + r : kOutOfRange,
+                                                       0, 0);
+    }
     __builtin_amdgcn_sched_barrier(0);
     const int poff = live ? ((gb + kb) * 3 * O + row0 + r) * 16 : kOutOfRange;  // past the end -> zeros
 #pragma unroll
@@ -416,19 +442,33 @@ __device__ __forceinline__ void w3_mfma_body(
     }
     __builtin_amdgcn_wave_barrier();
 
-    f32x4_t d[RT][NH];
+    f32x4_t d[RT][NH], dg[CORR ? RT : 1][CORR ? NH : 1];
 #pragma unroll
     for (int tt = 0; tt < RT; ++tt)
 #pragma unroll
-      for (int h = 0; h < NH; ++h) d[tt][h] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      for (int h = 0; h < NH; ++h) {
+        d[tt][h] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        if constexpr (CORR) dg[tt][h] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      }
+    unsigned zmask[RT];
+    if constexpr (CORR) {
+#pragma unroll
+      for (int tt = 0; tt < RT; ++tt)
+        zmask[tt] = ((L.za[tt] | zero_default) & 0xffu) == 4u ? 0xffffffffu : 0u;  // absent zero-points: 4
+    }
 #pragma unroll
     for (int word = 0; word < 4; ++word) {
-      u32x4_t a[RT][4];
+      u32x4_t a[RT][4], ag[CORR ? RT : 1][4];
 #pragma unroll
       for (int tt = 0; tt < RT; ++tt) {
         const u32x4_t* w = L.w[tt];
         if constexpr (FIELDS) dequant_fields(w[0][word], w[1][word], w[2][word], a[tt]);
         else dequant_word(w[0][word], w[1][word], w[2][word], a[tt]);
+        if constexpr (CORR) {
+          unsigned g0, g1;
+          corrected_planes(w[0][word], w[1][word], w[2][word], zmask[tt], g0, g1);
+          dequant_word(g0, g1, w[2][word], ag[tt]);
+        }
       }
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
@@ -443,6 +483,14 @@ __device__ __forceinline__ void w3_mfma_body(
             else
               d[tt][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
                   __builtin_bit_cast(f16x8_t, a[tt][s]), __builtin_bit_cast(f16x8_t, b), d[tt][h], 0, 0, 0);
+            if constexpr (CORR) {
+              if constexpr (XDT == kBF16)
+                dg[tt][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                    __builtin_bit_cast(bf16x8_t, ag[tt][s]), __builtin_bit_cast(bf16x8_t, b), dg[tt][h], 0, 0, 0);
+              else
+                dg[tt][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                    __builtin_bit_cast(f16x8_t, ag[tt][s]), __builtin_bit_cast(f16x8_t, b), dg[tt][h], 0, 0, 0);
+            }
           }
         }
       }
@@ -470,6 +518,12 @@ __device__ __forceinline__ void w3_mfma_body(
         const float zf = float((zw >> (8 * j)) & 0xffu);
 #pragma unroll
         for (int h = 0; h < NH; ++h) acc[tt][h][j] += se * (ldexpf(d[tt][h][j], fev[h]) - zf * sxv[h]);
+        if constexpr (CORR) {
+          // bf16(3 s) - 3 s: 3 s is exact in fp32 (s has 8 significant bits)
+          const float eps = round_to<kBF16>(3.f * se) - 3.f * se;
+#pragma unroll
+          for (int h = 0; h < NH; ++h) acc[tt][h][j] += eps * ldexpf(d[tt][h][j] - dg[tt][h][j], fev[h]);
+        }
       }
     }
     __builtin_amdgcn_wave_barrier();
@@ -642,9 +696,10 @@ __device__ __forceinline__ void w3_mfma_body(
 // flight per wave).  NORMIN takes no permutation: its caller hands it h and the
 // norm weights in the payload's sorted column order (a producer epilogue's
 // ep_index output, weights reordered once at bind time).
+// CORR: decoded_bf16 arithmetic (bf16 scales, zero-points 3 or 4; planar layout).
 template <int NW, int PD, int MB, int RT, bool PERM, int XDT, int SDT, bool NORMIN = false, int VSEL = 0,
-          bool FIELDS = false>
-__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(MB == 1 && RT == 1 && PD == 1 ? 6 : 1)))
+          bool FIELDS = false, bool CORR = false>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(MB == 1 && RT == 1 && PD == 1 && !CORR ? 6 : 1)))
 void w3_mfma_kernel(
     const uint16_t* __restrict__ x, const int16_t* __restrict__ perm,
     const uint8_t* __restrict__ planes, const uint16_t* __restrict__ scales,
@@ -674,14 +729,15 @@ void w3_mfma_kernel(
     asm volatile("" ::"s"(ra.pro_partial), "s"(ra.pro_n), "s"(ra.pro_weight), "s"(ra.pro_eps));
   static_assert(!FIELDS || (MB == 1 && PD == 1), "field layout: one activation row, one batch in flight");
   static_assert(!(PERM && NORMIN), "the normalising prologue reads its activations in sorted order");
+  static_assert(!CORR || (SDT == kBF16 && !FIELDS && !NORMIN), "decoded_bf16: bf16 scales, planar layout");
   __shared__ MfmaShared<NW, MB, RT> sh;
   extern __shared__ u32x4_t x_stage[];  // PERM with x_lds: x [MB, K], MB * K * 2 bytes of dynamic LDS
   if (VSEL == 1 || (VSEL == 0 && (O & 3) == 0))
-    w3_mfma_body<NW, PD, MB, RT, PERM, XDT, SDT, NORMIN, VSEL != 2, FIELDS>(sh, x, perm, planes, scales, zeros,
+    w3_mfma_body<NW, PD, MB, RT, PERM, XDT, SDT, NORMIN, VSEL != 2, FIELDS, CORR>(sh, x, perm, planes, scales, zeros,
                                                                            partial, out, O, G, gps, row_blocks,
                                                                            swiglu, ra, x_lds, x_stage, split);
   else
-    w3_mfma_body<NW, PD, MB, RT, PERM, XDT, SDT, NORMIN, VSEL == 1, FIELDS>(sh, x, perm, planes, scales, zeros,
+    w3_mfma_body<NW, PD, MB, RT, PERM, XDT, SDT, NORMIN, VSEL == 1, FIELDS, CORR>(sh, x, perm, planes, scales, zeros,
                                                                            partial, out, O, G, gps, row_blocks,
                                                                            swiglu, ra, x_lds, x_stage, split);
 }

@@ -78,6 +78,11 @@ FX_MFMA_DECL(dispatch_mfma_f16_t1_perm)
 FX_MFMA_DECL(dispatch_mfma_f16_t2_perm)
 #undef FX_MFMA_DECL
 
+// decoded_bf16 arithmetic (the +-3 correction as a second MFMA chain): one
+// activation row, one tile and one batch in flight per wave, bf16 scales, planar
+// payload, identity or permuted order; nw in {4, 8}.
+bool dispatch_mfma_corr(int nw, int xdt, const MfmaArgs& a, dim3 grid, hipStream_t s);
+
 // The normalising-prologue instantiations: one activation row, one 16-row tile
 // and one batch in flight per wave, no permutation; nw in {4, 8}.
 bool dispatch_mfma_normin(int nw, int xdt, int sdt, const MfmaArgs& a, dim3 grid, hipStream_t s);

@@ -42,16 +42,22 @@ _MLP = ("mlp.gate_proj", "mlp.up_proj", "mlp.down_proj")
 
 
 def _one_launch_w3(module) -> bool:
-    """A W3 Linear whose packed route is the one-launch MFMA GEMV (structural
-    arithmetic, one group per split, no bias): the form the decode chain fuses.
-    Table-route modules (``decoded_bf16``, ``groups_per_split > 1``) keep their
-    own split contract and summation order."""
+    """A W3 Linear whose packed route is the one-launch MFMA GEMV (one group per
+    split, no bias): the form that fuses with its neighbours into one GEMV.
+    Table-route modules (``groups_per_split > 1``) keep their own split contract
+    and summation order."""
     return isinstance(module, PackedW3Linear) and not module.uses_table_route and module.bias is None
 
 
+def _structural_w3(module) -> bool:
+    """A one-launch W3 Linear with structural arithmetic: what the fused decode
+    forms (SwiGLU epilogue, residual epilogue, normalising prologue) compute."""
+    return _one_launch_w3(module) and module.arithmetic == "structural"
+
+
 class _Linear:
-    """One decode Linear writing ``out``: the W3 MFMA GEMV, the module's own table
-    route (``decoded_bf16`` or ``groups_per_split > 1``: ``fx_w3_m1_out`` with its
+    """One decode Linear writing ``out``: the W3 MFMA GEMV (either arithmetic), the
+    module's own table route (``groups_per_split > 1``: ``fx_w3_m1_out`` with its
     row tile and split, as ``PackedW3Linear.forward`` runs it), the hybrid two-base
     GEMV (``fx_hybrid_gemv`` through the module's own packed kernel and
     workspace), or a dense matmul."""
@@ -162,7 +168,7 @@ class _GateUpSwiGLU:
 
     @staticmethod
     def build(gate, up):
-        if not (_one_launch_w3(gate) and _one_launch_w3(up)):
+        if not (_structural_w3(gate) and _structural_w3(up)):
             return None
         g, u = gate.layout(), up.layout()
         if (gate.in_features != up.in_features
@@ -309,7 +315,7 @@ class _ResidualStream:
     def _build_w3(session, payload_format=None):
         for layer, qkv, swiglu in zip(session.layers, session.qkv, session.swiglu):
             o, down = layer.self_attn.o_proj, layer.mlp.down_proj
-            if not (_one_launch_w3(o) and _one_launch_w3(down)) or qkv is None or swiglu is None:
+            if not (_structural_w3(o) and _structural_w3(down)) or qkv is None or swiglu is None:
                 return None
             gemv = qkv.call
             if not (isinstance(gemv, W3Gemv) and gemv.arith == _lib.ARITH_STRUCTURAL):

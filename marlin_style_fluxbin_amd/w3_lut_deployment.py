@@ -8,9 +8,11 @@ packed route: a missing library raises.
 
 Differences from the reference, all deliberate:
 * The layout may carry ``zeros`` and fp16 scales (see ``gptq_deployment``).
-* ``PackedW3Linear`` with ``structural`` arithmetic and one group per split runs
-  the one-launch MFMA kernel (the same structural sum, another fp32 order); every
-  other route runs the reference's split contract on the table kernel.
+* ``PackedW3Linear`` with one group per split runs the one-launch MFMA kernel in
+  either arithmetic (the same sums, another fp32 order; ``decoded_bf16`` adds the
+  +-3 correction as a second MFMA chain); a route that splits K over
+  ``groups_per_split > 1`` groups runs the reference's split contract on the table
+  kernel.
 * ``PackedW3Linear(max_packed_rows=n)`` opts 2..n-row inputs into the packed
   route (config 1's small-M GEMV); by default they take the dense fallback, as
   in the reference.
@@ -318,11 +320,12 @@ class PackedW3Linear(PackedLinearBase):
 
     Reference: ``w3_lut_deployment.py:190-359``; the route / fallback / binding
     protocol is ``packed_linear.PackedLinearBase``.  The packed route is the MFMA
-    kernel for ``structural`` arithmetic with one group per split (one launch),
+    kernel with one group per split (one launch; ``decoded_bf16`` arithmetic --
+    the ``fast_corrected`` route -- adds the +-3 correction as a second MFMA chain),
     and the reference's table contract (``w3_lut_m1_out``: ``row_tile``,
-    ``groups_per_split``, split partials summed in order) otherwise, which is how
-    ``decoded_bf16`` routes such as ``fast_corrected`` and ``observed_exact`` run.
-    The dense fallback dequantizes with the HIP restore kernel on GPU.
+    ``groups_per_split``, split partials summed in order) for routes that split K,
+    as ``observed_exact`` does at the gate/up and down shapes.  The dense fallback
+    dequantizes with the HIP restore kernel on GPU.
 
     ``max_packed_rows`` (not in the reference; default 1) lets 2..8-row inputs
     take the MFMA kernel too; they are then counted under ``packed_small_m``.
@@ -361,9 +364,11 @@ class PackedW3Linear(PackedLinearBase):
 
     @property
     def uses_table_route(self) -> bool:
-        """True when the packed route is the reference's table contract rather
-        than the one-launch MFMA kernel."""
-        return self.arithmetic != "structural" or self.groups_per_split != 1
+        """True when the packed route is the reference's table contract (K split
+        into groups_per_split-group partials summed in split order) rather than the
+        one-launch MFMA kernel, which serves one group per split in both
+        arithmetics (decoded_bf16: the +-3 correction as a second MFMA chain)."""
+        return self.groups_per_split != 1
 
     def layout(self) -> dict:
         return {name: getattr(self, name) for name in self._fields}

@@ -82,8 +82,13 @@ def test_linear_carries_explicit_arithmetic_and_split_policy():
     module = wl.PackedW3Linear(tiny_layout(), row_tile=256, groups_per_split=1, arithmetic="decoded_bf16",
                                route="fast_corrected")
     assert (module.arithmetic, module.groups_per_split, module.route) == ("decoded_bf16", 1, "fast_corrected")
-    assert module.uses_table_route
+    assert not module.uses_table_route  # one group per split: the one-launch MFMA kernel
     assert not wl.PackedW3Linear(tiny_layout(), row_tile=256).uses_table_route
+    two_groups = {"planes": gd.planar_from_codes(torch.zeros(256, 8, dtype=torch.uint8)),
+                  "scales": torch.ones(2, 8, dtype=torch.bfloat16), "perm": torch.arange(256, dtype=torch.int16)}
+    two = wl.PackedW3Linear(two_groups, row_tile=256, groups_per_split=2, arithmetic="decoded_bf16",
+                            route="observed_exact")
+    assert two.uses_table_route  # a K split: the reference's split contract on the table kernel
     assert wl.PackedW3Linear(tiny_layout(), row_tile=256, groups_per_split=1).route_counts == {
         "packed_m1": 0, "dense_fallback": 0}
     with pytest.raises(ValueError):

@@ -139,3 +139,64 @@ def test_mfma_result_independent_of_waves_and_prefetch(gpu, o, k, m):
         outs.append(out)
     for out in outs[1:]:
         assert torch.equal(out, outs[0])
+
+
+def _decoded(gpu, x, dl, o):
+    """fx_w3_gemv with decoded_bf16 arithmetic (one row: the MFMA kernel with the
+    +-3 correction chain)."""
+    from marlin_style_fluxbin_amd.w3_lut_deployment import W3Gemv
+
+    out = torch.full((x.shape[0], o), float("nan"), dtype=x.dtype, device=gpu)
+    W3Gemv(dl, arithmetic="decoded_bf16")(x.to(gpu), out)
+    return out
+
+
+@pytest.mark.parametrize("o,k", [(4096, 4096), (1024, 4096), (12288, 4096), (4096, 12288), (37, 1536), (300, 2048)])
+@pytest.mark.parametrize("permute", [False, True])
+@pytest.mark.parametrize("zeros", [True, False])
+def test_mfma_decoded_bf16_matches_the_decoded_oracle(gpu, o, k, permute, zeros):
+    """decoded_bf16 on the matrix cores: each weight bf16(s (q - z)), zero-points 3 / 4
+    (or the implicit 4), against the float64 dot with the oracle's restored weight
+    (``oracle.w3.matvec_decoded``): half a bf16 ulp plus the fp32 accumulation.  The
+    same payload's structural result differs from it (the correction is live)."""
+    print(f"decoded_bf16 MFMA {o}x{k} perm {permute} zeros {zeros}", flush=True)
+    codes, scales, zero, perm = config_codes(o, k, seed=o + k, zeros=zeros, scale_dtype=torch.bfloat16,
+                                             permute=permute)
+    layout = layout_from_codes(codes, scales, zero, perm)
+    dl = {n: t.to(gpu) for n, t in layout.items()}
+    x = torch.randn(1, k, generator=torch.Generator().manual_seed(k)).to(torch.bfloat16)
+    got = _decoded(gpu, x, dl, o).float().cpu().numpy()
+    truth = w3.matvec_decoded(x.float().numpy(), oracle_layout(layout), "bf16")
+    assert_half_ulp(got, truth, "bf16", rel_slack=2e-6, what=f"decoded {o}x{k}")
+    if o >= 1024:  # the correction is live: some outputs round differently from the structural kernel's
+        from marlin_style_fluxbin_amd.w3_lut_deployment import W3Gemv
+
+        structural = torch.empty(1, o, dtype=torch.bfloat16, device=gpu)
+        W3Gemv(dl)(x.to(gpu), structural)
+        assert (structural.float().cpu().numpy() != got).any()
+
+
+@pytest.mark.parametrize("xdtype,tag,slack", [(torch.float16, "f16", 3e-5), (torch.bfloat16, "bf16", 2e-6)])
+def test_mfma_decoded_bf16_activation_dtypes_and_outliers(gpu, xdtype, tag, slack):
+    """fp16 activations (the fp16 MFMA rounds products of subnormal operands at
+    ~2e-7 relative, hence 3e-5), and an outlier channel 2^10 times its group."""
+    o, k = 512, 4096
+    codes, scales, zero, _ = config_codes(o, k, seed=3, zeros=True, scale_dtype=torch.bfloat16)
+    layout = layout_from_codes(codes, scales, zero, None)
+    dl = {n: t.to(gpu) for n, t in layout.items()}
+    for x in (torch.randn(1, k, generator=torch.Generator().manual_seed(1)).to(xdtype),
+              outlier_activations(1, k, ratio=2.0 ** 10, seed=2, channels=[130, 2000], dtype=xdtype)):
+        got = _decoded(gpu, x, dl, o).float().cpu().numpy()
+        truth = w3.matvec_decoded(x.float().numpy(), oracle_layout(layout), "bf16")
+        assert_half_ulp(got, truth, tag, rel_slack=slack, what=f"decoded {tag}")
+
+
+def test_mfma_decoded_bf16_rejects_fp16_scales(gpu):
+    lib = _lib.library()
+    t = torch.zeros(3 * 16 * 16, dtype=torch.uint8, device=gpu)
+    x = torch.zeros(1, 128, dtype=torch.bfloat16, device=gpu)
+    sc = torch.ones(1, 16, dtype=torch.float16, device=gpu)
+    out = torch.zeros(1, 16, dtype=torch.bfloat16, device=gpu)
+    rc = lib.fx_w3_gemv(x.data_ptr(), 2, t.data_ptr(), sc.data_ptr(), 1, None, None, None, 0, out.data_ptr(), 1, 16,
+                        128, _lib.ARITH_DECODED_BF16, None)
+    assert rc == 1 and "bf16 scales" in lib.fx_last_error().decode()
