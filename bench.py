@@ -339,6 +339,94 @@ def bench_shape(o, k, device, steps, warmup, stream, min_bytes=320e6, min_copies
     }
 
 
+FIELDS_PLANS = [(1, 8, 1, 1), (1, 8, 3, 3), (2, 4, 2, 1), (3, 4, 2, 1), (4, 2, 4, 1)]
+SWEEP_SHAPES = {"q/o": (4096, 4096), "k/v": (1024, 4096), "gate/up": (12288, 4096), "down": (4096, 12288),
+                "gate|up": (24576, 4096), "q|k|v": (6144, 4096)}
+
+
+def fields_plan_sweep(device, stream, shapes=None, min_bytes=320e6, min_copies=50, steady_state=True):
+    """µs per launch of the field-layout GEMV under every plan that can take each
+    Qwen3-8B shape (fx_w3_fields_plan) and the one-tile kernel (plan "one-tile"),
+    graph-timed over rotating payloads with the paired protocol; the outputs of
+    every plan are checked bit-equal to the one-tile kernel's on the first copy."""
+    import torch
+
+    from marlin_style_fluxbin_amd import _lib
+
+    lib = _lib.library()
+    result = {}
+    for name, (o, k) in (shapes or SWEEP_SHAPES).items():
+        gen = torch.Generator(device=device).manual_seed(o + 3 * k)
+        copies = max(min_copies, int(min_bytes // algorithmic_bytes(o, k)) + 1)
+        with torch.cuda.stream(stream):  # every allocation, repack and call on the one stream
+            stacked, payloads = make_payloads(o, k, device, gen, copies)
+            fields = torch.empty_like(stacked["planes"])
+            for p in range(copies):
+                _lib.check(lib.fx_w3_planes_to_fields(stacked["planes"][p].data_ptr(), fields[p].data_ptr(), o, k,
+                                                      _lib.stream_handle(device)), "planes_to_fields")
+            x = torch.randn(1, k, device=device, generator=gen).to(torch.bfloat16)
+            out = torch.empty(1, o, device=device, dtype=torch.bfloat16)
+        torch.cuda.synchronize()
+
+        def call(p, dst=out):
+            _lib.check(lib.fx_w3_gemv_fields(x.data_ptr(), _lib.FX_BF16, fields[p].data_ptr(),
+                                             payloads[p]["scales"].data_ptr(), _lib.FX_F16,
+                                             payloads[p]["zeros"].data_ptr(), dst.data_ptr(), o, k,
+                                             _lib.stream_handle(device)), "gemv_fields")
+
+        def run():
+            for p in range(copies):
+                call(p)
+
+        plans = [("one-tile", (-1, 0, 0, 0))]
+        plans += [(",".join(map(str, pl)), pl) for pl in FIELDS_PLANS
+                  if o % 16 == 0 and k % 512 == 0 and k // 512 <= pl[3] * pl[0] * pl[1]]
+        graphs, first = {}, {}
+        for label, plan in plans:
+            _lib.check(lib.fx_w3_fields_plan(*plan), "fields plan")
+            try:
+                with torch.cuda.stream(stream):
+                    refs = [torch.full_like(out, float("nan")) for _ in range(2)]
+                    for ref in refs:
+                        call(0, ref)
+                    torch.cuda.synchronize()
+                    first[label] = refs
+                    graphs[label] = (capture(run, stream), copies)
+            finally:
+                _lib.check(lib.fx_w3_fields_plan(0, 0, 0, 0), "fields plan reset")
+        want = first["one-tile"][0]
+        differing = {label: int((refs[0] != want).sum()) + int((refs[1] != want).sum()) for label, refs in first.items()}
+        same = all(n == 0 for n in differing.values())
+        timing = paired_graph_timing(graphs, stream, repeats=10)
+        # steady state: one strided launch walks every payload (no per-launch cost)
+        steady = {}
+        if steady_state and (o // 16) % 8 == 0:
+            xs = torch.randn(copies, k, device=device, generator=gen).to(torch.bfloat16)
+            outs = torch.empty(copies, o, device=device, dtype=torch.bfloat16)
+            torch.cuda.synchronize()
+            sgraphs = {}
+            for label, plan in plans:
+                if plan[0] > 0 and (o // 16 + plan[0] - 1) // plan[0] % 8:
+                    continue
+                _lib.check(lib.fx_w3_fields_plan(*plan), "fields plan")
+                try:
+                    sgraphs[label] = (capture(lambda: batched_call(lib, xs, fields, stacked, outs, o, k,
+                                                                   _lib.PAYLOAD_FIELDS, device), stream), copies)
+                finally:
+                    _lib.check(lib.fx_w3_fields_plan(0, 0, 0, 0), "fields plan reset")
+            steady = {label: round(t["us"], 3) for label, t in paired_graph_timing(sgraphs, stream, repeats=5).items()}
+            del sgraphs, xs, outs
+        nbytes = algorithmic_bytes(o, k)
+        result[name] = {"O": o, "K": k, "bit_equal": same, "differing": differing,
+                        "us": {label: round(t["us"], 3) for label, t in timing.items()},
+                        "steady_us": steady,
+                        "frac_hbm": {label: round(nbytes / (t["us"] * 1e3) / HBM_PEAK_GBPS, 4) for label, t in timing.items()}}
+        print(f"# sweep {name}: {result[name]}", file=sys.stderr, flush=True)
+        del graphs, fields, stacked, payloads
+        torch.cuda.empty_cache()
+    return result
+
+
 def fused_ops_bench(device, steps, warmup, stream, launches=64, seed=0):
     """Config 2: the fused non-Linear decode ops at Qwen3-8B shapes, batch 1, one
     token.  Per launch (a graph of ``launches`` calls over distinct inputs and
@@ -1278,6 +1366,8 @@ def main():
                         help="run the counter-collection workload of the decode attention")
     parser.add_argument("--summarize-counters", nargs="+", metavar="ARG",
                         help="NAME CSV [CSV ...]: every counter per dispatch of kernels matching NAME")
+    parser.add_argument("--sweep-fields", action="store_true",
+                        help="time every field-layout plan at the Qwen3-8B shapes (one JSON line)")
     parser.add_argument("--summarize-trace", nargs=2, metavar=("CSV", "LAST"),
                         help="per-kernel summary of the last LAST dispatches of a kernel-trace CSV")
     args = parser.parse_args()
@@ -1313,6 +1403,12 @@ def main():
         return
     if args.decode:
         print(json.dumps(decode_bench(layers=args.decode_layers)), flush=True)
+        return
+    if args.sweep_fields:
+        import torch
+
+        device = torch.device("cuda:0")
+        print(json.dumps(fields_plan_sweep(device, torch.cuda.Stream(device))), flush=True)
         return
     if args.fused_ops:
         import torch

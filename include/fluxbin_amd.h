@@ -188,6 +188,17 @@ int fx_w3_planes_to_fields(const uint8_t *planes, uint8_t *fields, int O, int K,
  * arithmetic (fp32 accumulation of exact products; the sum order differs). */
 int fx_w3_gemv_fields(const void *x, int x_dtype, const uint8_t *fields, const void *scales, int scale_dtype,
                       const uint8_t *zeros, void *out, int O, int K, void *stream);
+/* Field-layout plans (no counterpart in the reference: benchmark sweeps and the
+ * plan-independence tests).  Every field-layout launch of the calling thread
+ * (fx_w3_gemv_fields, the FX_W3_FIELDS forms of fx_w3_gemv_swiglu / _residual /
+ * _rmsnormed and fx_w3_gemv_strided_batched) runs the given plan until the next
+ * call: tiles > 0 the shared-staging kernel with tiles 16-row tiles x parts K
+ * parts per workgroup, prefetch batches (512 columns) in flight and stage staged
+ * batches per wave -- one of (1,8,1,1) (1,8,3,3) (2,4,2,1) (3,4,2,1) (4,2,4,1),
+ * else FX_EINVAL, and a launch whose shape the plan cannot run (O % 16, K % 512,
+ * more batches than it stages) fails with FX_EINVAL; tiles <= 0 the one-tile
+ * kernel, the default.  Every plan gives the same bits.  Thread-local state. */
+int fx_w3_fields_plan(int tiles, int parts, int prefetch, int stage);
 /* Structural MFMA path with an explicit tiling (benchmark sweeps): waves per
  * workgroup in {4,8}, 4-group batches kept in flight per wave in {1,2},
  * groups per K split (rounded up to a multiple of 4, clamped to the padded group

@@ -568,7 +568,7 @@ bool two_base_config(int O, int G, int waves, int prefetch, int groups_per_split
 
 extern "C" {
 
-int fx_abi_version(void) { return 16; }
+int fx_abi_version(void) { return 17; }
 
 const char* fx_last_error(void) { return g_error; }
 
@@ -726,19 +726,69 @@ int check_out_index(const int16_t* out_index) {
   return FX_OK;
 }
 
-// One-row field-layout launch (one K split); epilogue and prologue from a.
-int run_fields(const MfmaArgs& base, int x_dtype, int scale_dtype, bool normin, hipStream_t s) {
+// ------------------------------------------------------------------ field-layout plans
+namespace {
+// The calling thread's field-layout plan (fx_w3_fields_plan): tiles > 0 a
+// shared-staging plan, otherwise the one-tile kernel.
+thread_local fx::WidePlan g_fields_plan{0, 0, 0, 0};
+constexpr size_t kWideMaxLds = 64 * 1024;
+}  // namespace
+
+// Why a shared-staging plan cannot run a shape (null: it can).
+const char* wide_plan_misfit(const fx::WidePlan& p, int O, int G, bool perm) {
+  if (O % 16 || G % 4) return "it needs O % 16 == 0 and K % 512 == 0";
+  if (G / 4 > p.stage * p.tiles * p.parts) return "K has more batches than its waves stage";
+  if (fx::wide_lds_bytes(p.tiles, G, perm) > kWideMaxLds) return "its LDS would exceed 64 KB";
+  if (perm && !fx::x_lds_fits(1, G * 128, p.tiles * p.parts)) return "the permuted copy of x does not fit";
+  return nullptr;
+}
+
+// One-row field-layout launch (one K split; batch payloads on grid.y when
+// a.batch is set); epilogue and prologue from a.
+int run_fields(const MfmaArgs& base, int x_dtype, int scale_dtype, bool normin, hipStream_t s, int batch = 1) {
+  const bool perm = base.perm != nullptr;
+  if (normin && perm) return fail(FX_EINVAL, "the normalising prologue takes no permutation");
+  // the one-tile kernel unless the thread asked for a shared-staging plan: no such
+  // plan measured faster at the Qwen3-8B shapes (per launch or in a strided batch)
+  const fx::WidePlan w = g_fields_plan;
+  if (w.tiles > 0) {
+    if (const char* why = wide_plan_misfit(w, base.O, base.G, perm))
+      return fail(FX_EINVAL, "field-layout plan (%d, %d, %d, %d) cannot run O = %d, K = %d: %s", w.tiles, w.parts,
+                  w.prefetch, w.stage, base.O, base.G * 128, why);
+  }
+  if (w.tiles > 0) {
+    MfmaArgs a = base;
+    a.row_blocks = (base.O / 16 + w.tiles - 1) / w.tiles;
+    a.gps = base.G;
+    a.x_lds = 0;
+    if (batch > 1 && a.row_blocks % 8)
+      return fail(FX_EINVAL, "a batch needs XCD-aligned row blocks (a multiple of 8), got %d", a.row_blocks);
+    const int mode = normin ? 1 : perm ? 2 : 0;
+    if (!fx::dispatch_fields_wide(w, x_dtype, scale_dtype, mode, a, dim3(a.row_blocks, batch), s))
+      return fail(FX_EINVAL, "no shared-staging field-layout kernel for this plan and dtype");
+    return check_launch("w3_fields_wide_kernel");
+  }
   MfmaPlan p = single_split_plan(base.O, base.G);
   const int tiles = fx::fields_row_tiles(normin, base.O);
   if (tiles != p.tiles) p = make_mfma_plan(base.O, base.G, p.nw, 1, base.G, tiles);
+  if (batch > 1 && p.row_blocks % 8)
+    return fail(FX_EINVAL, "a batch needs O / 16 to be a multiple of 8 (XCD-aligned row blocks), got O = %d", base.O);
   MfmaArgs a = base;
   a.gps = p.gps;
   a.row_blocks = p.row_blocks;
   a.x_lds = a.perm && fx::x_lds_fits(1, base.G * 128, p.nw);
-  if (!fx::dispatch_mfma_fields(p.nw, normin, x_dtype, scale_dtype, a, dim3(p.row_blocks, 1), s))
+  if (!fx::dispatch_mfma_fields(p.nw, normin, x_dtype, scale_dtype, a, dim3(p.row_blocks, batch), s))
     return fail(FX_EINVAL, "no field-layout MFMA kernel for waves %d", p.nw);
   return check_launch("w3_mfma_kernel (field layout)");
 }
+
+int fx_w3_fields_plan(int tiles, int parts, int prefetch, int stage) {
+  if (tiles > 0 && !fx::wide_plan_instantiated(fx::WidePlan{tiles, parts, prefetch, stage}))
+    return fail(FX_EINVAL, "no shared-staging kernel for plan (%d, %d, %d, %d)", tiles, parts, prefetch, stage);
+  g_fields_plan = tiles > 0 ? fx::WidePlan{tiles, parts, prefetch, stage} : fx::WidePlan{tiles < 0 ? -1 : 0, 0, 0, 0};
+  return FX_OK;
+}
+
 
 int fx_w3_gemv_swiglu(const void* x, int x_dtype, const uint8_t* planes, const void* scales,
                       int scale_dtype, const uint8_t* zeros, const int16_t* perm, const int16_t* out_index,
@@ -860,11 +910,20 @@ int fx_w3_gemv_strided_batched(const void* x, int x_dtype, long long x_stride, c
     return fail(FX_EINVAL, "strides must cover one payload, activation row and output row each");
   if (planes_stride % 16 || x_stride % 8)
     return fail(FX_EINVAL, "planes stride must be a multiple of 16 bytes and x stride of 8 elements");
-  MfmaPlan p = single_split_plan(O, G);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
   if (payload_format == FX_W3_FIELDS) {
-    const int tiles = fx::fields_row_tiles(false, O);
-    if (tiles != p.tiles) p = make_mfma_plan(O, G, p.nw, 1, G, tiles);
+    MfmaArgs a{};
+    a.x = static_cast<const uint16_t*>(x);
+    a.planes = planes;
+    a.scales = static_cast<const uint16_t*>(scales);
+    a.zeros = zeros;
+    a.out = static_cast<uint16_t*>(out);
+    a.O = O;
+    a.G = G;
+    if (batch > 1) a.batch = fx::StridedArgs{x_stride, planes_stride, scales_stride, zeros_stride, out_stride};
+    return run_fields(a, x_dtype, scale_dtype, false, s, batch);
   }
+  MfmaPlan p = single_split_plan(O, G);
   if (batch > 1 && p.row_blocks % 8)
     return fail(FX_EINVAL, "a batch needs O / 16 to be a multiple of 8 (XCD-aligned row blocks), got O = %d", O);
   MfmaArgs a{};
@@ -879,12 +938,6 @@ int fx_w3_gemv_strided_batched(const void* x, int x_dtype, long long x_stride, c
   a.row_blocks = p.row_blocks;
   if (batch > 1) a.batch = fx::StridedArgs{x_stride, planes_stride, scales_stride, zeros_stride, out_stride};
   const dim3 grid(p.row_blocks, batch);
-  const hipStream_t s = static_cast<hipStream_t>(stream);
-  if (payload_format == FX_W3_FIELDS) {
-    if (!fx::dispatch_mfma_fields(p.nw, false, x_dtype, scale_dtype, a, grid, s))
-      return fail(FX_EINVAL, "no field-layout MFMA kernel for waves %d", p.nw);
-    return check_launch("w3_mfma_kernel (field layout, strided batch)");
-  }
   if (!fx::dispatch_mfma(x_dtype, 1, p.nw, 1, 1, scale_dtype, a, grid, s))
     return fail(FX_EINVAL, "no MFMA kernel for waves %d", p.nw);
   return check_launch("w3_mfma_kernel (strided batch)");

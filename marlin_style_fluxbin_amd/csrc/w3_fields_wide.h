@@ -1,0 +1,374 @@
+// One-row field-layout GEMV with workgroup-shared activation staging.
+//
+// A workgroup owns T 16-row tiles and splits K into P parts: wave (tile, part)
+// multiplies its tile by the batches (4 groups, 512 columns) of its part.  The
+// workgroup builds the B operands of every batch once (wave w stages batches w,
+// w + T P, ...) into LDS, so the T tiles share one staging instead of each wave
+// staging the batch it multiplies; each wave keeps PD batches of weights in
+// flight and issues them before any wait.
+//
+// Same arithmetic, same bits as the one-tile field-layout kernel (w3_mfma.hip)
+// for every plan: the same B operands (stage_fields8), the same 16-MFMA chain
+// per batch and epilogue term (accumulate_group), and the same K order -- the
+// eight "virtual waves" k = 0..7 of a row each sum batches k, k + 8, ... in
+// turn, their group slots meet through the same two DPP adds, and the eight
+// sums are added in k order.  Part p serves virtual waves p, p + P, ... and
+// walks each one's batches before the next, so a wave holds one accumulator set.
+//
+// Measured on MI355X at the Qwen3-8B shapes, it is not the default: no plan beat
+// the one-tile kernel per launch (gate/up 12288 x 4096: 6.25 us one-tile, 6.81
+// at (1,8,1,1), 7.36 at (3,4,2,1)), and in a strided batch of 50 payloads it won
+// 2-7% only at the narrow shapes.  The counters show why: VALU per weight fell
+// (304 -> 213 per wave-batch at (3,4,2,1)) but every wave waits at the barrier
+// after the staging for the slowest wave of its workgroup, and a wave's serial
+// chain got longer (wave cycles 2510 -> 3467), which is what bounds a launch
+// whose loads all issue at once.  The plans stay for sweeps and the
+// plan-independence tests (fx_w3_fields_plan).
+//
+// Issue order: norm partials and output indices, the activations (and norm
+// weights or column indices) of the wave's staged batches, then the weight ring
+// (planes, non-temporal, then scales and zero-points).  Loads complete in issue
+// order, so the staging waits only for the L2-resident activations.
+#pragma once
+#include "w3_mfma.hip"
+#include "w3_mfma_launch.h"
+
+namespace fx {
+
+static_assert(kWideStage == 4 * kStageStride<1> && kWideVirtualWaves == kSumLanes, "LDS layout of wide_lds_bytes");
+
+template <int T, int P, int PD, int S, int XDT, int SDT, bool NORMIN, bool PERM>
+__global__ __launch_bounds__(T * P * 64) void w3_fields_wide_kernel(
+    const uint16_t* __restrict__ x, const int16_t* __restrict__ perm, const uint8_t* __restrict__ fields,
+    const uint16_t* __restrict__ scales, const uint8_t* __restrict__ zeros, uint16_t* out, int O, int G,
+    int row_blocks, int swiglu, ResidualArgs ra, StridedArgs sb) {
+  constexpr int NW = T * P;
+  static_assert(kSumLanes % P == 0, "parts must divide the eight virtual waves");
+  static_assert(16 * T <= 64 * NW, "one thread per output row");
+  static_assert(!(PERM && NORMIN), "the normalising prologue reads its activations in sorted order");
+  asm volatile("" ::"s"(x), "s"(perm), "s"(fields), "s"(scales), "s"(zeros), "s"(out), "s"(O), "s"(G),
+               "s"(row_blocks), "s"(swiglu), "s"(ra.ep_residual), "s"(ra.ep_partial), "s"(ra.ep_index),
+               "s"(ra.ep_sorted), "s"(sb.x), "s"(sb.planes), "s"(sb.scales), "s"(sb.zeros), "s"(sb.out));
+  if constexpr (NORMIN)
+    asm volatile("" ::"s"(ra.pro_partial), "s"(ra.pro_n), "s"(ra.pro_weight), "s"(ra.pro_eps));
+  if (sb.planes) {  // strided batch: grid.y walks the payloads
+    const long long p = blockIdx.y;
+    x += p * sb.x;
+    fields += p * sb.planes;
+    scales += p * sb.scales;
+    if (zeros) zeros += p * sb.zeros;
+    out += p * sb.out;
+  }
+  const int nbatch = (G + 3) >> 2;
+  extern __shared__ u32x4_t lds[];
+  u32x4_t* bst = lds;                                            // [nbatch][4 k-blocks][kStageStride]
+  u32x4_t* bzero = bst + nbatch * kWideStage;                    // [16 steps]
+  float* gsum = reinterpret_cast<float*>(bzero + 16);            // [nbatch][4]
+  int* gexp = reinterpret_cast<int*>(gsum + 4 * nbatch);         // [nbatch][4]
+  float* red = reinterpret_cast<float*>(gexp + 4 * nbatch);      // [8 virtual waves][16 T rows]
+  u32x4_t* xs = reinterpret_cast<u32x4_t*>(red + kSumLanes * 16 * T);  // PERM: x [K]
+
+  const int t = threadIdx.x, lane = t & 63, wave = wave_index();
+  const int part = wave % P, tile = wave / P;
+  const int K = G * 128;
+  const int row_base = xcd_local_index8(blockIdx.x, row_blocks) * (16 * T);
+  const int row0 = row_base + 16 * tile;
+  const unsigned zero_default = zeros ? 0u : 0x04040404u;
+
+  const auto rp = buffer_resource(fields, size_t(G) * 3 * O * 16);
+  const auto rs = buffer_resource(scales, size_t(G) * O * 2);
+  const auto rz = buffer_resource(zeros ? (const void*)zeros : (const void*)scales, zeros ? size_t(G) * O : 0);
+  const auto rx = buffer_resource(x, size_t(K) * 2);
+  const auto rperm = buffer_resource(PERM ? (const void*)perm : (const void*)x, PERM ? size_t(K) * 2 : 0);
+  const auto rwn = buffer_resource(NORMIN ? (const void*)ra.pro_weight : (const void*)x, NORMIN ? size_t(K) * 2 : 0);
+
+  float pp[kMaxNormPartialsPerLane];
+  if constexpr (NORMIN) {
+    const auto rpp = buffer_resource(ra.pro_partial, size_t(ra.pro_n) * 4);
+#pragma unroll
+    for (int k = 0; k < kMaxNormPartialsPerLane; ++k) {
+      const int idx = lane + 64 * k;
+      pp[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rpp, idx < ra.pro_n ? idx * 4 : kOutOfRange, 0, 0));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  // the output index of this thread's epilogue row (residual: row row_base + t;
+  // SwiGLU: pair row_base / 2 + t)
+  int ep_to = -1;
+  if (ra.ep_index) {
+    const int n_idx = ra.ep_residual ? O : O / 2;
+    const int at = ra.ep_residual ? (t < 16 * T ? row_base + t : n_idx) : (2 * t < 16 * T ? row_base / 2 + t : n_idx);
+    const auto rix = buffer_resource(ra.ep_index, size_t(n_idx) * 2);
+    ep_to = int(int16_t(__builtin_amdgcn_raw_buffer_load_b16(rix, at < n_idx ? at * 2 : kOutOfRange, 0, 0)));
+  }
+
+  const int r = lane & 15;   // A role: row within tile; x role: 8-column chunk
+  const int kb = lane >> 4;  // A role: k-block = group slot; D role: row block
+  const int c = lane & 15;   // B / D role: column (c < 4: group slot c of the one activation row)
+  const int cslot = c & 3;
+
+  // staging loads: batch wave + NW i of the workgroup, this lane's 8 columns
+  u32x4_t sx[S], sw[NORMIN ? S : 1];
+#pragma unroll
+  for (int i = 0; i < S; ++i) {
+    const int b = wave + NW * i;
+    const int g = 4 * b + kb;
+    const bool real = b < nbatch && g < G;
+    const int col = g * 128 + 8 * r;
+    if constexpr (PERM) sx[i] = load_b128(rperm, real ? col * 2 : kOutOfRange, 0);
+    else sx[i] = load_b128(rx, real ? col * 2 : kOutOfRange, 0);
+    if constexpr (NORMIN) sw[i] = load_b128(rwn, real ? col * 2 : kOutOfRange, 0);
+  }
+  constexpr int kXChunks = 4;
+  u32x4_t xc[PERM ? kXChunks : 1];
+  const int n16 = K / 8;
+  if constexpr (PERM) {
+#pragma unroll
+    for (int j = 0; j < kXChunks; ++j) {
+      const int cc = t + j * NW * 64;
+      xc[j] = load_b128(rx, cc < n16 ? cc * 16 : kOutOfRange, 0);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // this wave's batch sequence: virtual waves k = part, part + P, ... (< 8), each
+  // one's batches k, k + 8, ... (< nbatch); b >= nbatch ends it
+  struct Seq {
+    int k, b;
+  };
+  auto advance = [&](Seq s) __attribute__((always_inline)) {
+    s.b += kSumLanes;
+    if (s.b >= nbatch) {
+      s.k += P;
+      s.b = s.k;
+    }
+    return s;
+  };
+  auto live = [&](Seq s) __attribute__((always_inline)) { return s.k < kSumLanes && s.b < nbatch; };
+
+  // Load offsets: the lane's part is fixed (group slot, row), the batch's part
+  // is wave-uniform and rides in the scalar offset, so a batch costs no vector
+  // address arithmetic.  live = false: the lane offset is out of range (zeros,
+  // no memory access), so every wave issues the same loads whatever its batch
+  // count.
+  // The scalar offset is not range-checked: every live load is in bounds by the
+  // plan's contract (O % 16 == 0, G % 4 == 0), and tiles past O issue none.
+  const int plane_stride = O * 16;
+  const int p_lane = (kb * 3 * O + row0 + r) * 16;
+  const int e_lane = cslot * O + row0 + 4 * kb;
+  const bool tile_on = row0 < O;
+  auto issue = [&](int batch, BatchLoads<1, 1>& L, bool live_batch) __attribute__((always_inline)) {
+    const bool on = live_batch && tile_on;
+    const int pv = on ? p_lane : kOutOfRange;
+    const int ps = batch * 4 * 3 * plane_stride;
+    L.w[0][0] = load_b128_stream(rp, pv, ps);
+    L.w[0][1] = load_b128_stream(rp, pv, ps + plane_stride);
+    L.w[0][2] = load_b128_stream(rp, pv, ps + 2 * plane_stride);
+    __builtin_amdgcn_sched_barrier(0);
+    const int ev = on ? e_lane : kOutOfRange;
+    const uint2 s4 = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rs, on ? 2 * e_lane : kOutOfRange,
+                                                                                     batch * 4 * O * 2, 0));
+    L.s[0][0] = s4.x;
+    L.s[0][1] = s4.y;
+    L.z[0] = __builtin_amdgcn_raw_buffer_load_b32(rz, ev, batch * 4 * O, 0);
+  };
+
+  BatchLoads<1, 1> ring[PD];
+  Seq is{part, part};
+#pragma unroll
+  for (int i = 0; i < PD; ++i) {
+    const bool on = live(is);
+    issue(is.b, ring[i], on);
+    if (on) is = advance(is);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  if (wave == 0 && lane < 16) bzero[lane] = u32x4_t{0u, 0u, 0u, 0u};
+  if constexpr (PERM) {
+#pragma unroll
+    for (int j = 0; j < kXChunks; ++j) {
+      const int cc = t + j * NW * 64;
+      if (cc < n16) xs[cc] = xc[j];
+    }
+    __syncthreads();
+  }
+  float norm_inv = 1.f;
+  if constexpr (NORMIN) {
+    float total = 0.f;
+#pragma unroll
+    for (int k = 0; k < kMaxNormPartialsPerLane; ++k) total += pp[k];
+    norm_inv = rsqrtf(wave_total(total) / float(K) + ra.pro_eps);
+  }
+#pragma unroll
+  for (int i = 0; i < S; ++i) {
+    const int b = wave + NW * i;
+    if (b < nbatch) {
+      float v[8];
+      if constexpr (PERM) {
+        const bool real = 4 * b + kb < G;
+        const unsigned pw[4] = {sx[i].x, sx[i].y, sx[i].z, sx[i].w};
+        const uint16_t* xs16 = reinterpret_cast<const uint16_t*>(xs);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int src = int(int16_t(pw[j >> 1] >> (16 * (j & 1))));
+          v[j] = to_f32<XDT>(real && unsigned(src) < unsigned(K) ? xs16[src] : uint16_t(0));
+        }
+      } else {
+        const unsigned xw[4] = {sx[i].x, sx[i].y, sx[i].z, sx[i].w};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = to_f32<XDT>(uint16_t(xw[j >> 1] >> (16 * (j & 1))));
+        if constexpr (NORMIN) normalize8<XDT>(v, sw[i], norm_inv);
+      }
+      u32x4_t o;
+      float sm;
+      int ge;
+      stage_fields8(v, r, o, sm, ge);
+      bst[b * kWideStage + kb * kStageStride<1> + r] = o;
+      if (r == 0) {
+        gsum[4 * b + kb] = sm;
+        gexp[4 * b + kb] = ge;
+      }
+    }
+  }
+  __syncthreads();
+
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  auto consume = [&](int b, const BatchLoads<1, 1>& L) __attribute__((always_inline)) {
+    const u32x4_t* bsrc = c == kb ? bst + b * kWideStage + kb * kStageStride<1> : bzero;
+    f32x4_t d = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int word = 0; word < 4; ++word) {
+      u32x4_t a[4];
+      dequant_fields(L.w[0][0][word], L.w[0][1][word], L.w[0][2][word], a);
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a[s]),
+                                                   __builtin_bit_cast(f16x8_t, bsrc[4 * word + s]), d, 0, 0, 0);
+    }
+    const float sxv = gsum[4 * b + cslot];
+    const int fev = gexp[4 * b + cslot];
+    const unsigned zw = L.z[0] | zero_default;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const unsigned sbits = (j & 1) ? (L.s[0][j >> 1] >> 16) : (L.s[0][j >> 1] & 0xffffu);
+      acc[j] = accumulate_group(acc[j], to_f32<SDT>(uint16_t(sbits)), float((zw >> (8 * j)) & 0xffu), d[j], fev, sxv);
+    }
+  };
+  // a virtual wave's sum: its four group slots meet (lanes c^1, c^2), and lanes
+  // c = 0 hold rows 4 kb .. 4 kb + 3 of the tile
+  auto finish = [&](int k) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float a = acc[j];
+      a += dpp_move<kDppXor1>(a);
+      a += dpp_move<kDppXor2>(a);
+      acc[j] = a;
+    }
+    if (c == 0)
+      *reinterpret_cast<f32x4_t*>(red + k * 16 * T + 16 * tile + 4 * kb) = f32x4_t{acc[0], acc[1], acc[2], acc[3]};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[j] = 0.f;
+  };
+
+  Seq cs{part, part};
+  bool more = live(cs);
+  while (more) {
+#pragma unroll
+    for (int i = 0; i < PD; ++i) {
+      if (more) {
+        consume(cs.b, ring[i]);
+        const bool on = live(is);
+        issue(is.b, ring[i], on);
+        if (on) is = advance(is);
+        const Seq nx = advance(cs);
+        if (nx.k != cs.k) finish(cs.k);
+        cs = nx;
+        more = live(cs);
+      }
+    }
+  }
+  __syncthreads();
+
+  // row i's sum over the virtual waves that hold batches, in k order (all eight
+  // reads issued at once; a virtual wave without batches is skipped -- it held
+  // +0, which adds nothing to a sum that starts at +0)
+  const int nk = nbatch < kSumLanes ? nbatch : kSumLanes;
+  auto k_order_sum = [&](int i) __attribute__((always_inline)) {
+    float v[kSumLanes];
+#pragma unroll
+    for (int k = 0; k < kSumLanes; ++k) v[k] = red[k * 16 * T + i];
+    float total = 0.f;
+#pragma unroll
+    for (int k = 0; k < kSumLanes; ++k)
+      if (k < nk) total += v[k];
+    return total;
+  };
+  if (ra.ep_residual) {
+    // out = round(residual + round(y)); each 16-row tile's sum of out^2 (DPP row sum)
+    if (t < 16 * T) {
+      const int orow = row_base + t;
+      float h2 = 0.f;
+      if (orow < O) {
+        const float total = k_order_sum(t);
+        const float h = round_to<XDT>(to_f32<XDT>(ra.ep_residual[orow]) + round_to<XDT>(total));
+        out[orow] = from_f32<XDT>(h);
+        if (ra.ep_index && unsigned(ep_to) < unsigned(O)) ra.ep_sorted[ep_to] = from_f32<XDT>(h);
+        h2 = h * h;
+      }
+      h2 = row16_sum(h2);
+      const int tile_id = orow / 16;
+      if (r == 0 && tile_id < (O + 15) / 16) ra.ep_partial[tile_id] = h2;
+    }
+    return;
+  }
+  if (swiglu) {
+    // (gate, up) row pairs: act = round(round(silu(g)) * u), O / 2 outputs
+    if (2 * t < 16 * T) {
+      const int i = 2 * t;
+      const float tg = k_order_sum(i), tu = k_order_sum(i + 1);
+      const int orow = row_base + i;
+      if (orow < O) {
+        const float g = round_to<XDT>(tg), u = round_to<XDT>(tu);
+        const float sg = round_to<XDT>(g / (1.f + __expf(-g)));
+        if (!ra.ep_index) out[orow / 2] = from_f32<XDT>(sg * u);
+        else if (unsigned(ep_to) < unsigned(O / 2)) out[ep_to] = from_f32<XDT>(sg * u);
+      }
+    }
+    return;
+  }
+  if (t < 16 * T) {
+    const int orow = row_base + t;
+    if (orow < O) out[orow] = from_f32<XDT>(k_order_sum(t));
+  }
+}
+
+// mode: 0 plain (identity order), 1 normalising prologue, 2 permuted columns.
+template <int T, int P, int PD, int S, int XDT, int SDT>
+void launch_fields_wide(int mode, const MfmaArgs& a, dim3 grid, hipStream_t s) {
+  const size_t lds = wide_lds_bytes(T, a.G, mode == 2);
+#define FX_WIDE_LAUNCH(NORMIN, PERM)                                                                          \
+  hipLaunchKernelGGL((w3_fields_wide_kernel<T, P, PD, S, XDT, SDT, NORMIN, PERM>), grid, dim3(T * P * 64), lds, s, \
+                     a.x, a.perm, a.planes, a.scales, a.zeros, a.out, a.O, a.G, a.row_blocks, a.swiglu, a.res, a.batch)
+  if (mode == 1) FX_WIDE_LAUNCH(true, false);
+  else if (mode == 2) FX_WIDE_LAUNCH(false, true);
+  else FX_WIDE_LAUNCH(false, false);
+#undef FX_WIDE_LAUNCH
+}
+
+template <int T, int P, int PD, int S, int XDT>
+bool fields_wide_sdt(int sdt, int mode, const MfmaArgs& a, dim3 grid, hipStream_t s) {
+  if (sdt == kF16) { launch_fields_wide<T, P, PD, S, XDT, kF16>(mode, a, grid, s); return true; }
+  if (sdt == kBF16) { launch_fields_wide<T, P, PD, S, XDT, kBF16>(mode, a, grid, s); return true; }
+  return false;
+}
+
+template <int XDT>
+bool dispatch_fields_wide_xdt(const WidePlan& p, int sdt, int mode, const MfmaArgs& a, dim3 grid, hipStream_t s) {
+#define FX_WIDE_CASE(T, P, PD, S) \
+  if (p.tiles == T && p.parts == P && p.prefetch == PD && p.stage == S) return fields_wide_sdt<T, P, PD, S, XDT>(sdt, mode, a, grid, s);
+  FX_WIDE_PLANS(FX_WIDE_CASE)
+#undef FX_WIDE_CASE
+  return false;
+}
+
+}  // namespace fx

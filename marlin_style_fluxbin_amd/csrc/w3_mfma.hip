@@ -136,6 +136,51 @@ constexpr unsigned long long field_shift_nibbles() {
   return v;
 }
 
+// Field-layout B operands of one lane's 8 activations (k-block kb, lanes r =
+// 0..15 of the DPP row hold the group's 128 columns): fp16 values x * 2^(E - p)
+// (exact: they keep the activation's 8 or 11 significant bits within fp16's
+// range) with p the mantissa position of the register each pair meets, the
+// group's sum of x and exponent offset.  Shared by both field-layout kernels so
+// their bits agree.
+__device__ __forceinline__ void stage_fields8(const float v[8], int r, u32x4_t& o, float& sum, int& exp_off) {
+  float mx = 0.f, sm = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    mx = fmaxf(mx, fabsf(v[i]));
+    sm += v[i];
+  }
+  mx = row16_max(mx);
+  sm = row16_sum(sm);
+  const int E = choose_exponent<kF16>(mx);
+  // the 2^-p of this lane's four element pairs (registers 4 (r % 4) + q),
+  // recomputed per batch (the asm keeps it from being hoisted and held across
+  // the batch loop, where it cost the 4-wave kernel a spill)
+  unsigned rr = unsigned(r & 3);
+  asm volatile("" : "+v"(rr));
+  const unsigned fsh = unsigned(field_shift_nibbles() >> (16 * rr)) & 0xffffu;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int e = E - int((fsh >> (4 * q)) & 0xfu);
+    o[q] = unsigned(f32_to_f16_bits(ldexpf(v[2 * q], e))) | (unsigned(f32_to_f16_bits(ldexpf(v[2 * q + 1], e))) << 16);
+  }
+  sum = sm;
+  exp_off = subnormal_exponent<kF16>() - E;
+}
+
+// Qwen3RMSNorm of 8 activations: round(w * round(h * inv)) in the activation type.
+template <int XDT>
+__device__ __forceinline__ void normalize8(float v[8], const u32x4_t& wn, float norm_inv) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    v[i] = round_to<XDT>(to_f32<XDT>(uint16_t(wn[i >> 1] >> (16 * (i & 1)))) * round_to<XDT>(v[i] * norm_inv));
+}
+
+// One (row, group) term of the epilogue: acc + s (D 2^fe - z sum(x)), as two
+// fused multiply-adds (the rounding every MFMA kernel of this file shares).
+__device__ __forceinline__ float accumulate_group(float acc, float se, float zf, float d, int fe, float sx) {
+  return fmaf(se, fmaf(-zf, sx, ldexpf(d, fe)), acc);
+}
+
 // Everything one wave loads for one batch, kept as raw bits: this lane's plane
 // rows (one per row tile), its 8 activations per row (or, with a permutation,
 // its 8 column indices), and the epilogue's scales and zero-points.  Nothing
@@ -276,6 +321,9 @@ __device__ __forceinline__ void w3_mfma_body(
     bsrc[h] = ((cslot == kb && row < MB) ? my_stage + kb * kStageStride<MB> : bzero) + rmc[h];
   }
   const int plane_stride = O * 16;
+  int prow[RT];  // the lane's A row of each tile, clamped into [0, O)
+#pragma unroll
+  for (int tt = 0; tt < RT; ++tt) prow[tt] = min(row0 + 16 * tt + r, O - 1);
   // x role: lane (kb, r) owns columns 8r .. 8r+7 of its group; they land in
   // steps 4(r>>2) + s, operand slots je (weight 1) and je + 4 (weight 16).
   const int xstep = 4 * (r >> 2);
@@ -301,12 +349,16 @@ __device__ __forceinline__ void w3_mfma_body(
                                                        0, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
-    const int poff = live ? ((gb + kb) * 3 * O + row0 + r) * 16 : kOutOfRange;  // past the end -> zeros
+    // groups past G: past the end -> zeros; rows past O read row O - 1 (never
+    // stored), since the plane stride rides in the scalar offset, which the
+    // range check does not cover
+    const int gbase = (gb + kb) * 3 * O;
 #pragma unroll
     for (int tt = 0; tt < RT; ++tt) {
-      L.w[tt][0] = load_b128_stream(rp, poff + tt * 256, 0);
-      L.w[tt][1] = load_b128_stream(rp, poff + tt * 256, plane_stride);
-      L.w[tt][2] = load_b128_stream(rp, poff + tt * 256, 2 * plane_stride);
+      const int poff = live ? (gbase + prow[tt]) * 16 : kOutOfRange;
+      L.w[tt][0] = load_b128_stream(rp, poff, 0);
+      L.w[tt][1] = load_b128_stream(rp, poff, plane_stride);
+      L.w[tt][2] = load_b128_stream(rp, poff, 2 * plane_stride);
     }
     __builtin_amdgcn_sched_barrier(0);
     const int eoff = (gb + cslot) * O + row0 + 4 * kb;
@@ -331,38 +383,26 @@ __device__ __forceinline__ void w3_mfma_body(
 
   // B operands of one batch for activation row m from this lane's 8 values.
   auto stage_row = [&](int m, const float v[8]) __attribute__((always_inline)) {
-    float mx = 0.f, sm = 0.f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      mx = fmaxf(mx, fabsf(v[i]));
-      sm += v[i];
-    }
-    mx = row16_max(mx);
-    sm = row16_sum(sm);
     if constexpr (FIELDS) {
-      // fp16 operands (exact: x * 2^(E - p) keeps the activation's 8 or 11
-      // significant bits within fp16's range); the lane's 8 columns are elements
-      // 0..7 of step r, one 16-byte write
-      const int E = choose_exponent<kF16>(mx);
-      // the 2^-p of this lane's four element pairs (registers 4 (r % 4) + q),
-      // recomputed per batch (the asm keeps it from being hoisted and held
-      // across the batch loop, where it cost the 4-wave kernel a spill)
-      unsigned rr = unsigned(r & 3);
-      asm volatile("" : "+v"(rr));
-      const unsigned fsh = unsigned(field_shift_nibbles() >> (16 * rr)) & 0xffffu;
+      // the lane's 8 columns are elements 0..7 of step r, one 16-byte write
       u32x4_t o;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int e = E - int((fsh >> (4 * q)) & 0xfu);
-        o[q] = unsigned(f32_to_f16_bits(ldexpf(v[2 * q], e))) |
-               (unsigned(f32_to_f16_bits(ldexpf(v[2 * q + 1], e))) << 16);
-      }
+      float sm;
+      int ge;
+      stage_fields8(v, r, o, sm, ge);
       my_stage[kb * kStageStride<MB> + r * MB + m] = o;
       if (r == 0) {
         gsum[wave][kb * MB + m] = sm;
-        gexp[wave][kb * MB + m] = subnormal_exponent<kF16>() - E;
+        gexp[wave][kb * MB + m] = ge;
       }
     } else {
+      float mx = 0.f, sm = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        mx = fmaxf(mx, fabsf(v[i]));
+        sm += v[i];
+      }
+      mx = row16_max(mx);
+      sm = row16_sum(sm);
       const int E = choose_exponent<XDT>(mx);
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
@@ -431,12 +471,7 @@ __device__ __forceinline__ void w3_mfma_body(
         float v[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) v[i] = to_f32<XDT>(uint16_t(xw[i >> 1] >> (16 * (i & 1))));
-        if constexpr (NORMIN) {  // Qwen3RMSNorm: round(w * round(h * inv))
-#pragma unroll
-          for (int i = 0; i < 8; ++i)
-            v[i] = round_to<XDT>(to_f32<XDT>(uint16_t(L.wn[i >> 1] >> (16 * (i & 1)))) *
-                                 round_to<XDT>(v[i] * norm_inv));
-        }
+        if constexpr (NORMIN) normalize8<XDT>(v, L.wn, norm_inv);
         stage_row(m, v);
       }
     }
@@ -517,7 +552,7 @@ __device__ __forceinline__ void w3_mfma_body(
         const float se = to_f32<SDT>(uint16_t(sb));
         const float zf = float((zw >> (8 * j)) & 0xffu);
 #pragma unroll
-        for (int h = 0; h < NH; ++h) acc[tt][h][j] += se * (ldexpf(d[tt][h][j], fev[h]) - zf * sxv[h]);
+        for (int h = 0; h < NH; ++h) acc[tt][h][j] = accumulate_group(acc[tt][h][j], se, zf, d[tt][h][j], fev[h], sxv[h]);
         if constexpr (CORR) {
           // bf16(3 s) - 3 s: 3 s is exact in fp32 (s has 8 significant bits)
           const float eps = round_to<kBF16>(3.f * se) - 3.f * se;

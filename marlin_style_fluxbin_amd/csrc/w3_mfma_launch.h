@@ -95,6 +95,45 @@ bool dispatch_mfma_normin(int nw, int xdt, int sdt, const MfmaArgs& a, dim3 grid
 bool dispatch_mfma_fields(int nw, bool normin, int xdt, int sdt, const MfmaArgs& a, dim3 grid, hipStream_t s);
 inline int fields_row_tiles(bool normin, int O) { return normin && O % 4 == 0 ? 2 : 1; }
 
+// The field-layout kernel with workgroup-shared staging (w3_fields_wide.h):
+// workgroups of tiles 16-row tiles x parts K parts (one wave each), prefetch
+// batches in flight per wave, stage staged batches per wave (the plan needs
+// ceil(G / 4) <= stage * tiles * parts).  One activation row, one K split,
+// O % 16 == 0 and G % 4 == 0 (the batch offsets ride in the loads' scalar
+// offset, which the range check does not cover, so every live load must be in
+// bounds); the grid is (ceil(O / (16 tiles)), payloads).  mode 0 plain,
+// 1 normalising prologue, 2 permuted columns (a.perm; x in LDS, x_lds_fits).
+struct WidePlan {
+  int tiles, parts, prefetch, stage;
+};
+// The instantiated plans (tiles, parts, batches in flight, staged batches per wave).
+#define FX_WIDE_PLANS(X) X(1, 8, 1, 1) X(1, 8, 3, 3) X(2, 4, 2, 1) X(3, 4, 2, 1) X(4, 2, 4, 1)
+inline bool wide_plan_instantiated(const WidePlan& p) {
+#define FX_WIDE_IS(T, P, PD, S) \
+  if (p.tiles == T && p.parts == P && p.prefetch == PD && p.stage == S) return true;
+  FX_WIDE_PLANS(FX_WIDE_IS)
+#undef FX_WIDE_IS
+  return false;
+}
+// Dynamic LDS of a plan: the staged batches (4 k-blocks of 17 16-byte slots
+// each), one zero operand per MFMA step, the groups' sums and exponent offsets,
+// the 8 virtual waves' sums of the 16 T rows and, permuted, a copy of x.
+constexpr int kWideStage = 4 * 17;
+constexpr int kWideVirtualWaves = 8;
+inline size_t wide_lds_bytes(int T, int G, bool perm) {
+  const size_t nb = size_t(G + 3) / 4;
+  return nb * kWideStage * 16 + 16 * 16 + nb * 4 * 8 + size_t(kWideVirtualWaves) * 16 * T * 4 +
+         (perm ? size_t(G) * 128 * 2 : 0);
+}
+bool dispatch_fields_wide_bf16(const WidePlan& p, int sdt, int mode, const MfmaArgs& a, dim3 grid, hipStream_t s);
+bool dispatch_fields_wide_f16(const WidePlan& p, int sdt, int mode, const MfmaArgs& a, dim3 grid, hipStream_t s);
+inline bool dispatch_fields_wide(const WidePlan& p, int xdt, int sdt, int mode, const MfmaArgs& a, dim3 grid,
+                                 hipStream_t s) {
+  if (xdt == kBF16) return dispatch_fields_wide_bf16(p, sdt, mode, a, grid, s);
+  if (xdt == kF16) return dispatch_fields_wide_f16(p, sdt, mode, a, grid, s);
+  return false;
+}
+
 // The bind-time repack planes [G, 3, O, 16] -> fields [G, 3, O, 16].
 void launch_planes_to_fields(const uint8_t* planes, uint8_t* fields, int O, int G, hipStream_t s);
 

@@ -60,6 +60,7 @@ DEFAULTS = {
     "fx_w3_gemv_strided_batched": dict(W3, O=128, x_stride=256, planes_stride=3 * 2 * 128 * 16, scales_stride=256,
                                        zeros_stride=256, out_stride=128, batch=4),
     "fx_w3_gemv_fields": dict(W3, fields=D),
+    "fx_w3_fields_plan": dict(tiles=3, parts=4, prefetch=2, stage=1),
     "fx_w3_gemv_config": dict(W3, waves=8, prefetch=1, tiles=1),
     "fx_w3_restore": dict(planes=D, scales=D, scale_dtype=2, zeros=None, perm=None, weight=D, weight_dtype=2,
                           O=64, K=256, stream=None),
@@ -179,6 +180,9 @@ CASES = [
     ("fx_w3_planes_to_fields", dict(planes=D + 4), "16-byte aligned"),
     ("fx_w3_planes_to_fields", dict(fields=None), "non-null"),
     ("fx_w3_gemv_fields", dict(out=None), "out must be non-null"),
+    ("fx_w3_fields_plan", dict(tiles=5), "no shared-staging kernel for plan (5, 4, 2, 1)"),
+    ("fx_w3_fields_plan", dict(prefetch=3), "no shared-staging kernel"),
+    ("fx_w3_fields_plan", dict(tiles=1, parts=8, prefetch=2, stage=2), "no shared-staging kernel"),
     ("fx_w3_gemv_fields", dict(fields=D + 8), "16-byte aligned"),
     # explicit tilings
     ("fx_w3_gemv_config", dict(waves=3), "unsupported waves/prefetch/tiles"),
