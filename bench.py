@@ -341,7 +341,9 @@ def bench_shape(o, k, device, steps, warmup, stream, min_bytes=320e6, min_copies
 
 FIELDS_PLANS = [(1, 8, 1, 1), (1, 8, 3, 3), (2, 4, 2, 1), (3, 4, 2, 1), (4, 2, 4, 1)]
 SWEEP_SHAPES = {"q/o": (4096, 4096), "k/v": (1024, 4096), "gate/up": (12288, 4096), "down": (4096, 12288),
-                "gate|up": (24576, 4096), "q|k|v": (6144, 4096)}
+                "gate|up": (24576, 4096), "q|k|v": (6144, 4096), "gate|up normed swiglu": (24576, 4096),
+                "q|k|v normed": (6144, 4096)}
+NORMED_SWEEP = {"gate|up normed swiglu": 1, "q|k|v normed": 0}  # name -> swiglu
 
 
 def fields_plan_sweep(device, stream, shapes=None, min_bytes=320e6, min_copies=50, steady_state=True):
@@ -374,6 +376,22 @@ def fields_plan_sweep(device, stream, shapes=None, min_bytes=320e6, min_copies=5
                                              payloads[p]["zeros"].data_ptr(), dst.data_ptr(), o, k,
                                              _lib.stream_handle(device)), "gemv_fields")
 
+        normed = name in NORMED_SWEEP
+        if normed:  # the decode chain's normalising form (and SwiGLU at gate|up)
+            h = x
+            sums = (h.float().view(-1, 16) ** 2).sum(1).contiguous()
+            norm_w = (1 + 0.05 * torch.randn(k, device=device, generator=gen)).to(torch.bfloat16)
+            swiglu = NORMED_SWEEP[name]
+            out = torch.empty(1, o // 2 if swiglu else o, device=device, dtype=torch.bfloat16)
+            torch.cuda.synchronize()
+
+            def call(p, dst=out):
+                _lib.check(lib.fx_w3_gemv_rmsnormed(h.data_ptr(), _lib.FX_BF16, fields[p].data_ptr(),
+                                                    payloads[p]["scales"].data_ptr(), _lib.FX_F16,
+                                                    payloads[p]["zeros"].data_ptr(), sums.data_ptr(), k // 16,
+                                                    norm_w.data_ptr(), 1e-6, None, dst.data_ptr(), o, k, swiglu,
+                                                    _lib.PAYLOAD_FIELDS, _lib.stream_handle(device)), "rmsnormed")
+
         def run():
             for p in range(copies):
                 call(p)
@@ -400,7 +418,7 @@ def fields_plan_sweep(device, stream, shapes=None, min_bytes=320e6, min_copies=5
         timing = paired_graph_timing(graphs, stream, repeats=10)
         # steady state: one strided launch walks every payload (no per-launch cost)
         steady = {}
-        if steady_state and (o // 16) % 8 == 0:
+        if steady_state and not normed and (o // 16) % 8 == 0:
             xs = torch.randn(copies, k, device=device, generator=gen).to(torch.bfloat16)
             outs = torch.empty(copies, o, device=device, dtype=torch.bfloat16)
             torch.cuda.synchronize()
@@ -1366,8 +1384,9 @@ def main():
                         help="run the counter-collection workload of the decode attention")
     parser.add_argument("--summarize-counters", nargs="+", metavar="ARG",
                         help="NAME CSV [CSV ...]: every counter per dispatch of kernels matching NAME")
-    parser.add_argument("--sweep-fields", action="store_true",
-                        help="time every field-layout plan at the Qwen3-8B shapes (one JSON line)")
+    parser.add_argument("--sweep-fields", nargs="?", const="all", default=None, metavar="NAMES",
+                        help="time every field-layout plan at the Qwen3-8B shapes (one JSON line); "
+                             "optional comma list of shape names")
     parser.add_argument("--summarize-trace", nargs=2, metavar=("CSV", "LAST"),
                         help="per-kernel summary of the last LAST dispatches of a kernel-trace CSV")
     args = parser.parse_args()
@@ -1408,7 +1427,9 @@ def main():
         import torch
 
         device = torch.device("cuda:0")
-        print(json.dumps(fields_plan_sweep(device, torch.cuda.Stream(device))), flush=True)
+        names = list(SWEEP_SHAPES) if args.sweep_fields == "all" else args.sweep_fields.split(",")
+        print(json.dumps(fields_plan_sweep(device, torch.cuda.Stream(device),
+                                           {n: SWEEP_SHAPES[n] for n in names})), flush=True)
         return
     if args.fused_ops:
         import torch
