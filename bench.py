@@ -1283,6 +1283,69 @@ def pmc_attention_target(layers=36, position=543, rounds=8):
         print(f"# pmc-attention round {r + 1}/{rounds}", flush=True)
 
 
+def attention_sweep(layers=36, positions=(512, 543), lmax=1024):
+    """µs per call of the decode attention (``fx_decode_attention_rope``, Qwen3-8B
+    heads, split + combine launches) under every (keys per thread, head groups)
+    plan (``fx_decode_attention_plan``), graph-timed over ``layers`` distinct
+    caches as the decode walks them, paired protocol; outputs checked bit-equal
+    across head groups (the per-head arithmetic does not depend on the group)."""
+    import math
+
+    import torch
+
+    from marlin_style_fluxbin_amd import _lib
+
+    device = torch.device("cuda:0")
+    stream = torch.cuda.Stream(device)
+    gen = torch.Generator(device=device).manual_seed(0)
+    hq, hk, d = 32, 8, 128
+    lib = _lib.library()
+    bf = torch.bfloat16
+    with torch.cuda.stream(stream):
+        kc = [torch.randn(hk, lmax, d, device=device, generator=gen).to(bf) for _ in range(layers)]
+        vc = [torch.randn(hk, lmax, d, device=device, generator=gen).to(bf) for _ in range(layers)]
+        qkv = torch.randn(hq * d + 2 * hk * d, device=device, generator=gen).to(bf)
+        w = (1 + 0.02 * torch.randn(2, d, device=device, generator=gen)).to(bf)
+        cos = torch.randn(d, device=device, generator=gen).to(bf)
+        sin = torch.randn(d, device=device, generator=gen).to(bf)
+        nbytes = lib.fx_decode_attention_workspace_bytes(hq, lmax, d)
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
+        outs = torch.empty(layers, hq * d, dtype=bf, device=device)
+    torch.cuda.synchronize()
+    q, k, v = qkv[:hq * d], qkv[hq * d:(hq + hk) * d], qkv[(hq + hk) * d:]
+    result = {}
+    for pos in positions:
+        def run(pos=pos):
+            for layer in range(layers):
+                _lib.check(lib.fx_decode_attention_rope(
+                    q.data_ptr(), k.data_ptr(), v.data_ptr(), w[0].data_ptr(), w[1].data_ptr(), cos.data_ptr(),
+                    sin.data_ptr(), 1e-6, _lib.ROPE_STOCK, kc[layer].data_ptr(), vc[layer].data_ptr(),
+                    ws.data_ptr(), nbytes, None, outs[layer].data_ptr(), hq, hk, lmax, d, pos, 1 / math.sqrt(d),
+                    _lib.FX_BF16, _lib.stream_handle(device)), "fx_decode_attention_rope")
+
+        graphs, first, equal = {}, {}, True
+        for kpt in (1, 2, 4):
+            for groups in (1, 2, 4):
+                _lib.check(lib.fx_decode_attention_plan(kpt, groups), "attention plan")
+                try:
+                    with torch.cuda.stream(stream):
+                        run()
+                    torch.cuda.synchronize()
+                    got = outs.clone()
+                    graphs[f"kpt{kpt}/g{groups}"] = (capture(run, stream), layers)
+                finally:
+                    _lib.check(lib.fx_decode_attention_plan(0, 0), "attention plan reset")
+                if kpt in first:
+                    equal = equal and torch.equal(got, first[kpt])
+                else:
+                    first[kpt] = got
+        timing = paired_graph_timing(graphs, stream, repeats=5)
+        result[f"pos {pos}"] = {"us": {n: round(t["us"], 3) for n, t in timing.items()}, "groups_bit_equal": equal}
+        print(f"# attention sweep pos {pos}: {result[f'pos {pos}']}", file=sys.stderr, flush=True)
+        del graphs
+    return result
+
+
 def summarize_pmc(csv_paths, out_json):
     """Average rocprofv3 counter CSVs per kernel; scale FETCH_SIZE / WRITE_SIZE
     (KiB per dispatch) by what they read for the copy kernel of known size."""
@@ -1384,6 +1447,8 @@ def main():
                         help="run the counter-collection workload of the decode attention")
     parser.add_argument("--summarize-counters", nargs="+", metavar="ARG",
                         help="NAME CSV [CSV ...]: every counter per dispatch of kernels matching NAME")
+    parser.add_argument("--sweep-attention", action="store_true",
+                        help="time every attention plan (keys per thread x head groups) at 513 and 544 keys")
     parser.add_argument("--sweep-fields", nargs="?", const="all", default=None, metavar="NAMES",
                         help="time every field-layout plan at the Qwen3-8B shapes (one JSON line); "
                              "optional comma list of shape names")
@@ -1422,6 +1487,9 @@ def main():
         return
     if args.decode:
         print(json.dumps(decode_bench(layers=args.decode_layers)), flush=True)
+        return
+    if args.sweep_attention:
+        print(json.dumps(attention_sweep()), flush=True)
         return
     if args.sweep_fields:
         import torch

@@ -259,6 +259,12 @@ int fx_head_norm_rope(int ntensors, const void *const *inputs, void *const *outp
                       const void *cos, const void *sin, const long long *cos_strides,
                       const int *position, float eps, int rope_mode, int dtype, void *stream);
 
+/* Attention plan of the calling thread (no counterpart in the reference: sweeps
+ * and tests): keys_per_thread 1, 2 or 4 and head_groups 1, 2 or 4 (query heads of
+ * a KV head split over that many 256-thread groups of the split workgroup); 0
+ * keeps the default for either.  Applies to fx_decode_attention(_rope) until the
+ * next call.  Thread-local state. */
+int fx_decode_attention_plan(int keys_per_thread, int head_groups);
 /*
  * Decode attention of one token over a static KV cache: the attention the
  * reference's decode runs inside stock HF Qwen3Attention (static_decode.py:73-81:

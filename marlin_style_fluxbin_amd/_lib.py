@@ -53,6 +53,7 @@ SIGNATURES: dict[str, tuple] = {
     "fx_rmsnorm": (_i, [_p, _p, _p, _p, _p, _i, _i, _f, _i, _p]),
     "fx_head_norm_rope": (_i, [_i, _p, _p, _p, _p, _p, _p, _i, _i, _i, _p, _p, _p, _p, _f, _i, _i, _p]),
     "fx_decode_attention_workspace_bytes": (_sz, [_i, _i, _i]),
+    "fx_decode_attention_plan": (_i, [_i, _i]),
     "fx_decode_attention": (_i, [_p, _p, _p, _p, _sz, _p, _p, _i, _i, _i, _i, _i, _f, _i, _p]),
     "fx_decode_attention_rope": (_i, [_p, _p, _p, _p, _p, _p, _p, ctypes.c_float, _i, _p, _p, _p, _sz, _p, _p, _i, _i, _i, _i, _i, ctypes.c_float, _i, _p]),
     "fx_silu_mul": (_i, [_p, _p, _p, _i, _i, _p]),

@@ -1120,6 +1120,10 @@ int fx_head_norm_rope(int ntensors, const void* const* inputs, void* const* outp
   return check_launch("head_norm_rope_kernel");
 }
 
+// Query-head groups per attention split workgroup (decode.hip: group g scores
+// heads g * 4 / groups, ... of the KV head).
+constexpr int kAttnDefaultGroups = 1;
+
 // Attention workspace: the fp32 partials, [Hq, splits, D] outputs then
 // [Hq, splits, 2] (max, sum).
 size_t fx_decode_attention_workspace_bytes(int n_q_heads, int max_len, int head_dim) {
@@ -1131,6 +1135,9 @@ size_t fx_decode_attention_workspace_bytes(int n_q_heads, int max_len, int head_
 }
 
 namespace {
+// The calling thread's attention plan (fx_decode_attention_plan): 0 = the default.
+thread_local int g_attn_kpt = 0, g_attn_groups = 0;
+
 int decode_attention(const void* q, const void* k_cache, const void* v_cache, void* workspace,
                      size_t workspace_bytes, void* out, int n_q_heads, int n_kv_heads, int max_len,
                      int head_dim, int position, float scale, int dtype, void* stream,
@@ -1187,7 +1194,13 @@ int decode_attention(const void* q, const void* k_cache, const void* v_cache, vo
       }
     }
   }
+  if (g_attn_kpt) a.kpt = g_attn_kpt;
   a.splits = splits_for(a.kpt);
+  // query-head groups: a group per kAttnHeadsPerPass / groups heads, no more
+  // groups than a KV head has query heads
+  const int per_kv = n_q_heads / n_kv_heads;
+  a.groups = g_attn_groups ? g_attn_groups : kAttnDefaultGroups;
+  while (a.groups > 1 && a.groups > per_kv) a.groups /= 2;
   if (a.splits > 65535) return fail(FX_EINVAL, "position %d needs %d key splits (at most 65535)", position, a.splits);
   a.scale = scale;
   a.pre = pre;
@@ -1196,6 +1209,16 @@ int decode_attention(const void* q, const void* k_cache, const void* v_cache, vo
 }
 
 }  // namespace
+
+int fx_decode_attention_plan(int keys_per_thread, int head_groups) {
+  if (keys_per_thread != 0 && keys_per_thread != 1 && keys_per_thread != 2 && keys_per_thread != 4)
+    return fail(FX_EINVAL, "keys_per_thread must be 0 (default), 1, 2 or 4, got %d", keys_per_thread);
+  if (head_groups != 0 && head_groups != 1 && head_groups != 2 && head_groups != 4)
+    return fail(FX_EINVAL, "head_groups must be 0 (default), 1, 2 or 4, got %d", head_groups);
+  g_attn_kpt = keys_per_thread;
+  g_attn_groups = head_groups;
+  return FX_OK;
+}
 
 int fx_decode_attention(const void* q, const void* k_cache, const void* v_cache, void* workspace,
                         size_t workspace_bytes, const int16_t* out_index, void* out, int n_q_heads,

@@ -88,8 +88,8 @@ __device__ __forceinline__ u32x4_t head_norm_rope8(const u32x4_t& x, const u32x4
   return o;
 }
 
-template <int DT, int D, int KPT, bool PRE>
-__global__ __launch_bounds__(256) void attn_split_kernel(const uint16_t* __restrict__ q,
+template <int DT, int D, int KPT, bool PRE, int NG>
+__global__ __launch_bounds__(256 * NG) void attn_split_kernel(const uint16_t* __restrict__ q,
                                                          const uint16_t* kc, const uint16_t* vc,
                                                          float* __restrict__ po, float* __restrict__ pml,
                                                          uint16_t* __restrict__ out,
@@ -101,12 +101,17 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const uint16_t* __restr
   if constexpr (PRE)
     asm volatile("" ::"s"(pre.k_raw), "s"(pre.v_raw), "s"(pre.q_weight), "s"(pre.k_weight), "s"(pre.cos),
                  "s"(pre.sin), "s"(pre.eps), "s"(pre.rope_mode));
-  constexpr int DB = D / 8, KS = 256 / DB, HB = kAttnHeadsPerPass;
-  __shared__ float red_o[KS][HB][D];
-  __shared__ float red_l[KS][HB];
-  __shared__ float red_m[4][HB];
-  __shared__ u32x4_t qsh[PRE ? 4 : 1][HB][DB];  // PRE: normalised queries of each wave
-  const int t = threadIdx.x, lane = t & 63, wave = wave_index();
+  // NG head groups of 256 threads: group grp scores query heads grp * HB + ...
+  // of each pass against the same chunk (its K and V rows come from L1 after
+  // the first group's loads), so a wave's serial chain covers HB heads, not 4
+  static_assert(kAttnHeadsPerPass % NG == 0, "head groups must divide the heads of a pass");
+  constexpr int DB = D / 8, KS = 256 / DB, HB = kAttnHeadsPerPass / NG;
+  __shared__ float red_o[NG][KS][HB][D];
+  __shared__ float red_l[NG][KS][HB];
+  __shared__ float red_m[NG][4][HB];
+  __shared__ u32x4_t qsh[PRE ? 4 * NG : 1][HB][DB];  // PRE: normalised queries of each wave
+  const int grp = int(threadIdx.x) >> 8, t = int(threadIdx.x) & 255, lane = t & 63, wave = wave_index();
+  const int gw = wave & 3;  // wave within the head group
   const int db = t % DB, ks = t / DB;
   const int g = blockIdx.x, chunk = blockIdx.y;
   const int first = chunk * (KS * KPT);
@@ -138,10 +143,13 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const uint16_t* __restr
     }
   };
   if constexpr (PRE) {
-    load_own(0);
+    load_own(grp * HB);
   } else {
 #pragma unroll
-    for (int hh = 0; hh < HB; ++hh) qr[hh] = load_b128(rq, hh < G ? (hh * D + 8 * db) * 2 : kOutOfRange, 0);
+    for (int hh = 0; hh < HB; ++hh) {
+      const int h = grp * HB + hh;
+      qr[hh] = load_b128(rq, h < G ? (h * D + 8 * db) * 2 : kOutOfRange, 0);
+    }
   }
   if constexpr (PRE) {
     const auto rd = [&](const uint16_t* p, bool on) {
@@ -188,16 +196,20 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const uint16_t* __restr
         if (first + ks + KS * i == pos) {
           kr[i] = kpos;
           vr[i] = vraw;
-          const size_t at = (size_t(g) * Lmax + pos) * D + 8 * db;
-          *reinterpret_cast<u32x4_t*>(const_cast<uint16_t*>(kc) + at) = kpos;
-          *reinterpret_cast<u32x4_t*>(const_cast<uint16_t*>(vc) + at) = vraw;
+          if (grp == 0) {  // one group writes the caches
+            const size_t at = (size_t(g) * Lmax + pos) * D + 8 * db;
+            *reinterpret_cast<u32x4_t*>(const_cast<uint16_t*>(kc) + at) = kpos;
+            *reinterpret_cast<u32x4_t*>(const_cast<uint16_t*>(vc) + at) = vraw;
+          }
         }
       }
     }
   }
 
-  for (int h0 = 0; h0 < G; h0 += HB) {
-    if (!PRE && h0 > 0) {
+  // every group runs the same number of passes (the barriers inside are workgroup-wide)
+  for (int pass = 0; pass * NG * HB < G; ++pass) {
+    const int h0 = (pass * NG + grp) * HB;
+    if (!PRE && pass > 0) {
 #pragma unroll
       for (int hh = 0; hh < HB; ++hh)
         qr[hh] = load_b128(rq, h0 + hh < G ? ((h0 + hh) * D + 8 * db) * 2 : kOutOfRange, 0);
@@ -208,7 +220,7 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const uint16_t* __restr
 #pragma unroll
       for (int e = 0; e < 8; ++e) kf[i][e] = to_f32<DT>(uint16_t(kr[i][e >> 1] >> (16 * (e & 1))));
     if constexpr (PRE) {
-      if (h0 > 0) {
+      if (pass > 0) {
         load_own(h0);
         normalise_queries();
       }
@@ -234,14 +246,14 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const uint16_t* __restr
     }
     if (lane == 0) {
 #pragma unroll
-      for (int hh = 0; hh < HB; ++hh) red_m[wave][hh] = mt[hh];
+      for (int hh = 0; hh < HB; ++hh) red_m[grp][gw][hh] = mt[hh];
     }
     __syncthreads();
     float o[HB][8], lt[HB];
 #pragma unroll
     for (int hh = 0; hh < HB; ++hh) {
       // the chunk's first key is live, so m is finite
-      const float m = fmaxf(fmaxf(red_m[0][hh], red_m[1][hh]), fmaxf(red_m[2][hh], red_m[3][hh]));
+      const float m = fmaxf(fmaxf(red_m[grp][0][hh], red_m[grp][1][hh]), fmaxf(red_m[grp][2][hh], red_m[grp][3][hh]));
       mt[hh] = m;
       lt[hh] = 0.f;
 #pragma unroll
@@ -256,23 +268,23 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const uint16_t* __restr
     }
 #pragma unroll
     for (int hh = 0; hh < HB; ++hh) {
-      float4* dst = reinterpret_cast<float4*>(&red_o[ks][hh][8 * db]);
+      float4* dst = reinterpret_cast<float4*>(&red_o[grp][ks][hh][8 * db]);
       dst[0] = make_float4(o[hh][0], o[hh][1], o[hh][2], o[hh][3]);
       dst[1] = make_float4(o[hh][4], o[hh][5], o[hh][6], o[hh][7]);
-      if (db == 0) red_l[ks][hh] = lt[hh];
+      if (db == 0) red_l[grp][ks][hh] = lt[hh];
     }
     __syncthreads();
     for (int idx = t; idx < HB * D; idx += 256) {
       const int hh = idx / D, d = idx % D, h = h0 + hh;
       float total = 0.f;
 #pragma unroll
-      for (int r = 0; r < KS; ++r) total += red_o[r][hh][d];
+      for (int r = 0; r < KS; ++r) total += red_o[grp][r][hh][d];
       if (h < G) {
         if (splits == 1) {
           // the whole context is this chunk: o = sum p v / sum p
           float l = 0.f;
 #pragma unroll
-          for (int r = 0; r < KS; ++r) l += red_l[r][hh];
+          for (int r = 0; r < KS; ++r) l += red_l[grp][r][hh];
           const int n_out = int(gridDim.x) * G * D;
           int at = (g * G + h) * D + d;
           if (out_index) at = out_index[at];
@@ -283,7 +295,7 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const uint16_t* __restr
           if (d == 0) {
             float l = 0.f;
 #pragma unroll
-            for (int r = 0; r < KS; ++r) l += red_l[r][hh];
+            for (int r = 0; r < KS; ++r) l += red_l[grp][r][hh];
             pml[slot * 2] = mt[hh];
             pml[slot * 2 + 1] = l;
           }
@@ -456,16 +468,23 @@ bool launch_decode_embed(int dt, const long long* token, const uint16_t* table, 
   return true;
 }
 
+template <int DT, int D, int KPT, int NG>
+void attn_split_launch(const AttnArgs& a, float* po, float* pml, hipStream_t s) {
+  if (a.pre.k_raw)
+    hipLaunchKernelGGL((attn_split_kernel<DT, D, KPT, true, NG>), dim3(a.Hk, a.splits), dim3(256 * NG), 0, s, a.q,
+                       a.k, a.v, po, pml, a.out, a.out_index, a.Hq / a.Hk, a.Lmax, a.pos, a.splits, a.scale, a.pre);
+  else
+    hipLaunchKernelGGL((attn_split_kernel<DT, D, KPT, false, NG>), dim3(a.Hk, a.splits), dim3(256 * NG), 0, s, a.q,
+                       a.k, a.v, po, pml, a.out, a.out_index, a.Hq / a.Hk, a.Lmax, a.pos, a.splits, a.scale, a.pre);
+}
+
 template <int DT, int D, int KPT>
 void attn_launch(const AttnArgs& a, hipStream_t s) {
   float* po = a.partial;
   float* pml = a.partial + size_t(a.Hq) * a.splits * D;
-  if (a.pre.k_raw)
-    hipLaunchKernelGGL((attn_split_kernel<DT, D, KPT, true>), dim3(a.Hk, a.splits), dim3(256), 0, s, a.q, a.k,
-                       a.v, po, pml, a.out, a.out_index, a.Hq / a.Hk, a.Lmax, a.pos, a.splits, a.scale, a.pre);
-  else
-    hipLaunchKernelGGL((attn_split_kernel<DT, D, KPT, false>), dim3(a.Hk, a.splits), dim3(256), 0, s, a.q, a.k,
-                       a.v, po, pml, a.out, a.out_index, a.Hq / a.Hk, a.Lmax, a.pos, a.splits, a.scale, a.pre);
+  if (a.groups == 4) attn_split_launch<DT, D, KPT, 4>(a, po, pml, s);
+  else if (a.groups == 2) attn_split_launch<DT, D, KPT, 2>(a, po, pml, s);
+  else attn_split_launch<DT, D, KPT, 1>(a, po, pml, s);
   if (a.splits > 1)
     hipLaunchKernelGGL((attn_combine_kernel<DT, D>), dim3(a.Hq), dim3(256), 0, s, po, pml, a.out, a.out_index,
                        a.splits);

@@ -28,6 +28,7 @@ struct AttnArgs {
   const int16_t* out_index;  // null: out in head order; else value i goes to out[out_index[i]]
   int Hq, Hk, Lmax, pos;
   int kpt, splits;     // keys per thread (1, 2, 4); splits = ceil((pos + 1) / (keys per workgroup))
+  int groups;          // query-head groups of 256 threads per split workgroup (1, 2, 4)
   float scale;
   AttnPre pre;
 };

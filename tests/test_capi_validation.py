@@ -61,6 +61,7 @@ DEFAULTS = {
                                        zeros_stride=256, out_stride=128, batch=4),
     "fx_w3_gemv_fields": dict(W3, fields=D),
     "fx_w3_fields_plan": dict(tiles=3, parts=4, prefetch=2, stage=1),
+    "fx_decode_attention_plan": dict(keys_per_thread=2, head_groups=2),
     "fx_w3_gemv_config": dict(W3, waves=8, prefetch=1, tiles=1),
     "fx_w3_restore": dict(planes=D, scales=D, scale_dtype=2, zeros=None, perm=None, weight=D, weight_dtype=2,
                           O=64, K=256, stream=None),
@@ -183,6 +184,8 @@ CASES = [
     ("fx_w3_fields_plan", dict(tiles=5), "no shared-staging kernel for plan (5, 4, 2, 1)"),
     ("fx_w3_fields_plan", dict(prefetch=3), "no shared-staging kernel"),
     ("fx_w3_fields_plan", dict(tiles=1, parts=8, prefetch=2, stage=2), "no shared-staging kernel"),
+    ("fx_decode_attention_plan", dict(keys_per_thread=3), "keys_per_thread must be 0 (default), 1, 2 or 4"),
+    ("fx_decode_attention_plan", dict(head_groups=8), "head_groups must be 0 (default), 1, 2 or 4"),
     ("fx_w3_gemv_fields", dict(fields=D + 8), "16-byte aligned"),
     # explicit tilings
     ("fx_w3_gemv_config", dict(waves=3), "unsupported waves/prefetch/tiles"),

@@ -113,6 +113,64 @@ def test_decode_attention_rope(gpu, dtype, hq, hk, d, lmax, pos, rope_mode):
     assert np.mean(np.abs(got - exact) <= 2 * _ulp(exact, dtype) + 1e-6 * np.abs(exact).max()) > 0.98
 
 
+@pytest.mark.parametrize("hq,hk,d,lmax,pos", [(32, 8, 128, 544, 543), (12, 2, 128, 200, 150), (4, 2, 64, 130, 100),
+                                              (8, 8, 256, 300, 299), (32, 8, 128, 600, 40)])
+def test_decode_attention_plans(gpu, hq, hk, d, lmax, pos):
+    """fx_decode_attention_plan: every keys-per-thread choice within the oracle bar
+    of test_decode_attention, and every head-group count bit-identical to one group
+    for the same keys per thread (a query head's arithmetic does not depend on the
+    group that scores it); the fused form's cache write too."""
+    from oracle import norms
+
+    g = torch.Generator().manual_seed(pos + hq)
+    q = torch.randn(hq, d, generator=g).bfloat16()
+    k = torch.randn(hk, d, generator=g).bfloat16()
+    v = torch.randn(hk, d, generator=g).bfloat16()
+    w = (1 + 0.2 * torch.randn(2, d, generator=g)).bfloat16()
+    cos_t, sin_t = norms.rope_cos_sin([pos], d, 1e6, "bf16")
+    kc0 = torch.randn(hk, lmax, d, generator=g).bfloat16()
+    vc0 = torch.randn(hk, lmax, d, generator=g).bfloat16()
+    lib = _lib.library()
+    nbytes = lib.fx_decode_attention_workspace_bytes(hq, lmax, d)
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device=gpu)
+    dev = {n: t.to(gpu) for n, t in dict(q=q, k=k, v=v, w=w).items()}
+    cos_d = torch.from_numpy(cos_t[0]).bfloat16().to(gpu)
+    sin_d = torch.from_numpy(sin_t[0]).bfloat16().to(gpu)
+    exact = decode.gqa_attention(q.float().numpy(), kc0.float().numpy(), vc0.float().numpy(), pos, 1 / np.sqrt(d))
+
+    def run(plan, fused):
+        kc, vc = kc0.to(gpu), vc0.to(gpu)
+        out = torch.full((hq, d), float("nan"), dtype=torch.bfloat16, device=gpu)
+        _lib.check(lib.fx_decode_attention_plan(*plan), "plan")
+        try:
+            if fused:
+                rc = lib.fx_decode_attention_rope(
+                    dev["q"].data_ptr(), dev["k"].data_ptr(), dev["v"].data_ptr(), dev["w"][0].data_ptr(),
+                    dev["w"][1].data_ptr(), cos_d.data_ptr(), sin_d.data_ptr(), 1e-6, _lib.ROPE_STOCK, kc.data_ptr(),
+                    vc.data_ptr(), ws.data_ptr(), nbytes, None, out.data_ptr(), hq, hk, lmax, d, pos, 1 / np.sqrt(d),
+                    _lib.FX_BF16, _lib.stream_handle(gpu))
+            else:
+                rc = lib.fx_decode_attention(dev["q"].data_ptr(), kc.data_ptr(), vc.data_ptr(), ws.data_ptr(),
+                                             nbytes, None, out.data_ptr(), hq, hk, lmax, d, pos, 1 / np.sqrt(d),
+                                             _lib.FX_BF16, _lib.stream_handle(gpu))
+            _lib.check(rc, "attention")
+        finally:
+            _lib.check(lib.fx_decode_attention_plan(0, 0), "plan reset")
+        torch.cuda.synchronize()
+        return out, kc, vc
+
+    for kpt in (1, 2, 4):
+        base, _, _ = run((kpt, 1), False)
+        got = base.float().cpu().numpy()
+        assert np.all(np.abs(got - exact) <= 2 * _ulp(exact, "bf16") + 1e-6 * np.abs(exact).max()), kpt
+        fused_base = run((kpt, 1), True)
+        for groups in (2, 4):
+            assert torch.equal(run((kpt, groups), False)[0], base), (kpt, groups)
+            fused = run((kpt, groups), True)
+            for a, b in zip(fused, fused_base):
+                assert torch.equal(a, b), (kpt, groups)
+
+
 @pytest.mark.parametrize("hq,hk", [(32, 8), (12, 2)])
 def test_decode_attention_workspace_reuse(gpu, hq, hk):
     """One workspace (no initial contents) serves a run of calls whose split
