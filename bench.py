@@ -1245,6 +1245,33 @@ def summarize_counters(csv_paths, name_filter):
             print(f"| {c} | {m[c]:.1f} | {per_wave} |")
 
 
+def pmc_small_m_target(shape, copies=24):
+    """Workload for ``rocprofv3`` passes over the small-M GEMV (config 1): the
+    planar ``fx_w3_gemv`` at one Qwen3-8B shape for M = 1, 2, 4, 8 (the default
+    plans), ``copies`` rotating payloads each, a progress line per M."""
+    import torch
+
+    from marlin_style_fluxbin_amd import _lib
+
+    lib = _lib.library()
+    device = torch.device("cuda:0")
+    o, k = UNIQUE[shape]
+    gen = torch.Generator(device=device).manual_seed(o + k)
+    stacked, payloads = make_payloads(o, k, device, gen, copies)
+    ws = torch.zeros(lib.fx_w3_gemv_workspace_bytes(8, o, k) + 256, dtype=torch.uint8, device=device)
+    for m in (1, 2, 4, 8):
+        x = torch.randn(m, k, device=device, generator=gen).to(torch.bfloat16)
+        out = torch.empty(m, o, device=device, dtype=torch.bfloat16)
+        torch.cuda.synchronize()
+        for p in range(copies):
+            _lib.check(lib.fx_w3_gemv(x.data_ptr(), _lib.FX_BF16, payloads[p]["planes"].data_ptr(),
+                                      payloads[p]["scales"].data_ptr(), _lib.FX_F16, payloads[p]["zeros"].data_ptr(),
+                                      None, ws.data_ptr(), ws.numel(), out.data_ptr(), m, o, k, _lib.ARITH_STRUCTURAL,
+                                      _lib.stream_handle(device)), "fx_w3_gemv")
+        torch.cuda.synchronize()
+        print(f"# pmc-small-m {shape} M = {m} done", flush=True)
+
+
 def pmc_attention_target(layers=36, position=543, rounds=8):
     """Workload for ``rocprofv3 --pmc`` passes over the decode attention: Qwen3-8B
     heads (32 query / 8 KV heads of 128), the native decode's call
@@ -1447,6 +1474,8 @@ def main():
                         help="run the counter-collection workload of the decode attention")
     parser.add_argument("--summarize-counters", nargs="+", metavar="ARG",
                         help="NAME CSV [CSV ...]: every counter per dispatch of kernels matching NAME")
+    parser.add_argument("--pmc-small-m", metavar="SHAPE",
+                        help="run the small-M counter workload at one shape (q/o, k/v, gate/up or down)")
     parser.add_argument("--sweep-attention", action="store_true",
                         help="time every attention plan (keys per thread x head groups) at 513 and 544 keys")
     parser.add_argument("--sweep-fields", nargs="?", const="all", default=None, metavar="NAMES",
@@ -1469,6 +1498,9 @@ def main():
         return
     if args.pmc_attention:
         pmc_attention_target()
+        return
+    if args.pmc_small_m:
+        pmc_small_m_target(args.pmc_small_m)
         return
     if args.summarize_counters:
         summarize_counters(args.summarize_counters[1:], args.summarize_counters[0])
