@@ -1136,7 +1136,12 @@ def summarize_trace(csv_path, last):
     rows = []
     with open(csv_path, newline="") as f:
         for r in csv.DictReader(f):
-            rows.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"], r.get("Grid_Size_X", "")))
+            # the full grid: a strided-batch launch shares a kernel and grid x with
+            # its single-GEMV form and walks its payloads on grid y
+            grid = r.get("Grid_Size_X", "")
+            if r.get("Grid_Size_Y", "1") not in ("", "1") or r.get("Grid_Size_Z", "1") not in ("", "1"):
+                grid = f"{grid} x {r.get('Grid_Size_Y', '1')} x {r.get('Grid_Size_Z', '1')}"
+            rows.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"], grid))
     rows.sort()
     tail = rows[-last:]
     groups = defaultdict(list)
@@ -1145,7 +1150,7 @@ def summarize_trace(csv_path, last):
     span = (tail[-1][1] - tail[0][0]) / 1000.0
     busy = sum(sum(v) for v in groups.values())
     print(f"last {len(tail)} dispatches: span {span:.1f} us, kernel time {busy:.1f} us ({100 * busy / span:.1f}%)")
-    print("| kernel | grid (threads) | dispatches | total us | mean us | median us |")
+    print("| kernel | grid (threads; x, or x x y x z) | dispatches | total us | mean us | median us |")
     print("|---|---:|---:|---:|---:|---:|")
     for (name, grid), v in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
         print(f"| `{name}` | {grid} | {len(v)} | {sum(v):.1f} | {statistics.mean(v):.2f} | {statistics.median(v):.2f} |")
