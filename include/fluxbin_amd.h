@@ -420,7 +420,9 @@ int fx_hybrid_gemv(const void *x, int x_dtype, const uint8_t *codes, const float
  * in one launch: no single reference entry point; it replaces the reference
  * decode's separate m1_out calls for q_proj, k_proj, v_proj (or gate_proj,
  * up_proj) (deployment.py:168-179) and gives each row the bits of its own
- * fx_hybrid_gemv call.  codes, rows, sparse_codes and sparse_rows are the
+ * fx_hybrid_gemv call when both split K over the same number of workgroups (the
+ * decode shapes); otherwise the rows' fp32 partials are summed in another order.
+ * codes, rows, sparse_codes and sparse_rows are the
  * segments' arrays concatenated along O ([G, O_total, ...]); columns, indices
  * and sparse_columns hold one pointer per segment (its [G, 128, 2], [G, 8],
  * [G, 8, 2] arrays); segment_rows[s] is segment s's row count, a multiple of 16

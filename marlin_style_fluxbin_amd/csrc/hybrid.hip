@@ -47,9 +47,11 @@ constexpr int kHyMaxUnits = 4;           // staged batches per wave
 // The K reduction always runs in the order of eight K parts: batch b of a split
 // feeds virtual part b % 8, each part accumulates its batches in order, and the
 // eight part sums are added in part order.  A plan with NK < 8 waves per tile
-// keeps 8 / NK accumulator sets per wave, so every plan (tiles, K parts) gives
-// the same bits and a fused q|k|v launch matches the separate projections
-// whatever plan each one picks.
+// keeps 8 / NK accumulator sets per wave, so every plan (tiles, K parts) with the
+// same number of K splits gives the same bits, and a fused q|k|v launch matches
+// the separate projections whatever tiling each one picks.  Different K-split
+// counts (narrow modules at long K) sum the splits' fp32 partials in another
+// order.
 constexpr int kHyVirtualParts = 8;
 
 __device__ __forceinline__ int hy_exponent(float max_abs) {

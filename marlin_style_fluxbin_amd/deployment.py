@@ -361,8 +361,12 @@ class HybridSegmentsGemv:
     scales, refinement codes and refinement row scales are concatenated along O
     once here; their column scales, refinement indices and refinement column
     scales stay per module.  ``out`` is ``[1, sum(out_features)]``, the modules'
-    outputs side by side, each row with the bits of its module's own call.
-    Raises ``ValueError`` unless 1..4 GPU modules share ``in_features``, carry no
+    outputs side by side, each row with the bits of its module's own call when the
+    fused launch and that call split K over the same number of workgroups (the
+    decode shapes: one split each); where the split counts differ (narrow modules
+    at long K, e.g. two 256-row modules at K = 16384: 1 split fused, 4 alone) the
+    fp32 partials are summed in another order and rows agree to the output's last
+    bit or so.  Raises ``ValueError`` unless 1..4 GPU modules share ``in_features``, carry no
     bias, and (for several) have row counts that are multiples of 16."""
 
     MAX_SEGMENTS = 4

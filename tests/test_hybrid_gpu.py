@@ -221,6 +221,29 @@ def test_segments_launch_equals_separate_calls(gpu, widths, g):
         assert torch.equal(replay, out)
 
 
+def test_segments_launch_with_other_split_count_agrees_to_the_last_bit(gpu):
+    """Two 256-row modules at K = 16384: alone each splits K over 4 workgroups,
+    the fused 512-row launch over one, so the fp32 partials meet in another order
+    and the rows are not bit-identical; they agree within half a bf16 ulp of the
+    row (plus the fp32 sums' reassociation) and both meet the oracle bar."""
+    from marlin_style_fluxbin_amd import _lib
+
+    lib = _lib.library()
+    assert lib.fx_hybrid_gemv_workspace_bytes(256, 16384) > 0  # alone: split K
+    assert lib.fx_hybrid_gemv_workspace_bytes(512, 16384) == 0  # fused: one split
+    payloads = [_payload(256, 128, seed=41 + i) for i in range(2)]
+    modules = [d.PackedHybridLinear(p, kernel="v5_p1024").to(gpu) for p in payloads]
+    x = torch.randn(1, 128 * 128, generator=torch.Generator().manual_seed(6)).to(torch.bfloat16).to(gpu)
+    out = torch.full((1, 512), float("nan"), dtype=torch.bfloat16, device=gpu)
+    d.HybridSegmentsGemv(modules)(x, out)
+    with torch.inference_mode():
+        want = torch.cat([m(x) for m in modules], 1)
+    got, ref = out.float().cpu().numpy(), want.float().cpu().numpy()
+    assert np.all(np.abs(got - ref) <= 2 ** -8 * np.abs(ref) + 1e-6 * np.abs(ref).max())
+    for i, p in enumerate(payloads):
+        _check(out[:, 256 * i:256 * (i + 1)], _reference(x, p))
+
+
 def test_segments_argument_checks(gpu):
     from marlin_style_fluxbin_amd import _lib
 
