@@ -240,6 +240,18 @@ def bench_shape(o, k, device, steps, warmup, stream, min_bytes=320e6, min_copies
 
     graphs["fields"] = (capture(over([lambda p=p, f=f: field_call(p, f) for p, f in zip(payloads, fields)]),
                                 stream), copies)
+    # config 1's small-M variants on the field layout (fx_w3_gemv_fields_rows)
+    fom = {m: torch.empty(m, o, device=device, dtype=torch.bfloat16) for m in (2, 4, 8)}
+
+    def rows_call(p, f, m):
+        _lib.check(lib.fx_w3_gemv_fields_rows(xm[m].data_ptr(), _lib.dtype_code(xm[m].dtype), f.data_ptr(),
+                                              p["scales"].data_ptr(), _lib.dtype_code(p["scales"].dtype),
+                                              p["zeros"].data_ptr(), fom[m].data_ptr(), m, o, k,
+                                              _lib.stream_handle(device)), "fx_w3_gemv_fields_rows")
+
+    for m in (2, 4, 8):
+        graphs[f"fields M={m}"] = (capture(over([lambda p=p, f=f, m=m: rows_call(p, f, m)
+                                                 for p, f in zip(payloads, fields)]), stream), copies)
     # steady state: the same payloads walked by one launch (fx_w3_gemv_strided_batched),
     # planar and field layout -- the kernel without the per-launch cost
     fields_stacked = torch.stack(fields)
@@ -298,11 +310,19 @@ def bench_shape(o, k, device, steps, warmup, stream, min_bytes=320e6, min_copies
         raise RuntimeError("strided-batch GEMV differs from the single launch")
     small_m = {}
     for m in (2, 4, 8):
-        m_us = t[f"M={m}"]["us"]
+        gemvs[-1](xm[m], om[m])
+        rows_call(payloads[-1], fields[-1], m)
+        torch.cuda.synchronize()
+        if not torch.allclose(fom[m].float(), om[m].float(), rtol=2 ** -7,
+                              atol=1e-3 * float(om[m].float().abs().max())):
+            raise RuntimeError(f"field-layout M={m} GEMV disagrees with the planar GEMV")
+        m_us, f_us = t[f"M={m}"]["us"], t[f"fields M={m}"]["us"]
         m_bytes = algorithmic_bytes(o, k, m)
         small_m[f"M={m}"] = {"us": round(m_us, 3), "GBps": round(m_bytes / m_us / 1e3, 1),
                              "frac_hbm": round(m_bytes / m_us / 1e3 / HBM_PEAK_GBPS, 4),
-                             "algorithmic_bytes": m_bytes, "vs_M=1": round(m_us / t["w3"]["us"], 3)}
+                             "algorithmic_bytes": m_bytes, "vs_M=1": round(m_us / t["w3"]["us"], 3),
+                             "fields_us": round(f_us, 3), "fields_GBps": round(m_bytes / f_us / 1e3, 1),
+                             "fields_vs_planar": round(f_us / m_us, 3)}
     w3_us, fields_us, bf16_us, perm_us = t["w3"]["us"], t["fields"]["us"], t["bf16"]["us"], t["w3_perm"]["us"]
     decoded_us, table_us = t["w3_decoded"]["us"], t["table_decoded"]["us"]
     restore_us, restore_perm_us = t["restore"]["us"], t["restore_permuted"]["us"]
@@ -441,6 +461,84 @@ def fields_plan_sweep(device, stream, shapes=None, min_bytes=320e6, min_copies=5
                         "frac_hbm": {label: round(nbytes / (t["us"] * 1e3) / HBM_PEAK_GBPS, 4) for label, t in timing.items()}}
         print(f"# sweep {name}: {result[name]}", file=sys.stderr, flush=True)
         del graphs, fields, stacked, payloads
+        torch.cuda.empty_cache()
+    return result
+
+
+ROWS_ONLY_PLANS = [(1, 12, 2, 2), (1, 16, 2, 2)]
+ROWS_SHAPES = {"q/o": (4096, 4096), "k/v": (1024, 4096), "gate/up": (12288, 4096), "down": (4096, 12288)}
+
+
+def rows_sweep(device, stream, shapes=None, rows=(2, 4, 8), min_bytes=320e6, min_copies=50):
+    """µs per launch of M activation rows (config 1's small-M case) on the field
+    layout (fx_w3_gemv_fields_rows, every plan that takes the shape and the default
+    one) next to the planar fx_w3_gemv on the same payloads, graph-timed over
+    rotating payloads with the paired protocol; every plan's output is checked
+    bit-equal to the default plan's."""
+    import torch
+
+    from marlin_style_fluxbin_amd import W3Gemv, _lib
+
+    lib = _lib.library()
+    result = {}
+    for name, (o, k) in (shapes or ROWS_SHAPES).items():
+        gen = torch.Generator(device=device).manual_seed(o + 5 * k)
+        copies = max(min_copies, int(min_bytes // algorithmic_bytes(o, k)) + 1)
+        with torch.cuda.stream(stream):
+            stacked, payloads = make_payloads(o, k, device, gen, copies)
+            fields = torch.empty_like(stacked["planes"])
+            for p in range(copies):
+                _lib.check(lib.fx_w3_planes_to_fields(stacked["planes"][p].data_ptr(), fields[p].data_ptr(), o, k,
+                                                      _lib.stream_handle(device)), "planes_to_fields")
+            gemvs = [W3Gemv(p, perm_identity=True) for p in payloads]
+        torch.cuda.synchronize()
+        shape = {"O": o, "K": k, "copies": copies}
+        for m in rows:
+            with torch.cuda.stream(stream):
+                x = torch.randn(m, k, device=device, generator=gen).to(torch.bfloat16)
+                out = torch.empty(m, o, device=device, dtype=torch.bfloat16)
+            torch.cuda.synchronize()
+
+            def call(p, dst=out, x=x, m=m):
+                _lib.check(lib.fx_w3_gemv_fields_rows(x.data_ptr(), _lib.FX_BF16, fields[p].data_ptr(),
+                                                      payloads[p]["scales"].data_ptr(), _lib.FX_F16,
+                                                      payloads[p]["zeros"].data_ptr(), dst.data_ptr(), m, o, k,
+                                                      _lib.stream_handle(device)), "gemv_fields_rows")
+
+            graphs = {"planar": (capture(lambda x=x, out=out: [g(x, out) for g in gemvs], stream), copies)}
+            refs = {}
+            nb = k // 512
+            # a solo plan (one tile) restages per batch; the others
+            # hold every batch in LDS: 24 of four rows (eight rows past 8 batches
+            # run as chunks of four)
+            plans = [("default", (0, 0, 0, 0))] + [
+                (",".join(map(str, pl)), pl) for pl in FIELDS_PLANS + ROWS_ONLY_PLANS
+                if nb <= pl[3] * pl[0] * pl[1] and (pl[0] == 1 or nb <= 24)]
+            for label, plan in plans:
+                _lib.check(lib.fx_w3_fields_plan(*plan), "fields plan")
+                try:
+                    with torch.cuda.stream(stream):
+                        refs[label] = torch.full_like(out, float("nan"))
+                        call(0, refs[label])
+                        torch.cuda.synchronize()
+                        graphs[label] = (capture(lambda: [call(p) for p in range(copies)], stream), copies)
+                finally:
+                    _lib.check(lib.fx_w3_fields_plan(0, 0, 0, 0), "fields plan reset")
+            with torch.cuda.stream(stream):
+                planar = torch.empty_like(out)
+                gemvs[0](x, planar)
+            torch.cuda.synchronize()
+            same = all(torch.equal(r, refs["default"]) for r in refs.values())
+            # the two layouts sum in other orders: within the GEMV's output ulps
+            close = torch.allclose(refs["default"].float(), planar.float(), rtol=2 ** -7,
+                                   atol=1e-3 * float(planar.float().abs().max()))
+            timing = paired_graph_timing(graphs, stream, repeats=10)
+            shape[f"M={m}"] = {"bit_equal_plans": same, "close_to_planar": close,
+                               "us": {label: round(t["us"], 3) for label, t in timing.items()}}
+            print(f"# rows {name} M={m}: {shape[f'M={m}']}", file=sys.stderr, flush=True)
+            del graphs
+        result[name] = shape
+        del fields, stacked, payloads, gemvs
         torch.cuda.empty_cache()
     return result
 
@@ -1486,6 +1584,9 @@ def main():
     parser.add_argument("--sweep-fields", nargs="?", const="all", default=None, metavar="NAMES",
                         help="time every field-layout plan at the Qwen3-8B shapes (one JSON line); "
                              "optional comma list of shape names")
+    parser.add_argument("--sweep-rows", nargs="?", const="all", default=None, metavar="NAMES",
+                        help="time M = 2, 4, 8 rows on the field layout (every plan) against the planar "
+                             "kernel at the Qwen3-8B shapes (one JSON line); optional comma list of shapes")
     parser.add_argument("--summarize-trace", nargs=2, metavar=("CSV", "LAST"),
                         help="per-kernel summary of the last LAST dispatches of a kernel-trace CSV")
     args = parser.parse_args()
@@ -1535,6 +1636,14 @@ def main():
         names = list(SWEEP_SHAPES) if args.sweep_fields == "all" else args.sweep_fields.split(",")
         print(json.dumps(fields_plan_sweep(device, torch.cuda.Stream(device),
                                            {n: SWEEP_SHAPES[n] for n in names})), flush=True)
+        return
+    if args.sweep_rows:
+        import torch
+
+        device = torch.device("cuda:0")
+        names = list(ROWS_SHAPES) if args.sweep_rows == "all" else args.sweep_rows.split(",")
+        print(json.dumps(rows_sweep(device, torch.cuda.Stream(device), {n: ROWS_SHAPES[n] for n in names})),
+              flush=True)
         return
     if args.fused_ops:
         import torch

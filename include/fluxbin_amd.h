@@ -188,6 +188,17 @@ int fx_w3_planes_to_fields(const uint8_t *planes, uint8_t *fields, int O, int K,
  * arithmetic (fp32 accumulation of exact products; the sum order differs). */
 int fx_w3_gemv_fields(const void *x, int x_dtype, const uint8_t *fields, const void *scales, int scale_dtype,
                       const uint8_t *zeros, void *out, int O, int K, void *stream);
+/* Field-layout GEMV of M <= 8 activation rows (no single counterpart: the
+ * small-M route of w3_lut_deployment.py:327-333 on the bind-time field layout):
+ * out [M, O] = x [M, K] @ W.T, structural arithmetic.  One row is
+ * fx_w3_gemv_fields; more run the M-row kernel in one launch (a workgroup of
+ * several row tiles stages each batch of all its rows once for them; one of a
+ * single tile restages per batch, wave by wave), with each batch's products
+ * summed in batch order, so every plan of fx_w3_fields_plan gives the same
+ * bits.  For M > 1: K a multiple of 512 and at most 16384 under the default
+ * plans, O a multiple of 16. */
+int fx_w3_gemv_fields_rows(const void *x, int x_dtype, const uint8_t *fields, const void *scales, int scale_dtype,
+                           const uint8_t *zeros, void *out, int M, int O, int K, void *stream);
 /* Field-layout plans (no counterpart in the reference: benchmark sweeps and the
  * plan-independence tests).  Every field-layout launch of the calling thread
  * (fx_w3_gemv_fields, the FX_W3_FIELDS forms of fx_w3_gemv_swiglu / _residual /
@@ -195,9 +206,11 @@ int fx_w3_gemv_fields(const void *x, int x_dtype, const uint8_t *fields, const v
  * call: tiles > 0 the shared-staging kernel with tiles 16-row tiles x parts K
  * parts per workgroup, prefetch batches (512 columns) in flight and stage staged
  * batches per wave -- one of (1,8,1,1) (1,8,3,3) (2,4,2,1) (3,4,2,1) (4,2,4,1),
- * else FX_EINVAL, and a launch whose shape the plan cannot run (O % 16, K % 512,
- * more batches than it stages) fails with FX_EINVAL; tiles <= 0 the one-tile
- * kernel, the default.  Every plan gives the same bits.  Thread-local state. */
+ * or (1,12,2,2) (1,16,2,2) for fx_w3_gemv_fields_rows only, else FX_EINVAL, and
+ * a launch whose shape the plan cannot run (O % 16, K % 512, more batches than
+ * it stages, an M-row-only plan on one row) fails with FX_EINVAL; tiles <= 0 the
+ * one-tile kernel (fx_w3_gemv_fields_rows: its default plans), the default.
+ * Every plan gives the same bits.  Thread-local state. */
 int fx_w3_fields_plan(int tiles, int parts, int prefetch, int stage);
 /* Structural MFMA path with an explicit tiling (benchmark sweeps): waves per
  * workgroup in {4,8}, 4-group batches kept in flight per wave in {1,2},

@@ -15,7 +15,7 @@ from pathlib import Path
 import torch
 
 LIBRARY_PATH = Path(__file__).resolve().parent / "libfluxbin_amd.so"
-ABI_VERSION = 17
+ABI_VERSION = 18
 PAYLOAD_PLANAR, PAYLOAD_FIELDS = 0, 1  # FX_W3_PLANAR / FX_W3_FIELDS
 
 FX_F32, FX_F16, FX_BF16 = 0, 1, 2
@@ -47,6 +47,7 @@ SIGNATURES: dict[str, tuple] = {
     "fx_w3_planes_to_fields": (_i, [_p, _p, _i, _i, _p]),
     "fx_w3_gemv_fields": (_i, [_p, _i, _p, _p, _i, _p, _p, _i, _i, _p]),
     "fx_w3_fields_plan": (_i, [_i, _i, _i, _i]),
+    "fx_w3_gemv_fields_rows": (_i, [_p, _i, _p, _p, _i, _p, _p, _i, _i, _i, _p]),
     "fx_w3_gemv_config_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _i, _i]),
     "fx_w3_gemv_config": (_i, [_p, _i, _p, _p, _i, _p, _p, _p, _sz, _p, _i, _i, _i, _i, _i, _i, _i, _p]),
     "fx_w3_restore": (_i, [_p, _p, _i, _p, _p, _p, _i, _i, _i, _p]),

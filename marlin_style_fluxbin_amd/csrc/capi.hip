@@ -568,7 +568,7 @@ bool two_base_config(int O, int G, int waves, int prefetch, int groups_per_split
 
 extern "C" {
 
-int fx_abi_version(void) { return 17; }
+int fx_abi_version(void) { return 18; }
 
 const char* fx_last_error(void) { return g_error; }
 
@@ -736,6 +736,7 @@ constexpr size_t kWideMaxLds = 64 * 1024;
 
 // Why a shared-staging plan cannot run a shape (null: it can).
 const char* wide_plan_misfit(const fx::WidePlan& p, int O, int G, bool perm) {
+  if (!fx::wide_plan_instantiated(p)) return "the plan has only the M-row form (fx_w3_gemv_fields_rows)";
   if (O % 16 || G % 4) return "it needs O % 16 == 0 and K % 512 == 0";
   if (G / 4 > p.stage * p.tiles * p.parts) return "K has more batches than its waves stage";
   if (fx::wide_lds_bytes(p.tiles, G, perm) > kWideMaxLds) return "its LDS would exceed 64 KB";
@@ -782,8 +783,70 @@ int run_fields(const MfmaArgs& base, int x_dtype, int scale_dtype, bool normin, 
   return check_launch("w3_mfma_kernel (field layout)");
 }
 
+// Field-layout GEMV of M <= 8 activation rows.  One row: run_fields.  More: the
+// M-row kernel (rows padded to MB = 2, 4 or 8); under a plan of several tiles, in
+// chunks of four rows where eight rows' staged operands would not fit its LDS
+// (K > 4096).  Default plan (measured at the Qwen3-8B shapes): for four or eight
+// rows, three tiles x four K parts sharing each staged batch where the row tiles
+// fill every CU three times over; else one tile x eight parts up to K = 4096 (a
+// batch each), one tile x sixteen parts past it (K <= 16384).
+fx::WidePlan default_rows_plan(int O, int G, int mb) {
+  const int tiles = O / 16, nb = G / 4;
+  if (mb >= 4 && tiles >= 3 * device_cu_count() && nb <= 8) return {3, 4, 2, 1};
+  if (nb <= 8) return {1, 8, 1, 1};
+  return {1, 16, 2, 2};
+}
+
+const char* rows_plan_misfit(const fx::WidePlan& p, int O, int G, int mb) {
+  if (O % 16 || G % 4) return "it needs O % 16 == 0 and K % 512 == 0";
+  if (G / 4 > p.stage * p.tiles * p.parts) return "K has more batches than its waves stage";
+  if (!fx::rows_plan_solo(p) && G / 4 > fx::rows_batch_limit(mb))
+    return "K has more batches than its LDS holds for these rows";
+  if (16 * p.tiles * mb > 64 * p.tiles * p.parts) return "too few waves for one thread per output value";
+  return nullptr;
+}
+
+int fx_w3_gemv_fields_rows(const void* x, int x_dtype, const uint8_t* fields, const void* scales, int scale_dtype,
+                           const uint8_t* zeros, void* out, int M, int O, int K, void* stream) {
+  int rc = validate_payload(x, x_dtype, fields, scales, scale_dtype, M, O, K, FX_ARITH_STRUCTURAL);
+  if (rc) return rc;
+  if (!out) return fail(FX_EINVAL, "out must be non-null");
+  if (M < 1 || M > 8) return fail(FX_EINVAL, "M must be in [1, 8], got %d", M);
+  MfmaArgs a{};
+  a.planes = fields;
+  a.scales = static_cast<const uint16_t*>(scales);
+  a.zeros = zeros;
+  a.O = O;
+  a.G = K / 128;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (M == 1) {
+    a.x = static_cast<const uint16_t*>(x);
+    a.out = static_cast<uint16_t*>(out);
+    return run_fields(a, x_dtype, scale_dtype, false, s);
+  }
+  for (int done = 0; done < M;) {
+    int mb = M - done <= 2 ? 2 : M - done <= 4 ? 4 : 8;
+    const fx::WidePlan w = g_fields_plan.tiles > 0 ? g_fields_plan : default_rows_plan(O, a.G, mb);
+    // eight rows' operands of every batch exceed the LDS: chunks of four
+    if (mb == 8 && !fx::rows_plan_solo(w) && a.G / 4 > fx::rows_batch_limit(8)) mb = 4;
+    const int rows = std::min(mb, M - done);
+    if (const char* why = rows_plan_misfit(w, O, a.G, mb))
+      return fail(FX_EINVAL, "field-layout plan (%d, %d, %d, %d) cannot run %d rows of O = %d, K = %d: %s", w.tiles,
+                  w.parts, w.prefetch, w.stage, mb, O, K, why);
+    a.x = static_cast<const uint16_t*>(x) + size_t(done) * K;
+    a.out = static_cast<uint16_t*>(out) + size_t(done) * O;
+    a.row_blocks = (O / 16 + w.tiles - 1) / w.tiles;
+    if (!fx::dispatch_fields_rows(w, mb, x_dtype, scale_dtype, a, rows, dim3(a.row_blocks), s))
+      return fail(FX_EINVAL, "no M-row field-layout kernel for this plan and dtype");
+    if ((rc = check_launch("w3_fields_rows_kernel"))) return rc;
+    done += rows;
+  }
+  return FX_OK;
+}
+
 int fx_w3_fields_plan(int tiles, int parts, int prefetch, int stage) {
-  if (tiles > 0 && !fx::wide_plan_instantiated(fx::WidePlan{tiles, parts, prefetch, stage}))
+  if (tiles > 0 && !fx::wide_plan_instantiated(fx::WidePlan{tiles, parts, prefetch, stage}) &&
+      !fx::rows_plan_instantiated(fx::WidePlan{tiles, parts, prefetch, stage}))
     return fail(FX_EINVAL, "no shared-staging kernel for plan (%d, %d, %d, %d)", tiles, parts, prefetch, stage);
   g_fields_plan = tiles > 0 ? fx::WidePlan{tiles, parts, prefetch, stage} : fx::WidePlan{tiles < 0 ? -1 : 0, 0, 0, 0};
   return FX_OK;

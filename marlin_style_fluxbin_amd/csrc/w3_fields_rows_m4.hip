@@ -1,0 +1,10 @@
+// Instantiations of the shared-staging field-layout kernel for 4 activation rows.
+#include "w3_fields_wide.h"
+
+namespace fx {
+bool dispatch_fields_rows_m4(const WidePlan& p, int xdt, int sdt, const MfmaArgs& a, int M, dim3 grid, hipStream_t s) {
+  if (xdt == kBF16) return dispatch_fields_rows_mb<4, kBF16>(p, sdt, a, M, grid, s);
+  if (xdt == kF16) return dispatch_fields_rows_mb<4, kF16>(p, sdt, a, M, grid, s);
+  return false;
+}
+}  // namespace fx

@@ -342,6 +342,239 @@ __global__ __launch_bounds__(T * P * 64) void w3_fields_wide_kernel(
   }
 }
 
+// The same plan structure for MB activation rows (MB in {2, 4, 8}; plain
+// epilogue, identity column order): a workgroup stages each batch of all its
+// rows once for its T tiles, which is where sharing pays most -- eight rows cost
+// a wave about as many staging instructions as its dequant and multiplies --
+// and each wave runs ceil(MB / 4) MFMA chains on one dequantized A operand (rows
+// 4h .. 4h+3 in chain h), as the one-tile kernel does for several rows.  Rows
+// m >= M load zeros and are not stored.
+//
+// Order of the sums: each batch's products reduce to one fp32 partial per output
+// (its four group slots meet through lanes c^1, c^2) and the partials add in
+// batch order, so any assignment of batches to waves -- every plan -- gives the
+// same bits.  Part p of a tile takes batches p, p + P, ...; with one tile (a
+// "solo" plan) wave w takes batches w, w + P, ..., exactly the ones it stages,
+// so it skips the workgroup barrier and restages one LDS slot of its own per
+// batch: any K the plan's waves stage runs with eight rows.  Other plans stage
+// every batch into LDS before the barrier (the host checks ceil(G / 4) against
+// both limits, the plan's staging and rows_max_batches).
+template <int MB>
+constexpr int rows_max_batches() { return MB == 8 ? 8 : 24; }  // rows_batch_limit
+
+template <int T, int P, int S, int MB>
+struct RowsShared {
+  static constexpr int NB = T == 1 ? P : T * P * S < rows_max_batches<MB>() ? T * P * S : rows_max_batches<MB>();
+  static constexpr int NR = T == 1 ? P * S : NB;  // batches a launch can hold (the host's limits)
+  u32x4_t bst[NB][4 * kStageStride<MB>];
+  u32x4_t bzero[16 * MB];
+  float gsum[NB][4 * MB];
+  int gexp[NB][4 * MB];
+  float red[NR][16 * T * MB];
+};
+
+template <int T, int P, int PD, int S, int MB, int XDT, int SDT>
+__global__ __launch_bounds__(T * P * 64) void w3_fields_rows_kernel(
+    const uint16_t* __restrict__ x, const uint8_t* __restrict__ fields, const uint16_t* __restrict__ scales,
+    const uint8_t* __restrict__ zeros, uint16_t* __restrict__ out, int M, int O, int G, int row_blocks) {
+  constexpr int NW = T * P, NH = (MB + 3) / 4;
+  constexpr bool SOLO = T == 1;
+  constexpr int JMAX = SOLO ? S : T * S;  // batches per wave (the host checks ceil(G / 4) <= NW S)
+  static_assert(16 * T * MB <= 64 * NW, "one thread per output value");
+  asm volatile("" ::"s"(x), "s"(fields), "s"(scales), "s"(zeros), "s"(out), "s"(M), "s"(O), "s"(G), "s"(row_blocks));
+  __shared__ RowsShared<T, P, S, MB> sh;
+  const int nbatch = (G + 3) >> 2;
+  const int t = threadIdx.x, lane = t & 63, wave = wave_index();
+  const int part = wave % P, tile = wave / P;
+  const int K = G * 128;
+  const int row_base = xcd_local_index8(blockIdx.x, row_blocks) * (16 * T);
+  const int row0 = row_base + 16 * tile;
+  const unsigned zero_default = zeros ? 0u : 0x04040404u;
+
+  const auto rp = buffer_resource(fields, size_t(G) * 3 * O * 16);
+  const auto rs = buffer_resource(scales, size_t(G) * O * 2);
+  const auto rz = buffer_resource(zeros ? (const void*)zeros : (const void*)scales, zeros ? size_t(G) * O : 0);
+  const auto rx = buffer_resource(x, size_t(M) * K * 2);  // rows past M read zeros
+
+  const int r = lane & 15, kb = lane >> 4, c = lane & 15, cslot = c & 3, cm = c >> 2;
+
+  // staging loads of batch wave + NW i, all rows
+  u32x4_t sx[S][MB];
+#pragma unroll
+  for (int i = 0; i < S; ++i) {
+    const int b = wave + NW * i;
+    const int g = 4 * b + kb;
+    const bool real = b < nbatch && g < G;
+#pragma unroll
+    for (int m = 0; m < MB; ++m) sx[i][m] = load_b128(rx, real && m < M ? (m * K + g * 128 + 8 * r) * 2 : kOutOfRange, 0);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // this wave's batches: c0 + CS j
+  constexpr int CS = SOLO ? NW : P;
+  const int c0 = SOLO ? wave : part;
+
+  // the scalar offset is not range-checked: live loads are in bounds by the
+  // plan's contract (O % 16 == 0, G % 4 == 0), tiles past O issue none
+  const int plane_stride = O * 16;
+  const int p_lane = (kb * 3 * O + row0 + r) * 16;
+  const int e_lane = cslot * O + row0 + 4 * kb;
+  const bool tile_on = row0 < O;
+  auto issue = [&](int batch, BatchLoads<1, 1>& L) __attribute__((always_inline)) {
+    const bool on = batch < nbatch && tile_on;
+    const int pv = on ? p_lane : kOutOfRange;
+    const int ps = on ? batch * 4 * 3 * plane_stride : 0;
+    L.w[0][0] = load_b128_stream(rp, pv, ps);
+    L.w[0][1] = load_b128_stream(rp, pv, ps + plane_stride);
+    L.w[0][2] = load_b128_stream(rp, pv, ps + 2 * plane_stride);
+    __builtin_amdgcn_sched_barrier(0);
+    const uint2 s4 = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rs, on ? 2 * e_lane : kOutOfRange,
+                                                                                     on ? batch * 4 * O * 2 : 0, 0));
+    L.s[0][0] = s4.x;
+    L.s[0][1] = s4.y;
+    L.z[0] = __builtin_amdgcn_raw_buffer_load_b32(rz, on ? e_lane : kOutOfRange, on ? batch * 4 * O : 0, 0);
+  };
+
+  BatchLoads<1, 1> ring[PD];
+#pragma unroll
+  for (int i = 0; i < PD; ++i) issue(c0 + CS * i, ring[i]);
+  __builtin_amdgcn_sched_barrier(0);
+
+  // the staged operands of the wave's i-th staged batch, all rows, into LDS slot `slot`
+  auto stage = [&](int i, int slot) __attribute__((always_inline)) {
+#pragma unroll
+    for (int m = 0; m < MB; ++m) {
+      const unsigned xw[4] = {sx[i][m].x, sx[i][m].y, sx[i][m].z, sx[i][m].w};
+      float v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = to_f32<XDT>(uint16_t(xw[j >> 1] >> (16 * (j & 1))));
+      u32x4_t o;
+      float sm;
+      int ge;
+      stage_fields8(v, r, o, sm, ge);
+      sh.bst[slot][kb * kStageStride<MB> + r * MB + m] = o;
+      if (r == 0) {
+        sh.gsum[slot][kb * MB + m] = sm;
+        sh.gexp[slot][kb * MB + m] = ge;
+      }
+    }
+  };
+  // a wave's own LDS writes and reads stay in program order (LDS executes a
+  // wave's instructions in order; this keeps the compiler from moving them)
+  auto wave_order = []() __attribute__((always_inline)) {
+    __builtin_amdgcn_wave_barrier();
+    asm volatile("" ::: "memory");
+  };
+
+  if constexpr (SOLO) {
+    for (int i = lane; i < 16 * MB; i += 64) sh.bzero[i] = u32x4_t{0u, 0u, 0u, 0u};  // every wave: the same zeros
+    wave_order();
+  } else {
+    for (int i = lane; i < 16 * MB; i += 64)
+      if (wave == 0) sh.bzero[i] = u32x4_t{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int i = 0; i < S; ++i) {
+      const int b = wave + NW * i;
+      if (b < nbatch && b < RowsShared<T, P, S, MB>::NB) stage(i, b);
+    }
+    __syncthreads();
+  }
+
+  // chain h: activation rows 4h .. 4h+3 sit in the D columns (column c = slot + 4 row)
+  int rmc[NH];
+  bool data[NH];
+#pragma unroll
+  for (int h = 0; h < NH; ++h) {
+    const int row = cm + 4 * h;
+    rmc[h] = row < MB ? row : 0;
+    data[h] = cslot == kb && row < MB;
+  }
+  // one batch: its products, reduced over the four group slots, into red[b]
+  auto consume = [&](int b, int slot, const BatchLoads<1, 1>& L) __attribute__((always_inline)) {
+    const u32x4_t* bsrc[NH];
+#pragma unroll
+    for (int h = 0; h < NH; ++h) bsrc[h] = (data[h] ? &sh.bst[slot][kb * kStageStride<MB>] : sh.bzero) + rmc[h];
+    f32x4_t d[NH];
+#pragma unroll
+    for (int h = 0; h < NH; ++h) d[h] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int word = 0; word < 4; ++word) {
+      u32x4_t a[4];
+      dequant_fields(L.w[0][0][word], L.w[0][1][word], L.w[0][2][word], a);
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int h = 0; h < NH; ++h)
+          d[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a[s]),
+                                                      __builtin_bit_cast(f16x8_t, bsrc[h][(4 * word + s) * MB]), d[h],
+                                                      0, 0, 0);
+    }
+    const unsigned zw = L.z[0] | zero_default;
+#pragma unroll
+    for (int h = 0; h < NH; ++h) {
+      const float sxv = sh.gsum[slot][cslot * MB + rmc[h]];
+      const int fev = sh.gexp[slot][cslot * MB + rmc[h]];
+      float acc[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const unsigned sbits = (j & 1) ? (L.s[0][j >> 1] >> 16) : (L.s[0][j >> 1] & 0xffffu);
+        const float se = to_f32<SDT>(uint16_t(sbits)), zf = float((zw >> (8 * j)) & 0xffu);
+        float a = accumulate_group(0.f, se, zf, d[h][j], fev, sxv);
+        a += dpp_move<kDppXor1>(a);
+        a += dpp_move<kDppXor2>(a);
+        acc[j] = a;
+      }
+      // lanes with slot 0 hold rows 4 kb + j of the tile, activation row cm + 4h
+      if (cslot == 0 && cm + 4 * h < MB) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) sh.red[b][(16 * tile + 4 * kb + j) * MB + cm + 4 * h] = acc[j];
+      }
+    }
+  };
+
+#pragma unroll
+  for (int j = 0; j < JMAX; ++j) {
+    const int b = c0 + CS * j;
+    if (b < nbatch) {
+      if constexpr (SOLO) {
+        stage(j, wave);
+        wave_order();
+      }
+      consume(b, SOLO ? wave : b, ring[j % PD]);
+      if constexpr (SOLO) wave_order();
+      issue(c0 + CS * (j + PD), ring[j % PD]);
+    }
+  }
+  __syncthreads();
+
+  if (t < 16 * T * MB) {
+    float total = 0.f;
+    for (int b = 0; b < nbatch; ++b) total += sh.red[b][t];
+    const int m = t % MB, orow = row_base + t / MB;
+    if (orow < O && m < M) out[size_t(m) * O + orow] = from_f32<XDT>(total);
+  }
+}
+
+template <int T, int P, int PD, int S, int MB, int XDT>
+bool fields_rows_sdt(int sdt, const MfmaArgs& a, int M, dim3 grid, hipStream_t s) {
+#define FX_ROWS_LAUNCH(SDT)                                                                                     \
+  hipLaunchKernelGGL((w3_fields_rows_kernel<T, P, PD, S, MB, XDT, SDT>), grid, dim3(T * P * 64), 0, s, a.x, a.planes, \
+                     a.scales, a.zeros, a.out, M, a.O, a.G, a.row_blocks)
+  if (sdt == kF16) { FX_ROWS_LAUNCH(kF16); return true; }
+  if (sdt == kBF16) { FX_ROWS_LAUNCH(kBF16); return true; }
+#undef FX_ROWS_LAUNCH
+  return false;
+}
+
+template <int MB, int XDT>
+bool dispatch_fields_rows_mb(const WidePlan& p, int sdt, const MfmaArgs& a, int M, dim3 grid, hipStream_t s) {
+#define FX_ROWS_CASE(T, P, PD, S) \
+  if (p.tiles == T && p.parts == P && p.prefetch == PD && p.stage == S) return fields_rows_sdt<T, P, PD, S, MB, XDT>(sdt, a, M, grid, s);
+  FX_ROWS_PLANS(FX_ROWS_CASE)
+#undef FX_ROWS_CASE
+  return false;
+}
+
 // mode: 0 plain (identity order), 1 normalising prologue, 2 permuted columns.
 template <int T, int P, int PD, int S, int XDT, int SDT>
 void launch_fields_wide(int mode, const MfmaArgs& a, dim3 grid, hipStream_t s) {

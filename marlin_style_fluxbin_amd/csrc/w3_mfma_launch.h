@@ -125,6 +125,32 @@ inline size_t wide_lds_bytes(int T, int G, bool perm) {
   return nb * kWideStage * 16 + 16 * 16 + nb * 4 * 8 + size_t(kWideVirtualWaves) * 16 * T * 4 +
          (perm ? size_t(G) * 128 * 2 : 0);
 }
+// The M-row form (w3_fields_rows_kernel): MB = 2, 4 or 8 activation rows of
+// which the first M are live, plain epilogue, identity order; the same plans and
+// two more of one tile (12 and 16 parts, the M-row form only).  Static LDS for at
+// most rows_batch_limit(MB) batches (K <= 512 * limit), except under a solo plan
+// (one tile), where each wave restages one slot of its own and only the plan's
+// staging bounds K.
+#define FX_ROWS_PLANS(X) FX_WIDE_PLANS(X) X(1, 12, 2, 2) X(1, 16, 2, 2)
+inline bool rows_plan_instantiated(const WidePlan& p) {
+#define FX_ROWS_IS(T, P, PD, S) \
+  if (p.tiles == T && p.parts == P && p.prefetch == PD && p.stage == S) return true;
+  FX_ROWS_PLANS(FX_ROWS_IS)
+#undef FX_ROWS_IS
+  return false;
+}
+inline int rows_batch_limit(int mb) { return mb == 8 ? 8 : 24; }
+inline bool rows_plan_solo(const WidePlan& p) { return p.tiles == 1; }
+bool dispatch_fields_rows_m2(const WidePlan& p, int xdt, int sdt, const MfmaArgs& a, int M, dim3 grid, hipStream_t s);
+bool dispatch_fields_rows_m4(const WidePlan& p, int xdt, int sdt, const MfmaArgs& a, int M, dim3 grid, hipStream_t s);
+bool dispatch_fields_rows_m8(const WidePlan& p, int xdt, int sdt, const MfmaArgs& a, int M, dim3 grid, hipStream_t s);
+inline bool dispatch_fields_rows(const WidePlan& p, int mb, int xdt, int sdt, const MfmaArgs& a, int M, dim3 grid,
+                                 hipStream_t s) {
+  if (mb == 2) return dispatch_fields_rows_m2(p, xdt, sdt, a, M, grid, s);
+  if (mb == 4) return dispatch_fields_rows_m4(p, xdt, sdt, a, M, grid, s);
+  if (mb == 8) return dispatch_fields_rows_m8(p, xdt, sdt, a, M, grid, s);
+  return false;
+}
 bool dispatch_fields_wide_bf16(const WidePlan& p, int sdt, int mode, const MfmaArgs& a, dim3 grid, hipStream_t s);
 bool dispatch_fields_wide_f16(const WidePlan& p, int sdt, int mode, const MfmaArgs& a, dim3 grid, hipStream_t s);
 inline bool dispatch_fields_wide(const WidePlan& p, int xdt, int sdt, int mode, const MfmaArgs& a, dim3 grid,

@@ -61,6 +61,7 @@ DEFAULTS = {
                                        zeros_stride=256, out_stride=128, batch=4),
     "fx_w3_gemv_fields": dict(W3, fields=D),
     "fx_w3_fields_plan": dict(tiles=3, parts=4, prefetch=2, stage=1),
+    "fx_w3_gemv_fields_rows": dict(W3, fields=D, M=8, O=128, K=1024),
     "fx_decode_attention_plan": dict(keys_per_thread=2, head_groups=2),
     "fx_w3_gemv_config": dict(W3, waves=8, prefetch=1, tiles=1),
     "fx_w3_restore": dict(planes=D, scales=D, scale_dtype=2, zeros=None, perm=None, weight=D, weight_dtype=2,
@@ -185,6 +186,10 @@ CASES = [
     ("fx_w3_fields_plan", dict(prefetch=3), "no shared-staging kernel"),
     ("fx_w3_fields_plan", dict(tiles=1, parts=8, prefetch=2, stage=2), "no shared-staging kernel"),
     ("fx_decode_attention_plan", dict(keys_per_thread=3), "keys_per_thread must be 0 (default), 1, 2 or 4"),
+    ("fx_w3_gemv_fields_rows", dict(M=9), "M must be in [1, 8]"),
+    ("fx_w3_gemv_fields_rows", dict(out=None), "out must be non-null"),
+    ("fx_w3_gemv_fields_rows", dict(O=120), "O % 16 == 0"),
+    ("fx_w3_gemv_fields_rows", dict(K=640), "K % 512 == 0"),
     ("fx_decode_attention_plan", dict(head_groups=8), "head_groups must be 0 (default), 1, 2 or 4"),
     ("fx_w3_gemv_fields", dict(fields=D + 8), "16-byte aligned"),
     # explicit tilings

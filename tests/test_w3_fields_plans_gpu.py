@@ -243,3 +243,63 @@ def test_wide_plan_matches_oracle_and_refuses_misfits(gpu):
                                    _lib.FX_F16, big["zeros"].data_ptr(), ob.data_ptr(), 256, 12288,
                                    _lib.stream_handle(gpu))
         assert rc == 1 and "more batches" in lib.fx_last_error().decode()
+    with fields_plan((1, 16, 2, 2)):  # an M-row plan only: the one-row call refuses it
+        rc = lib.fx_w3_gemv_fields(x.to(gpu).data_ptr(), _lib.FX_BF16, dl["fields"].data_ptr(), dl["scales"].data_ptr(),
+                                   _lib.FX_F16, dl["zeros"].data_ptr(), out.data_ptr(), o, k, _lib.stream_handle(gpu))
+        assert rc == 1 and "only the M-row form" in lib.fx_last_error().decode()
+
+
+ROWS_PLANS = PLANS + [(1, 12, 2, 2), (1, 16, 2, 2)]
+
+
+def rows_fit(plan, k, m):
+    """Whether fx_w3_gemv_fields_rows takes (k, m) under `plan`: the waves stage
+    every batch, and a plan of several tiles holds every batch of a launch's rows
+    in LDS (8 of eight rows, 24 of four; eight rows run as chunks of four where
+    they do not fit), where a solo plan (one tile) restages per batch."""
+    t, p, _, st = plan
+    nb, solo = k // 512, t == 1
+    mb = 2 if m <= 2 else 4 if m <= 4 else 8
+    if mb == 8 and not solo and nb > 8:
+        mb = 4
+    return nb <= st * t * p and (solo or nb <= (8 if mb == 8 else 24))
+
+
+@pytest.mark.parametrize("o,k,m", [(768, 4096, 2), (768, 4096, 3), (768, 4096, 8), (1040, 2048, 5), (4096, 4096, 8),
+                                   (256, 12288, 4), (256, 12288, 8), (12288, 4096, 8), (512, 1024, 6)])
+@pytest.mark.parametrize("xdtype,scale_dtype,zeros", [(torch.bfloat16, torch.float16, True),
+                                                       (torch.float16, torch.bfloat16, False)])
+def test_rows_gemv_matches_oracle_and_plans(gpu, o, k, m, xdtype, scale_dtype, zeros):
+    """fx_w3_gemv_fields_rows (M = 2..8 on the field layout): every row within the
+    bar of the one-row field kernel (half an ulp of the float64 oracle plus 3e-5
+    of the largest output), rows past M untouched, and every plan that takes the
+    shape bit-identical to the default one (chunks of four rows where eight rows'
+    staged operands do not fit, K = 12288)."""
+    print(f"rows {o}x{k} M={m} {xdtype}", flush=True)
+    layout, dl = _payload(gpu, o, k, seed=o + k + m, scale_dtype=scale_dtype, zeros=zeros)
+    x = torch.randn(m, k, generator=torch.Generator().manual_seed(m + o)).to(xdtype)
+    lib = _lib.library()
+
+    def run():
+        out = torch.full((m + 1, o), float("nan"), dtype=xdtype, device=gpu)
+        _lib.check(lib.fx_w3_gemv_fields_rows(x.to(gpu).data_ptr(), _lib.dtype_code(xdtype), dl["fields"].data_ptr(),
+                                              dl["scales"].data_ptr(), _lib.dtype_code(scale_dtype),
+                                              _lib.ptr(dl.get("zeros")), out.data_ptr(), m, o, k,
+                                              _lib.stream_handle(gpu)), "gemv_fields_rows")
+        torch.cuda.synchronize()
+        return out
+
+    want = run()
+    assert torch.isnan(want[m].float()).all()  # the row past M is not written
+    exact = w3.matvec_exact(x.float().numpy(), oracle_layout(layout))
+    tag = "bf16" if xdtype == torch.bfloat16 else "f16"
+    assert_half_ulp(want[:m].float().cpu().numpy(), exact, tag, rel_slack=3e-5, what=f"rows {o}x{k} M={m}")
+    ran = 0
+    for plan in ROWS_PLANS:
+        if not rows_fit(plan, k, m):
+            continue
+        with fields_plan(plan):
+            got = run()
+        assert torch.equal(got[:m], want[:m]), plan
+        ran += 1
+    assert ran > 0
