@@ -1351,7 +1351,8 @@ def summarize_counters(csv_paths, name_filter):
 def pmc_small_m_target(shape, copies=24):
     """Workload for ``rocprofv3`` passes over the small-M GEMV (config 1): the
     planar ``fx_w3_gemv`` at one Qwen3-8B shape for M = 1, 2, 4, 8 (the default
-    plans), ``copies`` rotating payloads each, a progress line per M."""
+    plans), then the field layout's ``fx_w3_gemv_fields_rows`` for M = 2, 4, 8 on
+    the same payloads, ``copies`` rotating payloads each, a progress line per M."""
     import torch
 
     from marlin_style_fluxbin_amd import _lib
@@ -1373,6 +1374,21 @@ def pmc_small_m_target(shape, copies=24):
                                       _lib.stream_handle(device)), "fx_w3_gemv")
         torch.cuda.synchronize()
         print(f"# pmc-small-m {shape} M = {m} done", flush=True)
+    fields = torch.empty_like(stacked["planes"])
+    for p in range(copies):
+        _lib.check(lib.fx_w3_planes_to_fields(stacked["planes"][p].data_ptr(), fields[p].data_ptr(), o, k,
+                                              _lib.stream_handle(device)), "fx_w3_planes_to_fields")
+    for m in (2, 4, 8):
+        x = torch.randn(m, k, device=device, generator=gen).to(torch.bfloat16)
+        out = torch.empty(m, o, device=device, dtype=torch.bfloat16)
+        torch.cuda.synchronize()
+        for p in range(copies):
+            _lib.check(lib.fx_w3_gemv_fields_rows(x.data_ptr(), _lib.FX_BF16, fields[p].data_ptr(),
+                                                  payloads[p]["scales"].data_ptr(), _lib.FX_F16,
+                                                  payloads[p]["zeros"].data_ptr(), out.data_ptr(), m, o, k,
+                                                  _lib.stream_handle(device)), "fx_w3_gemv_fields_rows")
+        torch.cuda.synchronize()
+        print(f"# pmc-small-m {shape} field rows M = {m} done", flush=True)
 
 
 def pmc_attention_target(layers=36, position=543, rounds=8):
