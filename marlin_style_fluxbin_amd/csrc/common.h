@@ -81,12 +81,22 @@ __device__ __forceinline__ float row16_sum(float v) {
   return v;
 }
 
+// row16_max takes magnitudes only (non-negative, not NaN: every caller forms
+// them with fmaxf from 0, which drops NaN).  Their bit patterns order as the
+// values do, so an unsigned max of the bits is the float max -- one DPP-combined
+// integer instruction per step, where a float max first canonicalises its DPP
+// operand (three more instructions per step).
+template <int CTRL>
+__device__ __forceinline__ unsigned dpp_move_u(unsigned v) {
+  return unsigned(__builtin_amdgcn_update_dpp(0, int(v), CTRL, 0xf, 0xf, false));
+}
 __device__ __forceinline__ float row16_max(float v) {
-  v = fmaxf(v, dpp_move<kDppXor1>(v));
-  v = fmaxf(v, dpp_move<kDppXor2>(v));
-  v = fmaxf(v, dpp_move<kDppHalfMirror>(v));
-  v = fmaxf(v, dpp_move<kDppMirror>(v));
-  return v;
+  unsigned u = __float_as_uint(v);
+  u = max(u, dpp_move_u<kDppXor1>(u));
+  u = max(u, dpp_move_u<kDppXor2>(u));
+  u = max(u, dpp_move_u<kDppHalfMirror>(u));
+  u = max(u, dpp_move_u<kDppMirror>(u));
+  return __uint_as_float(u);
 }
 
 typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
