@@ -26,6 +26,13 @@ __device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
 __device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
   return __builtin_bit_cast(uint16_t, _Float16(f));
 }
+// Two floats to fp16 (lo = a, hi = b), rounded as f32_to_f16_bits rounds each:
+// one packed convert on gfx950 instead of two converts and an OR.
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ unsigned f32x2_to_f16x2_bits(float a, float b) {
+  return __builtin_bit_cast(unsigned, __builtin_convertvector(f32x2_t{a, b}, f16x2_t));
+}
 
 template <int DT>
 __device__ __forceinline__ float to_f32(uint16_t bits) {

@@ -161,7 +161,7 @@ __device__ __forceinline__ void stage_fields8(const float v[8], int r, u32x4_t& 
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const int e = E - int((fsh >> (4 * q)) & 0xfu);
-    o[q] = unsigned(f32_to_f16_bits(ldexpf(v[2 * q], e))) | (unsigned(f32_to_f16_bits(ldexpf(v[2 * q + 1], e))) << 16);
+    o[q] = f32x2_to_f16x2_bits(ldexpf(v[2 * q], e), ldexpf(v[2 * q + 1], e));
   }
   sum = sm;
   exp_off = subnormal_exponent<kF16>() - E;
