@@ -222,7 +222,7 @@ __global__ __launch_bounds__(T * P * 64) void w3_fields_wide_kernel(
       u32x4_t o;
       float sm;
       int ge;
-      stage_fields8(v, r, o, sm, ge);
+      stage_fields8(v, field_positions(r), o, sm, ge);
       bst[b * kWideStage + kb * kStageStride<1> + r] = o;
       if (r == 0) {
         gsum[4 * b + kb] = sm;
@@ -442,6 +442,7 @@ __global__ __launch_bounds__(T * P * 64) void w3_fields_rows_kernel(
 
   // the staged operands of the wave's i-th staged batch, all rows, into LDS slot `slot`
   auto stage = [&](int i, int slot) __attribute__((always_inline)) {
+    const unsigned fsh = field_positions(r);
 #pragma unroll
     for (int m = 0; m < MB; ++m) {
       const unsigned xw[4] = {sx[i][m].x, sx[i][m].y, sx[i][m].z, sx[i][m].w};
@@ -451,7 +452,7 @@ __global__ __launch_bounds__(T * P * 64) void w3_fields_rows_kernel(
       u32x4_t o;
       float sm;
       int ge;
-      stage_fields8(v, r, o, sm, ge);
+      stage_fields8(v, fsh, o, sm, ge);
       sh.bst[slot][kb * kStageStride<MB> + r * MB + m] = o;
       if (r == 0) {
         sh.gsum[slot][kb * MB + m] = sm;

@@ -142,7 +142,17 @@ constexpr unsigned long long field_shift_nibbles() {
 // range) with p the mantissa position of the register each pair meets, the
 // group's sum of x and exponent offset.  Shared by both field-layout kernels so
 // their bits agree.
-__device__ __forceinline__ void stage_fields8(const float v[8], int r, u32x4_t& o, float& sum, int& exp_off) {
+// The mantissa positions p of lane r's four element pairs (registers 4 (r % 4) +
+// q), a nibble each; formed once per staged batch and shared by its rows (the
+// asm keeps it from being hoisted and held across the batch loop, where it cost
+// the 4-wave kernel a spill).
+__device__ __forceinline__ unsigned field_positions(int r) {
+  unsigned rr = unsigned(r & 3);
+  asm volatile("" : "+v"(rr));
+  return unsigned(field_shift_nibbles() >> (16 * rr)) & 0xffffu;
+}
+
+__device__ __forceinline__ void stage_fields8(const float v[8], unsigned fsh, u32x4_t& o, float& sum, int& exp_off) {
   float mx = 0.f, sm = 0.f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
@@ -152,12 +162,6 @@ __device__ __forceinline__ void stage_fields8(const float v[8], int r, u32x4_t& 
   mx = row16_max(mx);
   sm = row16_sum(sm);
   const int E = choose_exponent<kF16>(mx);
-  // the 2^-p of this lane's four element pairs (registers 4 (r % 4) + q),
-  // recomputed per batch (the asm keeps it from being hoisted and held across
-  // the batch loop, where it cost the 4-wave kernel a spill)
-  unsigned rr = unsigned(r & 3);
-  asm volatile("" : "+v"(rr));
-  const unsigned fsh = unsigned(field_shift_nibbles() >> (16 * rr)) & 0xffffu;
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const int e = E - int((fsh >> (4 * q)) & 0xfu);
@@ -388,7 +392,7 @@ __device__ __forceinline__ void w3_mfma_body(
       u32x4_t o;
       float sm;
       int ge;
-      stage_fields8(v, r, o, sm, ge);
+      stage_fields8(v, field_positions(r), o, sm, ge);
       my_stage[kb * kStageStride<MB> + r * MB + m] = o;
       if (r == 0) {
         gsum[wave][kb * MB + m] = sm;
