@@ -303,3 +303,53 @@ def test_rows_gemv_matches_oracle_and_plans(gpu, o, k, m, xdtype, scale_dtype, z
         assert torch.equal(got[:m], want[:m]), plan
         ran += 1
     assert ran > 0
+
+
+def _rows_call(lib, gpu, x, dl, out, m, o, k, scale_dtype=torch.float16):
+    _lib.check(lib.fx_w3_gemv_fields_rows(x.data_ptr(), _lib.dtype_code(x.dtype), dl["fields"].data_ptr(),
+                                          dl["scales"].data_ptr(), _lib.dtype_code(scale_dtype),
+                                          _lib.ptr(dl.get("zeros")), out.data_ptr(), m, o, k,
+                                          _lib.stream_handle(gpu)), "gemv_fields_rows")
+
+
+def test_rows_gemv_one_row_is_the_field_gemv(gpu):
+    """M = 1 through fx_w3_gemv_fields_rows is fx_w3_gemv_fields, bit for bit."""
+    o, k = 768, 4096
+    _, dl = _payload(gpu, o, k, seed=21)
+    x = torch.randn(1, k, generator=torch.Generator().manual_seed(4)).bfloat16().to(gpu)
+    lib = _lib.library()
+    a = torch.empty(1, o, dtype=torch.bfloat16, device=gpu)
+    b = torch.empty_like(a)
+    _rows_call(lib, gpu, x, dl, a, 1, o, k)
+    _lib.check(lib.fx_w3_gemv_fields(x.data_ptr(), _lib.FX_BF16, dl["fields"].data_ptr(), dl["scales"].data_ptr(),
+                                     _lib.FX_F16, dl["zeros"].data_ptr(), b.data_ptr(), o, k,
+                                     _lib.stream_handle(gpu)), "gemv_fields")
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("o,k,m", [(1040, 2048, 8), (256, 12288, 5)])
+def test_rows_gemv_graph_replays_match_eager(gpu, o, k, m):
+    """The M-row launch captured in a hipGraph: every replay, with eager work and
+    synchronisations between replays, equals the eager result bit for bit."""
+    _, dl = _payload(gpu, o, k, seed=o + m)
+    lib = _lib.library()
+    stream = torch.cuda.Stream(gpu)
+    with torch.cuda.stream(stream):
+        x = torch.randn(m, k, device=gpu, generator=torch.Generator(device=gpu).manual_seed(m)).bfloat16()
+        eager = torch.empty(m, o, dtype=torch.bfloat16, device=gpu)
+        out = torch.full_like(eager, float("nan"))
+        _rows_call(lib, gpu, x, dl, eager, m, o, k)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        _rows_call(lib, gpu, x, dl, out, m, o, k)
+    torch.cuda.synchronize()
+    for i in range(4):
+        out.fill_(float("nan"))
+        scratch = torch.randn(4096, device=gpu).sum()  # eager work between the replays
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), i
+        assert torch.isfinite(scratch)
