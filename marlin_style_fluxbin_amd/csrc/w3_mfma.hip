@@ -88,14 +88,23 @@ __device__ __forceinline__ unsigned bitfield_insert(unsigned mask, unsigned a, u
   return (a & mask) | (b & ~mask);  // v_bfi_b32
 }
 
+// T_s from three-input bit operations (v_bitop3_b32, gfx950): u = M1 ? b : ~c
+// (table 0xB1, operand order b, c, m: the inversion of stored plane 2 folded in),
+// then T = M0 ? a : u (table 0xE4).  The complement of the shifted plane differs
+// from the shifted complement only in shifted-in bits, which land in bits the
+// masks take from the other planes or in the don't-care bit.  Two instructions
+// per T_s where the compiler's own rewrite of the inserts took three to four.
+__device__ __forceinline__ unsigned select3(unsigned a, unsigned b, unsigned c, unsigned m0, unsigned m1) {
+  return __builtin_amdgcn_bitop3_b32(a, __builtin_amdgcn_bitop3_b32(b, c, m1, 0xB1), m0, 0xE4);
+}
+
 __device__ __forceinline__ void dequant_word(unsigned p0, unsigned p1, unsigned p2, u32x4_t a[4]) {
   const unsigned M0 = 0x11111111u, M1 = 0x22222222u;
-  const unsigned q2 = ~p2;  // stored plane 2 is inverted
   unsigned tw[4];
-  tw[0] = bitfield_insert(M0, p0, bitfield_insert(M1, p1 << 1, q2 << 2));
-  tw[1] = bitfield_insert(M0, p0 >> 1, bitfield_insert(M1, p1, q2 << 1));
-  tw[2] = bitfield_insert(M0, p0 >> 2, bitfield_insert(M1, p1 >> 1, q2));
-  tw[3] = bitfield_insert(M0, p0 >> 3, bitfield_insert(M1, p1 >> 2, q2 >> 1));
+  tw[0] = select3(p0, p1 << 1, p2 << 2, M0, M1);
+  tw[1] = select3(p0 >> 1, p1, p2 << 1, M0, M1);
+  tw[2] = select3(p0 >> 2, p1 >> 1, p2, M0, M1);
+  tw[3] = select3(p0 >> 3, p1 >> 2, p2 >> 1, M0, M1);
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
     const unsigned t = tw[s], th = t >> 8;
