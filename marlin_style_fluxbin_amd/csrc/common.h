@@ -107,6 +107,14 @@ __device__ __forceinline__ float row16_max(float v) {
 }
 
 typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+// lane_index * rows for a lane index below 4 and rows <= 3 * 2^20 (every entry
+// point checks O <= 2^20 before a launch): both factors and the product fit 24
+// bits, so the full-rate 24-bit multiply gives the 32-bit product
+// (v_mul_lo_u32 runs at quarter rate).
+__device__ __forceinline__ int lane_times_rows(int lane_index, int rows) {
+  return int(__umul24(unsigned(lane_index), unsigned(rows)));
+}
+
 
 // Index of the calling wave in its workgroup, as a wave-uniform (scalar) value:
 // the compiler cannot tell that threadIdx.x / 64 is the same across a wave, and
@@ -148,6 +156,13 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_resource(const void* ba
   // it put the descriptor in VGPRs, and every load through it in a waterfall loop)
   const int records = (bytes >> 31) != 0 ? 0x7fffffff : int(bytes);
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), short(0), records, 0x00020000);
+}
+
+// The same over a size below 2 GiB (the GEMV payload arrays and activations:
+// every entry point checks their sizes before a launch), formed in 32-bit
+// arithmetic, so no clamp and no compare reach the vector unit.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_resource_2g(const void* base, unsigned bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), short(0), int(bytes), 0x00020000);
 }
 
 __device__ __forceinline__ u32x4_t load_b128(__amdgpu_buffer_rsrc_t r, int offset, int soffset) {

@@ -75,10 +75,11 @@ __global__ __launch_bounds__(T * P * 64) void w3_fields_wide_kernel(
   const int row0 = row_base + 16 * tile;
   const unsigned zero_default = zeros ? 0u : 0x04040404u;
 
-  const auto rp = buffer_resource(fields, size_t(G) * 3 * O * 16);
-  const auto rs = buffer_resource(scales, size_t(G) * O * 2);
-  const auto rz = buffer_resource(zeros ? (const void*)zeros : (const void*)scales, zeros ? size_t(G) * O : 0);
-  const auto rx = buffer_resource(x, size_t(K) * 2);
+  const unsigned go = unsigned(G) * unsigned(O);
+  const auto rp = buffer_resource_2g(fields, go * 48u);
+  const auto rs = buffer_resource_2g(scales, go * 2u);
+  const auto rz = buffer_resource_2g(zeros ? (const void*)zeros : (const void*)scales, zeros ? go : 0u);
+  const auto rx = buffer_resource_2g(x, unsigned(K) * 2u);
   const auto rperm = buffer_resource(PERM ? (const void*)perm : (const void*)x, PERM ? size_t(K) * 2 : 0);
   const auto rwn = buffer_resource(NORMIN ? (const void*)ra.pro_weight : (const void*)x, NORMIN ? size_t(K) * 2 : 0);
 
@@ -154,8 +155,8 @@ __global__ __launch_bounds__(T * P * 64) void w3_fields_wide_kernel(
   // The scalar offset is not range-checked: every live load is in bounds by the
   // plan's contract (O % 16 == 0, G % 4 == 0), and tiles past O issue none.
   const int plane_stride = O * 16;
-  const int p_lane = (kb * 3 * O + row0 + r) * 16;
-  const int e_lane = cslot * O + row0 + 4 * kb;
+  const int p_lane = (lane_times_rows(kb, 3 * O) + row0 + r) * 16;
+  const int e_lane = lane_times_rows(cslot, O) + row0 + 4 * kb;
   const bool tile_on = row0 < O;
   auto issue = [&](int batch, BatchLoads<1, 1>& L, bool live_batch) __attribute__((always_inline)) {
     const bool on = live_batch && tile_on;
@@ -391,10 +392,11 @@ __global__ __launch_bounds__(T * P * 64) void w3_fields_rows_kernel(
   const int row0 = row_base + 16 * tile;
   const unsigned zero_default = zeros ? 0u : 0x04040404u;
 
-  const auto rp = buffer_resource(fields, size_t(G) * 3 * O * 16);
-  const auto rs = buffer_resource(scales, size_t(G) * O * 2);
-  const auto rz = buffer_resource(zeros ? (const void*)zeros : (const void*)scales, zeros ? size_t(G) * O : 0);
-  const auto rx = buffer_resource(x, size_t(M) * K * 2);  // rows past M read zeros
+  const unsigned go = unsigned(G) * unsigned(O);
+  const auto rp = buffer_resource_2g(fields, go * 48u);
+  const auto rs = buffer_resource_2g(scales, go * 2u);
+  const auto rz = buffer_resource_2g(zeros ? (const void*)zeros : (const void*)scales, zeros ? go : 0u);
+  const auto rx = buffer_resource_2g(x, unsigned(M) * unsigned(K) * 2u);  // rows past M read zeros
 
   const int r = lane & 15, kb = lane >> 4, c = lane & 15, cslot = c & 3, cm = c >> 2;
 
@@ -417,8 +419,8 @@ __global__ __launch_bounds__(T * P * 64) void w3_fields_rows_kernel(
   // the scalar offset is not range-checked: live loads are in bounds by the
   // plan's contract (O % 16 == 0, G % 4 == 0), tiles past O issue none
   const int plane_stride = O * 16;
-  const int p_lane = (kb * 3 * O + row0 + r) * 16;
-  const int e_lane = cslot * O + row0 + 4 * kb;
+  const int p_lane = (lane_times_rows(kb, 3 * O) + row0 + r) * 16;
+  const int e_lane = lane_times_rows(cslot, O) + row0 + 4 * kb;
   const bool tile_on = row0 < O;
   auto issue = [&](int batch, BatchLoads<1, 1>& L) __attribute__((always_inline)) {
     const bool on = batch < nbatch && tile_on;

@@ -127,7 +127,11 @@ __device__ __forceinline__ void dequant_word(unsigned p0, unsigned p1, unsigned 
 __device__ __forceinline__ void dequant_fields(unsigned w0, unsigned w1, unsigned w2, u32x4_t a[4]) {
   const unsigned M0 = 0x00070007u, M3 = 0x00380038u, M6 = 0x01c001c0u;
   const unsigned h0 = w0 >> 9, h1 = w1 >> 9, h2 = w2 >> 9;
-  const unsigned spare = ((w0 >> 15) & 0x00010001u) | ((w1 >> 14) & 0x00020002u) | ((w2 >> 13) & 0x00040004u);
+  // the spare pair: bit 0 / 16 from w0, 1 / 17 from w1, 2 / 18 from w2 (two
+  // selects, table 0xE4: m ? a : b, over a masked w2 term)
+  const unsigned spare = __builtin_amdgcn_bitop3_b32(
+      w0 >> 15, __builtin_amdgcn_bitop3_b32(w1 >> 14, (w2 >> 13) & 0x00040004u, 0x00020002u, 0xE4), 0x00010001u,
+      0xE4);
   a[0] = u32x4_t{w0 & M0, w0 & M3, w0 & M6, h0 & M0};
   a[1] = u32x4_t{h0 & M3, w1 & M0, w1 & M3, w1 & M6};
   a[2] = u32x4_t{h1 & M0, h1 & M3, w2 & M0, w2 & M3};
@@ -281,11 +285,11 @@ __device__ __forceinline__ void w3_mfma_body(
   // absent zero-points read as 0 (empty buffer) and become 4 through this OR
   const unsigned zero_default = zeros ? 0u : 0x04040404u;
 
-  const auto rp = buffer_resource(planes, size_t(G) * 3 * O * 16);
-  const auto rs = buffer_resource(scales, size_t(G) * O * 2);
-  const auto rz = buffer_resource(zeros ? (const void*)zeros : (const void*)scales,
-                                  zeros ? size_t(G) * O : 0);
-  const auto rx = buffer_resource(x, size_t(MB) * K * 2);
+  const unsigned go = unsigned(G) * unsigned(O);
+  const auto rp = buffer_resource_2g(planes, go * 48u);
+  const auto rs = buffer_resource_2g(scales, go * 2u);
+  const auto rz = buffer_resource_2g(zeros ? (const void*)zeros : (const void*)scales, zeros ? go : 0u);
+  const auto rx = buffer_resource_2g(x, unsigned(MB) * unsigned(K) * 2u);
   const auto rperm = buffer_resource(PERM ? (const void*)perm : (const void*)x, PERM ? size_t(K) * 2 : 0);
   // NORMIN: the row's RMSNorm weights, and 1 / rms from the tile partials (each
   // wave reduces them itself, in a fixed order: lane l adds partials l, l + 64,
@@ -358,14 +362,14 @@ __device__ __forceinline__ void w3_mfma_body(
     if constexpr (CORR) {  // the A row's zero-point (needed by the dequant, ahead of the planes)
 #pragma unroll
       for (int tt = 0; tt < RT; ++tt)
-        L.za[tt] = __builtin_amdgcn_raw_buffer_load_b8(rz, real ? (gb + kb) * O + row0 + 16 * tt + r : kOutOfRange,
+        L.za[tt] = __builtin_amdgcn_raw_buffer_load_b8(rz, real ? gb * O + lane_times_rows(kb, O) + row0 + 16 * tt + r : kOutOfRange,
                                                        0, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
     // groups past G: past the end -> zeros; rows past O read row O - 1 (never
     // stored), since the plane stride rides in the scalar offset, which the
     // range check does not cover
-    const int gbase = (gb + kb) * 3 * O;
+    const int gbase = gb * 3 * O + lane_times_rows(kb, 3 * O);  // gb is wave-uniform
 #pragma unroll
     for (int tt = 0; tt < RT; ++tt) {
       const int poff = live ? (gbase + prow[tt]) * 16 : kOutOfRange;
@@ -374,7 +378,7 @@ __device__ __forceinline__ void w3_mfma_body(
       L.w[tt][2] = load_b128_stream(rp, poff, 2 * plane_stride);
     }
     __builtin_amdgcn_sched_barrier(0);
-    const int eoff = (gb + cslot) * O + row0 + 4 * kb;
+    const int eoff = gb * O + lane_times_rows(cslot, O) + row0 + 4 * kb;
 #pragma unroll
     for (int tt = 0; tt < RT; ++tt) {
       const int e = eoff + 16 * tt;
