@@ -188,8 +188,15 @@ __device__ __forceinline__ void stage_fields8(const float v[8], unsigned fsh, u3
 template <int XDT>
 __device__ __forceinline__ void normalize8(float v[8], const u32x4_t& wn, float norm_inv) {
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
-    v[i] = round_to<XDT>(to_f32<XDT>(uint16_t(wn[i >> 1] >> (16 * (i & 1)))) * round_to<XDT>(v[i] * norm_inv));
+  for (int i = 0; i < 8; i += 2) {
+    float a = v[i] * norm_inv, b = v[i + 1] * norm_inv;
+    round_pair<XDT>(a, b);
+    a *= to_f32<XDT>(uint16_t(wn[i >> 1]));
+    b *= to_f32<XDT>(uint16_t(wn[i >> 1] >> 16));
+    round_pair<XDT>(a, b);
+    v[i] = a;
+    v[i + 1] = b;
+  }
 }
 
 // One (row, group) term of the epilogue: acc + s (D 2^fe - z sum(x)), as two
