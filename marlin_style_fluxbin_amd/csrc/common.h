@@ -55,20 +55,28 @@ __device__ __forceinline__ float round_to(float v) {
 // round_to on two values at once: one packed convert (v_cvt_pk_bf16_f32 /
 // v_cvt_pk_f16_f32 on gfx950) and the two widenings, the same bits as two
 // round_to calls.
+// round_pair_bits also returns the two stored values (a in the low half).
 template <int DT>
-__device__ __forceinline__ void round_pair(float& a, float& b) {
+__device__ __forceinline__ unsigned round_pair_bits(float& a, float& b) {
   typedef float f2_t __attribute__((ext_vector_type(2)));
   if constexpr (DT == kBF16) {
     typedef __bf16 b2_t __attribute__((ext_vector_type(2)));
     const unsigned p = __builtin_bit_cast(unsigned, __builtin_convertvector(f2_t{a, b}, b2_t));
     a = __uint_as_float(p << 16);
     b = __uint_as_float(p & 0xffff0000u);
+    return p;
   } else {
     typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
-    const f2_t w = __builtin_convertvector(__builtin_convertvector(f2_t{a, b}, h2_t), f2_t);
+    const h2_t h = __builtin_convertvector(f2_t{a, b}, h2_t);
+    const f2_t w = __builtin_convertvector(h, f2_t);
     a = w.x;
     b = w.y;
+    return __builtin_bit_cast(unsigned, h);
   }
+}
+template <int DT>
+__device__ __forceinline__ void round_pair(float& a, float& b) {
+  (void)round_pair_bits<DT>(a, b);
 }
 
 // Butterfly sum over the 64 lanes of a wavefront (xor shuffles lower to DPP /

@@ -198,18 +198,24 @@ __global__ __launch_bounds__(NT * NK * 64) void hybrid_kernel(HybridArgs a) {
       if constexpr (NORMIN || SWIGLU) {  // the activation the GEMV reads, staged for the refinement too
         u32x4_t nb;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
+        for (int j = 0; j < 8; j += 2) {  // element pairs: one packed convert per rounding
+          float a, b;
           if constexpr (NORMIN) {  // Qwen3RMSNorm: round(w * round(h * inv))
-            xv[j] = round_to<XDT>(to_f32<XDT>(uint16_t(swn[q][j >> 1] >> (16 * (j & 1)))) *
-                                  round_to<XDT>(xv[j] * norm_inv));
+            a = xv[j] * norm_inv;
+            b = xv[j + 1] * norm_inv;
+            round_pair<XDT>(a, b);
+            a *= to_f32<XDT>(uint16_t(swn[q][j >> 1]));
+            b *= to_f32<XDT>(uint16_t(swn[q][j >> 1] >> 16));
           } else {  // Qwen3MLP: round(round(silu(gate)) * up), silu(g) = g / (1 + e^-g)
-            const float gv = xv[j];
-            const float sg = round_to<XDT>(gv / (1.f + __expf(-gv)));
-            xv[j] = round_to<XDT>(sg * to_f32<XDT>(uint16_t(sup[q][j >> 1] >> (16 * (j & 1)))));
+            a = xv[j] / (1.f + __expf(-xv[j]));
+            b = xv[j + 1] / (1.f + __expf(-xv[j + 1]));
+            round_pair<XDT>(a, b);
+            a *= to_f32<XDT>(uint16_t(sup[q][j >> 1]));
+            b *= to_f32<XDT>(uint16_t(sup[q][j >> 1] >> 16));
           }
-          const unsigned bits = from_f32<XDT>(xv[j]);
-          if (j & 1) nb[j >> 1] |= bits << 16;
-          else nb[j >> 1] = bits;
+          nb[j >> 1] = round_pair_bits<XDT>(a, b);
+          xv[j] = a;
+          xv[j + 1] = b;
         }
         xs[bt * 64 + lane] = nb;
       } else {
