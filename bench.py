@@ -416,7 +416,7 @@ def fields_plan_sweep(device, stream, shapes=None, min_bytes=320e6, min_copies=5
             for p in range(copies):
                 call(p)
 
-        plans = [("one-tile", (-1, 0, 0, 0))]
+        plans = [("one-tile", (-1, 0, 0, 0)), ("default", (0, 0, 0, 0))]
         plans += [(",".join(map(str, pl)), pl) for pl in FIELDS_PLANS
                   if o % 16 == 0 and k % 512 == 0 and k // 512 <= pl[3] * pl[0] * pl[1]]
         graphs, first = {}, {}

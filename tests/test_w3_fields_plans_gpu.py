@@ -2,12 +2,12 @@
 
 Every field-layout entry point (plain, SwiGLU and residual epilogues, the
 normalising prologue, permuted columns, output indices, the strided batch) runs
-once per plan that can take the shape (``fx_w3_fields_plan``) and once on the
-one-tile kernel; every output -- values, reordered copies, tile sums of squares
--- must be bitwise equal across all of them.  The shapes include a partial last
-row block (65 tiles: a workgroup of 2, 3, 4 or 6 tiles holds tiles past O), a
-K with fewer batches than virtual waves (4), and K = 12288 (24 batches, three
-per virtual wave).  The one-tile kernel itself is held to the float64 oracle by
+once per plan that can take the shape (``fx_w3_fields_plan``), once on the
+one-tile kernel and once under the default plan; every output -- values,
+reordered copies, tile sums of squares -- must be bitwise equal across all of
+them.  The shapes include a partial last row block (65 tiles: a workgroup of 2,
+3, 4 or 6 tiles holds tiles past O), a K with fewer batches than virtual waves
+(4), 9 batches, K = 12288 (24 batches, three per virtual wave) and K = 16384.  The one-tile kernel itself is held to the float64 oracle by
 tests/test_w3_fields_gpu.py; one wide plan is checked against it here too.
 """
 from __future__ import annotations
@@ -67,14 +67,18 @@ def _index(n, seed, gpu):
     return torch.randperm(n, generator=torch.Generator().manual_seed(seed)).to(torch.int16).to(gpu)
 
 
+DEFAULT = (0, 0, 0, 0)  # the entry points' own choice
+
+
 def _across_plans(run, o, k, perm=False):
-    """run() -> tuple of output tensors, under the one-tile kernel and every plan
-    that takes (o, k); asserts bitwise equality; returns the one-tile outputs."""
+    """run() -> tuple of output tensors, under the one-tile kernel, the default
+    and every plan that takes (o, k); asserts bitwise equality; returns the
+    one-tile outputs."""
     with fields_plan(ONE_TILE):
         want = [t.clone() for t in run()]
     ran = 0
-    for plan in PLANS:
-        if not fits(plan, o, k, perm):
+    for plan in [DEFAULT] + PLANS:
+        if plan != DEFAULT and not fits(plan, o, k, perm):
             continue
         with fields_plan(plan):
             got = run()
@@ -86,7 +90,7 @@ def _across_plans(run, o, k, perm=False):
     return want
 
 
-SHAPES = [(768, 4096), (1040, 2048), (256, 12288), (4096, 4096)]
+SHAPES = [(768, 4096), (1040, 2048), (256, 12288), (4096, 4096), (1040, 4608), (512, 8192), (256, 16384)]
 
 
 @pytest.mark.parametrize("o,k", SHAPES)
@@ -110,7 +114,7 @@ def test_plain_gemv_same_bits_every_plan(gpu, o, k, xdtype, scale_dtype, zeros):
     assert torch.isfinite(out.float()).all()
 
 
-@pytest.mark.parametrize("o,k", [(768, 4096), (1040, 2048), (256, 12288)])
+@pytest.mark.parametrize("o,k", [(768, 4096), (1040, 2048), (256, 12288), (4096, 12288), (1040, 4608)])
 @pytest.mark.parametrize("permuted", [False, True])
 @pytest.mark.parametrize("indexed", [False, True])
 def test_residual_epilogue_same_bits_every_plan(gpu, o, k, permuted, indexed):
@@ -139,7 +143,7 @@ def test_residual_epilogue_same_bits_every_plan(gpu, o, k, permuted, indexed):
         assert torch.equal(outs[2][0, index.long()], outs[0][0])
 
 
-@pytest.mark.parametrize("o,k", [(1536, 4096), (1056, 2048)])
+@pytest.mark.parametrize("o,k", [(1536, 4096), (1056, 2048), (512, 12288)])
 @pytest.mark.parametrize("permuted", [False, True])
 @pytest.mark.parametrize("indexed", [False, True])
 def test_swiglu_epilogue_same_bits_every_plan(gpu, o, k, permuted, indexed):
@@ -187,7 +191,7 @@ def test_normalising_prologue_same_bits_every_plan(gpu, o, k, swiglu):
     assert torch.isfinite(out.float()).all()
 
 
-@pytest.mark.parametrize("o,k,batch", [(1536, 4096, 3), (256, 12288, 2)])
+@pytest.mark.parametrize("o,k,batch", [(1536, 4096, 3), (256, 12288, 2), (128, 16384, 3)])
 def test_strided_batch_same_bits_every_plan(gpu, o, k, batch):
     print(f"strided {o}x{k} x{batch}", flush=True)
     lib = _lib.library()
@@ -209,8 +213,8 @@ def test_strided_batch_same_bits_every_plan(gpu, o, k, batch):
     # plans whose row blocks are not a multiple of 8 refuse a batch; run the rest
     with fields_plan(ONE_TILE):
         want = run()[0].clone()
-    for plan in PLANS:
-        if not fits(plan, o, k) or (o // 16 + plan[0] - 1) // plan[0] % 8:
+    for plan in [DEFAULT] + PLANS:
+        if plan != DEFAULT and (not fits(plan, o, k) or (o // 16 + plan[0] - 1) // plan[0] % 8):
             continue
         with fields_plan(plan):
             got = run()[0]
