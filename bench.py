@@ -1510,10 +1510,15 @@ def summarize_pmc(csv_paths, out_json):
         if "copyBuffer" in k:
             mean[k] = {c: sum(sorted(v)[-16:]) / len(sorted(v)[-16:]) for c, v in d.items()}
     copy = [k for k in mean if "copyBuffer" in k and "FETCH_SIZE" in mean[k]]
-    # the planar kernel (FIELDS = false, the last template argument) and the
-    # field-layout one
-    w3 = [k for k in mean if "w3_mfma_kernel" in k and not k.split("(")[0].endswith("true>")]
-    w3_fields = [k for k in mean if "w3_mfma_kernel" in k and k.split("(")[0].endswith("true>")]
+    # the planar kernel and the field-layout one: FIELDS is the tenth template
+    # argument of w3_mfma_kernel
+    def fields_arg(name):
+        head = name.split("(")[0]
+        args = head[head.index("<") + 1:head.rindex(">")].split(",")
+        return len(args) > 9 and args[9].strip() == "true"
+
+    w3 = [k for k in mean if "w3_mfma_kernel" in k and not fields_arg(k)]
+    w3_fields = [k for k in mean if "w3_mfma_kernel" in k and fields_arg(k)]
     if not copy or not w3:
         raise SystemExit("counter CSVs lack the copy kernel or the W3 kernel")
     kib = CALIBRATION_BYTES / 1024
