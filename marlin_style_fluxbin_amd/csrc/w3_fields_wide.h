@@ -1,4 +1,6 @@
-// One-row field-layout GEMV with workgroup-shared activation staging.
+// Field-layout GEMVs with workgroup-shared activation staging: the one-row form
+// (w3_fields_wide_kernel, plans for sweeps and tests) and the M-row form
+// (w3_fields_rows_kernel, the default of fx_w3_gemv_fields_rows, further down).
 //
 // A workgroup owns T 16-row tiles and splits K into P parts: wave (tile, part)
 // multiplies its tile by the batches (4 groups, 512 columns) of its part.  The
