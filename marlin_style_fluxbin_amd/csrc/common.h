@@ -93,6 +93,7 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+
 // DPP lane moves within the 16-lane rows of a wavefront.
 template <int CTRL>
 __device__ __forceinline__ float dpp_move(float v) {
@@ -131,6 +132,31 @@ __device__ __forceinline__ float row16_max(float v) {
   u = max(u, dpp_move_u<kDppHalfMirror>(u));
   u = max(u, dpp_move_u<kDppMirror>(u));
   return __uint_as_float(u);
+}
+
+// Max over the 64 lanes of values that are never NaN (attention scores: finite
+// or -inf) through order-preserving unsigned keys (a non-negative float with its
+// sign bit set, a negative one with every bit flipped): an integer max per step,
+// where fmaxf first canonicalises the shuffled operand.  Equal to wave_max on
+// such values (up to the sign of a zero maximum).
+__device__ __forceinline__ unsigned float_order_key(float f) {
+  const unsigned b = __float_as_uint(f);
+  return b ^ (unsigned(int(b) >> 31) | 0x80000000u);
+}
+__device__ __forceinline__ float float_from_order_key(unsigned k) {
+  return __uint_as_float(k ^ (int(k) < 0 ? 0x80000000u : 0xffffffffu));
+}
+__device__ __forceinline__ float wave_max_not_nan(float v) {
+  unsigned k = float_order_key(v);
+  // within each 16-lane row by DPP (one combined instruction per step), then
+  // across the four rows
+  k = max(k, dpp_move_u<kDppXor1>(k));
+  k = max(k, dpp_move_u<kDppXor2>(k));
+  k = max(k, dpp_move_u<kDppHalfMirror>(k));
+  k = max(k, dpp_move_u<kDppMirror>(k));
+  k = max(k, unsigned(__shfl_xor(int(k), 16, 64)));
+  k = max(k, unsigned(__shfl_xor(int(k), 32, 64)));
+  return float_from_order_key(k);
 }
 
 typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));

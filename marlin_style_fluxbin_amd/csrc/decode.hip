@@ -59,17 +59,22 @@ __device__ __forceinline__ u32x4_t head_norm_rope8(const u32x4_t& x, const u32x4
                                                   const u32x4_t& sn, bool lower, float eps, int rope_mode) {
   constexpr int DB = D / 8;
   const float inv = rsqrtf(key_row_sum<DB>(sum_sq8<DT>(x)) / float(D) + eps);
+  // element pairs: each rounding point is one packed convert (round_pair)
   float y[8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const float xv = to_f32<DT>(uint16_t(x[e >> 1] >> (16 * (e & 1))));
-    const float wv = to_f32<DT>(uint16_t(w[e >> 1] >> (16 * (e & 1))));
-    y[e] = round_to<DT>(wv * round_to<DT>(xv * inv));
+  for (int e = 0; e < 8; e += 2) {
+    float a = to_f32<DT>(uint16_t(x[e >> 1])) * inv, b = to_f32<DT>(uint16_t(x[e >> 1] >> 16)) * inv;
+    round_pair<DT>(a, b);
+    a *= to_f32<DT>(uint16_t(w[e >> 1]));
+    b *= to_f32<DT>(uint16_t(w[e >> 1] >> 16));
+    round_pair<DT>(a, b);
+    y[e] = a;
+    y[e + 1] = b;
   }
   u32x4_t o;
 #pragma unroll
   for (int e = 0; e < 8; e += 2) {
-    float r[2];
+    float rot[2], yc[2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       // rotate_half(y) = (-y[D/2:], y[:D/2]): the partner dim sits DB/2 lanes away
@@ -77,13 +82,15 @@ __device__ __forceinline__ u32x4_t head_norm_rope8(const u32x4_t& x, const u32x4
       float partner;
       if constexpr (DB == 16) partner = dpp_move<kDppRowRor8>(y[e + h]);
       else partner = __shfl_xor(y[e + h], DB / 2, 64);
-      const float c = to_f32<DT>(uint16_t(cs[(e + h) >> 1] >> (16 * ((e + h) & 1))));
-      const float sv = to_f32<DT>(uint16_t(sn[(e + h) >> 1] >> (16 * ((e + h) & 1))));
-      float rot = (lower ? -partner : partner) * sv;
-      if (rope_mode == kRopeStock) rot = round_to<DT>(rot);
-      r[h] = round_to<DT>(y[e + h] * c) + rot;
+      const float c = to_f32<DT>(uint16_t(cs[e >> 1] >> (16 * h)));
+      const float sv = to_f32<DT>(uint16_t(sn[e >> 1] >> (16 * h)));
+      rot[h] = (lower ? -partner : partner) * sv;
+      yc[h] = y[e + h] * c;
     }
-    o[e >> 1] = unsigned(from_f32<DT>(r[0])) | (unsigned(from_f32<DT>(r[1])) << 16);
+    if (rope_mode == kRopeStock) round_pair<DT>(rot[0], rot[1]);
+    round_pair<DT>(yc[0], yc[1]);
+    float r0 = yc[0] + rot[0], r1 = yc[1] + rot[1];
+    o[e >> 1] = round_pair_bits<DT>(r0, r1);
   }
   return o;
 }
@@ -242,7 +249,7 @@ __global__ __launch_bounds__(256 * NG) void attn_split_kernel(const uint16_t* __
         s[hh][i] = live[i] ? acc : -INFINITY;
         mt[hh] = fmaxf(mt[hh], s[hh][i]);
       }
-      mt[hh] = wave_max(mt[hh]);
+      mt[hh] = wave_max_not_nan(mt[hh]);  // scores are finite or -inf (keys past pos)
     }
     if (lane == 0) {
 #pragma unroll
@@ -344,7 +351,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
       v0[u] = cc < n ? vo[size_t(c0 + cc) * D + d0] : 0.f;
       m0[u] = cc < n ? ml[size_t(c0 + cc) * 2] : -INFINITY;
     }
-    const float Mn = fmaxf(M, wave_max(mc));
+    const float Mn = fmaxf(M, wave_max_not_nan(mc));  // split maxima: finite, -inf past n
     const float rescale = M == -INFINITY ? 0.f : __expf(M - Mn);
     L = L * rescale + wave_sum(lane < n ? __expf(mc - Mn) * lc : 0.f);
     o *= rescale;
