@@ -20,9 +20,11 @@ Protocol of the reference's packed-M=1 PPL runner
 * the result keys of each arm, the three comparisons and the summary's status
   words.
 
-Not carried: the reference's A100 / Python / library version gates and its CUDA
-extension-cache manifests (this build loads one prebuilt HIP library, which
-fails loudly when absent).  Tokens come from a safetensors file holding one
+Not carried: the reference's A100 / Python / library version gates.  In place of
+its CUDA extension-cache manifests every arm's provenance holds the kernel
+library's build contract key and library digest (``w3_lut_extension_build``: this
+build loads one prebuilt HIP library, which fails loudly when absent), so a
+resumed run refuses arms scored by other kernels.  Tokens come from a safetensors file holding one
 ``tokens`` tensor, checked against expected hashes when they are given, and cut
 into blocks of ``sequence_length``.
 
@@ -295,8 +297,12 @@ def run_ppl(load_model: Callable[[], torch.nn.Module], blocks: list[list[int]], 
     from .fused_modules import fused_qwen3_modules
 
     output_dir = Path(output_dir)
+    from .w3_lut_deployment import w3_lut_extension_build
+
+    _, build = w3_lut_extension_build(256)  # one library: the same contract for every row tile
     provenance = dict(provenance or {}, blocks_sha256=sha256_token_sequences(blocks),
-                      w3_layout_manifest_sha256=expected_manifest_sha256)
+                      w3_layout_manifest_sha256=expected_manifest_sha256,
+                      w3_kernel_build_cache_key=build["cache_key"], w3_kernel_library_sha256=build["library_sha256"])
     if resume:
         if not (output_dir / "arms").is_dir():
             raise FileNotFoundError(output_dir / "arms")

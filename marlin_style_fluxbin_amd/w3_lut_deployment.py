@@ -105,6 +105,83 @@ class _Extension:
             _lib.stream_handle(x.device)), "fx_w3_m1_out")
 
 
+BUILD_CONTRACT_SCHEMA = 1
+
+
+def _check_build_request(row_tile: int, uniform_index_probe: bool) -> None:
+    if row_tile not in EXPERIMENTAL_ROW_TILES:
+        raise ValueError(f"row_tile must be one of {EXPERIMENTAL_ROW_TILES}")
+    if uniform_index_probe:
+        raise ValueError("the uniform-index probe build is not provided; use rocprof LDS counters")
+
+
+@lru_cache(maxsize=1)
+def _hipcc_identity() -> dict:
+    import subprocess
+
+    from .build import hipcc
+
+    try:
+        exe = hipcc()
+    except RuntimeError:
+        return {"executable": "unresolved", "version": "unresolved"}
+    try:
+        done = subprocess.run([exe, "--version"], capture_output=True, text=True, timeout=30, check=False)
+        version = (done.stdout or done.stderr).strip()
+    except (OSError, subprocess.TimeoutExpired) as exc:
+        version = type(exc).__name__
+    return {"executable": exe, "version": version}
+
+
+def w3_lut_extension_build(row_tile: int, uniform_index_probe: bool = False) -> tuple[dict, dict]:
+    """Load description and auditable build contract of the kernel library, as
+    the reference's ``w3_lut_extension_build`` (``w3_lut_deployment.py:49-68``,
+    ``extension_cache.py:74-149``) returns them for its per-row-tile extension.
+
+    Here every row tile is served by the one prebuilt ``libfluxbin_amd.so``
+    (``row_tile`` is a tuning hint), so the contract is the same for all of them:
+    the name, every HIP source and header with its SHA-256, the hipcc flags and
+    target, the interpreter / torch / HIP runtime and the compiler identity, and
+    ``cache_key``, the SHA-256 of those fields in canonical JSON.  Any change of
+    a source byte, flag or toolchain changes the key; a documentation change does
+    not.  ``library_sha256`` (outside the key) is the built library's digest, or
+    None when it is not built."""
+    import hashlib
+    import json
+    import platform
+    import sys
+
+    from . import build as _build
+
+    _check_build_request(row_tile, uniform_index_probe)
+    sources = sorted(_build.CSRC.glob("*.hip")) + sorted(_build.CSRC.glob("*.h"))
+    header = _build.PACKAGE.parent / "include" / "fluxbin_amd.h"
+    dependencies = [header] if header.is_file() else []
+    contract = {
+        "schema_version": BUILD_CONTRACT_SCHEMA,
+        "name": "fluxbin_amd",
+        "sources": [{"name": p.name, "sha256": hashlib.sha256(p.read_bytes()).hexdigest()}
+                    for p in sources + dependencies],
+        "extra_hip_cflags": list(_build.HIPCC_FLAGS),
+        "target_architecture": _build.ARCH,
+        "python": f"{sys.version_info.major}.{sys.version_info.minor}",
+        "platform": platform.system(),
+        "machine": platform.machine(),
+        "torch": torch.__version__,
+        "torch_hip_runtime": torch.version.hip,
+        "compiler": {"hipcc": _hipcc_identity()},
+    }
+    encoded = json.dumps(contract, sort_keys=True, separators=(",", ":")).encode()
+    contract["cache_key"] = hashlib.sha256(encoded).hexdigest()
+    contract["compile_sources"] = [p.name for p in sources if p.suffix == ".hip"]
+    contract["content_dependencies"] = [p.name for p in sources if p.suffix == ".h"] + [p.name for p in dependencies]
+    library = _lib.LIBRARY_PATH
+    contract["library_sha256"] = hashlib.sha256(library.read_bytes()).hexdigest() if library.is_file() else None
+    kwargs = {"name": contract["name"], "sources": [str(p) for p in sources], "library": str(library),
+              "extra_hip_cflags": list(_build.HIPCC_FLAGS), "row_tile": row_tile}
+    return kwargs, contract
+
+
 @lru_cache(maxsize=2 * len(EXPERIMENTAL_ROW_TILES))
 def load_w3_lut_extension(row_tile: int, uniform_index_probe: bool = False):
     """Return the loaded kernel library for one row tile.
@@ -113,10 +190,7 @@ def load_w3_lut_extension(row_tile: int, uniform_index_probe: bool = False):
     ``csrc/w3_lut.cu:17-27``) is not offered: LDS bank conflicts are read from
     rocprof counters instead, so no build ever returns wrong values on purpose.
     """
-    if row_tile not in EXPERIMENTAL_ROW_TILES:
-        raise ValueError(f"row_tile must be one of {EXPERIMENTAL_ROW_TILES}")
-    if uniform_index_probe:
-        raise ValueError("the uniform-index probe build is not provided; use rocprof LDS counters")
+    _check_build_request(row_tile, uniform_index_probe)
     if not torch.cuda.is_available():
         raise RuntimeError("W3 LUT requires a ROCm GPU; there is no CPU substitute")
     return _Extension(row_tile)

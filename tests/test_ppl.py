@@ -168,6 +168,16 @@ def test_command_line_dense_arms_and_resume(tmp_path):
     again = ppl.main(argv(out) + ["--resume"])
     assert again["arms"] == summary["arms"]
     record = json.loads((out / "arms" / "decoded_w3_bf16.json").read_text())
+    # every arm records the kernel library's build contract key
+    from marlin_style_fluxbin_amd.w3_lut_deployment import w3_lut_extension_build
+
+    assert record["provenance"]["w3_kernel_build_cache_key"] == w3_lut_extension_build(256)[1]["cache_key"]
+    kept = dict(record)
+    record["provenance"] = dict(record["provenance"], w3_kernel_build_cache_key="0" * 64)
+    (out / "arms" / "decoded_w3_bf16.json").write_text(json.dumps(record))
+    with pytest.raises(ValueError, match="resumable"):
+        ppl.main(argv(out) + ["--resume"])
+    record = kept
     record["provenance"]["blocks_sha256"] = "0" * 64
     (out / "arms" / "decoded_w3_bf16.json").write_text(json.dumps(record))
     with pytest.raises(ValueError, match="resumable"):

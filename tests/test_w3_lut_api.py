@@ -190,6 +190,51 @@ def test_extension_loader_contract(monkeypatch):
         wl.load_w3_lut_extension.cache_clear()
 
 
+def test_extension_build_contract(monkeypatch, tmp_path):
+    """w3_lut_extension_build (reference w3_lut_deployment.py:49-68): one contract
+    for every row tile, a key over the canonical fields that follows source bytes
+    and flags but not documentation, and the reference's refusals."""
+    import hashlib
+    import json
+    import shutil
+
+    from marlin_style_fluxbin_amd import build
+
+    with pytest.raises(ValueError, match="row_tile"):
+        wl.w3_lut_extension_build(128)
+    with pytest.raises(ValueError, match="probe"):
+        wl.w3_lut_extension_build(256, uniform_index_probe=True)
+    contracts = [wl.w3_lut_extension_build(r)[1] for r in wl.EXPERIMENTAL_ROW_TILES]
+    assert all(c == contracts[0] for c in contracts)
+    kwargs, contract = wl.w3_lut_extension_build(256)
+    assert kwargs["row_tile"] == 256 and kwargs["library"].endswith("libfluxbin_amd.so")
+    names = {s["name"] for s in contract["sources"]}
+    assert {"capi.hip", "w3_mfma.hip", "common.h", "fluxbin_amd.h"} <= names
+    assert set(contract["compile_sources"]) == {p.name for p in build.CSRC.glob("*.hip")}
+    keyed = {k: v for k, v in contract.items()
+             if k not in ("cache_key", "compile_sources", "content_dependencies", "library_sha256")}
+    canonical = json.dumps(keyed, sort_keys=True, separators=(",", ":")).encode()
+    assert contract["cache_key"] == hashlib.sha256(canonical).hexdigest()
+
+    # a copy of the tree: one source byte or one flag moves the key, a note does not
+    pkg = tmp_path / "pkg"
+    shutil.copytree(build.CSRC, pkg / "csrc", ignore=shutil.ignore_patterns("*.o"))
+    (tmp_path / "include").mkdir()
+    shutil.copy(build.PACKAGE.parent / "include" / "fluxbin_amd.h", tmp_path / "include")
+    monkeypatch.setattr(build, "CSRC", pkg / "csrc")
+    monkeypatch.setattr(build, "PACKAGE", pkg)
+    base = wl.w3_lut_extension_build(512)[1]["cache_key"]
+    assert base == contract["cache_key"]
+    (pkg / "NOTES.md").write_text("documentation only\n")
+    assert wl.w3_lut_extension_build(512)[1]["cache_key"] == base
+    src = pkg / "csrc" / "norms.hip"
+    src.write_bytes(src.read_bytes() + b"\n")
+    edited = wl.w3_lut_extension_build(512)[1]["cache_key"]
+    assert edited != base
+    monkeypatch.setattr(build, "HIPCC_FLAGS", build.HIPCC_FLAGS + ["-DFX_EXTRA=1"])
+    assert wl.w3_lut_extension_build(512)[1]["cache_key"] not in (base, edited)
+
+
 def test_engine_backends_for_w3_and_hybrid_formats():
     from marlin_style_fluxbin_amd import deployment as d
     from marlin_style_fluxbin_amd.engine_interface import M1Backend, W3Backend, backend_for_format
