@@ -1,8 +1,11 @@
 """Dense materialisation of the two-base formats and tensor hashing.
 
-Reference: ``evaluation.py`` (``tensor_sha256`` :28-34,
-``materialize_global_two_base_weight`` :59-95, ``materialize_hybrid_s8_weight``
-:98-175).  The materialisers are the dequantize step of the two-base
+Reference: ``evaluation.py`` (``sha256_file`` :20-25, ``tensor_sha256`` :28-34,
+``sha256_token_sequences`` :37-45, ``materialize_global_two_base_weight`` :59-95,
+``materialize_hybrid_s8_weight`` :98-175, ``atomic_json`` :205-212).  The file and
+token-sequence hashes are the ones the artifact loader and the PPL harness record
+(``w3_lut_artifacts.sha256_file``, ``ppl.sha256_token_sequences``), so hashes
+recorded by either side compare.  The materialisers are the dequantize step of the two-base
 PackedHybridLinear's dense fallback; they run fp32 torch arithmetic in the
 reference's order (per base ``(sign * row) * col`` added to a zero start, the
 refinement formed the same way and scatter-added at its columns) and cast once.
@@ -11,10 +14,35 @@ from __future__ import annotations
 
 import hashlib
 import json
+import os
+from pathlib import Path
+from typing import Any, Iterable, Sequence
 
 import torch
 
 from .packing import unpack_two_bases
+
+
+def sha256_file(path: Path | str) -> str:
+    from .w3_lut_artifacts import sha256_file as digest
+
+    return digest(Path(path))
+
+
+def sha256_token_sequences(sequences: Iterable[Sequence[int]]) -> str:
+    from .ppl import sha256_token_sequences as digest
+
+    return digest(sequences)
+
+
+def atomic_json(path: Path | str, value: dict[str, Any]) -> None:
+    """Write ``value`` as sorted, indented JSON through a temporary file and one
+    rename, so a reader sees the old file or the new one, never a partial one."""
+    path = Path(path)
+    path.parent.mkdir(parents=True, exist_ok=True)
+    tmp = path.with_name(f".{path.name}.tmp-{os.getpid()}")
+    tmp.write_text(json.dumps(value, indent=2, sort_keys=True) + "\n", encoding="utf-8")
+    os.replace(tmp, path)
 
 
 def tensor_sha256(tensor: torch.Tensor) -> str:

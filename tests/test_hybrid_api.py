@@ -194,3 +194,80 @@ def test_real_qwen3_block_with_dense_fallback_is_bit_equal():
         out_new = out_new[0] if isinstance(out_new, tuple) else out_new
         assert torch.equal(out_ref, out_new)
     assert all(m.rows.dtype == torch.float32 for m in candidate.modules() if isinstance(m, d.PackedHybridLinear))
+
+
+@pytest.mark.parametrize("o,g", [(1, 1), (7, 3), (33, 4)])
+@pytest.mark.parametrize("kernel", ["v1", "v5_p512"])
+def test_structural_reference_matches_oracle(o, g, kernel):
+    """factored_reference.structural_reference (reference factored_reference.py:8-42)
+    on interleaved and planar layouts against the numpy oracle, which the oracle's
+    own tests pin to an independent factored dot."""
+    from marlin_style_fluxbin_amd.factored_reference import structural_reference
+
+    p = payload(o, g, seed=o + g)
+    layout = d.convert_artifact(p, kernel=kernel)
+    x = torch.randn(1, 128 * g, generator=torch.Generator().manual_seed(g), dtype=torch.float64)
+    got = structural_reference(x, layout)
+    want = tb.structural_reference(x.numpy(), {k: v.numpy() for k, v in layout.items()})
+    assert got.dtype == torch.float64 and got.shape == (1, o)
+    np.testing.assert_allclose(got.numpy(), want, rtol=1e-12, atol=1e-12)
+    with pytest.raises(ValueError, match="G\\*128"):
+        structural_reference(x[:, :64], layout)
+
+
+def test_structural_reference_known_answer():
+    """All signs +1, unit scales: every main weight is 2; the refinement (signs +1,
+    row scales 1 and 2, column scale 1) adds 3 at its columns."""
+    from marlin_style_fluxbin_amd.factored_reference import structural_reference
+
+    o = 3
+    layout = {
+        "codes": torch.full((1, o, 32), 0xFF, dtype=torch.uint8),
+        "rows": torch.ones(1, o, 2), "columns": torch.ones(1, 128, 2),
+        "indices": torch.tensor([[0, 5, 9, 40, 64, 77, 100, 127]], dtype=torch.int16),
+        "sparse_codes": torch.full((1, o, 2), 0xFF, dtype=torch.uint8),
+        "sparse_rows": torch.tensor([[[1.0, 2.0]] * o]), "sparse_columns": torch.ones(1, 8, 2),
+    }
+    x = torch.zeros(1, 128, dtype=torch.float64)
+    x[0, 5], x[0, 6] = 1.0, 10.0  # a refined and an unrefined column
+    y = structural_reference(x, layout)
+    assert torch.equal(y, torch.full((1, o), 2.0 * 1 + 3.0 * 1 + 2.0 * 10, dtype=torch.float64))
+
+
+def test_structural_gate_thresholds():
+    """structural_gate: bf16 outputs within 0.02 (rms + |e|) elementwise and NRMSE
+    0.005 pass; fp32 outputs keep numerical_gate's 0.002 bars; the record names the
+    reference."""
+    from marlin_style_fluxbin_amd.factored_reference import REFERENCE, structural_gate
+
+    e = torch.linspace(-1, 1, 64, dtype=torch.float64)[None]
+    rms = float(e.square().mean().sqrt())
+    ok = structural_gate((e * (1 + 2e-3)).to(torch.bfloat16), e)
+    assert ok["passed"] and ok["reference"] == REFERENCE and ok["normalized_rmse_limit"] == 0.005
+    bad = e.clone()
+    bad[0, 3] += 0.05 * (rms + abs(float(e[0, 3])))
+    assert not structural_gate(bad.to(torch.bfloat16), e)["passed"]
+    spread = structural_gate((e * 1.008).to(torch.bfloat16), e)  # NRMSE 0.008 > 0.005
+    assert not spread["passed"]
+    f32 = structural_gate((e * (1 + 2e-3)).float(), e)
+    assert not f32["passed"] and f32["elementwise_tolerance_factor"] == 0.002
+    assert not structural_gate(torch.full_like(e, float("nan")).to(torch.bfloat16), e)["passed"]
+
+
+def test_evaluation_hashes_and_atomic_json(tmp_path):
+    """evaluation.sha256_file / sha256_token_sequences / atomic_json (reference
+    evaluation.py:20-45,205-212): the token framing is a big-endian uint64 length
+    then big-endian int64 tokens per sequence; the file hash is the plain digest."""
+    import hashlib
+    import json
+    import struct
+
+    from marlin_style_fluxbin_amd import evaluation as ev
+
+    framed = struct.pack(">Q", 2) + struct.pack(">qq", 1, -2) + struct.pack(">Q", 0)
+    assert ev.sha256_token_sequences([[1, -2], []]) == hashlib.sha256(framed).hexdigest()
+    target = tmp_path / "sub" / "record.json"
+    ev.atomic_json(target, {"b": [1, 2], "a": 0.5})
+    assert json.loads(target.read_text()) == {"a": 0.5, "b": [1, 2]}
+    assert target.read_text().startswith('{\n  "a"') and not list(target.parent.glob(".*tmp*"))
+    assert ev.sha256_file(target) == hashlib.sha256(target.read_bytes()).hexdigest()

@@ -350,3 +350,21 @@ def test_rmsnormed_prologue(gpu, widths, g, dtype):
         fused.sparse_rows.data_ptr(), fused._scols_ptrs, sums.data_ptr(), sums.numel() + 1, weight.data_ptr(), 1e-6,
         None, 0, got.data_ptr(), k, None)
     assert rc == 1 and "n_tiles" in lib.fx_last_error().decode()
+
+
+@pytest.mark.parametrize("o,g", [(4096, 32), (12288, 32)])
+def test_packed_linear_passes_the_product_structural_gate(gpu, o, g):
+    """The reference trial's check: a packed hybrid Linear's bf16 output against
+    factored_reference.structural_reference under structural_gate, both computed
+    on the GPU from the module's own layout."""
+    from marlin_style_fluxbin_amd.factored_reference import structural_gate, structural_reference
+
+    p = _payload(o, g, seed=o)
+    module = d.PackedHybridLinear(p, kernel="v5_p1024").to(gpu)
+    x = torch.randn(1, g * 128, generator=torch.Generator().manual_seed(5)).to(torch.bfloat16).to(gpu)
+    with torch.inference_mode():
+        y = module(x)
+        expected = structural_reference(x, module.layout())
+    gate = structural_gate(y, expected)
+    assert gate["passed"], gate
+    np.testing.assert_allclose(expected.cpu().numpy(), _reference(x, p), rtol=1e-12, atol=1e-12)
