@@ -297,6 +297,8 @@ class PackedHybridLinear(PackedLinearBase):
     (move with ``.to(device)``, never ``.half()``): both routes check them.
     """
 
+    bias_in_place = False
+
     def __init__(self, payload, *, bias=None, fallback="error", groups_per_split=8, kernel="v1"):
         super().__init__()
         if kernel not in KERNELS:

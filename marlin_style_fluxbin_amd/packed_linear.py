@@ -38,6 +38,10 @@ class PackedLinearBase(nn.Module):
     """Route selection, fallback policy, counters and the prepared binding."""
 
     max_packed_rows = 1
+    # forward's bias add: in place into the output (its dtype kept: PackedW3Linear,
+    # w3_lut_deployment.py:357-358) or out of place (type promotion: the hybrid
+    # Linear, deployment.py:295-296); the bound decode route adds in place for both
+    bias_in_place = True
 
     def _init_protocol(self, *, fallback: str, bias: torch.Tensor | None) -> None:
         if fallback not in ("error", "dense"):
@@ -151,7 +155,7 @@ class PackedLinearBase(nn.Module):
         out = torch.empty((rows, self.out_features), device=x.device, dtype=x.dtype)
         self._packed_kernel(rows, x.device)(x.reshape(rows, self.in_features).contiguous(), out)
         if self.bias is not None:
-            out = out + self.bias
+            out = out.add_(self.bias) if self.bias_in_place else out + self.bias
         return out.reshape(*x.shape[:-1], self.out_features)
 
 

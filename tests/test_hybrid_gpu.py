@@ -368,3 +368,22 @@ def test_packed_linear_passes_the_product_structural_gate(gpu, o, g):
     gate = structural_gate(y, expected)
     assert gate["passed"], gate
     np.testing.assert_allclose(expected.cpu().numpy(), _reference(x, p), rtol=1e-12, atol=1e-12)
+
+
+def test_bias_add_promotes_as_the_reference_does(gpu):
+    """PackedHybridLinear's forward adds its bias out of place (deployment.py:
+    295-296): a float32 bias gives a float32 output; the bound decode route adds
+    it in place into its bf16 buffer (:262)."""
+    o, g = 64, 2
+    p = _payload(o, g, seed=11)
+    bias = torch.randn(o, generator=torch.Generator().manual_seed(4)).to(gpu)
+    x = torch.randn(1, g * 128, generator=torch.Generator().manual_seed(6)).to(torch.bfloat16).to(gpu)
+    plain = d.PackedHybridLinear(p, kernel="v5_p1024").to(gpu)
+    module = d.PackedHybridLinear(p, bias=bias, kernel="v5_p1024").to(gpu)
+    with torch.inference_mode():
+        y0 = plain(x)
+        y = module(x)
+        assert y.dtype == torch.float32 and torch.equal(y, y0 + bias)
+        module.bind_prepared_decode(torch.bfloat16)
+        yb = module(x.view(1, 1, -1))
+        assert yb.dtype == torch.bfloat16 and torch.equal(yb.view(1, o), (y0.float() + bias).to(torch.bfloat16))

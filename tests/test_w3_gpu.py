@@ -268,6 +268,25 @@ def test_dense_fallback_on_gpu_uses_device_restore(gpu):
     assert_rel(y.float().cpu().numpy(), decoded, 1e-2)
 
 
+def test_bias_is_added_in_place_as_the_reference_does(gpu):
+    """PackedW3Linear adds its bias into the output in place (w3_lut_deployment.py:
+    313-314, 357-358): a float32 bias leaves a bf16 output bf16, on the packed route
+    and on the bound decode route, and the sum is rounded once."""
+    layout, dl, ol = _setup(64, 256, seed=9, zeros=False)
+    bias = torch.randn(64, generator=torch.Generator().manual_seed(3)).to(gpu)
+    x = _x(1, 256, torch.bfloat16, seed=9).to(gpu)
+    plain = PackedW3Linear(dl, row_tile=256)
+    module = PackedW3Linear(dl, bias=bias, row_tile=256)
+    with torch.inference_mode():
+        y0 = plain(x)
+        y = module(x)
+        assert y.dtype == torch.bfloat16
+        assert torch.equal(y, (y0.float() + bias).to(torch.bfloat16))
+        module.bind_prepared_decode(torch.bfloat16)
+        yb = module(x.view(1, 1, 256))
+        assert yb.dtype == torch.bfloat16 and torch.equal(yb.view(1, 64), y)
+
+
 @pytest.mark.parametrize("o,k", [(4096, 4096), (12288, 4096), (4096, 12288), (1024, 4096)])
 @pytest.mark.parametrize("route", ["fast_corrected", "observed_exact", "structural"])
 def test_module_routes_follow_the_reference_split_contract(gpu, o, k, route):
