@@ -211,6 +211,14 @@ def test_structural_reference_matches_oracle(o, g, kernel):
     want = tb.structural_reference(x.numpy(), {k: v.numpy() for k, v in layout.items()})
     assert got.dtype == torch.float64 and got.shape == (1, o)
     np.testing.assert_allclose(got.numpy(), want, rtol=1e-12, atol=1e-12)
+    # its own bf16 rounding passes the gate; the bf16-weight dense product is a
+    # different (rounded-weight) result (reference tests/test_factored_reference.py:21-24)
+    from marlin_style_fluxbin_amd.factored_reference import structural_gate
+
+    assert structural_gate(got.to(torch.bfloat16), got)["passed"]
+    if o * g >= 21:
+        legacy = x @ d.decode_layout(layout, torch.bfloat16).double().t()
+        assert float((got - legacy).abs().max()) > 1e-5
     with pytest.raises(ValueError, match="G\\*128"):
         structural_reference(x[:, :64], layout)
 
