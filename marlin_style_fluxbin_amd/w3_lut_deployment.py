@@ -177,7 +177,8 @@ def w3_lut_extension_build(row_tile: int, uniform_index_probe: bool = False) -> 
     contract["content_dependencies"] = [p.name for p in sources if p.suffix == ".h"] + [p.name for p in dependencies]
     library = _lib.LIBRARY_PATH
     contract["library_sha256"] = hashlib.sha256(library.read_bytes()).hexdigest() if library.is_file() else None
-    kwargs = {"name": contract["name"], "sources": [str(p) for p in sources], "library": str(library),
+    kwargs = {"name": contract["name"], "sources": [str(p) for p in sources if p.suffix == ".hip"],
+              "library": str(library),
               "extra_hip_cflags": list(_build.HIPCC_FLAGS), "row_tile": row_tile}
     return kwargs, contract
 

@@ -231,6 +231,14 @@ def test_extension_build_contract(monkeypatch, tmp_path):
     src.write_bytes(src.read_bytes() + b"\n")
     edited = wl.w3_lut_extension_build(512)[1]["cache_key"]
     assert edited != base
+    # a header is a content dependency: it moves the key but is not a compile source
+    header = pkg / "csrc" / "common.h"
+    header.write_bytes(header.read_bytes() + b"\n")
+    kwargs2, contract2 = wl.w3_lut_extension_build(512)
+    assert contract2["cache_key"] not in (base, edited)
+    assert all(s.endswith(".hip") for s in kwargs2["sources"]) and "common.h" in contract2["content_dependencies"]
+    edited = contract2["cache_key"]
+    assert "git" not in contract2
     monkeypatch.setattr(build, "HIPCC_FLAGS", build.HIPCC_FLAGS + ["-DFX_EXTRA=1"])
     assert wl.w3_lut_extension_build(512)[1]["cache_key"] not in (base, edited)
 
