@@ -42,6 +42,12 @@ def sources() -> list[Path]:
     return sorted(CSRC.glob("*.hip"), key=lambda p: (p.name != "capi.hip", p.name))
 
 
+def compile_units() -> list[Path]:
+    """The translation units hipcc compiles; w3_lut.hip holds kernel templates only
+    and is included by its instantiation units, not compiled alone."""
+    return [s for s in sources() if s.name != "w3_lut.hip"]
+
+
 def _compile(source: Path, obj: Path, verbose: bool) -> subprocess.CompletedProcess:
     cmd = [hipcc(), *HIPCC_FLAGS, "-c", "-I", str(PACKAGE.parent / "include"),
            str(source), "-o", str(obj)]
@@ -54,8 +60,7 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
     """Always recompile (the build check must compile every time it is called)."""
     from concurrent.futures import ThreadPoolExecutor
 
-    # w3_lut.hip holds kernel templates only; it is included, not compiled alone.
-    units = [s for s in sources() if s.name != "w3_lut.hip"]
+    units = compile_units()
     objdir = PACKAGE / "_build"
     objdir.mkdir(exist_ok=True)
     objects = [objdir / (s.stem + ".o") for s in units]

@@ -173,11 +173,12 @@ def w3_lut_extension_build(row_tile: int, uniform_index_probe: bool = False) -> 
     }
     encoded = json.dumps(contract, sort_keys=True, separators=(",", ":")).encode()
     contract["cache_key"] = hashlib.sha256(encoded).hexdigest()
-    contract["compile_sources"] = [p.name for p in sources if p.suffix == ".hip"]
-    contract["content_dependencies"] = [p.name for p in sources if p.suffix == ".h"] + [p.name for p in dependencies]
+    units = {p.name for p in _build.compile_units()}
+    contract["compile_sources"] = [p.name for p in sources if p.name in units]
+    contract["content_dependencies"] = [p.name for p in sources + dependencies if p.name not in units]
     library = _lib.LIBRARY_PATH
     contract["library_sha256"] = hashlib.sha256(library.read_bytes()).hexdigest() if library.is_file() else None
-    kwargs = {"name": contract["name"], "sources": [str(p) for p in sources if p.suffix == ".hip"],
+    kwargs = {"name": contract["name"], "sources": [str(p) for p in sources if p.name in units],
               "library": str(library),
               "extra_hip_cflags": list(_build.HIPCC_FLAGS), "row_tile": row_tile}
     return kwargs, contract

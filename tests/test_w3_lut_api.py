@@ -197,6 +197,7 @@ def test_extension_build_contract(monkeypatch, tmp_path):
     import hashlib
     import json
     import shutil
+    from pathlib import Path
 
     from marlin_style_fluxbin_amd import build
 
@@ -210,7 +211,8 @@ def test_extension_build_contract(monkeypatch, tmp_path):
     assert kwargs["row_tile"] == 256 and kwargs["library"].endswith("libfluxbin_amd.so")
     names = {s["name"] for s in contract["sources"]}
     assert {"capi.hip", "w3_mfma.hip", "common.h", "fluxbin_amd.h"} <= names
-    assert set(contract["compile_sources"]) == {p.name for p in build.CSRC.glob("*.hip")}
+    assert set(contract["compile_sources"]) == {p.name for p in build.compile_units()}
+    assert "w3_lut.hip" in contract["content_dependencies"]  # included by its instantiation units
     keyed = {k: v for k, v in contract.items()
              if k not in ("cache_key", "compile_sources", "content_dependencies", "library_sha256")}
     canonical = json.dumps(keyed, sort_keys=True, separators=(",", ":")).encode()
@@ -236,7 +238,8 @@ def test_extension_build_contract(monkeypatch, tmp_path):
     header.write_bytes(header.read_bytes() + b"\n")
     kwargs2, contract2 = wl.w3_lut_extension_build(512)
     assert contract2["cache_key"] not in (base, edited)
-    assert all(s.endswith(".hip") for s in kwargs2["sources"]) and "common.h" in contract2["content_dependencies"]
+    assert {Path(s).name for s in kwargs2["sources"]} == set(contract2["compile_sources"])
+    assert "common.h" in contract2["content_dependencies"]
     edited = contract2["cache_key"]
     assert "git" not in contract2
     monkeypatch.setattr(build, "HIPCC_FLAGS", build.HIPCC_FLAGS + ["-DFX_EXTRA=1"])
