@@ -22,6 +22,23 @@ def test_numerical_gate_thresholds():
     nan = b.clone()
     nan[0] = float("nan")
     assert numerical_gate(nan, b)["reason"] == "nonfinite output"
+    # the reference's zero-reference cases (tests/test_acceleration_preparation.py:16-21)
+    zero = torch.zeros(1, 7, dtype=torch.bfloat16)
+    assert numerical_gate(zero, zero)["passed"]
+    assert not numerical_gate(torch.ones_like(zero), zero)["passed"]
+    assert not numerical_gate(zero + float("nan"), zero)["passed"]
+    assert not numerical_gate(torch.zeros(2, 7), zero)["passed"]
+
+
+def test_engine_backend_contract_known_answers():
+    """M1Backend's contract (reference tests/test_acceleration_preparation.py:23-28)."""
+    from marlin_style_fluxbin_amd.engine_interface import M1Backend
+
+    backend = M1Backend()
+    assert backend.contract.supported_m == (1,) and not backend.contract.tensor_parallel
+    assert backend.workspace_shape(4096, 12288) == (12, 4096)
+    with pytest.raises(ValueError):
+        M1Backend(0)
 
 
 def test_stepwise_nrmse():
