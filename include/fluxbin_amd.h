@@ -42,9 +42,11 @@ extern "C" {
 #define FX_ARITH_DECODED_BF16 1 /* + per-weight bf16 rounding of s*(q-z) (bf16 scales, zero 3 or 4) */
 
 /* Payload formats of the one-row decode GEMVs: the reference's planar layout, or
- * the library's field layout (fx_w3_planes_to_fields; the same sorted column order). */
+ * the library's field layout (fx_w3_planes_to_fields) or fp6 layout
+ * (fx_w3_planes_to_fp6), both in the same sorted column order. */
 #define FX_W3_PLANAR 0
 #define FX_W3_FIELDS 1
+#define FX_W3_FP6 2
 
 /* ABI version of this header (bumped on any signature change). */
 int fx_abi_version(void);
@@ -149,8 +151,9 @@ int fx_w3_gemv_swiglu(const void *x, int x_dtype, const uint8_t *planes, const v
  * GEMV's perm, that GEMV's result is bit-identical to the same GEMV given the
  * row-ordered activation and the perm.  Entries outside [0, outputs) are not
  * written.
- * payload_format (all): FX_W3_PLANAR, or FX_W3_FIELDS with `planes` holding the
- * field layout. */
+ * payload_format (all): FX_W3_PLANAR, FX_W3_FIELDS with `planes` holding the
+ * field layout, or FX_W3_FP6 with `planes` holding the fp6 layout (bf16
+ * activations, no perm, O % 16 == 0, K % 512 == 0). */
 int fx_w3_gemv_residual(const void *x, int x_dtype, const uint8_t *planes, const void *scales,
                         int scale_dtype, const uint8_t *zeros, const int16_t *perm, const void *residual,
                         void *out, float *tile_sumsq, const int16_t *out_index, void *sorted_out, int O, int K,
@@ -188,6 +191,25 @@ int fx_w3_planes_to_fields(const uint8_t *planes, uint8_t *fields, int O, int K,
  * arithmetic (fp32 accumulation of exact products; the sum order differs). */
 int fx_w3_gemv_fields(const void *x, int x_dtype, const uint8_t *fields, const void *scales, int scale_dtype,
                       const uint8_t *zeros, void *out, int O, int K, void *stream);
+/* No reference counterpart: a second bind-time repack of the planes, for
+ * gfx950's v_mfma_scale_f32_16x16x128_f8f6f4 with fp6 e2m3 weight operands (a
+ * field with zero sign and exponent bits and the code in its mantissa is exactly
+ * q / 8).  Same byte count as the planes, ordered [K / 512, O, k-block (4),
+ * group slot (4), 3 words]: field e of A lane block kb multiplies group column
+ * 32 (2 (kb % 2) + e / 16) + 16 (kb / 2) + e % 16, and the three words expand
+ * into the six fp6 registers with two masks, two shift-and-masks and one
+ * register that takes bits 29, 30 from bits 1, 2 of the third word (M0 =
+ * 0xC71C71C7 for registers 0, 3; M1 = 0x71C71C71 for 1, 4; M2 = 0x1C71C71C for
+ * 2, 5, of the first words shifted right by one).  K a multiple of 512; fp6
+ * must not alias planes; both 16-byte aligned. */
+int fx_w3_planes_to_fp6(const uint8_t *planes, uint8_t *fp6, int O, int K, void *stream);
+/* One-row structural GEMV on the fp6 layout: out [1, O] = x [1, K] @ W.T with x
+ * bf16 in sorted column order, each group's activations split into two fp8 e4m3
+ * digits (exact down to 2^-10 of the group's max|x|), one scaled matrix
+ * instruction per group and 16-row tile, fp32 accumulation.  O a multiple of
+ * 16, K of 512. */
+int fx_w3_gemv_fp6(const void *x, int x_dtype, const uint8_t *fp6, const void *scales, int scale_dtype,
+                   const uint8_t *zeros, void *out, int O, int K, void *stream);
 /* Field-layout GEMV of M <= 8 activation rows (no single counterpart: the
  * small-M route of w3_lut_deployment.py:327-333 on the bind-time field layout):
  * out [M, O] = x [M, K] @ W.T, structural arithmetic.  One row is

@@ -15,8 +15,8 @@ from pathlib import Path
 import torch
 
 LIBRARY_PATH = Path(__file__).resolve().parent / "libfluxbin_amd.so"
-ABI_VERSION = 18
-PAYLOAD_PLANAR, PAYLOAD_FIELDS = 0, 1  # FX_W3_PLANAR / FX_W3_FIELDS
+ABI_VERSION = 19
+PAYLOAD_PLANAR, PAYLOAD_FIELDS, PAYLOAD_FP6 = 0, 1, 2  # FX_W3_PLANAR / FX_W3_FIELDS / FX_W3_FP6
 
 FX_F32, FX_F16, FX_BF16 = 0, 1, 2
 ARITH_STRUCTURAL, ARITH_DECODED_BF16 = 0, 1
@@ -46,6 +46,8 @@ SIGNATURES: dict[str, tuple] = {
                                         _p, ctypes.c_longlong, _p, ctypes.c_longlong, _i, _i, _i, _i, _p]),
     "fx_w3_planes_to_fields": (_i, [_p, _p, _i, _i, _p]),
     "fx_w3_gemv_fields": (_i, [_p, _i, _p, _p, _i, _p, _p, _i, _i, _p]),
+    "fx_w3_planes_to_fp6": (_i, [_p, _p, _i, _i, _p]),
+    "fx_w3_gemv_fp6": (_i, [_p, _i, _p, _p, _i, _p, _p, _i, _i, _p]),
     "fx_w3_fields_plan": (_i, [_i, _i, _i, _i]),
     "fx_w3_gemv_fields_rows": (_i, [_p, _i, _p, _p, _i, _p, _p, _i, _i, _i, _p]),
     "fx_w3_gemv_config_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _i, _i]),

@@ -568,7 +568,7 @@ bool two_base_config(int O, int G, int waves, int prefetch, int groups_per_split
 
 extern "C" {
 
-int fx_abi_version(void) { return 18; }
+int fx_abi_version(void) { return 19; }
 
 const char* fx_last_error(void) { return g_error; }
 
@@ -713,8 +713,8 @@ MfmaPlan single_split_plan(int O, int G) {
 
 // Payload format check of the one-row entry points.
 int check_format(int payload_format) {
-  if (payload_format != FX_W3_PLANAR && payload_format != FX_W3_FIELDS)
-    return fail(FX_EINVAL, "payload_format must be FX_W3_PLANAR or FX_W3_FIELDS, got %d", payload_format);
+  if (payload_format != FX_W3_PLANAR && payload_format != FX_W3_FIELDS && payload_format != FX_W3_FP6)
+    return fail(FX_EINVAL, "payload_format must be FX_W3_PLANAR, FX_W3_FIELDS or FX_W3_FP6, got %d", payload_format);
   return FX_OK;
 }
 
@@ -781,6 +781,26 @@ int run_fields(const MfmaArgs& base, int x_dtype, int scale_dtype, bool normin, 
   if (!fx::dispatch_mfma_fields(p.nw, normin, x_dtype, scale_dtype, a, dim3(p.row_blocks, batch), s))
     return fail(FX_EINVAL, "no field-layout MFMA kernel for waves %d", p.nw);
   return check_launch("w3_mfma_kernel (field layout)");
+}
+
+// One-row fp6-layout launch (one K split, batch payloads on grid.y when a.batch
+// is set): bf16 activations in sorted column order, O % 16 == 0, K % 512 == 0.
+int run_fp6(const MfmaArgs& base, int x_dtype, int scale_dtype, bool normin, hipStream_t s, int batch = 1) {
+  if (x_dtype != FX_BF16) return fail(FX_EINVAL, "the fp6 layout takes bf16 activations");
+  if (base.perm) return fail(FX_EINVAL, "the fp6 layout takes activations in sorted column order (no permutation)");
+  if (base.O % 16 || base.G % 4) return fail(FX_EINVAL, "the fp6 layout needs O %% 16 == 0 and K %% 512 == 0");
+  MfmaPlan p = single_split_plan(base.O, base.G);
+  const int tiles = fx::fields_row_tiles(normin, base.O);
+  if (tiles != p.tiles) p = make_mfma_plan(base.O, base.G, p.nw, 1, base.G, tiles);
+  if (batch > 1 && p.row_blocks % 8)
+    return fail(FX_EINVAL, "a batch needs O / 16 to be a multiple of 8 (XCD-aligned row blocks), got O = %d", base.O);
+  MfmaArgs a = base;
+  a.gps = p.gps;
+  a.row_blocks = p.row_blocks;
+  a.x_lds = 0;
+  if (!fx::dispatch_mfma_fp6(p.nw, normin, scale_dtype, a, dim3(p.row_blocks, batch), s))
+    return fail(FX_EINVAL, "no fp6-layout MFMA kernel for waves %d", p.nw);
+  return check_launch("w3_mfma_kernel (fp6 layout)");
 }
 
 // Field-layout GEMV of M <= 8 activation rows.  One row: run_fields.  More: the
@@ -877,6 +897,20 @@ int fx_w3_gemv_swiglu(const void* x, int x_dtype, const uint8_t* planes, const v
     a.res.ep_index = out_index;
     return run_fields(a, x_dtype, scale_dtype, false, static_cast<hipStream_t>(stream));
   }
+  if (payload_format == FX_W3_FP6) {
+    MfmaArgs a{};
+    a.x = static_cast<const uint16_t*>(x);
+    a.perm = perm;
+    a.planes = planes;
+    a.scales = static_cast<const uint16_t*>(scales);
+    a.zeros = zeros;
+    a.out = static_cast<uint16_t*>(out);
+    a.O = O;
+    a.G = G;
+    a.swiglu = 1;
+    a.res.ep_index = out_index;
+    return run_fp6(a, x_dtype, scale_dtype, false, static_cast<hipStream_t>(stream));
+  }
   MfmaPlan p = default_mfma_plan(O, G);
   if (p.splits > 1) p = make_mfma_plan(O, G, 8, 1, G, 1);  // the fused epilogue needs one K split
   return run_mfma(x, x_dtype, planes, scales, scale_dtype, zeros, perm, nullptr, 0, out, 1, O, K, p,
@@ -913,6 +947,7 @@ int fx_w3_gemv_residual(const void* x, int x_dtype, const uint8_t* planes, const
   a.res.ep_index = out_index;
   a.res.ep_sorted = static_cast<uint16_t*>(sorted_out);
   if (payload_format == FX_W3_FIELDS) return run_fields(a, x_dtype, scale_dtype, false, static_cast<hipStream_t>(stream));
+  if (payload_format == FX_W3_FP6) return run_fp6(a, x_dtype, scale_dtype, false, static_cast<hipStream_t>(stream));
   a.x_lds = perm && fx::x_lds_fits(1, K, p.nw);
   if (!fx::dispatch_mfma(x_dtype, 1, p.nw, 1, 1, scale_dtype, a, dim3(p.row_blocks, 1), static_cast<hipStream_t>(stream)))
     return fail(FX_EINVAL, "no MFMA kernel for waves %d", p.nw);
@@ -952,6 +987,7 @@ int fx_w3_gemv_rmsnormed(const void* h, int x_dtype, const uint8_t* planes, cons
   a.res.pro_eps = eps;
   a.res.ep_index = out_index;
   if (payload_format == FX_W3_FIELDS) return run_fields(a, x_dtype, scale_dtype, true, static_cast<hipStream_t>(stream));
+  if (payload_format == FX_W3_FP6) return run_fp6(a, x_dtype, scale_dtype, true, static_cast<hipStream_t>(stream));
   if (!fx::dispatch_mfma_normin(p.nw, x_dtype, scale_dtype, a, dim3(p.row_blocks, 1), static_cast<hipStream_t>(stream)))
     return fail(FX_EINVAL, "no normalising MFMA kernel for waves %d", p.nw);
   return check_launch("w3_mfma_kernel (normalising prologue)");
@@ -974,7 +1010,7 @@ int fx_w3_gemv_strided_batched(const void* x, int x_dtype, long long x_stride, c
   if (planes_stride % 16 || x_stride % 8)
     return fail(FX_EINVAL, "planes stride must be a multiple of 16 bytes and x stride of 8 elements");
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  if (payload_format == FX_W3_FIELDS) {
+  if (payload_format == FX_W3_FIELDS || payload_format == FX_W3_FP6) {
     MfmaArgs a{};
     a.x = static_cast<const uint16_t*>(x);
     a.planes = planes;
@@ -984,7 +1020,8 @@ int fx_w3_gemv_strided_batched(const void* x, int x_dtype, long long x_stride, c
     a.O = O;
     a.G = G;
     if (batch > 1) a.batch = fx::StridedArgs{x_stride, planes_stride, scales_stride, zeros_stride, out_stride};
-    return run_fields(a, x_dtype, scale_dtype, false, s, batch);
+    return payload_format == FX_W3_FP6 ? run_fp6(a, x_dtype, scale_dtype, false, s, batch)
+                                       : run_fields(a, x_dtype, scale_dtype, false, s, batch);
   }
   MfmaPlan p = single_split_plan(O, G);
   if (batch > 1 && p.row_blocks % 8)
@@ -1014,6 +1051,32 @@ int fx_w3_planes_to_fields(const uint8_t* planes, uint8_t* fields, int O, int K,
   if (planes == fields) return fail(FX_EINVAL, "the repack cannot run in place");
   fx::launch_planes_to_fields(planes, fields, O, K / 128, static_cast<hipStream_t>(stream));
   return check_launch("w3_planes_to_fields_kernel");
+}
+
+int fx_w3_planes_to_fp6(const uint8_t* planes, uint8_t* fp6, int O, int K, void* stream) {
+  if (!planes || !fp6) return fail(FX_EINVAL, "planes and fp6 must be non-null");
+  if (O < 1 || K < 512 || K % 512) return fail(FX_EINVAL, "O must be positive and K a multiple of 512");
+  if (reinterpret_cast<uintptr_t>(planes) % 16 != 0 || reinterpret_cast<uintptr_t>(fp6) % 16 != 0)
+    return fail(FX_EINVAL, "planes and fp6 must be 16-byte aligned");
+  if (planes == fp6) return fail(FX_EINVAL, "the repack cannot run in place");
+  fx::launch_planes_to_fp6(planes, fp6, O, K / 128, static_cast<hipStream_t>(stream));
+  return check_launch("w3_planes_to_fp6_kernel");
+}
+
+int fx_w3_gemv_fp6(const void* x, int x_dtype, const uint8_t* fp6, const void* scales, int scale_dtype,
+                   const uint8_t* zeros, void* out, int O, int K, void* stream) {
+  int rc = validate_payload(x, x_dtype, fp6, scales, scale_dtype, 1, O, K, FX_ARITH_STRUCTURAL);
+  if (rc) return rc;
+  if (!out) return fail(FX_EINVAL, "out must be non-null");
+  MfmaArgs a{};
+  a.x = static_cast<const uint16_t*>(x);
+  a.planes = fp6;
+  a.scales = static_cast<const uint16_t*>(scales);
+  a.zeros = zeros;
+  a.out = static_cast<uint16_t*>(out);
+  a.O = O;
+  a.G = K / 128;
+  return run_fp6(a, x_dtype, scale_dtype, false, static_cast<hipStream_t>(stream));
 }
 
 int fx_w3_gemv_fields(const void* x, int x_dtype, const uint8_t* fields, const void* scales, int scale_dtype,

@@ -104,6 +104,7 @@ constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
 constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
 constexpr int kDppHalfMirror = 0x141; // lane i <-> 7 - i within each half row
 constexpr int kDppMirror = 0x140;     // lane i <-> 15 - i within each row
+constexpr int kDppRowShl4 = 0x104;    // lane i reads lane i + 4 of its row (0 past the row end)
 
 // Sum / max over each 16-lane row; every lane of the row gets the same bits
 // (each step adds a lane's value to its partner's, and both partners form the

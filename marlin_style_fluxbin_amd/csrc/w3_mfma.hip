@@ -138,6 +138,60 @@ __device__ __forceinline__ void dequant_fields(unsigned w0, unsigned w1, unsigne
   a[3] = u32x4_t{w2 & M6, h2 & M0, h2 & M3, spare};
 }
 
+// fp6 layout (fx_w3_planes_to_fp6): a lane's three words for one group expand
+// into the six fp6 e2m3 registers of v_mfma_scale_f32_16x16x128_f8f6f4's A
+// operand (field e at bits [6 e, 6 e + 6): sign and exponent bits zero, the code
+// in the mantissa, the exact value q / 8).  Two masks, two shifted masks and one
+// register that takes bits 29 and 30 from the low end of the third word.
+typedef int i32x8_t __attribute__((ext_vector_type(8)));
+constexpr unsigned kFp6M0 = 0xC71C71C7u, kFp6M1 = 0x71C71C71u, kFp6M2 = 0x1C71C71Cu;
+__device__ __forceinline__ i32x8_t expand_fp6(unsigned s0, unsigned s1, unsigned s2) {
+  const unsigned mid = __builtin_amdgcn_bitop3_b32(s2 << 28, s2 >> 3, 0x60000000u, 0xE4);  // m ? a : b
+  return i32x8_t{int(s0 & kFp6M0), int(s2 & kFp6M1), int((s0 >> 1) & kFp6M2), int(s1 & kFp6M0),
+                 int(mid & kFp6M1), int((s1 >> 1) & kFp6M2), 0, 0};
+}
+
+// fp6-layout B operands of one lane's 8 bf16 activations: two fp8 e4m3 digits,
+// hi = fp8(x / S) and lo = fp8((x - hi S) / S) with S = 2^(e - 8) for the group's
+// max|x| in [2^(e-1), 2^e) (so |x| / S < 256, inside e4m3's range); hi + lo is x
+// exactly down to 2^-10 of the group's maximum (a bf16 value's 8 significant
+// bits split 4 + 4).  Returns the group's sum of x (exact values) and the
+// epilogue's exponent e - 5 (the A fields carry q / 8).
+__device__ __forceinline__ void stage_fp6_8(const float v[8], uint2& hi, uint2& lo, float& sum, int& exp_off) {
+  float mx = 0.f, sm = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    mx = fmaxf(mx, fabsf(v[i]));
+    sm += v[i];
+  }
+  mx = row16_max(mx);
+  sm = row16_sum(sm);
+  int e = 0;
+  if (mx > 0.f) frexpf(mx, &e);
+  e = max(e, -118);  // S stays a normal float; groups below 2^-118 flush toward zero
+  const float S = ldexpf(1.f, e - 8);
+  typedef short i16x2_t __attribute__((ext_vector_type(2)));
+  unsigned h[2], l[2];
+#pragma unroll
+  for (int w = 0; w < 2; ++w) {
+    const float* x = v + 4 * w;
+    i16x2_t a = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(i16x2_t{0, 0}, x[0], x[1], S, false);
+    a = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(a, x[2], x[3], S, true);
+    const unsigned hw = __builtin_bit_cast(unsigned, a);
+    typedef float f32x2_t __attribute__((ext_vector_type(2)));
+    const f32x2_t b01 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(hw, S, false);
+    const f32x2_t b23 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(hw, S, true);
+    i16x2_t c = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(i16x2_t{0, 0}, x[0] - b01.x, x[1] - b01.y, S, false);
+    c = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(c, x[2] - b23.x, x[3] - b23.y, S, true);
+    h[w] = hw;
+    l[w] = __builtin_bit_cast(unsigned, c);
+  }
+  hi = uint2{h[0], h[1]};
+  lo = uint2{l[0], l[1]};
+  sum = sm;
+  exp_off = e - 5;
+}
+
 // Mantissa position p of register i's codes in the field layout (the B operand
 // carries the matching 2^-p).
 constexpr int kFieldShift[16] = {0, 3, 6, 0, 3, 0, 3, 6, 0, 3, 0, 3, 6, 0, 3, 0};
@@ -271,7 +325,7 @@ struct MfmaShared {
 // keeps the load count per batch fixed, so the wait before staging covers only
 // the activations.
 template <int NW, int PD, int MB, int RT, bool PERM, int XDT, int SDT, bool NORMIN, bool VEC, bool FIELDS,
-          bool CORR>
+          bool CORR, bool FP6 = false>
 __device__ __forceinline__ void w3_mfma_body(
     MfmaShared<NW, MB, RT>& sh, const uint16_t* __restrict__ x, const int16_t* __restrict__ perm,
     const uint8_t* __restrict__ planes, const uint16_t* __restrict__ scales,
@@ -344,6 +398,15 @@ __device__ __forceinline__ void w3_mfma_body(
     rmc[h] = row < MB ? row : 0;
     bsrc[h] = ((cslot == kb && row < MB) ? my_stage + kb * kStageStride<MB> : bzero) + rmc[h];
   }
+  // FP6: the B operand of group slot g's instruction is this lane's 32 bytes of
+  // [slot][digit][k-block] in the stage when its column is g (hi digit) or 4 + g
+  // (lo digit), else zeros; D column g then holds the hi dot and 4 + g the lo dot
+  const u32x4_t* fp6_src[4];
+  if constexpr (FP6) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+      fp6_src[g] = (cslot == g && c < 8) ? my_stage + ((g * 2 + (c >> 2)) * 4 + kb) * 2 : bzero;
+  }
   const int plane_stride = O * 16;
   int prow[RT];  // the lane's A row of each tile, clamped into [0, O)
 #pragma unroll
@@ -376,13 +439,24 @@ __device__ __forceinline__ void w3_mfma_body(
     // groups past G: past the end -> zeros; rows past O read row O - 1 (never
     // stored), since the plane stride rides in the scalar offset, which the
     // range check does not cover
-    const int gbase = gb * 3 * O + lane_times_rows(kb, 3 * O);  // gb is wave-uniform
+    if constexpr (FP6) {
+      // [G / 4, O, k-block, slot, 3 words]: the lane's 48 bytes of the batch are contiguous
 #pragma unroll
-    for (int tt = 0; tt < RT; ++tt) {
-      const int poff = live ? (gbase + prow[tt]) * 16 : kOutOfRange;
-      L.w[tt][0] = load_b128_stream(rp, poff, 0);
-      L.w[tt][1] = load_b128_stream(rp, poff, plane_stride);
-      L.w[tt][2] = load_b128_stream(rp, poff, 2 * plane_stride);
+      for (int tt = 0; tt < RT; ++tt) {
+        const int poff = live ? ((gb >> 2) * O + prow[tt]) * 192 + kb * 48 : kOutOfRange;
+        L.w[tt][0] = load_b128_stream(rp, poff, 0);
+        L.w[tt][1] = load_b128_stream(rp, poff, 16);
+        L.w[tt][2] = load_b128_stream(rp, poff, 32);
+      }
+    } else {
+      const int gbase = gb * 3 * O + lane_times_rows(kb, 3 * O);  // gb is wave-uniform
+#pragma unroll
+      for (int tt = 0; tt < RT; ++tt) {
+        const int poff = live ? (gbase + prow[tt]) * 16 : kOutOfRange;
+        L.w[tt][0] = load_b128_stream(rp, poff, 0);
+        L.w[tt][1] = load_b128_stream(rp, poff, plane_stride);
+        L.w[tt][2] = load_b128_stream(rp, poff, 2 * plane_stride);
+      }
     }
     __builtin_amdgcn_sched_barrier(0);
     const int eoff = gb * O + lane_times_rows(cslot, O) + row0 + 4 * kb;
@@ -407,7 +481,20 @@ __device__ __forceinline__ void w3_mfma_body(
 
   // B operands of one batch for activation row m from this lane's 8 values.
   auto stage_row = [&](int m, const float v[8]) __attribute__((always_inline)) {
-    if constexpr (FIELDS) {
+    if constexpr (FP6) {
+      // the lane's 8 columns of slot kb sit in B k-block r / 4, bytes 8 (r % 4) ..
+      uint2 hi, lo;
+      float sm;
+      int ge;
+      stage_fp6_8(v, hi, lo, sm, ge);
+      uint2* st8 = reinterpret_cast<uint2*>(my_stage);
+      st8[((kb * 2 + 0) * 4 + (r >> 2)) * 4 + (r & 3)] = hi;
+      st8[((kb * 2 + 1) * 4 + (r >> 2)) * 4 + (r & 3)] = lo;
+      if (r == 0) {
+        gsum[wave][kb * MB + m] = sm;
+        gexp[wave][kb * MB + m] = ge;
+      }
+    } else if constexpr (FIELDS) {
       // the lane's 8 columns are elements 0..7 of step r, one 16-byte write
       u32x4_t o;
       float sm;
@@ -515,6 +602,26 @@ __device__ __forceinline__ void w3_mfma_body(
       for (int tt = 0; tt < RT; ++tt)
         zmask[tt] = ((L.za[tt] | zero_default) & 0xffu) == 4u ? 0xffffffffu : 0u;  // absent zero-points: 4
     }
+    if constexpr (FP6) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const u32x4_t b0 = fp6_src[g][0], b1 = fp6_src[g][1];
+        const i32x8_t bv = {int(b0.x), int(b0.y), int(b0.z), int(b0.w), int(b1.x), int(b1.y), int(b1.z), int(b1.w)};
+#pragma unroll
+        for (int tt = 0; tt < RT; ++tt) {
+          const u32x4_t* w = L.w[tt];  // slot g: words 3 g .. 3 g + 2 of the lane's twelve
+          const i32x8_t av = expand_fp6(w[(3 * g) / 4][(3 * g) % 4], w[(3 * g + 1) / 4][(3 * g + 1) % 4],
+                                        w[(3 * g + 2) / 4][(3 * g + 2) % 4]);
+          // A fp6 e2m3 (cbsz 2), B fp8 e4m3 (blgp 0), unit block scales (E8M0 127)
+          d[tt][0] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, d[tt][0], 2, 0, 0, 127, 0, 127);
+        }
+      }
+      // column g += column 4 + g: the lo digit's dot into the hi digit's lane
+#pragma unroll
+      for (int tt = 0; tt < RT; ++tt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) d[tt][0][j] += dpp_move<kDppRowShl4>(d[tt][0][j]);
+    } else
 #pragma unroll
     for (int word = 0; word < 4; ++word) {
       u32x4_t a[RT][4], ag[CORR ? RT : 1][4];
@@ -757,8 +864,9 @@ __device__ __forceinline__ void w3_mfma_body(
 // ep_index output, weights reordered once at bind time).
 // CORR: decoded_bf16 arithmetic (bf16 scales, zero-points 3 or 4; planar layout).
 template <int NW, int PD, int MB, int RT, bool PERM, int XDT, int SDT, bool NORMIN = false, int VSEL = 0,
-          bool FIELDS = false, bool CORR = false>
-__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(MB == 1 && RT == 1 && PD == 1 && !CORR ? 6 : 1)))
+          bool FIELDS = false, bool CORR = false, bool FP6 = false>
+__global__ __launch_bounds__(NW * 64)
+__attribute__((amdgpu_waves_per_eu(MB == 1 && RT == 1 && PD == 1 && !CORR && !FP6 ? 6 : 1)))
 void w3_mfma_kernel(
     const uint16_t* __restrict__ x, const int16_t* __restrict__ perm,
     const uint8_t* __restrict__ planes, const uint16_t* __restrict__ scales,
@@ -789,14 +897,16 @@ void w3_mfma_kernel(
   static_assert(!FIELDS || (MB == 1 && PD == 1), "field layout: one activation row, one batch in flight");
   static_assert(!(PERM && NORMIN), "the normalising prologue reads its activations in sorted order");
   static_assert(!CORR || (SDT == kBF16 && !FIELDS && !NORMIN), "decoded_bf16: bf16 scales, planar layout");
+  static_assert(!FP6 || (FIELDS && !PERM && !CORR && XDT == kBF16 && VSEL == 1),
+                "fp6 layout: one bf16 activation row, sorted columns, vector scale loads");
   __shared__ MfmaShared<NW, MB, RT> sh;
   extern __shared__ u32x4_t x_stage[];  // PERM with x_lds: x [MB, K], MB * K * 2 bytes of dynamic LDS
   if (VSEL == 1 || (VSEL == 0 && (O & 3) == 0))
-    w3_mfma_body<NW, PD, MB, RT, PERM, XDT, SDT, NORMIN, VSEL != 2, FIELDS, CORR>(sh, x, perm, planes, scales, zeros,
+    w3_mfma_body<NW, PD, MB, RT, PERM, XDT, SDT, NORMIN, VSEL != 2, FIELDS, CORR, FP6>(sh, x, perm, planes, scales, zeros,
                                                                            partial, out, O, G, gps, row_blocks,
                                                                            swiglu, ra, x_lds, x_stage, split);
   else
-    w3_mfma_body<NW, PD, MB, RT, PERM, XDT, SDT, NORMIN, VSEL == 1, FIELDS, CORR>(sh, x, perm, planes, scales, zeros,
+    w3_mfma_body<NW, PD, MB, RT, PERM, XDT, SDT, NORMIN, VSEL == 1, FIELDS, CORR, FP6>(sh, x, perm, planes, scales, zeros,
                                                                            partial, out, O, G, gps, row_blocks,
                                                                            swiglu, ra, x_lds, x_stage, split);
 }

@@ -162,6 +162,10 @@ inline bool dispatch_fields_wide(const WidePlan& p, int xdt, int sdt, int mode, 
 
 // The bind-time repack planes [G, 3, O, 16] -> fields [G, 3, O, 16].
 void launch_planes_to_fields(const uint8_t* planes, uint8_t* fields, int O, int G, hipStream_t s);
+// fp6 layout (G % 4 == 0): the bind-time repack and the one-row GEMV launches
+// (bf16 activations, vector scale loads; normin: two row tiles per wave).
+void launch_planes_to_fp6(const uint8_t* planes, uint8_t* out, int O, int G, hipStream_t s);
+bool dispatch_mfma_fp6(int nw, bool normin, int sdt, const MfmaArgs& a, dim3 grid, hipStream_t s);
 
 inline bool dispatch_mfma(int xdt, int tiles, int nw, int pd, int mb, int sdt, const MfmaArgs& a,
                           dim3 grid, hipStream_t s) {

@@ -300,3 +300,103 @@ def sorted_codes_from_fields(fields: np.ndarray) -> np.ndarray:
 def fields_from_planar(planes: np.ndarray) -> np.ndarray:
     """The bind-time repack: planes ``[G,3,O,16]`` -> fields ``[G,3,O,16]`` (same sorted order)."""
     return fields_from_sorted_codes(codes_from_planar(planes))
+
+
+# --------------------------------------------------------------------------- fp6 layout
+# A second bind-time repack (no reference counterpart), for gfx950's
+# v_mfma_scale_f32_16x16x128_f8f6f4 with fp6 e2m3 A operands: a 6-bit field
+# with zero sign and exponent bits and the code q in its three mantissa bits is
+# exactly q / 8.  One instruction covers a 16-row tile and one group (128
+# columns): A lane block kb (lanes 16 kb .. 16 kb + 15, row = lane % 16) holds 32
+# fields, field e at bits [6 e, 6 e + 6) of six 32-bit registers, and meets the
+# fp8 B element of group column FP6_COLUMN(kb, e) (measured pairing of the
+# instruction: A block kb, element e <-> B block 2 (kb % 2) + e // 16, element
+# 16 (kb // 2) + e % 16, B block k holding columns 32 k .. 32 k + 31).
+# Storage: bytes of the planes' size, ordered [G / 4, O, kb (4), group slot (4),
+# 3 words]: the 12 bytes a lane reads for one group of its 4-group batch.  The
+# kernel expands the three words s0, s1, s2 into the six registers with
+#   R0 = s0 & M0, R2 = (s0 >> 1) & M2, R3 = s1 & M0, R5 = (s1 >> 1) & M2,
+#   R1 = s2 & M1, R4 = ((s2 >> 3) with bits 29, 30 from s2 bits 1, 2) & M1
+# (M0 = 0xC71C71C7, M1 = 0x71C71C71, M2 = 0x1C71C71C: the mantissa bits of the
+# fields in each register); FP6_STORED_BIT restates that map bit by bit.
+FP6_M0, FP6_M1, FP6_M2 = 0xC71C71C7, 0x71C71C71, 0x1C71C71C
+
+
+def fp6_column(kb: int, e: int) -> int:
+    """The group column that field e of A lane block kb multiplies."""
+    return 32 * (2 * (kb % 2) + e // 16) + 16 * (kb // 2) + e % 16
+
+
+def fp6_register_bit(e: int, j: int) -> tuple[int, int]:
+    """(register, bit) of mantissa bit j of field e."""
+    p = 6 * e + j
+    return p // 32, p % 32
+
+
+def fp6_stored_bit(reg: int, bit: int) -> tuple[int, int]:
+    """(stored word, bit) that register bit (reg, bit) is expanded from."""
+    if reg in (0, 3):
+        return reg // 3, bit
+    if reg in (2, 5):
+        return (0 if reg == 2 else 1), bit + 1
+    if reg == 1:
+        return 2, bit
+    return 2, (bit - 28) if bit in (29, 30) else bit + 3
+
+
+def _fp6_slots() -> np.ndarray:
+    """[kb, e, j] -> stored bit index (word * 32 + bit) within a lane's 3 words."""
+    slots = np.zeros((4, 32, 3), dtype=np.int64)
+    for kb in range(4):
+        for e in range(32):
+            for j in range(3):
+                w, b = fp6_stored_bit(*fp6_register_bit(e, j))
+                slots[kb, e, j] = 32 * w + b
+    return slots
+
+
+def fp6_from_sorted_codes(sorted_codes: np.ndarray) -> np.ndarray:
+    """Sorted-order codes ``[K, O]`` -> fp6 layout (uint8, the planes' shape ``[G, 3, O, 16]``)."""
+    codes = np.asarray(sorted_codes, dtype=np.uint32)
+    k, o = codes.shape
+    if k % (4 * GROUP):
+        raise ValueError("K must be a multiple of 512")
+    g = k // GROUP
+    grouped = codes.reshape(g // 4, 4, GROUP, o).transpose(0, 3, 1, 2)  # [G/4, O, slot, 128]
+    words = np.zeros((g // 4, o, 4, 4, 3), dtype=np.uint32)          # [G/4, O, kb, slot, 3]
+    slots = _fp6_slots()
+    for kb in range(4):
+        for e in range(32):
+            q = grouped[:, :, :, fp6_column(kb, e)]                   # [G/4, O, slot]
+            for j in range(3):
+                w, b = divmod(int(slots[kb, e, j]), 32)
+                words[:, :, kb, :, w] |= ((q >> j) & 1) << np.uint32(b)
+    return np.ascontiguousarray(words.astype("<u4").view(np.uint8).reshape(g, 3, o, 16))
+
+
+def sorted_codes_from_fp6(fp6: np.ndarray) -> np.ndarray:
+    """fp6 layout -> sorted-order codes ``[K, O]``."""
+    fp6 = np.asarray(fp6, dtype=np.uint8)
+    g, three, o, sixteen = fp6.shape
+    if three != 3 or sixteen != 16 or g % 4:
+        raise ValueError("fp6 payload must be [G,3,O,16] bytes with G % 4 == 0")
+    words = np.ascontiguousarray(fp6).view("<u4").reshape(g // 4, o, 4, 4, 3).astype(np.uint32)
+    grouped = np.zeros((g // 4, o, 4, GROUP), dtype=np.uint32)
+    slots = _fp6_slots()
+    for kb in range(4):
+        for e in range(32):
+            for j in range(3):
+                w, b = divmod(int(slots[kb, e, j]), 32)
+                grouped[:, :, :, fp6_column(kb, e)] |= ((words[:, :, kb, :, w] >> np.uint32(b)) & 1) << np.uint32(j)
+    return np.ascontiguousarray(grouped.transpose(0, 2, 3, 1).reshape(g * GROUP, o).astype(np.uint8))
+
+
+def fp6_from_planar(planes: np.ndarray) -> np.ndarray:
+    """The bind-time repack: planes -> fp6 layout (same sorted order)."""
+    return fp6_from_sorted_codes(codes_from_planar(planes))
+
+
+def fp6_expand(s0: int, s1: int, s2: int) -> list[int]:
+    """The kernel's expansion of one lane's three words into six fp6 registers."""
+    mid = ((s2 >> 3) & ~0x60000000 | (s2 << 28) & 0x60000000) & 0xFFFFFFFF
+    return [s0 & FP6_M0, s2 & FP6_M1, (s0 >> 1) & FP6_M2, s1 & FP6_M0, mid & FP6_M1, (s1 >> 1) & FP6_M2]

@@ -60,6 +60,8 @@ DEFAULTS = {
     "fx_w3_gemv_strided_batched": dict(W3, O=128, x_stride=256, planes_stride=3 * 2 * 128 * 16, scales_stride=256,
                                        zeros_stride=256, out_stride=128, batch=4),
     "fx_w3_gemv_fields": dict(W3, fields=D),
+    "fx_w3_planes_to_fp6": dict(planes=D, fp6=D + 4096, O=64, K=512, stream=None),
+    "fx_w3_gemv_fp6": dict(W3, fp6=D, K=512),
     "fx_w3_fields_plan": dict(tiles=3, parts=4, prefetch=2, stage=1),
     "fx_w3_gemv_fields_rows": dict(W3, fields=D, M=8, O=128, K=1024),
     "fx_decode_attention_plan": dict(keys_per_thread=2, head_groups=2),
@@ -182,6 +184,16 @@ CASES = [
     ("fx_w3_planes_to_fields", dict(planes=D + 4), "16-byte aligned"),
     ("fx_w3_planes_to_fields", dict(fields=None), "non-null"),
     ("fx_w3_gemv_fields", dict(out=None), "out must be non-null"),
+    ("fx_w3_planes_to_fp6", dict(fp6=D), "cannot run in place"),
+    ("fx_w3_planes_to_fp6", dict(K=384), "K a multiple of 512"),
+    ("fx_w3_planes_to_fp6", dict(planes=D + 4), "16-byte aligned"),
+    ("fx_w3_planes_to_fp6", dict(fp6=None), "non-null"),
+    ("fx_w3_gemv_fp6", dict(out=None), "out must be non-null"),
+    ("fx_w3_gemv_fp6", dict(x_dtype=1), "bf16 activations"),
+    ("fx_w3_gemv_fp6", dict(O=40), "O % 16 == 0 and K % 512 == 0"),
+    ("fx_w3_gemv_fp6", dict(K=256), "O % 16 == 0 and K % 512 == 0"),
+    ("fx_w3_gemv_residual", dict(payload_format=2, perm=D, K=512), "no permutation"),
+    ("fx_w3_gemv_residual", dict(payload_format=3), "FX_W3_FP6"),
     ("fx_w3_fields_plan", dict(tiles=5), "no shared-staging kernel for plan (5, 4, 2, 1)"),
     ("fx_w3_fields_plan", dict(prefetch=3), "no shared-staging kernel"),
     ("fx_w3_fields_plan", dict(tiles=1, parts=8, prefetch=2, stage=2), "no shared-staging kernel"),

@@ -297,3 +297,36 @@ def test_outlier_case_quiet_rows_and_sensitivity(permute, ratio):
     lossy = w3.matvec_exact(flushed.numpy(), layout)
     with pytest.raises(AssertionError):
         assert_within_terms(lossy, exact, "bf16", x, scales, 2.0 ** -18)
+
+
+def test_fp6_layout_bijection_round_trip_and_expansion():
+    """The fp6 layout: every lane's 96 stored bits carry exactly its 32 codes' bits,
+    codes survive the round trip, and the kernel's six-register expansion puts each
+    code in the mantissa of the field that meets its column (the instruction's
+    measured pairing), with sign and exponent bits zero."""
+    slots = w3._fp6_slots()
+    for kb in range(4):
+        assert sorted(slots[kb].reshape(-1)) == list(range(96))
+        assert sorted(w3.fp6_column(kb, e) for e in range(32)) == sorted(
+            32 * (2 * (kb % 2) + h) + 16 * (kb // 2) + i for h in range(2) for i in range(16))
+    assert sorted(w3.fp6_column(kb, e) for kb in range(4) for e in range(32)) == list(range(128))
+    rng = np.random.default_rng(5)
+    codes = rng.integers(0, 8, size=(1024, 40)).astype(np.uint8)
+    f = w3.fp6_from_sorted_codes(codes)
+    assert f.shape == (8, 3, 40, 16) and f.nbytes == w3.planar_from_codes(codes).nbytes
+    assert np.array_equal(w3.sorted_codes_from_fp6(f), codes)
+    assert np.array_equal(w3.fp6_from_planar(w3.planar_from_codes(codes)), f)
+    words = f.view("<u4").reshape(2, 40, 4, 4, 3)
+    for bt, o, kb, b in ((0, 0, 0, 0), (1, 39, 3, 3), (0, 17, 1, 2), (1, 5, 2, 1)):
+        regs = w3.fp6_expand(*[int(v) for v in words[bt, o, kb, b]])
+        bits = sum(r << (32 * i) for i, r in enumerate(regs))
+        for e in range(32):
+            assert (bits >> (6 * e)) & 63 == codes[(4 * bt + b) * 128 + w3.fp6_column(kb, e), o]
+    # known answer: one code 7 at sorted column 128 * 4 + 16 (batch 1, slot 0) of row 2:
+    # lane block 2 (16 (kb // 2) = 16), field 0, i.e. bits 0..2 of register 0 = stored word 0
+    one = np.zeros((1024, 4), dtype=np.uint8)
+    one[4 * 128 + 16, 2] = 7
+    w = w3.fp6_from_sorted_codes(one).view("<u4").reshape(2, 4, 4, 4, 3)
+    assert int(w[1, 2, 2, 0, 0]) == 7 and int(w.sum()) == 7
+    with pytest.raises(ValueError):
+        w3.fp6_from_sorted_codes(np.zeros((384, 4), dtype=np.uint8))
