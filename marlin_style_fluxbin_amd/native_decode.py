@@ -267,8 +267,9 @@ class _ResidualStream:
             raise ValueError("W3 planes must be contiguous")
         fields = torch.empty_like(planes)
         g, _, o, _ = planes.shape
-        _lib.check(self.lib.fx_w3_planes_to_fields(planes.data_ptr(), fields.data_ptr(), o, 128 * g,
-                                                   _lib.stream_handle(planes.device)), "fx_w3_planes_to_fields")
+        name = "fx_w3_planes_to_fp6" if self.format == _lib.PAYLOAD_FP6 else "fx_w3_planes_to_fields"
+        _lib.check(getattr(self.lib, name)(planes.data_ptr(), fields.data_ptr(), o, 128 * g,
+                                           _lib.stream_handle(planes.device)), name)
         self._fields[planes.data_ptr()] = (planes, fields)
 
     @staticmethod
@@ -495,8 +496,8 @@ class NativeDecodeSession:
         self.swiglu = [_GateUpSwiGLU.build(*(b.get_submodule(n) for n in _MLP[:2])) for b in self.layers]
         self.gate_up = [None if f is not None else _FusedLinear.build([b.get_submodule(n) for n in _MLP[:2]])
                         for f, b in zip(self.swiglu, self.layers)]
-        if w3_payload not in ("fields", "planar"):
-            raise ValueError(f"w3_payload must be 'fields' or 'planar', got {w3_payload!r}")
+        if w3_payload not in ("fields", "planar", "fp6"):
+            raise ValueError(f"w3_payload must be 'fields', 'planar' or 'fp6', got {w3_payload!r}")
         self.in_norm = [b.input_layernorm.weight for b in self.layers]
         self.post_norm = [b.post_attention_layernorm.weight for b in self.layers]
         self.q_norm = [b.self_attn.q_norm.weight for b in self.layers]
@@ -519,7 +520,7 @@ class NativeDecodeSession:
         self.logits = torch.empty((self.steps, cfg.vocab_size), dtype=dtype, device=self.device)
         self.predictions = torch.empty((self.steps, 1), dtype=torch.int64, device=self.device)
         self.stream = _ResidualStream.build(
-            self, _lib.PAYLOAD_FIELDS if w3_payload == "fields" else _lib.PAYLOAD_PLANAR)
+            self, {"fields": _lib.PAYLOAD_FIELDS, "planar": _lib.PAYLOAD_PLANAR, "fp6": _lib.PAYLOAD_FP6}[w3_payload])
         lib = _lib.library()
         self.lib = lib
         # the final RMSNorm, LM head and argmax as one launch where the head allows it

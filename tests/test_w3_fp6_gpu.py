@@ -158,3 +158,36 @@ def test_fp6_refuses_what_it_cannot_run(gpu):
                               dl["scales"].data_ptr(), _lib.dtype_code(torch.float16), dl["zeros"].data_ptr(),
                               out.data_ptr(), 64, 512, s) != 0  # fp16 activations
     assert b"bf16" in lib.fx_last_error()
+
+
+def test_native_decode_session_on_the_fp6_layout(gpu):
+    """A whole decode run (NativeDecodeSession, w3_payload="fp6") against the same
+    model's run on the field layout: the captured graph replays its own eager
+    pass bit for bit, and the logits stay within the activation digits' rounding
+    of the field layout's (each GEMV within a few output ulps of the other,
+    compounded over three layers and eight steps)."""
+    from marlin_style_fluxbin_amd.native_decode import NativeDecodeSession
+    from marlin_style_fluxbin_amd.qwen3 import qwen3_config, random_qwen3_model, w3_quantize_qwen3_model
+
+    # hidden and intermediate sizes whose K splits into whole four-group tiles
+    config = qwen3_config(hidden_size=512, intermediate_size=1024, num_hidden_layers=3, num_attention_heads=8,
+                          num_key_value_heads=2, head_dim=64, vocab_size=384, max_position_embeddings=128)
+    model = random_qwen3_model(config, device=gpu, dtype=torch.bfloat16, seed=3)
+    w3_quantize_qwen3_model(model)
+    g = torch.Generator().manual_seed(6)
+    ids = torch.randint(0, 384, (1, 20), generator=g).to(gpu)
+    forced = torch.randint(0, 384, (1, 8), generator=g).to(gpu)
+    with torch.inference_mode():
+        sessions = {fmt: NativeDecodeSession(model, ids, forced, w3_payload=fmt) for fmt in ("fields", "fp6")}
+        eager = sessions["fp6"].audit()
+        graphs = {fmt: s.capture() for fmt, s in sessions.items()}
+        assert torch.equal(graphs["fp6"]["logits"], eager["logits"])
+        _, replay = sessions["fp6"].measure("sequence_graph")
+        assert torch.equal(replay["logits"], graphs["fp6"]["logits"])
+    a, b = graphs["fp6"]["logits"].float(), graphs["fields"]["logits"].float()
+    nrmse = float(((a - b).square().mean() / b.square().mean()).sqrt())
+    print(f"fp6 against fields: logits NRMSE {nrmse:.3g}", flush=True)
+    # a wrong field, pairing or digit moves the logits by O(1) relative
+    assert nrmse <= 0.03, nrmse
+    with pytest.raises(ValueError, match="w3_payload"):
+        NativeDecodeSession(model, ids, forced, w3_payload="fp4")
