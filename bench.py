@@ -18,7 +18,9 @@ finish launch only for split-K plans); the same-run bf16 arm runs torch.matmul
 is the gate/up shape's measurement: the dominant kernel of a decode step.
 ``config.field_layout`` (and each shape's ``fields_*``) times the same payloads
 after the library's bind-time repack into its field layout (same bytes, half
-the dequant instructions), the format the native decode reads.
+the dequant instructions), the format the native decode reads; each shape's
+``fp6_*`` times the opt-in fp6 layout (gfx950's scaled f8f6f4 instruction) on
+the same payloads.
 ``roofline.traffic`` is the HBM bytes per launch measured with rocprofv3 PMC
 counters (FETCH_SIZE + WRITE_SIZE, scaled by a plain read kernel of known size),
 read from ``profiles/w3_mfma_traffic.json`` when present.
@@ -240,6 +242,20 @@ def bench_shape(o, k, device, steps, warmup, stream, min_bytes=320e6, min_copies
 
     graphs["fields"] = (capture(over([lambda p=p, f=f: field_call(p, f) for p, f in zip(payloads, fields)]),
                                 stream), copies)
+    # the opt-in fp6 layout (fx_w3_planes_to_fp6 / fx_w3_gemv_fp6) on the same payloads
+    fp6 = [torch.empty_like(p["planes"]) for p in payloads]
+    for p, f in zip(payloads, fp6):
+        _lib.check(lib.fx_w3_planes_to_fp6(p["planes"].data_ptr(), f.data_ptr(), o, k,
+                                           _lib.stream_handle(device)), "fx_w3_planes_to_fp6")
+    f6out = torch.empty_like(out)
+
+    def fp6_call(p, f):
+        _lib.check(lib.fx_w3_gemv_fp6(x.data_ptr(), _lib.dtype_code(x.dtype), f.data_ptr(),
+                                      p["scales"].data_ptr(), _lib.dtype_code(p["scales"].dtype),
+                                      p["zeros"].data_ptr(), f6out.data_ptr(), o, k,
+                                      _lib.stream_handle(device)), "fx_w3_gemv_fp6")
+
+    graphs["fp6"] = (capture(over([lambda p=p, f=f: fp6_call(p, f) for p, f in zip(payloads, fp6)]), stream), copies)
     # config 1's small-M variants on the field layout (fx_w3_gemv_fields_rows)
     fom = {m: torch.empty(m, o, device=device, dtype=torch.bfloat16) for m in (2, 4, 8)}
 
@@ -290,12 +306,15 @@ def bench_shape(o, k, device, steps, warmup, stream, min_bytes=320e6, min_copies
     # bit-equal to the identity kernel on the gathered row
     gemvs[-1](x, out)
     field_call(payloads[-1], fields[-1])
+    fp6_call(payloads[-1], fp6[-1])
     permuted[-1](x, pout)
     gathered = torch.empty_like(out)
     gemvs[-1](x[:, permuted[-1].layout["perm"].long()].contiguous(), gathered)
     torch.cuda.synchronize()
     if not torch.allclose(fout.float(), out.float(), rtol=2 ** -7, atol=1e-3 * float(out.float().abs().max())):
         raise RuntimeError("field-layout GEMV disagrees with the planar GEMV")
+    if not torch.allclose(f6out.float(), out.float(), rtol=2 ** -7, atol=1e-3 * float(out.float().abs().max())):
+        raise RuntimeError("fp6-layout GEMV disagrees with the planar GEMV")
     if not torch.equal(pout, gathered):
         raise RuntimeError("permuted GEMV differs from the identity GEMV on the gathered activations")
     decoded[-1](x, dout)
@@ -333,7 +352,8 @@ def bench_shape(o, k, device, steps, warmup, stream, min_bytes=320e6, min_copies
                         "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBPS, 4)}
     steady["note"] = (f"one fx_w3_gemv_strided_batched launch over the {copies} payloads (bit-identical "
                       "outputs): the kernel's rate without the per-launch cost")
-    del graphs, shuffled, weights, payloads, gemvs, permuted, fields, fields_stacked, stacked, batch_out, decoded
+    fp6_us = t["fp6"]["us"]
+    del graphs, shuffled, weights, payloads, gemvs, permuted, fields, fp6, fields_stacked, stacked, batch_out, decoded
     del decoded_views, scales16, table_ws
     torch.cuda.empty_cache()
     return {
@@ -348,6 +368,8 @@ def bench_shape(o, k, device, steps, warmup, stream, min_bytes=320e6, min_copies
         "w3_speedup_vs_bf16": round(bf16_us / w3_us, 3),
         "fields_us": round(fields_us, 3), "fields_GBps": round(nbytes / fields_us / 1e3, 1),
         "fields_frac_hbm": round(nbytes / fields_us / 1e3 / HBM_PEAK_GBPS, 4),
+        "fp6_us": round(fp6_us, 3), "fp6_GBps": round(nbytes / fp6_us / 1e3, 1),
+        "fp6_vs_fields": round(fp6_us / fields_us, 3),
         "small_m": small_m,
         "steady_state": steady,
         "restore_us": round(restore_us, 3), "restore_GBps": round(restore_bytes / restore_us / 1e3, 1),
